@@ -1,0 +1,207 @@
+/*
+ * pkx.h -- C ABI of the MI355X (gfx950) FastConformer encoder for parakeet.cpp.
+ *
+ * Plain C: pointers, sizes and int status codes (0 = ok, nonzero = error with
+ * a message in pkx_last_error()).  No C++ exception crosses this boundary.
+ * "dev" pointers are device (HBM) addresses; "host" pointers are CPU memory.
+ * Every compute call is asynchronous on the given stream (NULL = default
+ * stream) unless stated otherwise.
+ *
+ * Layouts follow the reference (see the citations on each entry point):
+ *   mel          [B][n_mels][T_max] f32      (MelBatch, src/encoder.hpp:17-23)
+ *   activations  [B][T][d_model]    f32      (ggml ne [d,T,B])
+ *   weights      GGUF v3 tensors, verbatim NeMo names, ggml ne order,
+ *                types f32 / f16 / q8_0 / q4_K (docs/conversion.md:21-128,
+ *                docs/quantization.md:74-99)
+ *
+ * One model handle owns its device weights and a grow-only workspace.  A
+ * handle is not re-entrant: calls on one handle must not overlap (the
+ * reference serialises all compute behind one mutex, src/ggml_graph.cpp:35,84);
+ * distinct handles may run concurrently on distinct streams.
+ */
+#ifndef PKX_H
+#define PKX_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PKX_ABI_VERSION 1
+
+typedef struct pkx_model pkx_model;
+
+/* ggml type ids accepted for weights (the GGUF layout's own numbering). */
+enum { PKX_TYPE_F32 = 0, PKX_TYPE_F16 = 1, PKX_TYPE_Q8_0 = 8, PKX_TYPE_Q4_K = 12 };
+
+/* Compute precision of a model handle.
+ *   F32: f32 activations, weights dequantised to f32, f32 MFMA (16x16x4) GEMMs
+ *        -- the exact-precision path (f32 GGUFs, parity at 1e-4).
+ *   F16: f32 residual stream and statistics, f16 GEMM/attention operands with
+ *        f32 accumulation, weights dequantised to f16 in registers
+ *        (f16 / q8_0 / q4_K GGUFs; f32 pointwise-conv weights are converted
+ *        to f16 at upload).
+ *   AUTO: F16 if any allowlisted linear is f16/q8_0/q4_K, else F32. */
+enum { PKX_PREC_AUTO = -1, PKX_PREC_F32 = 0, PKX_PREC_F16 = 1 };
+
+/* Subsampling time-masking semantics.
+ *   BATCHED: zero trailing frames before every conv stage
+ *            (Subsampling::build_graph_batched, src/subsampling.cpp:95-147,
+ *            used by Encoder::forward_batch).
+ *   SCALAR:  mask only the flattened output (Subsampling::build_graph,
+ *            src/subsampling.cpp:281-300, used by Encoder::forward). */
+enum { PKX_MASK_BATCHED = 0, PKX_MASK_SCALAR = 1 };
+
+/* Encoder hyper-parameters (the encoder fields of pk::ParakeetConfig,
+ * src/model_loader.hpp:27-52; GGUF keys parakeet.encoder.*). */
+typedef struct {
+    int d_model, n_layers, n_heads, ff_dim, conv_kernel;
+    int n_mels;          /* parakeet.encoder.feat_in */
+    int sub_channels;    /* parakeet.encoder.subsampling_conv_channels */
+    int xscaling;        /* parakeet.encoder.xscaling */
+    int vocab_size;      /* parakeet.vocab_size (CTC/TDT heads: vocab_size + 1 tokens) */
+    int n_durations;     /* len(parakeet.tdt.durations), 0 if no TDT head */
+} pkx_config;
+
+/* ---- status ---------------------------------------------------------------- */
+int         pkx_abi_version(void);
+/* Message of the last failing call on this thread ("" if none). */
+const char* pkx_last_error(void);
+
+/* ---- device plumbing (HIP runtime, for callers without their own) ---------- */
+int pkx_device_count(int* n);
+int pkx_malloc(void** dev, size_t bytes);
+int pkx_free(void* dev);
+int pkx_memcpy_h2d(void* dev_dst, const void* host_src, size_t bytes, void* stream);
+int pkx_memcpy_d2h(void* host_dst, const void* dev_src, size_t bytes, void* stream);
+int pkx_memcpy_d2d(void* dev_dst, const void* dev_src, size_t bytes, void* stream);
+int pkx_stream_create(void** stream);
+int pkx_stream_destroy(void* stream);
+int pkx_stream_synchronize(void* stream);
+int pkx_event_create(void** event);
+int pkx_event_destroy(void* event);
+int pkx_event_record(void* event, void* stream);
+int pkx_event_elapsed_ms(float* ms, void* start, void* stop);   /* synchronises on stop */
+
+/* ---- model handle ----------------------------------------------------------
+ * Replaces pk::ModelLoader::load + realize_weights (src/model_loader.cpp:47-167)
+ * for the encoder path: weights are uploaded once and never re-copied. */
+
+/* Read a GGUF v3 file (parakeet.* KV + verbatim tensor names) and upload the
+ * encoder, CTC-head and TDT-joint tensors.  precision: PKX_PREC_*. */
+int pkx_model_load_gguf(const char* path, int precision, pkx_model** out);
+
+/* Build a handle from tensors supplied one by one (same names, ggml ne order
+ * and raw bytes as in a GGUF), then pkx_model_finalize(). */
+int pkx_model_create(const pkx_config* cfg, int precision, pkx_model** out);
+int pkx_model_set_tensor(pkx_model* m, const char* name, int ggml_type, int n_dims,
+                         const int64_t* ne, const void* host_data, size_t nbytes);
+int pkx_model_finalize(pkx_model* m);
+int pkx_model_free(pkx_model* m);
+/* precision: resolved PKX_PREC_F32/F16; has_ctc/has_joint: heads present. */
+int pkx_model_info(pkx_model* m, pkx_config* cfg, int* precision, int* has_ctc, int* has_joint);
+
+/* ---- length arithmetic (pk::Subsampling::valid_out_len, src/subsampling.cpp:25-46) */
+int pkx_subsampled_len(int T_mel);
+int pkx_valid_out_len(int T_mel, int in_valid);   /* in_valid < 0: offline T-1 */
+
+/* ---- hot path ----------------------------------------------------------------
+ * Replaces pk::Encoder::forward_batch (src/encoder.cpp:97-167) and
+ * forward_capture (src/encoder.cpp:30-95): subsampling -> xscaling ->
+ * rel-pos table -> n_layers conformer blocks, one stream-ordered launch
+ * sequence.
+ *   mel_dev     [B][n_mels][T_max] f32
+ *   valid_T     host [B]: true mel frames per item (NULL = T_max); the entry
+ *               valid length is valid_T[b]-1 (src/encoder.cpp:111-112)
+ *   out_dev     [B][T'][d_model] f32, T' = pkx_subsampled_len(T_max); frames
+ *               t >= valid_out[b] are padding (not zeroed, as in the reference)
+ *   T_out       host: T'
+ *   valid_out   host [B] (may be NULL)
+ *   capture_dev NULL, or [n_layers][B][T'][d_model] f32 per-layer outputs */
+int pkx_encoder_forward(pkx_model* m, const float* mel_dev, int B, int T_max,
+                        const int* valid_T, int mask_mode, float* out_dev, int* T_out,
+                        int* valid_out, float* capture_dev, void* stream);
+
+/* Per-item channels-first compaction of an encoder output
+ * (src/encoder.cpp:158-166): item b -> out_dev + offs[b], [d_model][valid[b]].
+ * valid_dev [B] int32 and offs_dev [B] int64 are device arrays. */
+int pkx_compact_channels_first(const float* x_dev, int B, int T, int d_model,
+                               const int* valid_dev, const int64_t* offs_dev, float* out_dev,
+                               void* stream);
+
+/* pk::Subsampling::forward / build_graph_batched (src/subsampling.cpp:48-240,
+ * :242-386, :388-419): out_dev [B][T'][d_model].  xscaling is not applied
+ * here (it belongs to the encoder, src/encoder.cpp:122-124). */
+int pkx_subsampling_forward(pkx_model* m, const float* mel_dev, int B, int T_max,
+                            const int* valid_T, int mask_mode, float* out_dev, int* T_out,
+                            int* valid_out, void* stream);
+
+/* pk::ConformerLayer::forward / forward_with_conv (src/conformer.cpp:426-516)
+ * and build_graph_batched (:285-353).  x_dev, out_dev [B][T][d_model] f32
+ * (may alias); valid host [B] (NULL = T); conv_out_dev NULL or [B][T][d_model]
+ * receives the conv-module output.  The rel-pos table is computed internally
+ * (pk::rel_pos_encoding). */
+int pkx_conformer_layer_forward(pkx_model* m, int layer, const float* x_dev, int B, int T,
+                                const int* valid, float* out_dev, float* conv_out_dev,
+                                void* stream);
+
+/* pk::RelPosAttention::forward / build_graph_batched
+ * (src/relpos_attention.cpp:162-306, :308-333): x_dev is the already
+ * normalised input [B][T][d_model]. */
+int pkx_relpos_attention_forward(pkx_model* m, int layer, const float* x_dev, int B, int T,
+                                 const int* valid, float* out_dev, void* stream);
+
+/* pk::ConformerLayer::conv_module_forward (src/conformer.cpp:518-543) and
+ * build_conv_module (:38-164): c_dev = norm_conv(residual). */
+int pkx_conv_module_forward(pkx_model* m, int layer, const float* c_dev, int B, int T,
+                            const int* valid, float* out_dev, void* stream);
+
+/* pk::CTCDecoder::forward (src/ctc_decoder.cpp:34-116) over M time-major frames
+ * enc_dev [M][d_model]: logprobs_dev [M][vocab+1] f32 (log_softmax) and
+ * argmax_dev [M] int32 (first max, src/search.cpp:57-61). */
+int pkx_ctc_forward(pkx_model* m, const float* enc_dev, int64_t M, float* logprobs_dev,
+                    int32_t* argmax_dev, void* stream);
+
+/* TDT joint over every frame with one prediction-net output g:
+ * Joint::precompute_enc_proj + step_logits (src/joint.cpp:37-104) and the
+ * split argmax of tdt_greedy (src/tdt.cpp:76-79).  g_dev [pred_hidden];
+ * logits_dev [M][vocab+1+n_durations]; tok_dev, dur_dev [M] int32. */
+int pkx_tdt_joint_argmax(pkx_model* m, const float* enc_dev, int64_t M, const float* g_dev,
+                         float* logits_dev, int32_t* tok_dev, int32_t* dur_dev, void* stream);
+
+/* ---- kernel-level entry points (ggml ops the encoder issues) ---------------- */
+
+/* Dequantise n raw ggml-layout elements (q8_0 / q4_K / f16) to f32, bit-exact
+ * with ggml's dequantize_row_* (the src0 side of ggml_mul_mat). */
+int pkx_dequantize(int ggml_type, const void* src_dev, float* dst_dev, int64_t n, void* stream);
+
+/* y = x . W^T (+ bias): ggml_mul_mat(W, x) + ggml_add with W given in raw GGUF
+ * layout (host_w, N rows of K), uploaded for this call.  precision selects the
+ * F32 or F16 path.  x_dev [M][K] f32, y_dev [M][N] f32. */
+int pkx_linear(int precision, int ggml_type, int N, int K, const void* host_w, size_t nbytes,
+               const float* bias_dev, const float* x_dev, int64_t M, float* y_dev, void* stream);
+
+/* LayerNorm over the last dim, f32 in/out (ggml_norm + mul + add,
+ * src/conformer.cpp:300-307). */
+int pkx_layernorm(const float* x_dev, const float* g_dev, const float* b_dev, float* y_dev,
+                  int64_t M, int D, float eps, void* stream);
+
+/* pk::rel_pos_encoding (src/pos_enc.cpp:10-34): out_dev [2T-1][D] f32. */
+int pkx_rel_pos_encoding(int T, int D, float* out_dev, void* stream);
+
+/* ---- profiling ----------------------------------------------------------------
+ * With profiling on, each kernel family is bracketed by events (serialising
+ * the stream); pkx_model_profile_read returns milliseconds and launch counts
+ * per family (arrays of PKX_PROF_FAMILIES entries, order:
+ * subsampling, layernorm, gemm_ffn, gemm_qkv, gemm_pos, attention, gemm_out,
+ * gemm_pw1_glu, dwconv, gemm_pw2, pos_enc). */
+#define PKX_PROF_FAMILIES 11
+int pkx_model_set_profiling(pkx_model* m, int on);
+int pkx_model_profile_read(pkx_model* m, double* ms, int64_t* launches);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PKX_H */

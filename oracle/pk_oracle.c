@@ -1,0 +1,677 @@
+/*
+ * pk_oracle.c -- CPU restatement of the parakeet.cpp encoder path.
+ *
+ * TEST INFRASTRUCTURE ONLY (parity checker + "port" CPU baseline); the
+ * product library never links it.  See pk_oracle.h for the layout contract.
+ * Each function cites the reference file:line whose graph it restates.
+ *
+ * Arithmetic conventions (the reference's ggml kernels are absent):
+ *   - dot products: f32 products summed in f32 lane partials (ggml's SIMD
+ *     sgemm accumulates the same way), OpenMP over output rows;
+ *   - LayerNorm statistics in f64 with an f32 mean (ggml_norm_f32);
+ *   - softmax / log-softmax statistics in f64;
+ *   - BatchNorm fold in f32 exactly as conformer.cpp:144-147.
+ */
+#include "pk_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+static int g_threads = 0;
+
+void orc_set_threads(int n) {
+    g_threads = n;
+#ifdef _OPENMP
+    if (n > 0) omp_set_num_threads(n);
+#endif
+}
+
+int orc_get_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}
+
+/* ------------------------------------------------------------------------ */
+/* binary16                                                                  */
+/* ------------------------------------------------------------------------ */
+
+float orc_f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h >> 15) << 31;
+    uint32_t ex = (h >> 10) & 0x1fu, man = h & 0x3ffu, bits;
+    float f;
+    if (ex == 0) {
+        /* zero or subnormal: man * 2^-24, exact in f32 */
+        f = (float)man * 5.9604644775390625e-8f;
+        memcpy(&bits, &f, 4);
+        bits |= sign;
+    } else if (ex == 31) {
+        bits = sign | 0x7f800000u | (man << 13);
+    } else {
+        bits = sign | ((ex + 112u) << 23) | (man << 13);
+    }
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+uint16_t orc_f32_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+    uint32_t ax = x & 0x7fffffffu;
+    if (ax > 0x7f800000u) return (uint16_t)(sign | 0x7e00u);       /* NaN */
+    if (ax >= 0x47800000u) return (uint16_t)(sign | 0x7c00u);      /* >= 2^16 -> inf */
+    if (ax < 0x38800000u) {
+        /* below 2^-14: subnormal result, mantissa = RNE(|f| * 2^24) (exact scale) */
+        float af;
+        memcpy(&af, &ax, 4);
+        return (uint16_t)(sign | (uint16_t)rintf(af * 16777216.0f));
+    }
+    uint32_t e = (ax >> 23) - 112u;
+    uint32_t m = ax & 0x7fffffu;
+    uint32_t h = (e << 10) | (m >> 13);
+    uint32_t rem = m & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;       /* carries into inf correctly */
+    return (uint16_t)(sign | h);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Block formats (docs/quantization.md; ggml v0.13.0 block_q8_0 / block_q4_K) */
+/* ------------------------------------------------------------------------ */
+
+#define QK8_0 32
+#define Q8_0_BYTES 34
+#define QK_K 256
+#define Q4_K_BYTES 144
+
+int64_t orc_row_bytes(int type, int64_t ne0) {
+    switch (type) {
+    case ORC_F32: return ne0 * 4;
+    case ORC_F16: return ne0 * 2;
+    case ORC_Q8_0: return (ne0 % QK8_0) ? 0 : (ne0 / QK8_0) * Q8_0_BYTES;
+    case ORC_Q4_K: return (ne0 % QK_K) ? 0 : (ne0 / QK_K) * Q4_K_BYTES;
+    default: return 0;
+    }
+}
+
+static uint16_t rd_u16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+static void wr_u16(uint8_t* p, uint16_t v) { p[0] = (uint8_t)v; p[1] = (uint8_t)(v >> 8); }
+
+/* 6-bit scale/min of sub-block j from the 12 packed bytes. */
+static void q4k_scale_min(int j, const uint8_t* q, int* sc, int* mn) {
+    if (j < 4) {
+        *sc = q[j] & 63;
+        *mn = q[j + 4] & 63;
+    } else {
+        *sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+        *mn = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+}
+
+int orc_dequantize(int type, const void* src, float* dst, int64_t n) {
+    const uint8_t* s = (const uint8_t*)src;
+    if (type == ORC_F32) { memcpy(dst, src, (size_t)n * 4); return 0; }
+    if (type == ORC_F16) {
+        for (int64_t i = 0; i < n; ++i) dst[i] = orc_f16_to_f32(rd_u16(s + 2 * i));
+        return 0;
+    }
+    if (type == ORC_Q8_0) {
+        if (n % QK8_0) return 1;
+        for (int64_t b = 0; b < n / QK8_0; ++b) {
+            const uint8_t* blk = s + b * Q8_0_BYTES;
+            float d = orc_f16_to_f32(rd_u16(blk));
+            for (int j = 0; j < QK8_0; ++j) dst[b * QK8_0 + j] = (float)(int8_t)blk[2 + j] * d;
+        }
+        return 0;
+    }
+    if (type == ORC_Q4_K) {
+        if (n % QK_K) return 1;
+        for (int64_t b = 0; b < n / QK_K; ++b) {
+            const uint8_t* blk = s + b * Q4_K_BYTES;
+            float d = orc_f16_to_f32(rd_u16(blk));
+            float dmin = orc_f16_to_f32(rd_u16(blk + 2));
+            const uint8_t* scales = blk + 4;
+            const uint8_t* qs = blk + 16;
+            float* y = dst + b * QK_K;
+            for (int c = 0; c < 4; ++c) {          /* 64-element chunk: two sub-blocks */
+                int sc, mn;
+                q4k_scale_min(2 * c, scales, &sc, &mn);
+                float d1 = d * (float)sc, m1 = dmin * (float)mn;
+                q4k_scale_min(2 * c + 1, scales, &sc, &mn);
+                float d2 = d * (float)sc, m2 = dmin * (float)mn;
+                for (int l = 0; l < 32; ++l) y[64 * c + l] = d1 * (float)(qs[32 * c + l] & 0xF) - m1;
+                for (int l = 0; l < 32; ++l) y[64 * c + 32 + l] = d2 * (float)(qs[32 * c + l] >> 4) - m2;
+            }
+        }
+        return 0;
+    }
+    return 2;
+}
+
+static int nearest_int(float v) { return (int)lrintf(v); }
+
+int orc_quantize(int type, const float* x, void* dst, int64_t n) {
+    uint8_t* o = (uint8_t*)dst;
+    if (type == ORC_F32) { memcpy(dst, x, (size_t)n * 4); return 0; }
+    if (type == ORC_F16) {
+        for (int64_t i = 0; i < n; ++i) wr_u16(o + 2 * i, orc_f32_to_f16(x[i]));
+        return 0;
+    }
+    if (type == ORC_Q8_0) {
+        if (n % QK8_0) return 1;
+        for (int64_t b = 0; b < n / QK8_0; ++b) {
+            const float* v = x + b * QK8_0;
+            uint8_t* blk = o + b * Q8_0_BYTES;
+            float amax = 0.f;
+            for (int j = 0; j < QK8_0; ++j) amax = fmaxf(amax, fabsf(v[j]));
+            float d = amax / 127.f, id = d != 0.f ? 1.f / d : 0.f;
+            wr_u16(blk, orc_f32_to_f16(d));
+            for (int j = 0; j < QK8_0; ++j) blk[2 + j] = (uint8_t)(int8_t)roundf(v[j] * id);
+        }
+        return 0;
+    }
+    if (type == ORC_Q4_K) {
+        /* Simple min/max affine fit per 32-sub-block, then 6-bit scale/min
+         * codes against the super-block d/dmin (own quantiser). */
+        if (n % QK_K) return 1;
+        for (int64_t b = 0; b < n / QK_K; ++b) {
+            const float* v = x + b * QK_K;
+            uint8_t* blk = o + b * Q4_K_BYTES;
+            float scale[8], minv[8], maxs = 0.f, maxm = 0.f;
+            for (int j = 0; j < 8; ++j) {
+                float lo = v[32 * j], hi = v[32 * j];
+                for (int l = 1; l < 32; ++l) { lo = fminf(lo, v[32 * j + l]); hi = fmaxf(hi, v[32 * j + l]); }
+                if (lo > 0.f) lo = 0.f;
+                scale[j] = (hi - lo) / 15.f;
+                minv[j] = -lo;
+                maxs = fmaxf(maxs, scale[j]);
+                maxm = fmaxf(maxm, minv[j]);
+            }
+            uint16_t dh = orc_f32_to_f16(maxs / 63.f), mh = orc_f32_to_f16(maxm / 63.f);
+            float d = orc_f16_to_f32(dh), dmin = orc_f16_to_f32(mh);
+            int sc[8], mn[8];
+            for (int j = 0; j < 8; ++j) {
+                sc[j] = d > 0.f ? nearest_int(scale[j] / d) : 0;
+                mn[j] = dmin > 0.f ? nearest_int(minv[j] / dmin) : 0;
+                if (sc[j] > 63) sc[j] = 63;
+                if (mn[j] > 63) mn[j] = 63;
+                if (sc[j] < 0) sc[j] = 0;
+                if (mn[j] < 0) mn[j] = 0;
+            }
+            wr_u16(blk, dh);
+            wr_u16(blk + 2, mh);
+            uint8_t* s = blk + 4;
+            for (int j = 0; j < 4; ++j) {
+                s[j] = (uint8_t)((sc[j] & 63) | ((sc[j + 4] >> 4) << 6));
+                s[j + 4] = (uint8_t)((mn[j] & 63) | ((mn[j + 4] >> 4) << 6));
+                s[j + 8] = (uint8_t)((sc[j + 4] & 0xF) | ((mn[j + 4] & 0xF) << 4));
+            }
+            uint8_t q[QK_K];
+            for (int j = 0; j < 8; ++j) {
+                float dj = d * (float)sc[j], mj = dmin * (float)mn[j];
+                for (int l = 0; l < 32; ++l) {
+                    int qi = dj > 0.f ? nearest_int((v[32 * j + l] + mj) / dj) : 0;
+                    q[32 * j + l] = (uint8_t)(qi < 0 ? 0 : qi > 15 ? 15 : qi);
+                }
+            }
+            uint8_t* qs = blk + 16;
+            for (int c = 0; c < 4; ++c)
+                for (int l = 0; l < 32; ++l)
+                    qs[32 * c + l] = (uint8_t)(q[64 * c + l] | (q[64 * c + 32 + l] << 4));
+        }
+        return 0;
+    }
+    return 2;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Positional encoding: pos_enc.cpp:10-34                                    */
+/* ------------------------------------------------------------------------ */
+
+void orc_rel_pos_encoding(int T, int d, float* out) {
+    const int P = 2 * T - 1, half = d / 2;
+    const double factor = -(log(10000.0) / (double)d);
+    double* div = (double*)malloc(sizeof(double) * (size_t)half);
+    for (int i = 0; i < half; ++i) div[i] = exp((double)(2 * i) * factor);
+    for (int p = 0; p < P; ++p) {
+        const double pos = (double)((T - 1) - p);
+        for (int i = 0; i < half; ++i) {
+            const double a = pos * div[i];
+            out[(size_t)p * d + 2 * i] = (float)sin(a);
+            out[(size_t)p * d + 2 * i + 1] = (float)cos(a);
+        }
+    }
+    free(div);
+}
+
+/* ------------------------------------------------------------------------ */
+/* LayerNorm: conformer.cpp:300-307 (ggml_norm + mul + add)                  */
+/* ------------------------------------------------------------------------ */
+
+void orc_layer_norm(const float* x, int64_t M, int D, const float* g,
+                    const float* b, float eps, float* y) {
+#pragma omp parallel for schedule(static)
+    for (int64_t m = 0; m < M; ++m) {
+        const float* xr = x + m * D;
+        float* yr = y + m * D;
+        double sum = 0.0;
+        for (int i = 0; i < D; ++i) sum += xr[i];
+        const float mean = (float)(sum / D);
+        double sum2 = 0.0;
+        for (int i = 0; i < D; ++i) {
+            const float v = xr[i] - mean;
+            yr[i] = v;
+            sum2 += (double)(v * v);
+        }
+        const float scale = 1.0f / sqrtf((float)(sum2 / D) + eps);
+        for (int i = 0; i < D; ++i) {
+            float t = yr[i] * scale;
+            t = t * g[i];
+            yr[i] = t + b[i];
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Linear: y = x . W^T + b  (ggml_mul_mat(W, x) + ggml_add)                  */
+/* ------------------------------------------------------------------------ */
+
+typedef float v8f __attribute__((vector_size(32)));
+
+static inline v8f ld8(const float* p) { v8f v; memcpy(&v, p, 32); return v; }
+static inline float hsum8(v8f v) {
+    return ((v[0] + v[4]) + (v[1] + v[5])) + ((v[2] + v[6]) + (v[3] + v[7]));
+}
+
+void orc_linear(const float* x, int64_t M, int K, const float* W, int N,
+                const float* bias, float* y) {
+    const int K8 = K & ~7;
+    const int64_t Mb = (M + 1) / 2;
+    const int Nb = (N + 3) / 4;
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int64_t mb = 0; mb < Mb; ++mb) {
+        for (int nb = 0; nb < Nb; ++nb) {
+            const int64_t m0 = 2 * mb;
+            const int n0 = 4 * nb;
+            const int mc = (M - m0) < 2 ? (int)(M - m0) : 2;
+            const int nc = (N - n0) < 4 ? (N - n0) : 4;
+            const float* xr[2];
+            const float* wr[4];
+            for (int i = 0; i < 2; ++i) xr[i] = x + (size_t)(m0 + (i < mc ? i : 0)) * K;
+            for (int j = 0; j < 4; ++j) wr[j] = W + (size_t)(n0 + (j < nc ? j : 0)) * K;
+            v8f acc[2][4];
+            for (int i = 0; i < 2; ++i)
+                for (int j = 0; j < 4; ++j) acc[i][j] = (v8f){0, 0, 0, 0, 0, 0, 0, 0};
+            for (int k = 0; k < K8; k += 8) {
+                const v8f a0 = ld8(xr[0] + k), a1 = ld8(xr[1] + k);
+                for (int j = 0; j < 4; ++j) {
+                    const v8f w = ld8(wr[j] + k);
+                    acc[0][j] += a0 * w;
+                    acc[1][j] += a1 * w;
+                }
+            }
+            for (int i = 0; i < mc; ++i)
+                for (int j = 0; j < nc; ++j) {
+                    float s = hsum8(acc[i][j]);
+                    for (int k = K8; k < K; ++k) s += xr[i][k] * wr[j][k];
+                    if (bias) s += bias[n0 + j];
+                    y[(size_t)(m0 + i) * N + n0 + j] = s;
+                }
+        }
+    }
+}
+
+static float silu_f(float v) { return (float)((double)v / (1.0 + exp(-(double)v))); }
+static float sigmoid_f(float v) { return (float)(1.0 / (1.0 + exp(-(double)v))); }
+
+static float* fbuf(size_t n) { return (float*)malloc(n * sizeof(float)); }
+
+/* ------------------------------------------------------------------------ */
+/* Rel-pos MHSA: relpos_attention.cpp:162-306                                */
+/* ------------------------------------------------------------------------ */
+
+void orc_relpos_attention(const orc_layer* L, const float* x, int B, int T,
+                          const float* pe, const int* valid, float* out) {
+    const int D = L->D, H = L->H, dk = D / H, P = 2 * T - 1;
+    const int64_t M = (int64_t)B * T;
+    const float scale = 1.0f / sqrtf((float)dk);
+    float* q = fbuf((size_t)M * D);
+    float* k = fbuf((size_t)M * D);
+    float* v = fbuf((size_t)M * D);
+    float* p = fbuf((size_t)P * D);
+    float* ctx = fbuf((size_t)M * D);
+    orc_linear(x, M, D, L->wq, D, L->bq, q);                  /* :191 */
+    orc_linear(x, M, D, L->wk, D, L->bk, k);                  /* :192 */
+    orc_linear(x, M, D, L->wv, D, L->bv, v);                  /* :193 */
+    orc_linear(pe, P, D, L->wpos, D, NULL, p);                /* :194, no bias */
+
+#pragma omp parallel
+    {
+        double* sc = (double*)malloc(sizeof(double) * (size_t)T);
+        float* qu = fbuf((size_t)dk);
+        float* qv = fbuf((size_t)dk);
+#pragma omp for collapse(3) schedule(static)
+        for (int b = 0; b < B; ++b)
+            for (int h = 0; h < H; ++h)
+                for (int i = 0; i < T; ++i) {
+                    const int vl = valid ? valid[b] : T;
+                    float* cr = ctx + ((size_t)b * T + i) * D + (size_t)h * dk;
+                    if (i >= vl) {                            /* :291-302 query mask */
+                        for (int c = 0; c < dk; ++c) cr[c] = 0.f;
+                        continue;
+                    }
+                    const float* qr = q + ((size_t)b * T + i) * D + (size_t)h * dk;
+                    for (int c = 0; c < dk; ++c) {            /* :213-220 */
+                        qu[c] = qr[c] + L->pos_bias_u[h * dk + c];
+                        qv[c] = qr[c] + L->pos_bias_v[h * dk + c];
+                    }
+                    double mx = -INFINITY;
+                    for (int j = 0; j < T; ++j) {
+                        if (j >= vl) { sc[j] = -INFINITY; continue; }   /* :252-277 key mask */
+                        const float* kr = k + ((size_t)b * T + j) * D + (size_t)h * dk;
+                        /* rel_shift (:226-238): bd_shift[i][j] = bd[i][T-1-i+j] */
+                        const float* pr = p + (size_t)(T - 1 - i + j) * D + (size_t)h * dk;
+                        float ac = 0.f, bd = 0.f;
+                        for (int c = 0; c < dk; ++c) { ac += qu[c] * kr[c]; bd += qv[c] * pr[c]; }
+                        const float s = (ac + bd) * scale;    /* softmax(scale*scores + mask) */
+                        sc[j] = s;
+                        if (s > mx) mx = s;
+                    }
+                    double den = 0.0;
+                    for (int j = 0; j < vl; ++j) { sc[j] = exp(sc[j] - mx); den += sc[j]; }
+                    for (int c = 0; c < dk; ++c) {
+                        double acc = 0.0;
+                        for (int j = 0; j < vl; ++j)
+                            acc += sc[j] * v[((size_t)b * T + j) * D + (size_t)h * dk + c];
+                        cr[c] = (float)(acc / den);
+                    }
+                }
+        free(sc);
+        free(qu);
+        free(qv);
+    }
+    orc_linear(ctx, M, D, L->wo, D, L->bo, out);              /* :305 */
+    free(q); free(k); free(v); free(p); free(ctx);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Conv module: conformer.cpp:38-164 (batch_norm variant, symmetric pad)     */
+/* ------------------------------------------------------------------------ */
+
+void orc_conv_module(const orc_layer* L, const float* c, int B, int T,
+                     const int* valid, float* out) {
+    const int D = L->D, K = L->K, pad = (K - 1) / 2;
+    const int64_t M = (int64_t)B * T;
+    float* y = fbuf((size_t)M * 2 * D);
+    float* g = fbuf((size_t)M * D);
+    float* n = fbuf((size_t)M * D);
+    float* bsc = fbuf((size_t)D);
+    float* bsh = fbuf((size_t)D);
+    orc_linear(c, M, D, L->pw1_w, 2 * D, L->pw1_b, y);        /* :48-53 */
+#pragma omp parallel for schedule(static)
+    for (int64_t m = 0; m < M; ++m) {                          /* :55-80 GLU + pad mask */
+        const int b = (int)(m / T), t = (int)(m % T);
+        const int vl = valid ? valid[b] : T;
+        for (int ch = 0; ch < D; ++ch) {
+            const float a = y[m * 2 * D + ch], gate = y[m * 2 * D + D + ch];
+            g[m * D + ch] = (t < vl) ? a * sigmoid_f(gate) : 0.f;
+        }
+    }
+    for (int ch = 0; ch < D; ++ch) {                           /* :134-154 BN fold */
+        bsc[ch] = L->bn_g[ch] / sqrtf(L->bn_var[ch] + 1e-5f);
+        bsh[ch] = L->bn_b[ch] - L->bn_mean[ch] * bsc[ch];
+    }
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int b = 0; b < B; ++b)
+        for (int t = 0; t < T; ++t)
+            for (int ch = 0; ch < D; ++ch) {                   /* :81-124 depthwise, :157 SiLU */
+                float acc = 0.f;
+                for (int kk = 0; kk < K; ++kk) {
+                    const int ts = t + kk - pad;
+                    if (ts < 0 || ts >= T) continue;
+                    acc += L->dw_w[ch * K + kk] * g[((size_t)b * T + ts) * D + ch];
+                }
+                if (L->dw_b) acc += L->dw_b[ch];
+                float nv = acc * bsc[ch];
+                nv = nv + bsh[ch];
+                n[((size_t)b * T + t) * D + ch] = silu_f(nv);
+            }
+    orc_linear(n, M, D, L->pw2_w, D, L->pw2_b, out);          /* :158-162 */
+    free(y); free(g); free(n); free(bsc); free(bsh);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Conformer layer: conformer.cpp:285-353                                    */
+/* ------------------------------------------------------------------------ */
+
+static void ffn(const float* xin, int64_t M, int D, int FF, const float* w1,
+                const float* b1, const float* w2, const float* b2, float* out) {
+    float* h = fbuf((size_t)M * FF);
+    orc_linear(xin, M, D, w1, FF, b1, h);
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < M * FF; ++i) h[i] = silu_f(h[i]);
+    orc_linear(h, M, FF, w2, D, b2, out);
+    free(h);
+}
+
+void orc_conformer_layer(const orc_layer* L, const float* x, int B, int T,
+                         const float* pe, const int* valid, float* out,
+                         float* conv_out) {
+    const int D = L->D;
+    const int64_t M = (int64_t)B * T, MD = M * D;
+    const float eps = 1e-5f;
+    float* r = fbuf((size_t)MD);
+    float* t1 = fbuf((size_t)MD);
+    float* t2 = fbuf((size_t)MD);
+    /* Stage A: r = x + 0.5*FFN1(LN(x)) */
+    orc_layer_norm(x, M, D, L->ff1_ln_g, L->ff1_ln_b, eps, t1);
+    ffn(t1, M, D, L->FF, L->ff1_w1, L->ff1_b1, L->ff1_w2, L->ff1_b2, t2);
+    for (int64_t i = 0; i < MD; ++i) r[i] = x[i] + t2[i] * 0.5f;
+    /* Stage B: r += MHSA(LN(r)) */
+    orc_layer_norm(r, M, D, L->att_ln_g, L->att_ln_b, eps, t1);
+    orc_relpos_attention(L, t1, B, T, pe, valid, t2);
+    for (int64_t i = 0; i < MD; ++i) r[i] += t2[i];
+    /* Stage C: r += conv(LN(r)) */
+    orc_layer_norm(r, M, D, L->conv_ln_g, L->conv_ln_b, eps, t1);
+    orc_conv_module(L, t1, B, T, valid, t2);
+    if (conv_out) memcpy(conv_out, t2, (size_t)MD * sizeof(float));
+    for (int64_t i = 0; i < MD; ++i) r[i] += t2[i];
+    /* Stage D: r += 0.5*FFN2(LN(r)); out = LN(r) */
+    orc_layer_norm(r, M, D, L->ff2_ln_g, L->ff2_ln_b, eps, t1);
+    ffn(t1, M, D, L->FF, L->ff2_w1, L->ff2_b1, L->ff2_w2, L->ff2_b2, t2);
+    for (int64_t i = 0; i < MD; ++i) r[i] += t2[i] * 0.5f;
+    orc_layer_norm(r, M, D, L->out_ln_g, L->out_ln_b, eps, out);
+    free(r); free(t1); free(t2);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Subsampling: subsampling.cpp:25-46, :48-240, :242-386                     */
+/* ------------------------------------------------------------------------ */
+
+int orc_subsampled_len(int T) {
+    int t = T;
+    for (int s = 0; s < 3; ++s) t = (t + 2 - 3) / 2 + 1;
+    return t;
+}
+
+int orc_valid_out_len(int T, int in_valid) {
+    int v = in_valid >= 0 ? in_valid : T - 1;
+    for (int s = 0; s < 3; ++s) v = (v + 2 - 3) / 2 + 1;
+    return v;
+}
+
+/* 3x3 stride-2 pad-1 depthwise conv over a channels-last [Ti][Fi][C] map,
+ * reading rows t >= vmask as zero; output channels-last [To][Fo][C] + bias. */
+static void dw3x3s2(const float* in, int Ti, int Fi, int C, int vmask,
+                    const float* w, const float* bias, float* out, int To, int Fo) {
+    for (int t = 0; t < To; ++t)
+        for (int f = 0; f < Fo; ++f)
+            for (int c = 0; c < C; ++c) {
+                float acc = 0.f;
+                for (int kh = 0; kh < 3; ++kh) {
+                    const int ti = 2 * t - 1 + kh;
+                    if (ti < 0 || ti >= Ti || ti >= vmask) continue;
+                    for (int kw = 0; kw < 3; ++kw) {
+                        const int fi = 2 * f - 1 + kw;
+                        if (fi < 0 || fi >= Fi) continue;
+                        acc += w[c * 9 + kh * 3 + kw] * in[((size_t)ti * Fi + fi) * C + c];
+                    }
+                }
+                out[((size_t)t * Fo + f) * C + c] = acc + bias[c];
+            }
+}
+
+int orc_subsampling(const orc_subsampling_w* S, const float* mel, int B, int F,
+                    int T, const int* valid_in, int stage_masks, float* out,
+                    int* valid_out) {
+    const int C = S->C, D = S->D;
+    const int T1 = (T - 1) / 2 + 1, F1 = (F - 1) / 2 + 1;
+    const int T2 = (T1 - 1) / 2 + 1, F2 = (F1 - 1) / 2 + 1;
+    const int T3 = (T2 - 1) / 2 + 1, F3 = (F2 - 1) / 2 + 1;
+    float* flat = fbuf((size_t)B * T3 * C * F3);
+    for (int b = 0; b < B; ++b) {
+        const int v0 = valid_in ? valid_in[b] : T - 1;
+        const int v1 = (v0 + 2 - 3) / 2 + 1, v2 = (v1 + 2 - 3) / 2 + 1;
+        const int vo = orc_valid_out_len(T, valid_in ? valid_in[b] : -1);
+        valid_out[b] = vo > T3 ? T3 : vo;
+        const int m0 = stage_masks ? v0 : T, m1 = stage_masks ? v1 : T1, m2 = stage_masks ? v2 : T2;
+        const float* mb = mel + (size_t)b * F * T;
+        float* a1 = fbuf((size_t)T1 * F1 * C);
+        float* a2 = fbuf((size_t)T2 * F2 * C);
+        float* a2p = fbuf((size_t)T2 * F2 * C);
+        float* a3 = fbuf((size_t)T3 * F3 * C);
+        float* a3p = fbuf((size_t)T3 * F3 * C);
+        /* conv.0: Conv2d(1->C, 3x3, s2, p1) + bias + ReLU (:143-157); H=time, W=feat */
+#pragma omp parallel for collapse(2) schedule(static)
+        for (int t = 0; t < T1; ++t)
+            for (int f = 0; f < F1; ++f)
+                for (int c = 0; c < C; ++c) {
+                    float acc = 0.f;
+                    for (int kh = 0; kh < 3; ++kh) {
+                        const int ti = 2 * t - 1 + kh;
+                        if (ti < 0 || ti >= T || ti >= m0) continue;
+                        for (int kw = 0; kw < 3; ++kw) {
+                            const int fi = 2 * f - 1 + kw;
+                            if (fi < 0 || fi >= F) continue;
+                            acc += S->w0[c * 9 + kh * 3 + kw] * mb[(size_t)fi * T + ti];
+                        }
+                    }
+                    acc += S->b0[c];
+                    a1[((size_t)t * F1 + f) * C + c] = acc > 0.f ? acc : 0.f;
+                }
+        /* conv.2 depthwise + bias, conv.3 pointwise + bias + ReLU (:159-192) */
+        dw3x3s2(a1, T1, F1, C, m1, S->w2, S->b2, a2, T2, F2);
+        orc_linear(a2, (int64_t)T2 * F2, C, S->w3, C, S->b3, a2p);
+        for (size_t i = 0; i < (size_t)T2 * F2 * C; ++i) a2p[i] = a2p[i] > 0.f ? a2p[i] : 0.f;
+        /* conv.5 depthwise + bias, conv.6 pointwise + bias + ReLU */
+        dw3x3s2(a2p, T2, F2, C, m2, S->w5, S->b5, a3, T3, F3);
+        orc_linear(a3, (int64_t)T3 * F3, C, S->w6, C, S->b6, a3p);
+        for (size_t i = 0; i < (size_t)T3 * F3 * C; ++i) a3p[i] = a3p[i] > 0.f ? a3p[i] : 0.f;
+        /* flatten channel-major per time step (idx c*F'+f, :194-202) + mask (:204-230) */
+        for (int t = 0; t < T3; ++t)
+            for (int c = 0; c < C; ++c)
+                for (int f = 0; f < F3; ++f)
+                    flat[((size_t)b * T3 + t) * C * F3 + (size_t)c * F3 + f] =
+                        (t < valid_out[b]) ? a3p[((size_t)t * F3 + f) * C + c] : 0.f;
+        free(a1); free(a2); free(a2p); free(a3); free(a3p);
+    }
+    orc_linear(flat, (int64_t)B * T3, C * F3, S->wout, D, S->bout, out);  /* :232-236 */
+    free(flat);
+    return T3;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Encoder: encoder.cpp:97-167                                               */
+/* ------------------------------------------------------------------------ */
+
+int orc_encoder_forward(const orc_subsampling_w* S, const orc_layer* layers,
+                        int n_layers, int xscaling, const float* mel, int B,
+                        int F, int T, const int* valid_in, int stage_masks,
+                        float* out, int* valid_out, float* capture) {
+    const int D = S->D;
+    const int Tp = orc_subsampled_len(T);
+    const size_t MD = (size_t)B * Tp * D;
+    float* x = fbuf(MD);
+    float* y = fbuf(MD);
+    orc_subsampling(S, mel, B, F, T, valid_in, stage_masks, x, valid_out);
+    if (xscaling) {                                            /* :123 / :186 */
+        const float s = sqrtf((float)D);
+        for (size_t i = 0; i < MD; ++i) x[i] *= s;
+    }
+    float* pe = fbuf((size_t)(2 * Tp - 1) * D);
+    orc_rel_pos_encoding(Tp, D, pe);
+    for (int l = 0; l < n_layers; ++l) {
+        orc_conformer_layer(&layers[l], x, B, Tp, pe, valid_out, y, NULL);
+        if (capture) memcpy(capture + (size_t)l * MD, y, MD * sizeof(float));
+        float* tmp = x; x = y; y = tmp;
+    }
+    memcpy(out, x, MD * sizeof(float));
+    free(x); free(y); free(pe);
+    return Tp;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Output heads                                                              */
+/* ------------------------------------------------------------------------ */
+
+void orc_ctc_head(const float* enc, int T, int D, const float* W, const float* b,
+                  int V, float* logprobs, int32_t* argmax) {
+    orc_linear(enc, T, D, W, V, b, logprobs);                  /* ctc_decoder.cpp:98-102 */
+    for (int t = 0; t < T; ++t) {
+        float* r = logprobs + (size_t)t * V;
+        float mx = r[0];
+        for (int v = 1; v < V; ++v) if (r[v] > mx) mx = r[v];
+        double den = 0.0;
+        for (int v = 0; v < V; ++v) den += exp((double)r[v] - (double)mx);
+        for (int v = 0; v < V; ++v)                            /* :107-108 log(softmax) */
+            r[v] = (float)(((double)r[v] - (double)mx) - log(den));
+        int best = 0;
+        for (int v = 1; v < V; ++v) if (r[v] > r[best]) best = v;   /* search.cpp:57-61 */
+        argmax[t] = best;
+    }
+}
+
+int orc_ctc_greedy(const int32_t* argmax, int T, int blank_id, int32_t* out) {
+    int n = 0;
+    int32_t prev = blank_id;
+    for (int t = 0; t < T; ++t) {                              /* search.cpp:63 */
+        const int32_t p = argmax[t];
+        if ((p != prev || prev == blank_id) && p != blank_id) out[n++] = p;
+        prev = p;
+    }
+    return n;
+}
+
+void orc_tdt_joint_argmax(const float* enc, int T, int D, const float* Wenc,
+                          const float* benc, int Hj, const float* g, int P,
+                          const float* Wpred, const float* bpred,
+                          const float* Wout, const float* bout, int n_tok,
+                          int n_dur, float* logits, int32_t* tok, int32_t* dur) {
+    const int V = n_tok + n_dur;
+    float* ep = fbuf((size_t)T * Hj);
+    float* pp = fbuf((size_t)Hj);
+    float* f = fbuf((size_t)T * Hj);
+    orc_linear(enc, T, D, Wenc, Hj, benc, ep);                 /* joint.cpp:37-63 */
+    orc_linear(g, 1, P, Wpred, Hj, bpred, pp);                 /* joint.cpp:89-93 */
+    for (int t = 0; t < T; ++t)
+        for (int h = 0; h < Hj; ++h) {                         /* :94-95 */
+            const float s = ep[(size_t)t * Hj + h] + pp[h];
+            f[(size_t)t * Hj + h] = s > 0.f ? s : 0.f;
+        }
+    orc_linear(f, T, Hj, Wout, V, bout, logits);               /* :96-100 */
+    for (int t = 0; t < T; ++t) {                              /* tdt.cpp:76-79 */
+        const float* r = logits + (size_t)t * V;
+        int bt = 0, bd = 0;
+        for (int i = 1; i < n_tok; ++i) if (r[i] > r[bt]) bt = i;
+        for (int i = 1; i < n_dur; ++i) if (r[n_tok + i] > r[n_tok + bd]) bd = i;
+        tok[t] = bt;
+        dur[t] = bd;
+    }
+    free(ep); free(pp); free(f);
+}

@@ -1,0 +1,143 @@
+/*
+ * pk_oracle.h -- CPU restatement of the parakeet.cpp FastConformer encoder path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the parity checker for the HIP
+ * encoder and the "port" CPU baseline that bench.py times beside it.  Only the
+ * tests, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it;
+ * the product library never links or calls it.
+ *
+ * Every function names the reference file:line it restates.  The reference's
+ * own arithmetic lives in ggml (an un-vendored submodule that is absent), so
+ * the restatement computes the exact math of each graph op in f32 storage with
+ * f32 (dot products) or f64 (norm/softmax statistics) accumulation.
+ *
+ * Layouts (all row-major, innermost last):
+ *   activations  [B][T][D]            (ggml ne [D,T,B])
+ *   weights      [N][K]               (ggml ne [K,N]; quant blocks along K)
+ *   pos_emb      [2T-1][D]
+ *   mel          [B][n_mels][T_max]   (MelBatch layout, src/encoder.hpp:17-23)
+ */
+#ifndef PK_ORACLE_H
+#define PK_ORACLE_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ggml type ids used by the GGUF weight layout. */
+enum { ORC_F32 = 0, ORC_F16 = 1, ORC_Q8_0 = 8, ORC_Q4_K = 12 };
+
+void     orc_set_threads(int n);
+int      orc_get_threads(void);
+
+/* IEEE binary16 <-> binary32, round-to-nearest-even (ggml FP32_TO_FP16). */
+float    orc_f16_to_f32(uint16_t h);
+uint16_t orc_f32_to_f16(float f);
+
+/* Bytes of one row of ne0 elements in the given type (0 if ne0 is not a
+ * multiple of the block size or the type is unknown). */
+int64_t  orc_row_bytes(int type, int64_t ne0);
+
+/* Dequantise n elements (n a multiple of the block size) to f32.
+ * q8_0: 34-byte block {f16 d; i8 q[32]}, w = d*q.
+ * q4_K: 144-byte super-block {f16 d; f16 dmin; u8 scales[12]; u8 qs[128]},
+ *       w = d*sc_j*q - dmin*m_j (ggml v0.13.0 block_q4_K). Returns 0 on success. */
+int      orc_dequantize(int type, const void* src, float* dst, int64_t n);
+/* Quantise n f32 values into the given type (f16, q8_0, q4_K). Any valid
+ * encoding is acceptable for q4_K (only dequantisation must match ggml). */
+int      orc_quantize(int type, const float* src, void* dst, int64_t n);
+
+/* pos_enc.cpp:10-34 -- table [2T-1][d] for positions +(T-1) .. -(T-1). */
+void orc_rel_pos_encoding(int T, int d, float* out);
+
+/* conformer.cpp:300-307 -- y = (x-mean)/sqrt(var+eps)*g + b over the last dim. */
+void orc_layer_norm(const float* x, int64_t M, int D, const float* g,
+                    const float* b, float eps, float* y);
+
+/* y[M][N] = x[M][K] . W[N][K]^T (+ bias[N]) -- ggml_mul_mat(W, x) (+ ggml_add). */
+void orc_linear(const float* x, int64_t M, int K, const float* W, int N,
+                const float* bias, float* y);
+
+/* One conformer layer's weights, dequantised to f32.  Optional biases may be
+ * NULL (bias=False checkpoints, relpos_attention.cpp:126-137). */
+typedef struct {
+    int D, H, FF, K;
+    const float *ff1_ln_g, *ff1_ln_b, *ff1_w1, *ff1_b1, *ff1_w2, *ff1_b2;
+    const float *att_ln_g, *att_ln_b;
+    const float *wq, *bq, *wk, *bk, *wv, *bv, *wo, *bo, *wpos;
+    const float *pos_bias_u, *pos_bias_v;              /* [H][dk] */
+    const float *conv_ln_g, *conv_ln_b;
+    const float *pw1_w, *pw1_b;                         /* [2D][D], [2D] */
+    const float *dw_w, *dw_b;                           /* [D][K], [D] */
+    const float *bn_g, *bn_b, *bn_mean, *bn_var;        /* [D] each */
+    const float *pw2_w, *pw2_b;                         /* [D][D], [D] */
+    const float *ff2_ln_g, *ff2_ln_b, *ff2_w1, *ff2_b1, *ff2_w2, *ff2_b2;
+    const float *out_ln_g, *out_ln_b;
+} orc_layer;
+
+/* dw_striding subsampling weights (torch layouts == GGUF memory order). */
+typedef struct {
+    int C, D;                      /* conv channels, d_model */
+    const float *w0, *b0;          /* conv.0  [C][1][3][3], [C] */
+    const float *w2, *b2;          /* conv.2  depthwise [C][1][3][3] */
+    const float *w3, *b3;          /* conv.3  pointwise [C][C] */
+    const float *w5, *b5;          /* conv.5  depthwise */
+    const float *w6, *b6;          /* conv.6  pointwise */
+    const float *wout, *bout;      /* out     [D][C*F'], [D] */
+} orc_subsampling_w;
+
+/* relpos_attention.cpp:162-306 (batched) / :40-160 (B=1).  x is the already
+ * normalised input [B][T][D]; pe [2T-1][D]; valid[B]; out [B][T][D]. */
+void orc_relpos_attention(const orc_layer* L, const float* x, int B, int T,
+                          const float* pe, const int* valid, float* out);
+
+/* conformer.cpp:38-164 -- conv module after norm_conv. */
+void orc_conv_module(const orc_layer* L, const float* c, int B, int T,
+                     const int* valid, float* out);
+
+/* conformer.cpp:285-353 -- full layer.  If conv_out != NULL it receives the
+ * conv-module output (forward_with_conv, conformer.cpp:434). */
+void orc_conformer_layer(const orc_layer* L, const float* x, int B, int T,
+                         const float* pe, const int* valid, float* out,
+                         float* conv_out);
+
+/* subsampling.cpp:25-46 */
+int  orc_valid_out_len(int T, int in_valid);
+int  orc_subsampled_len(int T);
+
+/* subsampling.cpp:48-240 (stage_masks=1, batched semantics) and :242-386
+ * (stage_masks=0, scalar semantics).  mel [B][F][T]; valid_in[b] is the entry
+ * valid length (NULL -> T-1 per item).  out [B][T'][D]; valid_out[B]. */
+int  orc_subsampling(const orc_subsampling_w* S, const float* mel, int B, int F,
+                     int T, const int* valid_in, int stage_masks, float* out,
+                     int* valid_out);
+
+/* encoder.cpp:97-167.  out [B][T'][D] (time-major, uncompacted).
+ * capture (optional) receives every layer output [L][B][T'][D]. */
+int  orc_encoder_forward(const orc_subsampling_w* S, const orc_layer* layers,
+                         int n_layers, int xscaling, const float* mel, int B,
+                         int F, int T, const int* valid_in, int stage_masks,
+                         float* out, int* valid_out, float* capture);
+
+/* ctc_decoder.cpp:34-116 -- log_softmax(enc . W^T + b) over V, enc [T][D]
+ * time-major; argmax with first-max tie-break (search.cpp:57-61). */
+void orc_ctc_head(const float* enc, int T, int D, const float* W, const float* b,
+                  int V, float* logprobs, int32_t* argmax);
+/* search.cpp:21-90 -- collapse repeats and blanks; returns the token count. */
+int  orc_ctc_greedy(const int32_t* argmax, int T, int blank_id, int32_t* out);
+
+/* joint.cpp:37-63 enc_proj, :65-104 step logits, tdt.cpp:76-79 split argmax.
+ * For every frame t: f = relu(enc_proj[t] + pred_proj), logits = Wout f + bout,
+ * tok[t] = argmax logits[0, n_tok), dur[t] = argmax logits[n_tok, n_tok+n_dur). */
+void orc_tdt_joint_argmax(const float* enc, int T, int D, const float* Wenc,
+                          const float* benc, int Hj, const float* g, int P,
+                          const float* Wpred, const float* bpred,
+                          const float* Wout, const float* bout, int n_tok,
+                          int n_dur, float* logits, int32_t* tok, int32_t* dur);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,327 @@
+// extern "C" boundary (include/pkx.h).  Every entry point catches all C++
+// exceptions and reports them through a thread-local last-error string, the
+// same no-throw convention as the reference C API (src/parakeet_capi.cpp:207-225).
+#include <cstring>
+#include <string>
+
+#include "../../include/pkx.h"
+#include "model.hpp"
+
+struct pkx_model {
+    pkx_config cfg;
+    int precision;
+    std::unique_ptr<pkx::Model> impl;
+};
+
+namespace {
+thread_local std::string g_last_error;
+
+template <typename F>
+int guarded(F&& f) {
+    try {
+        f();
+        g_last_error.clear();
+        return 0;
+    } catch (const std::exception& e) {
+        g_last_error = e.what();
+    } catch (...) {
+        g_last_error = "unknown error";
+    }
+    return 1;
+}
+
+hipStream_t st(void* s) { return (hipStream_t)s; }
+
+void need(bool ok, const char* what) {
+    if (!ok) throw std::invalid_argument(what);
+}
+
+pkx::ModelConfig to_internal(const pkx_config& c) {
+    pkx::ModelConfig m;
+    m.d_model = c.d_model;
+    m.n_layers = c.n_layers;
+    m.n_heads = c.n_heads;
+    m.ff_dim = c.ff_dim;
+    m.conv_kernel = c.conv_kernel;
+    m.n_mels = c.n_mels;
+    m.sub_channels = c.sub_channels;
+    m.xscaling = c.xscaling;
+    m.vocab_size = c.vocab_size;
+    m.n_durations = c.n_durations;
+    return m;
+}
+
+pkx_config to_public(const pkx::ModelConfig& m) {
+    pkx_config c;
+    c.d_model = m.d_model;
+    c.n_layers = m.n_layers;
+    c.n_heads = m.n_heads;
+    c.ff_dim = m.ff_dim;
+    c.conv_kernel = m.conv_kernel;
+    c.n_mels = m.n_mels;
+    c.sub_channels = m.sub_channels;
+    c.xscaling = m.xscaling;
+    c.vocab_size = m.vocab_size;
+    c.n_durations = m.n_durations;
+    return c;
+}
+}  // namespace
+
+extern "C" {
+
+int pkx_abi_version(void) { return PKX_ABI_VERSION; }
+const char* pkx_last_error(void) { return g_last_error.c_str(); }
+
+int pkx_device_count(int* n) {
+    return guarded([&] { need(n, "null n"); PKX_HIP(hipGetDeviceCount(n)); });
+}
+int pkx_malloc(void** dev, size_t bytes) {
+    return guarded([&] { need(dev, "null out"); PKX_HIP(hipMalloc(dev, bytes ? bytes : 16)); });
+}
+int pkx_free(void* dev) {
+    return guarded([&] { if (dev) PKX_HIP(hipFree(dev)); });
+}
+int pkx_memcpy_h2d(void* dst, const void* src, size_t bytes, void* s) {
+    return guarded([&] {
+        PKX_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, st(s)));
+        PKX_HIP(hipStreamSynchronize(st(s)));
+    });
+}
+int pkx_memcpy_d2h(void* dst, const void* src, size_t bytes, void* s) {
+    return guarded([&] {
+        PKX_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, st(s)));
+        PKX_HIP(hipStreamSynchronize(st(s)));
+    });
+}
+int pkx_memcpy_d2d(void* dst, const void* src, size_t bytes, void* s) {
+    return guarded([&] { PKX_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, st(s))); });
+}
+int pkx_stream_create(void** s) {
+    return guarded([&] {
+        need(s, "null out");
+        hipStream_t h;
+        PKX_HIP(hipStreamCreateWithFlags(&h, hipStreamNonBlocking));
+        *s = h;
+    });
+}
+int pkx_stream_destroy(void* s) {
+    return guarded([&] { if (s) PKX_HIP(hipStreamDestroy(st(s))); });
+}
+int pkx_stream_synchronize(void* s) {
+    return guarded([&] { PKX_HIP(hipStreamSynchronize(st(s))); });
+}
+int pkx_event_create(void** e) {
+    return guarded([&] {
+        need(e, "null out");
+        hipEvent_t h;
+        PKX_HIP(hipEventCreate(&h));
+        *e = h;
+    });
+}
+int pkx_event_destroy(void* e) {
+    return guarded([&] { if (e) PKX_HIP(hipEventDestroy((hipEvent_t)e)); });
+}
+int pkx_event_record(void* e, void* s) {
+    return guarded([&] { PKX_HIP(hipEventRecord((hipEvent_t)e, st(s))); });
+}
+int pkx_event_elapsed_ms(float* ms, void* a, void* b) {
+    return guarded([&] {
+        need(ms && a && b, "null argument");
+        PKX_HIP(hipEventSynchronize((hipEvent_t)b));
+        PKX_HIP(hipEventElapsedTime(ms, (hipEvent_t)a, (hipEvent_t)b));
+    });
+}
+
+int pkx_model_load_gguf(const char* path, int precision, pkx_model** out) {
+    return guarded([&] {
+        need(path && out, "null argument");
+        *out = nullptr;
+        std::unique_ptr<pkx::Model> impl = pkx::load_gguf(path, precision);
+        pkx_model* m = new pkx_model;
+        m->cfg = to_public(impl->config());
+        m->precision = impl->precision();
+        m->impl = std::move(impl);
+        *out = m;
+    });
+}
+
+int pkx_model_create(const pkx_config* cfg, int precision, pkx_model** out) {
+    return guarded([&] {
+        need(cfg && out, "null argument");
+        need(precision >= -1 && precision <= 1, "precision must be PKX_PREC_AUTO/F32/F16");
+        *out = nullptr;
+        pkx_model* m = new pkx_model;
+        m->cfg = *cfg;
+        m->precision = precision;
+        try {
+            m->impl.reset(new pkx::Model(to_internal(*cfg), precision));
+        } catch (...) {
+            delete m;
+            throw;
+        }
+        *out = m;
+    });
+}
+
+int pkx_model_set_tensor(pkx_model* m, const char* name, int gtype, int n_dims, const int64_t* ne,
+                         const void* data, size_t nbytes) {
+    return guarded([&] {
+        need(m && name && ne && data, "null argument");
+        m->impl->set_tensor(name, gtype, n_dims, ne, data, nbytes);
+    });
+}
+
+int pkx_model_finalize(pkx_model* m) {
+    return guarded([&] {
+        need(m, "null model");
+        m->impl->finalize();
+        m->precision = m->impl->precision();
+    });
+}
+
+int pkx_model_free(pkx_model* m) {
+    return guarded([&] { delete m; });
+}
+
+int pkx_model_info(pkx_model* m, pkx_config* cfg, int* precision, int* has_ctc, int* has_joint) {
+    return guarded([&] {
+        need(m, "null model");
+        if (cfg) *cfg = to_public(m->impl->config());
+        if (precision) *precision = m->impl->precision();
+        if (has_ctc) *has_ctc = m->impl->has_ctc() ? 1 : 0;
+        if (has_joint) *has_joint = m->impl->has_joint() ? 1 : 0;
+    });
+}
+
+int pkx_subsampled_len(int T) { return pkx::subsampled_len(T); }
+int pkx_valid_out_len(int T, int in_valid) { return pkx::valid_out_len(T, in_valid); }
+
+int pkx_encoder_forward(pkx_model* m, const float* mel, int B, int T_max, const int* valid_T, int mask_mode,
+                        float* out, int* T_out, int* valid_out, float* capture, void* s) {
+    return guarded([&] {
+        need(m && mel && out, "null argument");
+        need(mask_mode == PKX_MASK_BATCHED || mask_mode == PKX_MASK_SCALAR, "bad mask_mode");
+        const int Tp = m->impl->encoder_forward(mel, B, T_max, valid_T, mask_mode == PKX_MASK_BATCHED, out,
+                                                valid_out, capture, st(s));
+        if (T_out) *T_out = Tp;
+    });
+}
+
+int pkx_compact_channels_first(const float* x, int B, int T, int D, const int* valid, const int64_t* offs,
+                               float* out, void* s) {
+    return guarded([&] {
+        need(x && valid && offs && out, "null argument");
+        pkx::launch_compact_channels_first(x, B, T, D, valid, offs, out, st(s));
+    });
+}
+
+int pkx_subsampling_forward(pkx_model* m, const float* mel, int B, int T_max, const int* valid_T, int mask_mode,
+                            float* out, int* T_out, int* valid_out, void* s) {
+    return guarded([&] {
+        need(m && mel && out, "null argument");
+        need(mask_mode == PKX_MASK_BATCHED || mask_mode == PKX_MASK_SCALAR, "bad mask_mode");
+        const int Tp = m->impl->subsampling_forward(mel, B, T_max, valid_T, mask_mode == PKX_MASK_BATCHED, out,
+                                                    valid_out, st(s), false);
+        if (T_out) *T_out = Tp;
+    });
+}
+
+int pkx_conformer_layer_forward(pkx_model* m, int layer, const float* x, int B, int T, const int* valid,
+                                float* out, float* conv_out, void* s) {
+    return guarded([&] {
+        need(m && x && out, "null argument");
+        m->impl->conformer_layer_forward(layer, x, B, T, valid, out, conv_out, st(s));
+    });
+}
+
+int pkx_relpos_attention_forward(pkx_model* m, int layer, const float* x, int B, int T, const int* valid,
+                                 float* out, void* s) {
+    return guarded([&] {
+        need(m && x && out, "null argument");
+        m->impl->relpos_attention_forward(layer, x, B, T, valid, out, st(s));
+    });
+}
+
+int pkx_conv_module_forward(pkx_model* m, int layer, const float* c, int B, int T, const int* valid,
+                            float* out, void* s) {
+    return guarded([&] {
+        need(m && c && out, "null argument");
+        m->impl->conv_module_forward(layer, c, B, T, valid, out, st(s));
+    });
+}
+
+int pkx_ctc_forward(pkx_model* m, const float* enc, int64_t M, float* logprobs, int32_t* argmax, void* s) {
+    return guarded([&] {
+        need(m && enc && logprobs && argmax, "null argument");
+        m->impl->ctc_forward(enc, M, logprobs, argmax, st(s));
+    });
+}
+
+int pkx_tdt_joint_argmax(pkx_model* m, const float* enc, int64_t M, const float* g, float* logits, int32_t* tok,
+                         int32_t* dur, void* s) {
+    return guarded([&] {
+        need(m && enc && g && logits && tok && dur, "null argument");
+        m->impl->tdt_joint_argmax(enc, M, g, logits, tok, dur, st(s));
+    });
+}
+
+int pkx_dequantize(int gtype, const void* src, float* dst, int64_t n, void* s) {
+    return guarded([&] {
+        need(src && dst, "null argument");
+        pkx::launch_dequantize(gtype, src, dst, n, st(s));
+    });
+}
+
+int pkx_linear(int precision, int gtype, int N, int K, const void* host_w, size_t nbytes, const float* bias,
+               const float* x, int64_t M, float* y, void* s) {
+    return guarded([&] {
+        need(host_w && x && y, "null argument");
+        need(precision == PKX_PREC_F32 || precision == PKX_PREC_F16, "precision must be F32 or F16");
+        pkx::HostTensor t;
+        t.gtype = gtype;
+        t.n_dims = 2;
+        t.ne[0] = K;
+        t.ne[1] = N;
+        t.bytes.assign((const uint8_t*)host_w, (const uint8_t*)host_w + nbytes);
+        pkx::linear_raw((pkx::Precision)precision, t, N, K, bias, x, M, y, st(s));
+    });
+}
+
+int pkx_layernorm(const float* x, const float* g, const float* b, float* y, int64_t M, int D, float eps,
+                  void* s) {
+    return guarded([&] {
+        need(x && g && b && y, "null argument");
+        pkx::LnParams p;
+        p.x = x;
+        p.g = g;
+        p.b = b;
+        p.y = y;
+        p.M = M;
+        p.D = D;
+        p.eps = eps;
+        pkx::launch_layernorm(pkx::PREC_F32, p, st(s));
+    });
+}
+
+int pkx_rel_pos_encoding(int T, int D, float* out, void* s) {
+    return guarded([&] {
+        need(out && T > 0 && D > 0, "bad argument");
+        pkx::launch_rel_pos_encoding(pkx::PREC_F32, out, T, D, st(s));
+    });
+}
+
+int pkx_model_set_profiling(pkx_model* m, int on) {
+    return guarded([&] {
+        need(m, "null model");
+        m->impl->set_profiling(on != 0);
+    });
+}
+
+int pkx_model_profile_read(pkx_model* m, double* ms, int64_t* launches) {
+    return guarded([&] {
+        need(m, "null model");
+        m->impl->profile_read(ms, launches);
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,65 @@
+// Shared device/host helpers for the gfx950 encoder kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <stdexcept>
+#include <string>
+
+namespace pkx {
+
+typedef _Float16 f16;
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+typedef _Float16 half8v __attribute__((ext_vector_type(8)));
+typedef float float2v __attribute__((ext_vector_type(2)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+typedef int int4v __attribute__((ext_vector_type(4)));
+
+// ggml type ids (the GGUF weight layout)
+enum GgmlType : int { GT_F32 = 0, GT_F16 = 1, GT_Q8_0 = 8, GT_Q4_K = 12 };
+
+// Activation storage type of a compute precision mode.
+enum Precision : int { PREC_F32 = 0, PREC_F16 = 1 };
+
+struct HipError : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+inline void hip_check(hipError_t e, const char* what, const char* file, int line) {
+    if (e != hipSuccess) {
+        char buf[512];
+        std::snprintf(buf, sizeof(buf), "%s failed: %s (%s:%d)", what, hipGetErrorString(e), file, line);
+        throw HipError(buf);
+    }
+}
+#define PKX_HIP(x) ::pkx::hip_check((x), #x, __FILE__, __LINE__)
+#define PKX_LAUNCH_CHECK() ::pkx::hip_check(hipGetLastError(), "kernel launch", __FILE__, __LINE__)
+
+inline void require(bool ok, const std::string& msg) {
+    if (!ok) throw std::invalid_argument(msg);
+}
+
+__device__ __forceinline__ float silu_dev(float v) { return v / (1.0f + __expf(-v)); }
+__device__ __forceinline__ float sigmoid_dev(float v) { return 1.0f / (1.0f + __expf(-v)); }
+
+template <typename T> __device__ __forceinline__ T to_act(float v);
+template <> __device__ __forceinline__ float to_act<float>(float v) { return v; }
+template <> __device__ __forceinline__ f16 to_act<f16>(float v) { return (f16)v; }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+inline int cdiv(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
+__host__ __device__ __forceinline__ int cdiv_dev(int a, int b) { return (a + b - 1) / b; }
+
+}  // namespace pkx

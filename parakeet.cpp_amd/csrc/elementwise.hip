@@ -1,0 +1,475 @@
+// Memory-bound kernels of the encoder path (see elementwise.hpp for the
+// reference ops each one replaces).  All are single passes over HBM with
+// 16-byte (f32) / 8-byte (f16) vector accesses along the channel dim.
+#include "elementwise.hpp"
+
+namespace pkx {
+
+// ---------------------------------------------------------------------------
+// LayerNorm: one wave per row, the row held in registers (NV float4 per lane).
+// ---------------------------------------------------------------------------
+template <int NV>
+__device__ __forceinline__ void ln_row(float4v (&v)[NV], int lane, int D, const float* g,
+                                       const float* b, float eps) {
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c = (lane + 64 * i) * 4;
+        if (c < D) s += (v[i][0] + v[i][1]) + (v[i][2] + v[i][3]);
+    }
+    const float mean = wave_sum(s) / (float)D;
+    float s2 = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c = (lane + 64 * i) * 4;
+        if (c < D) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float d = v[i][e] - mean;
+                v[i][e] = d;
+                s2 += d * d;
+            }
+        }
+    }
+    const float rs = 1.0f / sqrtf(wave_sum(s2) / (float)D + eps);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c = (lane + 64 * i) * 4;
+        if (c < D) {
+            const float4v gg = *(const float4v*)(g + c);
+            const float4v bb = *(const float4v*)(b + c);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[i][e] = (v[i][e] * rs) * gg[e] + bb[e];
+        }
+    }
+}
+
+template <typename T> __device__ __forceinline__ void store4(T* p, const float4v& v);
+template <> __device__ __forceinline__ void store4<float>(float* p, const float4v& v) { *(float4v*)p = v; }
+template <> __device__ __forceinline__ void store4<f16>(f16* p, const float4v& v) {
+    half4v h = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+    *(half4v*)p = h;
+}
+
+// MODE 0: y = LN(x); MODE 1: y_f32 = LN(x), y = LN2(y_f32); MODE 2: y_f32 = LN(x).
+template <int NV, typename OutT, int MODE>
+__global__ __launch_bounds__(256) void layernorm_kernel(LnParams p) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= p.M) return;
+    const float* xr = p.x + row * p.D;
+    float4v v[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c = (lane + 64 * i) * 4;
+        v[i] = c < p.D ? *(const float4v*)(xr + c) : (float4v){0.f, 0.f, 0.f, 0.f};
+    }
+    ln_row<NV>(v, lane, p.D, p.g, p.b, p.eps);
+    if constexpr (MODE != 0) {
+        float* yr = p.y_f32 + row * p.D;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int c = (lane + 64 * i) * 4;
+            if (c < p.D) *(float4v*)(yr + c) = v[i];
+        }
+        if constexpr (MODE == 2) return;
+        ln_row<NV>(v, lane, p.D, p.g2, p.b2, p.eps);
+    }
+    OutT* yo = (OutT*)p.y + row * p.D;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c = (lane + 64 * i) * 4;
+        if (c < p.D) store4<OutT>(yo + c, v[i]);
+    }
+}
+
+template <int NV, typename OutT>
+static void ln_go(const LnParams& p, hipStream_t s) {
+    const dim3 grid(cdiv(p.M, 4));
+    if (p.y_f32 && p.y)
+        hipLaunchKernelGGL((layernorm_kernel<NV, OutT, 1>), grid, dim3(256), 0, s, p);
+    else if (p.y_f32)
+        hipLaunchKernelGGL((layernorm_kernel<NV, OutT, 2>), grid, dim3(256), 0, s, p);
+    else
+        hipLaunchKernelGGL((layernorm_kernel<NV, OutT, 0>), grid, dim3(256), 0, s, p);
+}
+
+template <typename OutT>
+static void ln_nv(const LnParams& p, hipStream_t s) {
+    const int nv = cdiv(p.D, 256);
+    if (nv <= 1) ln_go<1, OutT>(p, s);
+    else if (nv <= 2) ln_go<2, OutT>(p, s);
+    else if (nv <= 4) ln_go<4, OutT>(p, s);
+    else if (nv <= 8) ln_go<8, OutT>(p, s);
+    else if (nv <= 16) ln_go<16, OutT>(p, s);
+    else throw std::invalid_argument("layernorm: D > 4096");
+}
+
+void launch_layernorm(Precision prec, const LnParams& p, hipStream_t s) {
+    require(p.D % 4 == 0, "layernorm: D must be a multiple of 4");
+    if (p.M == 0) return;
+    if (prec == PREC_F16) ln_nv<f16>(p, s);
+    else ln_nv<float>(p, s);
+    PKX_LAUNCH_CHECK();
+}
+
+// ---------------------------------------------------------------------------
+// Depthwise conv1d + bias + folded BatchNorm + SiLU, sliding window over time
+// in registers; VEC channels per thread (half2 for f16), TT frames per block.
+// ---------------------------------------------------------------------------
+template <typename T, int VEC> struct Vec;
+template <> struct Vec<float, 1> {
+    static __device__ __forceinline__ void ld(const float* p, float* o) { o[0] = *p; }
+    static __device__ __forceinline__ void st(float* p, const float* o) { *p = o[0]; }
+};
+template <> struct Vec<f16, 2> {
+    static __device__ __forceinline__ void ld(const f16* p, float* o) {
+        const half2v h = *(const half2v*)p;
+        o[0] = (float)h[0];
+        o[1] = (float)h[1];
+    }
+    static __device__ __forceinline__ void st(f16* p, const float* o) {
+        half2v h = {(f16)o[0], (f16)o[1]};
+        *(half2v*)p = h;
+    }
+};
+
+template <typename T, int VEC, int K, int TT>
+__global__ __launch_bounds__(256) void dwconv_bn_silu_kernel(const T* in, T* out, const float* w,
+                                                             const float* dwb, const float* sc,
+                                                             const float* sh, int Tn, int D) {
+    const int c0 = (blockIdx.x * 256 + threadIdx.x) * VEC;
+    if (c0 >= D) return;
+    const int t0 = blockIdx.y * TT, b = blockIdx.z;
+    constexpr int PAD = (K - 1) / 2, NW = TT + K - 1;
+    const T* base = in + (int64_t)b * Tn * D + c0;
+    float win[NW][VEC];
+#pragma unroll
+    for (int r = 0; r < NW; ++r) {
+        const int t = t0 - PAD + r;
+        if (t >= 0 && t < Tn) {
+            Vec<T, VEC>::ld(base + (int64_t)t * D, win[r]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) win[r][e] = 0.f;
+        }
+    }
+    float wk[VEC][K], bias[VEC], scale[VEC], shift[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+#pragma unroll
+        for (int k = 0; k < K; ++k) wk[e][k] = w[(c0 + e) * K + k];
+        bias[e] = dwb ? dwb[c0 + e] : 0.f;
+        scale[e] = sc[c0 + e];
+        shift[e] = sh[c0 + e];
+    }
+    T* ob = out + (int64_t)b * Tn * D + c0;
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) {
+        const int t = t0 + tt;
+        if (t >= Tn) break;
+        float o[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+            float acc = 0.f;
+#pragma unroll
+            for (int k = 0; k < K; ++k) acc += wk[e][k] * win[tt + k][e];
+            const float y = (acc + bias[e]) * scale[e] + shift[e];
+            o[e] = silu_dev(y);
+        }
+        Vec<T, VEC>::st(ob + (int64_t)t * D, o);
+    }
+}
+
+template <typename ET, int VEC, int K>
+static void dw_go(const void* in, void* out, const float* w, const float* dwb, const float* sc,
+                  const float* sh, int B, int Tn, int D, hipStream_t s) {
+    constexpr int TT = 16;
+    const dim3 grid(cdiv(D / VEC, 256), cdiv(Tn, TT), B);
+    hipLaunchKernelGGL((dwconv_bn_silu_kernel<ET, VEC, K, TT>), grid, dim3(256), 0, s, (const ET*)in,
+                       (ET*)out, w, dwb, sc, sh, Tn, D);
+}
+
+template <typename ET, int VEC>
+static void dw_k(const void* in, void* out, const float* w, const float* dwb, const float* sc,
+                 const float* sh, int B, int Tn, int D, int K, hipStream_t s) {
+    switch (K) {
+    case 3: dw_go<ET, VEC, 3>(in, out, w, dwb, sc, sh, B, Tn, D, s); break;
+    case 5: dw_go<ET, VEC, 5>(in, out, w, dwb, sc, sh, B, Tn, D, s); break;
+    case 7: dw_go<ET, VEC, 7>(in, out, w, dwb, sc, sh, B, Tn, D, s); break;
+    case 9: dw_go<ET, VEC, 9>(in, out, w, dwb, sc, sh, B, Tn, D, s); break;
+    case 15: dw_go<ET, VEC, 15>(in, out, w, dwb, sc, sh, B, Tn, D, s); break;
+    case 31: dw_go<ET, VEC, 31>(in, out, w, dwb, sc, sh, B, Tn, D, s); break;
+    default: throw std::invalid_argument("dwconv: unsupported kernel size");
+    }
+}
+
+void launch_dwconv_bn_silu(Precision prec, const void* in, void* out, const float* w,
+                           const float* dw_bias, const float* bn_scale, const float* bn_shift,
+                           int B, int T, int D, int K, hipStream_t s) {
+    if (B == 0 || T == 0) return;
+    if (prec == PREC_F16) {
+        require(D % 2 == 0, "dwconv: D must be even");
+        dw_k<f16, 2>(in, out, w, dw_bias, bn_scale, bn_shift, B, T, D, K, s);
+    } else {
+        dw_k<float, 1>(in, out, w, dw_bias, bn_scale, bn_shift, B, T, D, K, s);
+    }
+    PKX_LAUNCH_CHECK();
+}
+
+// ---------------------------------------------------------------------------
+// Subsampling convs (H = time, W = feature; ggml conv layout [W,H,C,N]).
+// ---------------------------------------------------------------------------
+constexpr int SUB_FS = 8;  // output feature columns per block
+
+template <typename T>
+__global__ __launch_bounds__(256) void sub_conv0_kernel(const float* mel, const int* valid0,
+                                                        const float* w, const float* bias, T* out,
+                                                        int F, int Tn, int C, int F1, int T1) {
+    __shared__ float patch[3][2 * SUB_FS + 1];
+    const int f1s = blockIdx.x * SUB_FS, t1 = blockIdx.y, b = blockIdx.z;
+    const int vlim = valid0 ? valid0[b] : Tn;
+    for (int idx = threadIdx.x; idx < 3 * (2 * SUB_FS + 1); idx += blockDim.x) {
+        const int kh = idx / (2 * SUB_FS + 1), kw = idx % (2 * SUB_FS + 1);
+        const int ti = 2 * t1 - 1 + kh, fi = 2 * f1s - 1 + kw;
+        float v = 0.f;
+        if (ti >= 0 && ti < Tn && ti < vlim && fi >= 0 && fi < F) v = mel[((int64_t)b * F + fi) * Tn + ti];
+        patch[kh][kw] = v;
+    }
+    __syncthreads();
+    for (int c = threadIdx.x; c < C; c += blockDim.x) {
+        float wk[9];
+#pragma unroll
+        for (int e = 0; e < 9; ++e) wk[e] = w[c * 9 + e];
+        const float bc = bias[c];
+#pragma unroll
+        for (int fo = 0; fo < SUB_FS; ++fo) {
+            const int f1 = f1s + fo;
+            if (f1 >= F1) break;
+            float acc = 0.f;
+#pragma unroll
+            for (int kh = 0; kh < 3; ++kh)
+#pragma unroll
+                for (int kw = 0; kw < 3; ++kw) acc += wk[kh * 3 + kw] * patch[kh][2 * fo + kw];
+            const float y = acc + bc;
+            out[(((int64_t)b * T1 + t1) * F1 + f1) * C + c] = to_act<T>(y > 0.f ? y : 0.f);
+        }
+    }
+}
+
+template <typename T> __device__ __forceinline__ float ld_act(const T* p) { return (float)*p; }
+
+template <typename T>
+__global__ __launch_bounds__(256) void sub_dwconv_kernel(const T* in, const int* vmask, const float* w,
+                                                         const float* bias, T* out, int Ti, int Fi,
+                                                         int C, int To, int Fo) {
+    const int fos = blockIdx.x * SUB_FS, to = blockIdx.y, b = blockIdx.z;
+    const int vlim = vmask ? vmask[b] : Ti;
+    for (int c = threadIdx.x; c < C; c += blockDim.x) {
+        float wk[9];
+#pragma unroll
+        for (int e = 0; e < 9; ++e) wk[e] = w[c * 9 + e];
+        const float bc = bias[c];
+        for (int fo = 0; fo < SUB_FS; ++fo) {
+            const int f = fos + fo;
+            if (f >= Fo) break;
+            float acc = 0.f;
+#pragma unroll
+            for (int kh = 0; kh < 3; ++kh) {
+                const int ti = 2 * to - 1 + kh;
+                if (ti < 0 || ti >= Ti || ti >= vlim) continue;
+#pragma unroll
+                for (int kw = 0; kw < 3; ++kw) {
+                    const int fi = 2 * f - 1 + kw;
+                    if (fi < 0 || fi >= Fi) continue;
+                    acc += wk[kh * 3 + kw] * ld_act<T>(in + (((int64_t)b * Ti + ti) * Fi + fi) * C + c);
+                }
+            }
+            out[(((int64_t)b * To + to) * Fo + f) * C + c] = to_act<T>(acc + bc);
+        }
+    }
+}
+
+void launch_sub_conv0(Precision prec, const float* mel, const int* valid0, const float* w,
+                      const float* bias, void* out, int B, int F, int T, int C, hipStream_t s) {
+    const int T1 = (T - 1) / 2 + 1, F1 = (F - 1) / 2 + 1;
+    const dim3 grid(cdiv(F1, SUB_FS), T1, B);
+    const int bs = C >= 256 ? 256 : ((C + 63) / 64) * 64;
+    if (prec == PREC_F16)
+        hipLaunchKernelGGL(sub_conv0_kernel<f16>, grid, dim3(bs), 0, s, mel, valid0, w, bias, (f16*)out, F, T, C, F1, T1);
+    else
+        hipLaunchKernelGGL(sub_conv0_kernel<float>, grid, dim3(bs), 0, s, mel, valid0, w, bias, (float*)out, F, T, C, F1, T1);
+    PKX_LAUNCH_CHECK();
+}
+
+void launch_sub_dwconv(Precision prec, const void* in, const int* vmask, const float* w,
+                       const float* bias, void* out, int B, int Ti, int Fi, int C, hipStream_t s) {
+    const int To = (Ti - 1) / 2 + 1, Fo = (Fi - 1) / 2 + 1;
+    const dim3 grid(cdiv(Fo, SUB_FS), To, B);
+    const int bs = C >= 256 ? 256 : ((C + 63) / 64) * 64;
+    if (prec == PREC_F16)
+        hipLaunchKernelGGL(sub_dwconv_kernel<f16>, grid, dim3(bs), 0, s, (const f16*)in, vmask, w, bias, (f16*)out, Ti, Fi, C, To, Fo);
+    else
+        hipLaunchKernelGGL(sub_dwconv_kernel<float>, grid, dim3(bs), 0, s, (const float*)in, vmask, w, bias, (float*)out, Ti, Fi, C, To, Fo);
+    PKX_LAUNCH_CHECK();
+}
+
+// ---------------------------------------------------------------------------
+// Relative positional table in f64 (positions +(T-1) .. -(T-1)).
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ void rel_pos_kernel(T* out, int Tn, int D) {
+    const int half = D / 2;
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t P = 2 * (int64_t)Tn - 1;
+    if (idx >= P * half) return;
+    const int p = (int)(idx / half), i = (int)(idx % half);
+    const double factor = -(log(10000.0) / (double)D);
+    const double div = exp((double)(2 * i) * factor);
+    const double a = (double)((Tn - 1) - p) * div;
+    out[(int64_t)p * D + 2 * i] = to_act<T>((float)sin(a));
+    out[(int64_t)p * D + 2 * i + 1] = to_act<T>((float)cos(a));
+}
+
+void launch_rel_pos_encoding(Precision prec, void* out, int T, int D, hipStream_t s) {
+    require(D % 2 == 0, "pos_enc: D must be even");
+    const int64_t n = (2 * (int64_t)T - 1) * (D / 2);
+    if (prec == PREC_F16)
+        hipLaunchKernelGGL(rel_pos_kernel<f16>, dim3(cdiv(n, 256)), dim3(256), 0, s, (f16*)out, T, D);
+    else
+        hipLaunchKernelGGL(rel_pos_kernel<float>, dim3(cdiv(n, 256)), dim3(256), 0, s, (float*)out, T, D);
+    PKX_LAUNCH_CHECK();
+}
+
+// ---------------------------------------------------------------------------
+// Heads: log-softmax + argmax, split argmax.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void argmax_merge(float& bv, int& bi, float ov, int oi) {
+    if (ov > bv || (ov == bv && oi < bi)) {
+        bv = ov;
+        bi = oi;
+    }
+}
+__device__ __forceinline__ void wave_argmax(float& bv, int& bi) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        argmax_merge(bv, bi, ov, oi);
+    }
+}
+
+__global__ __launch_bounds__(256) void log_softmax_argmax_kernel(const float* x, float* y, int32_t* am,
+                                                                 int64_t M, int V) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= M) return;
+    const float* xr = x + row * V;
+    float* yr = y + row * V;
+    float mx = -INFINITY;
+    for (int v = lane; v < V; v += 64) mx = fmaxf(mx, xr[v]);
+    mx = wave_max(mx);
+    float sum = 0.f;
+    for (int v = lane; v < V; v += 64) sum += expf(xr[v] - mx);
+    const float lse = logf(wave_sum(sum));
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int v = lane; v < V; v += 64) {
+        const float lp = (xr[v] - mx) - lse;
+        yr[v] = lp;
+        argmax_merge(bv, bi, lp, v);
+    }
+    wave_argmax(bv, bi);
+    if (lane == 0) am[row] = bi;
+}
+
+__global__ __launch_bounds__(256) void split_argmax_kernel(const float* x, int64_t M, int nt, int nd,
+                                                           int32_t* tok, int32_t* dur) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= M) return;
+    const float* xr = x + row * (nt + nd);
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int v = lane; v < nt; v += 64) argmax_merge(bv, bi, xr[v], v);
+    wave_argmax(bv, bi);
+    float dv = -INFINITY;
+    int di = 0x7fffffff;
+    for (int v = lane; v < nd; v += 64) argmax_merge(dv, di, xr[nt + v], v);
+    wave_argmax(dv, di);
+    if (lane == 0) {
+        tok[row] = bi;
+        dur[row] = di;
+    }
+}
+
+void launch_log_softmax_argmax(const float* logits, float* logprobs, int32_t* argmax, int64_t M,
+                               int V, hipStream_t s) {
+    if (M == 0) return;
+    hipLaunchKernelGGL(log_softmax_argmax_kernel, dim3(cdiv(M, 4)), dim3(256), 0, s, logits, logprobs, argmax, M, V);
+    PKX_LAUNCH_CHECK();
+}
+
+void launch_split_argmax(const float* logits, int64_t M, int n_tok, int n_dur, int32_t* tok,
+                         int32_t* dur, hipStream_t s) {
+    if (M == 0) return;
+    hipLaunchKernelGGL(split_argmax_kernel, dim3(cdiv(M, 4)), dim3(256), 0, s, logits, M, n_tok, n_dur, tok, dur);
+    PKX_LAUNCH_CHECK();
+}
+
+// ---------------------------------------------------------------------------
+// Cast / add
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ void cast_f32_kernel(const float* x, T* y, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = to_act<T>(x[i]);
+}
+__global__ void add_f32_kernel(float* x, const float* y, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) x[i] += y[i];
+}
+void launch_cast_f32(Precision prec, const float* x, void* y, int64_t n, hipStream_t s) {
+    if (n == 0) return;
+    if (prec == PREC_F16)
+        hipLaunchKernelGGL(cast_f32_kernel<f16>, dim3(cdiv(n, 256)), dim3(256), 0, s, x, (f16*)y, n);
+    else
+        hipLaunchKernelGGL(cast_f32_kernel<float>, dim3(cdiv(n, 256)), dim3(256), 0, s, x, (float*)y, n);
+    PKX_LAUNCH_CHECK();
+}
+void launch_add_f32(float* x, const float* y, int64_t n, hipStream_t s) {
+    if (n == 0) return;
+    hipLaunchKernelGGL(add_f32_kernel, dim3(cdiv(n, 256)), dim3(256), 0, s, x, y, n);
+    PKX_LAUNCH_CHECK();
+}
+
+// ---------------------------------------------------------------------------
+// [B][T][D] -> per-item [D][valid[b]] (32x32 LDS tile transpose).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void compact_cf_kernel(const float* x, int Tn, int D, const int* valid,
+                                                         const int64_t* offs, float* out) {
+    __shared__ float tile[32][33];
+    const int b = blockIdx.z, t0 = blockIdx.x * 32, c0 = blockIdx.y * 32;
+    const int vb = valid[b];
+    if (t0 >= vb) return;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+    for (int r = ty; r < 32; r += 8) {
+        const int t = t0 + r, c = c0 + tx;
+        tile[r][tx] = (t < vb && c < D) ? x[((int64_t)b * Tn + t) * D + c] : 0.f;
+    }
+    __syncthreads();
+    float* ob = out + offs[b];
+    for (int r = ty; r < 32; r += 8) {
+        const int c = c0 + r, t = t0 + tx;
+        if (c < D && t < vb) ob[(int64_t)c * vb + t] = tile[tx][r];
+    }
+}
+
+void launch_compact_channels_first(const float* x, int B, int T, int D, const int* valid,
+                                   const int64_t* offs, float* out, hipStream_t s) {
+    const dim3 grid(cdiv(T, 32), cdiv(D, 32), B);
+    hipLaunchKernelGGL(compact_cf_kernel, grid, dim3(256), 0, s, x, T, D, valid, offs, out);
+    PKX_LAUNCH_CHECK();
+}
+
+}  // namespace pkx

@@ -1,0 +1,67 @@
+// Memory-bound kernels of the encoder path.
+#pragma once
+#include "common.hpp"
+
+namespace pkx {
+
+// LayerNorm over the last dim (conformer.cpp:300-307, eps 1e-5).
+//   y = LN(x; g, b) written as the activation type of `prec`, or, with
+//   y_f32 != nullptr, first y_f32 = LN(x; g, b) (may alias x) and then
+//   y = LN(y_f32; g2, b2): the layer's norm_out fused with the next layer's
+//   norm_feed_forward1 (one pass over the residual stream).
+// With y == nullptr only y_f32 = LN(x) is written (f32 output in any mode).
+struct LnParams {
+    const float* x = nullptr;
+    const float* g = nullptr;
+    const float* b = nullptr;
+    float* y_f32 = nullptr;
+    const float* g2 = nullptr;
+    const float* b2 = nullptr;
+    void* y = nullptr;
+    int64_t M = 0;
+    int D = 0;
+    float eps = 1e-5f;
+};
+void launch_layernorm(Precision prec, const LnParams& p, hipStream_t s);
+
+// Conv module middle (conformer.cpp:81-157): depthwise conv (K taps, symmetric
+// pad (K-1)/2, cross-correlation) + bias, folded BatchNorm scale/shift, SiLU.
+// in/out [B][T][D] activation type; w [D][K].
+void launch_dwconv_bn_silu(Precision prec, const void* in, void* out, const float* w,
+                           const float* dw_bias, const float* bn_scale, const float* bn_shift,
+                           int B, int T, int D, int K, hipStream_t s);
+
+// Subsampling conv.0 (subsampling.cpp:143-157): Conv2d(1->C, 3x3, s2, p1) + bias
+// + ReLU over mel [B][F][T] (f32), time frames t >= valid0[b] read as zero when
+// valid0 != nullptr; output channels-last [B][T1][F1][C] activation type.
+void launch_sub_conv0(Precision prec, const float* mel, const int* valid0, const float* w,
+                      const float* bias, void* out, int B, int F, int T, int C, hipStream_t s);
+
+// Subsampling depthwise 3x3 s2 p1 + bias (subsampling.cpp:168-184), channels-last,
+// input time rows t >= vmask[b] read as zero when vmask != nullptr.
+void launch_sub_dwconv(Precision prec, const void* in, const int* vmask, const float* w,
+                       const float* bias, void* out, int B, int Ti, int Fi, int C, hipStream_t s);
+
+// pos_enc.cpp:10-34 in f64, stored as the activation type: [2T-1][D].
+void launch_rel_pos_encoding(Precision prec, void* out, int T, int D, hipStream_t s);
+
+// Row-wise log_softmax + first-max argmax over V (ctc_decoder.cpp:107-108,
+// search.cpp:57-61).  logits [M][V] f32 in, logprobs [M][V] f32 out (may alias).
+void launch_log_softmax_argmax(const float* logits, float* logprobs, int32_t* argmax, int64_t M,
+                               int V, hipStream_t s);
+
+// Split argmax per row (tdt.cpp:76-79): tok = argmax[0,n_tok), dur = argmax[n_tok, n_tok+n_dur).
+void launch_split_argmax(const float* logits, int64_t M, int n_tok, int n_dur, int32_t* tok,
+                         int32_t* dur, hipStream_t s);
+
+// f32 -> activation type copy (f16 mode inputs of the unit entry points).
+void launch_cast_f32(Precision prec, const float* x, void* y, int64_t n, hipStream_t s);
+// x[i] += y[i] (f32).
+void launch_add_f32(float* x, const float* y, int64_t n, hipStream_t s);
+
+// Time-major [B][T][D] f32 -> per-item channels-first [D][valid[b]] compacted,
+// item b at out + offs[b] (encoder.cpp:158-166).
+void launch_compact_channels_first(const float* x, int B, int T, int D, const int* valid,
+                                   const int64_t* offs, float* out, hipStream_t s);
+
+}  // namespace pkx

@@ -1,0 +1,50 @@
+// GEMM family: Y = epilogue(X[M][K] . W[N][K]^T) on gfx950 MFMA.
+//
+// Replaces ggml_mul_mat(W, x) for every linear on the encoder path
+// (conformer.cpp:309-324 FFN, relpos_attention.cpp:180-194,305 q/k/v/pos/out,
+// conformer.cpp:48-53,158-162 pointwise convs, subsampling.cpp:189,233-236,
+// ctc_decoder.cpp:98, joint.cpp:55-56) together with the element-wise ops that
+// follow each of them in the reference graph (bias add, SiLU, GLU + pad mask,
+// x0.5 residual, ReLU, flatten transpose), fused into the epilogue.
+#pragma once
+#include "common.hpp"
+
+namespace pkx {
+
+enum Epi : int {
+    EPI_STORE = 0,      // Y(act) = alpha*(acc + bias)
+    EPI_STORE_F32 = 1,  // Y(f32) = alpha*(acc + bias)
+    EPI_SILU = 2,       // Y(act) = silu(acc + bias)                         conformer.cpp:321
+    EPI_RESID = 3,      // R(f32) += alpha*(acc + bias)                       conformer.cpp:326-352
+    EPI_GLU = 4,        // Y(act)[m][j] = a*sigmoid(b), 0 for t >= valid     conformer.cpp:55-80
+    EPI_RELU = 5,       // Y(act) = relu(acc + bias)                          subsampling.cpp:189-191
+    EPI_RELU_TR = 6,    // relu + flatten to [b][t][c][f], 0 for t >= valid   subsampling.cpp:194-230
+    EPI_RELU2_F32 = 7,  // Y(f32) = relu((acc + bias) + bias2)                joint.cpp:89-95
+    EPI_COUNT = 8
+};
+
+struct GemmParams {
+    const void* A = nullptr;   // activations, row stride lda elements
+    int64_t lda = 0;
+    const void* Wq = nullptr;  // weight payload (device layout per type, see DevWeight)
+    const void* Ws = nullptr;  // per-block scales (q8_0: f16 [N][K/32]; q4_K: float2 [N][K/32])
+    const float* bias = nullptr;
+    const float* bias2 = nullptr;
+    void* Y = nullptr;         // output (EPI_RESID: the f32 residual updated in place)
+    int64_t ldy = 0;
+    float alpha = 1.0f;
+    const int* valid = nullptr;  // per-item valid rows; row m -> item m / T, time m % T
+    int T = 1;
+    int trF = 1;               // EPI_RELU_TR: rows are (b, t, f) with f fastest, F' = trF
+    int M = 0, N = 0, K = 0;
+};
+
+// Launch one GEMM.  prec selects the activation type (f16: MFMA 16x16x32 f16
+// with weights dequantised to f16 in registers; f32: MFMA 16x16x4 f32 with
+// weights dequantised to f32).  wtype is the ggml type of the device weight.
+void launch_gemm(Precision prec, int wtype, int epi, const GemmParams& p, hipStream_t s);
+
+// Bit-exact dequantisation of raw ggml blocks (GGUF layout) to f32.
+void launch_dequantize(int wtype, const void* src, float* dst, int64_t n, hipStream_t s);
+
+}  // namespace pkx

@@ -1,0 +1,210 @@
+// GGUF v3 reader for the encoder path (pk::ModelLoader::load,
+// src/model_loader.cpp:99-167): parakeet.* KV -> ModelConfig, verbatim NeMo
+// tensor names -> Model::set_tensor.  Only the tensors the encoder, the CTC
+// head and the TDT joint use are read; the file is streamed tensor by tensor.
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "model.hpp"
+
+namespace pkx {
+namespace {
+
+enum : uint32_t {
+    KV_U8 = 0, KV_I8 = 1, KV_U16 = 2, KV_I16 = 3, KV_U32 = 4, KV_I32 = 5, KV_F32 = 6,
+    KV_BOOL = 7, KV_STR = 8, KV_ARR = 9, KV_U64 = 10, KV_I64 = 11, KV_F64 = 12
+};
+
+struct File {
+    FILE* f = nullptr;
+    explicit File(const std::string& p) : f(std::fopen(p.c_str(), "rb")) {
+        require(f != nullptr, "cannot open GGUF file: " + p);
+    }
+    ~File() { if (f) std::fclose(f); }
+    void read(void* dst, size_t n) {
+        require(std::fread(dst, 1, n, f) == n, "GGUF: truncated file");
+    }
+    template <typename T> T get() {
+        T v;
+        read(&v, sizeof(T));
+        return v;
+    }
+    std::string str() {
+        const uint64_t n = get<uint64_t>();
+        require(n < (1ull << 24), "GGUF: string too long");
+        std::string s((size_t)n, '\0');
+        if (n) read(&s[0], (size_t)n);
+        return s;
+    }
+    void skip(uint64_t n) { require(std::fseek(f, (long)n, SEEK_CUR) == 0, "GGUF: seek failed"); }
+    void seek(uint64_t off) { require(std::fseek(f, (long)off, SEEK_SET) == 0, "GGUF: seek failed"); }
+    uint64_t tell() { return (uint64_t)std::ftell(f); }
+};
+
+struct KvVal {
+    uint32_t type = 0;
+    int64_t i = 0;
+    double d = 0;
+    std::string s;
+    std::vector<int64_t> arr;
+    uint32_t arr_type = 0;
+};
+
+size_t scalar_size(uint32_t t) {
+    switch (t) {
+    case KV_U8: case KV_I8: case KV_BOOL: return 1;
+    case KV_U16: case KV_I16: return 2;
+    case KV_U32: case KV_I32: case KV_F32: return 4;
+    case KV_U64: case KV_I64: case KV_F64: return 8;
+    default: return 0;
+    }
+}
+
+int64_t read_int(File& f, uint32_t t) {
+    switch (t) {
+    case KV_U8: return f.get<uint8_t>();
+    case KV_I8: return f.get<int8_t>();
+    case KV_U16: return f.get<uint16_t>();
+    case KV_I16: return f.get<int16_t>();
+    case KV_U32: return f.get<uint32_t>();
+    case KV_I32: return f.get<int32_t>();
+    case KV_U64: return (int64_t)f.get<uint64_t>();
+    case KV_I64: return f.get<int64_t>();
+    case KV_BOOL: return f.get<uint8_t>() ? 1 : 0;
+    default: throw std::invalid_argument("GGUF: not an integer type");
+    }
+}
+
+KvVal read_val(File& f, uint32_t t) {
+    KvVal v;
+    v.type = t;
+    if (t == KV_STR) {
+        v.s = f.str();
+    } else if (t == KV_F32) {
+        v.d = f.get<float>();
+    } else if (t == KV_F64) {
+        v.d = f.get<double>();
+    } else if (t == KV_ARR) {
+        v.arr_type = f.get<uint32_t>();
+        const uint64_t n = f.get<uint64_t>();
+        if (v.arr_type == KV_STR) {
+            for (uint64_t k = 0; k < n; ++k) f.skip(f.get<uint64_t>());   // e.g. tokenizer pieces
+        } else if (v.arr_type == KV_F32 || v.arr_type == KV_F64) {
+            f.skip(n * scalar_size(v.arr_type));
+        } else {
+            require(scalar_size(v.arr_type) > 0, "GGUF: bad array element type");
+            v.arr.reserve((size_t)n);
+            for (uint64_t k = 0; k < n; ++k) v.arr.push_back(read_int(f, v.arr_type));
+        }
+    } else {
+        require(scalar_size(t) > 0, "GGUF: bad KV type " + std::to_string(t));
+        v.i = read_int(f, t);
+    }
+    return v;
+}
+
+struct TensorInfo {
+    std::string name;
+    int n_dims = 0;
+    int64_t ne[4] = {1, 1, 1, 1};
+    int gtype = 0;
+    uint64_t offset = 0;
+};
+
+int64_t tensor_bytes(const TensorInfo& t) {
+    int64_t blk = 1, bs = 4;
+    switch (t.gtype) {
+    case GT_F32: blk = 1; bs = 4; break;
+    case GT_F16: blk = 1; bs = 2; break;
+    case GT_Q8_0: blk = 32; bs = 34; break;
+    case GT_Q4_K: blk = 256; bs = 144; break;
+    default: return -1;
+    }
+    require(t.ne[0] % blk == 0, "GGUF: row not a multiple of the block size in " + t.name);
+    return t.ne[0] / blk * bs * t.ne[1] * t.ne[2] * t.ne[3];
+}
+
+bool wanted(const std::string& n) {
+    auto starts = [&](const char* p) { return n.compare(0, std::strlen(p), p) == 0; };
+    return starts("encoder.") || starts("ctc_decoder.") || starts("decoder.decoder_layers.") ||
+           starts("joint.enc.") || starts("joint.pred.") || starts("joint.joint_net.2.");
+}
+
+}  // namespace
+
+std::unique_ptr<Model> load_gguf(const std::string& path, int precision) {
+    File f(path);
+    require(f.get<uint32_t>() == 0x46554747u, "not a GGUF file: " + path);
+    const uint32_t version = f.get<uint32_t>();
+    require(version == 3 || version == 2, "unsupported GGUF version " + std::to_string(version));
+    const uint64_t n_tensors = f.get<uint64_t>();
+    const uint64_t n_kv = f.get<uint64_t>();
+    std::map<std::string, KvVal> kv;
+    for (uint64_t i = 0; i < n_kv; ++i) {
+        std::string key = f.str();
+        const uint32_t t = f.get<uint32_t>();
+        kv[key] = read_val(f, t);
+    }
+    std::vector<TensorInfo> infos((size_t)n_tensors);
+    for (auto& ti : infos) {
+        ti.name = f.str();
+        ti.n_dims = (int)f.get<uint32_t>();
+        require(ti.n_dims >= 1 && ti.n_dims <= 4, "GGUF: bad n_dims");
+        for (int d = 0; d < ti.n_dims; ++d) ti.ne[d] = (int64_t)f.get<uint64_t>();
+        ti.gtype = (int)f.get<uint32_t>();
+        ti.offset = f.get<uint64_t>();
+    }
+    uint64_t align = 32;
+    if (kv.count("general.alignment")) align = (uint64_t)kv["general.alignment"].i;
+    const uint64_t data0 = (f.tell() + align - 1) / align * align;
+
+    auto u = [&](const char* k, int64_t dflt) -> int64_t {
+        auto it = kv.find(k);
+        return it == kv.end() ? dflt : it->second.i;
+    };
+    auto s = [&](const char* k, const char* dflt) -> std::string {
+        auto it = kv.find(k);
+        return it == kv.end() ? std::string(dflt) : it->second.s;
+    };
+    // model_loader.cpp:103-161 keys and defaults
+    ModelConfig c;
+    c.d_model = (int)u("parakeet.encoder.d_model", 0);
+    c.n_layers = (int)u("parakeet.encoder.n_layers", 0);
+    c.n_heads = (int)u("parakeet.encoder.n_heads", 0);
+    c.ff_dim = (int)u("parakeet.encoder.ff_dim", 0);
+    c.conv_kernel = (int)u("parakeet.encoder.conv_kernel", 0);
+    c.n_mels = (int)u("parakeet.encoder.feat_in", 0);
+    c.sub_channels = (int)u("parakeet.encoder.subsampling_conv_channels", 0);
+    c.xscaling = (int)u("parakeet.encoder.xscaling", 1);
+    c.vocab_size = (int)u("parakeet.vocab_size", 0);
+    if (kv.count("parakeet.tdt.durations")) c.n_durations = (int)kv["parakeet.tdt.durations"].arr.size();
+    require(c.d_model > 0 && c.vocab_size > 0, "GGUF: missing parakeet.encoder.d_model / parakeet.vocab_size");
+    require(s("parakeet.encoder.conv_norm_type", "batch_norm") == "batch_norm",
+            "conv_norm_type=layer_norm (streaming models) is not supported by this encoder");
+    require(s("parakeet.encoder.att_context_style", "regular") == "regular",
+            "chunked_limited attention (streaming models) is not supported by this encoder");
+    require(u("parakeet.encoder.causal_downsampling", 0) == 0 && u("parakeet.encoder.conv_causal", 0) == 0,
+            "causal subsampling / depthwise conv (streaming models) is not supported by this encoder");
+    const int64_t sf = u("parakeet.encoder.subsampling_factor", 8);
+    require(sf == 8, "only dw_striding x8 subsampling is supported");
+
+    std::unique_ptr<Model> m(new Model(c, precision));
+    std::vector<uint8_t> buf;
+    for (const auto& ti : infos) {
+        if (!wanted(ti.name)) continue;
+        const int64_t nb = tensor_bytes(ti);
+        require(nb >= 0, "GGUF: unsupported type " + std::to_string(ti.gtype) + " for tensor " + ti.name);
+        buf.resize((size_t)nb);
+        f.seek(data0 + ti.offset);
+        f.read(buf.data(), (size_t)nb);
+        m->set_tensor(ti.name, ti.gtype, ti.n_dims, ti.ne, buf.data(), (size_t)nb);
+    }
+    m->finalize();
+    return m;
+}
+
+}  // namespace pkx

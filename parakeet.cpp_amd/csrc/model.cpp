@@ -1,0 +1,895 @@
+// Device model: upload + repack, workspace, and the encoder forward schedule.
+#include "model.hpp"
+
+#include <cmath>
+#include <cstring>
+
+namespace pkx {
+
+// ---------------------------------------------------------------------------
+// host binary16 helpers (IEEE 754, round to nearest even)
+// ---------------------------------------------------------------------------
+static float half_bits_to_float(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h >> 15) << 31;
+    const uint32_t ex = (h >> 10) & 0x1fu, man = h & 0x3ffu;
+    uint32_t bits;
+    float f;
+    if (ex == 0) {
+        f = std::ldexp((float)man, -24);
+        std::memcpy(&bits, &f, 4);
+        bits |= sign;
+    } else if (ex == 31) {
+        bits = sign | 0x7f800000u | (man << 13);
+    } else {
+        bits = sign | ((ex + 112u) << 23) | (man << 13);
+    }
+    std::memcpy(&f, &bits, 4);
+    return f;
+}
+
+static uint16_t float_to_half_bits(float f) {
+    uint32_t x;
+    std::memcpy(&x, &f, 4);
+    const uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+    const uint32_t ax = x & 0x7fffffffu;
+    if (ax > 0x7f800000u) return (uint16_t)(sign | 0x7e00u);
+    if (ax >= 0x47800000u) return (uint16_t)(sign | 0x7c00u);
+    if (ax < 0x38800000u) {
+        float af;
+        std::memcpy(&af, &ax, 4);
+        return (uint16_t)(sign | (uint16_t)std::nearbyint(af * 16777216.0f));
+    }
+    const uint32_t e = (ax >> 23) - 112u, m = ax & 0x7fffffu;
+    uint32_t h = (e << 10) | (m >> 13);
+    const uint32_t rem = m & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) ++h;
+    return (uint16_t)(sign | h);
+}
+
+static int64_t row_bytes(int gtype, int64_t K) {
+    switch (gtype) {
+    case GT_F32: return K * 4;
+    case GT_F16: return K * 2;
+    case GT_Q8_0: return K / 32 * 34;
+    case GT_Q4_K: return K / 256 * 144;
+    default: throw std::invalid_argument("unsupported ggml type " + std::to_string(gtype));
+    }
+}
+
+int subsampled_len(int T) {
+    int t = T;
+    for (int s = 0; s < 3; ++s) t = (t + 2 - 3) / 2 + 1;
+    return t;
+}
+
+int valid_out_len(int T, int in_valid) {
+    int v = in_valid >= 0 ? in_valid : T - 1;
+    for (int s = 0; s < 3; ++s) v = (v + 2 - 3) / 2 + 1;
+    return v;
+}
+
+// ---------------------------------------------------------------------------
+// workspace
+// ---------------------------------------------------------------------------
+struct Buf {
+    void* p = nullptr;
+    size_t cap = 0;
+};
+
+struct Model::Ws {
+    Buf a1, a2, a2p, a3, flat;          // subsampling maps
+    Buf h, u, qkv, g, pe, p, xin, tmp;  // layer activations
+    Buf logits, pp;                     // heads
+    int* d_valid = nullptr;             // 4 x Bcap ints: v0, v1, v2, vout
+    int* h_valid = nullptr;             // pinned staging
+    int Bcap = 0;
+    hipEvent_t staged = nullptr;
+};
+
+static void grow(Buf& b, size_t bytes) {
+    if (bytes <= b.cap) return;
+    if (b.p) PKX_HIP(hipFree(b.p));
+    b.p = nullptr;
+    b.cap = 0;
+    PKX_HIP(hipMalloc(&b.p, bytes));
+    b.cap = bytes;
+}
+
+// ---------------------------------------------------------------------------
+// construction / upload
+// ---------------------------------------------------------------------------
+Model::Model(const ModelConfig& cfg, int precision) : cfg_(cfg), ws_(new Ws) {
+    require(cfg.d_model > 0 && cfg.n_layers > 0 && cfg.n_heads > 0 && cfg.ff_dim > 0, "config: bad encoder dims");
+    require(cfg.d_model % cfg.n_heads == 0, "config: d_model % n_heads != 0");
+    require(cfg.conv_kernel % 2 == 1, "config: depthwise kernel must be odd");
+    require(cfg.n_mels > 0 && cfg.sub_channels > 0 && cfg.sub_channels % 8 == 0,
+            "config: subsampling channels must be a positive multiple of 8");
+    prec_ = precision == PREC_F32 ? PREC_F32 : PREC_F16;
+    if (precision < 0) prec_ = (Precision)-1;  // resolved in finalize()
+}
+
+Model::~Model() {
+    auto fr = [](void* p) { if (p) (void)hipFree(p); };
+    for (void* p : allocs_) fr(p);
+    if (ws_) {
+        for (Buf* b : {&ws_->a1, &ws_->a2, &ws_->a2p, &ws_->a3, &ws_->flat, &ws_->h, &ws_->u, &ws_->qkv,
+                       &ws_->g, &ws_->pe, &ws_->p, &ws_->xin, &ws_->tmp, &ws_->logits, &ws_->pp})
+            fr(b->p);
+        fr(ws_->d_valid);
+        if (ws_->h_valid) (void)hipHostFree(ws_->h_valid);
+        if (ws_->staged) (void)hipEventDestroy(ws_->staged);
+    }
+    for (hipEvent_t e : ev_)
+        if (e) (void)hipEventDestroy(e);
+}
+
+void Model::set_tensor(const std::string& name, int gtype, int n_dims, const int64_t* ne,
+                       const void* data, size_t nbytes) {
+    require(!finalized_, "set_tensor after finalize");
+    require(n_dims >= 1 && n_dims <= 4, "set_tensor: n_dims must be 1..4");
+    HostTensor t;
+    t.gtype = gtype;
+    t.n_dims = n_dims;
+    for (int i = 0; i < n_dims; ++i) t.ne[i] = ne[i];
+    const int64_t rows = t.nelem() / t.ne[0];
+    const int64_t want = row_bytes(gtype, t.ne[0]) * rows;
+    require((int64_t)nbytes == want, "set_tensor '" + name + "': expected " + std::to_string(want) +
+                                         " bytes, got " + std::to_string(nbytes));
+    t.bytes.assign((const uint8_t*)data, (const uint8_t*)data + nbytes);
+    host_[name] = std::move(t);
+}
+
+const HostTensor* Model::find(const std::string& n) const {
+    auto it = host_.find(n);
+    return it == host_.end() ? nullptr : &it->second;
+}
+
+const HostTensor& Model::need(const std::string& n) const {
+    const HostTensor* t = find(n);
+    require(t != nullptr, "missing tensor '" + n + "'");
+    return *t;
+}
+
+void* Model::dalloc(size_t bytes) {
+    void* p = nullptr;
+    PKX_HIP(hipMalloc(&p, bytes ? bytes : 16));
+    allocs_.push_back(p);
+    return p;
+}
+
+static std::vector<float> to_f32(const HostTensor& t) {
+    const int64_t n = t.nelem();
+    std::vector<float> v((size_t)n);
+    if (t.gtype == GT_F32) {
+        std::memcpy(v.data(), t.bytes.data(), (size_t)n * 4);
+    } else if (t.gtype == GT_F16) {
+        const uint16_t* h = (const uint16_t*)t.bytes.data();
+        for (int64_t i = 0; i < n; ++i) v[(size_t)i] = half_bits_to_float(h[i]);
+    } else {
+        throw std::invalid_argument("expected an f32/f16 vector tensor");
+    }
+    return v;
+}
+
+float* Model::upload_f32(const std::vector<float>& v) {
+    float* d = (float*)dalloc(v.size() * 4);
+    PKX_HIP(hipMemcpy(d, v.data(), v.size() * 4, hipMemcpyHostToDevice));
+    return d;
+}
+
+float* Model::upload_f32(const HostTensor& t) { return upload_f32(to_f32(t)); }
+
+static void* dalloc_into(std::vector<void*>& allocs, size_t bytes) {
+    void* p = nullptr;
+    PKX_HIP(hipMalloc(&p, bytes ? bytes : 16));
+    allocs.push_back(p);
+    return p;
+}
+
+DevWeight Model::make_weight(const HostTensor& t, int N, int K, bool f16_gemm) {
+    return build_weight(t, N, K, f16_gemm, allocs_);
+}
+
+// Raw rows (GGUF layout) -> device layout for the GEMM family.
+DevWeight build_weight(const HostTensor& t, int N, int K, bool f16_gemm, std::vector<void*>& allocs) {
+    require(t.nelem() == (int64_t)N * K, "weight shape mismatch");
+    auto dalloc = [&](size_t bytes) { return dalloc_into(allocs, bytes); };
+    DevWeight w;
+    w.N = N;
+    w.K = K;
+    const uint8_t* src = t.bytes.data();
+    switch (t.gtype) {
+    case GT_F32:
+        if (f16_gemm) {
+            std::vector<uint16_t> h((size_t)N * K);
+            const float* f = (const float*)src;
+            for (size_t i = 0; i < h.size(); ++i) h[i] = float_to_half_bits(f[i]);
+            w.gtype = GT_F16;
+            w.q = dalloc(h.size() * 2);
+            PKX_HIP(hipMemcpy(w.q, h.data(), h.size() * 2, hipMemcpyHostToDevice));
+        } else {
+            w.gtype = GT_F32;
+            w.q = dalloc((size_t)N * K * 4);
+            PKX_HIP(hipMemcpy(w.q, src, (size_t)N * K * 4, hipMemcpyHostToDevice));
+        }
+        break;
+    case GT_F16:
+        w.gtype = GT_F16;
+        w.q = dalloc((size_t)N * K * 2);
+        PKX_HIP(hipMemcpy(w.q, src, (size_t)N * K * 2, hipMemcpyHostToDevice));
+        break;
+    case GT_Q8_0: {
+        require(K % 32 == 0, "q8_0 weight K % 32 != 0");
+        const int nb = K / 32;
+        std::vector<int8_t> q((size_t)N * K);
+        std::vector<uint16_t> d((size_t)N * nb);
+        for (int n = 0; n < N; ++n)
+            for (int b = 0; b < nb; ++b) {
+                const uint8_t* blk = src + ((size_t)n * nb + b) * 34;
+                d[(size_t)n * nb + b] = (uint16_t)(blk[0] | (blk[1] << 8));
+                std::memcpy(&q[(size_t)n * K + (size_t)b * 32], blk + 2, 32);
+            }
+        w.gtype = GT_Q8_0;
+        w.q = dalloc(q.size());
+        w.s = dalloc(d.size() * 2);
+        PKX_HIP(hipMemcpy(w.q, q.data(), q.size(), hipMemcpyHostToDevice));
+        PKX_HIP(hipMemcpy(w.s, d.data(), d.size() * 2, hipMemcpyHostToDevice));
+        break;
+    }
+    case GT_Q4_K: {
+        require(K % 256 == 0, "q4_K weight K % 256 != 0");
+        const int nb = K / 256;
+        std::vector<uint8_t> qs((size_t)N * K / 2);
+        std::vector<float> sc((size_t)N * (K / 32) * 2);
+        for (int n = 0; n < N; ++n)
+            for (int b = 0; b < nb; ++b) {
+                const uint8_t* blk = src + ((size_t)n * nb + b) * 144;
+                const float d = half_bits_to_float((uint16_t)(blk[0] | (blk[1] << 8)));
+                const float dmin = half_bits_to_float((uint16_t)(blk[2] | (blk[3] << 8)));
+                const uint8_t* s6 = blk + 4;
+                for (int j = 0; j < 8; ++j) {
+                    int s, m;
+                    if (j < 4) {
+                        s = s6[j] & 63;
+                        m = s6[j + 4] & 63;
+                    } else {
+                        s = (s6[j + 4] & 0xF) | ((s6[j - 4] >> 6) << 4);
+                        m = (s6[j + 4] >> 4) | ((s6[j] >> 6) << 4);
+                    }
+                    float* o = &sc[((size_t)n * (K / 32) + (size_t)b * 8 + j) * 2];
+                    o[0] = d * (float)s;
+                    o[1] = dmin * (float)m;
+                }
+                std::memcpy(&qs[(size_t)n * (K / 2) + (size_t)b * 128], blk + 16, 128);
+            }
+        w.gtype = GT_Q4_K;
+        w.q = dalloc(qs.size());
+        w.s = dalloc(sc.size() * 4);
+        PKX_HIP(hipMemcpy(w.q, qs.data(), qs.size(), hipMemcpyHostToDevice));
+        PKX_HIP(hipMemcpy(w.s, sc.data(), sc.size() * 4, hipMemcpyHostToDevice));
+        break;
+    }
+    default:
+        throw std::invalid_argument("unsupported weight type " + std::to_string(t.gtype));
+    }
+    return w;
+}
+
+// Concatenate the rows of several same-typed weights (q|k|v), or interleave the
+// two halves of one weight in 16-row groups (pointwise_conv1 for the GLU epilogue).
+DevWeight Model::make_weight_rows(const std::vector<const HostTensor*>& parts, int K,
+                                  bool f16_gemm, bool glu_interleave) {
+    const int gt = parts[0]->gtype;
+    const int64_t rb = row_bytes(gt, K);
+    int N = 0;
+    for (const HostTensor* p : parts) {
+        require(p->gtype == gt, "concatenated weights must share a type");
+        require(p->nelem() % K == 0, "concatenated weight K mismatch");
+        N += (int)(p->nelem() / K);
+    }
+    HostTensor cat;
+    cat.gtype = gt;
+    cat.n_dims = 2;
+    cat.ne[0] = K;
+    cat.ne[1] = N;
+    cat.bytes.resize((size_t)rb * N);
+    if (glu_interleave) {
+        require(parts.size() == 1 && N % 32 == 0, "GLU interleave needs one weight with 2D rows, D % 16 == 0");
+        const int D = N / 2;
+        for (int r = 0; r < N; ++r) {
+            const int g = r / 32, i = r % 32;
+            const int src = i < 16 ? 16 * g + i : D + 16 * g + (i - 16);
+            std::memcpy(&cat.bytes[(size_t)r * rb], &parts[0]->bytes[(size_t)src * rb], (size_t)rb);
+        }
+    } else {
+        size_t off = 0;
+        for (const HostTensor* p : parts) {
+            std::memcpy(&cat.bytes[off], p->bytes.data(), p->bytes.size());
+            off += p->bytes.size();
+        }
+    }
+    return make_weight(cat, N, K, f16_gemm);
+}
+
+void linear_raw(Precision prec, const HostTensor& t, int N, int K, const float* bias, const float* x,
+                int64_t M, float* y, hipStream_t s) {
+    std::vector<void*> allocs;
+    try {
+        const DevWeight w = build_weight(t, N, K, prec == PREC_F16, allocs);
+        const void* A = x;
+        if (prec == PREC_F16) {
+            void* xa = dalloc_into(allocs, (size_t)M * K * 2);
+            launch_cast_f32(prec, x, xa, M * K, s);
+            A = xa;
+        }
+        GemmParams p;
+        p.A = A;
+        p.lda = K;
+        p.Wq = w.q;
+        p.Ws = w.s;
+        p.bias = bias;
+        p.Y = y;
+        p.ldy = N;
+        p.M = (int)M;
+        p.N = N;
+        p.K = K;
+        launch_gemm(prec, w.gtype, EPI_STORE_F32, p, s);
+        PKX_HIP(hipStreamSynchronize(s));
+    } catch (...) {
+        (void)hipStreamSynchronize(s);
+        for (void* a : allocs) (void)hipFree(a);
+        throw;
+    }
+    for (void* a : allocs) PKX_HIP(hipFree(a));
+}
+
+static bool quantizable_linear(const std::string& n) {
+    return n.find("feed_forward") != std::string::npos || n.find("self_attn.linear_") != std::string::npos ||
+           n == "encoder.pre_encode.out.weight";
+}
+
+void Model::finalize() {
+    require(!finalized_, "finalize called twice");
+    const ModelConfig& c = cfg_;
+    const int D = c.d_model, FF = c.ff_dim, H = c.n_heads, dk = D / H, K = c.conv_kernel, C = c.sub_channels;
+    require(D % 16 == 0, "d_model must be a multiple of 16");
+
+    if ((int)prec_ < 0) {
+        bool any_low = false;
+        for (auto& kv : host_)
+            if (quantizable_linear(kv.first) && kv.second.gtype != GT_F32) any_low = true;
+        prec_ = any_low ? PREC_F16 : PREC_F32;
+    }
+    const bool f16g = prec_ == PREC_F16;
+
+    auto optb = [&](const std::string& n) -> float* {
+        const HostTensor* t = find(n);
+        return t ? upload_f32(*t) : nullptr;
+    };
+
+    layers_.resize(c.n_layers);
+    for (int i = 0; i < c.n_layers; ++i) {
+        const std::string p = "encoder.layers." + std::to_string(i) + ".";
+        LayerDev& L = layers_[i];
+        L.ff1_ln_g = upload_f32(need(p + "norm_feed_forward1.weight"));
+        L.ff1_ln_b = upload_f32(need(p + "norm_feed_forward1.bias"));
+        L.att_ln_g = upload_f32(need(p + "norm_self_att.weight"));
+        L.att_ln_b = upload_f32(need(p + "norm_self_att.bias"));
+        L.conv_ln_g = upload_f32(need(p + "norm_conv.weight"));
+        L.conv_ln_b = upload_f32(need(p + "norm_conv.bias"));
+        L.ff2_ln_g = upload_f32(need(p + "norm_feed_forward2.weight"));
+        L.ff2_ln_b = upload_f32(need(p + "norm_feed_forward2.bias"));
+        L.out_ln_g = upload_f32(need(p + "norm_out.weight"));
+        L.out_ln_b = upload_f32(need(p + "norm_out.bias"));
+        L.ff1_w1 = make_weight(need(p + "feed_forward1.linear1.weight"), FF, D, f16g);
+        L.ff1_w2 = make_weight(need(p + "feed_forward1.linear2.weight"), D, FF, f16g);
+        L.ff2_w1 = make_weight(need(p + "feed_forward2.linear1.weight"), FF, D, f16g);
+        L.ff2_w2 = make_weight(need(p + "feed_forward2.linear2.weight"), D, FF, f16g);
+        L.ff1_b1 = optb(p + "feed_forward1.linear1.bias");
+        L.ff1_b2 = optb(p + "feed_forward1.linear2.bias");
+        L.ff2_b1 = optb(p + "feed_forward2.linear1.bias");
+        L.ff2_b2 = optb(p + "feed_forward2.linear2.bias");
+        const std::string a = p + "self_attn.";
+        L.wqkv = make_weight_rows({&need(a + "linear_q.weight"), &need(a + "linear_k.weight"),
+                                   &need(a + "linear_v.weight")}, D, f16g, false);
+        {
+            const HostTensor *bq = find(a + "linear_q.bias"), *bk = find(a + "linear_k.bias"),
+                             *bv = find(a + "linear_v.bias");
+            if (bq || bk || bv) {
+                std::vector<float> cat((size_t)3 * D, 0.0f);
+                const HostTensor* bb[3] = {bq, bk, bv};
+                for (int j = 0; j < 3; ++j)
+                    if (bb[j]) {
+                        std::vector<float> v = to_f32(*bb[j]);
+                        std::memcpy(&cat[(size_t)j * D], v.data(), (size_t)D * 4);
+                    }
+                L.bqkv = upload_f32(cat);
+            }
+        }
+        L.wo = make_weight(need(a + "linear_out.weight"), D, D, f16g);
+        L.bo = optb(a + "linear_out.bias");
+        L.wpos = make_weight(need(a + "linear_pos.weight"), D, D, f16g);
+        L.pos_u = upload_f32(need(a + "pos_bias_u"));
+        L.pos_v = upload_f32(need(a + "pos_bias_v"));
+        require(need(a + "pos_bias_u").nelem() == (int64_t)H * dk, "pos_bias_u shape");
+
+        const std::string cv = p + "conv.";
+        L.pw1 = make_weight_rows({&need(cv + "pointwise_conv1.weight")}, D, f16g, true);
+        if (const HostTensor* b1 = find(cv + "pointwise_conv1.bias")) {
+            std::vector<float> v = to_f32(*b1), il(v.size());
+            for (int r = 0; r < 2 * D; ++r) {
+                const int g = r / 32, j = r % 32;
+                il[(size_t)r] = v[(size_t)(j < 16 ? 16 * g + j : D + 16 * g + (j - 16))];
+            }
+            L.pw1_b = upload_f32(il);
+        }
+        L.pw2 = make_weight(need(cv + "pointwise_conv2.weight"), D, D, f16g);
+        L.pw2_b = optb(cv + "pointwise_conv2.bias");
+        {
+            const HostTensor& dw = need(cv + "depthwise_conv.weight");
+            require(dw.nelem() == (int64_t)D * K, "depthwise_conv.weight shape");
+            L.dw_w = upload_f32(dw);
+        }
+        L.dw_b = optb(cv + "depthwise_conv.bias");
+        {
+            // BatchNorm fold, exactly conformer.cpp:144-147 (f32).
+            std::vector<float> g = to_f32(need(cv + "batch_norm.weight")),
+                               bb = to_f32(need(cv + "batch_norm.bias")),
+                               m = to_f32(need(cv + "batch_norm.running_mean")),
+                               var = to_f32(need(cv + "batch_norm.running_var"));
+            std::vector<float> sc((size_t)D), sh((size_t)D);
+            for (int ch = 0; ch < D; ++ch) {
+                sc[(size_t)ch] = g[(size_t)ch] / std::sqrt(var[(size_t)ch] + 1e-5f);
+                sh[(size_t)ch] = bb[(size_t)ch] - m[(size_t)ch] * sc[(size_t)ch];
+            }
+            L.bn_scale = upload_f32(sc);
+            L.bn_shift = upload_f32(sh);
+        }
+    }
+
+    // subsampling
+    {
+        const std::string p = "encoder.pre_encode.";
+        int F = c.n_mels;
+        for (int s = 0; s < 3; ++s) F = (F - 1) / 2 + 1;
+        sub_.w0 = upload_f32(need(p + "conv.0.weight"));
+        sub_.b0 = upload_f32(need(p + "conv.0.bias"));
+        sub_.w2 = upload_f32(need(p + "conv.2.weight"));
+        sub_.b2 = upload_f32(need(p + "conv.2.bias"));
+        sub_.w5 = upload_f32(need(p + "conv.5.weight"));
+        sub_.b5 = upload_f32(need(p + "conv.5.bias"));
+        require(need(p + "conv.0.weight").nelem() == (int64_t)C * 9, "conv.0.weight shape");
+        sub_.w3 = make_weight(need(p + "conv.3.weight"), C, C, f16g);
+        sub_.b3 = upload_f32(need(p + "conv.3.bias"));
+        sub_.w6 = make_weight(need(p + "conv.6.weight"), C, C, f16g);
+        sub_.b6 = upload_f32(need(p + "conv.6.bias"));
+        sub_.out = make_weight(need(p + "out.weight"), D, C * F, f16g);
+        sub_.bout = upload_f32(need(p + "out.bias"));
+    }
+
+    // optional heads (always on the f32 GEMM path: argmax outputs)
+    {
+        const HostTensor* cw = find("ctc_decoder.decoder_layers.0.weight");
+        std::string cb = "ctc_decoder.decoder_layers.0.bias";
+        if (!cw) {
+            cw = find("decoder.decoder_layers.0.weight");
+            cb = "decoder.decoder_layers.0.bias";
+        }
+        if (cw) {
+            const int V = (int)(cw->nelem() / D);
+            heads_.ctc = make_weight(*cw, V, D, false);
+            heads_.ctc_b = upload_f32(need(cb));
+        }
+        const HostTensor* je = find("joint.enc.weight");
+        const HostTensor* jp = find("joint.pred.weight");
+        const HostTensor* jo = find("joint.joint_net.2.weight");
+        if (je && jp && jo) {
+            const int Hj = (int)(je->nelem() / D);
+            const int P = (int)(jp->nelem() / Hj);
+            const int V = (int)(jo->nelem() / Hj);
+            heads_.jenc = make_weight(*je, Hj, D, false);
+            heads_.jpred = make_weight(*jp, Hj, P, false);
+            heads_.jout = make_weight(*jo, V, Hj, false);
+            heads_.jenc_b = upload_f32(need("joint.enc.bias"));
+            heads_.jpred_b = upload_f32(need("joint.pred.bias"));
+            heads_.jout_b = upload_f32(need("joint.joint_net.2.bias"));
+            heads_.n_dur = c.n_durations;
+            heads_.n_tok = V - c.n_durations;
+            require(heads_.n_tok > 0, "joint: vocab/durations mismatch");
+        }
+    }
+    host_.clear();
+    finalized_ = true;
+}
+
+// ---------------------------------------------------------------------------
+// helpers
+// ---------------------------------------------------------------------------
+void Model::set_profiling(bool on) {
+    profiling_ = on;
+    if (on && !ev_[0]) {
+        PKX_HIP(hipEventCreate(&ev_[0]));
+        PKX_HIP(hipEventCreate(&ev_[1]));
+    }
+    for (int i = 0; i < KF_COUNT; ++i) {
+        prof_ms_[i] = 0;
+        prof_n_[i] = 0;
+    }
+}
+
+void Model::profile_read(double* ms, int64_t* n) {
+    for (int i = 0; i < KF_COUNT; ++i) {
+        if (ms) ms[i] = prof_ms_[i];
+        if (n) n[i] = prof_n_[i];
+    }
+}
+
+void Model::mark(int fam, hipStream_t s, bool begin) {
+    if (!profiling_ || fam < 0) return;
+    if (begin) {
+        PKX_HIP(hipEventRecord(ev_[0], s));
+    } else {
+        PKX_HIP(hipEventRecord(ev_[1], s));
+        PKX_HIP(hipEventSynchronize(ev_[1]));
+        float ms = 0.f;
+        PKX_HIP(hipEventElapsedTime(&ms, ev_[0], ev_[1]));
+        prof_ms_[fam] += ms;
+        prof_n_[fam] += 1;
+    }
+}
+
+void Model::gemm(const DevWeight& w, int epi, const void* A, int64_t lda, int64_t M,
+                 const float* bias, void* Y, int64_t ldy, float alpha, const int* valid, int T,
+                 hipStream_t s, Precision prec, int fam, const float* bias2, int trF) {
+    GemmParams p;
+    p.A = A;
+    p.lda = lda;
+    p.Wq = w.q;
+    p.Ws = w.s;
+    p.bias = bias;
+    p.bias2 = bias2;
+    p.Y = Y;
+    p.ldy = ldy;
+    p.alpha = alpha;
+    p.valid = valid;
+    p.T = T;
+    p.trF = trF;
+    p.M = (int)M;
+    p.N = w.N;
+    p.K = w.K;
+    mark(fam, s, true);
+    launch_gemm(prec, w.gtype, epi, p, s);
+    mark(fam, s, false);
+}
+
+void Model::ensure_ws(int B, int T_max) {
+    const ModelConfig& c = cfg_;
+    const size_t as = prec_ == PREC_F16 ? 2 : 4;
+    const int T1 = (T_max - 1) / 2 + 1, T2 = (T1 - 1) / 2 + 1, T3 = (T2 - 1) / 2 + 1;
+    const int F1 = (c.n_mels - 1) / 2 + 1, F2 = (F1 - 1) / 2 + 1, F3 = (F2 - 1) / 2 + 1;
+    const size_t C = c.sub_channels, D = c.d_model, M = (size_t)B * T3, P = 2 * (size_t)T3 - 1;
+    Ws& w = *ws_;
+    grow(w.a1, (size_t)B * T1 * F1 * C * as);
+    grow(w.a2, (size_t)B * T2 * F2 * C * as);
+    grow(w.a2p, (size_t)B * T2 * F2 * C * as);
+    grow(w.a3, (size_t)B * T3 * F3 * C * as);
+    grow(w.flat, (size_t)B * T3 * F3 * C * as);
+    grow(w.h, M * D * as);
+    grow(w.u, M * c.ff_dim * as);
+    grow(w.qkv, M * 3 * D * as);
+    grow(w.g, M * D * as);
+    grow(w.pe, P * D * as);
+    grow(w.p, P * D * as);
+    grow(w.tmp, M * D * 4);
+    if (B > w.Bcap) {
+        if (w.d_valid) PKX_HIP(hipFree(w.d_valid));
+        if (w.h_valid) PKX_HIP(hipHostFree(w.h_valid));
+        w.d_valid = nullptr;
+        w.h_valid = nullptr;
+        PKX_HIP(hipMalloc(&w.d_valid, sizeof(int) * 4 * (size_t)B));
+        PKX_HIP(hipHostMalloc(&w.h_valid, sizeof(int) * 4 * (size_t)B, hipHostMallocDefault));
+        w.Bcap = B;
+    }
+    if (!w.staged) PKX_HIP(hipEventCreateWithFlags(&w.staged, hipEventDisableTiming));
+}
+
+// Stage per-item lengths (slots v0, v1, v2, vout) through pinned memory in one copy.
+void Model::stage_valid(const std::vector<int>* v[4], hipStream_t s) {
+    Ws& w = *ws_;
+    PKX_HIP(hipEventSynchronize(w.staged));   // the previous copy out of the staging buffer is done
+    for (int k = 0; k < 4; ++k)
+        std::memcpy(w.h_valid + (size_t)k * w.Bcap, v[k]->data(), v[k]->size() * sizeof(int));
+    PKX_HIP(hipMemcpyAsync(w.d_valid, w.h_valid, sizeof(int) * 4 * (size_t)w.Bcap, hipMemcpyHostToDevice, s));
+    PKX_HIP(hipEventRecord(w.staged, s));
+}
+
+void Model::ensure_pe(int T, hipStream_t s) {
+    mark(KF_POS_ENC, s, true);
+    launch_rel_pos_encoding(prec_, ws_->pe.p, T, cfg_.d_model, s);
+    mark(KF_POS_ENC, s, false);
+}
+
+void* Model::cast_to_act(const float* x, int64_t n, hipStream_t s) {
+    grow(ws_->xin, (size_t)n * (prec_ == PREC_F16 ? 2 : 4));
+    launch_cast_f32(prec_, x, ws_->xin.p, n, s);
+    return ws_->xin.p;
+}
+
+// ---------------------------------------------------------------------------
+// subsampling (subsampling.cpp:48-240 batched / :242-386 scalar masking)
+// ---------------------------------------------------------------------------
+int Model::subsampling_forward(const float* mel, int B, int T_max, const int* valid_T,
+                               bool stage_masks, float* out, int* valid_out, hipStream_t s,
+                               bool apply_xscaling) {
+    require(finalized_, "model not finalized");
+    require(B > 0 && T_max > 0, "subsampling: empty batch");
+    ensure_ws(B, T_max);
+    const ModelConfig& c = cfg_;
+    const int C = c.sub_channels, F = c.n_mels;
+    const int T1 = (T_max - 1) / 2 + 1, T2 = (T1 - 1) / 2 + 1, T3 = (T2 - 1) / 2 + 1;
+    const int F1 = (F - 1) / 2 + 1, F2 = (F1 - 1) / 2 + 1, F3 = (F2 - 1) / 2 + 1;
+    std::vector<int> v0(B), v1(B), v2(B), vo(B);
+    for (int b = 0; b < B; ++b) {
+        const int vt = valid_T ? valid_T[b] : T_max;
+        require(vt >= 1 && vt <= T_max, "valid_T out of range");
+        v0[b] = vt - 1;                                 // offline T-1 entry convention
+        v1[b] = (v0[b] + 2 - 3) / 2 + 1;
+        v2[b] = (v1[b] + 2 - 3) / 2 + 1;
+        const int vv = valid_out_len(T_max, v0[b]);
+        vo[b] = vv > T3 ? T3 : vv;
+        if (valid_out) valid_out[b] = vo[b];
+    }
+    const std::vector<int>* slots[4] = {&v0, &v1, &v2, &vo};
+    stage_valid(slots, s);
+    Ws& w = *ws_;
+    const int* dv = w.d_valid;
+    const int Bc = w.Bcap;
+    mark(KF_SUBSAMPLING, s, true);
+    launch_sub_conv0(prec_, mel, stage_masks ? dv : nullptr, sub_.w0, sub_.b0, w.a1.p, B, F, T_max, C, s);
+    launch_sub_dwconv(prec_, w.a1.p, stage_masks ? dv + Bc : nullptr, sub_.w2, sub_.b2, w.a2.p, B, T1, F1, C, s);
+    gemm(sub_.w3, EPI_RELU, w.a2.p, C, (int64_t)B * T2 * F2, sub_.b3, w.a2p.p, C, 1.f, nullptr, 1, s, prec_, -1);
+    launch_sub_dwconv(prec_, w.a2p.p, stage_masks ? dv + 2 * Bc : nullptr, sub_.w5, sub_.b5, w.a3.p, B, T2, F2, C, s);
+    gemm(sub_.w6, EPI_RELU_TR, w.a3.p, C, (int64_t)B * T3 * F3, sub_.b6, w.flat.p, 0, 1.f, dv + 3 * Bc, T3, s,
+         prec_, -1, nullptr, F3);
+    const float xs = (apply_xscaling && c.xscaling) ? std::sqrt((float)c.d_model) : 1.0f;  // encoder.cpp:122-124
+    gemm(sub_.out, EPI_STORE_F32, w.flat.p, (int64_t)C * F3, (int64_t)B * T3, sub_.bout, out, c.d_model, xs,
+         nullptr, 1, s, prec_, -1);
+    mark(KF_SUBSAMPLING, s, false);
+    return T3;
+}
+
+// ---------------------------------------------------------------------------
+// one conformer layer (conformer.cpp:285-353) on the f32 residual stream x
+// ---------------------------------------------------------------------------
+void Model::layer_body(int l, float* x, int B, int T, const int* d_valid, bool first_ln_done,
+                       bool fuse_next_ln, hipStream_t s) {
+    const ModelConfig& c = cfg_;
+    const LayerDev& L = layers_[l];
+    const int D = c.d_model, H = c.n_heads, dk = D / H;
+    const int64_t M = (int64_t)B * T;
+    Ws& w = *ws_;
+    auto ln = [&](const float* g, const float* b) {
+        LnParams p;
+        p.x = x;
+        p.g = g;
+        p.b = b;
+        p.y = w.h.p;
+        p.M = M;
+        p.D = D;
+        mark(KF_LAYERNORM, s, true);
+        launch_layernorm(prec_, p, s);
+        mark(KF_LAYERNORM, s, false);
+    };
+    // Stage A: x += 0.5 * FFN1(LN(x))
+    if (!first_ln_done) ln(L.ff1_ln_g, L.ff1_ln_b);
+    gemm(L.ff1_w1, EPI_SILU, w.h.p, D, M, L.ff1_b1, w.u.p, c.ff_dim, 1.f, nullptr, 1, s, prec_, KF_GEMM_FFN);
+    gemm(L.ff1_w2, EPI_RESID, w.u.p, c.ff_dim, M, L.ff1_b2, x, D, 0.5f, nullptr, 1, s, prec_, KF_GEMM_FFN);
+    // Stage B: x += MHSA(LN(x))
+    ln(L.att_ln_g, L.att_ln_b);
+    gemm(L.wqkv, EPI_STORE, w.h.p, D, M, L.bqkv, w.qkv.p, 3 * D, 1.f, nullptr, 1, s, prec_, KF_GEMM_QKV);
+    gemm(L.wpos, EPI_STORE, w.pe.p, D, 2 * (int64_t)T - 1, nullptr, w.p.p, D, 1.f, nullptr, 1, s, prec_,
+         KF_GEMM_POS);
+    {
+        const size_t as = prec_ == PREC_F16 ? 2 : 4;
+        AttnParams a;
+        a.q = w.qkv.p;
+        a.k = (const uint8_t*)w.qkv.p + (size_t)D * as;
+        a.v = (const uint8_t*)w.qkv.p + (size_t)2 * D * as;
+        a.ldq = a.ldk = a.ldv = 3 * D;
+        a.p = w.p.p;
+        a.ldp = D;
+        a.bias_u = L.pos_u;
+        a.bias_v = L.pos_v;
+        a.valid = d_valid;
+        a.out = w.h.p;
+        a.ldo = D;
+        a.B = B;
+        a.T = T;
+        a.H = H;
+        a.dk = dk;
+        a.scale = 1.0f / std::sqrt((float)dk);
+        mark(KF_ATTENTION, s, true);
+        launch_relpos_attention(prec_, a, s);
+        mark(KF_ATTENTION, s, false);
+    }
+    gemm(L.wo, EPI_RESID, w.h.p, D, M, L.bo, x, D, 1.f, nullptr, 1, s, prec_, KF_GEMM_OUT);
+    // Stage C: x += conv(LN(x))
+    ln(L.conv_ln_g, L.conv_ln_b);
+    gemm(L.pw1, EPI_GLU, w.h.p, D, M, L.pw1_b, w.g.p, D, 1.f, d_valid, T, s, prec_, KF_GEMM_PW1_GLU);
+    mark(KF_DWCONV, s, true);
+    launch_dwconv_bn_silu(prec_, w.g.p, w.h.p, L.dw_w, L.dw_b, L.bn_scale, L.bn_shift, B, T, D, c.conv_kernel, s);
+    mark(KF_DWCONV, s, false);
+    if (conv_capture_) {
+        gemm(L.pw2, EPI_STORE_F32, w.h.p, D, M, L.pw2_b, conv_capture_, D, 1.f, nullptr, 1, s, prec_, KF_GEMM_PW2);
+        launch_add_f32(x, conv_capture_, M * D, s);
+    } else {
+        gemm(L.pw2, EPI_RESID, w.h.p, D, M, L.pw2_b, x, D, 1.f, nullptr, 1, s, prec_, KF_GEMM_PW2);
+    }
+    // Stage D: x += 0.5 * FFN2(LN(x)); x = LN_out(x) [fused with next layer's LN_ff1]
+    ln(L.ff2_ln_g, L.ff2_ln_b);
+    gemm(L.ff2_w1, EPI_SILU, w.h.p, D, M, L.ff2_b1, w.u.p, c.ff_dim, 1.f, nullptr, 1, s, prec_, KF_GEMM_FFN);
+    gemm(L.ff2_w2, EPI_RESID, w.u.p, c.ff_dim, M, L.ff2_b2, x, D, 0.5f, nullptr, 1, s, prec_, KF_GEMM_FFN);
+    {
+        LnParams p;
+        p.x = x;
+        p.g = L.out_ln_g;
+        p.b = L.out_ln_b;
+        p.y_f32 = x;
+        if (fuse_next_ln) {
+            p.g2 = layers_[l + 1].ff1_ln_g;
+            p.b2 = layers_[l + 1].ff1_ln_b;
+            p.y = w.h.p;
+        }
+        p.M = M;
+        p.D = D;
+        mark(KF_LAYERNORM, s, true);
+        launch_layernorm(prec_, p, s);
+        mark(KF_LAYERNORM, s, false);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// encoder (encoder.cpp:97-167)
+// ---------------------------------------------------------------------------
+int Model::encoder_forward(const float* mel, int B, int T_max, const int* valid_T, bool stage_masks,
+                           float* out, int* valid_out, float* capture, hipStream_t s) {
+    std::vector<int> vo(B);
+    const int T3 = subsampling_forward(mel, B, T_max, valid_T, stage_masks, out, vo.data(), s, true);
+    if (valid_out) std::memcpy(valid_out, vo.data(), sizeof(int) * B);
+    const int* dvalid = ws_->d_valid + 3 * ws_->Bcap;
+    ensure_pe(T3, s);
+    const int L = cfg_.n_layers;
+    const size_t MD = (size_t)B * T3 * cfg_.d_model;
+    for (int l = 0; l < L; ++l) {
+        layer_body(l, out, B, T3, dvalid, l > 0, l + 1 < L, s);
+        if (capture)
+            PKX_HIP(hipMemcpyAsync(capture + (size_t)l * MD, out, MD * 4, hipMemcpyDeviceToDevice, s));
+    }
+    return T3;
+}
+
+void Model::conformer_layer_forward(int layer, const float* x, int B, int T, const int* valid,
+                                    float* out, float* conv_out, hipStream_t s) {
+    require(finalized_, "model not finalized");
+    require(layer >= 0 && layer < cfg_.n_layers, "layer index out of range");
+    const int T_mel = 8 * T;  // any T_max whose subsampled length is >= T sizes the workspace
+    ensure_ws(B, T_mel);
+    std::vector<int> v(B);
+    for (int b = 0; b < B; ++b) {
+        v[b] = valid ? valid[b] : T;
+        require(v[b] >= 1 && v[b] <= T, "valid out of range");
+    }
+    {
+        const std::vector<int>* slots[4] = {&v, &v, &v, &v};
+        stage_valid(slots, s);
+    }
+    ensure_pe(T, s);
+    const size_t MD = (size_t)B * T * cfg_.d_model;
+    if (out != x) PKX_HIP(hipMemcpyAsync(out, x, MD * 4, hipMemcpyDeviceToDevice, s));
+    conv_capture_ = conv_out;
+    try {
+        layer_body(layer, out, B, T, ws_->d_valid + 3 * ws_->Bcap, false, false, s);
+    } catch (...) {
+        conv_capture_ = nullptr;
+        throw;
+    }
+    conv_capture_ = nullptr;
+}
+
+void Model::relpos_attention_forward(int layer, const float* x, int B, int T, const int* valid,
+                                     float* out, hipStream_t s) {
+    require(finalized_, "model not finalized");
+    require(layer >= 0 && layer < cfg_.n_layers, "layer index out of range");
+    ensure_ws(B, 8 * T);
+    std::vector<int> v(B);
+    for (int b = 0; b < B; ++b) {
+        v[b] = valid ? valid[b] : T;
+        require(v[b] >= 1 && v[b] <= T, "valid out of range");
+    }
+    {
+        const std::vector<int>* slots[4] = {&v, &v, &v, &v};
+        stage_valid(slots, s);
+    }
+    ensure_pe(T, s);
+    const ModelConfig& c = cfg_;
+    const LayerDev& L = layers_[layer];
+    const int D = c.d_model, H = c.n_heads, dk = D / H;
+    const int64_t M = (int64_t)B * T;
+    Ws& w = *ws_;
+    void* xa = cast_to_act(x, M * D, s);
+    gemm(L.wqkv, EPI_STORE, xa, D, M, L.bqkv, w.qkv.p, 3 * D, 1.f, nullptr, 1, s, prec_, KF_GEMM_QKV);
+    gemm(L.wpos, EPI_STORE, w.pe.p, D, 2 * (int64_t)T - 1, nullptr, w.p.p, D, 1.f, nullptr, 1, s, prec_, KF_GEMM_POS);
+    const size_t as = prec_ == PREC_F16 ? 2 : 4;
+    AttnParams a;
+    a.q = w.qkv.p;
+    a.k = (const uint8_t*)w.qkv.p + (size_t)D * as;
+    a.v = (const uint8_t*)w.qkv.p + (size_t)2 * D * as;
+    a.ldq = a.ldk = a.ldv = 3 * D;
+    a.p = w.p.p;
+    a.ldp = D;
+    a.bias_u = L.pos_u;
+    a.bias_v = L.pos_v;
+    a.valid = w.d_valid + 3 * w.Bcap;
+    a.out = w.h.p;
+    a.ldo = D;
+    a.B = B;
+    a.T = T;
+    a.H = H;
+    a.dk = dk;
+    a.scale = 1.0f / std::sqrt((float)dk);
+    launch_relpos_attention(prec_, a, s);
+    gemm(L.wo, EPI_STORE_F32, w.h.p, D, M, L.bo, out, D, 1.f, nullptr, 1, s, prec_, KF_GEMM_OUT);
+}
+
+void Model::conv_module_forward(int layer, const float* cin, int B, int T, const int* valid, float* out,
+                                hipStream_t s) {
+    require(finalized_, "model not finalized");
+    require(layer >= 0 && layer < cfg_.n_layers, "layer index out of range");
+    ensure_ws(B, 8 * T);
+    std::vector<int> v(B);
+    for (int b = 0; b < B; ++b) {
+        v[b] = valid ? valid[b] : T;
+        require(v[b] >= 1 && v[b] <= T, "valid out of range");
+    }
+    {
+        const std::vector<int>* slots[4] = {&v, &v, &v, &v};
+        stage_valid(slots, s);
+    }
+    const ModelConfig& c = cfg_;
+    const LayerDev& L = layers_[layer];
+    const int D = c.d_model;
+    const int64_t M = (int64_t)B * T;
+    Ws& w = *ws_;
+    void* xa = cast_to_act(cin, M * D, s);
+    gemm(L.pw1, EPI_GLU, xa, D, M, L.pw1_b, w.g.p, D, 1.f, w.d_valid + 3 * w.Bcap, T, s, prec_, KF_GEMM_PW1_GLU);
+    launch_dwconv_bn_silu(prec_, w.g.p, w.h.p, L.dw_w, L.dw_b, L.bn_scale, L.bn_shift, B, T, D, c.conv_kernel, s);
+    gemm(L.pw2, EPI_STORE_F32, w.h.p, D, M, L.pw2_b, out, D, 1.f, nullptr, 1, s, prec_, KF_GEMM_PW2);
+}
+
+// ---------------------------------------------------------------------------
+// heads
+// ---------------------------------------------------------------------------
+void Model::ctc_forward(const float* enc, int64_t M, float* logprobs, int32_t* argmax, hipStream_t s) {
+    require(finalized_ && heads_.ctc.ok(), "model has no CTC head");
+    gemm(heads_.ctc, EPI_STORE_F32, enc, cfg_.d_model, M, heads_.ctc_b, logprobs, heads_.ctc.N, 1.f, nullptr, 1,
+         s, PREC_F32, -1);
+    launch_log_softmax_argmax(logprobs, logprobs, argmax, M, heads_.ctc.N, s);
+}
+
+void Model::tdt_joint_argmax(const float* enc, int64_t M, const float* g, float* logits, int32_t* tok,
+                             int32_t* dur, hipStream_t s) {
+    require(finalized_ && heads_.jout.ok(), "model has no TDT joint");
+    const int Hj = heads_.jenc.N;
+    Ws& w = *ws_;
+    grow(w.pp, (size_t)Hj * 4);
+    grow(w.logits, (size_t)M * Hj * 4);
+    gemm(heads_.jpred, EPI_STORE_F32, g, heads_.jpred.K, 1, heads_.jpred_b, w.pp.p, Hj, 1.f, nullptr, 1, s,
+         PREC_F32, -1);
+    gemm(heads_.jenc, EPI_RELU2_F32, enc, cfg_.d_model, M, heads_.jenc_b, w.logits.p, Hj, 1.f, nullptr, 1, s,
+         PREC_F32, -1, (const float*)w.pp.p);
+    gemm(heads_.jout, EPI_STORE_F32, w.logits.p, Hj, M, heads_.jout_b, logits, heads_.jout.N, 1.f, nullptr, 1, s,
+         PREC_F32, -1);
+    launch_split_argmax(logits, M, heads_.n_tok, heads_.n_dur, tok, dur, s);
+}
+
+}  // namespace pkx

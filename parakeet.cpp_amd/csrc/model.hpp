@@ -1,0 +1,169 @@
+// Device-resident encoder model and its forward orchestration.
+//
+// Replaces the reference's L2 graph runtime for the encoder path
+// (backend.cpp:140-285, ggml_graph.cpp:81-98, model_loader.cpp:47-98): weights
+// are uploaded once, repacked into MFMA-friendly layouts (q8_0 -> int8 + f16
+// scale planes, q4_K -> nibble plane + {d*sc, dmin*m} pairs, pointwise_conv1
+// rows interleaved for the fused GLU epilogue, q/k/v concatenated), BatchNorm
+// is folded once at upload instead of per call (conformer.cpp:134-154), and a
+// grow-only workspace holds every activation of a forward.
+#pragma once
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "attention.hpp"
+#include "common.hpp"
+#include "elementwise.hpp"
+#include "gemm.hpp"
+
+namespace pkx {
+
+struct ModelConfig {
+    int d_model = 0, n_layers = 0, n_heads = 0, ff_dim = 0, conv_kernel = 0;
+    int n_mels = 0, sub_channels = 0;
+    int xscaling = 0;
+    int vocab_size = 0, n_durations = 0;
+};
+
+struct HostTensor {
+    int gtype = GT_F32;
+    int n_dims = 0;
+    int64_t ne[4] = {1, 1, 1, 1};   // ggml order (ne[0] fastest)
+    std::vector<uint8_t> bytes;
+    int64_t nelem() const { return ne[0] * ne[1] * ne[2] * ne[3]; }
+};
+
+struct DevWeight {
+    int gtype = -1;   // device storage type (GT_F32/GT_F16/GT_Q8_0/GT_Q4_K)
+    int N = 0, K = 0;
+    void* q = nullptr;
+    void* s = nullptr;
+    bool ok() const { return gtype >= 0; }
+};
+
+struct LayerDev {
+    float *ff1_ln_g = nullptr, *ff1_ln_b = nullptr, *att_ln_g = nullptr, *att_ln_b = nullptr;
+    float *conv_ln_g = nullptr, *conv_ln_b = nullptr, *ff2_ln_g = nullptr, *ff2_ln_b = nullptr;
+    float *out_ln_g = nullptr, *out_ln_b = nullptr;
+    DevWeight ff1_w1, ff1_w2, ff2_w1, ff2_w2;
+    float *ff1_b1 = nullptr, *ff1_b2 = nullptr, *ff2_b1 = nullptr, *ff2_b2 = nullptr;
+    DevWeight wqkv, wo, wpos;
+    float *bqkv = nullptr, *bo = nullptr, *pos_u = nullptr, *pos_v = nullptr;
+    DevWeight pw1, pw2;
+    float *pw1_b = nullptr, *pw2_b = nullptr, *dw_w = nullptr, *dw_b = nullptr;
+    float *bn_scale = nullptr, *bn_shift = nullptr;
+};
+
+struct SubDev {
+    float *w0 = nullptr, *b0 = nullptr, *w2 = nullptr, *b2 = nullptr, *w5 = nullptr, *b5 = nullptr;
+    DevWeight w3, w6, out;
+    float *b3 = nullptr, *b6 = nullptr, *bout = nullptr;
+};
+
+struct HeadsDev {
+    DevWeight ctc;
+    float* ctc_b = nullptr;
+    DevWeight jenc, jpred, jout;
+    float *jenc_b = nullptr, *jpred_b = nullptr, *jout_b = nullptr;
+    int n_tok = 0, n_dur = 0;
+};
+
+// Per-kernel-family timing collected when profiling is enabled.
+enum KFam : int {
+    KF_SUBSAMPLING = 0, KF_LAYERNORM, KF_GEMM_FFN, KF_GEMM_QKV, KF_GEMM_POS, KF_ATTENTION,
+    KF_GEMM_OUT, KF_GEMM_PW1_GLU, KF_DWCONV, KF_GEMM_PW2, KF_POS_ENC, KF_COUNT
+};
+
+class Model {
+public:
+    Model(const ModelConfig& cfg, int precision);
+    ~Model();
+    Model(const Model&) = delete;
+    Model& operator=(const Model&) = delete;
+
+    void set_tensor(const std::string& name, int gtype, int n_dims, const int64_t* ne,
+                    const void* data, size_t nbytes);
+    void finalize();
+
+    const ModelConfig& config() const { return cfg_; }
+    Precision precision() const { return prec_; }
+    bool has_ctc() const { return heads_.ctc.ok(); }
+    bool has_joint() const { return heads_.jout.ok(); }
+
+    // Encoder (encoder.cpp:97-167).  mel [B][n_mels][T_max] f32 device,
+    // valid_T host (true mel frames per item, nullptr = T_max).  out [B][T'][D]
+    // f32 device; valid_out host [B].  stage_masks selects the batched
+    // subsampling masking (subsampling.cpp:109-147) or the scalar one.
+    int encoder_forward(const float* mel, int B, int T_max, const int* valid_T, bool stage_masks,
+                        float* out, int* valid_out, float* capture, hipStream_t s);
+    int subsampling_forward(const float* mel, int B, int T_max, const int* valid_T,
+                            bool stage_masks, float* out, int* valid_out, hipStream_t s,
+                            bool apply_xscaling = false);
+    void conformer_layer_forward(int layer, const float* x, int B, int T, const int* valid,
+                                 float* out, float* conv_out, hipStream_t s);
+    void relpos_attention_forward(int layer, const float* x, int B, int T, const int* valid,
+                                  float* out, hipStream_t s);
+    void conv_module_forward(int layer, const float* c, int B, int T, const int* valid, float* out,
+                             hipStream_t s);
+    void ctc_forward(const float* enc, int64_t M, float* logprobs, int32_t* argmax, hipStream_t s);
+    void tdt_joint_argmax(const float* enc, int64_t M, const float* g, float* logits, int32_t* tok,
+                          int32_t* dur, hipStream_t s);
+    void set_profiling(bool on);
+    void profile_read(double* ms_per_family, int64_t* launches_per_family);
+
+private:
+    struct Ws;
+    void* dalloc(size_t bytes);
+    float* upload_f32(const HostTensor& t);
+    float* upload_f32(const std::vector<float>& v);
+    DevWeight make_weight(const HostTensor& t, int N, int K, bool f16_gemm);
+    DevWeight make_weight_rows(const std::vector<const HostTensor*>& parts, int K, bool f16_gemm,
+                               bool glu_interleave);
+    const HostTensor* find(const std::string& n) const;
+    const HostTensor& need(const std::string& n) const;
+    void ensure_ws(int B, int T_max);
+    void gemm(const DevWeight& w, int epi, const void* A, int64_t lda, int64_t M,
+              const float* bias, void* Y, int64_t ldy, float alpha, const int* valid, int T,
+              hipStream_t s, Precision prec, int fam, const float* bias2 = nullptr, int trF = 1);
+    void layer_body(int l, float* x, int B, int T, const int* d_valid, bool first_ln_done,
+                    bool fuse_next_ln, hipStream_t s);
+    void ensure_pe(int T, hipStream_t s);
+    void stage_valid(const std::vector<int>* v[4], hipStream_t s);
+    void mark(int fam, hipStream_t s, bool begin);
+    void* cast_to_act(const float* x, int64_t n, hipStream_t s);
+
+    ModelConfig cfg_;
+    Precision prec_;
+    bool finalized_ = false;
+    std::map<std::string, HostTensor> host_;
+    std::vector<void*> allocs_;
+    std::vector<LayerDev> layers_;
+    SubDev sub_;
+    HeadsDev heads_;
+    std::unique_ptr<Ws> ws_;
+    float* conv_capture_ = nullptr;   // conformer_layer_forward's conv-module output
+    bool profiling_ = false;
+    double prof_ms_[KF_COUNT] = {};
+    int64_t prof_n_[KF_COUNT] = {};
+    hipEvent_t ev_[2] = {nullptr, nullptr};
+};
+
+// Upload one raw-layout weight (repacked for the f16 or f32 GEMM path); the
+// device buffers are appended to `allocs`.
+DevWeight build_weight(const HostTensor& t, int N, int K, bool f16_gemm, std::vector<void*>& allocs);
+
+// y[M][N] = x[M][K] . W^T (+ bias) for one raw weight, f32 in/out; the weight
+// is uploaded for this call and freed after the stream drains.
+void linear_raw(Precision prec, const HostTensor& t, int N, int K, const float* bias, const float* x,
+                int64_t M, float* y, hipStream_t s);
+
+// GGUF v3 reader: fills a Model with the encoder (+ head) tensors and config.
+std::unique_ptr<Model> load_gguf(const std::string& path, int precision);
+
+// subsampling.cpp:25-46 arithmetic
+int subsampled_len(int T);
+int valid_out_len(int T, int in_valid);
+
+}  // namespace pkx

@@ -1,0 +1,331 @@
+"""ctypes binding of libpkx.so (include/pkx.h) for tests, smoke and bench.
+
+The native library owns device memory and streams through its own HIP
+runtime, so no other GPU framework needs to be loaded in the same process.
+Importing this module never falls back to anything: if libpkx.so is missing
+or fails to load, it raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(PKG, "build", "libpkx.so")
+
+PREC_AUTO, PREC_F32, PREC_F16 = -1, 0, 1
+MASK_BATCHED, MASK_SCALAR = 0, 1
+PROF_FAMILIES = ["subsampling", "layernorm", "gemm_ffn", "gemm_qkv", "gemm_pos", "attention",
+                 "gemm_out", "gemm_pw1_glu", "dwconv", "gemm_pw2", "pos_enc"]
+
+_vp = C.c_void_p
+_f = C.POINTER(C.c_float)
+_ip = C.POINTER(C.c_int)
+
+
+class PkxError(RuntimeError):
+    pass
+
+
+class Config(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("d_model", "n_layers", "n_heads", "ff_dim", "conv_kernel",
+                                        "n_mels", "sub_channels", "xscaling", "vocab_size",
+                                        "n_durations")]
+
+
+SIGS = {
+    "pkx_abi_version": ([], C.c_int),
+    "pkx_last_error": ([], C.c_char_p),
+    "pkx_device_count": ([_ip], C.c_int),
+    "pkx_malloc": ([C.POINTER(_vp), C.c_size_t], C.c_int),
+    "pkx_free": ([_vp], C.c_int),
+    "pkx_memcpy_h2d": ([_vp, _vp, C.c_size_t, _vp], C.c_int),
+    "pkx_memcpy_d2h": ([_vp, _vp, C.c_size_t, _vp], C.c_int),
+    "pkx_memcpy_d2d": ([_vp, _vp, C.c_size_t, _vp], C.c_int),
+    "pkx_stream_create": ([C.POINTER(_vp)], C.c_int),
+    "pkx_stream_destroy": ([_vp], C.c_int),
+    "pkx_stream_synchronize": ([_vp], C.c_int),
+    "pkx_event_create": ([C.POINTER(_vp)], C.c_int),
+    "pkx_event_destroy": ([_vp], C.c_int),
+    "pkx_event_record": ([_vp, _vp], C.c_int),
+    "pkx_event_elapsed_ms": ([_f, _vp, _vp], C.c_int),
+    "pkx_model_load_gguf": ([C.c_char_p, C.c_int, C.POINTER(_vp)], C.c_int),
+    "pkx_model_create": ([C.POINTER(Config), C.c_int, C.POINTER(_vp)], C.c_int),
+    "pkx_model_set_tensor": ([_vp, C.c_char_p, C.c_int, C.c_int, C.POINTER(C.c_int64), _vp,
+                              C.c_size_t], C.c_int),
+    "pkx_model_finalize": ([_vp], C.c_int),
+    "pkx_model_free": ([_vp], C.c_int),
+    "pkx_model_info": ([_vp, C.POINTER(Config), _ip, _ip, _ip], C.c_int),
+    "pkx_subsampled_len": ([C.c_int], C.c_int),
+    "pkx_valid_out_len": ([C.c_int, C.c_int], C.c_int),
+    "pkx_encoder_forward": ([_vp, _vp, C.c_int, C.c_int, _ip, C.c_int, _vp, _ip, _ip, _vp, _vp],
+                            C.c_int),
+    "pkx_compact_channels_first": ([_vp, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp, _vp], C.c_int),
+    "pkx_subsampling_forward": ([_vp, _vp, C.c_int, C.c_int, _ip, C.c_int, _vp, _ip, _ip, _vp],
+                                C.c_int),
+    "pkx_conformer_layer_forward": ([_vp, C.c_int, _vp, C.c_int, C.c_int, _ip, _vp, _vp, _vp],
+                                    C.c_int),
+    "pkx_relpos_attention_forward": ([_vp, C.c_int, _vp, C.c_int, C.c_int, _ip, _vp, _vp], C.c_int),
+    "pkx_conv_module_forward": ([_vp, C.c_int, _vp, C.c_int, C.c_int, _ip, _vp, _vp], C.c_int),
+    "pkx_ctc_forward": ([_vp, _vp, C.c_int64, _vp, _vp, _vp], C.c_int),
+    "pkx_tdt_joint_argmax": ([_vp, _vp, C.c_int64, _vp, _vp, _vp, _vp, _vp], C.c_int),
+    "pkx_dequantize": ([C.c_int, _vp, _vp, C.c_int64, _vp], C.c_int),
+    "pkx_linear": ([C.c_int, C.c_int, C.c_int, C.c_int, _vp, C.c_size_t, _vp, _vp, C.c_int64, _vp,
+                    _vp], C.c_int),
+    "pkx_layernorm": ([_vp, _vp, _vp, _vp, C.c_int64, C.c_int, C.c_float, _vp], C.c_int),
+    "pkx_rel_pos_encoding": ([C.c_int, C.c_int, _vp, _vp], C.c_int),
+    "pkx_model_set_profiling": ([_vp, C.c_int], C.c_int),
+    "pkx_model_profile_read": ([_vp, C.POINTER(C.c_double), C.POINTER(C.c_int64)], C.c_int),
+}
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise PkxError(f"{LIB_PATH} is not built (run __graft_entry__.build())")
+        L = C.CDLL(LIB_PATH)
+        for name, (args, res) in SIGS.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = res
+        _lib = L
+    return _lib
+
+
+def check(rc):
+    if rc != 0:
+        raise PkxError(lib().pkx_last_error().decode())
+
+
+def device_count() -> int:
+    n = C.c_int(0)
+    check(lib().pkx_device_count(C.byref(n)))
+    return n.value
+
+
+def _sh(stream):
+    return stream.handle if stream is not None else None
+
+
+def _iptr(a):
+    if a is None:
+        return None
+    return a.ctypes.data_as(_ip)
+
+
+class DeviceArray:
+    """A device allocation with a numpy-like shape/dtype (no arithmetic)."""
+
+    def __init__(self, shape, dtype=np.float32):
+        self.shape = tuple(int(s) for s in shape)
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape)) * self.dtype.itemsize
+        p = _vp()
+        check(lib().pkx_malloc(C.byref(p), max(self.nbytes, 16)))
+        self.ptr = p.value
+
+    @classmethod
+    def from_numpy(cls, a, stream=None):
+        a = np.ascontiguousarray(a)
+        d = cls(a.shape, a.dtype)
+        d.upload(a, stream)
+        return d
+
+    def upload(self, a, stream=None):
+        a = np.ascontiguousarray(a, dtype=self.dtype)
+        assert a.nbytes == self.nbytes, (a.shape, self.shape)
+        check(lib().pkx_memcpy_h2d(self.ptr, a.ctypes.data, self.nbytes, _sh(stream)))
+
+    def numpy(self, stream=None):
+        out = np.empty(self.shape, dtype=self.dtype)
+        check(lib().pkx_memcpy_d2h(out.ctypes.data, self.ptr, self.nbytes, _sh(stream)))
+        return out
+
+    def free(self):
+        if self.ptr:
+            lib().pkx_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Stream:
+    def __init__(self):
+        p = _vp()
+        check(lib().pkx_stream_create(C.byref(p)))
+        self.handle = p.value
+
+    def sync(self):
+        check(lib().pkx_stream_synchronize(self.handle))
+
+    def __del__(self):
+        try:
+            if self.handle:
+                lib().pkx_stream_destroy(self.handle)
+        except Exception:
+            pass
+
+
+class Event:
+    def __init__(self):
+        p = _vp()
+        check(lib().pkx_event_create(C.byref(p)))
+        self.handle = p.value
+
+    def record(self, stream):
+        check(lib().pkx_event_record(self.handle, stream.handle if stream else None))
+
+    def elapsed_ms(self, stop) -> float:
+        ms = C.c_float(0)
+        check(lib().pkx_event_elapsed_ms(C.byref(ms), self.handle, stop.handle))
+        return ms.value
+
+    def __del__(self):
+        try:
+            if self.handle:
+                lib().pkx_event_destroy(self.handle)
+        except Exception:
+            pass
+
+
+def dequantize(gtype, raw_dev: DeviceArray, n, out: DeviceArray, stream=None):
+    check(lib().pkx_dequantize(gtype, raw_dev.ptr, out.ptr, n, _sh(stream)))
+
+
+def linear(precision, gtype, N, K, w_raw: np.ndarray, x: DeviceArray, M, y: DeviceArray,
+           bias: DeviceArray = None, stream=None):
+    w_raw = np.ascontiguousarray(w_raw)
+    check(lib().pkx_linear(precision, gtype, N, K, w_raw.ctypes.data, w_raw.nbytes,
+                           bias.ptr if bias is not None else None, x.ptr, M, y.ptr, _sh(stream)))
+
+
+def layernorm(x: DeviceArray, g: DeviceArray, b: DeviceArray, y: DeviceArray, M, D, eps=1e-5,
+              stream=None):
+    check(lib().pkx_layernorm(x.ptr, g.ptr, b.ptr, y.ptr, M, D, eps, _sh(stream)))
+
+
+def rel_pos_encoding(T, D, out: DeviceArray, stream=None):
+    check(lib().pkx_rel_pos_encoding(T, D, out.ptr, _sh(stream)))
+
+
+def subsampled_len(T):
+    return lib().pkx_subsampled_len(T)
+
+
+class Model:
+    """A device-resident encoder (pkx_model handle)."""
+
+    def __init__(self, handle):
+        self.handle = handle
+        cfg = Config()
+        prec, hc, hj = C.c_int(), C.c_int(), C.c_int()
+        check(lib().pkx_model_info(handle, C.byref(cfg), C.byref(prec), C.byref(hc), C.byref(hj)))
+        self.cfg = cfg
+        self.precision = prec.value
+        self.has_ctc = bool(hc.value)
+        self.has_joint = bool(hj.value)
+
+    @classmethod
+    def from_tensors(cls, model, precision=PREC_AUTO):
+        """Upload a pk_model.Model (verbatim names, GGUF byte layout)."""
+        c = model.cfg
+        cfg = Config(c.d_model, c.n_layers, c.n_heads, c.ff_dim, c.conv_kernel, c.n_mels,
+                     c.sub_channels, int(c.xscaling), c.vocab_size, len(c.tdt_durations))
+        h = _vp()
+        check(lib().pkx_model_create(C.byref(cfg), precision, C.byref(h)))
+        try:
+            for name, t in model.tensors.items():
+                ne = (C.c_int64 * len(t.ne))(*t.ne)
+                data = np.ascontiguousarray(t.data)
+                check(lib().pkx_model_set_tensor(h, name.encode(), t.gtype, len(t.ne), ne,
+                                                 data.ctypes.data, data.nbytes))
+            check(lib().pkx_model_finalize(h))
+        except Exception:
+            lib().pkx_model_free(h)
+            raise
+        return cls(h.value)
+
+    @classmethod
+    def load_gguf(cls, path, precision=PREC_AUTO):
+        h = _vp()
+        check(lib().pkx_model_load_gguf(str(path).encode(), precision, C.byref(h)))
+        return cls(h.value)
+
+    def close(self):
+        if self.handle:
+            lib().pkx_model_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # -- hot path ---------------------------------------------------------------
+    def encoder_forward(self, mel: DeviceArray, valid_T, out: DeviceArray, mask_mode=MASK_BATCHED,
+                        capture: DeviceArray = None, stream=None):
+        B, F, T = mel.shape
+        vt = None if valid_T is None else np.ascontiguousarray(valid_T, dtype=np.int32)
+        tout = C.c_int(0)
+        vo = np.zeros(B, dtype=np.int32)
+        check(lib().pkx_encoder_forward(self.handle, mel.ptr, B, T, _iptr(vt), mask_mode, out.ptr,
+                                        C.byref(tout), _iptr(vo),
+                                        capture.ptr if capture is not None else None, _sh(stream)))
+        return tout.value, vo
+
+    def subsampling_forward(self, mel: DeviceArray, valid_T, out: DeviceArray,
+                            mask_mode=MASK_BATCHED, stream=None):
+        B, F, T = mel.shape
+        vt = None if valid_T is None else np.ascontiguousarray(valid_T, dtype=np.int32)
+        tout = C.c_int(0)
+        vo = np.zeros(B, dtype=np.int32)
+        check(lib().pkx_subsampling_forward(self.handle, mel.ptr, B, T, _iptr(vt), mask_mode, out.ptr,
+                                            C.byref(tout), _iptr(vo), _sh(stream)))
+        return tout.value, vo
+
+    def conformer_layer(self, layer, x: DeviceArray, valid, out: DeviceArray,
+                        conv_out: DeviceArray = None, stream=None):
+        B, T, D = x.shape
+        v = None if valid is None else np.ascontiguousarray(valid, dtype=np.int32)
+        check(lib().pkx_conformer_layer_forward(self.handle, layer, x.ptr, B, T, _iptr(v), out.ptr,
+                                                conv_out.ptr if conv_out is not None else None,
+                                                _sh(stream)))
+
+    def relpos_attention(self, layer, x: DeviceArray, valid, out: DeviceArray, stream=None):
+        B, T, D = x.shape
+        v = None if valid is None else np.ascontiguousarray(valid, dtype=np.int32)
+        check(lib().pkx_relpos_attention_forward(self.handle, layer, x.ptr, B, T, _iptr(v), out.ptr,
+                                                 _sh(stream)))
+
+    def conv_module(self, layer, c: DeviceArray, valid, out: DeviceArray, stream=None):
+        B, T, D = c.shape
+        v = None if valid is None else np.ascontiguousarray(valid, dtype=np.int32)
+        check(lib().pkx_conv_module_forward(self.handle, layer, c.ptr, B, T, _iptr(v), out.ptr,
+                                            _sh(stream)))
+
+    def ctc(self, enc: DeviceArray, M, logprobs: DeviceArray, argmax: DeviceArray, stream=None):
+        check(lib().pkx_ctc_forward(self.handle, enc.ptr, M, logprobs.ptr, argmax.ptr, _sh(stream)))
+
+    def tdt_joint(self, enc: DeviceArray, M, g: DeviceArray, logits: DeviceArray, tok: DeviceArray,
+                  dur: DeviceArray, stream=None):
+        check(lib().pkx_tdt_joint_argmax(self.handle, enc.ptr, M, g.ptr, logits.ptr, tok.ptr, dur.ptr,
+                                         _sh(stream)))
+
+    def set_profiling(self, on: bool):
+        check(lib().pkx_model_set_profiling(self.handle, 1 if on else 0))
+
+    def profile(self):
+        ms = (C.c_double * len(PROF_FAMILIES))()
+        n = (C.c_int64 * len(PROF_FAMILIES))()
+        check(lib().pkx_model_profile_read(self.handle, ms, n))
+        return {f: (ms[i], n[i]) for i, f in enumerate(PROF_FAMILIES)}

@@ -1,0 +1,135 @@
+"""Encoder-level parity through the C ABI vs the CPU oracle: subsampling
+(batched and scalar masking), the full encoder per layer, and the CTC / TDT
+argmax heads (token ids identical)."""
+import numpy as np
+import pytest
+
+import oracle
+import pk_model as pm
+from conftest import rel_l2
+
+pytestmark = pytest.mark.gpu
+
+CASES = {
+    "f32": (dict(d_model=128, n_heads=4, ff_dim=256, n_mels=32), "f32", 0),
+    "f32_80mel_xscale": (dict(d_model=128, n_heads=4, ff_dim=256, n_mels=80, xscaling=True), "f32", 0),
+    "q8_0": (dict(d_model=256, n_heads=2, ff_dim=512, n_mels=128), "q8_0", 1),
+    "q4_k": (dict(d_model=256, n_heads=4, ff_dim=512, n_mels=128), "q4_k", 1),
+    "f16": (dict(d_model=128, n_heads=2, ff_dim=256, n_mels=64), "f16", 1),
+}
+_CACHE = {}
+
+
+def _models(gpu, name, n_layers=3):
+    if name not in _CACHE:
+        kw, wt, prec = CASES[name]
+        base = dict(n_layers=n_layers, conv_kernel=9, sub_channels=32, vocab_size=127,
+                    joint_hidden=64, pred_hidden=64)
+        base.update(kw)
+        m = pm.synthesize(pm.Config(**base), wt, bn_random=True)
+        _CACHE[name] = (m, oracle.OracleModel(m), gpu.Model.from_tensors(m, prec), prec)
+    return _CACHE[name]
+
+
+def _tol(prec):
+    return 1e-4 if prec == 0 else 1e-2
+
+
+def _mel(B, F, T, valid_T, seed):
+    rng = np.random.default_rng(seed)
+    mel = rng.normal(0, 1, (B, F, T)).astype(np.float32)
+    for b, v in enumerate(valid_T):
+        mel[b, :, v:] = 0.0          # MelBatch zero-pads to T_max (src/model.cpp:119-144)
+    return mel
+
+
+@pytest.mark.parametrize("name", list(CASES))
+@pytest.mark.parametrize("mask_mode", [0, 1])
+@pytest.mark.parametrize("T,valid_T", [(1000, [1000]), (333, [333, 200, 17]), (9, [9, 2])])
+def test_subsampling(gpu, stream, name, mask_mode, T, valid_T):
+    m, om, gm, prec = _models(gpu, name)
+    B, F = len(valid_T), m.cfg.n_mels
+    mel = _mel(B, F, T, valid_T, T)
+    vin = np.array(valid_T) - 1
+    print(f"[sub] {name} mask={mask_mode} T={T} valid={valid_T}", flush=True)
+    ref, vo_ref = om.subsampling(mel, vin, stage_masks=(mask_mode == 0))
+    Tp = oracle.subsampled_len(T)
+    dm = gpu.DeviceArray.from_numpy(mel, stream)
+    dy = gpu.DeviceArray((B, Tp, m.cfg.d_model), np.float32)
+    tp, vo = gm.subsampling_forward(dm, valid_T, dy, mask_mode, stream)
+    got = dy.numpy(stream)
+    assert tp == Tp and list(vo) == list(vo_ref)
+    mask = np.arange(Tp)[None, :] < vo[:, None]
+    assert rel_l2(got[mask], ref[mask]) < _tol(prec)
+
+
+@pytest.mark.parametrize("name", list(CASES))
+@pytest.mark.parametrize("T,valid_T", [(400, [400]), (320, [320, 201])])
+def test_encoder_per_layer(gpu, stream, name, T, valid_T):
+    m, om, gm, prec = _models(gpu, name)
+    B, F, D, L = len(valid_T), m.cfg.n_mels, m.cfg.d_model, m.cfg.n_layers
+    mel = _mel(B, F, T, valid_T, 5 * T)
+    print(f"[enc] {name} T={T} valid={valid_T}", flush=True)
+    ref, vo_ref, cap_ref = om.encoder(mel, np.array(valid_T) - 1, capture=True)
+    Tp = oracle.subsampled_len(T)
+    dm = gpu.DeviceArray.from_numpy(mel, stream)
+    dy = gpu.DeviceArray((B, Tp, D), np.float32)
+    dcap = gpu.DeviceArray((L, B, Tp, D), np.float32)
+    tp, vo = gm.encoder_forward(dm, valid_T, dy, capture=dcap, stream=stream)
+    got, cap = dy.numpy(stream), dcap.numpy(stream)
+    assert tp == Tp and list(vo) == list(vo_ref)
+    mask = np.arange(Tp)[None, :] < vo[:, None]
+    for l in range(L):
+        err = rel_l2(cap[l][mask], cap_ref[l][mask])
+        print(f"  layer {l}: rel_l2 {err:.3e}")
+        assert err < _tol(prec), (l, err)
+    assert rel_l2(got[mask], ref[mask]) < _tol(prec)
+
+
+def _margin_ok(logits, idx):
+    """True where the top-1 beats the runner-up by more than 1e-3 (ties flagged)."""
+    s = np.sort(logits, axis=-1)
+    return (s[..., -1] - s[..., -2]) > 1e-3
+
+
+@pytest.mark.parametrize("name", ["f32", "q8_0"])
+def test_ctc_head(gpu, stream, name):
+    m, om, gm, prec = _models(gpu, name)
+    T, D = 150, m.cfg.d_model
+    rng = np.random.default_rng(3)
+    enc = rng.normal(0, 1, (T, D)).astype(np.float32)
+    lp_ref, am_ref = om.ctc(enc)
+    de = gpu.DeviceArray.from_numpy(enc, stream)
+    V = m.cfg.vocab_size + 1
+    dlp = gpu.DeviceArray((T, V), np.float32)
+    dam = gpu.DeviceArray((T,), np.int32)
+    gm.ctc(de, T, dlp, dam, stream)
+    lp, am = dlp.numpy(stream), dam.numpy(stream)
+    assert np.abs(lp - lp_ref).max() < 1e-4
+    ok = _margin_ok(lp_ref, am_ref)
+    assert np.array_equal(am[ok], am_ref[ok])
+    assert ok.mean() > 0.9
+    assert np.array_equal(oracle.ctc_greedy(am, m.cfg.vocab_size), oracle.ctc_greedy(am_ref, m.cfg.vocab_size)) \
+        or not ok.all()
+
+
+@pytest.mark.parametrize("name", ["f32", "q8_0", "q4_k"])
+def test_tdt_joint_argmax(gpu, stream, name):
+    m, om, gm, prec = _models(gpu, name)
+    T, D = 120, m.cfg.d_model
+    rng = np.random.default_rng(4)
+    enc = rng.normal(0, 1, (T, D)).astype(np.float32)
+    g = rng.normal(0, 1, m.cfg.pred_hidden).astype(np.float32)
+    lg_ref, tok_ref, dur_ref = om.tdt_joint(enc, g)
+    de, dg = gpu.DeviceArray.from_numpy(enc, stream), gpu.DeviceArray.from_numpy(g, stream)
+    V = lg_ref.shape[1]
+    dl = gpu.DeviceArray((T, V), np.float32)
+    dt, dd = gpu.DeviceArray((T,), np.int32), gpu.DeviceArray((T,), np.int32)
+    gm.tdt_joint(de, T, dg, dl, dt, dd, stream)
+    lg, tok, dur = dl.numpy(stream), dt.numpy(stream), dd.numpy(stream)
+    assert rel_l2(lg, lg_ref) < 1e-5
+    n_tok = V - len(m.cfg.tdt_durations)
+    ok_t = _margin_ok(lg_ref[:, :n_tok], tok_ref)
+    ok_d = _margin_ok(lg_ref[:, n_tok:], dur_ref)
+    assert np.array_equal(tok[ok_t], tok_ref[ok_t])
+    assert np.array_equal(dur[ok_d], dur_ref[ok_d])

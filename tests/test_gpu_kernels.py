@@ -1,0 +1,94 @@
+"""Kernel-level parity: HIP path (through the C ABI) vs the CPU oracle.
+
+Bars: dequantisation bit-exact; f32 path within 1e-5 relative L2 of the
+oracle's f32 arithmetic; f16 path (f16 operands, f32 accumulation) within
+2e-3 relative L2 for a single GEMM.
+"""
+import numpy as np
+import pytest
+
+import oracle
+import pk_model as pm
+from conftest import rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def _rng(seed=7):
+    return np.random.default_rng(seed)
+
+
+@pytest.mark.parametrize("gtype,n", [(pm.GGML_Q8_0, 32 * 1000), (pm.GGML_Q4_K, 256 * 300),
+                                     (pm.GGML_F16, 4096)])
+def test_dequantize_bit_exact(gpu, stream, gtype, n):
+    rng = _rng()
+    if gtype == pm.GGML_Q8_0:
+        raw = pm.synth_q8_0(rng, n)
+    elif gtype == pm.GGML_Q4_K:
+        raw = pm.synth_q4_k(rng, n)
+    else:
+        raw = rng.normal(0, 1, n).astype(np.float16).view(np.uint16)
+    print(f"[dequant] type={gtype} n={n}", flush=True)
+    ref = oracle.dequantize(gtype, raw, n)
+    d_raw = gpu.DeviceArray.from_numpy(raw.view(np.uint8), stream)
+    out = gpu.DeviceArray((n,), np.float32)
+    gpu.dequantize(gtype, d_raw, n, out, stream)
+    got = out.numpy(stream)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def _weights(gtype, N, K, rng):
+    if gtype == pm.GGML_F32:
+        w = rng.normal(0, 0.05, (N, K)).astype(np.float32)
+        return w, w
+    if gtype == pm.GGML_F16:
+        h = rng.normal(0, 0.05, (N, K)).astype(np.float16)
+        return h.view(np.uint16), h.astype(np.float32)
+    raw = pm.synth_q8_0(rng, N * K) if gtype == pm.GGML_Q8_0 else pm.synth_q4_k(rng, N * K)
+    return raw, oracle.dequantize(gtype, raw, N * K).reshape(N, K)
+
+
+@pytest.mark.parametrize("prec", [0, 1])
+@pytest.mark.parametrize("gtype", [pm.GGML_F32, pm.GGML_F16, pm.GGML_Q8_0, pm.GGML_Q4_K])
+@pytest.mark.parametrize("M,N,K", [(77, 96, 256), (300, 200, 512), (1, 64, 256), (130, 1030, 768)])
+def test_linear(gpu, stream, prec, gtype, M, N, K):
+    rng = _rng(M + N + K)
+    raw, wf = _weights(gtype, N, K, rng)
+    x = rng.normal(0, 1, (M, K)).astype(np.float32)
+    b = rng.normal(0, 0.1, N).astype(np.float32)
+    print(f"[linear] prec={prec} type={gtype} M={M} N={N} K={K}", flush=True)
+    ref = oracle.linear(x, wf, b)
+    dx = gpu.DeviceArray.from_numpy(x, stream)
+    db = gpu.DeviceArray.from_numpy(b, stream)
+    dy = gpu.DeviceArray((M, N), np.float32)
+    gpu.linear(prec, gtype, N, K, raw, dx, M, dy, db, stream)
+    got = dy.numpy(stream)
+    err = rel_l2(got, ref)
+    tol = 1e-5 if prec == 0 else 2e-3
+    assert err < tol, err
+
+
+@pytest.mark.parametrize("M,D", [(1, 64), (257, 512), (2000, 1024), (33, 640)])
+def test_layernorm(gpu, stream, M, D):
+    rng = _rng(M * D)
+    x = (rng.normal(0, 2, (M, D)) + rng.normal(0, 3, (M, 1))).astype(np.float32)
+    g = (1 + rng.normal(0, 0.1, D)).astype(np.float32)
+    b = rng.normal(0, 0.1, D).astype(np.float32)
+    ref = oracle.layer_norm(x, g, b)
+    dx, dg, db = (gpu.DeviceArray.from_numpy(a, stream) for a in (x, g, b))
+    dy = gpu.DeviceArray((M, D), np.float32)
+    gpu.layernorm(dx, dg, db, dy, M, D, 1e-5, stream)
+    got = dy.numpy(stream)
+    assert rel_l2(got, ref) < 1e-6
+    assert np.abs(got - ref).max() < 1e-5
+
+
+@pytest.mark.parametrize("T,D", [(1, 64), (125, 1024), (375, 512), (26, 512)])
+def test_rel_pos_encoding(gpu, stream, T, D):
+    ref = oracle.rel_pos_encoding(T, D)
+    out = gpu.DeviceArray((2 * T - 1, D), np.float32)
+    gpu.rel_pos_encoding(T, D, out, stream)
+    got = out.numpy(stream)
+    # f64 sin/cos then one rounding to f32: equal up to at most 1 f32 ulp
+    ulp = np.abs(got.view(np.int32).astype(np.int64) - ref.view(np.int32).astype(np.int64))
+    assert ulp.max() <= 1

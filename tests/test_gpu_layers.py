@@ -1,0 +1,135 @@
+"""Layer-level parity through the C ABI vs the CPU oracle.
+
+Bars (relative L2 over valid frames): F32 path 1e-4; F16 path (f16, q8_0 and
+q4_K weights) 1e-2.  Ragged batches exercise the key/query masks and the
+depthwise-conv pad mask; the reference's own batch invariants (batched ==
+per-item, padding invariance; tests/test_relpos_attention_batch.cpp:98-146,
+tests/test_conformer_batch.cpp:103-152) are checked on the GPU path too.
+"""
+import numpy as np
+import pytest
+
+import oracle
+import pk_model as pm
+from conftest import rel_l2
+
+pytestmark = pytest.mark.gpu
+
+CASES = {
+    # name: (config kwargs, weight type, precision)
+    "f32_dk32": (dict(d_model=128, n_heads=4, ff_dim=256), "f32", 0),
+    "q8_dk64": (dict(d_model=256, n_heads=4, ff_dim=512), "q8_0", 1),
+    "q4k_dk128": (dict(d_model=256, n_heads=2, ff_dim=512), "q4_k", 1),
+    "f16_dk64": (dict(d_model=128, n_heads=2, ff_dim=256, attn_bias=False, conv_bias=False), "f16", 1),
+}
+
+
+def _cfg(kw, n_layers=2):
+    base = dict(n_layers=n_layers, conv_kernel=9, n_mels=32, sub_channels=32, vocab_size=63,
+                joint_hidden=64, pred_hidden=64)
+    base.update(kw)
+    return pm.Config(**base)
+
+
+_CACHE = {}
+
+
+def _models(gpu, name):
+    if name not in _CACHE:
+        kw, wt, prec = CASES[name]
+        m = pm.synthesize(_cfg(kw), wt, bn_random=True)
+        _CACHE[name] = (m, oracle.OracleModel(m), gpu.Model.from_tensors(m, prec), prec)
+    return _CACHE[name]
+
+
+def _tol(prec):
+    return 1e-4 if prec == 0 else 1e-2
+
+
+def _valid_mask(B, T, valid):
+    return np.arange(T)[None, :] < np.asarray(valid)[:, None]
+
+
+@pytest.mark.parametrize("name", list(CASES))
+@pytest.mark.parametrize("B,T,valid", [(1, 1, [1]), (2, 37, [37, 20]), (3, 70, [70, 64, 1]),
+                                       (2, 130, [130, 99])])
+def test_relpos_attention(gpu, stream, name, B, T, valid):
+    m, om, gm, prec = _models(gpu, name)
+    D = m.cfg.d_model
+    rng = np.random.default_rng(B * 1000 + T)
+    x = rng.normal(0, 1, (B, T, D)).astype(np.float32)
+    print(f"[attn] {name} B={B} T={T} valid={valid}", flush=True)
+    ref = om.relpos_attention(0, x, oracle.rel_pos_encoding(T, D), valid)
+    dx = gpu.DeviceArray.from_numpy(x, stream)
+    dy = gpu.DeviceArray((B, T, D), np.float32)
+    gm.relpos_attention(0, dx, valid, dy, stream)
+    got = dy.numpy(stream)
+    mask = _valid_mask(B, T, valid)
+    assert rel_l2(got[mask], ref[mask]) < _tol(prec)
+    # padded query rows reduce to linear_out.bias (relpos_attention.cpp:291-305)
+    assert rel_l2(got[~mask], ref[~mask]) < _tol(prec) if (~mask).any() else True
+
+
+@pytest.mark.parametrize("name", list(CASES))
+@pytest.mark.parametrize("B,T,valid", [(1, 5, [5]), (2, 37, [37, 20]), (3, 129, [129, 100, 3])])
+def test_conv_module(gpu, stream, name, B, T, valid):
+    m, om, gm, prec = _models(gpu, name)
+    D = m.cfg.d_model
+    rng = np.random.default_rng(B * 7 + T)
+    c = rng.normal(0, 1, (B, T, D)).astype(np.float32)
+    print(f"[conv] {name} B={B} T={T} valid={valid}", flush=True)
+    ref = om.conv_module(0, c, valid)
+    dc = gpu.DeviceArray.from_numpy(c, stream)
+    dy = gpu.DeviceArray((B, T, D), np.float32)
+    gm.conv_module(0, dc, valid, dy, stream)
+    got = dy.numpy(stream)
+    mask = _valid_mask(B, T, valid)
+    assert rel_l2(got[mask], ref[mask]) < _tol(prec)
+
+
+@pytest.mark.parametrize("name", list(CASES))
+@pytest.mark.parametrize("B,T,valid", [(1, 26, [26]), (2, 63, [63, 40])])
+def test_conformer_layer(gpu, stream, name, B, T, valid):
+    m, om, gm, prec = _models(gpu, name)
+    D = m.cfg.d_model
+    rng = np.random.default_rng(B + 3 * T)
+    x = rng.normal(0, 1, (B, T, D)).astype(np.float32)
+    print(f"[layer] {name} B={B} T={T} valid={valid}", flush=True)
+    ref, ref_conv = om.conformer_layer(1, x, oracle.rel_pos_encoding(T, D), valid, want_conv=True)
+    dx = gpu.DeviceArray.from_numpy(x, stream)
+    dy = gpu.DeviceArray((B, T, D), np.float32)
+    dconv = gpu.DeviceArray((B, T, D), np.float32)
+    gm.conformer_layer(1, dx, valid, dy, dconv, stream)
+    got, got_conv = dy.numpy(stream), dconv.numpy(stream)
+    mask = _valid_mask(B, T, valid)
+    assert rel_l2(got[mask], ref[mask]) < _tol(prec)
+    assert rel_l2(got_conv[mask], ref_conv[mask]) < _tol(prec)
+    # sublayer delta, not only the residual-dominated output
+    delta_ref = ref[mask] - x[mask]
+    delta_got = got[mask] - x[mask]
+    assert rel_l2(delta_got, delta_ref) < 3 * _tol(prec)
+
+
+@pytest.mark.parametrize("name", ["f32_dk32", "q8_dk64"])
+def test_batched_equals_per_item(gpu, stream, name):
+    """tests/test_conformer_batch.cpp:103-152 on the GPU path: a full item is
+    unchanged by a shorter neighbour; the short item's valid rows equal its
+    standalone run."""
+    m, om, gm, prec = _models(gpu, name)
+    D, T = m.cfg.d_model, 48
+    rng = np.random.default_rng(11)
+    x = rng.normal(0, 1, (2, T, D)).astype(np.float32)
+    x[1] = x[0]
+    valid = [T, T // 2]
+    dx = gpu.DeviceArray.from_numpy(x, stream)
+    dy = gpu.DeviceArray((2, T, D), np.float32)
+    gm.conformer_layer(0, dx, valid, dy, None, stream)
+    both = dy.numpy(stream)
+    d1 = gpu.DeviceArray.from_numpy(x[:1].copy(), stream)
+    y1 = gpu.DeviceArray((1, T, D), np.float32)
+    gm.conformer_layer(0, d1, [T], y1, None, stream)
+    full = y1.numpy(stream)[0]
+    gm.conformer_layer(0, d1, [T // 2], y1, None, stream)
+    short = y1.numpy(stream)[0]
+    assert rel_l2(both[0], full) < 1e-3
+    assert rel_l2(both[1, :T // 2], short[:T // 2]) < 1e-3
