@@ -1,0 +1,181 @@
+#!/usr/bin/env python3
+"""Encoder throughput on one MI355X: the 0.6B FastConformer encoder with q8_0
+linears, batch 16 x 10 s of synthetic 128-bin log-mel (1000 frames -> T'=125).
+
+One step = one encoder forward (subsampling + 24 conformer blocks) over the
+batch, inputs already resident in HBM.  Prints ONE JSON line with encoder RTFx
+(audio seconds per wall second), the dominant kernel's roofline position
+(measured with HIP events on the launch stream), and the CPU baseline (the
+oracle restatement timed on this host's cores on a bounded sample).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [os.path.join(ROOT, "parakeet.cpp_amd", "python"), os.path.join(ROOT, "oracle")]
+
+import pk_model as pm  # noqa: E402
+import pkx  # noqa: E402
+
+PEAK_F16_TFLOPS = 2500.0   # MI355X dense f16/bf16 MFMA
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+
+# 0.6B shape (parakeet-tdt-0.6b-v2: no linear/conv biases)
+CFG = dict(d_model=1024, n_layers=24, n_heads=8, ff_dim=4096, conv_kernel=9, n_mels=128,
+           sub_channels=256, xscaling=False, vocab_size=1024, attn_bias=False, ff_bias=False,
+           conv_bias=False)
+B, T_MEL, HOP_S = 16, 1000, 0.01
+
+
+def family_work(cfg, B, Tp):
+    """Algorithmic FLOPs (GEMM/attention) or HBM bytes (memory-bound) per launch."""
+    D, FF, H = cfg.d_model, cfg.ff_dim, cfg.n_heads
+    dk, M, P = D // H, B * Tp, 2 * Tp - 1
+    return {
+        "gemm_ffn": ("TFLOP/s", 2.0 * M * D * FF),
+        "gemm_qkv": ("TFLOP/s", 2.0 * M * D * 3 * D),
+        "gemm_pos": ("TFLOP/s", 2.0 * P * D * D),
+        "gemm_out": ("TFLOP/s", 2.0 * M * D * D),
+        "gemm_pw1_glu": ("TFLOP/s", 2.0 * M * D * 2 * D),
+        "gemm_pw2": ("TFLOP/s", 2.0 * M * D * D),
+        "attention": ("TFLOP/s", 6.0 * B * H * Tp * Tp * dk),
+        # f16 write of the normalised rows + f32 read of the residual stream (single LN);
+        # the fused norm_out/next-LN pass also writes the f32 stream back.
+        "layernorm": ("GB/s", None),
+        "dwconv": ("GB/s", 2.0 * M * D * 2 + D * (cfg.conv_kernel + 3) * 4),
+    }
+
+
+def layernorm_bytes(cfg, B, Tp):
+    D, L, M = cfg.d_model, cfg.n_layers, B * Tp
+    single = M * D * (4 + 2)
+    fused = M * D * (4 + 4 + 2)
+    last = M * D * (4 + 4)
+    # per layer: norm_self_att, norm_conv, norm_feed_forward2 (+ layer 0's norm_feed_forward1);
+    # norm_out fused with the next layer's norm_feed_forward1, the last one f32-only
+    total = (3 * L + 1) * single + (L - 1) * fused + last
+    launches = 4 * L + 1
+    return total / launches
+
+
+def cpu_baseline(model, mel_item, budget_s=12.0):
+    import oracle
+    om = oracle.OracleModel(model)
+    threads = oracle.get_threads()
+    om.encoder(mel_item[:, :, :200])                         # warm-up (page in weights)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        om.encoder(mel_item)
+        n += 1
+        el = time.perf_counter() - t0
+        if el > budget_s or n >= 8:
+            break
+    audio = n * mel_item.shape[2] * HOP_S
+    return {"value": round(audio / el, 3), "unit": "RTFx (audio s / wall s)", "cores": threads,
+            "kind": "port",
+            "sample": f"{n} x 1 clip of {mel_item.shape[2]} frames (10 s), same 0.6B q8_0 weights "
+                      f"dequantised to f32, C restatement of the reference encoder (ggml absent), "
+                      f"{el:.1f} s wall, OpenMP {threads} threads"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this encoder build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(utterance-level data parallelism across GPUs is described, not built).", file=sys.stderr)
+        sys.exit(2)
+
+    cfg = pm.Config(**CFG)
+    t0 = time.perf_counter()
+    model = pm.synthesize(cfg, "q8_0", heads=False)
+    gm = pkx.Model.from_tensors(model, pkx.PREC_AUTO)
+    assert gm.precision == pkx.PREC_F16
+    setup_s = time.perf_counter() - t0
+
+    rng = np.random.default_rng(42)
+    mel = rng.standard_normal((B, cfg.n_mels, T_MEL)).astype(np.float32)
+    stream = pkx.Stream()
+    d_mel = pkx.DeviceArray.from_numpy(mel, stream)
+    Tp = pkx.subsampled_len(T_MEL)
+    d_out = pkx.DeviceArray((B, Tp, cfg.d_model), np.float32)
+    valid = np.full(B, T_MEL, dtype=np.int32)
+
+    for _ in range(args.warmup):
+        gm.encoder_forward(d_mel, valid, d_out, stream=stream)
+    stream.sync()
+    e0, e1 = pkx.Event(), pkx.Event()
+    e0.record(stream)
+    for _ in range(args.steps):
+        gm.encoder_forward(d_mel, valid, d_out, stream=stream)
+    e1.record(stream)
+    ms_total = e0.elapsed_ms(e1)
+    stream.sync()
+    ms_step = ms_total / args.steps
+    out = d_out.numpy(stream)
+    assert np.isfinite(out).all(), "non-finite encoder output"
+
+    # Per-family kernel timing (events around each launch; serialising, separate pass).
+    gm.set_profiling(True)
+    for _ in range(2):
+        gm.encoder_forward(d_mel, valid, d_out, stream=stream)
+    prof = gm.profile()
+    gm.set_profiling(False)
+    work = family_work(cfg, B, Tp)
+    kernels = {}
+    for fam, (ms, n) in prof.items():
+        if n == 0:
+            continue
+        avg_s = ms / 1e3 / n
+        rec = {"launches": int(n), "avg_us": round(avg_s * 1e6, 2)}
+        if fam in work:
+            unit, per = work[fam]
+            if fam == "layernorm":
+                per = layernorm_bytes(cfg, B, Tp)
+            if unit == "TFLOP/s":
+                rec.update(achieved=round(per / avg_s / 1e12, 2), unit=unit,
+                           frac=round(per / avg_s / 1e12 / PEAK_F16_TFLOPS, 4))
+            else:
+                rec.update(achieved=round(per / avg_s / 1e9, 1), unit=unit,
+                           frac=round(per / avg_s / 1e9 / PEAK_HBM_GBS, 4))
+        kernels[fam] = rec
+    ffn = kernels["gemm_ffn"]
+    roofline = {"bound": "mfma", "kernel": "gemm_ffn (f16 MFMA, q8_0 in-register dequant)",
+                "achieved": ffn["achieved"], "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
+                "frac": ffn["frac"], "traffic": None,
+                "per_launch": "2*M*D*FF = %.3f GFLOP (M=B*T'=%d, D=%d, FF=%d)" % (
+                    work["gemm_ffn"][1] / 1e9, B * Tp, cfg.d_model, cfg.ff_dim)}
+
+    audio_s = B * T_MEL * HOP_S
+    rtfx = audio_s / (ms_step / 1e3)
+    line = {
+        "metric": "encoder RTFx + HBM GB/s / MFMA util, 0.6B conformer q8_0 bs16 on 1 MI355X",
+        "value": round(rtfx, 1), "unit": "RTFx (audio s / wall s)",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
+        "data": "synthetic (seeded N(0,1) log-mel; random-init q8_0 weights)",
+        "config": {"workload": "FastConformer encoder 0.6B shape: 24 blocks, d_model 1024, 8 heads x 128, "
+                               "ff 4096, conv kernel 9, dw-striding x8 (256 ch); q8_0 linears; "
+                               "128-mel, batch 16 x 1000 frames (10 s) -> T'=125",
+                   "global_batch": B, "seq_len": T_MEL, "parallelism": "none (1 GPU)"},
+        "frames_per_s": round(B * Tp / (ms_step / 1e3), 1),
+        "roofline": roofline,
+        "kernels": kernels,
+        "setup_s": round(setup_s, 1),
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(model, mel[:1].copy())
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()
