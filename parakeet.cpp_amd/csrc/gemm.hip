@@ -56,29 +56,33 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, float4v (&acc)[TM]
                                          int nw, int lane) {
     const int lr = 4 * (lane >> 4), lc = lane & 15;
     if constexpr (EPI == EPI_GLU) {
-        // Weight rows were interleaved in 16-row groups (a0..15, b0..15, a16..31, ...),
-        // so subtile 2jj holds GLU inputs a and subtile 2jj+1 the matching gates b.
+        // pointwise_conv1 rows are interleaved in 32-row groups (a0..31, b0..31, ...):
+        // in each 64-column group, subtiles 0-1 hold GLU inputs a, subtiles 2-3 the gates b.
+        static_assert(TN % 4 == 0, "GLU needs 64-column wave tiles");
         const int half_n = p.N / 2;
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int jj = 0; jj < TN / 2; ++jj)
+            for (int jj = 0; jj < TN / 4; ++jj)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int m = mw + 16 * i + lr + r;
-                    const int na = nw + 32 * jj + lc;
-                    const int og = nw / 2 + 16 * jj + lc;
-                    if (m < p.M && og < half_n) {
-                        const float a = acc[i][2 * jj][r] + (p.bias ? p.bias[na] : 0.f);
-                        const float g = acc[i][2 * jj + 1][r] + (p.bias ? p.bias[na + 16] : 0.f);
-                        float o = a * sigmoid_dev(g);
-                        if (p.valid) {
-                            const int b = m / p.T, t = m - b * p.T;
-                            if (t >= p.valid[b]) o = 0.f;
+                for (int jh = 0; jh < 2; ++jh)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int ja = 4 * jj + jh;
+                        const int m = mw + 16 * i + lr + r;
+                        const int na = nw + 16 * ja + lc;
+                        const int og = nw / 2 + 32 * jj + 16 * jh + lc;
+                        if (m < p.M && og < half_n) {
+                            const float a = acc[i][ja][r] + (p.bias ? p.bias[na] : 0.f);
+                            const float g = acc[i][ja + 2][r] + (p.bias ? p.bias[na + 32] : 0.f);
+                            float o = a * sigmoid_dev(g);
+                            if (p.valid) {
+                                const int b = m / p.T, t = m - b * p.T;
+                                if (t >= p.valid[b]) o = 0.f;
+                            }
+                            ((ActT*)p.Y)[(int64_t)m * p.ldy + og] = to_act<ActT>(o);
                         }
-                        ((ActT*)p.Y)[(int64_t)m * p.ldy + og] = to_act<ActT>(o);
                     }
-                }
     } else {
 #pragma unroll
         for (int i = 0; i < TM; ++i)
@@ -95,30 +99,41 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, float4v (&acc)[TM]
 
 // ===========================================================================
 // f16 path: A f16, weights -> f16, v_mfma_f32_16x16x32_f16, BK = 64
+//
+// All global reads are raw buffer loads: rows past M / N and columns past K
+// (offsets pushed beyond the buffer's num_records) return zero in hardware, so
+// the loop has no branches.  Raw loads stay in registers two K slabs ahead of
+// the MFMAs; they are dequantised only when written to LDS.
 // ===========================================================================
 constexpr int BK16 = 64;
-constexpr int LDK16 = BK16 + 8;  // +16 B row pad: 8 consecutive rows cover all banks
+constexpr int LDK16 = BK16 + 8;   // +16 B row pad: 8 consecutive rows cover all banks
+constexpr uint32_t OOB = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+    const int n = bytes > 0x7fffffff ? 0x7fffffff : (int)bytes;
+    return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, n, 0x00020000);
+}
+__device__ __forceinline__ int4v bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+}
 
 template <int BM> struct ALoad16 {
     static constexpr int NC = (BM * 8 + 255) / 256;  // 16-byte chunks per thread
-    half8v r[NC];
-    __device__ void load(const GemmParams& p, int m0, int k0, int tid) {
-        const f16* A = (const f16*)p.A;
+    int4v r[NC];
+    __device__ void load(__amdgpu_buffer_rsrc_t rs, const GemmParams& p, int m0, int k0, int tid) {
 #pragma unroll
         for (int i = 0; i < NC; ++i) {
             const int c = tid + 256 * i;
-            const int row = c >> 3, col = (c & 7) * 8;
-            const int m = m0 + row, k = k0 + col;
-            half8v v = {};
-            if (c < BM * 8 && m < p.M && k < p.K) v = *(const half8v*)(A + (int64_t)m * p.lda + k);
-            r[i] = v;
+            const int m = m0 + (c >> 3), k = k0 + (c & 7) * 8;
+            const uint32_t off = (k < p.K && m < p.M) ? (uint32_t)(((int64_t)m * p.lda + k) * 2) : OOB;
+            r[i] = bload16(rs, off);
         }
     }
     __device__ void store(f16* As, int tid) const {
 #pragma unroll
         for (int i = 0; i < NC; ++i) {
             const int c = tid + 256 * i;
-            if (c < BM * 8) *(half8v*)(As + (c >> 3) * LDK16 + (c & 7) * 8) = r[i];
+            if (c < BM * 8) *(int4v*)(As + (c >> 3) * LDK16 + (c & 7) * 8) = r[i];
         }
     }
 };
@@ -127,49 +142,53 @@ template <int WT, int BN> struct BLoad16;
 
 template <int BN> struct BLoad16<GT_F16, BN> {
     static constexpr int NC = (BN * 8 + 255) / 256;
-    half8v r[NC];
-    __device__ void load(const GemmParams& p, int n0, int k0, int tid) {
-        const f16* W = (const f16*)p.Wq;
+    int4v r[NC];
+    __device__ void load(__amdgpu_buffer_rsrc_t rq, __amdgpu_buffer_rsrc_t, const GemmParams& p, int n0,
+                         int k0, int tid) {
 #pragma unroll
         for (int i = 0; i < NC; ++i) {
             const int c = tid + 256 * i;
-            const int row = c >> 3, col = (c & 7) * 8;
-            const int n = n0 + row, k = k0 + col;
-            half8v v = {};
-            if (c < BN * 8 && n < p.N && k < p.K) v = *(const half8v*)(W + (int64_t)n * p.K + k);
-            r[i] = v;
+            const int n = n0 + (c >> 3), k = k0 + (c & 7) * 8;
+            const uint32_t off = (k < p.K && n < p.N) ? (uint32_t)(((int64_t)n * p.K + k) * 2) : OOB;
+            r[i] = bload16(rq, off);
         }
     }
     __device__ void store(f16* Bs, int tid) const {
 #pragma unroll
         for (int i = 0; i < NC; ++i) {
             const int c = tid + 256 * i;
-            if (c < BN * 8) *(half8v*)(Bs + (c >> 3) * LDK16 + (c & 7) * 8) = r[i];
+            if (c < BN * 8) *(int4v*)(Bs + (c >> 3) * LDK16 + (c & 7) * 8) = r[i];
         }
     }
 };
+
+// Exact int8 -> f16 for 4 packed bytes: byte b (two's complement) becomes the
+// f16 with bit pattern 0x6400 | (b ^ 0x80) = 1024 + (b + 128); subtracting
+// 1152 leaves b exactly.  Then one correctly rounded f16 multiply by d.
+__device__ __forceinline__ void i8x4_to_f16(uint32_t w, half2v d2, half2v& lo, half2v& hi) {
+    const uint32_t u = w ^ 0x80808080u;
+    const uint32_t a = __builtin_amdgcn_perm(0x64646464u, u, 0x07010700u) ;  // [0x64,b1,0x64,b0]
+    const uint32_t b = __builtin_amdgcn_perm(0x64646464u, u, 0x07030702u);   // [0x64,b3,0x64,b2]
+    const half2v bias = {(f16)1152.0f, (f16)1152.0f};
+    lo = (__builtin_bit_cast(half2v, a) - bias) * d2;
+    hi = (__builtin_bit_cast(half2v, b) - bias) * d2;
+}
 
 // q8_0 device layout: int8 q[N][K] and f16 d[N][K/32]; w = d*q.
 template <int BN> struct BLoad16<GT_Q8_0, BN> {
     static constexpr int NC = (BN * 4 + 255) / 256;
     int4v q[NC];
-    f16 d[NC];
-    __device__ void load(const GemmParams& p, int n0, int k0, int tid) {
-        const int8_t* W = (const int8_t*)p.Wq;
-        const f16* S = (const f16*)p.Ws;
+    uint32_t d[NC];
+    __device__ void load(__amdgpu_buffer_rsrc_t rq, __amdgpu_buffer_rsrc_t rs, const GemmParams& p, int n0,
+                         int k0, int tid) {
 #pragma unroll
         for (int i = 0; i < NC; ++i) {
             const int c = tid + 256 * i;
-            const int row = c >> 2, col = (c & 3) * 16;
-            const int n = n0 + row, k = k0 + col;
-            int4v v = {};
-            f16 s = (f16)0.f;
-            if (c < BN * 4 && n < p.N && k < p.K) {
-                v = *(const int4v*)(W + (int64_t)n * p.K + k);
-                s = S[(int64_t)n * (p.K / 32) + k / 32];
-            }
-            q[i] = v;
-            d[i] = s;
+            const int n = n0 + (c >> 2), k = k0 + (c & 3) * 16;
+            const bool in = k < p.K && n < p.N;
+            q[i] = bload16(rq, in ? (uint32_t)((int64_t)n * p.K + k) : OOB);
+            d[i] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(
+                rs, (int)(in ? (uint32_t)(((int64_t)n * (p.K / 32) + k / 32) * 2) : OOB), 0, 0);
         }
     }
     __device__ void store(f16* Bs, int tid) const {
@@ -178,14 +197,19 @@ template <int BN> struct BLoad16<GT_Q8_0, BN> {
             const int c = tid + 256 * i;
             if (c >= BN * 4) continue;
             f16* dst = Bs + (c >> 2) * LDK16 + (c & 3) * 16;
-            half8v lo, hi;
+            const f16 dh = __builtin_bit_cast(f16, (uint16_t)d[i]);
+            const half2v d2 = {dh, dh};
+            half2v h[8];
 #pragma unroll
-            for (int b = 0; b < 8; ++b) {
-                lo[b] = (f16)(float)(int8_t)(q[i][b >> 2] >> ((b & 3) * 8)) * d[i];
-                hi[b] = (f16)(float)(int8_t)(q[i][2 + (b >> 2)] >> ((b & 3) * 8)) * d[i];
+            for (int w = 0; w < 4; ++w) i8x4_to_f16((uint32_t)q[i][w], d2, h[2 * w], h[2 * w + 1]);
+            int4v lo, hi;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                lo[w] = __builtin_bit_cast(int, h[w]);
+                hi[w] = __builtin_bit_cast(int, h[4 + w]);
             }
-            *(half8v*)dst = lo;
-            *(half8v*)(dst + 8) = hi;
+            *(int4v*)dst = lo;
+            *(int4v*)(dst + 8) = hi;
         }
     }
 };
@@ -196,25 +220,16 @@ template <int BN> struct BLoad16<GT_Q8_0, BN> {
 template <int BN> struct BLoad16<GT_Q4_K, BN> {
     static constexpr int NC = (BN * 2 + 255) / 256;
     int4v q[NC];
-    float2v s0[NC], s1[NC];
-    __device__ void load(const GemmParams& p, int n0, int k0, int tid) {
-        const uint8_t* W = (const uint8_t*)p.Wq;
-        const float2v* S = (const float2v*)p.Ws;
+    float4v s[NC];   // {sc0, min0, sc1, min1}
+    __device__ void load(__amdgpu_buffer_rsrc_t rq, __amdgpu_buffer_rsrc_t rs, const GemmParams& p, int n0,
+                         int k0, int tid) {
 #pragma unroll
         for (int i = 0; i < NC; ++i) {
             const int c = tid + 256 * i;
-            const int row = c >> 1, h = c & 1;
-            const int n = n0 + row;
-            int4v v = {};
-            float2v a = {0.f, 0.f}, b = {0.f, 0.f};
-            if (c < BN * 2 && n < p.N && k0 < p.K) {
-                v = *(const int4v*)(W + (int64_t)n * (p.K / 2) + k0 / 2 + 16 * h);
-                a = S[(int64_t)n * (p.K / 32) + k0 / 32];
-                b = S[(int64_t)n * (p.K / 32) + k0 / 32 + 1];
-            }
-            q[i] = v;
-            s0[i] = a;
-            s1[i] = b;
+            const int n = n0 + (c >> 1), h = c & 1;
+            const bool in = k0 < p.K && n < p.N;
+            q[i] = bload16(rq, in ? (uint32_t)((int64_t)n * (p.K / 2) + k0 / 2 + 16 * h) : OOB);
+            s[i] = __builtin_bit_cast(float4v, bload16(rs, in ? (uint32_t)(((int64_t)n * (p.K / 32) + k0 / 32) * 8) : OOB));
         }
     }
     __device__ void store(f16* Bs, int tid) const {
@@ -229,10 +244,10 @@ template <int BN> struct BLoad16<GT_Q4_K, BN> {
             for (int b = 0; b < 8; ++b) {
                 const uint32_t w0 = (uint32_t)q[i][b >> 2] >> ((b & 3) * 8);
                 const uint32_t w1 = (uint32_t)q[i][2 + (b >> 2)] >> ((b & 3) * 8);
-                l0[b] = (f16)(s0[i].x * (float)(w0 & 0xF) - s0[i].y);
-                l1[b] = (f16)(s0[i].x * (float)(w1 & 0xF) - s0[i].y);
-                h0[b] = (f16)(s1[i].x * (float)((w0 >> 4) & 0xF) - s1[i].y);
-                h1[b] = (f16)(s1[i].x * (float)((w1 >> 4) & 0xF) - s1[i].y);
+                l0[b] = (f16)(s[i][0] * (float)(w0 & 0xF) - s[i][1]);
+                l1[b] = (f16)(s[i][0] * (float)(w1 & 0xF) - s[i][1]);
+                h0[b] = (f16)(s[i][2] * (float)((w0 >> 4) & 0xF) - s[i][3]);
+                h1[b] = (f16)(s[i][2] * (float)((w1 >> 4) & 0xF) - s[i][3]);
             }
             *(half8v*)dst = l0;
             *(half8v*)(dst + 8) = l1;
@@ -242,7 +257,27 @@ template <int BN> struct BLoad16<GT_Q4_K, BN> {
     }
 };
 
-template <int TM, int TN, int WT, int EPI>
+template <int TM, int TN>
+__device__ __forceinline__ void mma_slab(const f16* as, const f16* bs, float4v (&acc)[TM][TN], int arow,
+                                         int brow, int kq) {
+#pragma unroll
+    for (int ks = 0; ks < BK16; ks += 32) {
+        half8v af[TM], bf[TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) af[i] = *(const half8v*)(as + (arow + 16 * i) * LDK16 + ks + kq);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) bf[j] = *(const half8v*)(bs + (brow + 16 * j) * LDK16 + ks + kq);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+}
+
+// PF = register stages in flight (1: the next slab is fetched while the
+// current one is consumed; 2: two slabs ahead, for tiles with spare VGPRs).
+template <int TM, int TN, int WT, int EPI, int PF>
 __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(GemmParams p) {
     constexpr int BM = 32 * TM, BN = 32 * TN;
     __shared__ __attribute__((aligned(16))) f16 As[2][BM * LDK16];
@@ -255,51 +290,414 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(GemmParams p) {
     const int bm = tile % nbm, bn = tile / nbm;
     const int m0 = bm * BM, n0 = bn * BN;
 
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, ((int64_t)(p.M - 1) * p.lda + p.K) * 2);
+    int64_t wq_bytes = (int64_t)p.N * p.K * 2, ws_bytes = 0;
+    if constexpr (WT == GT_Q8_0) { wq_bytes = (int64_t)p.N * p.K; ws_bytes = (int64_t)p.N * (p.K / 32) * 2; }
+    if constexpr (WT == GT_Q4_K) { wq_bytes = (int64_t)p.N * p.K / 2; ws_bytes = (int64_t)p.N * (p.K / 32) * 8; }
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(p.Wq, wq_bytes);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(WT == GT_F16 ? p.Wq : p.Ws, WT == GT_F16 ? wq_bytes : ws_bytes);
+
     float4v acc[TM][TN];
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = (float4v){0.f, 0.f, 0.f, 0.f};
 
-    ALoad16<BM> al;
-    BLoad16<WT, BN> bl;
-    const int nk = cdiv_dev(p.K, BK16);
-    al.load(p, m0, 0, tid);
-    bl.load(p, n0, 0, tid);
-    al.store(As[0], tid);
-    bl.store(Bs[0], tid);
-    __syncthreads();
-
     const int arow = wm * TM * 16 + (lane & 15), brow = wn * TN * 16 + (lane & 15);
     const int kq = (lane >> 4) * 8;
-    for (int kt = 0; kt < nk; ++kt) {
-        const int cur = kt & 1;
-        if (kt + 1 < nk) {
-            al.load(p, m0, (kt + 1) * BK16, tid);
-            bl.load(p, n0, (kt + 1) * BK16, tid);
+    const int nk = cdiv_dev(p.K, BK16);
+
+    if constexpr (PF == 1) {
+        ALoad16<BM> al;
+        BLoad16<WT, BN> bl;
+        al.load(ra, p, m0, 0, tid);
+        bl.load(rq, rs, p, n0, 0, tid);
+        al.store(As[0], tid);
+        bl.store(Bs[0], tid);
+        __syncthreads();
+        for (int kt = 0; kt < nk; ++kt) {
+            const int cur = kt & 1;
+            if (kt + 1 < nk) {
+                al.load(ra, p, m0, (kt + 1) * BK16, tid);
+                bl.load(rq, rs, p, n0, (kt + 1) * BK16, tid);
+            }
+            mma_slab<TM, TN>(As[cur], Bs[cur], acc, arow, brow, kq);
+            if (kt + 1 < nk) {
+                al.store(As[cur ^ 1], tid);
+                bl.store(Bs[cur ^ 1], tid);
+            }
+            __syncthreads();
         }
-        const f16* as = As[cur];
-        const f16* bs = Bs[cur];
-#pragma unroll
-        for (int ks = 0; ks < BK16; ks += 32) {
-            half8v af[TM], bf[TN];
-#pragma unroll
-            for (int i = 0; i < TM; ++i) af[i] = *(const half8v*)(as + (arow + 16 * i) * LDK16 + ks + kq);
-#pragma unroll
-            for (int j = 0; j < TN; ++j) bf[j] = *(const half8v*)(bs + (brow + 16 * j) * LDK16 + ks + kq);
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-#pragma unroll
-                for (int j = 0; j < TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    } else {
+        // two register stages in flight: slab s lives in stage s & 1
+        ALoad16<BM> a0, a1;
+        BLoad16<WT, BN> b0, b1;
+        a0.load(ra, p, m0, 0, tid);
+        b0.load(rq, rs, p, n0, 0, tid);
+        if (nk > 1) {
+            a1.load(ra, p, m0, BK16, tid);
+            b1.load(rq, rs, p, n0, BK16, tid);
         }
-        if (kt + 1 < nk) {
-            al.store(As[cur ^ 1], tid);
-            bl.store(Bs[cur ^ 1], tid);
+        a0.store(As[0], tid);
+        b0.store(Bs[0], tid);
+        if (nk > 2) {
+            a0.load(ra, p, m0, 2 * BK16, tid);
+            b0.load(rq, rs, p, n0, 2 * BK16, tid);
         }
         __syncthreads();
+        for (int kt = 0; kt < nk; kt += 2) {
+            // phase 0: MFMAs on slab kt (LDS 0); slab kt+1 (stage 1) -> LDS 1; fetch slab kt+3
+            mma_slab<TM, TN>(As[0], Bs[0], acc, arow, brow, kq);
+            if (kt + 1 < nk) {
+                a1.store(As[1], tid);
+                b1.store(Bs[1], tid);
+                if (kt + 3 < nk) {
+                    a1.load(ra, p, m0, (kt + 3) * BK16, tid);
+                    b1.load(rq, rs, p, n0, (kt + 3) * BK16, tid);
+                }
+            }
+            __syncthreads();
+            if (kt + 1 >= nk) break;
+            // phase 1: MFMAs on slab kt+1 (LDS 1); slab kt+2 (stage 0) -> LDS 0; fetch slab kt+4
+            mma_slab<TM, TN>(As[1], Bs[1], acc, arow, brow, kq);
+            if (kt + 2 < nk) {
+                a0.store(As[0], tid);
+                b0.store(Bs[0], tid);
+                if (kt + 4 < nk) {
+                    a0.load(ra, p, m0, (kt + 4) * BK16, tid);
+                    b0.load(rq, rs, p, n0, (kt + 4) * BK16, tid);
+                }
+            }
+            __syncthreads();
+        }
     }
     epilogue<EPI, f16, TM, TN>(p, acc, m0 + wm * TM * 16, n0 + wn * TN * 16, lane);
+}
+
+// ===========================================================================
+// f16 path, LDS-DMA + 32x32x16 MFMA (K % 64 == 0; f16 or q8_0 weights).
+//
+// v_mfma_f32_32x32x16_f16 sustains twice the f16 rate of the 16x16x32 form on
+// gfx950, so the main tile family uses it: 4 waves in a 2x2 grid, each wave a
+// (32*TM) x (32*TN) tile of 32x32 MFMA blocks.
+//
+// global_load_lds_dwordx4 moves 16 B per lane straight into LDS (lane L lands
+// at base + 16 L), so a 3-stage LDS ring is kept full with no staging
+// registers: slab kt+2 is in flight while slab kt is multiplied.  Tiles are
+// stored with XOR-swizzled 16 B chunks (the swizzle is applied through each
+// lane's source address) so 8 consecutive fragment rows hit distinct banks.
+// q8_0 weights stay int8 in LDS next to their f16 scales and are dequantised
+// after the LDS read.
+//
+// K permutation (identical for A and B, so the contraction is unchanged): in
+// substep s (0..3) of a 64-wide slab, lane half q = lane/32 holds
+// k = 32q + 8s + [0..7].  A lane's 32 k-values are then one contiguous q8_0
+// block: one scale per lane per slab and 32 contiguous weight bytes.
+// ===========================================================================
+constexpr int DMA_NS = 3;
+
+__device__ __forceinline__ void dma16(const void* src, void* lds_wave_base) {
+    __builtin_amdgcn_global_load_lds(src, (void __attribute__((address_space(3)))*)lds_wave_base, 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const void* src, void* lds_wave_base) {
+    __builtin_amdgcn_global_load_lds(src, (void __attribute__((address_space(3)))*)lds_wave_base, 4, 0, 0);
+}
+// s_waitcnt with only the vector-memory counter bounded (gfx9 encoding).
+template <int N> __device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+template <int TM, int TN, int WT>
+struct DmaCfg {
+    static constexpr int BM = 64 * TM, BN = 64 * TN;      // 2x2 waves of (32 TM) x (32 TN)
+    static constexpr int A_BYTES = BM * 128;
+    static constexpr int B_BYTES = WT == GT_Q8_0 ? BN * 64 : BN * 128;
+    static constexpr int S_BYTES = WT == GT_Q8_0 ? BN * 4 : 0;
+    static constexpr int STAGE = A_BYTES + B_BYTES + S_BYTES;
+    static constexpr int A_INSTR = A_BYTES / 1024 / 4;                 // per wave
+    static constexpr int B_INSTR = B_BYTES / 1024 / 4;
+    static constexpr int S_INSTR = WT == GT_Q8_0 ? (BN + 63) / 64 : 0; // every wave loads all scales
+    static constexpr int PER_SLAB = A_INSTR + B_INSTR + S_INSTR;
+    static_assert(A_BYTES % 4096 == 0 && B_BYTES % 4096 == 0, "tile must split into 1 KB per wave");
+};
+
+template <int TM, int TN, int WT>
+__device__ __forceinline__ void dma_slab(const GemmParams& p, uint8_t* st, int m0, int n0, int k0, int wid,
+                                         int lane) {
+    typedef DmaCfg<TM, TN, WT> C;
+    const f16* A = (const f16*)p.A;
+#pragma unroll
+    for (int i = 0; i < C::A_INSTR; ++i) {
+        const int blk = wid * C::A_INSTR + i;                 // 1 KB block = 8 rows of 128 B
+        const int slot = blk * 64 + lane;
+        const int row = slot >> 3, c = (slot & 7) ^ (row & 7);
+        const int m = min(m0 + row, p.M - 1);
+        dma16(A + (int64_t)m * p.lda + k0 + 8 * c, st + blk * 1024);
+    }
+    uint8_t* bs = st + C::A_BYTES;
+    if constexpr (WT == GT_Q8_0) {
+        const int8_t* W = (const int8_t*)p.Wq;
+#pragma unroll
+        for (int i = 0; i < C::B_INSTR; ++i) {
+            const int blk = wid * C::B_INSTR + i;             // 16 rows of 64 B
+            const int slot = blk * 64 + lane;
+            const int row = slot >> 2, c = (slot & 3) ^ ((row >> 1) & 3);
+            const int n = min(n0 + row, p.N - 1);
+            dma16(W + (int64_t)n * p.K + k0 + 16 * c, bs + blk * 1024);
+        }
+        const f16* S = (const f16*)p.Ws;
+        uint8_t* ss = bs + C::B_BYTES;
+#pragma unroll
+        for (int i = 0; i < C::S_INSTR; ++i) {
+            const int row = i * 64 + lane;                    // 4 B = the slab's 2 scales of a row
+            const int n = min(n0 + row, p.N - 1);
+            dma4(S + (int64_t)n * (p.K / 32) + k0 / 32, ss + i * 256);
+        }
+    } else {
+        const f16* W = (const f16*)p.Wq;
+#pragma unroll
+        for (int i = 0; i < C::B_INSTR; ++i) {
+            const int blk = wid * C::B_INSTR + i;
+            const int slot = blk * 64 + lane;
+            const int row = slot >> 3, c = (slot & 7) ^ (row & 7);
+            const int n = min(n0 + row, p.N - 1);
+            dma16(W + (int64_t)n * p.K + k0 + 8 * c, bs + blk * 1024);
+        }
+    }
+}
+
+template <int TM, int TN, int WT>
+__device__ __forceinline__ void mma32_slab(const uint8_t* st, float16v (&acc)[TM][TN], int wm, int wn,
+                                           int lane) {
+    typedef DmaCfg<TM, TN, WT> C;
+    const int q = lane >> 5, r32 = lane & 31;
+    const uint8_t* bs = st + C::A_BYTES;
+    // B fragments for the 4 substeps: bf[j][s]
+    half8v bf[TN][4];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const int row = wn * TN * 32 + 32 * j + r32;
+        if constexpr (WT == GT_Q8_0) {
+            const int sw = (row >> 1) & 3;
+            const int4v raw0 = *(const int4v*)(bs + row * 64 + (((2 * q) ^ sw) << 4));
+            const int4v raw1 = *(const int4v*)(bs + row * 64 + (((2 * q + 1) ^ sw) << 4));
+            const f16 dh = *(const f16*)(bs + C::B_BYTES + row * 4 + q * 2);
+            const half2v d2 = {dh, dh};
+#pragma unroll
+            for (int s2 = 0; s2 < 4; ++s2) {
+                const uint32_t w0 = (uint32_t)(s2 < 2 ? raw0[2 * s2] : raw1[2 * (s2 - 2)]);
+                const uint32_t w1 = (uint32_t)(s2 < 2 ? raw0[2 * s2 + 1] : raw1[2 * (s2 - 2) + 1]);
+                half2v h0, h1, h2, h3;
+                i8x4_to_f16(w0, d2, h0, h1);
+                i8x4_to_f16(w1, d2, h2, h3);
+                bf[j][s2] = (half8v){h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
+            }
+        } else {
+            const uint8_t* rp = bs + row * 128;
+#pragma unroll
+            for (int s2 = 0; s2 < 4; ++s2) bf[j][s2] = *(const half8v*)(rp + (((4 * q + s2) ^ (row & 7)) << 4));
+        }
+    }
+#pragma unroll
+    for (int s2 = 0; s2 < 4; ++s2) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            const int row = wm * TM * 32 + 32 * i + r32;
+            const half8v af = *(const half8v*)(st + row * 128 + (((4 * q + s2) ^ (row & 7)) << 4));
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[j][s2], acc[i][j], 0, 0, 0);
+        }
+    }
+}
+
+// Epilogue for the 32x32 accumulator layout: register r of a lane holds
+// row 8*(r/4) + 4*(lane/32) + r%4, column lane%32 of its 32x32 block.
+template <int EPI, typename ActT, int TM, int TN>
+__device__ __forceinline__ void epilogue32(const GemmParams& p, float16v (&acc)[TM][TN], int mw, int nw,
+                                           int lane) {
+    const int lr = 4 * (lane >> 5), lc = lane & 31;
+    if constexpr (EPI == EPI_GLU) {
+        // pointwise_conv1 rows are interleaved in 32-row groups (a0..31, b0..31, ...):
+        // block 2jj holds the GLU inputs a, block 2jj+1 the matching gates b.
+        static_assert(TN % 2 == 0, "GLU needs an even number of 32-column blocks");
+        const int half_n = p.N / 2;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int jj = 0; jj < TN / 2; ++jj)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int m = mw + 32 * i + 8 * (r >> 2) + lr + (r & 3);
+                    const int na = nw + 64 * jj + lc;
+                    const int og = nw / 2 + 32 * jj + lc;
+                    if (m < p.M && og < half_n) {
+                        const float a = acc[i][2 * jj][r] + (p.bias ? p.bias[na] : 0.f);
+                        const float g = acc[i][2 * jj + 1][r] + (p.bias ? p.bias[na + 32] : 0.f);
+                        float o = a * sigmoid_dev(g);
+                        if (p.valid) {
+                            const int b = m / p.T, t = m - b * p.T;
+                            if (t >= p.valid[b]) o = 0.f;
+                        }
+                        ((ActT*)p.Y)[(int64_t)m * p.ldy + og] = to_act<ActT>(o);
+                    }
+                }
+    } else {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int m = mw + 32 * i + 8 * (r >> 2) + lr + (r & 3);
+                    const int n = nw + 32 * j + lc;
+                    if (m < p.M && n < p.N) epi_one<EPI, ActT>(p, m, n, acc[i][j][r]);
+                }
+    }
+}
+
+// Coalesced epilogue: each wave stages its finished tile (after the elementwise
+// epilogue math) in its own LDS region, then writes rows out with 16-byte
+// stores; the residual update reads and writes the f32 stream in 16-byte
+// vectors too.  The accumulator layout alone would give 2- or 4-byte stores
+// scattered over 8 rows per instruction.
+template <int EPI, int TM, int TN>
+__device__ __forceinline__ void epilogue32_lds(const GemmParams& p, float16v (&acc)[TM][TN], float* wsm,
+                                               int mw, int nw, int lane) {
+    constexpr int WR = 32 * TM;
+    constexpr int WC = EPI == EPI_GLU ? 16 * TN : 32 * TN;   // output columns of this wave
+    constexpr int LDW = WC + 4;
+    const int lr = 4 * (lane >> 5), lc = lane & 31;
+    // 1) elementwise math in registers, staged as f32
+    if constexpr (EPI == EPI_GLU) {
+        static_assert(TN % 2 == 0, "GLU needs an even number of 32-column blocks");
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int jj = 0; jj < TN / 2; ++jj) {
+                const int na = nw + 64 * jj + lc;
+                const float ba = p.bias ? p.bias[min(na, p.N - 1)] : 0.f;
+                const float bg = p.bias ? p.bias[min(na + 32, p.N - 1)] : 0.f;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int rr = 32 * i + 8 * (r >> 2) + lr + (r & 3);
+                    const int m = mw + rr;
+                    float o = (acc[i][2 * jj][r] + ba) * sigmoid_dev(acc[i][2 * jj + 1][r] + bg);
+                    if (p.valid && m < p.M) {
+                        const int b = m / p.T, t = m - b * p.T;
+                        if (t >= p.valid[b]) o = 0.f;
+                    }
+                    wsm[rr * LDW + 32 * jj + lc] = o;
+                }
+            }
+    } else {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int n = nw + 32 * j + lc;
+                const float bb = p.bias ? p.bias[min(n, p.N - 1)] : 0.f;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int rr = 32 * i + 8 * (r >> 2) + lr + (r & 3);
+                    float v = acc[i][j][r] + bb;
+                    if constexpr (EPI == EPI_SILU) v = silu_dev(v);
+                    else if constexpr (EPI == EPI_RELU) v = v > 0.f ? v : 0.f;
+                    else v = v * p.alpha;    // STORE, STORE_F32, RESID
+                    wsm[rr * LDW + 32 * j + lc] = v;
+                }
+            }
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's LDS writes are done
+    __builtin_amdgcn_wave_barrier();
+    // 2) coalesced copy-out
+    const int ncol = EPI == EPI_GLU ? p.N / 2 : p.N;
+    const int n0 = EPI == EPI_GLU ? nw / 2 : nw;
+    if constexpr (EPI == EPI_STORE_F32 || EPI == EPI_RESID) {
+        constexpr int CPR = WC / 4;   // float4 chunks per row
+        for (int c = lane; c < WR * CPR; c += 64) {
+            const int rr = c / CPR, cc = (c % CPR) * 4;
+            const int m = mw + rr, n = n0 + cc;
+            if (m >= p.M) continue;
+            const float4v v = *(const float4v*)(wsm + rr * LDW + cc);
+            float* dst = (float*)p.Y + (int64_t)m * p.ldy + n;
+            if (n + 3 < ncol) {
+                if constexpr (EPI == EPI_RESID) *(float4v*)dst = *(const float4v*)dst + v;
+                else *(float4v*)dst = v;
+            } else {
+                for (int e = 0; e < 4 && n + e < ncol; ++e) {
+                    if constexpr (EPI == EPI_RESID) dst[e] += v[e];
+                    else dst[e] = v[e];
+                }
+            }
+        }
+    } else {
+        constexpr int CPR = WC / 8;   // 8-half chunks per row
+        for (int c = lane; c < WR * CPR; c += 64) {
+            const int rr = c / CPR, cc = (c % CPR) * 8;
+            const int m = mw + rr, n = n0 + cc;
+            if (m >= p.M) continue;
+            const float4v v0 = *(const float4v*)(wsm + rr * LDW + cc);
+            const float4v v1 = *(const float4v*)(wsm + rr * LDW + cc + 4);
+            f16* dst = (f16*)p.Y + (int64_t)m * p.ldy + n;
+            if (n + 7 < ncol) {
+                const half8v h = {(f16)v0[0], (f16)v0[1], (f16)v0[2], (f16)v0[3],
+                                  (f16)v1[0], (f16)v1[1], (f16)v1[2], (f16)v1[3]};
+                *(half8v*)dst = h;
+            } else {
+                for (int e = 0; e < 8 && n + e < ncol; ++e) dst[e] = (f16)(e < 4 ? v0[e] : v1[e - 4]);
+            }
+        }
+    }
+}
+
+template <int TM, int TN, int WT, int EPI>
+__global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmParams p) {
+    typedef DmaCfg<TM, TN, WT> C;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[DMA_NS * C::STAGE];
+
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int wm = wid >> 1, wn = wid & 1;
+    const int nbm = cdiv_dev(p.M, C::BM), nbn = cdiv_dev(p.N, C::BN);
+    const int tile = xcd_tile(blockIdx.x, nbm * nbn);
+    const int bm = tile % nbm, bn = tile / nbm;
+    const int m0 = bm * C::BM, n0 = bn * C::BN;
+
+    float16v acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = (float16v){};
+
+    const int nk = p.K / 64;
+    dma_slab<TM, TN, WT>(p, smem, m0, n0, 0, wid, lane);
+    if (nk > 1) dma_slab<TM, TN, WT>(p, smem + C::STAGE, m0, n0, 64, wid, lane);
+    int st = 0;
+    for (int kt = 0; kt < nk; ++kt) {
+        // this wave's DMAs for slab kt have landed (slab kt+1 may still be in flight)
+        if (kt + 1 < nk) wait_vmcnt<C::PER_SLAB>();
+        else wait_vmcnt<0>();
+        // Every wave's part of slab kt is in LDS and stage (kt+2)%3 is no longer read.
+        // A bare s_barrier: the DMA counter was bounded above, and a fenced
+        // __syncthreads() would also drain the DMAs of slab kt+1.
+        __builtin_amdgcn_s_barrier();
+        if (kt + 2 < nk) {
+            const int st2 = st + 2 >= DMA_NS ? st + 2 - DMA_NS : st + 2;
+            dma_slab<TM, TN, WT>(p, smem + st2 * C::STAGE, m0, n0, (kt + 2) * 64, wid, lane);
+        }
+        mma32_slab<TM, TN, WT>(smem + st * C::STAGE, acc, wm, wn, lane);
+        st = st + 1 == DMA_NS ? 0 : st + 1;
+    }
+    if constexpr (EPI == EPI_RELU_TR || EPI == EPI_RELU2_F32) {
+        epilogue32<EPI, f16, TM, TN>(p, acc, m0 + wm * TM * 32, n0 + wn * TN * 32, lane);
+    } else {
+        // the LDS ring is free once every wave has finished its last slab
+        static_assert(4 * 32 * TM * (32 * TN + 4) * 4 <= DMA_NS * C::STAGE, "epilogue staging exceeds LDS ring");
+        __syncthreads();
+        float* wsm = (float*)smem + wid * (32 * TM) * ((EPI == EPI_GLU ? 16 * TN : 32 * TN) + 4);
+        epilogue32_lds<EPI, TM, TN>(p, acc, wsm, m0 + wm * TM * 32, n0 + wn * TN * 32, lane);
+    }
 }
 
 // ===========================================================================
@@ -542,8 +940,9 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmParams p) {
 // ===========================================================================
 template <int TM, int TN, int WT, int EPI>
 static void run_f16(const GemmParams& p, hipStream_t s) {
+    constexpr int PF = TM * TN >= 16 ? 1 : 2;
     const int tiles = cdiv(p.M, 32 * TM) * cdiv(p.N, 32 * TN);
-    hipLaunchKernelGGL((gemm_f16_kernel<TM, TN, WT, EPI>), dim3(tiles), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((gemm_f16_kernel<TM, TN, WT, EPI, PF>), dim3(tiles), dim3(256), 0, s, p);
     PKX_LAUNCH_CHECK();
 }
 template <int TM, int TN, int WT, int EPI>
@@ -566,8 +965,17 @@ static void run_f32(const GemmParams& p, hipStream_t s) {
     default: throw std::invalid_argument("gemm: bad epilogue");                 \
     }
 
+template <int TM, int TN, int WT, int EPI>
+static void run_dma(const GemmParams& p, hipStream_t s) {
+    const int tiles = cdiv(p.M, 64 * TM) * cdiv(p.N, 64 * TN);
+    hipLaunchKernelGGL((gemm_dma_kernel<TM, TN, WT, EPI>), dim3(tiles), dim3(256), 0, s, p);
+    PKX_LAUNCH_CHECK();
+}
+
 template <int TM, int TN, int WT>
 static void f16_epi(int epi, const GemmParams& p, hipStream_t s) { PKX_EPI_SWITCH(run_f16, TM, TN, WT) }
+template <int TM, int TN, int WT>
+static void dma_epi(int epi, const GemmParams& p, hipStream_t s) { PKX_EPI_SWITCH(run_dma, TM, TN, WT) }
 template <int TM, int TN, int WT>
 static void f32_epi(int epi, const GemmParams& p, hipStream_t s) { PKX_EPI_SWITCH(run_f32, TM, TN, WT) }
 
@@ -577,10 +985,14 @@ void launch_gemm(Precision prec, int wtype, int epi, const GemmParams& p, hipStr
     require(p.lda >= p.K && p.lda % 8 == 0, "gemm: lda must be >= K and a multiple of 8 (16-byte rows)");
     if (wtype == GT_Q8_0) require(p.K % 32 == 0, "gemm: q8_0 needs K % 32 == 0");
     if (wtype == GT_Q4_K) require(p.K % 256 == 0, "gemm: q4_K needs K % 256 == 0");
-    if (epi == EPI_GLU) require(p.N % 32 == 0, "gemm: GLU needs N % 32 == 0");
+    if (epi == EPI_GLU) require(p.N % 64 == 0, "gemm: GLU needs N % 64 == 0");
     // Tile choice: 128x128 when that already gives >= 256 tiles, else 64x128.
     const bool big = (int64_t)cdiv(p.M, 128) * cdiv(p.N, 128) >= 256;
-    if (prec == PREC_F16) {
+    if (prec == PREC_F16 && p.K % 64 == 0 && p.ldy % 8 == 0 && (wtype == GT_F16 || wtype == GT_Q8_0)) {
+        const bool wide = (int64_t)cdiv(p.M, 128) * cdiv(p.N, 128) >= 256;
+        if (wtype == GT_Q8_0) wide ? dma_epi<2, 2, GT_Q8_0>(epi, p, s) : dma_epi<1, 2, GT_Q8_0>(epi, p, s);
+        else wide ? dma_epi<2, 2, GT_F16>(epi, p, s) : dma_epi<1, 2, GT_F16>(epi, p, s);
+    } else if (prec == PREC_F16) {
         switch (wtype) {
         case GT_F16: big ? f16_epi<4, 4, GT_F16>(epi, p, s) : f16_epi<2, 4, GT_F16>(epi, p, s); break;
         case GT_Q8_0: big ? f16_epi<4, 4, GT_Q8_0>(epi, p, s) : f16_epi<2, 4, GT_Q8_0>(epi, p, s); break;

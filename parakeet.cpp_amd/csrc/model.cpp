@@ -294,11 +294,11 @@ DevWeight Model::make_weight_rows(const std::vector<const HostTensor*>& parts, i
     cat.ne[1] = N;
     cat.bytes.resize((size_t)rb * N);
     if (glu_interleave) {
-        require(parts.size() == 1 && N % 32 == 0, "GLU interleave needs one weight with 2D rows, D % 16 == 0");
+        require(parts.size() == 1 && N % 64 == 0, "GLU interleave needs one weight with 2D rows, D % 32 == 0");
         const int D = N / 2;
         for (int r = 0; r < N; ++r) {
-            const int g = r / 32, i = r % 32;
-            const int src = i < 16 ? 16 * g + i : D + 16 * g + (i - 16);
+            const int g = r / 64, i = r % 64;
+            const int src = i < 32 ? 32 * g + i : D + 32 * g + (i - 32);
             std::memcpy(&cat.bytes[(size_t)r * rb], &parts[0]->bytes[(size_t)src * rb], (size_t)rb);
         }
     } else {
@@ -352,7 +352,7 @@ void Model::finalize() {
     require(!finalized_, "finalize called twice");
     const ModelConfig& c = cfg_;
     const int D = c.d_model, FF = c.ff_dim, H = c.n_heads, dk = D / H, K = c.conv_kernel, C = c.sub_channels;
-    require(D % 16 == 0, "d_model must be a multiple of 16");
+    require(D % 32 == 0, "d_model must be a multiple of 32");
 
     if ((int)prec_ < 0) {
         bool any_low = false;
@@ -418,8 +418,8 @@ void Model::finalize() {
         if (const HostTensor* b1 = find(cv + "pointwise_conv1.bias")) {
             std::vector<float> v = to_f32(*b1), il(v.size());
             for (int r = 0; r < 2 * D; ++r) {
-                const int g = r / 32, j = r % 32;
-                il[(size_t)r] = v[(size_t)(j < 16 ? 16 * g + j : D + 16 * g + (j - 16))];
+                const int g = r / 64, j = r % 64;
+                il[(size_t)r] = v[(size_t)(j < 32 ? 32 * g + j : D + 32 * g + (j - 32))];
             }
             L.pw1_b = upload_f32(il);
         }
