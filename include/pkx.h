@@ -192,13 +192,21 @@ int pkx_layernorm(const float* x_dev, const float* g_dev, const float* b_dev, fl
 int pkx_rel_pos_encoding(int T, int D, float* out_dev, void* stream);
 
 /* ---- profiling ----------------------------------------------------------------
- * With profiling on, each kernel family is bracketed by events (serialising
- * the stream); pkx_model_profile_read returns milliseconds and launch counts
- * per family (arrays of PKX_PROF_FAMILIES entries, order:
+ * No counterpart in the reference (its benchmarks time whole calls).
+ * family_mask selects kernel families by bit (bit i = family i in the order
  * subsampling, layernorm, gemm_ffn, gemm_qkv, gemm_pos, attention, gemm_out,
- * gemm_pw1_glu, dwconv, gemm_pw2, pos_enc). */
+ * gemm_pw1_glu, dwconv, gemm_pw2, pos_enc); 0 turns profiling off and every
+ * call resets the totals.  Kernels of a selected family are launched with
+ * start/stop events on their own dispatch (no extra packets, no host syncs), so
+ * the times are kernel execution times.  stride >= 1 samples every stride-th
+ * launch of the selected families (counted across calls), which keeps the
+ * per-launch event cost off most launches of a timed run.  pkx_model_profile_read waits for the
+ * pending launches and returns accumulated milliseconds and kernel launch
+ * counts per family (arrays of PKX_PROF_FAMILIES entries).  Profiling state is
+ * per model and per calling thread. */
 #define PKX_PROF_FAMILIES 11
-int pkx_model_set_profiling(pkx_model* m, int on);
+#define PKX_PROF_ALL ((1u << PKX_PROF_FAMILIES) - 1u)
+int pkx_model_set_profiling(pkx_model* m, unsigned family_mask, int stride);
 int pkx_model_profile_read(pkx_model* m, double* ms, int64_t* launches);
 
 #ifdef __cplusplus

@@ -268,18 +268,18 @@ void launch_relpos_attention(Precision prec, const AttnParams& a, hipStream_t s)
     if (prec == PREC_F16) {
         const dim3 grid(cdiv(a.T, AQ), a.H, a.B);
         if (a.dk == 128) {
-            hipLaunchKernelGGL(relpos_attn_f16_kernel<128>, grid, dim3(256), 0, s, a);
+            launch(relpos_attn_f16_kernel<128>, grid, dim3(256), 0, s, a);
         } else if (a.dk == 64) {
-            hipLaunchKernelGGL(relpos_attn_f16_kernel<64>, grid, dim3(256), 0, s, a);
+            launch(relpos_attn_f16_kernel<64>, grid, dim3(256), 0, s, a);
         } else if (a.dk == 32) {
-            hipLaunchKernelGGL(relpos_attn_f16_kernel<32>, grid, dim3(256), 0, s, a);
+            launch(relpos_attn_f16_kernel<32>, grid, dim3(256), 0, s, a);
         } else {
             throw std::invalid_argument("attention(f16): head dim must be 32, 64 or 128");
         }
     } else {
         const size_t smem = sizeof(float) * (2 * (size_t)a.dk + (size_t)a.T);
         require(smem <= 64 * 1024, "attention(f32): T too large for the LDS score row");
-        hipLaunchKernelGGL(relpos_attn_f32_kernel, dim3(a.T, a.H, a.B), dim3(64), smem, s, a, a.dk);
+        launch(relpos_attn_f32_kernel, dim3(a.T, a.H, a.B), dim3(64), smem, s, a, a.dk);
     }
     PKX_LAUNCH_CHECK();
 }

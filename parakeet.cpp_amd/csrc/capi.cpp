@@ -27,6 +27,7 @@ int guarded(F&& f) {
     } catch (...) {
         g_last_error = "unknown error";
     }
+    pkx::tl_launch_hook = nullptr;   // a failed call may leave a profiled region open
     return 1;
 }
 
@@ -310,10 +311,10 @@ int pkx_rel_pos_encoding(int T, int D, float* out, void* s) {
     });
 }
 
-int pkx_model_set_profiling(pkx_model* m, int on) {
+int pkx_model_set_profiling(pkx_model* m, unsigned family_mask, int stride) {
     return guarded([&] {
         need(m, "null model");
-        m->impl->set_profiling(on != 0);
+        m->impl->set_profiling(family_mask, stride);
     });
 }
 

@@ -1,11 +1,13 @@
 // Shared device/host helpers for the gfx950 encoder kernels.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 
 #include <cstdint>
 #include <cstdio>
 #include <stdexcept>
 #include <string>
+#include <tuple>
 
 namespace pkx {
 
@@ -37,6 +39,32 @@ inline void hip_check(hipError_t e, const char* what, const char* file, int line
 }
 #define PKX_HIP(x) ::pkx::hip_check((x), #x, __FILE__, __LINE__)
 #define PKX_LAUNCH_CHECK() ::pkx::hip_check(hipGetLastError(), "kernel launch", __FILE__, __LINE__)
+
+// Per-launch timing.  When a hook is installed on the calling thread and it
+// hands out an event pair, the launch carries those events on its own dispatch
+// packet (hipExtLaunchKernel), so the elapsed time between them is the
+// kernel's execution time, with no marker packets or host syncs in between.
+struct LaunchHook {
+    virtual bool take(hipEvent_t* start, hipEvent_t* stop) = 0;
+    virtual ~LaunchHook() = default;
+};
+extern thread_local LaunchHook* tl_launch_hook;
+
+template <typename... KA, typename... A>
+inline void launch(void (*kernel)(KA...), dim3 grid, dim3 block, uint32_t shmem, hipStream_t s,
+                   A... args) {
+    static_assert(sizeof...(KA) == sizeof...(A), "kernel argument count");
+    std::tuple<KA...> packed{static_cast<KA>(args)...};
+    void* ptrs[sizeof...(KA) > 0 ? sizeof...(KA) : 1];
+    std::apply([&](auto&... x) {
+        int i = 0;
+        ((ptrs[i++] = (void*)&x), ...);
+    }, packed);
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (tl_launch_hook && !tl_launch_hook->take(&e0, &e1)) e0 = e1 = nullptr;
+    hip_check(hipExtLaunchKernel((const void*)kernel, grid, block, ptrs, shmem, s, e0, e1, 0),
+              "kernel launch", __FILE__, __LINE__);
+}
 
 inline void require(bool ok, const std::string& msg) {
     if (!ok) throw std::invalid_argument(msg);

@@ -87,11 +87,11 @@ template <int NV, typename OutT>
 static void ln_go(const LnParams& p, hipStream_t s) {
     const dim3 grid(cdiv(p.M, 4));
     if (p.y_f32 && p.y)
-        hipLaunchKernelGGL((layernorm_kernel<NV, OutT, 1>), grid, dim3(256), 0, s, p);
+        launch((layernorm_kernel<NV, OutT, 1>), grid, dim3(256), 0, s, p);
     else if (p.y_f32)
-        hipLaunchKernelGGL((layernorm_kernel<NV, OutT, 2>), grid, dim3(256), 0, s, p);
+        launch((layernorm_kernel<NV, OutT, 2>), grid, dim3(256), 0, s, p);
     else
-        hipLaunchKernelGGL((layernorm_kernel<NV, OutT, 0>), grid, dim3(256), 0, s, p);
+        launch((layernorm_kernel<NV, OutT, 0>), grid, dim3(256), 0, s, p);
 }
 
 template <typename OutT>
@@ -186,7 +186,7 @@ static void dw_go(const void* in, void* out, const float* w, const float* dwb, c
                   const float* sh, int B, int Tn, int D, hipStream_t s) {
     constexpr int TT = 16;
     const dim3 grid(cdiv(D / VEC, 256), cdiv(Tn, TT), B);
-    hipLaunchKernelGGL((dwconv_bn_silu_kernel<ET, VEC, K, TT>), grid, dim3(256), 0, s, (const ET*)in,
+    launch((dwconv_bn_silu_kernel<ET, VEC, K, TT>), grid, dim3(256), 0, s, (const ET*)in,
                        (ET*)out, w, dwb, sc, sh, Tn, D);
 }
 
@@ -296,9 +296,9 @@ void launch_sub_conv0(Precision prec, const float* mel, const int* valid0, const
     const dim3 grid(cdiv(F1, SUB_FS), T1, B);
     const int bs = C >= 256 ? 256 : ((C + 63) / 64) * 64;
     if (prec == PREC_F16)
-        hipLaunchKernelGGL(sub_conv0_kernel<f16>, grid, dim3(bs), 0, s, mel, valid0, w, bias, (f16*)out, F, T, C, F1, T1);
+        launch(sub_conv0_kernel<f16>, grid, dim3(bs), 0, s, mel, valid0, w, bias, (f16*)out, F, T, C, F1, T1);
     else
-        hipLaunchKernelGGL(sub_conv0_kernel<float>, grid, dim3(bs), 0, s, mel, valid0, w, bias, (float*)out, F, T, C, F1, T1);
+        launch(sub_conv0_kernel<float>, grid, dim3(bs), 0, s, mel, valid0, w, bias, (float*)out, F, T, C, F1, T1);
     PKX_LAUNCH_CHECK();
 }
 
@@ -308,9 +308,9 @@ void launch_sub_dwconv(Precision prec, const void* in, const int* vmask, const f
     const dim3 grid(cdiv(Fo, SUB_FS), To, B);
     const int bs = C >= 256 ? 256 : ((C + 63) / 64) * 64;
     if (prec == PREC_F16)
-        hipLaunchKernelGGL(sub_dwconv_kernel<f16>, grid, dim3(bs), 0, s, (const f16*)in, vmask, w, bias, (f16*)out, Ti, Fi, C, To, Fo);
+        launch(sub_dwconv_kernel<f16>, grid, dim3(bs), 0, s, (const f16*)in, vmask, w, bias, (f16*)out, Ti, Fi, C, To, Fo);
     else
-        hipLaunchKernelGGL(sub_dwconv_kernel<float>, grid, dim3(bs), 0, s, (const float*)in, vmask, w, bias, (float*)out, Ti, Fi, C, To, Fo);
+        launch(sub_dwconv_kernel<float>, grid, dim3(bs), 0, s, (const float*)in, vmask, w, bias, (float*)out, Ti, Fi, C, To, Fo);
     PKX_LAUNCH_CHECK();
 }
 
@@ -335,9 +335,9 @@ void launch_rel_pos_encoding(Precision prec, void* out, int T, int D, hipStream_
     require(D % 2 == 0, "pos_enc: D must be even");
     const int64_t n = (2 * (int64_t)T - 1) * (D / 2);
     if (prec == PREC_F16)
-        hipLaunchKernelGGL(rel_pos_kernel<f16>, dim3(cdiv(n, 256)), dim3(256), 0, s, (f16*)out, T, D);
+        launch(rel_pos_kernel<f16>, dim3(cdiv(n, 256)), dim3(256), 0, s, (f16*)out, T, D);
     else
-        hipLaunchKernelGGL(rel_pos_kernel<float>, dim3(cdiv(n, 256)), dim3(256), 0, s, (float*)out, T, D);
+        launch(rel_pos_kernel<float>, dim3(cdiv(n, 256)), dim3(256), 0, s, (float*)out, T, D);
     PKX_LAUNCH_CHECK();
 }
 
@@ -406,14 +406,14 @@ __global__ __launch_bounds__(256) void split_argmax_kernel(const float* x, int64
 void launch_log_softmax_argmax(const float* logits, float* logprobs, int32_t* argmax, int64_t M,
                                int V, hipStream_t s) {
     if (M == 0) return;
-    hipLaunchKernelGGL(log_softmax_argmax_kernel, dim3(cdiv(M, 4)), dim3(256), 0, s, logits, logprobs, argmax, M, V);
+    launch(log_softmax_argmax_kernel, dim3(cdiv(M, 4)), dim3(256), 0, s, logits, logprobs, argmax, M, V);
     PKX_LAUNCH_CHECK();
 }
 
 void launch_split_argmax(const float* logits, int64_t M, int n_tok, int n_dur, int32_t* tok,
                          int32_t* dur, hipStream_t s) {
     if (M == 0) return;
-    hipLaunchKernelGGL(split_argmax_kernel, dim3(cdiv(M, 4)), dim3(256), 0, s, logits, M, n_tok, n_dur, tok, dur);
+    launch(split_argmax_kernel, dim3(cdiv(M, 4)), dim3(256), 0, s, logits, M, n_tok, n_dur, tok, dur);
     PKX_LAUNCH_CHECK();
 }
 
@@ -432,14 +432,14 @@ __global__ void add_f32_kernel(float* x, const float* y, int64_t n) {
 void launch_cast_f32(Precision prec, const float* x, void* y, int64_t n, hipStream_t s) {
     if (n == 0) return;
     if (prec == PREC_F16)
-        hipLaunchKernelGGL(cast_f32_kernel<f16>, dim3(cdiv(n, 256)), dim3(256), 0, s, x, (f16*)y, n);
+        launch(cast_f32_kernel<f16>, dim3(cdiv(n, 256)), dim3(256), 0, s, x, (f16*)y, n);
     else
-        hipLaunchKernelGGL(cast_f32_kernel<float>, dim3(cdiv(n, 256)), dim3(256), 0, s, x, (float*)y, n);
+        launch(cast_f32_kernel<float>, dim3(cdiv(n, 256)), dim3(256), 0, s, x, (float*)y, n);
     PKX_LAUNCH_CHECK();
 }
 void launch_add_f32(float* x, const float* y, int64_t n, hipStream_t s) {
     if (n == 0) return;
-    hipLaunchKernelGGL(add_f32_kernel, dim3(cdiv(n, 256)), dim3(256), 0, s, x, y, n);
+    launch(add_f32_kernel, dim3(cdiv(n, 256)), dim3(256), 0, s, x, y, n);
     PKX_LAUNCH_CHECK();
 }
 
@@ -468,7 +468,7 @@ __global__ __launch_bounds__(256) void compact_cf_kernel(const float* x, int Tn,
 void launch_compact_channels_first(const float* x, int B, int T, int D, const int* valid,
                                    const int64_t* offs, float* out, hipStream_t s) {
     const dim3 grid(cdiv(T, 32), cdiv(D, 32), B);
-    hipLaunchKernelGGL(compact_cf_kernel, grid, dim3(256), 0, s, x, T, D, valid, offs, out);
+    launch(compact_cf_kernel, grid, dim3(256), 0, s, x, T, D, valid, offs, out);
     PKX_LAUNCH_CHECK();
 }
 

@@ -942,13 +942,13 @@ template <int TM, int TN, int WT, int EPI>
 static void run_f16(const GemmParams& p, hipStream_t s) {
     constexpr int PF = TM * TN >= 16 ? 1 : 2;
     const int tiles = cdiv(p.M, 32 * TM) * cdiv(p.N, 32 * TN);
-    hipLaunchKernelGGL((gemm_f16_kernel<TM, TN, WT, EPI, PF>), dim3(tiles), dim3(256), 0, s, p);
+    launch((gemm_f16_kernel<TM, TN, WT, EPI, PF>), dim3(tiles), dim3(256), 0, s, p);
     PKX_LAUNCH_CHECK();
 }
 template <int TM, int TN, int WT, int EPI>
 static void run_f32(const GemmParams& p, hipStream_t s) {
     const int tiles = cdiv(p.M, 32 * TM) * cdiv(p.N, 32 * TN);
-    hipLaunchKernelGGL((gemm_f32_kernel<TM, TN, WT, EPI>), dim3(tiles), dim3(256), 0, s, p);
+    launch((gemm_f32_kernel<TM, TN, WT, EPI>), dim3(tiles), dim3(256), 0, s, p);
     PKX_LAUNCH_CHECK();
 }
 
@@ -967,9 +967,13 @@ static void run_f32(const GemmParams& p, hipStream_t s) {
 
 template <int TM, int TN, int WT, int EPI>
 static void run_dma(const GemmParams& p, hipStream_t s) {
-    const int tiles = cdiv(p.M, 64 * TM) * cdiv(p.N, 64 * TN);
-    hipLaunchKernelGGL((gemm_dma_kernel<TM, TN, WT, EPI>), dim3(tiles), dim3(256), 0, s, p);
-    PKX_LAUNCH_CHECK();
+    if constexpr (EPI == EPI_GLU && TN % 2 != 0) {
+        throw std::logic_error("gemm: GLU epilogue dispatched to a 64-wide tile");
+    } else {
+        const int tiles = cdiv(p.M, 64 * TM) * cdiv(p.N, 64 * TN);
+        launch((gemm_dma_kernel<TM, TN, WT, EPI>), dim3(tiles), dim3(256), 0, s, p);
+        PKX_LAUNCH_CHECK();
+    }
 }
 
 template <int TM, int TN, int WT>
@@ -986,12 +990,23 @@ void launch_gemm(Precision prec, int wtype, int epi, const GemmParams& p, hipStr
     if (wtype == GT_Q8_0) require(p.K % 32 == 0, "gemm: q8_0 needs K % 32 == 0");
     if (wtype == GT_Q4_K) require(p.K % 256 == 0, "gemm: q4_K needs K % 256 == 0");
     if (epi == EPI_GLU) require(p.N % 64 == 0, "gemm: GLU needs N % 64 == 0");
-    // Tile choice: 128x128 when that already gives >= 256 tiles, else 64x128.
     const bool big = (int64_t)cdiv(p.M, 128) * cdiv(p.N, 128) >= 256;
     if (prec == PREC_F16 && p.K % 64 == 0 && p.ldy % 8 == 0 && (wtype == GT_F16 || wtype == GT_Q8_0)) {
-        const bool wide = (int64_t)cdiv(p.M, 128) * cdiv(p.N, 128) >= 256;
-        if (wtype == GT_Q8_0) wide ? dma_epi<2, 2, GT_Q8_0>(epi, p, s) : dma_epi<1, 2, GT_Q8_0>(epi, p, s);
-        else wide ? dma_epi<2, 2, GT_F16>(epi, p, s) : dma_epi<1, 2, GT_F16>(epi, p, s);
+        // Tile shapes from a sweep over the encoder's shapes on MI355X (M = B*T' = 2000):
+        // q8_0 weights prefer 128x128 when the grid holds >= 384 of them (N >= 3072),
+        // 128x64 when >= 128 of those fill the chip (N = 1024), 64x64 for the short
+        // positional projection; f16 weights run best at 64x128 throughout.  The GLU
+        // epilogue pairs 64-column groups, so it needs a tile at least 128 wide.
+        const int64_t t22 = (int64_t)cdiv(p.M, 128) * cdiv(p.N, 128);
+        const int64_t t21 = (int64_t)cdiv(p.M, 128) * cdiv(p.N, 64);
+        if (wtype == GT_Q8_0) {
+            if (t22 >= 384 || (epi == EPI_GLU && t22 >= 256)) dma_epi<2, 2, GT_Q8_0>(epi, p, s);
+            else if (epi == EPI_GLU) dma_epi<1, 2, GT_Q8_0>(epi, p, s);
+            else if (t21 >= 128) dma_epi<2, 1, GT_Q8_0>(epi, p, s);
+            else dma_epi<1, 1, GT_Q8_0>(epi, p, s);
+        } else {
+            dma_epi<1, 2, GT_F16>(epi, p, s);
+        }
     } else if (prec == PREC_F16) {
         switch (wtype) {
         case GT_F16: big ? f16_epi<4, 4, GT_F16>(epi, p, s) : f16_epi<2, 4, GT_F16>(epi, p, s); break;
@@ -1052,12 +1067,12 @@ void launch_dequantize(int wtype, const void* src, float* dst, int64_t n, hipStr
     const int bs = 256;
     if (wtype == GT_Q8_0) {
         require(n % 32 == 0, "dequantize: q8_0 needs n % 32 == 0");
-        hipLaunchKernelGGL(dequant_q8_0_kernel, dim3(cdiv(n, bs)), dim3(bs), 0, s, (const uint8_t*)src, dst, n / 32);
+        launch(dequant_q8_0_kernel, dim3(cdiv(n, bs)), dim3(bs), 0, s, (const uint8_t*)src, dst, n / 32);
     } else if (wtype == GT_Q4_K) {
         require(n % 256 == 0, "dequantize: q4_K needs n % 256 == 0");
-        hipLaunchKernelGGL(dequant_q4_k_kernel, dim3(cdiv(n, bs)), dim3(bs), 0, s, (const uint8_t*)src, dst, n / 256);
+        launch(dequant_q4_k_kernel, dim3(cdiv(n, bs)), dim3(bs), 0, s, (const uint8_t*)src, dst, n / 256);
     } else if (wtype == GT_F16) {
-        hipLaunchKernelGGL(dequant_f16_kernel, dim3(cdiv(n, bs)), dim3(bs), 0, s, (const f16*)src, dst, n);
+        launch(dequant_f16_kernel, dim3(cdiv(n, bs)), dim3(bs), 0, s, (const f16*)src, dst, n);
     } else {
         throw std::invalid_argument("dequantize: unsupported type");
     }

@@ -119,8 +119,11 @@ Model::~Model() {
         if (ws_->h_valid) (void)hipHostFree(ws_->h_valid);
         if (ws_->staged) (void)hipEventDestroy(ws_->staged);
     }
-    for (hipEvent_t e : ev_)
-        if (e) (void)hipEventDestroy(e);
+    if (tl_launch_hook && tl_launch_hook == (LaunchHook*)prof_hook_.get()) tl_launch_hook = nullptr;
+    for (auto& e : prof_ev_) {
+        (void)hipEventDestroy(e.first);
+        (void)hipEventDestroy(e.second);
+    }
 }
 
 void Model::set_tensor(const std::string& name, int gtype, int n_dims, const int64_t* ne,
@@ -505,12 +508,44 @@ void Model::finalize() {
 // ---------------------------------------------------------------------------
 // helpers
 // ---------------------------------------------------------------------------
-void Model::set_profiling(bool on) {
-    profiling_ = on;
-    if (on && !ev_[0]) {
-        PKX_HIP(hipEventCreate(&ev_[0]));
-        PKX_HIP(hipEventCreate(&ev_[1]));
+thread_local LaunchHook* tl_launch_hook = nullptr;
+
+// Hands an event pair to every launch made inside a profiled family region.
+struct Model::ProfHook final : LaunchHook {
+    Model* m = nullptr;
+    bool take(hipEvent_t* a, hipEvent_t* b) override {
+        if (m->cur_fam_ < 0) return false;
+        if (m->prof_seen_++ % m->prof_stride_ != 0) return false;
+        if (m->prof_pending_.size() == m->prof_ev_.size()) {
+            hipEvent_t e0 = nullptr, e1 = nullptr;
+            // timing-only events: no system-scope fence (no cache writeback at the
+            // kernel's end that would lengthen what is being measured)
+            if (hipEventCreateWithFlags(&e0, hipEventDisableSystemFence) != hipSuccess) return false;
+            if (hipEventCreateWithFlags(&e1, hipEventDisableSystemFence) != hipSuccess) {
+                (void)hipEventDestroy(e0);
+                return false;
+            }
+            m->prof_ev_.push_back({e0, e1});
+        }
+        const size_t i = m->prof_pending_.size();
+        m->prof_pending_.push_back(m->cur_fam_);
+        *a = m->prof_ev_[i].first;
+        *b = m->prof_ev_[i].second;
+        return true;
     }
+};
+
+void Model::set_profiling(unsigned mask, int stride) {
+    require(stride >= 1, "profiling: stride must be >= 1");
+    prof_mask_ = mask & ((1u << KF_COUNT) - 1);
+    prof_stride_ = stride;
+    prof_seen_ = 0;
+    if (!prof_hook_) {
+        prof_hook_ = std::make_unique<ProfHook>();
+        prof_hook_->m = this;
+    }
+    prof_pending_.clear();
+    cur_fam_ = -1;
     for (int i = 0; i < KF_COUNT; ++i) {
         prof_ms_[i] = 0;
         prof_n_[i] = 0;
@@ -518,23 +553,33 @@ void Model::set_profiling(bool on) {
 }
 
 void Model::profile_read(double* ms, int64_t* n) {
+    if (!prof_pending_.empty()) {
+        PKX_HIP(hipEventSynchronize(prof_ev_[prof_pending_.size() - 1].second));
+        for (size_t i = 0; i < prof_pending_.size(); ++i) {
+            float t = 0.f;
+            PKX_HIP(hipEventElapsedTime(&t, prof_ev_[i].first, prof_ev_[i].second));
+            prof_ms_[prof_pending_[i]] += t;
+            prof_n_[prof_pending_[i]] += 1;
+        }
+        prof_pending_.clear();
+    }
     for (int i = 0; i < KF_COUNT; ++i) {
         if (ms) ms[i] = prof_ms_[i];
         if (n) n[i] = prof_n_[i];
     }
 }
 
-void Model::mark(int fam, hipStream_t s, bool begin) {
-    if (!profiling_ || fam < 0) return;
+// Opens (begin) or closes a family region: while open, every kernel launched
+// on this thread is timed into that family.  Regions do not nest; fam < 0 is
+// a no-op so helpers called inside another family's region stay in it.
+void Model::mark(int fam, bool begin) {
+    if (fam < 0 || !(prof_mask_ >> fam & 1u)) return;
     if (begin) {
-        PKX_HIP(hipEventRecord(ev_[0], s));
+        cur_fam_ = fam;
+        tl_launch_hook = prof_hook_.get();
     } else {
-        PKX_HIP(hipEventRecord(ev_[1], s));
-        PKX_HIP(hipEventSynchronize(ev_[1]));
-        float ms = 0.f;
-        PKX_HIP(hipEventElapsedTime(&ms, ev_[0], ev_[1]));
-        prof_ms_[fam] += ms;
-        prof_n_[fam] += 1;
+        cur_fam_ = -1;
+        tl_launch_hook = nullptr;
     }
 }
 
@@ -557,9 +602,9 @@ void Model::gemm(const DevWeight& w, int epi, const void* A, int64_t lda, int64_
     p.M = (int)M;
     p.N = w.N;
     p.K = w.K;
-    mark(fam, s, true);
+    mark(fam, true);
     launch_gemm(prec, w.gtype, epi, p, s);
-    mark(fam, s, false);
+    mark(fam, false);
 }
 
 void Model::ensure_ws(int B, int T_max) {
@@ -604,9 +649,9 @@ void Model::stage_valid(const std::vector<int>* v[4], hipStream_t s) {
 }
 
 void Model::ensure_pe(int T, hipStream_t s) {
-    mark(KF_POS_ENC, s, true);
+    mark(KF_POS_ENC, true);
     launch_rel_pos_encoding(prec_, ws_->pe.p, T, cfg_.d_model, s);
-    mark(KF_POS_ENC, s, false);
+    mark(KF_POS_ENC, false);
 }
 
 void* Model::cast_to_act(const float* x, int64_t n, hipStream_t s) {
@@ -644,7 +689,7 @@ int Model::subsampling_forward(const float* mel, int B, int T_max, const int* va
     Ws& w = *ws_;
     const int* dv = w.d_valid;
     const int Bc = w.Bcap;
-    mark(KF_SUBSAMPLING, s, true);
+    mark(KF_SUBSAMPLING, true);
     launch_sub_conv0(prec_, mel, stage_masks ? dv : nullptr, sub_.w0, sub_.b0, w.a1.p, B, F, T_max, C, s);
     launch_sub_dwconv(prec_, w.a1.p, stage_masks ? dv + Bc : nullptr, sub_.w2, sub_.b2, w.a2.p, B, T1, F1, C, s);
     gemm(sub_.w3, EPI_RELU, w.a2.p, C, (int64_t)B * T2 * F2, sub_.b3, w.a2p.p, C, 1.f, nullptr, 1, s, prec_, -1);
@@ -654,7 +699,7 @@ int Model::subsampling_forward(const float* mel, int B, int T_max, const int* va
     const float xs = (apply_xscaling && c.xscaling) ? std::sqrt((float)c.d_model) : 1.0f;  // encoder.cpp:122-124
     gemm(sub_.out, EPI_STORE_F32, w.flat.p, (int64_t)C * F3, (int64_t)B * T3, sub_.bout, out, c.d_model, xs,
          nullptr, 1, s, prec_, -1);
-    mark(KF_SUBSAMPLING, s, false);
+    mark(KF_SUBSAMPLING, false);
     return T3;
 }
 
@@ -676,9 +721,9 @@ void Model::layer_body(int l, float* x, int B, int T, const int* d_valid, bool f
         p.y = w.h.p;
         p.M = M;
         p.D = D;
-        mark(KF_LAYERNORM, s, true);
+        mark(KF_LAYERNORM, true);
         launch_layernorm(prec_, p, s);
-        mark(KF_LAYERNORM, s, false);
+        mark(KF_LAYERNORM, false);
     };
     // Stage A: x += 0.5 * FFN1(LN(x))
     if (!first_ln_done) ln(L.ff1_ln_g, L.ff1_ln_b);
@@ -708,17 +753,17 @@ void Model::layer_body(int l, float* x, int B, int T, const int* d_valid, bool f
         a.H = H;
         a.dk = dk;
         a.scale = 1.0f / std::sqrt((float)dk);
-        mark(KF_ATTENTION, s, true);
+        mark(KF_ATTENTION, true);
         launch_relpos_attention(prec_, a, s);
-        mark(KF_ATTENTION, s, false);
+        mark(KF_ATTENTION, false);
     }
     gemm(L.wo, EPI_RESID, w.h.p, D, M, L.bo, x, D, 1.f, nullptr, 1, s, prec_, KF_GEMM_OUT);
     // Stage C: x += conv(LN(x))
     ln(L.conv_ln_g, L.conv_ln_b);
     gemm(L.pw1, EPI_GLU, w.h.p, D, M, L.pw1_b, w.g.p, D, 1.f, d_valid, T, s, prec_, KF_GEMM_PW1_GLU);
-    mark(KF_DWCONV, s, true);
+    mark(KF_DWCONV, true);
     launch_dwconv_bn_silu(prec_, w.g.p, w.h.p, L.dw_w, L.dw_b, L.bn_scale, L.bn_shift, B, T, D, c.conv_kernel, s);
-    mark(KF_DWCONV, s, false);
+    mark(KF_DWCONV, false);
     if (conv_capture_) {
         gemm(L.pw2, EPI_STORE_F32, w.h.p, D, M, L.pw2_b, conv_capture_, D, 1.f, nullptr, 1, s, prec_, KF_GEMM_PW2);
         launch_add_f32(x, conv_capture_, M * D, s);
@@ -742,9 +787,9 @@ void Model::layer_body(int l, float* x, int B, int T, const int* d_valid, bool f
         }
         p.M = M;
         p.D = D;
-        mark(KF_LAYERNORM, s, true);
+        mark(KF_LAYERNORM, true);
         launch_layernorm(prec_, p, s);
-        mark(KF_LAYERNORM, s, false);
+        mark(KF_LAYERNORM, false);
     }
 }
 

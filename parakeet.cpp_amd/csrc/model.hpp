@@ -110,7 +110,7 @@ public:
     void ctc_forward(const float* enc, int64_t M, float* logprobs, int32_t* argmax, hipStream_t s);
     void tdt_joint_argmax(const float* enc, int64_t M, const float* g, float* logits, int32_t* tok,
                           int32_t* dur, hipStream_t s);
-    void set_profiling(bool on);
+    void set_profiling(unsigned family_mask, int stride);
     void profile_read(double* ms_per_family, int64_t* launches_per_family);
 
 private:
@@ -131,7 +131,7 @@ private:
                     bool fuse_next_ln, hipStream_t s);
     void ensure_pe(int T, hipStream_t s);
     void stage_valid(const std::vector<int>* v[4], hipStream_t s);
-    void mark(int fam, hipStream_t s, bool begin);
+    void mark(int fam, bool begin);
     void* cast_to_act(const float* x, int64_t n, hipStream_t s);
 
     ModelConfig cfg_;
@@ -144,10 +144,16 @@ private:
     HeadsDev heads_;
     std::unique_ptr<Ws> ws_;
     float* conv_capture_ = nullptr;   // conformer_layer_forward's conv-module output
-    bool profiling_ = false;
+    struct ProfHook;
+    unsigned prof_mask_ = 0;
+    int prof_stride_ = 1;        // time every stride-th launch of the selected families
+    int64_t prof_seen_ = 0;
+    int cur_fam_ = -1;
+    std::unique_ptr<ProfHook> prof_hook_;
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> prof_ev_;   // event pool, reused
+    std::vector<int> prof_pending_;                             // family of pool entry i
     double prof_ms_[KF_COUNT] = {};
     int64_t prof_n_[KF_COUNT] = {};
-    hipEvent_t ev_[2] = {nullptr, nullptr};
 };
 
 // Upload one raw-layout weight (repacked for the f16 or f32 GEMM path); the

@@ -280,8 +280,9 @@ def _wval(f, t, v):
         raise ValueError(t)
 
 
-def write_gguf(model: Model, path: str, align: int = 32):
-    kv = _kv_items(model.cfg)
+def write_gguf(model: Model, path: str, align: int = 32, extra_kv=()):
+    """extra_kv: additional (key, gguf type id, value) items, e.g. streaming keys."""
+    kv = _kv_items(model.cfg) + list(extra_kv)
     names = model.names()
     offs, off = [], 0
     for n in names:

@@ -76,7 +76,7 @@ SIGS = {
                     _vp], C.c_int),
     "pkx_layernorm": ([_vp, _vp, _vp, _vp, C.c_int64, C.c_int, C.c_float, _vp], C.c_int),
     "pkx_rel_pos_encoding": ([C.c_int, C.c_int, _vp, _vp], C.c_int),
-    "pkx_model_set_profiling": ([_vp, C.c_int], C.c_int),
+    "pkx_model_set_profiling": ([_vp, C.c_uint, C.c_int], C.c_int),
     "pkx_model_profile_read": ([_vp, C.POINTER(C.c_double), C.POINTER(C.c_int64)], C.c_int),
 }
 
@@ -321,8 +321,18 @@ class Model:
         check(lib().pkx_tdt_joint_argmax(self.handle, enc.ptr, M, g.ptr, logits.ptr, tok.ptr, dur.ptr,
                                          _sh(stream)))
 
-    def set_profiling(self, on: bool):
-        check(lib().pkx_model_set_profiling(self.handle, 1 if on else 0))
+    def set_profiling(self, families=True, stride=1):
+        """families: True (all), False/None (off), or an iterable of PROF_FAMILIES names;
+        stride: time every stride-th launch of those families."""
+        if families is True:
+            mask = (1 << len(PROF_FAMILIES)) - 1
+        elif not families:
+            mask = 0
+        else:
+            mask = 0
+            for f in families:
+                mask |= 1 << PROF_FAMILIES.index(f)
+        check(lib().pkx_model_set_profiling(self.handle, mask, int(stride)))
 
     def profile(self):
         ms = (C.c_double * len(PROF_FAMILIES))()

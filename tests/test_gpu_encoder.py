@@ -133,3 +133,34 @@ def test_tdt_joint_argmax(gpu, stream, name):
     ok_d = _margin_ok(lg_ref[:, n_tok:], dur_ref)
     assert np.array_equal(tok[ok_t], tok_ref[ok_t])
     assert np.array_equal(dur[ok_d], dur_ref[ok_d])
+
+
+def test_profiling_counts_and_sampling(gpu, stream):
+    """Per-dispatch profiling: every family of a 3-layer encoder forward is
+    seen with the expected launch counts, times are positive, outputs are
+    unchanged by profiling, and stride sampling times every stride-th launch."""
+    m, om, gm, prec = _models(gpu, "q8_0")
+    L, B, T = m.cfg.n_layers, 2, 200
+    mel = _mel(B, m.cfg.n_mels, T, [200, 120], 5)
+    dm = gpu.DeviceArray.from_numpy(mel, stream)
+    Tp = oracle.subsampled_len(T)
+    dy = gpu.DeviceArray((B, Tp, m.cfg.d_model), np.float32)
+    gm.encoder_forward(dm, [200, 120], dy, stream=stream)
+    plain = dy.numpy(stream)
+    gm.set_profiling(True)
+    gm.encoder_forward(dm, [200, 120], dy, stream=stream)
+    prof = gm.profile()
+    assert np.array_equal(dy.numpy(stream), plain)
+    expect = {"subsampling": 6, "layernorm": 4 * L + 1, "gemm_ffn": 4 * L, "gemm_qkv": L, "gemm_pos": L,
+              "attention": L, "gemm_out": L, "gemm_pw1_glu": L, "dwconv": L, "gemm_pw2": L, "pos_enc": 1}
+    for fam, n in expect.items():
+        ms, got_n = prof[fam]
+        assert got_n == n, (fam, got_n, n)
+        assert ms > 0, fam
+    gm.set_profiling(["gemm_ffn"], stride=5)
+    for _ in range(5):
+        gm.encoder_forward(dm, [200, 120], dy, stream=stream)
+    prof = gm.profile()
+    assert prof["gemm_ffn"][1] == len(range(0, 5 * 4 * L, 5))
+    assert prof["layernorm"][1] == 0
+    gm.set_profiling(False)

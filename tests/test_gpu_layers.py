@@ -133,3 +133,33 @@ def test_batched_equals_per_item(gpu, stream, name):
     short = y1.numpy(stream)[0]
     assert rel_l2(both[0], full) < 1e-3
     assert rel_l2(both[1, :T // 2], short[:T // 2]) < 1e-3
+
+
+@pytest.mark.parametrize("ragged", [False, True])
+def test_conformer_layer_production_shape(gpu, stream, ragged):
+    """One 0.6B-shape block (d=1024, 8 heads x 128, FFN 4096, q8_0 linears) at
+    batch 16 x T'=125: the tile shapes and epilogues the encoder benchmark runs
+    (128x128 SiLU/store, 128x64 residual, 64x64 positional projection, f16
+    64x128 GLU) all checked against the oracle."""
+    cfg = _cfg(dict(d_model=1024, n_heads=8, ff_dim=4096, attn_bias=False, ff_bias=False, conv_bias=False),
+               n_layers=1)
+    m = pm.synthesize(cfg, "q8_0", bn_random=True)
+    om = oracle.OracleModel(m)
+    gm = gpu.Model.from_tensors(m, 1)
+    B, T, D = 16, 125, 1024
+    rng = np.random.default_rng(2026 + ragged)
+    valid = rng.integers(2, T + 1, B).tolist() if ragged else [T] * B
+    valid[0] = T
+    x = rng.normal(0, 1, (B, T, D)).astype(np.float32)
+    print(f"[layer-0.6B] B={B} T={T} valid={valid}", flush=True)
+    ref, ref_conv = om.conformer_layer(0, x, oracle.rel_pos_encoding(T, D), valid, want_conv=True)
+    dx = gpu.DeviceArray.from_numpy(x, stream)
+    dy = gpu.DeviceArray((B, T, D), np.float32)
+    dconv = gpu.DeviceArray((B, T, D), np.float32)
+    gm.conformer_layer(0, dx, valid, dy, dconv, stream)
+    got, got_conv = dy.numpy(stream), dconv.numpy(stream)
+    gm.close()
+    mask = _valid_mask(B, T, valid)
+    assert rel_l2(got[mask], ref[mask]) < 1e-2
+    assert rel_l2(got_conv[mask], ref_conv[mask]) < 1e-2
+    assert rel_l2(got[mask] - x[mask], ref[mask] - x[mask]) < 3e-2
