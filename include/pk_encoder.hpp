@@ -1,0 +1,185 @@
+// pk_encoder.hpp -- C++ host classes of parakeet.cpp's encoder path, backed by
+// the gfx950 kernels behind the pkx C ABI (pkx.h).
+//
+// Same class names, method names, argument meaning and layouts as the
+// reference's host API for this path, so code written against it (the
+// transcribe paths in src/model.cpp, the CLI bench, the tests) compiles
+// against this header unchanged:
+//   pk::ModelLoader       src/model_loader.hpp:53-83 (load + config only)
+//   pk::MelBatch          src/encoder.hpp:17-23
+//   pk::Encoder           src/encoder.hpp:25-62
+//   pk::Subsampling       src/subsampling.hpp:11-76
+//   pk::ConformerLayer    src/conformer.hpp:48-110
+//   pk::RelPosAttention   src/relpos_attention.hpp:31-66
+//   pk::rel_pos_encoding  src/pos_enc.hpp:20
+// The ggml graph builders (build_graph, build_graph_batched) have no
+// counterpart: nothing here builds a graph.  Their batched semantics are
+// offered as forward_batch() overloads on host vectors instead.
+//
+// Errors: ModelLoader::load returns false (message in last_error() and on
+// stderr), like the reference.  A failing forward throws std::runtime_error
+// carrying pkx_last_error(); the reference asserts instead (src/encoder.cpp:90).
+//
+// Threading: one ModelLoader owns one device model and one HIP stream; the
+// forward calls of every object built on it are serialised by a mutex inside
+// it (the reference serialises all compute behind one global mutex,
+// src/ggml_graph.cpp:35,84).  Distinct loaders run independently.
+#pragma once
+
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "pkx.h"
+
+namespace pk {
+
+// Encoder fields of the reference's ParakeetConfig (src/model_loader.hpp:27-52).
+struct ParakeetConfig {
+    int feat_in = 0;                     // n_mels
+    int d_model = 0;
+    int n_layers = 0;
+    int n_heads = 0;
+    int ff_dim = 0;
+    int conv_kernel = 0;
+    int subsampling_conv_channels = 0;
+    bool xscaling = true;
+    int vocab_size = 0;
+    int n_durations = 0;                 // len(tdt.durations); 0 without a TDT head
+};
+
+class ModelLoader {
+public:
+    ModelLoader();
+    ~ModelLoader();
+    ModelLoader(const ModelLoader&) = delete;
+    ModelLoader& operator=(const ModelLoader&) = delete;
+
+    // Read a GGUF (parakeet.* KV, verbatim NeMo tensor names) and upload the
+    // encoder weights once.  precision: PKX_PREC_AUTO / _F32 / _F16.
+    bool load(const std::string& path) { return load(path, PKX_PREC_AUTO); }
+    bool load(const std::string& path, int precision);
+    const ParakeetConfig& config() const { return cfg_; }
+    const std::string& last_error() const { return err_; }
+
+    pkx_model* handle() const { return model_; }
+    int precision() const { return precision_; }
+
+    struct Device;                        // stream, staging buffers, lock
+    Device& device() const { return *dev_; }
+
+private:
+    pkx_model* model_ = nullptr;
+    ParakeetConfig cfg_;
+    int precision_ = PKX_PREC_AUTO;
+    std::string err_;
+    std::unique_ptr<Device> dev_;
+};
+
+// A batch of clips' mel features, pre-stacked to T_max.
+struct MelBatch {
+    std::vector<float> data;     // [B][n_mels][T_max]: data[(b*n_mels + m)*T_max + t]
+    int n_mels = 0;
+    int T_max = 0;
+    int B = 0;
+    std::vector<int> valid_T;    // true mel frames per item, size B (<= T_max)
+};
+
+class Encoder {
+public:
+    explicit Encoder(const ModelLoader& ml);
+
+    // mel [n_mels][T] -> enc_out [d_model][Tout] (channels-first).
+    void forward(const std::vector<float>& mel, int n_mels, int T,
+                 std::vector<float>& enc_out, int& d_model, int& Tout) const;
+
+    // All B clips in one launch sequence; enc_outs[b] is [d_model][valid_Tout[b]].
+    void forward_batch(const MelBatch& mels, std::vector<std::vector<float>>& enc_outs,
+                       int& d_model, int& Tout, std::vector<int>& valid_Tout) const;
+
+    // forward() plus the outputs of the layers listed in capture_layers, each
+    // [T'][d_model], in layer_outs (parallel to capture_layers).
+    void forward_capture(const std::vector<float>& mel, int n_mels, int T,
+                         std::vector<float>& enc_out, int& d_model, int& Tout,
+                         const std::vector<int>& capture_layers,
+                         std::vector<std::vector<float>>& layer_outs) const;
+
+private:
+    const ModelLoader& ml_;
+    int d_model_;
+    int n_layers_;
+    bool xscaling_;
+};
+
+class Subsampling {
+public:
+    explicit Subsampling(const ModelLoader& ml);
+
+    // mel [n_mels][T] -> out [Tout][d_model] (scalar-path masking).
+    void forward(const std::vector<float>& mel, int n_mels, int T,
+                 std::vector<float>& out, int& Tout, int& d_model) const;
+    void forward(const std::vector<float>& mel, int n_mels, int T,
+                 std::vector<float>& out, int& Tout, int& d_model, int& valid_len) const;
+    // in_valid_frames >= 0 replaces the offline T-1 entry valid length; values
+    // above T-1 (whole-window streaming chunks) are outside this offline build.
+    void forward(const std::vector<float>& mel, int n_mels, int T,
+                 std::vector<float>& out, int& Tout, int& d_model, int& valid_len,
+                 int in_valid_frames) const;
+
+    // build_graph_batched semantics (per-stage time masks): mel [B][n_mels][T],
+    // valid_in[b] is the entry valid length (< 0: T-1); out [B][Tp][d_model].
+    void forward_batch(const float* mel, int n_mels, int T, int B, const std::vector<int>& valid_in,
+                       std::vector<float>& out, int& Tp, std::vector<int>& valid_out) const;
+
+    int valid_out_len(int T, int in_valid_frames = -1) const;
+
+private:
+    const ModelLoader& ml_;
+    int d_model_;
+};
+
+class ConformerLayer {
+public:
+    ConformerLayer(const ModelLoader& ml, int layer_idx);
+
+    // x [T][d_model]; pos_emb [pos_len = 2T-1][d_model] must be
+    // rel_pos_encoding(T, d_model) (the device path regenerates that table);
+    // out [T][d_model].
+    void forward(const std::vector<float>& x, int T, const std::vector<float>& pos_emb,
+                 int pos_len, int valid_len, std::vector<float>& out) const;
+    void forward_with_conv(const std::vector<float>& x, int T, const std::vector<float>& pos_emb,
+                           int pos_len, int valid_len, std::vector<float>& out,
+                           std::vector<float>& conv_out) const;
+    // The conv module alone on conv_in = norm_conv(residual), [T][d_model].
+    void conv_module_forward(const std::vector<float>& conv_in, int T, int valid_len,
+                             std::vector<float>& out) const;
+    // build_graph_batched semantics: x, out [B][T][d_model], valid_len size B.
+    void forward_batch(const std::vector<float>& x, int T, int B, const std::vector<float>& pos_emb,
+                       int pos_len, const std::vector<int>& valid_len, std::vector<float>& out) const;
+
+private:
+    const ModelLoader& ml_;
+    int layer_idx_;
+    int d_model_;
+};
+
+class RelPosAttention {
+public:
+    RelPosAttention(const ModelLoader& ml, int layer_idx);
+
+    // x [T][d_model] (already normalised); pos_emb as for ConformerLayer.
+    void forward(const std::vector<float>& x, int T, const std::vector<float>& pos_emb,
+                 int pos_len, int valid_len, std::vector<float>& out) const;
+    void forward_batch(const std::vector<float>& x, int T, int B, const std::vector<float>& pos_emb,
+                       int pos_len, const std::vector<int>& valid_len, std::vector<float>& out) const;
+
+private:
+    const ModelLoader& ml_;
+    int layer_idx_;
+    int d_model_;
+};
+
+// pos_emb [2T-1][d_model] f32 (computed on the device in double, then f32).
+void rel_pos_encoding(int T, int d_model, std::vector<float>& out);
+
+}  // namespace pk

@@ -1,0 +1,410 @@
+// Host classes of the encoder path (include/pk_encoder.hpp) over the pkx C ABI.
+// Each call stages host vectors into grow-only device buffers owned by the
+// loader, runs the device path on the loader's stream and copies the result
+// back.  Plain C++17; the only device interface is pkx.h.
+#include "pk_encoder.hpp"
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <stdexcept>
+
+namespace pk {
+
+namespace {
+
+void chk(int rc, const char* what) {
+    if (rc != 0) throw std::runtime_error(std::string(what) + ": " + pkx_last_error());
+}
+
+void need(bool ok, const std::string& msg) {
+    if (!ok) throw std::invalid_argument(msg);
+}
+
+// The positional table the device regenerates (src/pos_enc.cpp:10-34):
+// row p is position T-1-p; columns 2i/2i+1 hold sin/cos of pos * 10000^(-2i/d),
+// evaluated in double and stored as f32.  Spot-checks rows 0, T-1 and 2T-2 of
+// a caller's table so a different table is refused rather than ignored.
+void check_pos_emb(const std::vector<float>& pe, int T, int pos_len, int d) {
+    need(T >= 1 && pos_len == 2 * T - 1, "pos_emb: pos_len must be 2T-1");
+    need(pe.size() == (size_t)pos_len * d, "pos_emb: size must be pos_len * d_model");
+    const double neg_log = -std::log(10000.0) / d;
+    for (int p : {0, T - 1, 2 * T - 2}) {
+        const double pos = (double)(T - 1 - p);
+        for (int i = 0; i < d / 2; ++i) {
+            const double ang = pos * std::exp((double)(2 * i) * neg_log);
+            const float s = (float)std::sin(ang), c = (float)std::cos(ang);
+            const float gs = pe[(size_t)p * d + 2 * i], gc = pe[(size_t)p * d + 2 * i + 1];
+            need(std::fabs(gs - s) <= 1e-5f + 1e-5f * std::fabs(s) && std::fabs(gc - c) <= 1e-5f + 1e-5f * std::fabs(c),
+                 "pos_emb: table differs from rel_pos_encoding(T, d_model); the device path "
+                 "only supports the standard table");
+        }
+    }
+}
+
+}  // namespace
+
+struct ModelLoader::Device {
+    struct Buf {
+        void* p = nullptr;
+        size_t n = 0;
+    };
+    void* stream = nullptr;
+    std::mutex mu;
+    Buf in, out, aux, cap, meta;
+
+    void* get(Buf& b, size_t bytes) {
+        if (bytes == 0) bytes = 1;
+        if (b.n < bytes) {
+            if (b.p) pkx_free(b.p);
+            b.p = nullptr;
+            b.n = 0;
+            chk(pkx_malloc(&b.p, bytes), "pkx_malloc");
+            b.n = bytes;
+        }
+        return b.p;
+    }
+    void h2d(void* dst, const void* src, size_t bytes) { chk(pkx_memcpy_h2d(dst, src, bytes, stream), "h2d"); }
+    void d2h(void* dst, const void* src, size_t bytes) { chk(pkx_memcpy_d2h(dst, src, bytes, stream), "d2h"); }
+    void sync() { chk(pkx_stream_synchronize(stream), "synchronize"); }
+    ~Device() {
+        for (Buf* b : {&in, &out, &aux, &cap, &meta})
+            if (b->p) pkx_free(b->p);
+        if (stream) pkx_stream_destroy(stream);
+    }
+};
+
+// ---------------------------------------------------------------------------
+// ModelLoader
+// ---------------------------------------------------------------------------
+ModelLoader::ModelLoader() = default;
+
+ModelLoader::~ModelLoader() {
+    dev_.reset();
+    if (model_) pkx_model_free(model_);
+}
+
+bool ModelLoader::load(const std::string& path, int precision) {
+    if (model_) {
+        err_ = "ModelLoader::load: already loaded";
+        std::fprintf(stderr, "[pk] %s\n", err_.c_str());
+        return false;
+    }
+    pkx_model* m = nullptr;
+    if (pkx_model_load_gguf(path.c_str(), precision, &m) != 0) {
+        err_ = std::string("gguf load failed: ") + path + ": " + pkx_last_error();
+        std::fprintf(stderr, "[pk] %s\n", err_.c_str());
+        return false;
+    }
+    pkx_config c{};
+    int prec = 0, has_ctc = 0, has_joint = 0;
+    auto dev = std::make_unique<Device>();
+    if (pkx_model_info(m, &c, &prec, &has_ctc, &has_joint) != 0 || pkx_stream_create(&dev->stream) != 0) {
+        err_ = std::string("device set-up failed: ") + pkx_last_error();
+        std::fprintf(stderr, "[pk] %s\n", err_.c_str());
+        pkx_model_free(m);
+        return false;
+    }
+    cfg_.feat_in = c.n_mels;
+    cfg_.d_model = c.d_model;
+    cfg_.n_layers = c.n_layers;
+    cfg_.n_heads = c.n_heads;
+    cfg_.ff_dim = c.ff_dim;
+    cfg_.conv_kernel = c.conv_kernel;
+    cfg_.subsampling_conv_channels = c.sub_channels;
+    cfg_.xscaling = c.xscaling != 0;
+    cfg_.vocab_size = c.vocab_size;
+    cfg_.n_durations = c.n_durations;
+    precision_ = prec;
+    model_ = m;
+    dev_ = std::move(dev);
+    err_.clear();
+    return true;
+}
+
+static ModelLoader::Device& dev_of(const ModelLoader& ml) {
+    need(ml.handle() != nullptr, "model not loaded");
+    return ml.device();
+}
+
+// ---------------------------------------------------------------------------
+// Encoder
+// ---------------------------------------------------------------------------
+Encoder::Encoder(const ModelLoader& ml)
+    : ml_(ml), d_model_(ml.config().d_model), n_layers_(ml.config().n_layers), xscaling_(ml.config().xscaling) {
+    need(ml.handle() != nullptr, "Encoder: model not loaded");
+}
+
+void Encoder::forward(const std::vector<float>& mel, int n_mels, int T, std::vector<float>& enc_out,
+                      int& d_model, int& Tout) const {
+    std::vector<std::vector<float>> none;
+    forward_capture(mel, n_mels, T, enc_out, d_model, Tout, {}, none);
+}
+
+void Encoder::forward_capture(const std::vector<float>& mel, int n_mels, int T, std::vector<float>& enc_out,
+                              int& d_model, int& Tout, const std::vector<int>& capture_layers,
+                              std::vector<std::vector<float>>& layer_outs) const {
+    need(n_mels == ml_.config().feat_in, "Encoder::forward: n_mels does not match the model");
+    need(T >= 1 && mel.size() == (size_t)n_mels * T, "Encoder::forward: mel must be [n_mels][T]");
+    for (int l : capture_layers) need(l >= 0 && l < n_layers_, "Encoder::forward_capture: layer out of range");
+    ModelLoader::Device& d = dev_of(ml_);
+    std::lock_guard<std::mutex> lock(d.mu);
+    const int Tp = pkx_subsampled_len(T), D = d_model_;
+    float* dmel = (float*)d.get(d.in, mel.size() * 4);
+    float* dout = (float*)d.get(d.out, (size_t)Tp * D * 4);
+    float* dcf = (float*)d.get(d.aux, (size_t)Tp * D * 4);
+    float* dcap = capture_layers.empty() ? nullptr : (float*)d.get(d.cap, (size_t)n_layers_ * Tp * D * 4);
+    struct { int32_t v; int32_t pad; int64_t off; } meta{0, 0, 0};
+    char* dmeta = (char*)d.get(d.meta, sizeof(meta));
+    d.h2d(dmel, mel.data(), mel.size() * 4);
+    int tout = 0, vout = 0;
+    // B=1 path: the scalar subsampling graph (src/encoder.cpp:30-95).
+    chk(pkx_encoder_forward(ml_.handle(), dmel, 1, T, nullptr, PKX_MASK_SCALAR, dout, &tout, &vout, dcap, d.stream),
+        "pkx_encoder_forward");
+    // full-width channels-first transpose (src/encoder.cpp:84-86)
+    meta.v = tout;
+    d.h2d(dmeta, &meta, sizeof(meta));
+    chk(pkx_compact_channels_first(dout, 1, tout, D, (const int*)dmeta, (const int64_t*)(dmeta + 8), dcf, d.stream),
+        "pkx_compact_channels_first");
+    enc_out.resize((size_t)D * tout);
+    d.d2h(enc_out.data(), dcf, enc_out.size() * 4);
+    layer_outs.assign(capture_layers.size(), {});
+    for (size_t i = 0; i < capture_layers.size(); ++i) {
+        layer_outs[i].resize((size_t)tout * D);
+        d.d2h(layer_outs[i].data(), dcap + (size_t)capture_layers[i] * tout * D, layer_outs[i].size() * 4);
+    }
+    d.sync();
+    d_model = D;
+    Tout = tout;
+}
+
+void Encoder::forward_batch(const MelBatch& mels, std::vector<std::vector<float>>& enc_outs, int& d_model,
+                            int& Tout, std::vector<int>& valid_Tout) const {
+    const int B = mels.B, F = mels.n_mels, T = mels.T_max, D = d_model_;
+    need(B >= 1 && T >= 1, "Encoder::forward_batch: empty batch");
+    need(F == ml_.config().feat_in, "Encoder::forward_batch: n_mels does not match the model");
+    need(mels.data.size() == (size_t)B * F * T, "Encoder::forward_batch: data must be [B][n_mels][T_max]");
+    need(mels.valid_T.size() == (size_t)B, "Encoder::forward_batch: valid_T must have B entries");
+    ModelLoader::Device& d = dev_of(ml_);
+    std::lock_guard<std::mutex> lock(d.mu);
+    const int Tp = pkx_subsampled_len(T);
+    float* dmel = (float*)d.get(d.in, mels.data.size() * 4);
+    float* dout = (float*)d.get(d.out, (size_t)B * Tp * D * 4);
+    float* dcf = (float*)d.get(d.aux, (size_t)B * Tp * D * 4);
+    d.h2d(dmel, mels.data.data(), mels.data.size() * 4);
+    int tout = 0;
+    std::vector<int> vo(B);
+    chk(pkx_encoder_forward(ml_.handle(), dmel, B, T, mels.valid_T.data(), PKX_MASK_BATCHED, dout, &tout,
+                            vo.data(), nullptr, d.stream),
+        "pkx_encoder_forward");
+    // per-item compaction to [d_model][valid_Tout[b]] (src/encoder.cpp:158-166)
+    std::vector<char> meta((size_t)B * 4 + 8 + (size_t)B * 8, 0);
+    std::vector<int64_t> offs(B);
+    int64_t total = 0;
+    for (int b = 0; b < B; ++b) {
+        offs[b] = total;
+        total += (int64_t)vo[b] * D;
+    }
+    const size_t off_pos = ((size_t)B * 4 + 7) / 8 * 8;
+    std::memcpy(meta.data(), vo.data(), (size_t)B * 4);
+    std::memcpy(meta.data() + off_pos, offs.data(), (size_t)B * 8);
+    char* dmeta = (char*)d.get(d.meta, meta.size());
+    d.h2d(dmeta, meta.data(), meta.size());
+    chk(pkx_compact_channels_first(dout, B, tout, D, (const int*)dmeta, (const int64_t*)(dmeta + off_pos), dcf,
+                                   d.stream),
+        "pkx_compact_channels_first");
+    std::vector<float> flat((size_t)total);
+    d.d2h(flat.data(), dcf, flat.size() * 4);
+    d.sync();
+    enc_outs.assign(B, {});
+    for (int b = 0; b < B; ++b)
+        enc_outs[b].assign(flat.begin() + offs[b], flat.begin() + offs[b] + (int64_t)vo[b] * D);
+    d_model = D;
+    Tout = tout;
+    valid_Tout = vo;
+}
+
+// ---------------------------------------------------------------------------
+// Subsampling
+// ---------------------------------------------------------------------------
+Subsampling::Subsampling(const ModelLoader& ml) : ml_(ml), d_model_(ml.config().d_model) {
+    need(ml.handle() != nullptr, "Subsampling: model not loaded");
+}
+
+void Subsampling::forward(const std::vector<float>& mel, int n_mels, int T, std::vector<float>& out, int& Tout,
+                          int& d_model) const {
+    int v = 0;
+    forward(mel, n_mels, T, out, Tout, d_model, v, -1);
+}
+
+void Subsampling::forward(const std::vector<float>& mel, int n_mels, int T, std::vector<float>& out, int& Tout,
+                          int& d_model, int& valid_len) const {
+    forward(mel, n_mels, T, out, Tout, d_model, valid_len, -1);
+}
+
+void Subsampling::forward(const std::vector<float>& mel, int n_mels, int T, std::vector<float>& out, int& Tout,
+                          int& d_model, int& valid_len, int in_valid_frames) const {
+    need(n_mels == ml_.config().feat_in, "Subsampling::forward: n_mels does not match the model");
+    need(T >= 1 && mel.size() == (size_t)n_mels * T, "Subsampling::forward: mel must be [n_mels][T]");
+    need(in_valid_frames <= T - 1,
+         "Subsampling::forward: in_valid_frames > T-1 is a streaming window (not in this offline build)");
+    ModelLoader::Device& d = dev_of(ml_);
+    std::lock_guard<std::mutex> lock(d.mu);
+    const int Tp = pkx_subsampled_len(T), D = d_model_;
+    float* dmel = (float*)d.get(d.in, mel.size() * 4);
+    float* dout = (float*)d.get(d.out, (size_t)Tp * D * 4);
+    d.h2d(dmel, mel.data(), mel.size() * 4);
+    // the C ABI takes true frame counts; the entry valid length is that minus one
+    const int vT = in_valid_frames < 0 ? T : in_valid_frames + 1;
+    int tout = 0, vo = 0;
+    chk(pkx_subsampling_forward(ml_.handle(), dmel, 1, T, &vT, PKX_MASK_SCALAR, dout, &tout, &vo, d.stream),
+        "pkx_subsampling_forward");
+    out.resize((size_t)tout * D);
+    d.d2h(out.data(), dout, out.size() * 4);
+    d.sync();
+    Tout = tout;
+    d_model = D;
+    valid_len = vo;
+}
+
+void Subsampling::forward_batch(const float* mel, int n_mels, int T, int B, const std::vector<int>& valid_in,
+                                std::vector<float>& out, int& Tp, std::vector<int>& valid_out) const {
+    need(mel != nullptr && B >= 1 && T >= 1, "Subsampling::forward_batch: empty batch");
+    need(n_mels == ml_.config().feat_in, "Subsampling::forward_batch: n_mels does not match the model");
+    need(valid_in.size() == (size_t)B, "Subsampling::forward_batch: valid_in must have B entries");
+    std::vector<int> vT(B);
+    for (int b = 0; b < B; ++b) {
+        need(valid_in[b] <= T - 1, "Subsampling::forward_batch: valid_in[b] must be <= T-1");
+        vT[b] = valid_in[b] < 0 ? T : valid_in[b] + 1;
+    }
+    ModelLoader::Device& d = dev_of(ml_);
+    std::lock_guard<std::mutex> lock(d.mu);
+    const int tp = pkx_subsampled_len(T), D = d_model_;
+    const size_t nmel = (size_t)B * n_mels * T;
+    float* dmel = (float*)d.get(d.in, nmel * 4);
+    float* dout = (float*)d.get(d.out, (size_t)B * tp * D * 4);
+    d.h2d(dmel, mel, nmel * 4);
+    int tout = 0;
+    std::vector<int> vo(B);
+    chk(pkx_subsampling_forward(ml_.handle(), dmel, B, T, vT.data(), PKX_MASK_BATCHED, dout, &tout, vo.data(),
+                                d.stream),
+        "pkx_subsampling_forward");
+    out.resize((size_t)B * tout * D);
+    d.d2h(out.data(), dout, out.size() * 4);
+    d.sync();
+    Tp = tout;
+    valid_out = vo;
+}
+
+int Subsampling::valid_out_len(int T, int in_valid_frames) const { return pkx_valid_out_len(T, in_valid_frames); }
+
+// ---------------------------------------------------------------------------
+// ConformerLayer / RelPosAttention
+// ---------------------------------------------------------------------------
+namespace {
+
+enum class Unit { Layer, Attention, Conv };
+
+void run_unit(const ModelLoader& ml, Unit u, int layer, const std::vector<float>& x, int T, int B,
+              const std::vector<int>& valid, std::vector<float>& out, std::vector<float>* conv_out) {
+    const int D = ml.config().d_model;
+    need(T >= 1 && B >= 1 && x.size() == (size_t)B * T * D, "input must be [B][T][d_model]");
+    need(valid.size() == (size_t)B, "valid_len must have B entries");
+    for (int v : valid) need(v >= 0 && v <= T, "valid_len must be in [0, T]");
+    ModelLoader::Device& d = dev_of(ml);
+    std::lock_guard<std::mutex> lock(d.mu);
+    const size_t n = x.size();
+    float* dx = (float*)d.get(d.in, n * 4);
+    float* dy = (float*)d.get(d.out, n * 4);
+    float* dc = conv_out ? (float*)d.get(d.aux, n * 4) : nullptr;
+    d.h2d(dx, x.data(), n * 4);
+    switch (u) {
+    case Unit::Layer:
+        chk(pkx_conformer_layer_forward(ml.handle(), layer, dx, B, T, valid.data(), dy, dc, d.stream),
+            "pkx_conformer_layer_forward");
+        break;
+    case Unit::Attention:
+        chk(pkx_relpos_attention_forward(ml.handle(), layer, dx, B, T, valid.data(), dy, d.stream),
+            "pkx_relpos_attention_forward");
+        break;
+    case Unit::Conv:
+        chk(pkx_conv_module_forward(ml.handle(), layer, dx, B, T, valid.data(), dy, d.stream),
+            "pkx_conv_module_forward");
+        break;
+    }
+    out.resize(n);
+    d.d2h(out.data(), dy, n * 4);
+    if (conv_out) {
+        conv_out->resize(n);
+        d.d2h(conv_out->data(), dc, n * 4);
+    }
+    d.sync();
+}
+
+}  // namespace
+
+ConformerLayer::ConformerLayer(const ModelLoader& ml, int layer_idx)
+    : ml_(ml), layer_idx_(layer_idx), d_model_(ml.config().d_model) {
+    need(ml.handle() != nullptr, "ConformerLayer: model not loaded");
+    need(layer_idx >= 0 && layer_idx < ml.config().n_layers, "ConformerLayer: layer index out of range");
+}
+
+void ConformerLayer::forward(const std::vector<float>& x, int T, const std::vector<float>& pos_emb, int pos_len,
+                             int valid_len, std::vector<float>& out) const {
+    check_pos_emb(pos_emb, T, pos_len, d_model_);
+    run_unit(ml_, Unit::Layer, layer_idx_, x, T, 1, {valid_len}, out, nullptr);
+}
+
+void ConformerLayer::forward_with_conv(const std::vector<float>& x, int T, const std::vector<float>& pos_emb,
+                                       int pos_len, int valid_len, std::vector<float>& out,
+                                       std::vector<float>& conv_out) const {
+    check_pos_emb(pos_emb, T, pos_len, d_model_);
+    run_unit(ml_, Unit::Layer, layer_idx_, x, T, 1, {valid_len}, out, &conv_out);
+}
+
+void ConformerLayer::conv_module_forward(const std::vector<float>& conv_in, int T, int valid_len,
+                                         std::vector<float>& out) const {
+    run_unit(ml_, Unit::Conv, layer_idx_, conv_in, T, 1, {valid_len}, out, nullptr);
+}
+
+void ConformerLayer::forward_batch(const std::vector<float>& x, int T, int B, const std::vector<float>& pos_emb,
+                                   int pos_len, const std::vector<int>& valid_len, std::vector<float>& out) const {
+    check_pos_emb(pos_emb, T, pos_len, d_model_);
+    run_unit(ml_, Unit::Layer, layer_idx_, x, T, B, valid_len, out, nullptr);
+}
+
+RelPosAttention::RelPosAttention(const ModelLoader& ml, int layer_idx)
+    : ml_(ml), layer_idx_(layer_idx), d_model_(ml.config().d_model) {
+    need(ml.handle() != nullptr, "RelPosAttention: model not loaded");
+    need(layer_idx >= 0 && layer_idx < ml.config().n_layers, "RelPosAttention: layer index out of range");
+}
+
+void RelPosAttention::forward(const std::vector<float>& x, int T, const std::vector<float>& pos_emb, int pos_len,
+                              int valid_len, std::vector<float>& out) const {
+    check_pos_emb(pos_emb, T, pos_len, d_model_);
+    run_unit(ml_, Unit::Attention, layer_idx_, x, T, 1, {valid_len}, out, nullptr);
+}
+
+void RelPosAttention::forward_batch(const std::vector<float>& x, int T, int B, const std::vector<float>& pos_emb,
+                                    int pos_len, const std::vector<int>& valid_len, std::vector<float>& out) const {
+    check_pos_emb(pos_emb, T, pos_len, d_model_);
+    run_unit(ml_, Unit::Attention, layer_idx_, x, T, B, valid_len, out, nullptr);
+}
+
+// ---------------------------------------------------------------------------
+void rel_pos_encoding(int T, int d_model, std::vector<float>& out) {
+    need(T >= 1 && d_model >= 2 && d_model % 2 == 0, "rel_pos_encoding: T >= 1 and even d_model");
+    const size_t n = (size_t)(2 * T - 1) * d_model;
+    void* dp = nullptr;
+    chk(pkx_malloc(&dp, n * 4), "pkx_malloc");
+    int rc = pkx_rel_pos_encoding(T, d_model, (float*)dp, nullptr);
+    out.resize(n);
+    if (rc == 0) rc = pkx_memcpy_d2h(out.data(), dp, n * 4, nullptr);
+    if (rc == 0) rc = pkx_stream_synchronize(nullptr);
+    const std::string msg = rc ? pkx_last_error() : "";
+    pkx_free(dp);
+    if (rc) throw std::runtime_error("rel_pos_encoding: " + msg);
+}
+
+}  // namespace pk

@@ -280,14 +280,14 @@ def _wval(f, t, v):
         raise ValueError(t)
 
 
-def write_gguf(model: Model, path: str, align: int = 32, extra_kv=()):
-    """extra_kv: additional (key, gguf type id, value) items, e.g. streaming keys."""
-    kv = _kv_items(model.cfg) + list(extra_kv)
-    names = model.names()
+def write_gguf_tensors(path: str, kv, tensors: dict, align: int = 32):
+    """GGUF v3: kv is a list of (key, gguf type id, value); tensors maps
+    name -> Tensor (ggml ne order taken from the torch-order shape)."""
+    names = list(tensors)
     offs, off = [], 0
     for n in names:
         offs.append(off)
-        off += model.tensors[n].nbytes()
+        off += tensors[n].nbytes()
         off = (off + align - 1) // align * align
     with open(path, "wb") as f:
         f.write(struct.pack("<IIQQ", 0x46554747, 3, len(names), len(kv)))
@@ -296,7 +296,7 @@ def write_gguf(model: Model, path: str, align: int = 32, extra_kv=()):
             f.write(struct.pack("<I", t))
             _wval(f, t, v)
         for n, o in zip(names, offs):
-            t = model.tensors[n]
+            t = tensors[n]
             _wstr(f, n)
             f.write(struct.pack("<I", len(t.ne)))
             for d in t.ne:
@@ -308,4 +308,25 @@ def write_gguf(model: Model, path: str, align: int = 32, extra_kv=()):
         for n, o in zip(names, offs):
             cur = f.tell() - base
             f.write(b"\0" * (o - cur))
-            f.write(np.ascontiguousarray(model.tensors[n].data).tobytes())
+            f.write(np.ascontiguousarray(tensors[n].data).tobytes())
+
+
+def write_gguf(model: Model, path: str, align: int = 32, extra_kv=()):
+    """extra_kv: additional (key, gguf type id, value) items, e.g. streaming keys."""
+    write_gguf_tensors(path, _kv_items(model.cfg) + list(extra_kv), model.tensors, align)
+
+
+GT_I32 = 26   # ggml's int32 tensor type
+
+
+def write_baseline_gguf(path: str, arrays: dict):
+    """Named f32 / int32 arrays (shape outermost first) in a GGUF, the layout of
+    the reference's parity baselines (tests/parity.hpp:12-41)."""
+    tensors = {}
+    for name, a in arrays.items():
+        a = np.asarray(a)
+        if a.dtype == np.int32:
+            tensors[name] = Tensor(GT_I32, tuple(a.shape), np.ascontiguousarray(a))
+        else:
+            tensors[name] = Tensor(0, tuple(a.shape), np.ascontiguousarray(a, dtype=np.float32))
+    write_gguf_tensors(path, [("general.architecture", 8, "parakeet-baseline")], tensors)

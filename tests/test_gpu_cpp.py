@@ -1,0 +1,74 @@
+"""The C++ encoder-path tests (tests/cpp/, written against the host classes in
+include/pk_encoder.hpp) run on the GPU against a synthetic model GGUF and a
+baseline GGUF whose tensors come from the oracle, named as the reference's
+parity baselines name them (tests/python/check_baseline.py:51-69):
+mel, subsampling_out, pos_emb, enc_pre_layers, l0_attn_in/out, l0_conv_out,
+enc_layer_{0,mid,last}, encoder_out.  The mel has 1001 frames, so T' = 126
+with 125 valid frames: the last frame is padding, as in the reference's
+fixtures (valid_len = T - 1 in its layer tests)."""
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+import oracle
+import pk_model as pm
+
+pytestmark = pytest.mark.gpu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+BIN = os.path.join(ROOT, "tests", "cpp", "build")
+TESTS = ["test_subsampling", "test_subsampling_batch", "test_relpos_attention", "test_relpos_attention_batch",
+         "test_conformer", "test_conformer_batch", "test_encoder", "test_encoder_batch"]
+_FILES = {}
+
+
+def _files(tmp_path_factory, wtype):
+    if wtype in _FILES:
+        return _FILES[wtype]
+    d = tmp_path_factory.mktemp(f"cpp_{wtype}")
+    cfg = pm.Config(d_model=256, n_layers=4, n_heads=4, ff_dim=1024, conv_kernel=9, n_mels=80, sub_channels=64,
+                    xscaling=True, vocab_size=127, joint_hidden=64, pred_hidden=64)
+    m = pm.synthesize(cfg, wtype, bn_random=True)
+    om = oracle.OracleModel(m)
+    rng = np.random.default_rng(42)
+    F, T = cfg.n_mels, 1001
+    mel = rng.standard_normal((F, T)).astype(np.float32)
+    sub, vo = om.subsampling(mel[None], None, stage_masks=False)
+    Tp, D = sub.shape[1], cfg.d_model
+    assert Tp == 126 and vo[0] == Tp - 1
+    pre = (sub[0] * np.float32(np.sqrt(D))).astype(np.float32)
+    pe = oracle.rel_pos_encoding(Tp, D)
+    enc, vo2, cap = om.encoder(mel[None], None, stage_masks=False, capture=True)
+    valid = [Tp - 1]
+    y0, conv0 = om.conformer_layer(0, pre[None], pe, valid, want_conv=True)
+    attn_in = rng.standard_normal((Tp, D)).astype(np.float32)
+    conv_in = rng.standard_normal((Tp, D)).astype(np.float32)
+    L = cfg.n_layers
+    base = {
+        "mel": mel, "subsampling_out": sub[0], "pos_emb": pe, "enc_pre_layers": pre,
+        "l0_attn_in": attn_in, "l0_attn_out": om.relpos_attention(0, attn_in[None], pe, valid)[0],
+        "l0_conv_out": conv0[0], "l0_conv_in": conv_in,
+        "l0_conv_module_out": om.conv_module(0, conv_in[None], valid)[0],
+        "enc_layer_0": y0[0], "enc_layer_mid": cap[L // 2][0], "enc_layer_last": cap[L - 1][0],
+        "encoder_out": np.ascontiguousarray(enc[0].T),
+    }
+    mp, bp = str(d / "model.gguf"), str(d / "baseline.gguf")
+    pm.write_gguf(m, mp)
+    pm.write_baseline_gguf(bp, base)
+    _FILES[wtype] = (mp, bp)
+    return _FILES[wtype]
+
+
+@pytest.mark.parametrize("wtype", ["f32", "q8_0"])
+@pytest.mark.parametrize("name", TESTS)
+def test_cpp(tmp_path_factory, wtype, name):
+    exe = os.path.join(BIN, name)
+    assert os.path.exists(exe), f"{exe} not built (make -C tests/cpp)"
+    mp, bp = _files(tmp_path_factory, wtype)
+    env = dict(os.environ, PARAKEET_TEST_GGUF=mp, PARAKEET_TEST_BASELINE=bp)
+    print(f"[cpp] {name} {wtype}", flush=True)
+    r = subprocess.run([exe], env=env, capture_output=True, text=True, timeout=120)
+    print(r.stderr)
+    assert r.returncode == 0, r.stdout + r.stderr
