@@ -131,6 +131,15 @@ def main():
     out = d_out.numpy(stream)
     assert np.isfinite(out).all(), "non-finite encoder output"
 
+    # A plain device-to-device copy of known size: under `rocprofv3 --pmc` its
+    # FETCH_SIZE / WRITE_SIZE calibrate the counters the traffic figure uses.
+    calib_n = 64 << 20
+    c_src, c_dst = pkx.DeviceArray((calib_n,), np.uint8), pkx.DeviceArray((calib_n,), np.uint8)
+    pkx.check(pkx.lib().pkx_memcpy_d2d(c_dst.ptr, c_src.ptr, calib_n, stream.handle))
+    stream.sync()
+    c_src.free()
+    c_dst.free()
+
     # Per-family breakdown: a separate pass with every launch timed the same way.
     n_prof = 3
     gm.set_profiling(True)

@@ -323,6 +323,45 @@ def test_pins_detect_planted_mistakes(tiny):
     assert rel_l2(dropped, ref) > 1e-4
 
 
+def test_pins_detect_more_planted_mistakes(tiny):
+    """Three more slips, each planted in the oracle's own weights (on the CPU):
+    a dropped 1/2 on the macaron FFN residual, depthwise taps applied as a
+    convolution instead of a cross-correlation, and a transposed query
+    projection.  Each moves the oracle far outside the torch pin's tolerance,
+    while the unmodified oracle sits within 1e-5 of it."""
+    m, om, tm, torch = tiny
+    rng = np.random.default_rng(13)
+    D = m.cfg.d_model
+    x = rng.normal(0, 1, (1, 11, D)).astype(np.float32)
+    pe = oracle.rel_pos_encoding(11, D)
+    xt, pet = torch.as_tensor(x, dtype=torch.float64), torch.as_tensor(pe, dtype=torch.float64)
+    ref_layer = tm.layer(0, xt, pet, [11]).numpy()
+    assert rel_l2(om.conformer_layer(0, x, pe, [11]), ref_layer) < 1e-5
+
+    def with_plant(name, fn, run):
+        keep = om.w[name].copy()
+        try:
+            om.w[name][...] = fn(keep)
+            return run()
+        finally:
+            om.w[name][...] = keep
+
+    # dropped 1/2: FFN1's output doubled
+    got = with_plant("encoder.layers.0.feed_forward1.linear2.weight", lambda w: 2 * w,
+                     lambda: om.conformer_layer(0, x, pe, [11]))
+    assert rel_l2(got, ref_layer) > 1e-3
+    # convolution instead of cross-correlation: taps reversed in time
+    ref_conv = tm.conv_module(0, xt, [11]).numpy()
+    got = with_plant("encoder.layers.0.conv.depthwise_conv.weight", lambda w: w[..., ::-1].copy(),
+                     lambda: om.conv_module(0, x, [11]))
+    assert rel_l2(got, ref_conv) > 1e-3
+    # transposed operand: W_q^T in place of W_q
+    ref_attn = tm.attention(0, xt, pe, [11]).numpy()
+    got = with_plant("encoder.layers.0.self_attn.linear_q.weight", lambda w: w.T.copy(),
+                     lambda: om.relpos_attention(0, x, pe, [11]))
+    assert rel_l2(got, ref_attn) > 1e-3
+
+
 # ---------------------------------------------------------------- length arithmetic
 def test_valid_length_arithmetic():
     # subsampling.cpp:25-46 with the offline T-1 entry convention
