@@ -170,9 +170,19 @@ def main():
         kernels[fam] = rec
     ffn_avg_s = ffn_ms / 1e3 / ffn_n
     ffn_tf = work["gemm_ffn"][1] / ffn_avg_s / 1e12
+    traffic, traffic_src = None, None
+    tpath = os.path.join(ROOT, "profiles", "gemm_ffn_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            tj = json.load(f)
+        traffic = tj["traffic_bytes_per_launch"]["family_avg"]
+        traffic_src = ("profiles/gemm_ffn_traffic.json: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE per dispatch, "
+                       "scaled by a 64 MiB copy (factors %.4f / %.4f); algorithmic %d B" % (
+                           tj["calibration"]["fetch_factor"], tj["calibration"]["write_factor"],
+                           tj["algorithmic_bytes_per_launch"]["family_avg"]))
     roofline = {"bound": "mfma", "kernel": "gemm_ffn (f16 MFMA, q8_0 dequant after LDS)",
                 "achieved": round(ffn_tf, 2), "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(ffn_tf / PEAK_F16_TFLOPS, 4), "traffic": None,
+                "frac": round(ffn_tf / PEAK_F16_TFLOPS, 4), "traffic": traffic, "traffic_source": traffic_src,
                 "avg_us": round(ffn_avg_s * 1e6, 2), "launches_sampled": int(ffn_n),
                 "launches_in_region": 4 * cfg.n_layers * args.steps,
                 "per_launch": "2*M*D*FF = %.3f GFLOP (M=B*T'=%d, D=%d, FF=%d)" % (
