@@ -20,6 +20,34 @@ __device__ __forceinline__ int xcd_tile(int bid, int total) {
     return x * per + (x < rem ? x : rem) + loc;
 }
 
+// Wave index as a wave-uniform (scalar) value.
+__device__ __forceinline__ int wave_id_uniform() { return __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6); }
+
+// 2-D XCD blocking: the nbm x nbn tile grid is cut into gm row bands x gn
+// column bands (gm * gn = 8), one rectangle per XCD, so an XCD's L2 sees only
+// its band of A rows and its band of weight columns (gn*|A| + gm*|W| bytes
+// over the chip instead of 8*|A| or 8*|W|).  xcd_tile gives each XCD a
+// contiguous range of positions; positions enumerate the rectangles in order,
+// each rectangle M-fastest, so the map is a bijection for any grid size.
+__device__ __forceinline__ void xcd_tile_2d(int bid, int nbm, int nbn, int gm, int& bm, int& bn) {
+    const int gn = 8 / gm;
+    int k = xcd_tile(bid, nbm * nbn);
+    for (int i = 0; i < gm; ++i) {
+        const int r0 = i * nbm / gm, r1 = (i + 1) * nbm / gm;
+        for (int j = 0; j < gn; ++j) {
+            const int c0 = j * nbn / gn, c1 = (j + 1) * nbn / gn;
+            const int sz = (r1 - r0) * (c1 - c0);
+            if (k < sz) {
+                bm = r0 + k % (r1 - r0);
+                bn = c0 + k / (r1 - r0);
+                return;
+            }
+            k -= sz;
+        }
+    }
+    bm = bn = 0;   // unreachable: the rectangles cover the grid
+}
+
 // ---------------------------------------------------------------------------
 // Epilogue for one accumulator element (everything except GLU).
 // ---------------------------------------------------------------------------
@@ -377,15 +405,20 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(GemmParams p) {
 // ===========================================================================
 // f16 path, LDS-DMA + 32x32x16 MFMA (K % 64 == 0; f16 or q8_0 weights).
 //
-// v_mfma_f32_32x32x16_f16 sustains twice the f16 rate of the 16x16x32 form on
-// gfx950, so the main tile family uses it: 4 waves in a 2x2 grid, each wave a
-// (32*TM) x (32*TN) tile of 32x32 MFMA blocks.
+// v_mfma_f32_32x32x16_f16 needs half the operand bytes per FLOP of the
+// 16x16x32 form (each 16-byte A or B fragment feeds 32 columns or rows), which
+// matters because LDS bandwidth, not the matrix core, bounds this kernel: 4
+// waves in a 2x2 grid, each wave a (32*TM) x (32*TN) tile of 32x32 blocks.
 //
 // global_load_lds_dwordx4 moves 16 B per lane straight into LDS (lane L lands
 // at base + 16 L), so a 3-stage LDS ring is kept full with no staging
 // registers: slab kt+2 is in flight while slab kt is multiplied.  Tiles are
 // stored with XOR-swizzled 16 B chunks (the swizzle is applied through each
-// lane's source address) so 8 consecutive fragment rows hit distinct banks.
+// lane's source address).  A 16-byte LDS read is served 16 lanes at a time
+// over 64 banks (256 B): with 128-byte rows two rows share a bank row, so the
+// chunk is XORed with (row >> 1) & 7 and 16 consecutive fragment rows land on
+// 16 distinct bank quads; 64-byte q8_0 rows (four per bank row) use
+// (row >> 2) & 3.
 // q8_0 weights stay int8 in LDS next to their f16 scales and are dequantised
 // after the LDS read.
 //
@@ -396,12 +429,6 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(GemmParams p) {
 // ===========================================================================
 constexpr int DMA_NS = 3;
 
-__device__ __forceinline__ void dma16(const void* src, void* lds_wave_base) {
-    __builtin_amdgcn_global_load_lds(src, (void __attribute__((address_space(3)))*)lds_wave_base, 16, 0, 0);
-}
-__device__ __forceinline__ void dma4(const void* src, void* lds_wave_base) {
-    __builtin_amdgcn_global_load_lds(src, (void __attribute__((address_space(3)))*)lds_wave_base, 4, 0, 0);
-}
 // s_waitcnt with only the vector-memory counter bounded (gfx9 encoding).
 template <int N> __device__ __forceinline__ void wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
@@ -422,50 +449,79 @@ struct DmaCfg {
     static_assert(A_BYTES % 4096 == 0 && B_BYTES % 4096 == 0, "tile must split into 1 KB per wave");
 };
 
-template <int TM, int TN, int WT>
-__device__ __forceinline__ void dma_slab(const GemmParams& p, uint8_t* st, int m0, int n0, int k0, int wid,
-                                         int lane) {
-    typedef DmaCfg<TM, TN, WT> C;
-    const f16* A = (const f16*)p.A;
-#pragma unroll
-    for (int i = 0; i < C::A_INSTR; ++i) {
-        const int blk = wid * C::A_INSTR + i;                 // 1 KB block = 8 rows of 128 B
-        const int slot = blk * 64 + lane;
-        const int row = slot >> 3, c = (slot & 7) ^ (row & 7);
-        const int m = min(m0 + row, p.M - 1);
-        dma16(A + (int64_t)m * p.lda + k0 + 8 * c, st + blk * 1024);
-    }
-    uint8_t* bs = st + C::A_BYTES;
-    if constexpr (WT == GT_Q8_0) {
-        const int8_t* W = (const int8_t*)p.Wq;
-#pragma unroll
-        for (int i = 0; i < C::B_INSTR; ++i) {
-            const int blk = wid * C::B_INSTR + i;             // 16 rows of 64 B
-            const int slot = blk * 64 + lane;
-            const int row = slot >> 2, c = (slot & 3) ^ ((row >> 1) & 3);
-            const int n = min(n0 + row, p.N - 1);
-            dma16(W + (int64_t)n * p.K + k0 + 16 * c, bs + blk * 1024);
-        }
-        const f16* S = (const f16*)p.Ws;
-        uint8_t* ss = bs + C::B_BYTES;
-#pragma unroll
-        for (int i = 0; i < C::S_INSTR; ++i) {
-            const int row = i * 64 + lane;                    // 4 B = the slab's 2 scales of a row
-            const int n = min(n0 + row, p.N - 1);
-            dma4(S + (int64_t)n * (p.K / 32) + k0 / 32, ss + i * 256);
-        }
-    } else {
-        const f16* W = (const f16*)p.Wq;
-#pragma unroll
-        for (int i = 0; i < C::B_INSTR; ++i) {
-            const int blk = wid * C::B_INSTR + i;
-            const int slot = blk * 64 + lane;
-            const int row = slot >> 3, c = (slot & 7) ^ (row & 7);
-            const int n = min(n0 + row, p.N - 1);
-            dma16(W + (int64_t)n * p.K + k0 + 8 * c, bs + blk * 1024);
-        }
-    }
+// Buffer load of 16 (4) bytes per lane straight into LDS: lane L's data lands
+// at lds + 16 L (4 L); soff is wave-uniform.
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds, uint32_t voff, int soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
 }
+__device__ __forceinline__ void lds_dma4(__amdgpu_buffer_rsrc_t r, uint8_t* lds, uint32_t voff, int soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 4, voff, soff, 0, 0);
+}
+
+// Per-lane source offsets of one wave's share of a K slab, computed once: in
+// the K loop a slab is issued with the K offset in a scalar register and the
+// LDS destination in m0, so issuing costs no vector ALU work.  Sources are
+// buffer resources based at the tile's first row (offsets stay 32-bit); rows
+// past M or N are clamped to the last valid one.
+template <int TM, int TN, int WT>
+struct DmaSrc {
+    typedef DmaCfg<TM, TN, WT> C;
+    __amdgpu_buffer_rsrc_t ra, rw, rs;
+    uint32_t va[C::A_INSTR], vb[C::B_INSTR], vs[C::S_INSTR > 0 ? C::S_INSTR : 1];
+    int wid;
+
+    __device__ __forceinline__ void init(const GemmParams& p, int m0, int n0, int wid_, int lane) {
+        wid = wid_;
+        ra = make_rsrc((const f16*)p.A + (int64_t)m0 * p.lda, ((int64_t)(p.M - m0 - 1) * p.lda + p.K) * 2);
+        const int wb = WT == GT_Q8_0 ? 1 : 2;
+        rw = make_rsrc((const uint8_t*)p.Wq + (int64_t)n0 * p.K * wb, (int64_t)(p.N - n0) * p.K * wb);
+#pragma unroll
+        for (int i = 0; i < C::A_INSTR; ++i) {
+            const int slot = (wid * C::A_INSTR + i) * 64 + lane;   // 1 KB block = 8 rows of 128 B
+            const int row = slot >> 3, c = (slot & 7) ^ ((row >> 1) & 7);
+            const int m = min(row, p.M - m0 - 1);
+            va[i] = (uint32_t)(((int64_t)m * p.lda + 8 * c) * 2);
+        }
+        if constexpr (WT == GT_Q8_0) {
+#pragma unroll
+            for (int i = 0; i < C::B_INSTR; ++i) {
+                const int slot = (wid * C::B_INSTR + i) * 64 + lane;   // 16 rows of 64 B
+                const int row = slot >> 2, c = (slot & 3) ^ ((row >> 2) & 3);
+                const int n = min(row, p.N - n0 - 1);
+                vb[i] = (uint32_t)((int64_t)n * p.K + 16 * c);
+            }
+            rs = make_rsrc((const f16*)p.Ws + (int64_t)n0 * (p.K / 32), (int64_t)(p.N - n0) * (p.K / 32) * 2);
+#pragma unroll
+            for (int i = 0; i < C::S_INSTR; ++i) {
+                const int n = min(i * 64 + lane, p.N - n0 - 1);    // 4 B = the slab's 2 scales of a row
+                vs[i] = (uint32_t)(n * (p.K / 32) * 2);
+            }
+        } else {
+            rs = rw;
+#pragma unroll
+            for (int i = 0; i < C::B_INSTR; ++i) {
+                const int slot = (wid * C::B_INSTR + i) * 64 + lane;
+                const int row = slot >> 3, c = (slot & 7) ^ ((row >> 1) & 7);
+                const int n = min(row, p.N - n0 - 1);
+                vb[i] = (uint32_t)(((int64_t)n * p.K + 8 * c) * 2);
+            }
+        }
+    }
+
+    __device__ __forceinline__ void issue(uint8_t* st, int k0) const {
+#pragma unroll
+        for (int i = 0; i < C::A_INSTR; ++i) lds_dma16(ra, st + (wid * C::A_INSTR + i) * 1024, va[i], k0 * 2);
+        uint8_t* bs = st + C::A_BYTES;
+#pragma unroll
+        for (int i = 0; i < C::B_INSTR; ++i)
+            lds_dma16(rw, bs + (wid * C::B_INSTR + i) * 1024, vb[i], WT == GT_Q8_0 ? k0 : k0 * 2);
+        if constexpr (WT == GT_Q8_0) {
+            uint8_t* ss = bs + C::B_BYTES;
+#pragma unroll
+            for (int i = 0; i < C::S_INSTR; ++i) lds_dma4(rs, ss + i * 256, vs[i], (k0 / 32) * 2);
+        }
+    }
+};
 
 template <int TM, int TN, int WT>
 __device__ __forceinline__ void mma32_slab(const uint8_t* st, float16v (&acc)[TM][TN], int wm, int wn,
@@ -479,7 +535,7 @@ __device__ __forceinline__ void mma32_slab(const uint8_t* st, float16v (&acc)[TM
     for (int j = 0; j < TN; ++j) {
         const int row = wn * TN * 32 + 32 * j + r32;
         if constexpr (WT == GT_Q8_0) {
-            const int sw = (row >> 1) & 3;
+            const int sw = (row >> 2) & 3;
             const int4v raw0 = *(const int4v*)(bs + row * 64 + (((2 * q) ^ sw) << 4));
             const int4v raw1 = *(const int4v*)(bs + row * 64 + (((2 * q + 1) ^ sw) << 4));
             const f16 dh = *(const f16*)(bs + C::B_BYTES + row * 4 + q * 2);
@@ -496,7 +552,7 @@ __device__ __forceinline__ void mma32_slab(const uint8_t* st, float16v (&acc)[TM
         } else {
             const uint8_t* rp = bs + row * 128;
 #pragma unroll
-            for (int s2 = 0; s2 < 4; ++s2) bf[j][s2] = *(const half8v*)(rp + (((4 * q + s2) ^ (row & 7)) << 4));
+            for (int s2 = 0; s2 < 4; ++s2) bf[j][s2] = *(const half8v*)(rp + (((4 * q + s2) ^ ((row >> 1) & 7)) << 4));
         }
     }
 #pragma unroll
@@ -504,7 +560,7 @@ __device__ __forceinline__ void mma32_slab(const uint8_t* st, float16v (&acc)[TM
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
             const int row = wm * TM * 32 + 32 * i + r32;
-            const half8v af = *(const half8v*)(st + row * 128 + (((4 * q + s2) ^ (row & 7)) << 4));
+            const half8v af = *(const half8v*)(st + row * 128 + (((4 * q + s2) ^ ((row >> 1) & 7)) << 4));
 #pragma unroll
             for (int j = 0; j < TN; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[j][s2], acc[i][j], 0, 0, 0);
@@ -657,11 +713,12 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmParams p) {
     typedef DmaCfg<TM, TN, WT> C;
     __shared__ __attribute__((aligned(1024))) uint8_t smem[DMA_NS * C::STAGE];
 
-    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wid = wave_id_uniform();
     const int wm = wid >> 1, wn = wid & 1;
     const int nbm = cdiv_dev(p.M, C::BM), nbn = cdiv_dev(p.N, C::BN);
-    const int tile = xcd_tile(blockIdx.x, nbm * nbn);
-    const int bm = tile % nbm, bn = tile / nbm;
+    int bm, bn;
+    xcd_tile_2d(blockIdx.x, nbm, nbn, p.xcd_gm, bm, bn);
     const int m0 = bm * C::BM, n0 = bn * C::BN;
 
     float16v acc[TM][TN];
@@ -671,8 +728,10 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmParams p) {
         for (int j = 0; j < TN; ++j) acc[i][j] = (float16v){};
 
     const int nk = p.K / 64;
-    dma_slab<TM, TN, WT>(p, smem, m0, n0, 0, wid, lane);
-    if (nk > 1) dma_slab<TM, TN, WT>(p, smem + C::STAGE, m0, n0, 64, wid, lane);
+    DmaSrc<TM, TN, WT> src;
+    src.init(p, m0, n0, wid, lane);
+    src.issue(smem, 0);
+    if (nk > 1) src.issue(smem + C::STAGE, 64);
     int st = 0;
     for (int kt = 0; kt < nk; ++kt) {
         // this wave's DMAs for slab kt have landed (slab kt+1 may still be in flight)
@@ -684,7 +743,7 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmParams p) {
         __builtin_amdgcn_s_barrier();
         if (kt + 2 < nk) {
             const int st2 = st + 2 >= DMA_NS ? st + 2 - DMA_NS : st + 2;
-            dma_slab<TM, TN, WT>(p, smem + st2 * C::STAGE, m0, n0, (kt + 2) * 64, wid, lane);
+            src.issue(smem + st2 * C::STAGE, (kt + 2) * 64);
         }
         mma32_slab<TM, TN, WT>(smem + st * C::STAGE, acc, wm, wn, lane);
         st = st + 1 == DMA_NS ? 0 : st + 1;
@@ -697,6 +756,201 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmParams p) {
         __syncthreads();
         float* wsm = (float*)smem + wid * (32 * TM) * ((EPI == EPI_GLU ? 16 * TN : 32 * TN) + 4);
         epilogue32_lds<EPI, TM, TN>(p, acc, wsm, m0 + wm * TM * 32, n0 + wn * TN * 32, lane);
+    }
+}
+
+// ===========================================================================
+// Register-direct K-split GEMM (f16 activations; f16 or q8_0 weights).
+//
+// The 4 waves of a workgroup are KS K-parts x NS = 4/KS column parts.  A wave
+// owns a (32 TM) x (32 TN) output tile over K/KS and streams its operands
+// straight from global memory into registers, PF K-slabs of 64 ahead of the
+// MFMAs: no operand is shared between waves, so the main loop has no LDS
+// traffic and no barriers.  The same K permutation as the LDS kernels
+// (lane half q holds k = 32q + 8s + e in substep s) makes every operand a
+// 16-byte load: 64 contiguous bytes of an activation row, 32 contiguous bytes
+// of a q8_0 weight row (exactly one quant block, one scale).  At the end the
+// KS partial tiles are summed through LDS in a fixed order (deterministic),
+// each wave keeping TM/KS row blocks, and leave through the LDS-staged
+// coalesced epilogue.
+// ===========================================================================
+template <int TM, int TN, int KS, int WT>
+struct SkCfg {
+    static constexpr int NS = 4 / KS;
+    static constexpr int BM = 32 * TM, BN = 32 * TN * NS;
+    static constexpr int KEEP = TM / KS;                           // row blocks a wave finalises
+    static constexpr int WCH = WT == GT_Q8_0 ? 2 : 4;              // 16-byte weight chunks per lane per slab
+    static constexpr int RED_BYTES = NS * KS * KS * KEEP * TN * 4096;
+    static constexpr int EPI_BYTES = 4 * 32 * KEEP * (32 * TN + 4) * 4;
+    static constexpr int LDS_BYTES = RED_BYTES > EPI_BYTES ? RED_BYTES : EPI_BYTES;
+    static_assert(KS == 1 || KS == 2 || KS == 4, "K split");
+    static_assert(TM % KS == 0, "each K part must finalise whole row blocks");
+};
+
+template <int TM, int TN, int KS, int WT, int EPI, int PF, int BLK = 0>
+__global__ __launch_bounds__(256, 1) void gemm_sk_kernel(GemmParams p) {
+    typedef SkCfg<TM, TN, KS, WT> C;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[C::LDS_BYTES];
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int kh = wid / C::NS, nh = wid % C::NS;
+    const int q = lane >> 5, r32 = lane & 31;
+    const int nbm = cdiv_dev(p.M, C::BM), nbn = cdiv_dev(p.N, C::BN);
+    int bm, bn;
+    xcd_tile_2d(blockIdx.x, nbm, nbn, p.xcd_gm, bm, bn);
+    const int m0 = bm * C::BM, nw0 = bn * C::BN + nh * 32 * TN;
+    const int Kw = p.K / KS, kbeg = kh * Kw, nk = Kw / 64;
+
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, ((int64_t)(p.M - 1) * p.lda + p.K) * 2);
+    const int64_t wq_bytes = (int64_t)p.N * p.K * (WT == GT_Q8_0 ? 1 : 2);
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.Wq, wq_bytes);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(WT == GT_Q8_0 ? p.Ws : p.Wq,
+                                                WT == GT_Q8_0 ? (int64_t)p.N * (p.K / 32) * 2 : wq_bytes);
+    uint32_t aoff[TM], woff[TN], soff[TN];
+    if constexpr (BLK) {
+        // fragment-major blocks: (32 rows, 64 k) -> 64 lanes x 64 B, lane-major per 16 B
+        const int nks = p.K / 64;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+            aoff[i] = (uint32_t)((((m0 / 32 + i) * nks + kbeg / 64) * 4096) + lane * 16);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int nb = nw0 / 32 + j;
+            woff[j] = (uint32_t)(((nb * nks + kbeg / 64) * (WT == GT_Q8_0 ? 2048 : 4096)) + lane * 16);
+            soff[j] = (uint32_t)(((nb * nks + kbeg / 64) * 128) + lane * 2);
+        }
+    } else {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        const int m = m0 + 32 * i + r32;
+        aoff[i] = m < p.M ? (uint32_t)(((int64_t)m * p.lda + kbeg + 32 * q) * 2) : OOB;
+    }
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const int n = nw0 + 32 * j + r32;
+        woff[j] = n < p.N ? (uint32_t)(((int64_t)n * p.K + kbeg + 32 * q) * (WT == GT_Q8_0 ? 1 : 2)) : OOB;
+        soff[j] = n < p.N ? (uint32_t)(((int64_t)n * (p.K / 32) + kbeg / 32 + q) * 2) : OOB;
+    }
+    }
+
+    int4v abuf[PF][TM][4];
+    int4v wbuf[PF][TN][C::WCH];
+    uint32_t sbuf[PF][TN];
+    auto load = [&](int u, int kt) {
+        const uint32_t ka = BLK ? (uint32_t)kt * 4096u : (uint32_t)kt * 128u;
+        const uint32_t kw = BLK ? (uint32_t)kt * (WT == GT_Q8_0 ? 2048u : 4096u) : (uint32_t)kt * (WT == GT_Q8_0 ? 64u : 128u);
+        const uint32_t cs = BLK ? 1024u : 16u;                          // stride between a lane's 16-byte chunks
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) abuf[u][i][c] = bload16(ra, aoff[i] + ka + cs * c);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+#pragma unroll
+            for (int c = 0; c < C::WCH; ++c) wbuf[u][j][c] = bload16(rw, woff[j] + kw + cs * c);
+            if constexpr (WT == GT_Q8_0)
+                sbuf[u][j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(
+                    rs, (int)(soff[j] + (uint32_t)kt * (BLK ? 128u : 4u)), 0, 0);
+        }
+    };
+
+    float16v acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = (float16v){};
+
+#pragma unroll
+    for (int u = 0; u < PF; ++u) load(u, u);
+    for (int kt0 = 0; kt0 < nk; kt0 += PF) {
+#pragma unroll
+        for (int u = 0; u < PF; ++u) {
+#pragma unroll
+            for (int s2 = 0; s2 < 4; ++s2) {
+                half8v bf[TN];
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    if constexpr (WT == GT_Q8_0) {
+                        const f16 dh = __builtin_bit_cast(f16, (uint16_t)sbuf[u][j]);
+                        const half2v d2 = {dh, dh};
+                        const int4v raw = wbuf[u][j][s2 >> 1];
+                        half2v h0, h1, h2, h3;
+                        i8x4_to_f16((uint32_t)raw[2 * (s2 & 1)], d2, h0, h1);
+                        i8x4_to_f16((uint32_t)raw[2 * (s2 & 1) + 1], d2, h2, h3);
+                        bf[j] = (half8v){h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
+                    } else {
+                        bf[j] = __builtin_bit_cast(half8v, wbuf[u][j][s2]);
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < TM; ++i) {
+                    const half8v af = __builtin_bit_cast(half8v, abuf[u][i][s2]);
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[j], acc[i][j], 0, 0, 0);
+                }
+            }
+            if (kt0 + u + PF < nk) load(u, kt0 + u + PF);
+        }
+    }
+
+    // ---- fixed-order sum of the KS partial tiles ----
+    float16v fin[C::KEEP][TN];
+    if constexpr (KS == 1) {
+#pragma unroll
+        for (int ii = 0; ii < C::KEEP; ++ii)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) fin[ii][j] = acc[ii][j];
+    } else {
+        // slot (nh, src, dst) holds src's partial of dst's row blocks, lane-major
+        // 16-byte chunks (conflict-free writes and reads)
+        float4v* red = (float4v*)smem;
+        auto slot = [&](int src, int dst, int ii, int j, int g) {
+            return ((((nh * KS + src) * KS + dst) * C::KEEP + ii) * TN + j) * 4 * 64 + g * 64 + lane;
+        };
+#pragma unroll
+        for (int dst = 0; dst < KS; ++dst) {
+            if (dst == kh) continue;
+#pragma unroll
+            for (int ii = 0; ii < C::KEEP; ++ii)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const float16v& a = acc[dst * C::KEEP + ii][j];
+                        red[slot(kh, dst, ii, j, g)] = (float4v){a[4 * g], a[4 * g + 1], a[4 * g + 2], a[4 * g + 3]};
+                    }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int ii = 0; ii < C::KEEP; ++ii)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                float16v sum = {};
+#pragma unroll
+                for (int src = 0; src < KS; ++src) {
+                    if (src == kh) {
+                        sum += acc[kh * C::KEEP + ii][j];
+                    } else {
+#pragma unroll
+                        for (int g = 0; g < 4; ++g) {
+                            const float4v v = red[slot(src, kh, ii, j, g)];
+                            sum[4 * g] += v[0];
+                            sum[4 * g + 1] += v[1];
+                            sum[4 * g + 2] += v[2];
+                            sum[4 * g + 3] += v[3];
+                        }
+                    }
+                }
+                fin[ii][j] = sum;
+            }
+        __syncthreads();   // the reduction slots are reused by the epilogue staging below
+    }
+    const int mw = m0 + kh * C::KEEP * 32;
+    if constexpr (EPI == EPI_RELU_TR || EPI == EPI_RELU2_F32) {
+        epilogue32<EPI, f16, C::KEEP, TN>(p, fin, mw, nw0, lane);
+    } else {
+        float* wsm = (float*)smem + wid * (32 * C::KEEP) * ((EPI == EPI_GLU ? 16 * TN : 32 * TN) + 4);
+        epilogue32_lds<EPI, C::KEEP, TN>(p, fin, wsm, mw, nw0, lane);
     }
 }
 
@@ -965,13 +1219,35 @@ static void run_f32(const GemmParams& p, hipStream_t s) {
     default: throw std::invalid_argument("gemm: bad epilogue");                 \
     }
 
+// Row/column band split of the tile grid over the 8 XCDs that minimises the
+// L2-miss bytes gn*|A| + gm*|W| (each XCD reads its A band and its W band).
+static int choose_xcd_gm(const GemmParams& p, int WT, int BM, int BN) {
+    const int nbm = cdiv(p.M, BM), nbn = cdiv(p.N, BN);
+    const double a_bytes = (double)p.M * p.K * 2;
+    const double w_bytes = (double)p.N * p.K * (WT == GT_Q8_0 ? 34.0 / 32 : 2.0);
+    int best = 1;
+    double best_cost = 1e300;
+    for (int gm : {1, 2, 4, 8}) {
+        const int gn = 8 / gm;
+        if (gm > nbm || gn > nbn) continue;
+        const double cost = gn * a_bytes + gm * w_bytes;
+        if (cost < best_cost) {
+            best_cost = cost;
+            best = gm;
+        }
+    }
+    return best_cost < 1e300 ? best : 1;
+}
+
 template <int TM, int TN, int WT, int EPI>
 static void run_dma(const GemmParams& p, hipStream_t s) {
     if constexpr (EPI == EPI_GLU && TN % 2 != 0) {
         throw std::logic_error("gemm: GLU epilogue dispatched to a 64-wide tile");
     } else {
         const int tiles = cdiv(p.M, 64 * TM) * cdiv(p.N, 64 * TN);
-        launch((gemm_dma_kernel<TM, TN, WT, EPI>), dim3(tiles), dim3(256), 0, s, p);
+        GemmParams q = p;
+        q.xcd_gm = choose_xcd_gm(p, WT, 64 * TM, 64 * TN);
+        launch((gemm_dma_kernel<TM, TN, WT, EPI>), dim3(tiles), dim3(256), 0, s, q);
         PKX_LAUNCH_CHECK();
     }
 }

@@ -37,6 +37,7 @@ struct GemmParams {
     int T = 1;
     int trF = 1;               // EPI_RELU_TR: rows are (b, t, f) with f fastest, F' = trF
     int M = 0, N = 0, K = 0;
+    int xcd_gm = 1;            // tile grid split over the 8 XCDs: xcd_gm row bands x (8 / xcd_gm) column bands
 };
 
 // Launch one GEMM.  prec selects the activation type (f16: MFMA 16x16x32 f16
