@@ -290,6 +290,105 @@ __global__ __launch_bounds__(256) void sub_dwconv_kernel(const T* in, const int*
     }
 }
 
+// First two subsampling stages fused: conv0 (1 -> C, 3x3, stride 2, pad 1)
+// + bias + ReLU, the stage mask on its output rows, then the depthwise 3x3
+// stride-2 conv + bias, written as [B][T2][F2][C].  The conv0 map (the
+// largest tensor of the encoder: B x T/2 x F/2 x C) never leaves registers.
+// A block takes one item and two output rows t2, t2+1; those need conv0 rows
+// t1 = 2 t2 - 1 .. 2 t2 + 3 and mel rows 4 t2 - 3 .. 4 t2 + 7, which are
+// staged in LDS (zero-padded, masked at t >= valid0).  One thread per channel
+// walks the feature axis with a sliding 3-column window of conv0 values, so
+// each conv0 value is computed once per block (the row shared by the two
+// output rows included).
+template <typename T>
+__global__ __launch_bounds__(256) void sub_stage1_kernel(const float* mel, const int* valid0, const int* valid1,
+                                                         const float* w0, const float* b0, const float* w2,
+                                                         const float* b2, T* out, int F, int Tn, int C, int T1,
+                                                         int F1, int T2, int F2) {
+    extern __shared__ float mp[];                 // [11][4 F2 + 5]: mel columns -1 .. 4 F2 + 3
+    const int b = blockIdx.y, t2a = 2 * blockIdx.x;
+    const int FP = 4 * F2 + 5;
+    const int v0 = valid0 ? valid0[b] : Tn;
+    const int v1 = valid1 ? valid1[b] : T1;
+    for (int idx = threadIdx.x; idx < 11 * FP; idx += blockDim.x) {
+        const int j = idx / FP, fi = idx % FP - 1;
+        const int t = 4 * t2a - 3 + j;
+        float v = 0.f;
+        if (t >= 0 && t < Tn && t < v0 && fi >= 0 && fi < F) v = mel[((int64_t)b * F + fi) * Tn + t];
+        mp[idx] = v;
+    }
+    __syncthreads();
+    bool rowok[5];
+#pragma unroll
+    for (int r = 0; r < 5; ++r) {
+        const int t1 = 2 * t2a - 1 + r;
+        rowok[r] = t1 >= 0 && t1 < T1 && t1 < v1;
+    }
+    const bool has_b = t2a + 1 < T2;
+    for (int c = threadIdx.x; c < C; c += blockDim.x) {
+        float k0[9], k2[9];
+#pragma unroll
+        for (int e = 0; e < 9; ++e) {
+            k0[e] = w0[c * 9 + e];
+            k2[e] = w2[c * 9 + e];
+        }
+        const float bc0 = b0[c], bc2 = b2[c];
+        float prev[5];
+#pragma unroll
+        for (int r = 0; r < 5; ++r) prev[r] = 0.f;    // conv0 column f1 = -1 is padding
+        for (int f2 = 0; f2 < F2; ++f2) {
+            // mel columns 4 f2 - 1 .. 4 f2 + 3 (LDS columns 4 f2 .. 4 f2 + 4) of the 11 rows
+            float m[11][5];
+#pragma unroll
+            for (int j = 0; j < 11; ++j)
+#pragma unroll
+                for (int q = 0; q < 5; ++q) m[j][q] = mp[j * FP + 4 * f2 + q];
+            float ca[5], cb[5];                       // conv0 columns f1 = 2 f2, 2 f2 + 1
+            const bool fa = 2 * f2 < F1, fb = 2 * f2 + 1 < F1;
+#pragma unroll
+            for (int r = 0; r < 5; ++r) {
+                float sa = bc0, sb = bc0;
+#pragma unroll
+                for (int kh = 0; kh < 3; ++kh)
+#pragma unroll
+                    for (int kw = 0; kw < 3; ++kw) {
+                        sa += k0[kh * 3 + kw] * m[2 * r + kh][kw];
+                        sb += k0[kh * 3 + kw] * m[2 * r + kh][2 + kw];
+                    }
+                ca[r] = (rowok[r] && fa && sa > 0.f) ? sa : 0.f;
+                cb[r] = (rowok[r] && fb && sb > 0.f) ? sb : 0.f;
+            }
+            float oa = bc2, ob = bc2;
+#pragma unroll
+            for (int kh = 0; kh < 3; ++kh) {
+                oa += k2[kh * 3] * prev[kh] + k2[kh * 3 + 1] * ca[kh] + k2[kh * 3 + 2] * cb[kh];
+                ob += k2[kh * 3] * prev[2 + kh] + k2[kh * 3 + 1] * ca[2 + kh] + k2[kh * 3 + 2] * cb[2 + kh];
+            }
+            out[(((int64_t)b * T2 + t2a) * F2 + f2) * C + c] = to_act<T>(oa);
+            if (has_b) out[(((int64_t)b * T2 + t2a + 1) * F2 + f2) * C + c] = to_act<T>(ob);
+#pragma unroll
+            for (int r = 0; r < 5; ++r) prev[r] = cb[r];
+        }
+    }
+}
+
+void launch_sub_stage1(Precision prec, const float* mel, const int* valid0, const int* valid1, const float* w0,
+                       const float* b0, const float* w2, const float* b2, void* out, int B, int F, int T, int C,
+                       hipStream_t s) {
+    const int T1 = (T - 1) / 2 + 1, F1 = (F - 1) / 2 + 1;
+    const int T2 = (T1 - 1) / 2 + 1, F2 = (F1 - 1) / 2 + 1;
+    const dim3 grid(cdiv(T2, 2), B);
+    const int bs = C >= 256 ? 256 : ((C + 63) / 64) * 64;
+    const uint32_t shm = 11u * (uint32_t)(4 * F2 + 5) * 4u;   // 4 F2 + 5 >= F + 2 covers the zero padding
+    if (prec == PREC_F16)
+        launch(sub_stage1_kernel<f16>, grid, dim3(bs), shm, s, mel, valid0, valid1, w0, b0, w2, b2, (f16*)out, F, T,
+               C, T1, F1, T2, F2);
+    else
+        launch(sub_stage1_kernel<float>, grid, dim3(bs), shm, s, mel, valid0, valid1, w0, b0, w2, b2, (float*)out,
+               F, T, C, T1, F1, T2, F2);
+    PKX_LAUNCH_CHECK();
+}
+
 void launch_sub_conv0(Precision prec, const float* mel, const int* valid0, const float* w,
                       const float* bias, void* out, int B, int F, int T, int C, hipStream_t s) {
     const int T1 = (T - 1) / 2 + 1, F1 = (F - 1) / 2 + 1;

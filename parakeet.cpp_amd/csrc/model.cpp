@@ -77,7 +77,7 @@ struct Buf {
 };
 
 struct Model::Ws {
-    Buf a1, a2, a2p, a3, flat;          // subsampling maps
+    Buf a2, a2p, a3, flat;              // subsampling maps
     Buf h, u, qkv, g, pe, p, xin, tmp;  // layer activations
     Buf logits, pp;                     // heads
     int* d_valid = nullptr;             // 4 x Bcap ints: v0, v1, v2, vout
@@ -112,7 +112,7 @@ Model::~Model() {
     auto fr = [](void* p) { if (p) (void)hipFree(p); };
     for (void* p : allocs_) fr(p);
     if (ws_) {
-        for (Buf* b : {&ws_->a1, &ws_->a2, &ws_->a2p, &ws_->a3, &ws_->flat, &ws_->h, &ws_->u, &ws_->qkv,
+        for (Buf* b : {&ws_->a2, &ws_->a2p, &ws_->a3, &ws_->flat, &ws_->h, &ws_->u, &ws_->qkv,
                        &ws_->g, &ws_->pe, &ws_->p, &ws_->xin, &ws_->tmp, &ws_->logits, &ws_->pp})
             fr(b->p);
         fr(ws_->d_valid);
@@ -614,7 +614,7 @@ void Model::ensure_ws(int B, int T_max) {
     const int F1 = (c.n_mels - 1) / 2 + 1, F2 = (F1 - 1) / 2 + 1, F3 = (F2 - 1) / 2 + 1;
     const size_t C = c.sub_channels, D = c.d_model, M = (size_t)B * T3, P = 2 * (size_t)T3 - 1;
     Ws& w = *ws_;
-    grow(w.a1, (size_t)B * T1 * F1 * C * as);
+    // (the conv0 map, B x T1 x F1 x C, is never materialised: see launch_sub_stage1)
     grow(w.a2, (size_t)B * T2 * F2 * C * as);
     grow(w.a2p, (size_t)B * T2 * F2 * C * as);
     grow(w.a3, (size_t)B * T3 * F3 * C * as);
@@ -690,8 +690,8 @@ int Model::subsampling_forward(const float* mel, int B, int T_max, const int* va
     const int* dv = w.d_valid;
     const int Bc = w.Bcap;
     mark(KF_SUBSAMPLING, true);
-    launch_sub_conv0(prec_, mel, stage_masks ? dv : nullptr, sub_.w0, sub_.b0, w.a1.p, B, F, T_max, C, s);
-    launch_sub_dwconv(prec_, w.a1.p, stage_masks ? dv + Bc : nullptr, sub_.w2, sub_.b2, w.a2.p, B, T1, F1, C, s);
+    launch_sub_stage1(prec_, mel, stage_masks ? dv : nullptr, stage_masks ? dv + Bc : nullptr, sub_.w0, sub_.b0,
+                      sub_.w2, sub_.b2, w.a2.p, B, F, T_max, C, s);
     gemm(sub_.w3, EPI_RELU, w.a2.p, C, (int64_t)B * T2 * F2, sub_.b3, w.a2p.p, C, 1.f, nullptr, 1, s, prec_, -1);
     launch_sub_dwconv(prec_, w.a2p.p, stage_masks ? dv + 2 * Bc : nullptr, sub_.w5, sub_.b5, w.a3.p, B, T2, F2, C, s);
     gemm(sub_.w6, EPI_RELU_TR, w.a3.p, C, (int64_t)B * T3 * F3, sub_.b6, w.flat.p, 0, 1.f, dv + 3 * Bc, T3, s,
