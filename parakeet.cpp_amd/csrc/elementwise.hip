@@ -220,73 +220,51 @@ void launch_dwconv_bn_silu(Precision prec, const void* in, void* out, const floa
 // ---------------------------------------------------------------------------
 // Subsampling convs (H = time, W = feature; ggml conv layout [W,H,C,N]).
 // ---------------------------------------------------------------------------
-constexpr int SUB_FS = 8;  // output feature columns per block
-
-template <typename T>
-__global__ __launch_bounds__(256) void sub_conv0_kernel(const float* mel, const int* valid0,
-                                                        const float* w, const float* bias, T* out,
-                                                        int F, int Tn, int C, int F1, int T1) {
-    __shared__ float patch[3][2 * SUB_FS + 1];
-    const int f1s = blockIdx.x * SUB_FS, t1 = blockIdx.y, b = blockIdx.z;
-    const int vlim = valid0 ? valid0[b] : Tn;
-    for (int idx = threadIdx.x; idx < 3 * (2 * SUB_FS + 1); idx += blockDim.x) {
-        const int kh = idx / (2 * SUB_FS + 1), kw = idx % (2 * SUB_FS + 1);
-        const int ti = 2 * t1 - 1 + kh, fi = 2 * f1s - 1 + kw;
-        float v = 0.f;
-        if (ti >= 0 && ti < Tn && ti < vlim && fi >= 0 && fi < F) v = mel[((int64_t)b * F + fi) * Tn + ti];
-        patch[kh][kw] = v;
-    }
-    __syncthreads();
-    for (int c = threadIdx.x; c < C; c += blockDim.x) {
-        float wk[9];
-#pragma unroll
-        for (int e = 0; e < 9; ++e) wk[e] = w[c * 9 + e];
-        const float bc = bias[c];
-#pragma unroll
-        for (int fo = 0; fo < SUB_FS; ++fo) {
-            const int f1 = f1s + fo;
-            if (f1 >= F1) break;
-            float acc = 0.f;
-#pragma unroll
-            for (int kh = 0; kh < 3; ++kh)
-#pragma unroll
-                for (int kw = 0; kw < 3; ++kw) acc += wk[kh * 3 + kw] * patch[kh][2 * fo + kw];
-            const float y = acc + bc;
-            out[(((int64_t)b * T1 + t1) * F1 + f1) * C + c] = to_act<T>(y > 0.f ? y : 0.f);
-        }
-    }
-}
-
-template <typename T> __device__ __forceinline__ float ld_act(const T* p) { return (float)*p; }
-
+// Depthwise 3x3 stride-2 conv (+bias) on a channels-last map [B][Ti][Fi][C],
+// rows t >= vmask[b] read as zero.  A thread owns 8 channels (16-byte loads
+// and stores, 32 threads cover 256 channels contiguously) and a set of output
+// columns of one output row; the 3x3 window loads hit L1/L2 for the 2.25x
+// overlap between neighbouring outputs.
 template <typename T>
 __global__ __launch_bounds__(256) void sub_dwconv_kernel(const T* in, const int* vmask, const float* w,
                                                          const float* bias, T* out, int Ti, int Fi,
                                                          int C, int To, int Fo) {
-    const int fos = blockIdx.x * SUB_FS, to = blockIdx.y, b = blockIdx.z;
+    constexpr int V = 16 / sizeof(T);                  // channels per thread
+    const int to = blockIdx.x, b = blockIdx.y;
+    const int groups = C / V, lanes_f = blockDim.x / groups;
+    const int g = threadIdx.x % groups, c0 = g * V;
+    if ((int)threadIdx.x >= groups * lanes_f) return;
     const int vlim = vmask ? vmask[b] : Ti;
-    for (int c = threadIdx.x; c < C; c += blockDim.x) {
-        float wk[9];
+    float wk[V][9], bb[V];
 #pragma unroll
-        for (int e = 0; e < 9; ++e) wk[e] = w[c * 9 + e];
-        const float bc = bias[c];
-        for (int fo = 0; fo < SUB_FS; ++fo) {
-            const int f = fos + fo;
-            if (f >= Fo) break;
-            float acc = 0.f;
+    for (int e = 0; e < V; ++e) {
+        bb[e] = bias[c0 + e];
 #pragma unroll
-            for (int kh = 0; kh < 3; ++kh) {
-                const int ti = 2 * to - 1 + kh;
-                if (ti < 0 || ti >= Ti || ti >= vlim) continue;
+        for (int q = 0; q < 9; ++q) wk[e][q] = w[(c0 + e) * 9 + q];
+    }
+    for (int fo = threadIdx.x / groups; fo < Fo; fo += lanes_f) {
+        float acc[V];
 #pragma unroll
-                for (int kw = 0; kw < 3; ++kw) {
-                    const int fi = 2 * f - 1 + kw;
-                    if (fi < 0 || fi >= Fi) continue;
-                    acc += wk[kh * 3 + kw] * ld_act<T>(in + (((int64_t)b * Ti + ti) * Fi + fi) * C + c);
-                }
+        for (int e = 0; e < V; ++e) acc[e] = bb[e];
+#pragma unroll
+        for (int kh = 0; kh < 3; ++kh) {
+            const int ti = 2 * to - 1 + kh;
+            if (ti < 0 || ti >= Ti || ti >= vlim) continue;
+#pragma unroll
+            for (int kw = 0; kw < 3; ++kw) {
+                const int fi = 2 * fo - 1 + kw;
+                if (fi < 0 || fi >= Fi) continue;
+                const T* src = in + (((int64_t)b * Ti + ti) * Fi + fi) * C + c0;
+                T x[V];
+                *(int4v*)x = *(const int4v*)src;
+#pragma unroll
+                for (int e = 0; e < V; ++e) acc[e] += wk[e][kh * 3 + kw] * (float)x[e];
             }
-            out[(((int64_t)b * To + to) * Fo + f) * C + c] = to_act<T>(acc + bc);
         }
+        T y[V];
+#pragma unroll
+        for (int e = 0; e < V; ++e) y[e] = to_act<T>(acc[e]);
+        *(int4v*)(out + (((int64_t)b * To + to) * Fo + fo) * C + c0) = *(const int4v*)y;
     }
 }
 
@@ -389,23 +367,12 @@ void launch_sub_stage1(Precision prec, const float* mel, const int* valid0, cons
     PKX_LAUNCH_CHECK();
 }
 
-void launch_sub_conv0(Precision prec, const float* mel, const int* valid0, const float* w,
-                      const float* bias, void* out, int B, int F, int T, int C, hipStream_t s) {
-    const int T1 = (T - 1) / 2 + 1, F1 = (F - 1) / 2 + 1;
-    const dim3 grid(cdiv(F1, SUB_FS), T1, B);
-    const int bs = C >= 256 ? 256 : ((C + 63) / 64) * 64;
-    if (prec == PREC_F16)
-        launch(sub_conv0_kernel<f16>, grid, dim3(bs), 0, s, mel, valid0, w, bias, (f16*)out, F, T, C, F1, T1);
-    else
-        launch(sub_conv0_kernel<float>, grid, dim3(bs), 0, s, mel, valid0, w, bias, (float*)out, F, T, C, F1, T1);
-    PKX_LAUNCH_CHECK();
-}
-
 void launch_sub_dwconv(Precision prec, const void* in, const int* vmask, const float* w,
                        const float* bias, void* out, int B, int Ti, int Fi, int C, hipStream_t s) {
     const int To = (Ti - 1) / 2 + 1, Fo = (Fi - 1) / 2 + 1;
-    const dim3 grid(cdiv(Fo, SUB_FS), To, B);
-    const int bs = C >= 256 ? 256 : ((C + 63) / 64) * 64;
+    require(C % 8 == 0 && C <= 2048, "subsampling: channels must be a multiple of 8 and at most 2048");
+    const dim3 grid(To, B);
+    const int bs = 256;
     if (prec == PREC_F16)
         launch(sub_dwconv_kernel<f16>, grid, dim3(bs), 0, s, (const f16*)in, vmask, w, bias, (f16*)out, Ti, Fi, C, To, Fo);
     else

@@ -31,16 +31,13 @@ void launch_dwconv_bn_silu(Precision prec, const void* in, void* out, const floa
                            const float* dw_bias, const float* bn_scale, const float* bn_shift,
                            int B, int T, int D, int K, hipStream_t s);
 
-// Subsampling conv.0 (subsampling.cpp:143-157): Conv2d(1->C, 3x3, s2, p1) + bias
-// + ReLU over mel [B][F][T] (f32), time frames t >= valid0[b] read as zero when
-// valid0 != nullptr; output channels-last [B][T1][F1][C] activation type.
-// conv0 + ReLU + stage mask + first depthwise conv, fused (no conv0 map in HBM).
+// Subsampling conv.0 (subsampling.cpp:143-157: Conv2d(1->C, 3x3, s2, p1) + bias
+// + ReLU over mel [B][F][T] f32, frames t >= valid0[b] zero when valid0 is set),
+// the stage mask on its rows (t1 >= valid1[b] zero) and the first depthwise
+// conv (subsampling.cpp:168-184), fused; output channels-last [B][T2][F2][C].
 void launch_sub_stage1(Precision prec, const float* mel, const int* valid0, const int* valid1, const float* w0,
                        const float* b0, const float* w2, const float* b2, void* out, int B, int F, int T, int C,
                        hipStream_t s);
-void launch_sub_conv0(Precision prec, const float* mel, const int* valid0, const float* w,
-                      const float* bias, void* out, int B, int F, int T, int C, hipStream_t s);
-
 // Subsampling depthwise 3x3 s2 p1 + bias (subsampling.cpp:168-184), channels-last,
 // input time rows t >= vmask[b] read as zero when vmask != nullptr.
 void launch_sub_dwconv(Precision prec, const void* in, const int* vmask, const float* w,

@@ -618,6 +618,58 @@ __device__ __forceinline__ void epilogue32(const GemmParams& p, float16v (&acc)[
 // stores; the residual update reads and writes the f32 stream in 16-byte
 // vectors too.  The accumulator layout alone would give 2- or 4-byte stores
 // scattered over 8 rows per instruction.
+// Coalesced form of the channel-major flatten epilogue (EPI_RELU_TR): GEMM row
+// m = (b, t, f) with f fastest, column n = channel; output row (b, t) holds
+// n * F + f.  A wave's rows cover whole (b, t) groups when 32 TM is a
+// multiple of F, and then its 32 TN columns form one contiguous run of
+// 32 TN * F outputs per (b, t): staged in LDS as [bt][f][n] (row pitch 32 TN
+// + 1 keeps both the staging writes and the gathering reads conflict-free)
+// and written with 16-byte stores.
+template <int TM, int TN>
+__device__ __forceinline__ void epilogue32_relu_tr(const GemmParams& p, float16v (&acc)[TM][TN], float* wsm,
+                                                   int mw, int nw, int lane) {
+    constexpr int WR = 32 * TM, WC = 32 * TN, LDN = WC + 1;
+    const int F = p.trF, nbt = WR / F;
+    const int lr = 4 * (lane >> 5), lc = lane & 31;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int n = nw + 32 * j + lc;
+            const float bb = p.bias ? p.bias[min(n, p.N - 1)] : 0.f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int rr = 32 * i + 8 * (r >> 2) + lr + (r & 3);
+                const float v = acc[i][j][r] + bb;
+                wsm[rr * LDN + 32 * j + lc] = v > 0.f ? v : 0.f;   // rr = bt_local * F + f
+            }
+        }
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+    const int run = WC * F;                       // outputs per (b, t) in this wave
+    for (int c = lane; c < nbt * (run / 8); c += 64) {
+        const int btl = c / (run / 8), e0 = (c % (run / 8)) * 8;
+        const int m_first = mw + btl * F;
+        if (m_first >= p.M) continue;
+        const int bt = m_first / F, t = bt % p.T, b = bt / p.T;
+        const bool dead = p.valid && t >= p.valid[b];
+        f16* dst = (f16*)p.Y + ((int64_t)bt * p.N + nw) * F + e0;
+        half8v h;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int idx = e0 + e, nl = idx / F, f = idx - nl * F;
+            h[e] = dead ? (f16)0.f : (f16)wsm[(btl * F + f) * LDN + nl];
+        }
+        if (nw + (e0 + 7) / F < p.N) {
+            *(half8v*)dst = h;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if (nw + (e0 + e) / F < p.N) dst[e] = h[e];
+        }
+    }
+}
+
 template <int EPI, int TM, int TN>
 __device__ __forceinline__ void epilogue32_lds(const GemmParams& p, float16v (&acc)[TM][TN], float* wsm,
                                                int mw, int nw, int lane) {
@@ -748,8 +800,17 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmParams p) {
         mma32_slab<TM, TN, WT>(smem + st * C::STAGE, acc, wm, wn, lane);
         st = st + 1 == DMA_NS ? 0 : st + 1;
     }
-    if constexpr (EPI == EPI_RELU_TR || EPI == EPI_RELU2_F32) {
+    if constexpr (EPI == EPI_RELU2_F32) {
         epilogue32<EPI, f16, TM, TN>(p, acc, m0 + wm * TM * 32, n0 + wn * TN * 32, lane);
+    } else if constexpr (EPI == EPI_RELU_TR) {
+        if ((32 * TM) % p.trF == 0 && (32 * TN * p.trF) % 8 == 0 && p.N % 8 == 0) {
+            static_assert(4 * 32 * TM * (32 * TN + 1) * 4 <= DMA_NS * C::STAGE, "epilogue staging exceeds LDS ring");
+            __syncthreads();
+            float* wsm = (float*)smem + wid * (32 * TM) * (32 * TN + 1);
+            epilogue32_relu_tr<TM, TN>(p, acc, wsm, m0 + wm * TM * 32, n0 + wn * TN * 32, lane);
+        } else {
+            epilogue32<EPI, f16, TM, TN>(p, acc, m0 + wm * TM * 32, n0 + wn * TN * 32, lane);
+        }
     } else {
         // the LDS ring is free once every wave has finished its last slab
         static_assert(4 * 32 * TM * (32 * TN + 4) * 4 <= DMA_NS * C::STAGE, "epilogue staging exceeds LDS ring");
