@@ -8,9 +8,11 @@ namespace pkx {
 // ---------------------------------------------------------------------------
 // LayerNorm: one wave per row, the row held in registers (NV float4 per lane).
 // ---------------------------------------------------------------------------
+// gamma/beta are loaded by the caller before the row statistics are formed,
+// so their memory latency overlaps the reductions instead of following them.
 template <int NV>
-__device__ __forceinline__ void ln_row(float4v (&v)[NV], int lane, int D, const float* g,
-                                       const float* b, float eps) {
+__device__ __forceinline__ void ln_row(float4v (&v)[NV], int lane, int D, const float4v (&gg)[NV],
+                                       const float4v (&bb)[NV], float eps) {
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
@@ -33,14 +35,17 @@ __device__ __forceinline__ void ln_row(float4v (&v)[NV], int lane, int D, const 
     }
     const float rs = 1.0f / sqrtf(wave_sum(s2) / (float)D + eps);
 #pragma unroll
+    for (int i = 0; i < NV; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[i][e] = (v[i][e] * rs) * gg[i][e] + bb[i][e];
+}
+
+template <int NV>
+__device__ __forceinline__ void ld_row4(float4v (&v)[NV], const float* src, int lane, int D) {
+#pragma unroll
     for (int i = 0; i < NV; ++i) {
         const int c = (lane + 64 * i) * 4;
-        if (c < D) {
-            const float4v gg = *(const float4v*)(g + c);
-            const float4v bb = *(const float4v*)(b + c);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) v[i][e] = (v[i][e] * rs) * gg[e] + bb[e];
-        }
+        v[i] = c < D ? *(const float4v*)(src + c) : (float4v){0.f, 0.f, 0.f, 0.f};
     }
 }
 
@@ -57,14 +62,15 @@ __global__ __launch_bounds__(256) void layernorm_kernel(LnParams p) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= p.M) return;
-    const float* xr = p.x + row * p.D;
-    float4v v[NV];
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        const int c = (lane + 64 * i) * 4;
-        v[i] = c < p.D ? *(const float4v*)(xr + c) : (float4v){0.f, 0.f, 0.f, 0.f};
+    float4v v[NV], g1[NV], b1[NV], g2[MODE == 1 ? NV : 1], b2[MODE == 1 ? NV : 1];
+    ld_row4<NV>(v, p.x + row * p.D, lane, p.D);
+    ld_row4<NV>(g1, p.g, lane, p.D);
+    ld_row4<NV>(b1, p.b, lane, p.D);
+    if constexpr (MODE == 1) {
+        ld_row4<NV>(g2, p.g2, lane, p.D);
+        ld_row4<NV>(b2, p.b2, lane, p.D);
     }
-    ln_row<NV>(v, lane, p.D, p.g, p.b, p.eps);
+    ln_row<NV>(v, lane, p.D, g1, b1, p.eps);
     if constexpr (MODE != 0) {
         float* yr = p.y_f32 + row * p.D;
 #pragma unroll
@@ -73,7 +79,7 @@ __global__ __launch_bounds__(256) void layernorm_kernel(LnParams p) {
             if (c < p.D) *(float4v*)(yr + c) = v[i];
         }
         if constexpr (MODE == 2) return;
-        ln_row<NV>(v, lane, p.D, p.g2, p.b2, p.eps);
+        else ln_row<NV>(v, lane, p.D, g2, b2, p.eps);
     }
     OutT* yo = (OutT*)p.y + row * p.D;
 #pragma unroll
@@ -115,30 +121,15 @@ void launch_layernorm(Precision prec, const LnParams& p, hipStream_t s) {
 
 // ---------------------------------------------------------------------------
 // Depthwise conv1d + bias + folded BatchNorm + SiLU, sliding window over time
-// in registers; VEC channels per thread (half2 for f16), TT frames per block.
+// in registers: a thread owns 16 bytes of channels (8 f16 / 4 f32) and TT
+// output frames, loading TT + K - 1 input frames once.
 // ---------------------------------------------------------------------------
-template <typename T, int VEC> struct Vec;
-template <> struct Vec<float, 1> {
-    static __device__ __forceinline__ void ld(const float* p, float* o) { o[0] = *p; }
-    static __device__ __forceinline__ void st(float* p, const float* o) { *p = o[0]; }
-};
-template <> struct Vec<f16, 2> {
-    static __device__ __forceinline__ void ld(const f16* p, float* o) {
-        const half2v h = *(const half2v*)p;
-        o[0] = (float)h[0];
-        o[1] = (float)h[1];
-    }
-    static __device__ __forceinline__ void st(f16* p, const float* o) {
-        half2v h = {(f16)o[0], (f16)o[1]};
-        *(half2v*)p = h;
-    }
-};
-
-template <typename T, int VEC, int K, int TT>
+template <typename T, int K, int TT>
 __global__ __launch_bounds__(256) void dwconv_bn_silu_kernel(const T* in, T* out, const float* w,
                                                              const float* dwb, const float* sc,
                                                              const float* sh, int Tn, int D) {
-    const int c0 = (blockIdx.x * 256 + threadIdx.x) * VEC;
+    constexpr int VEC = 16 / sizeof(T);
+    const int c0 = (blockIdx.x * blockDim.x + threadIdx.x) * VEC;
     if (c0 >= D) return;
     const int t0 = blockIdx.y * TT, b = blockIdx.z;
     constexpr int PAD = (K - 1) / 2, NW = TT + K - 1;
@@ -147,12 +138,15 @@ __global__ __launch_bounds__(256) void dwconv_bn_silu_kernel(const T* in, T* out
 #pragma unroll
     for (int r = 0; r < NW; ++r) {
         const int t = t0 - PAD + r;
+        T x[VEC];
         if (t >= 0 && t < Tn) {
-            Vec<T, VEC>::ld(base + (int64_t)t * D, win[r]);
+            *(int4v*)x = *(const int4v*)(base + (int64_t)t * D);
         } else {
 #pragma unroll
-            for (int e = 0; e < VEC; ++e) win[r][e] = 0.f;
+            for (int e = 0; e < VEC; ++e) x[e] = (T)0.f;
         }
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) win[r][e] = (float)x[e];
     }
     float wk[VEC][K], bias[VEC], scale[VEC], shift[VEC];
 #pragma unroll
@@ -168,38 +162,42 @@ __global__ __launch_bounds__(256) void dwconv_bn_silu_kernel(const T* in, T* out
     for (int tt = 0; tt < TT; ++tt) {
         const int t = t0 + tt;
         if (t >= Tn) break;
-        float o[VEC];
+        T o[VEC];
 #pragma unroll
         for (int e = 0; e < VEC; ++e) {
             float acc = 0.f;
 #pragma unroll
             for (int k = 0; k < K; ++k) acc += wk[e][k] * win[tt + k][e];
             const float y = (acc + bias[e]) * scale[e] + shift[e];
-            o[e] = silu_dev(y);
+            o[e] = to_act<T>(silu_dev(y));
         }
-        Vec<T, VEC>::st(ob + (int64_t)t * D, o);
+        *(int4v*)(ob + (int64_t)t * D) = *(const int4v*)o;
     }
 }
 
-template <typename ET, int VEC, int K>
+template <typename ET, int K>
 static void dw_go(const void* in, void* out, const float* w, const float* dwb, const float* sc,
                   const float* sh, int B, int Tn, int D, hipStream_t s) {
-    constexpr int TT = 16;
-    const dim3 grid(cdiv(D / VEC, 256), cdiv(Tn, TT), B);
-    launch((dwconv_bn_silu_kernel<ET, VEC, K, TT>), grid, dim3(256), 0, s, (const ET*)in,
-                       (ET*)out, w, dwb, sc, sh, Tn, D);
+    // one wave per (64 channel vectors, 4 frames, item): enough waves in flight
+    // to cover the load latency of this small pass (B*T*D/2048 waves)
+    constexpr int TT = 4, VEC = 16 / sizeof(ET);
+    const int nvec = D / VEC;
+    const int bs = 64;
+    const dim3 grid(cdiv(nvec, bs), cdiv(Tn, TT), B);
+    launch((dwconv_bn_silu_kernel<ET, K, TT>), grid, dim3(bs), 0, s, (const ET*)in, (ET*)out, w, dwb, sc, sh, Tn,
+           D);
 }
 
-template <typename ET, int VEC>
+template <typename ET>
 static void dw_k(const void* in, void* out, const float* w, const float* dwb, const float* sc,
                  const float* sh, int B, int Tn, int D, int K, hipStream_t s) {
     switch (K) {
-    case 3: dw_go<ET, VEC, 3>(in, out, w, dwb, sc, sh, B, Tn, D, s); break;
-    case 5: dw_go<ET, VEC, 5>(in, out, w, dwb, sc, sh, B, Tn, D, s); break;
-    case 7: dw_go<ET, VEC, 7>(in, out, w, dwb, sc, sh, B, Tn, D, s); break;
-    case 9: dw_go<ET, VEC, 9>(in, out, w, dwb, sc, sh, B, Tn, D, s); break;
-    case 15: dw_go<ET, VEC, 15>(in, out, w, dwb, sc, sh, B, Tn, D, s); break;
-    case 31: dw_go<ET, VEC, 31>(in, out, w, dwb, sc, sh, B, Tn, D, s); break;
+    case 3: dw_go<ET, 3>(in, out, w, dwb, sc, sh, B, Tn, D, s); break;
+    case 5: dw_go<ET, 5>(in, out, w, dwb, sc, sh, B, Tn, D, s); break;
+    case 7: dw_go<ET, 7>(in, out, w, dwb, sc, sh, B, Tn, D, s); break;
+    case 9: dw_go<ET, 9>(in, out, w, dwb, sc, sh, B, Tn, D, s); break;
+    case 15: dw_go<ET, 15>(in, out, w, dwb, sc, sh, B, Tn, D, s); break;
+    case 31: dw_go<ET, 31>(in, out, w, dwb, sc, sh, B, Tn, D, s); break;
     default: throw std::invalid_argument("dwconv: unsupported kernel size");
     }
 }
@@ -208,12 +206,9 @@ void launch_dwconv_bn_silu(Precision prec, const void* in, void* out, const floa
                            const float* dw_bias, const float* bn_scale, const float* bn_shift,
                            int B, int T, int D, int K, hipStream_t s) {
     if (B == 0 || T == 0) return;
-    if (prec == PREC_F16) {
-        require(D % 2 == 0, "dwconv: D must be even");
-        dw_k<f16, 2>(in, out, w, dw_bias, bn_scale, bn_shift, B, T, D, K, s);
-    } else {
-        dw_k<float, 1>(in, out, w, dw_bias, bn_scale, bn_shift, B, T, D, K, s);
-    }
+    require(D % 8 == 0, "dwconv: D must be a multiple of 8");
+    if (prec == PREC_F16) dw_k<f16>(in, out, w, dw_bias, bn_scale, bn_shift, B, T, D, K, s);
+    else dw_k<float>(in, out, w, dw_bias, bn_scale, bn_shift, B, T, D, K, s);
     PKX_LAUNCH_CHECK();
 }
 
