@@ -314,6 +314,28 @@ DevWeight Model::make_weight_rows(const std::vector<const HostTensor*>& parts, i
     return make_weight(cat, N, K, f16_gemm);
 }
 
+// Rows [row0, row0 + nrows) of a device weight, as a weight of its own (no copy):
+// every device layout stores rows contiguously, payload and scales alike.
+DevWeight weight_rows_view(const DevWeight& w, int row0, int nrows) {
+    DevWeight v = w;
+    v.N = nrows;
+    const int64_t r = row0, K = w.K;
+    switch (w.gtype) {
+    case GT_F32: v.q = (uint8_t*)w.q + r * K * 4; break;
+    case GT_F16: v.q = (uint8_t*)w.q + r * K * 2; break;
+    case GT_Q8_0:
+        v.q = (uint8_t*)w.q + r * K;
+        v.s = (uint8_t*)w.s + r * (K / 32) * 2;
+        break;
+    case GT_Q4_K:
+        v.q = (uint8_t*)w.q + r * K / 2;
+        v.s = (uint8_t*)w.s + r * (K / 32) * 8;
+        break;
+    default: throw std::logic_error("weight view: unknown type");
+    }
+    return v;
+}
+
 void linear_raw(Precision prec, const HostTensor& t, int N, int K, const float* bias, const float* x,
                 int64_t M, float* y, hipStream_t s) {
     std::vector<void*> allocs;
@@ -411,7 +433,8 @@ void Model::finalize() {
         }
         L.wo = make_weight(need(a + "linear_out.weight"), D, D, f16g);
         L.bo = optb(a + "linear_out.bias");
-        L.wpos = make_weight(need(a + "linear_pos.weight"), D, D, f16g);
+        // linear_pos: a row view into the all-layer concatenation built below
+        require(need(a + "linear_pos.weight").nelem() == (int64_t)D * D, "linear_pos shape");
         L.pos_u = upload_f32(need(a + "pos_bias_u"));
         L.pos_v = upload_f32(need(a + "pos_bias_v"));
         require(need(a + "pos_bias_u").nelem() == (int64_t)H * dk, "pos_bias_u shape");
@@ -447,6 +470,24 @@ void Model::finalize() {
             }
             L.bn_scale = upload_f32(sc);
             L.bn_shift = upload_f32(sh);
+        }
+    }
+
+    // linear_pos of every layer as one [L*D][D] weight: the positional table is
+    // the same for all layers, so a forward projects it once for all of them
+    // (one GEMM of N = L*D instead of L GEMMs over 2T'-1 rows).
+    {
+        std::vector<const HostTensor*> parts;
+        bool same = true;
+        for (int i = 0; i < c.n_layers; ++i) {
+            parts.push_back(&need("encoder.layers." + std::to_string(i) + ".self_attn.linear_pos.weight"));
+            same = same && parts.back()->gtype == parts[0]->gtype;
+        }
+        if (same) {
+            wpos_all_ = make_weight_rows(parts, D, f16g, false);
+            for (int i = 0; i < c.n_layers; ++i) layers_[i].wpos = weight_rows_view(wpos_all_, i * D, D);
+        } else {
+            for (int i = 0; i < c.n_layers; ++i) layers_[i].wpos = make_weight(*parts[i], D, D, f16g);
         }
     }
 
@@ -624,7 +665,7 @@ void Model::ensure_ws(int B, int T_max) {
     grow(w.qkv, M * 3 * D * as);
     grow(w.g, M * D * as);
     grow(w.pe, P * D * as);
-    grow(w.p, P * D * as);
+    grow(w.p, P * D * c.n_layers * as);   // all layers' positional projections
     grow(w.tmp, M * D * 4);
     if (B > w.Bcap) {
         if (w.d_valid) PKX_HIP(hipFree(w.d_valid));
@@ -707,7 +748,7 @@ int Model::subsampling_forward(const float* mel, int B, int T_max, const int* va
 // one conformer layer (conformer.cpp:285-353) on the f32 residual stream x
 // ---------------------------------------------------------------------------
 void Model::layer_body(int l, float* x, int B, int T, const int* d_valid, bool first_ln_done,
-                       bool fuse_next_ln, hipStream_t s) {
+                       bool fuse_next_ln, bool pos_all, hipStream_t s) {
     const ModelConfig& c = cfg_;
     const LayerDev& L = layers_[l];
     const int D = c.d_model, H = c.n_heads, dk = D / H;
@@ -732,17 +773,20 @@ void Model::layer_body(int l, float* x, int B, int T, const int* d_valid, bool f
     // Stage B: x += MHSA(LN(x))
     ln(L.att_ln_g, L.att_ln_b);
     gemm(L.wqkv, EPI_STORE, w.h.p, D, M, L.bqkv, w.qkv.p, 3 * D, 1.f, nullptr, 1, s, prec_, KF_GEMM_QKV);
-    gemm(L.wpos, EPI_STORE, w.pe.p, D, 2 * (int64_t)T - 1, nullptr, w.p.p, D, 1.f, nullptr, 1, s, prec_,
-         KF_GEMM_POS);
+    const size_t as = prec_ == PREC_F16 ? 2 : 4;
+    const int ldp = pos_all ? c.n_layers * D : D;
+    const void* pl = pos_all ? (const void*)((const uint8_t*)w.p.p + (size_t)l * D * as) : w.p.p;
+    if (!pos_all)
+        gemm(L.wpos, EPI_STORE, w.pe.p, D, 2 * (int64_t)T - 1, nullptr, w.p.p, D, 1.f, nullptr, 1, s, prec_,
+             KF_GEMM_POS);
     {
-        const size_t as = prec_ == PREC_F16 ? 2 : 4;
         AttnParams a;
         a.q = w.qkv.p;
         a.k = (const uint8_t*)w.qkv.p + (size_t)D * as;
         a.v = (const uint8_t*)w.qkv.p + (size_t)2 * D * as;
         a.ldq = a.ldk = a.ldv = 3 * D;
-        a.p = w.p.p;
-        a.ldp = D;
+        a.p = pl;
+        a.ldp = ldp;
         a.bias_u = L.pos_u;
         a.bias_v = L.pos_v;
         a.valid = d_valid;
@@ -805,8 +849,12 @@ int Model::encoder_forward(const float* mel, int B, int T_max, const int* valid_
     ensure_pe(T3, s);
     const int L = cfg_.n_layers;
     const size_t MD = (size_t)B * T3 * cfg_.d_model;
+    const bool pos_all = wpos_all_.ok();
+    if (pos_all)
+        gemm(wpos_all_, EPI_STORE, ws_->pe.p, cfg_.d_model, 2 * (int64_t)T3 - 1, nullptr, ws_->p.p,
+             (int64_t)L * cfg_.d_model, 1.f, nullptr, 1, s, prec_, KF_GEMM_POS);
     for (int l = 0; l < L; ++l) {
-        layer_body(l, out, B, T3, dvalid, l > 0, l + 1 < L, s);
+        layer_body(l, out, B, T3, dvalid, l > 0, l + 1 < L, pos_all, s);
         if (capture)
             PKX_HIP(hipMemcpyAsync(capture + (size_t)l * MD, out, MD * 4, hipMemcpyDeviceToDevice, s));
     }
@@ -833,7 +881,7 @@ void Model::conformer_layer_forward(int layer, const float* x, int B, int T, con
     if (out != x) PKX_HIP(hipMemcpyAsync(out, x, MD * 4, hipMemcpyDeviceToDevice, s));
     conv_capture_ = conv_out;
     try {
-        layer_body(layer, out, B, T, ws_->d_valid + 3 * ws_->Bcap, false, false, s);
+        layer_body(layer, out, B, T, ws_->d_valid + 3 * ws_->Bcap, false, false, false, s);
     } catch (...) {
         conv_capture_ = nullptr;
         throw;

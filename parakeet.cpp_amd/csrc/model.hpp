@@ -128,7 +128,7 @@ private:
               const float* bias, void* Y, int64_t ldy, float alpha, const int* valid, int T,
               hipStream_t s, Precision prec, int fam, const float* bias2 = nullptr, int trF = 1);
     void layer_body(int l, float* x, int B, int T, const int* d_valid, bool first_ln_done,
-                    bool fuse_next_ln, hipStream_t s);
+                    bool fuse_next_ln, bool pos_all, hipStream_t s);
     void ensure_pe(int T, hipStream_t s);
     void stage_valid(const std::vector<int>* v[4], hipStream_t s);
     void mark(int fam, bool begin);
@@ -141,6 +141,7 @@ private:
     std::vector<void*> allocs_;
     std::vector<LayerDev> layers_;
     SubDev sub_;
+    DevWeight wpos_all_;   // linear_pos of all layers, [L*D][D]; layers_[l].wpos are row views
     HeadsDev heads_;
     std::unique_ptr<Ws> ws_;
     float* conv_capture_ = nullptr;   // conformer_layer_forward's conv-module output
@@ -159,6 +160,9 @@ private:
 // Upload one raw-layout weight (repacked for the f16 or f32 GEMM path); the
 // device buffers are appended to `allocs`.
 DevWeight build_weight(const HostTensor& t, int N, int K, bool f16_gemm, std::vector<void*>& allocs);
+
+// Rows [row0, row0 + nrows) of a device weight, sharing its storage.
+DevWeight weight_rows_view(const DevWeight& w, int row0, int nrows);
 
 // y[M][N] = x[M][K] . W^T (+ bias) for one raw weight, f32 in/out; the weight
 // is uploaded for this call and freed after the stream drains.

@@ -151,7 +151,7 @@ def test_profiling_counts_and_sampling(gpu, stream):
     gm.encoder_forward(dm, [200, 120], dy, stream=stream)
     prof = gm.profile()
     assert np.array_equal(dy.numpy(stream), plain)
-    expect = {"subsampling": 5, "layernorm": 4 * L + 1, "gemm_ffn": 4 * L, "gemm_qkv": L, "gemm_pos": L,
+    expect = {"subsampling": 5, "layernorm": 4 * L + 1, "gemm_ffn": 4 * L, "gemm_qkv": L, "gemm_pos": 1,
               "attention": L, "gemm_out": L, "gemm_pw1_glu": L, "dwconv": L, "gemm_pw2": L, "pos_enc": 1}
     for fam, n in expect.items():
         ms, got_n = prof[fam]
