@@ -760,10 +760,11 @@ __device__ __forceinline__ void epilogue32_lds(const GemmParams& p, float16v (&a
     }
 }
 
-template <int TM, int TN, int WT, int EPI>
+template <int TM, int TN, int WT, int EPI, int NS = DMA_NS>
 __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmParams p) {
     typedef DmaCfg<TM, TN, WT> C;
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[DMA_NS * C::STAGE];
+    static_assert(NS == 2 || NS == 3, "LDS ring depth");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * C::STAGE];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wid = wave_id_uniform();
@@ -783,28 +784,29 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmParams p) {
     DmaSrc<TM, TN, WT> src;
     src.init(p, m0, n0, wid, lane);
     src.issue(smem, 0);
-    if (nk > 1) src.issue(smem + C::STAGE, 64);
+    if (NS == 3 && nk > 1) src.issue(smem + C::STAGE, 64);
     int st = 0;
     for (int kt = 0; kt < nk; ++kt) {
-        // this wave's DMAs for slab kt have landed (slab kt+1 may still be in flight)
-        if (kt + 1 < nk) wait_vmcnt<C::PER_SLAB>();
+        // this wave's DMAs for slab kt have landed (with 3 stages slab kt+1 may
+        // still be in flight)
+        if (NS == 3 && kt + 1 < nk) wait_vmcnt<C::PER_SLAB>();
         else wait_vmcnt<0>();
-        // Every wave's part of slab kt is in LDS and stage (kt+2)%3 is no longer read.
-        // A bare s_barrier: the DMA counter was bounded above, and a fenced
-        // __syncthreads() would also drain the DMAs of slab kt+1.
+        // Every wave's part of slab kt is in LDS and stage (kt+NS-1)%NS is no
+        // longer read.  A bare s_barrier: the DMA counter was bounded above, and
+        // a fenced __syncthreads() would also drain the DMAs still in flight.
         __builtin_amdgcn_s_barrier();
-        if (kt + 2 < nk) {
-            const int st2 = st + 2 >= DMA_NS ? st + 2 - DMA_NS : st + 2;
-            src.issue(smem + st2 * C::STAGE, (kt + 2) * 64);
+        if (kt + NS - 1 < nk) {
+            const int st2 = st + NS - 1 >= NS ? st - 1 : st + NS - 1;
+            src.issue(smem + st2 * C::STAGE, (kt + NS - 1) * 64);
         }
         mma32_slab<TM, TN, WT>(smem + st * C::STAGE, acc, wm, wn, lane);
-        st = st + 1 == DMA_NS ? 0 : st + 1;
+        st = st + 1 == NS ? 0 : st + 1;
     }
     if constexpr (EPI == EPI_RELU2_F32) {
         epilogue32<EPI, f16, TM, TN>(p, acc, m0 + wm * TM * 32, n0 + wn * TN * 32, lane);
     } else if constexpr (EPI == EPI_RELU_TR) {
         if ((32 * TM) % p.trF == 0 && (32 * TN * p.trF) % 8 == 0 && p.N % 8 == 0) {
-            static_assert(4 * 32 * TM * (32 * TN + 1) * 4 <= DMA_NS * C::STAGE, "epilogue staging exceeds LDS ring");
+            static_assert(4 * 32 * TM * (32 * TN + 1) * 4 <= NS * C::STAGE, "epilogue staging exceeds LDS ring");
             __syncthreads();
             float* wsm = (float*)smem + wid * (32 * TM) * (32 * TN + 1);
             epilogue32_relu_tr<TM, TN>(p, acc, wsm, m0 + wm * TM * 32, n0 + wn * TN * 32, lane);
@@ -812,11 +814,29 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmParams p) {
             epilogue32<EPI, f16, TM, TN>(p, acc, m0 + wm * TM * 32, n0 + wn * TN * 32, lane);
         }
     } else {
-        // the LDS ring is free once every wave has finished its last slab
-        static_assert(4 * 32 * TM * (32 * TN + 4) * 4 <= DMA_NS * C::STAGE, "epilogue staging exceeds LDS ring");
-        __syncthreads();
-        float* wsm = (float*)smem + wid * (32 * TM) * ((EPI == EPI_GLU ? 16 * TN : 32 * TN) + 4);
-        epilogue32_lds<EPI, TM, TN>(p, acc, wsm, m0 + wm * TM * 32, n0 + wn * TN * 32, lane);
+        // the LDS ring is free once every wave has finished its last slab; tiles
+        // whose staging exceeds it leave in row halves
+        constexpr bool whole = 4 * 32 * TM * (32 * TN + 4) * 4 <= NS * C::STAGE;
+        static_assert(whole || (TM % 2 == 0 && 4 * 16 * TM * (32 * TN + 4) * 4 <= NS * C::STAGE),
+                      "epilogue staging exceeds LDS ring");
+        if constexpr (whole) {
+            __syncthreads();
+            float* wsm = (float*)smem + wid * (32 * TM) * ((EPI == EPI_GLU ? 16 * TN : 32 * TN) + 4);
+            epilogue32_lds<EPI, TM, TN>(p, acc, wsm, m0 + wm * TM * 32, n0 + wn * TN * 32, lane);
+        } else {
+            constexpr int TH = TM / 2;
+            float* wsm = (float*)smem + wid * (32 * TH) * ((EPI == EPI_GLU ? 16 * TN : 32 * TN) + 4);
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                float16v part[TH][TN];
+#pragma unroll
+                for (int i = 0; i < TH; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j) part[i][j] = acc[hh * TH + i][j];
+                __syncthreads();
+                epilogue32_lds<EPI, TH, TN>(p, part, wsm, m0 + wm * TM * 32 + hh * TH * 32, n0 + wn * TN * 32, lane);
+            }
+        }
     }
 }
 
