@@ -63,6 +63,53 @@ def layernorm_bytes(cfg, B, Tp):
     return total / launches
 
 
+def other_config(name, qtype, cfg_kw, lens, T_max, steps, warmup, stream):
+    """The other benchmark shapes, same measurement (one GPU, inputs resident,
+    FFN GEMM sampled with per-dispatch events inside the timed region)."""
+    kw = dict(CFG)
+    kw.update(cfg_kw)
+    cfg = pm.Config(**kw)
+    model = pm.synthesize(cfg, qtype, heads=False)
+    gm = pkx.Model.from_tensors(model, pkx.PREC_AUTO)
+    del model
+    Bc = len(lens)
+    rng = np.random.default_rng(42)
+    mel = rng.standard_normal((Bc, cfg.n_mels, T_max)).astype(np.float32)
+    for b, v in enumerate(lens):
+        mel[b, :, v:] = 0.0
+    d_mel = pkx.DeviceArray.from_numpy(mel, stream)
+    Tp = pkx.subsampled_len(T_max)
+    d_out = pkx.DeviceArray((Bc, Tp, cfg.d_model), np.float32)
+    valid = np.asarray(lens, dtype=np.int32)
+    for _ in range(warmup):
+        gm.encoder_forward(d_mel, valid, d_out, stream=stream)
+    stream.sync()
+    gm.set_profiling(["gemm_ffn"], stride=25)
+    e0, e1 = pkx.Event(), pkx.Event()
+    e0.record(stream)
+    vo = None
+    for _ in range(steps):
+        _, vo = gm.encoder_forward(d_mel, valid, d_out, stream=stream)
+    e1.record(stream)
+    ms = e0.elapsed_ms(e1) / steps
+    stream.sync()
+    ffn_ms, ffn_n = gm.profile()["gemm_ffn"]
+    gm.set_profiling(False)
+    M = Bc * Tp
+    ffn_flop = 2.0 * M * cfg.d_model * cfg.ff_dim
+    ffn_tf = ffn_flop / (ffn_ms / 1e3 / ffn_n) / 1e12
+    audio_s = float(np.sum(lens)) * HOP_S
+    out = {"workload": name, "ms_per_step": round(ms, 4), "rtfx": round(audio_s / (ms / 1e3), 1),
+           "frames_per_s": round(float(np.sum(vo)) / (ms / 1e3), 1),
+           "gemm_ffn": {"avg_us": round(ffn_ms / ffn_n * 1e3, 2), "achieved": round(ffn_tf, 2),
+                        "unit": "TFLOP/s", "frac": round(ffn_tf / PEAK_F16_TFLOPS, 4)},
+           "steps": steps}
+    d_mel.free()
+    d_out.free()
+    gm.close()
+    return out
+
+
 def cpu_baseline(model, mel_item, budget_s=12.0):
     import oracle
     om = oracle.OracleModel(model)
@@ -89,6 +136,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-extra", action="store_true", help="skip the other workload shapes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this encoder build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -206,6 +254,15 @@ def main():
         "kernel_busy_ms_per_step": round(busy_ms, 4),
         "setup_s": round(setup_s, 1),
     }
+    if not args.no_extra:
+        # the ragged f16 batch (16 clips of 2-20 s) and the 1.1B shape at 8 x 30 s
+        lens = (200 + np.floor(np.random.default_rng(7).random(16) * 1801)).astype(np.int32)
+        line["other_configs"] = [
+            other_config("0.6B f16 weights, batch 16 ragged 2-20 s (T_max %d frames)" % int(lens.max()), "f16", {},
+                         lens, int(lens.max()), 10, 2, stream),
+            other_config("1.1B shape q8_0 (42 blocks), batch 8 x 30 s (3000 frames -> T'=375)", "q8_0",
+                         dict(n_layers=42), np.full(8, 3000, dtype=np.int32), 3000, 5, 1, stream),
+        ]
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(model, mel[:1].copy())
     print(json.dumps(line))
