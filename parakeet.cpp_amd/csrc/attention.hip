@@ -8,20 +8,22 @@
 // keys are streamed in tiles of 64 with an online softmax, and the shifted
 // term uses the identity bd_shift[i][j] = bd[i][T-1-i+j]: for a 16-query x
 // 64-key tile the needed positional rows form one band of 79 rows, computed
-// as a 16x80 MFMA product into LDS and gathered along the diagonal.
+// as a 16x80 MFMA product into LDS and gathered along the diagonal.  Each
+// wave's G rows and probabilities are private to it, so only the shared
+// K / V^T / band staging needs block-wide barriers.
 #include "attention.hpp"
 
 namespace pkx {
 
 // ---------------------------------------------------------------------------
-// f16 MFMA kernel
+// f16 MFMA kernel.  NW waves per block, 16 query rows per wave (AQ = 16 NW).
 // ---------------------------------------------------------------------------
-constexpr int AQ = 64;   // query rows per block (16 per wave)
 constexpr int AK = 64;   // keys per tile
-constexpr int APB = 128; // positional band rows staged per key tile
 
-template <int DK>
+template <int DK, int NW>
 struct AttnSmem {
+    static constexpr int AQ = 16 * NW;
+    static constexpr int APB = (AQ + AK - 1 + 15) / 16 * 16;  // positional band rows per key tile
     static constexpr int LDK = DK + 8;   // K and P rows (halves)
     static constexpr int LDV = AK + 8;   // transposed V rows (halves)
     static constexpr int LDG = 80;       // band product (floats)
@@ -29,14 +31,15 @@ struct AttnSmem {
     f16 k[AK * LDK];
     f16 vt[DK * LDV];
     f16 p[APB * LDK];
-    float g[4][16 * LDG];
-    f16 prob[4][16 * LDP];
+    float g[NW][16 * LDG];
+    f16 prob[NW][16 * LDP];
 };
 
-template <int DK>
-__global__ __launch_bounds__(256, 1) void relpos_attn_f16_kernel(AttnParams a) {
+template <int DK, int NW>
+__global__ __launch_bounds__(64 * NW, 1) void relpos_attn_f16_kernel(AttnParams a) {
     static_assert(DK % 32 == 0, "head dim must be a multiple of 32");
-    typedef AttnSmem<DK> S;
+    typedef AttnSmem<DK, NW> S;
+    constexpr int AQ = S::AQ, NT = 64 * NW;
     __shared__ __attribute__((aligned(16))) S sm;
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -82,19 +85,32 @@ __global__ __launch_bounds__(256, 1) void relpos_attn_f16_kernel(AttnParams a) {
     for (int j0 = 0; j0 < vl; j0 += AK) {
         // ---- stage K tile, transposed V tile and the positional band in LDS ----
         const int rlo = T - 1 - (i0 + AQ - 1) + j0;
-        for (int c = tid; c < AK * (DK / 8); c += 256) {
+        for (int c = tid; c < AK * (DK / 8); c += NT) {
             const int r = c / (DK / 8), col = (c % (DK / 8)) * 8;
             const int j = j0 + r;
-            half8v kv = {}, vv = {};
-            if (j < T) {
-                kv = *(const half8v*)(k + (rowq + j) * a.ldk + h * DK + col);
-                vv = *(const half8v*)(v + (rowq + j) * a.ldv + h * DK + col);
-            }
+            half8v kv = {};
+            if (j < T) kv = *(const half8v*)(k + (rowq + j) * a.ldk + h * DK + col);
             *(half8v*)(sm.k + r * S::LDK + col) = kv;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) sm.vt[(col + e) * S::LDV + r] = vv[e];
         }
-        for (int c = tid; c < APB * (DK / 8); c += 256) {
+        // V^T in 8 x 8 blocks: 8 row loads of 16 B, transposed in registers,
+        // 8 row stores of 16 B (keys contiguous)
+        for (int c = tid; c < (AK / 8) * (DK / 8); c += NT) {
+            const int kg = c % (AK / 8), dg = c / (AK / 8);
+            half8v rows[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int j = j0 + 8 * kg + e;
+                rows[e] = j < T ? *(const half8v*)(v + (rowq + j) * a.ldv + h * DK + 8 * dg) : (half8v){};
+            }
+#pragma unroll
+            for (int d = 0; d < 8; ++d) {
+                half8v col;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) col[e] = rows[e][d];
+                *(half8v*)(sm.vt + (8 * dg + d) * S::LDV + 8 * kg) = col;
+            }
+        }
+        for (int c = tid; c < S::APB * (DK / 8); c += NT) {
             const int r = c / (DK / 8), col = (c % (DK / 8)) * 8;
             const int pr = rlo + r;
             half8v pv = {};
@@ -114,9 +130,9 @@ __global__ __launch_bounds__(256, 1) void relpos_attn_f16_kernel(AttnParams a) {
                 sac[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qu[kc], kf, sac[jt], 0, 0, 0);
             }
         }
-        // ---- band product G = qv . p_band^T : 16 x 80, band rows start at 48 - 16w ----
+        // ---- band product G = qv . p_band^T : 16 x 80, band rows start at AQ - 16 - 16 w ----
         {
-            const int pb = 48 - 16 * w;
+            const int pb = AQ - 16 - 16 * w;
 #pragma unroll
             for (int gt = 0; gt < 5; ++gt) {
                 float4v g = {0.f, 0.f, 0.f, 0.f};
@@ -129,7 +145,9 @@ __global__ __launch_bounds__(256, 1) void relpos_attn_f16_kernel(AttnParams a) {
                 for (int r = 0; r < 4; ++r) sm.g[w][(lr + r) * S::LDG + 16 * gt + lc] = g[r];
             }
         }
-        __syncthreads();
+        // each wave reads back only its own G rows: a wave-local barrier suffices
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        __builtin_amdgcn_wave_barrier();
 
         // ---- scores, rel_shift gather, key mask, online softmax ----
         float s[4][4];
@@ -176,7 +194,9 @@ __global__ __launch_bounds__(256, 1) void relpos_attn_f16_kernel(AttnParams a) {
         for (int d = 0; d < NDT; ++d)
 #pragma unroll
             for (int r = 0; r < 4; ++r) o[d][r] *= corr[r];
-        __syncthreads();
+        // the probabilities are wave-private too
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        __builtin_amdgcn_wave_barrier();
 
         // ---- o += prob . v : A = prob (16 x 64 keys), B = v^T rows ----
 #pragma unroll
@@ -188,7 +208,7 @@ __global__ __launch_bounds__(256, 1) void relpos_attn_f16_kernel(AttnParams a) {
                 o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf, vf, o[d], 0, 0, 0);
             }
         }
-        __syncthreads();
+        __syncthreads();   // the next tile's staging overwrites K, V^T and the band
     }
 
     // ---- normalise, zero padded query rows, merge heads into ctx[b*T+i][h*DK+c] ----
@@ -266,13 +286,16 @@ __global__ __launch_bounds__(64) void relpos_attn_f32_kernel(AttnParams a, int d
 void launch_relpos_attention(Precision prec, const AttnParams& a, hipStream_t s) {
     require(a.T > 0 && a.B > 0 && a.H > 0, "attention: empty shape");
     if (prec == PREC_F16) {
-        const dim3 grid(cdiv(a.T, AQ), a.H, a.B);
+        // 32 queries (2 waves) per block: twice the blocks of a 64-query tiling
+        // and an LDS footprint that lets two blocks share a CU.
+        constexpr int NW = 4;
+        const dim3 grid(cdiv(a.T, 16 * NW), a.H, a.B);
         if (a.dk == 128) {
-            launch(relpos_attn_f16_kernel<128>, grid, dim3(256), 0, s, a);
+            launch(relpos_attn_f16_kernel<128, NW>, grid, dim3(64 * NW), 0, s, a);
         } else if (a.dk == 64) {
-            launch(relpos_attn_f16_kernel<64>, grid, dim3(256), 0, s, a);
+            launch(relpos_attn_f16_kernel<64, NW>, grid, dim3(64 * NW), 0, s, a);
         } else if (a.dk == 32) {
-            launch(relpos_attn_f16_kernel<32>, grid, dim3(256), 0, s, a);
+            launch(relpos_attn_f16_kernel<32, NW>, grid, dim3(64 * NW), 0, s, a);
         } else {
             throw std::invalid_argument("attention(f16): head dim must be 32, 64 or 128");
         }
