@@ -1349,18 +1349,18 @@ void launch_gemm(Precision prec, int wtype, int epi, const GemmParams& p, hipStr
     if (epi == EPI_GLU) require(p.N % 64 == 0, "gemm: GLU needs N % 64 == 0");
     const bool big = (int64_t)cdiv(p.M, 128) * cdiv(p.N, 128) >= 256;
     if (prec == PREC_F16 && p.K % 64 == 0 && p.ldy % 8 == 0 && (wtype == GT_F16 || wtype == GT_Q8_0)) {
-        // Tile shapes from a sweep over the encoder's shapes on MI355X (M = B*T' = 2000):
-        // q8_0 weights prefer 128x128 when the grid holds >= 384 of them (N >= 3072),
-        // 128x64 for the long-K N=1024 product (FFN2, K=4096), 64x64 for K=1024 at
-        // N=1024 (attention output; equal to 128x64 there) and for the short
-        // positional projection; f16 weights run best at 64x128 throughout.  The GLU
-        // epilogue pairs 64-column groups, so it needs a tile at least 128 wide.
+        // Tile shapes from sweeps over the encoder's shapes on MI355X (M = B*T' = 2000):
+        // q8_0 weights prefer 128x128 when the grid holds >= 384 of them (N >= 3072,
+        // and the all-layer positional projection), 128x64 at N = 1024 (FFN2, attention
+        // output), 64x64 for grids too small to fill the chip; f16 weights run best at
+        // 64x128 throughout.  The GLU epilogue pairs 64-column groups, so it needs a
+        // tile at least 128 wide.
         const int64_t t22 = (int64_t)cdiv(p.M, 128) * cdiv(p.N, 128);
         const int64_t t21 = (int64_t)cdiv(p.M, 128) * cdiv(p.N, 64);
         if (wtype == GT_Q8_0) {
             if (t22 >= 384 || (epi == EPI_GLU && t22 >= 256)) dma_epi<2, 2, GT_Q8_0>(epi, p, s);
             else if (epi == EPI_GLU) dma_epi<1, 2, GT_Q8_0>(epi, p, s);
-            else if (t21 >= 128 && p.K >= 2048) dma_epi<2, 1, GT_Q8_0>(epi, p, s);
+            else if (t21 >= 128) dma_epi<2, 1, GT_Q8_0>(epi, p, s);
             else dma_epi<1, 1, GT_Q8_0>(epi, p, s);
         } else {
             dma_epi<1, 2, GT_F16>(epi, p, s);
