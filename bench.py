@@ -262,6 +262,8 @@ def main():
                          lens, int(lens.max()), 10, 2, stream),
             other_config("1.1B shape q8_0 (42 blocks), batch 8 x 30 s (3000 frames -> T'=375)", "q8_0",
                          dict(n_layers=42), np.full(8, 3000, dtype=np.int32), 3000, 5, 1, stream),
+            other_config("0.6B q4_K weights, batch 16 x 10 s", "q4_k", {}, np.full(16, 1000, dtype=np.int32), 1000,
+                         10, 2, stream),
         ]
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(model, mel[:1].copy())

@@ -202,6 +202,22 @@ __device__ __forceinline__ void i8x4_to_f16(uint32_t w, half2v d2, half2v& lo, h
     hi = (__builtin_bit_cast(half2v, b) - bias) * d2;
 }
 
+// Four 4-bit weights (nibble `hi` of each byte of w) to f16, w = s*q - m with
+// nm2 = -m: the nibble is placed in an f16 mantissa so that the half reads
+// 1024 + q (low nibble, exponent byte 0x64) or 64 + q (high nibble in mantissa
+// bits 4..7, exponent byte 0x54); subtracting 1024 or 64 is exact, then one
+// rounding in the fma.
+__device__ __forceinline__ void nib4_to_f16(uint32_t w, int hi, half2v s2, half2v nm2, half2v& lo, half2v& up) {
+    const uint32_t e = hi ? 0x54545454u : 0x64646464u;
+    const uint32_t mask = hi ? 0xFFF0FFF0u : 0xFF0FFF0Fu;
+    const f16 off = hi ? (f16)64.0f : (f16)1024.0f;
+    const half2v off2 = {off, off};
+    const uint32_t a = __builtin_amdgcn_perm(e, w, 0x07010700u) & mask;  // bytes 0, 1
+    const uint32_t b = __builtin_amdgcn_perm(e, w, 0x07030702u) & mask;  // bytes 2, 3
+    lo = (__builtin_bit_cast(half2v, a) - off2) * s2 + nm2;
+    up = (__builtin_bit_cast(half2v, b) - off2) * s2 + nm2;
+}
+
 // q8_0 device layout: int8 q[N][K] and f16 d[N][K/32]; w = d*q.
 template <int BN> struct BLoad16<GT_Q8_0, BN> {
     static constexpr int NC = (BN * 4 + 255) / 256;
@@ -439,14 +455,17 @@ template <int TM, int TN, int WT>
 struct DmaCfg {
     static constexpr int BM = 64 * TM, BN = 64 * TN;      // 2x2 waves of (32 TM) x (32 TN)
     static constexpr int A_BYTES = BM * 128;
-    static constexpr int B_BYTES = WT == GT_Q8_0 ? BN * 64 : BN * 128;
-    static constexpr int S_BYTES = WT == GT_Q8_0 ? BN * 4 : 0;
+    static constexpr int B_BYTES = WT == GT_Q8_0 ? BN * 64 : WT == GT_Q4_K ? BN * 32 : BN * 128;
+    static constexpr int S_BYTES = WT == GT_Q8_0 ? BN * 4 : WT == GT_Q4_K ? BN * 16 : 0;
     static constexpr int STAGE = A_BYTES + B_BYTES + S_BYTES;
+    static constexpr int B_DMA = B_BYTES % 4096 == 0 ? 16 : 4;         // bytes per lane per weight DMA
     static constexpr int A_INSTR = A_BYTES / 1024 / 4;                 // per wave
-    static constexpr int B_INSTR = B_BYTES / 1024 / 4;
-    static constexpr int S_INSTR = WT == GT_Q8_0 ? (BN + 63) / 64 : 0; // every wave loads all scales
+    static constexpr int B_INSTR = B_BYTES / (64 * B_DMA) / 4;
+    // q8_0: every wave loads all scales (BN * 4 bytes); q4_K: the waves split
+    // the {scale, min} pairs (BN * 16 bytes) in 256-byte pieces
+    static constexpr int S_INSTR = WT == GT_Q8_0 ? (BN + 63) / 64 : WT == GT_Q4_K ? S_BYTES / 1024 : 0;
     static constexpr int PER_SLAB = A_INSTR + B_INSTR + S_INSTR;
-    static_assert(A_BYTES % 4096 == 0 && B_BYTES % 4096 == 0, "tile must split into 1 KB per wave");
+    static_assert(A_BYTES % 4096 == 0 && B_BYTES % 1024 == 0, "tile must split into equal parts per wave");
 };
 
 // Buffer load of 16 (4) bytes per lane straight into LDS: lane L's data lands
@@ -473,8 +492,8 @@ struct DmaSrc {
     __device__ __forceinline__ void init(const GemmParams& p, int m0, int n0, int wid_, int lane) {
         wid = wid_;
         ra = make_rsrc((const f16*)p.A + (int64_t)m0 * p.lda, ((int64_t)(p.M - m0 - 1) * p.lda + p.K) * 2);
-        const int wb = WT == GT_Q8_0 ? 1 : 2;
-        rw = make_rsrc((const uint8_t*)p.Wq + (int64_t)n0 * p.K * wb, (int64_t)(p.N - n0) * p.K * wb);
+        const int64_t wrow = WT == GT_Q8_0 ? p.K : WT == GT_Q4_K ? p.K / 2 : (int64_t)p.K * 2;  // bytes per row
+        rw = make_rsrc((const uint8_t*)p.Wq + n0 * wrow, (p.N - n0) * wrow);
 #pragma unroll
         for (int i = 0; i < C::A_INSTR; ++i) {
             const int slot = (wid * C::A_INSTR + i) * 64 + lane;   // 1 KB block = 8 rows of 128 B
@@ -496,6 +515,30 @@ struct DmaSrc {
                 const int n = min(i * 64 + lane, p.N - n0 - 1);    // 4 B = the slab's 2 scales of a row
                 vs[i] = (uint32_t)(n * (p.K / 32) * 2);
             }
+        } else if constexpr (WT == GT_Q4_K) {
+            // 32 nibble bytes per row and slab, 16-byte chunk c stored at c ^ ((row >> 3) & 1)
+#pragma unroll
+            for (int i = 0; i < C::B_INSTR; ++i) {
+                const int slot = (wid * C::B_INSTR + i) * 64 + lane;
+                int row, off;
+                if constexpr (C::B_DMA == 16) {
+                    row = slot >> 1;
+                    off = 16 * ((slot & 1) ^ ((row >> 3) & 1));
+                } else {
+                    row = slot >> 3;
+                    off = 16 * (((slot >> 2) & 1) ^ ((row >> 3) & 1)) + 4 * (slot & 3);
+                }
+                const int n = min(row, p.N - n0 - 1);
+                vb[i] = (uint32_t)((int64_t)n * (p.K / 2) + off);
+            }
+            // {d*sc, dmin*m} float pairs of the slab's two sub-blocks: 16 B per row
+            rs = make_rsrc((const float*)p.Ws + (int64_t)n0 * (p.K / 32) * 2, (int64_t)(p.N - n0) * (p.K / 32) * 8);
+#pragma unroll
+            for (int i = 0; i < C::S_INSTR; ++i) {
+                const int slot = (wid * C::S_INSTR + i) * 64 + lane;
+                const int n = min(slot >> 2, p.N - n0 - 1);
+                vs[i] = (uint32_t)(n * (p.K / 32) * 8 + 4 * (slot & 3));
+            }
         } else {
             rs = rw;
 #pragma unroll
@@ -512,13 +555,19 @@ struct DmaSrc {
 #pragma unroll
         for (int i = 0; i < C::A_INSTR; ++i) lds_dma16(ra, st + (wid * C::A_INSTR + i) * 1024, va[i], k0 * 2);
         uint8_t* bs = st + C::A_BYTES;
+        const int kb = WT == GT_Q8_0 ? k0 : WT == GT_Q4_K ? k0 / 2 : k0 * 2;
 #pragma unroll
-        for (int i = 0; i < C::B_INSTR; ++i)
-            lds_dma16(rw, bs + (wid * C::B_INSTR + i) * 1024, vb[i], WT == GT_Q8_0 ? k0 : k0 * 2);
+        for (int i = 0; i < C::B_INSTR; ++i) {
+            if constexpr (C::B_DMA == 16) lds_dma16(rw, bs + (wid * C::B_INSTR + i) * 1024, vb[i], kb);
+            else lds_dma4(rw, bs + (wid * C::B_INSTR + i) * 256, vb[i], kb);
+        }
+        uint8_t* ss = bs + C::B_BYTES;
         if constexpr (WT == GT_Q8_0) {
-            uint8_t* ss = bs + C::B_BYTES;
 #pragma unroll
             for (int i = 0; i < C::S_INSTR; ++i) lds_dma4(rs, ss + i * 256, vs[i], (k0 / 32) * 2);
+        } else if constexpr (WT == GT_Q4_K) {
+#pragma unroll
+            for (int i = 0; i < C::S_INSTR; ++i) lds_dma4(rs, ss + (wid * C::S_INSTR + i) * 256, vs[i], k0 / 4);
         }
     }
 };
@@ -548,6 +597,21 @@ __device__ __forceinline__ void mma32_slab(const uint8_t* st, float16v (&acc)[TM
                 i8x4_to_f16(w0, d2, h0, h1);
                 i8x4_to_f16(w1, d2, h2, h3);
                 bf[j][s2] = (half8v){h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
+            }
+        } else if constexpr (WT == GT_Q4_K) {
+            const int sw = (row >> 3) & 1;
+            const int4v raw0 = *(const int4v*)(bs + row * 32 + (sw << 4));
+            const int4v raw1 = *(const int4v*)(bs + row * 32 + ((sw ^ 1) << 4));
+            const float2v sm = *(const float2v*)(bs + C::B_BYTES + row * 16 + q * 8);
+            const half2v s2 = {(f16)sm.x, (f16)sm.x}, nm2 = {(f16)-sm.y, (f16)-sm.y};
+#pragma unroll
+            for (int s2i = 0; s2i < 4; ++s2i) {
+                const uint32_t w0 = (uint32_t)(s2i < 2 ? raw0[2 * s2i] : raw1[2 * (s2i - 2)]);
+                const uint32_t w1 = (uint32_t)(s2i < 2 ? raw0[2 * s2i + 1] : raw1[2 * (s2i - 2) + 1]);
+                half2v h0, h1, h2, h3;
+                nib4_to_f16(w0, q, s2, nm2, h0, h1);
+                nib4_to_f16(w1, q, s2, nm2, h2, h3);
+                bf[j][s2i] = (half8v){h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
             }
         } else {
             const uint8_t* rp = bs + row * 128;
@@ -1305,7 +1369,7 @@ static void run_f32(const GemmParams& p, hipStream_t s) {
 static int choose_xcd_gm(const GemmParams& p, int WT, int BM, int BN) {
     const int nbm = cdiv(p.M, BM), nbn = cdiv(p.N, BN);
     const double a_bytes = (double)p.M * p.K * 2;
-    const double w_bytes = (double)p.N * p.K * (WT == GT_Q8_0 ? 34.0 / 32 : 2.0);
+    const double w_bytes = (double)p.N * p.K * (WT == GT_Q8_0 ? 34.0 / 32 : WT == GT_Q4_K ? 0.75 : 2.0);
     int best = 1;
     double best_cost = 1e300;
     for (int gm : {1, 2, 4, 8}) {
@@ -1348,9 +1412,10 @@ void launch_gemm(Precision prec, int wtype, int epi, const GemmParams& p, hipStr
     if (wtype == GT_Q4_K) require(p.K % 256 == 0, "gemm: q4_K needs K % 256 == 0");
     if (epi == EPI_GLU) require(p.N % 64 == 0, "gemm: GLU needs N % 64 == 0");
     const bool big = (int64_t)cdiv(p.M, 128) * cdiv(p.N, 128) >= 256;
-    if (prec == PREC_F16 && p.K % 64 == 0 && p.ldy % 8 == 0 && (wtype == GT_F16 || wtype == GT_Q8_0)) {
+    if (prec == PREC_F16 && p.K % 64 == 0 && p.ldy % 8 == 0 &&
+        (wtype == GT_F16 || wtype == GT_Q8_0 || wtype == GT_Q4_K)) {
         // Tile shapes from sweeps over the encoder's shapes on MI355X (M = B*T' = 2000):
-        // q8_0 weights prefer 128x128 when the grid holds >= 384 of them (N >= 3072,
+        // q8_0 and q4_K weights prefer 128x128 when the grid holds >= 384 of them (N >= 3072,
         // and the all-layer positional projection), 128x64 at N = 1024 (FFN2, attention
         // output), 64x64 for grids too small to fill the chip; f16 weights run best at
         // 64x128 throughout.  The GLU epilogue pairs 64-column groups, so it needs a
@@ -1362,6 +1427,11 @@ void launch_gemm(Precision prec, int wtype, int epi, const GemmParams& p, hipStr
             else if (epi == EPI_GLU) dma_epi<1, 2, GT_Q8_0>(epi, p, s);
             else if (t21 >= 128) dma_epi<2, 1, GT_Q8_0>(epi, p, s);
             else dma_epi<1, 1, GT_Q8_0>(epi, p, s);
+        } else if (wtype == GT_Q4_K) {
+            if (t22 >= 384 || (epi == EPI_GLU && t22 >= 256)) dma_epi<2, 2, GT_Q4_K>(epi, p, s);
+            else if (epi == EPI_GLU) dma_epi<1, 2, GT_Q4_K>(epi, p, s);
+            else if (t21 >= 128) dma_epi<2, 1, GT_Q4_K>(epi, p, s);
+            else dma_epi<1, 1, GT_Q4_K>(epi, p, s);
         } else {
             dma_epi<1, 2, GT_F16>(epi, p, s);
         }

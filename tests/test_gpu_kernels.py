@@ -92,3 +92,22 @@ def test_rel_pos_encoding(gpu, stream, T, D):
     # f64 sin/cos then one rounding to f32: equal up to at most 1 f32 ulp
     ulp = np.abs(got.view(np.int32).astype(np.int64) - ref.view(np.int32).astype(np.int64))
     assert ulp.max() <= 1
+
+
+@pytest.mark.parametrize("gtype", [pm.GGML_F16, pm.GGML_Q8_0, pm.GGML_Q4_K])
+@pytest.mark.parametrize("M,N,K", [(1000, 3072, 512), (2000, 4096, 256), (333, 2048, 1024), (129, 320, 1280)])
+def test_linear_tile_shapes(gpu, stream, gtype, M, N, K):
+    """f16 path at shapes that select each MFMA tile (64x64, 128x64, 128x128)
+    and leave partial tiles on both edges."""
+    rng = _rng(M * 7 + N + K)
+    raw, wf = _weights(gtype, N, K, rng)
+    x = rng.normal(0, 1, (M, K)).astype(np.float32)
+    b = rng.normal(0, 0.1, N).astype(np.float32)
+    print(f"[linear-tiles] type={gtype} M={M} N={N} K={K}", flush=True)
+    ref = oracle.linear(x, wf, b)
+    dx = gpu.DeviceArray.from_numpy(x, stream)
+    db = gpu.DeviceArray.from_numpy(b, stream)
+    dy = gpu.DeviceArray((M, N), np.float32)
+    gpu.linear(1, gtype, N, K, raw, dx, M, dy, db, stream)
+    err = rel_l2(dy.numpy(stream), ref)
+    assert err < 2e-3, err
