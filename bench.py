@@ -41,6 +41,7 @@ def family_work(cfg, B, Tp):
         "gemm_qkv": ("TFLOP/s", 2.0 * M * D * 3 * D),
         "gemm_pos": ("TFLOP/s", 2.0 * P * D * D),
         "gemm_out": ("TFLOP/s", 2.0 * M * D * D),
+        # pointwise_conv1 (+ GLU, and with kernel 9 the depthwise conv + BN + SiLU in its epilogue)
         "gemm_pw1_glu": ("TFLOP/s", 2.0 * M * D * 2 * D),
         "gemm_pw2": ("TFLOP/s", 2.0 * M * D * D),
         "attention": ("TFLOP/s", 6.0 * B * H * Tp * Tp * dk),

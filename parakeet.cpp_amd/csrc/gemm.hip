@@ -491,14 +491,15 @@ struct DmaSrc {
 
     __device__ __forceinline__ void init(const GemmParams& p, int m0, int n0, int wid_, int lane) {
         wid = wid_;
-        ra = make_rsrc((const f16*)p.A + (int64_t)m0 * p.lda, ((int64_t)(p.M - m0 - 1) * p.lda + p.K) * 2);
+        const int mb = max(m0, 0);   // tiles of the fused conv-module epilogue start H rows early
+        ra = make_rsrc((const f16*)p.A + (int64_t)mb * p.lda, ((int64_t)(p.M - mb - 1) * p.lda + p.K) * 2);
         const int64_t wrow = WT == GT_Q8_0 ? p.K : WT == GT_Q4_K ? p.K / 2 : (int64_t)p.K * 2;  // bytes per row
         rw = make_rsrc((const uint8_t*)p.Wq + n0 * wrow, (p.N - n0) * wrow);
 #pragma unroll
         for (int i = 0; i < C::A_INSTR; ++i) {
             const int slot = (wid * C::A_INSTR + i) * 64 + lane;   // 1 KB block = 8 rows of 128 B
             const int row = slot >> 3, c = (slot & 7) ^ ((row >> 1) & 7);
-            const int m = min(row, p.M - m0 - 1);
+            const int m = min(max(m0 + row, 0), p.M - 1) - mb;
             va[i] = (uint32_t)(((int64_t)m * p.lda + 8 * c) * 2);
         }
         if constexpr (WT == GT_Q8_0) {
@@ -824,6 +825,76 @@ __device__ __forceinline__ void epilogue32_lds(const GemmParams& p, float16v (&a
     }
 }
 
+// Conformer convolution module after pointwise_conv1, in one pass over the
+// tile: GLU + pad mask (rows t >= valid -> 0) staged for the whole workgroup
+// tile in LDS as f32 [64 TM rows][32 TN channels], then the depthwise conv
+// over time (zero padding outside each item), its bias, the folded BatchNorm
+// and SiLU for the tile's inner 64 TM - 2 H rows (conformer.cpp:55-157).
+// m0 is the tile's first GEMM row (H rows before the first row written).
+template <int TM, int TN>
+__device__ __forceinline__ void epilogue32_glu_dw(const GemmParams& p, float16v (&acc)[TM][TN], float* G, int m0,
+                                                  int n0, int wm, int wn, int tid) {
+    static_assert(TN % 2 == 0, "GLU needs an even number of 32-column blocks");
+    constexpr int BM = 64 * TM, CW = 32 * TN, LDG = CW + 2, K = GLU_DW_K, H = (K - 1) / 2;
+    constexpr int CP = CW / 2, RG = 256 / CP, NR = BM - 2 * H, RPG = (NR + RG - 1) / RG;
+    static_assert(256 % CP == 0, "channel pairs must divide the workgroup");
+    const int lane = tid & 63, lr = 4 * (lane >> 5), lc = lane & 31;
+    // 1) GLU + pad mask into LDS
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int jj = 0; jj < TN / 2; ++jj) {
+            const int na = n0 + wn * 32 * TN + 64 * jj + lc;
+            const float ba = p.bias ? p.bias[min(na, p.N - 1)] : 0.f;
+            const float bg = p.bias ? p.bias[min(na + 32, p.N - 1)] : 0.f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int rr = wm * 32 * TM + 32 * i + 8 * (r >> 2) + lr + (r & 3);
+                const int m = m0 + rr;
+                float o = (acc[i][2 * jj][r] + ba) * sigmoid_dev(acc[i][2 * jj + 1][r] + bg);
+                if (m < 0 || m >= p.M) {
+                    o = 0.f;
+                } else if (p.valid) {
+                    const int b = m / p.T, t = m - b * p.T;
+                    if (t >= p.valid[b]) o = 0.f;
+                }
+                G[rr * LDG + wn * 16 * TN + 32 * jj + lc] = o;
+            }
+        }
+    __syncthreads();
+    // 2) depthwise conv: a thread owns 2 channels and RPG consecutive rows,
+    //    with the K-row window in registers
+    const int cp = tid % CP, g = tid / CP;
+    const int cl = 2 * cp, c = n0 / 2 + cl;
+    if (c >= p.N / 2) return;
+    float2v wk[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) wk[j] = (float2v){p.dw_w[c * K + j], p.dw_w[(c + 1) * K + j]};
+    const float2v db = p.dw_b ? (float2v){p.dw_b[c], p.dw_b[c + 1]} : (float2v){0.f, 0.f};
+    const float2v sc = {p.dw_scale[c], p.dw_scale[c + 1]}, sh = {p.dw_shift[c], p.dw_shift[c + 1]};
+    const int r0 = H + g * RPG;
+    float2v win[RPG + K - 1];
+#pragma unroll
+    for (int q = 0; q < RPG + K - 1; ++q) {
+        const int row = r0 - H + q;
+        win[q] = row < BM ? *(const float2v*)(G + row * LDG + cl) : (float2v){0.f, 0.f};
+    }
+#pragma unroll
+    for (int q = 0; q < RPG; ++q) {
+        const int r = r0 + q, m = m0 + r;
+        if (r < BM - H && m < p.M) {
+            const int t = m % p.T;
+            float2v a = {0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < K; ++j)
+                if ((unsigned)(t + j - H) < (unsigned)p.T) a += wk[j] * win[q + j];
+            const float2v y = (a + db) * sc + sh;
+            const half2v h = {(f16)silu_dev(y[0]), (f16)silu_dev(y[1])};
+            *(half2v*)((f16*)p.Y + (int64_t)m * p.ldy + c) = h;
+        }
+    }
+}
+
 template <int TM, int TN, int WT, int EPI, int NS = DMA_NS>
 __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmParams p) {
     typedef DmaCfg<TM, TN, WT> C;
@@ -833,10 +904,14 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmParams p) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wid = wave_id_uniform();
     const int wm = wid >> 1, wn = wid & 1;
-    const int nbm = cdiv_dev(p.M, C::BM), nbn = cdiv_dev(p.N, C::BN);
+    // The fused conv-module epilogue needs DWH rows of GLU output either side
+    // of the rows it writes: its tiles overlap by 2 DWH rows.
+    constexpr int DWH = EPI == EPI_GLU_DW ? (GLU_DW_K - 1) / 2 : 0;
+    constexpr int SM = C::BM - 2 * DWH;
+    const int nbm = cdiv_dev(p.M, SM), nbn = cdiv_dev(p.N, C::BN);
     int bm, bn;
     xcd_tile_2d(blockIdx.x, nbm, nbn, p.xcd_gm, bm, bn);
-    const int m0 = bm * C::BM, n0 = bn * C::BN;
+    const int m0 = bm * SM - DWH, n0 = bn * C::BN;
 
     float16v acc[TM][TN];
 #pragma unroll
@@ -868,6 +943,10 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmParams p) {
     }
     if constexpr (EPI == EPI_RELU2_F32) {
         epilogue32<EPI, f16, TM, TN>(p, acc, m0 + wm * TM * 32, n0 + wn * TN * 32, lane);
+    } else if constexpr (EPI == EPI_GLU_DW) {
+        static_assert(C::BM * (32 * TN + 2) * 4 <= NS * C::STAGE, "conv staging exceeds LDS ring");
+        __syncthreads();
+        epilogue32_glu_dw<TM, TN>(p, acc, (float*)smem, m0, n0, wm, wn, tid);
     } else if constexpr (EPI == EPI_RELU_TR) {
         if ((32 * TM) % p.trF == 0 && (32 * TN * p.trF) % 8 == 0 && p.N % 8 == 0) {
             static_assert(4 * 32 * TM * (32 * TN + 1) * 4 <= NS * C::STAGE, "epilogue staging exceeds LDS ring");
@@ -1367,7 +1446,7 @@ static void run_f32(const GemmParams& p, hipStream_t s) {
 // Row/column band split of the tile grid over the 8 XCDs that minimises the
 // L2-miss bytes gn*|A| + gm*|W| (each XCD reads its A band and its W band).
 static int choose_xcd_gm(const GemmParams& p, int WT, int BM, int BN) {
-    const int nbm = cdiv(p.M, BM), nbn = cdiv(p.N, BN);
+    const int nbm = cdiv(p.M, BM), nbn = cdiv(p.N, BN);   // BM: output rows per tile
     const double a_bytes = (double)p.M * p.K * 2;
     const double w_bytes = (double)p.N * p.K * (WT == GT_Q8_0 ? 34.0 / 32 : WT == GT_Q4_K ? 0.75 : 2.0);
     int best = 1;
@@ -1384,15 +1463,16 @@ static int choose_xcd_gm(const GemmParams& p, int WT, int BM, int BN) {
     return best_cost < 1e300 ? best : 1;
 }
 
-template <int TM, int TN, int WT, int EPI>
+template <int TM, int TN, int WT, int EPI, int NS = DMA_NS>
 static void run_dma(const GemmParams& p, hipStream_t s) {
-    if constexpr (EPI == EPI_GLU && TN % 2 != 0) {
+    if constexpr ((EPI == EPI_GLU || EPI == EPI_GLU_DW) && TN % 2 != 0) {
         throw std::logic_error("gemm: GLU epilogue dispatched to a 64-wide tile");
     } else {
-        const int tiles = cdiv(p.M, 64 * TM) * cdiv(p.N, 64 * TN);
+        const int sm = 64 * TM - (EPI == EPI_GLU_DW ? GLU_DW_K - 1 : 0);   // output rows per tile
+        const int tiles = cdiv(p.M, sm) * cdiv(p.N, 64 * TN);
         GemmParams q = p;
-        q.xcd_gm = choose_xcd_gm(p, WT, 64 * TM, 64 * TN);
-        launch((gemm_dma_kernel<TM, TN, WT, EPI>), dim3(tiles), dim3(256), 0, s, q);
+        q.xcd_gm = choose_xcd_gm(p, WT, sm, 64 * TN);
+        launch((gemm_dma_kernel<TM, TN, WT, EPI, NS>), dim3(tiles), dim3(256), 0, s, q);
         PKX_LAUNCH_CHECK();
     }
 }
@@ -1404,6 +1484,11 @@ static void dma_epi(int epi, const GemmParams& p, hipStream_t s) { PKX_EPI_SWITC
 template <int TM, int TN, int WT>
 static void f32_epi(int epi, const GemmParams& p, hipStream_t s) { PKX_EPI_SWITCH(run_f32, TM, TN, WT) }
 
+bool gemm_glu_dw_supported(Precision prec, int wtype, int N, int K) {
+    return prec == PREC_F16 && N % 64 == 0 && K % 64 == 0 &&
+           (wtype == GT_F16 || wtype == GT_Q8_0 || (wtype == GT_Q4_K && K % 256 == 0));
+}
+
 void launch_gemm(Precision prec, int wtype, int epi, const GemmParams& p, hipStream_t s) {
     require(p.M > 0 && p.N > 0 && p.K > 0, "gemm: empty shape");
     require(p.K % 8 == 0, "gemm: K must be a multiple of 8");
@@ -1411,6 +1496,21 @@ void launch_gemm(Precision prec, int wtype, int epi, const GemmParams& p, hipStr
     if (wtype == GT_Q8_0) require(p.K % 32 == 0, "gemm: q8_0 needs K % 32 == 0");
     if (wtype == GT_Q4_K) require(p.K % 256 == 0, "gemm: q4_K needs K % 256 == 0");
     if (epi == EPI_GLU) require(p.N % 64 == 0, "gemm: GLU needs N % 64 == 0");
+    if (epi == EPI_GLU_DW) {
+        require(gemm_glu_dw_supported(prec, wtype, p.N, p.K) && p.ldy % 8 == 0,
+                "gemm: fused conv-module epilogue needs the f16 path, N % 64 == 0, K % 64 == 0, ldy % 8 == 0");
+        require(p.dw_w && p.dw_scale && p.dw_shift && p.T >= 1, "gemm: fused conv-module epilogue parameters");
+    }
+    if (epi == EPI_GLU_DW) {
+        // 64 x 128 tiles (56 output rows, 64 channels) on a 2-stage ring, three
+        // workgroups per CU: the overlapping row tiles outnumber two slots per CU
+        switch (wtype) {
+        case GT_F16: run_dma<1, 2, GT_F16, EPI_GLU_DW, 2>(p, s); break;
+        case GT_Q8_0: run_dma<1, 2, GT_Q8_0, EPI_GLU_DW, 2>(p, s); break;
+        default: run_dma<1, 2, GT_Q4_K, EPI_GLU_DW, 2>(p, s); break;
+        }
+        return;
+    }
     const bool big = (int64_t)cdiv(p.M, 128) * cdiv(p.N, 128) >= 256;
     if (prec == PREC_F16 && p.K % 64 == 0 && p.ldy % 8 == 0 &&
         (wtype == GT_F16 || wtype == GT_Q8_0 || wtype == GT_Q4_K)) {
@@ -1422,14 +1522,15 @@ void launch_gemm(Precision prec, int wtype, int epi, const GemmParams& p, hipStr
         // tile at least 128 wide.
         const int64_t t22 = (int64_t)cdiv(p.M, 128) * cdiv(p.N, 128);
         const int64_t t21 = (int64_t)cdiv(p.M, 128) * cdiv(p.N, 64);
+        const bool glu = epi == EPI_GLU || epi == EPI_GLU_DW;
         if (wtype == GT_Q8_0) {
-            if (t22 >= 384 || (epi == EPI_GLU && t22 >= 256)) dma_epi<2, 2, GT_Q8_0>(epi, p, s);
-            else if (epi == EPI_GLU) dma_epi<1, 2, GT_Q8_0>(epi, p, s);
+            if (t22 >= 384 || (glu && t22 >= 256)) dma_epi<2, 2, GT_Q8_0>(epi, p, s);
+            else if (glu) dma_epi<1, 2, GT_Q8_0>(epi, p, s);
             else if (t21 >= 128) dma_epi<2, 1, GT_Q8_0>(epi, p, s);
             else dma_epi<1, 1, GT_Q8_0>(epi, p, s);
         } else if (wtype == GT_Q4_K) {
-            if (t22 >= 384 || (epi == EPI_GLU && t22 >= 256)) dma_epi<2, 2, GT_Q4_K>(epi, p, s);
-            else if (epi == EPI_GLU) dma_epi<1, 2, GT_Q4_K>(epi, p, s);
+            if (t22 >= 384 || (glu && t22 >= 256)) dma_epi<2, 2, GT_Q4_K>(epi, p, s);
+            else if (glu) dma_epi<1, 2, GT_Q4_K>(epi, p, s);
             else if (t21 >= 128) dma_epi<2, 1, GT_Q4_K>(epi, p, s);
             else dma_epi<1, 1, GT_Q4_K>(epi, p, s);
         } else {

@@ -20,8 +20,13 @@ enum Epi : int {
     EPI_RELU = 5,       // Y(act) = relu(acc + bias)                          subsampling.cpp:189-191
     EPI_RELU_TR = 6,    // relu + flatten to [b][t][c][f], 0 for t >= valid   subsampling.cpp:194-230
     EPI_RELU2_F32 = 7,  // Y(f32) = relu((acc + bias) + bias2)                joint.cpp:89-95
-    EPI_COUNT = 8
+    // GLU + pad mask, then depthwise conv over time (K = GLU_DW_K, zero padding
+    // at each item's edges) + bias + folded BatchNorm + SiLU     conformer.cpp:55-157
+    EPI_GLU_DW = 8,
+    EPI_COUNT = 9
 };
+
+constexpr int GLU_DW_K = 9;   // depthwise kernel size of the fused conv-module epilogue
 
 struct GemmParams {
     const void* A = nullptr;   // activations, row stride lda elements
@@ -38,7 +43,17 @@ struct GemmParams {
     int trF = 1;               // EPI_RELU_TR: rows are (b, t, f) with f fastest, F' = trF
     int M = 0, N = 0, K = 0;
     int xcd_gm = 1;            // tile grid split over the 8 XCDs: xcd_gm row bands x (8 / xcd_gm) column bands
+    // EPI_GLU_DW: depthwise weights [N/2][GLU_DW_K], its bias, BatchNorm folded to
+    // y = (conv + dw_b) * dw_scale + dw_shift (per channel)
+    const float* dw_w = nullptr;
+    const float* dw_b = nullptr;
+    const float* dw_scale = nullptr;
+    const float* dw_shift = nullptr;
 };
+
+// True when launch_gemm can run EPI_GLU_DW for this shape: the f16 MFMA path,
+// N (= 2 x channels) a multiple of 64 and K a multiple of 64.
+bool gemm_glu_dw_supported(Precision prec, int wtype, int N, int K);
 
 // Launch one GEMM.  prec selects the activation type (f16: MFMA 16x16x32 f16
 // with weights dequantised to f16 in registers; f32: MFMA 16x16x4 f32 with

@@ -648,6 +648,46 @@ void Model::gemm(const DevWeight& w, int epi, const void* A, int64_t lda, int64_
     mark(fam, false);
 }
 
+void Model::conv_front(const LayerDev& L, const void* A, int64_t M, const int* valid, int B, int T, void* Y,
+                       hipStream_t s) {
+    const ModelConfig& c = cfg_;
+    const int D = c.d_model;
+    if (c.conv_kernel == GLU_DW_K && gemm_glu_dw_supported(prec_, L.pw1.gtype, L.pw1.N, L.pw1.K)) {
+        // one pass: the GEMM epilogue stages GLU rows in LDS and runs the
+        // depthwise conv over time on them (conformer.cpp:48-157)
+        GemmParams p;
+        p.A = A;
+        p.lda = D;
+        p.Wq = L.pw1.q;
+        p.Ws = L.pw1.s;
+        p.bias = L.pw1_b;
+        p.Y = Y;
+        p.ldy = D;
+        p.valid = valid;
+        p.T = T;
+        p.M = (int)M;
+        p.N = L.pw1.N;
+        p.K = L.pw1.K;
+        p.dw_w = L.dw_w;
+        p.dw_b = L.dw_b;
+        p.dw_scale = L.bn_scale;
+        p.dw_shift = L.bn_shift;
+        mark(KF_GEMM_PW1_GLU, true);
+        launch_gemm(prec_, L.pw1.gtype, EPI_GLU_DW, p, s);
+        mark(KF_GEMM_PW1_GLU, false);
+        return;
+    }
+    // GLU output in a scratch buffer that is neither A nor Y
+    Ws& w = *ws_;
+    Buf& glu = (Y == w.g.p) ? w.u : w.g;
+    grow(glu, (size_t)M * D * (prec_ == PREC_F16 ? 2 : 4));
+    require(glu.p != A, "conv module: input aliases the GLU scratch");
+    gemm(L.pw1, EPI_GLU, A, D, M, L.pw1_b, glu.p, D, 1.f, valid, T, s, prec_, KF_GEMM_PW1_GLU);
+    mark(KF_DWCONV, true);
+    launch_dwconv_bn_silu(prec_, glu.p, Y, L.dw_w, L.dw_b, L.bn_scale, L.bn_shift, B, T, D, c.conv_kernel, s);
+    mark(KF_DWCONV, false);
+}
+
 void Model::ensure_ws(int B, int T_max) {
     const ModelConfig& c = cfg_;
     const size_t as = prec_ == PREC_F16 ? 2 : 4;
@@ -804,15 +844,12 @@ void Model::layer_body(int l, float* x, int B, int T, const int* d_valid, bool f
     gemm(L.wo, EPI_RESID, w.h.p, D, M, L.bo, x, D, 1.f, nullptr, 1, s, prec_, KF_GEMM_OUT);
     // Stage C: x += conv(LN(x))
     ln(L.conv_ln_g, L.conv_ln_b);
-    gemm(L.pw1, EPI_GLU, w.h.p, D, M, L.pw1_b, w.g.p, D, 1.f, d_valid, T, s, prec_, KF_GEMM_PW1_GLU);
-    mark(KF_DWCONV, true);
-    launch_dwconv_bn_silu(prec_, w.g.p, w.h.p, L.dw_w, L.dw_b, L.bn_scale, L.bn_shift, B, T, D, c.conv_kernel, s);
-    mark(KF_DWCONV, false);
+    conv_front(L, w.h.p, M, d_valid, B, T, w.g.p, s);
     if (conv_capture_) {
-        gemm(L.pw2, EPI_STORE_F32, w.h.p, D, M, L.pw2_b, conv_capture_, D, 1.f, nullptr, 1, s, prec_, KF_GEMM_PW2);
+        gemm(L.pw2, EPI_STORE_F32, w.g.p, D, M, L.pw2_b, conv_capture_, D, 1.f, nullptr, 1, s, prec_, KF_GEMM_PW2);
         launch_add_f32(x, conv_capture_, M * D, s);
     } else {
-        gemm(L.pw2, EPI_RESID, w.h.p, D, M, L.pw2_b, x, D, 1.f, nullptr, 1, s, prec_, KF_GEMM_PW2);
+        gemm(L.pw2, EPI_RESID, w.g.p, D, M, L.pw2_b, x, D, 1.f, nullptr, 1, s, prec_, KF_GEMM_PW2);
     }
     // Stage D: x += 0.5 * FFN2(LN(x)); x = LN_out(x) [fused with next layer's LN_ff1]
     ln(L.ff2_ln_g, L.ff2_ln_b);
@@ -954,8 +991,7 @@ void Model::conv_module_forward(int layer, const float* cin, int B, int T, const
     const int64_t M = (int64_t)B * T;
     Ws& w = *ws_;
     void* xa = cast_to_act(cin, M * D, s);
-    gemm(L.pw1, EPI_GLU, xa, D, M, L.pw1_b, w.g.p, D, 1.f, w.d_valid + 3 * w.Bcap, T, s, prec_, KF_GEMM_PW1_GLU);
-    launch_dwconv_bn_silu(prec_, w.g.p, w.h.p, L.dw_w, L.dw_b, L.bn_scale, L.bn_shift, B, T, D, c.conv_kernel, s);
+    conv_front(L, xa, M, w.d_valid + 3 * w.Bcap, B, T, w.h.p, s);
     gemm(L.pw2, EPI_STORE_F32, w.h.p, D, M, L.pw2_b, out, D, 1.f, nullptr, 1, s, prec_, KF_GEMM_PW2);
 }
 

@@ -124,6 +124,10 @@ private:
     const HostTensor* find(const std::string& n) const;
     const HostTensor& need(const std::string& n) const;
     void ensure_ws(int B, int T_max);
+    // pointwise_conv1 + GLU + pad mask + depthwise conv + bias + folded BN + SiLU
+    // of the conv module, from the normed input A [M][D] to Y [M][D]
+    void conv_front(const LayerDev& L, const void* A, int64_t M, const int* valid, int B, int T, void* Y,
+                    hipStream_t s);
     void gemm(const DevWeight& w, int epi, const void* A, int64_t lda, int64_t M,
               const float* bias, void* Y, int64_t ldy, float alpha, const int* valid, int T,
               hipStream_t s, Precision prec, int fam, const float* bias2 = nullptr, int trF = 1);

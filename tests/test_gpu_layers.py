@@ -21,6 +21,9 @@ CASES = {
     "q8_dk64": (dict(d_model=256, n_heads=4, ff_dim=512), "q8_0", 1),
     "q4k_dk128": (dict(d_model=256, n_heads=2, ff_dim=512), "q4_k", 1),
     "f16_dk64": (dict(d_model=128, n_heads=2, ff_dim=256, attn_bias=False, conv_bias=False), "f16", 1),
+    # depthwise kernel 5: the f16 path runs GLU GEMM + separate depthwise pass
+    # (kernel 9 takes the fused one-pass conv-module GEMM)
+    "f16_k5": (dict(d_model=128, n_heads=2, ff_dim=256, conv_kernel=5), "f16", 1),
 }
 
 
