@@ -895,15 +895,24 @@ __device__ __forceinline__ void epilogue32_glu_dw(const GemmParams& p, float16v 
     }
 }
 
-template <int TM, int TN, int WT, int EPI, int NS = DMA_NS>
-__global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmParams p) {
+// KG = 2: eight waves in two groups of four; group g streams K slabs
+// [g nk/2, (g+1) nk/2) through its own LDS ring, and the two partial tiles are
+// summed in LDS (group 0 + group 1, a fixed order) before group 0 runs the
+// epilogue.  For grids of about one tile per CU: two waves per SIMD instead of
+// one.
+template <int TM, int TN, int WT, int EPI, int NS = DMA_NS, int KG = 1>
+__global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(GemmParams p) {
     typedef DmaCfg<TM, TN, WT> C;
     static_assert(NS == 2 || NS == 3, "LDS ring depth");
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * C::STAGE];
+    static_assert(KG == 1 || (KG == 2 && (EPI == EPI_STORE || EPI == EPI_STORE_F32 || EPI == EPI_RESID ||
+                                          EPI == EPI_SILU)), "K groups: LDS-staged epilogues only");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem_all[KG * NS * C::STAGE];
 
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wid = wave_id_uniform();
+    const int tid = threadIdx.x & 255, lane = tid & 63;
+    const int wid_all = wave_id_uniform();
+    const int kg = wid_all >> 2, wid = wid_all & 3;
     const int wm = wid >> 1, wn = wid & 1;
+    uint8_t* smem = smem_all + kg * NS * C::STAGE;
     // The fused conv-module epilogue needs DWH rows of GLU output either side
     // of the rows it writes: its tiles overlap by 2 DWH rows.
     constexpr int DWH = EPI == EPI_GLU_DW ? (GLU_DW_K - 1) / 2 : 0;
@@ -919,11 +928,11 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmParams p) {
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = (float16v){};
 
-    const int nk = p.K / 64;
+    const int nk = p.K / 64 / KG, kb = kg * nk * 64;   // slabs of this group, its first K
     DmaSrc<TM, TN, WT> src;
     src.init(p, m0, n0, wid, lane);
-    src.issue(smem, 0);
-    if (NS == 3 && nk > 1) src.issue(smem + C::STAGE, 64);
+    src.issue(smem, kb);
+    if (NS == 3 && nk > 1) src.issue(smem + C::STAGE, kb + 64);
     int st = 0;
     for (int kt = 0; kt < nk; ++kt) {
         // this wave's DMAs for slab kt have landed (with 3 stages slab kt+1 may
@@ -936,10 +945,34 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmParams p) {
         __builtin_amdgcn_s_barrier();
         if (kt + NS - 1 < nk) {
             const int st2 = st + NS - 1 >= NS ? st - 1 : st + NS - 1;
-            src.issue(smem + st2 * C::STAGE, (kt + NS - 1) * 64);
+            src.issue(smem + st2 * C::STAGE, kb + (kt + NS - 1) * 64);
         }
         mma32_slab<TM, TN, WT>(smem + st * C::STAGE, acc, wm, wn, lane);
         st = st + 1 == NS ? 0 : st + 1;
+    }
+    if constexpr (KG == 2) {
+        // lane-major [wave][register][lane] f32: conflict-free both ways
+        constexpr int R = TM * TN * 16;
+        static_assert(4 * R * 64 * 4 <= KG * NS * C::STAGE, "partial tile exceeds LDS");
+        float* red = (float*)smem_all + wid * R * 64 + lane;
+        __syncthreads();
+        if (kg == 1) {
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) red[((i * TN + j) * 16 + r) * 64] = acc[i][j][r];
+        }
+        __syncthreads();
+        if (kg == 0) {
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[i][j][r] += red[((i * TN + j) * 16 + r) * 64];
+        }
     }
     if constexpr (EPI == EPI_RELU2_F32) {
         epilogue32<EPI, f16, TM, TN>(p, acc, m0 + wm * TM * 32, n0 + wn * TN * 32, lane);
@@ -965,7 +998,7 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmParams p) {
         if constexpr (whole) {
             __syncthreads();
             float* wsm = (float*)smem + wid * (32 * TM) * ((EPI == EPI_GLU ? 16 * TN : 32 * TN) + 4);
-            epilogue32_lds<EPI, TM, TN>(p, acc, wsm, m0 + wm * TM * 32, n0 + wn * TN * 32, lane);
+            if (kg == 0) epilogue32_lds<EPI, TM, TN>(p, acc, wsm, m0 + wm * TM * 32, n0 + wn * TN * 32, lane);
         } else {
             constexpr int TH = TM / 2;
             float* wsm = (float*)smem + wid * (32 * TH) * ((EPI == EPI_GLU ? 16 * TN : 32 * TN) + 4);
@@ -977,7 +1010,9 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmParams p) {
 #pragma unroll
                     for (int j = 0; j < TN; ++j) part[i][j] = acc[hh * TH + i][j];
                 __syncthreads();
-                epilogue32_lds<EPI, TH, TN>(p, part, wsm, m0 + wm * TM * 32 + hh * TH * 32, n0 + wn * TN * 32, lane);
+                if (kg == 0)
+                    epilogue32_lds<EPI, TH, TN>(p, part, wsm, m0 + wm * TM * 32 + hh * TH * 32, n0 + wn * TN * 32,
+                                                lane);
             }
         }
     }
@@ -1463,16 +1498,17 @@ static int choose_xcd_gm(const GemmParams& p, int WT, int BM, int BN) {
     return best_cost < 1e300 ? best : 1;
 }
 
-template <int TM, int TN, int WT, int EPI, int NS = DMA_NS>
+template <int TM, int TN, int WT, int EPI, int NS = DMA_NS, int KG = 1>
 static void run_dma(const GemmParams& p, hipStream_t s) {
     if constexpr ((EPI == EPI_GLU || EPI == EPI_GLU_DW) && TN % 2 != 0) {
         throw std::logic_error("gemm: GLU epilogue dispatched to a 64-wide tile");
     } else {
+        require(p.K % (64 * KG) == 0, "gemm: K must split into whole 64-wide slabs per K group");
         const int sm = 64 * TM - (EPI == EPI_GLU_DW ? GLU_DW_K - 1 : 0);   // output rows per tile
         const int tiles = cdiv(p.M, sm) * cdiv(p.N, 64 * TN);
         GemmParams q = p;
         q.xcd_gm = choose_xcd_gm(p, WT, sm, 64 * TN);
-        launch((gemm_dma_kernel<TM, TN, WT, EPI, NS>), dim3(tiles), dim3(256), 0, s, q);
+        launch((gemm_dma_kernel<TM, TN, WT, EPI, NS, KG>), dim3(tiles), dim3(256 * KG), 0, s, q);
         PKX_LAUNCH_CHECK();
     }
 }
@@ -1481,6 +1517,19 @@ template <int TM, int TN, int WT>
 static void f16_epi(int epi, const GemmParams& p, hipStream_t s) { PKX_EPI_SWITCH(run_f16, TM, TN, WT) }
 template <int TM, int TN, int WT>
 static void dma_epi(int epi, const GemmParams& p, hipStream_t s) { PKX_EPI_SWITCH(run_dma, TM, TN, WT) }
+// 128 x 64 tiles with two K groups (eight waves): long-K products whose grid is
+// about one tile per CU
+template <int WT>
+static bool dma_kg2(int epi, const GemmParams& p, hipStream_t s) {
+    if (p.K % 128 != 0 || p.K < 2048 || (int64_t)cdiv(p.M, 128) * cdiv(p.N, 64) > 256) return false;
+    switch (epi) {
+    case EPI_STORE: run_dma<2, 1, WT, EPI_STORE, DMA_NS, 2>(p, s); return true;
+    case EPI_STORE_F32: run_dma<2, 1, WT, EPI_STORE_F32, DMA_NS, 2>(p, s); return true;
+    case EPI_RESID: run_dma<2, 1, WT, EPI_RESID, DMA_NS, 2>(p, s); return true;
+    case EPI_SILU: run_dma<2, 1, WT, EPI_SILU, DMA_NS, 2>(p, s); return true;
+    default: return false;
+    }
+}
 template <int TM, int TN, int WT>
 static void f32_epi(int epi, const GemmParams& p, hipStream_t s) { PKX_EPI_SWITCH(run_f32, TM, TN, WT) }
 
@@ -1523,6 +1572,9 @@ void launch_gemm(Precision prec, int wtype, int epi, const GemmParams& p, hipStr
         const int64_t t22 = (int64_t)cdiv(p.M, 128) * cdiv(p.N, 128);
         const int64_t t21 = (int64_t)cdiv(p.M, 128) * cdiv(p.N, 64);
         const bool glu = epi == EPI_GLU || epi == EPI_GLU_DW;
+        if (wtype == GT_Q8_0 && dma_kg2<GT_Q8_0>(epi, p, s)) return;
+        if (wtype == GT_Q4_K && dma_kg2<GT_Q4_K>(epi, p, s)) return;
+        if (wtype == GT_F16 && dma_kg2<GT_F16>(epi, p, s)) return;
         if (wtype == GT_Q8_0) {
             if (t22 >= 384 || (glu && t22 >= 256)) dma_epi<2, 2, GT_Q8_0>(epi, p, s);
             else if (glu) dma_epi<1, 2, GT_Q8_0>(epi, p, s);
