@@ -52,16 +52,20 @@ def family_work(cfg, B, Tp):
     }
 
 
-def layernorm_bytes(cfg, B, Tp):
+def layernorm_bytes(cfg, B, Tp, launches):
+    """HBM bytes per LayerNorm launch.  Unfolded (4 L + 1 launches): norm_self_att,
+    norm_conv, norm_feed_forward2 and layer 0's norm_feed_forward1 read the f32
+    stream and write f16; norm_out is fused with the next layer's
+    norm_feed_forward1 (and also writes the f32 stream back), the last one f32
+    only.  Folded (L + 1 launches): only layer 0's norm_feed_forward1 and the
+    norm_out passes remain."""
     D, L, M = cfg.d_model, cfg.n_layers, B * Tp
     single = M * D * (4 + 2)
     fused = M * D * (4 + 4 + 2)
     last = M * D * (4 + 4)
-    # per layer: norm_self_att, norm_conv, norm_feed_forward2 (+ layer 0's norm_feed_forward1);
-    # norm_out fused with the next layer's norm_feed_forward1, the last one f32-only
-    total = (3 * L + 1) * single + (L - 1) * fused + last
-    launches = 4 * L + 1
-    return total / launches
+    if launches == L + 1:
+        return (single + (L - 1) * fused + last) / launches
+    return ((3 * L + 1) * single + (L - 1) * fused + last) / launches
 
 
 def other_config(name, qtype, cfg_kw, lens, T_max, steps, warmup, stream):
@@ -209,7 +213,7 @@ def main():
         if fam in work:
             unit, per = work[fam]
             if fam == "layernorm":
-                per = layernorm_bytes(cfg, B, Tp)
+                per = layernorm_bytes(cfg, B, Tp, round(n / n_prof))
             if unit == "TFLOP/s":
                 rec.update(achieved=round(per / avg_s / 1e12, 2), unit=unit,
                            frac=round(per / avg_s / 1e12 / PEAK_F16_TFLOPS, 4))

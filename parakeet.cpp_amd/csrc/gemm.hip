@@ -23,6 +23,22 @@ __device__ __forceinline__ int xcd_tile(int bid, int total) {
 // Wave index as a wave-uniform (scalar) value.
 __device__ __forceinline__ int wave_id_uniform() { return __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6); }
 
+// Sum over aligned groups of n consecutive lanes (n = 1, 2, 4, 8 or 16,
+// wave-uniform), every lane of a group receiving the total: DPP steps
+// quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror.
+template <int CTRL> __device__ __forceinline__ float dpp_add(float v) {
+    const int o = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false);
+    return v + __builtin_bit_cast(float, o);
+}
+__device__ __forceinline__ float group_sum(float v, int n) {
+    if (n > 1) v = dpp_add<0xB1>(v);    // quad_perm [1,0,3,2]
+    if (n > 2) v = dpp_add<0x4E>(v);    // quad_perm [2,3,0,1]
+    if (n > 4) v = dpp_add<0x141>(v);   // row_half_mirror
+    if (n > 8) v = dpp_add<0x140>(v);   // row_mirror
+    return v;
+}
+
+
 // 2-D XCD blocking: the nbm x nbn tile grid is cut into gm row bands x gn
 // column bands (gm * gn = 8), one rectangle per XCD, so an XCD's L2 sees only
 // its band of A rows and its band of weight columns (gn*|A| + gm*|W| bytes
@@ -735,9 +751,14 @@ __device__ __forceinline__ void epilogue32_relu_tr(const GemmParams& p, float16v
     }
 }
 
+// fold: ftab (LDS) holds {mean, rstd} of the workgroup tile's rows for a
+// folded LayerNorm, indexed from the tile's first row; trow0 is this wave's
+// first row within the tile.  (ftab is always a valid LDS address, so that its
+// loads stay LDS loads.)
 template <int EPI, int TM, int TN>
 __device__ __forceinline__ void epilogue32_lds(const GemmParams& p, float16v (&acc)[TM][TN], float* wsm,
-                                               int mw, int nw, int lane) {
+                                               int mw, int nw, int lane, bool fold = false,
+                                               const float2v* ftab = nullptr, int trow0 = 0) {
     constexpr int WR = 32 * TM;
     constexpr int WC = EPI == EPI_GLU ? 16 * TN : 32 * TN;   // output columns of this wave
     constexpr int LDW = WC + 4;
@@ -746,17 +767,29 @@ __device__ __forceinline__ void epilogue32_lds(const GemmParams& p, float16v (&a
     if constexpr (EPI == EPI_GLU) {
         static_assert(TN % 2 == 0, "GLU needs an even number of 32-column blocks");
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+        for (int i = 0; i < TM; ++i) {
+            float2v st[16];   // folded LayerNorm {mean, rstd} of this lane's 16 rows
+            if (fold) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) st[r] = ftab[trow0 + 32 * i + 8 * (r >> 2) + lr + (r & 3)];
+            }
 #pragma unroll
             for (int jj = 0; jj < TN / 2; ++jj) {
                 const int na = nw + 64 * jj + lc;
                 const float ba = p.bias ? p.bias[min(na, p.N - 1)] : 0.f;
                 const float bg = p.bias ? p.bias[min(na + 32, p.N - 1)] : 0.f;
+                const float ca = fold ? p.fold_c1[min(na, p.N - 1)] : 0.f;
+                const float cg = fold ? p.fold_c1[min(na + 32, p.N - 1)] : 0.f;
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int rr = 32 * i + 8 * (r >> 2) + lr + (r & 3);
                     const int m = mw + rr;
-                    float o = (acc[i][2 * jj][r] + ba) * sigmoid_dev(acc[i][2 * jj + 1][r] + bg);
+                    float xa = acc[i][2 * jj][r], xg = acc[i][2 * jj + 1][r];
+                    if (fold) {
+                        xa = st[r].y * (xa - st[r].x * ca);
+                        xg = st[r].y * (xg - st[r].x * cg);
+                    }
+                    float o = (xa + ba) * sigmoid_dev(xg + bg);
                     if (p.valid && m < p.M) {
                         const int b = m / p.T, t = m - b * p.T;
                         if (t >= p.valid[b]) o = 0.f;
@@ -764,30 +797,67 @@ __device__ __forceinline__ void epilogue32_lds(const GemmParams& p, float16v (&a
                     wsm[rr * LDW + 32 * jj + lc] = o;
                 }
             }
+        }
     } else {
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+        for (int i = 0; i < TM; ++i) {
+            float2v st[16];   // folded LayerNorm {mean, rstd} of this lane's 16 rows
+            if (fold) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) st[r] = ftab[trow0 + 32 * i + 8 * (r >> 2) + lr + (r & 3)];
+            }
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
                 const int n = nw + 32 * j + lc;
                 const float bb = p.bias ? p.bias[min(n, p.N - 1)] : 0.f;
+                const float c1 = fold ? p.fold_c1[min(n, p.N - 1)] : 0.f;
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int rr = 32 * i + 8 * (r >> 2) + lr + (r & 3);
-                    float v = acc[i][j][r] + bb;
+                    float v = acc[i][j][r];
+                    if (fold) v = st[r].y * (v - st[r].x * c1);
+                    v += bb;
                     if constexpr (EPI == EPI_SILU) v = silu_dev(v);
                     else if constexpr (EPI == EPI_RELU) v = v > 0.f ? v : 0.f;
                     else v = v * p.alpha;    // STORE, STORE_F32, RESID
                     wsm[rr * LDW + 32 * j + lc] = v;
                 }
             }
+        }
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's LDS writes are done
     __builtin_amdgcn_wave_barrier();
     // 2) coalesced copy-out
     const int ncol = EPI == EPI_GLU ? p.N / 2 : p.N;
     const int n0 = EPI == EPI_GLU ? nw / 2 : nw;
-    if constexpr (EPI == EPI_STORE_F32 || EPI == EPI_RESID) {
+    if constexpr (EPI == EPI_RESID_LN) {
+        // 8 lanes hold one row's 32-column group: residual update, x * gamma in
+        // f16, and the group's mean and sum of squared deviations (two passes
+        // over registers, shuffles within the 8 lanes)
+        constexpr int CPR = WC / 4;
+        static_assert(CPR % 8 == 0 && 64 % CPR == 0, "RESID_LN: whole 32-column groups per wave");
+        const int G = p.N / 32;
+        const int cc = (lane % CPR) * 4, n = n0 + cc;   // a lane's columns are the same on every row
+        const float4v g = n < p.N ? *(const float4v*)(p.ln_g + n) : (float4v){0.f, 0.f, 0.f, 0.f};
+        for (int c = lane; c < WR * CPR; c += 64) {
+            const int rr = c / CPR;
+            const int m = mw + rr;
+            if (m < p.M && n < p.N) {   // uniform over the 8 lanes of a group (same row, N % 32 == 0)
+                const float4v v = *(const float4v*)(wsm + rr * LDW + cc);
+                float* dst = (float*)p.Y + (int64_t)m * p.ldy + n;
+                const float4v x = *(const float4v*)dst + v;
+                *(float4v*)dst = x;
+                const half4v h = {(f16)(x[0] * g[0]), (f16)(x[1] * g[1]), (f16)(x[2] * g[2]), (f16)(x[3] * g[3])};
+                *(half4v*)((f16*)p.ln_h + (int64_t)m * p.N + n) = h;
+                const float mean = group_sum((x[0] + x[1]) + (x[2] + x[3]), 8) * (1.0f / 32.0f);
+                float d2 = 0.f;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) d2 += (x[e] - mean) * (x[e] - mean);
+                d2 = group_sum(d2, 8);
+                if ((lane & 7) == 0) ((float2v*)p.ln_stats)[(int64_t)m * G + n / 32] = (float2v){mean, d2};
+            }
+        }
+    } else if constexpr (EPI == EPI_STORE_F32 || EPI == EPI_RESID) {
         constexpr int CPR = WC / 4;   // float4 chunks per row
         for (int c = lane; c < WR * CPR; c += 64) {
             const int rr = c / CPR, cc = (c % CPR) * 4;
@@ -833,7 +903,7 @@ __device__ __forceinline__ void epilogue32_lds(const GemmParams& p, float16v (&a
 // m0 is the tile's first GEMM row (H rows before the first row written).
 template <int TM, int TN>
 __device__ __forceinline__ void epilogue32_glu_dw(const GemmParams& p, float16v (&acc)[TM][TN], float* G, int m0,
-                                                  int n0, int wm, int wn, int tid) {
+                                                  int n0, int wm, int wn, int tid, bool fold, const float2v* ftab) {
     static_assert(TN % 2 == 0, "GLU needs an even number of 32-column blocks");
     constexpr int BM = 64 * TM, CW = 32 * TN, LDG = CW + 2, K = GLU_DW_K, H = (K - 1) / 2;
     constexpr int CP = CW / 2, RG = 256 / CP, NR = BM - 2 * H, RPG = (NR + RG - 1) / RG;
@@ -847,11 +917,19 @@ __device__ __forceinline__ void epilogue32_glu_dw(const GemmParams& p, float16v 
             const int na = n0 + wn * 32 * TN + 64 * jj + lc;
             const float ba = p.bias ? p.bias[min(na, p.N - 1)] : 0.f;
             const float bg = p.bias ? p.bias[min(na + 32, p.N - 1)] : 0.f;
+            const float ca = fold ? p.fold_c1[min(na, p.N - 1)] : 0.f;
+            const float cg = fold ? p.fold_c1[min(na + 32, p.N - 1)] : 0.f;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int rr = wm * 32 * TM + 32 * i + 8 * (r >> 2) + lr + (r & 3);
                 const int m = m0 + rr;
-                float o = (acc[i][2 * jj][r] + ba) * sigmoid_dev(acc[i][2 * jj + 1][r] + bg);
+                float xa = acc[i][2 * jj][r], xg = acc[i][2 * jj + 1][r];
+                if (fold) {
+                    const float2v st = ftab[rr];
+                    xa = st.y * (xa - st.x * ca);
+                    xg = st.y * (xg - st.x * cg);
+                }
+                float o = (xa + ba) * sigmoid_dev(xg + bg);
                 if (m < 0 || m >= p.M) {
                     o = 0.f;
                 } else if (p.valid) {
@@ -895,6 +973,55 @@ __device__ __forceinline__ void epilogue32_glu_dw(const GemmParams& p, float16v 
     }
 }
 
+// Folded LayerNorm row statistics of a tile.  The tile's rows hold G = N/32
+// partials {mean, sum of squared deviations} each, BM * G * 8 contiguous bytes
+// (rows clamped to [0, M)): prefetch() loads them as 16-byte chunks before the
+// main loop (thread t takes chunks t, t + 256, ...; G/2 consecutive chunks per
+// row, so a row's chunks sit in G/2 consecutive lanes of one wave), and
+// finish() combines each row with shuffles (Chan's pairwise formula) into
+// {mean, 1/sqrt(var + eps)} in LDS.
+template <int BM>
+struct FoldStats {
+    static constexpr int MAXC = BM * 32 / 2 / 256;   // chunks per thread for G <= 32
+    float4v c[MAXC];
+    __device__ __forceinline__ void prefetch(const GemmParams& p, int m0, int t) {
+        const int lc = __builtin_ctz(p.fold_groups / 2), total = BM << lc;   // log2 chunks per row
+#pragma unroll
+        for (int i = 0; i < MAXC; ++i) {
+            const int ch = t + 256 * i;
+            if (ch < total) {
+                const int r = ch >> lc, m = min(max(m0 + r, 0), p.M - 1);
+                c[i] = *((const float4v*)p.fold_stats + ((int64_t)m << lc) + (ch & ((1 << lc) - 1)));
+            } else {
+                c[i] = (float4v){0.f, 0.f, 0.f, 0.f};
+            }
+        }
+    }
+    template <int CPR>
+    __device__ __forceinline__ void finish_t(const GemmParams& p, float2v* tab, int t) const {
+        constexpr int G = 2 * CPR, NC = BM * CPR / 256 > 0 ? BM * CPR / 256 : 1;
+        static_assert(NC <= MAXC, "chunks");
+#pragma unroll
+        for (int i = 0; i < NC; ++i) {
+            const int ch = t + 256 * i;
+            const float mean = group_sum(c[i][0] + c[i][2], CPR) * (1.0f / G);
+            const float da = c[i][0] - mean, db = c[i][2] - mean;
+            const float q = group_sum(c[i][1] + c[i][3] + 32.0f * (da * da + db * db), CPR);
+            if (ch < BM * CPR && (ch & (CPR - 1)) == 0)
+                tab[ch / CPR] = (float2v){mean, rsqrtf(q * (1.0f / (32.0f * G)) + p.fold_eps)};
+        }
+    }
+    __device__ __forceinline__ void finish(const GemmParams& p, float2v* tab, int t) const {
+        switch (p.fold_groups) {
+        case 2: finish_t<1>(p, tab, t); break;
+        case 4: finish_t<2>(p, tab, t); break;
+        case 8: finish_t<4>(p, tab, t); break;
+        case 16: finish_t<8>(p, tab, t); break;
+        default: finish_t<16>(p, tab, t); break;
+        }
+    }
+};
+
 // KG = 2: eight waves in two groups of four; group g streams K slabs
 // [g nk/2, (g+1) nk/2) through its own LDS ring, and the two partial tiles are
 // summed in LDS (group 0 + group 1, a fixed order) before group 0 runs the
@@ -905,7 +1032,8 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
     typedef DmaCfg<TM, TN, WT> C;
     static_assert(NS == 2 || NS == 3, "LDS ring depth");
     static_assert(KG == 1 || (KG == 2 && (EPI == EPI_STORE || EPI == EPI_STORE_F32 || EPI == EPI_RESID ||
-                                          EPI == EPI_SILU)), "K groups: LDS-staged epilogues only");
+                                          EPI == EPI_SILU || EPI == EPI_RESID_LN)),
+                  "K groups: LDS-staged epilogues only");
     __shared__ __attribute__((aligned(1024))) uint8_t smem_all[KG * NS * C::STAGE];
 
     const int tid = threadIdx.x & 255, lane = tid & 63;
@@ -927,6 +1055,14 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
     for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = (float16v){};
+
+    // folded LayerNorm: the row statistics' loads go out before the DMAs (oldest
+    // in the vector-memory counter) and are combined after the main loop
+    constexpr bool FOLD = EPI == EPI_STORE || EPI == EPI_SILU || EPI == EPI_GLU || EPI == EPI_GLU_DW;
+    FoldStats<FOLD ? C::BM : 8> fst;
+    if constexpr (FOLD) {
+        if (p.fold_stats && kg == 0) fst.prefetch(p, m0, tid);
+    }
 
     const int nk = p.K / 64 / KG, kb = kg * nk * 64;   // slabs of this group, its first K
     DmaSrc<TM, TN, WT> src;
@@ -974,12 +1110,22 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
                     for (int r = 0; r < 16; ++r) acc[i][j][r] += red[((i * TN + j) * 16 + r) * 64];
         }
     }
+    // folded LayerNorm: the tile's row statistics at the top of the LDS block
+    // (published by the barrier before the staging below)
+    float2v* ftab = (float2v*)(smem_all + KG * NS * C::STAGE) - C::BM;
+    const bool fold = FOLD && p.fold_stats != nullptr;
+    if constexpr (FOLD) {
+        if (fold) {
+            __syncthreads();
+            if (kg == 0) fst.finish(p, ftab, tid);
+        }
+    }
     if constexpr (EPI == EPI_RELU2_F32) {
         epilogue32<EPI, f16, TM, TN>(p, acc, m0 + wm * TM * 32, n0 + wn * TN * 32, lane);
     } else if constexpr (EPI == EPI_GLU_DW) {
-        static_assert(C::BM * (32 * TN + 2) * 4 <= NS * C::STAGE, "conv staging exceeds LDS ring");
+        static_assert(C::BM * (32 * TN + 2) * 4 + C::BM * 8 <= NS * C::STAGE, "conv staging exceeds LDS ring");
         __syncthreads();
-        epilogue32_glu_dw<TM, TN>(p, acc, (float*)smem, m0, n0, wm, wn, tid);
+        epilogue32_glu_dw<TM, TN>(p, acc, (float*)smem, m0, n0, wm, wn, tid, fold, ftab);
     } else if constexpr (EPI == EPI_RELU_TR) {
         if ((32 * TM) % p.trF == 0 && (32 * TN * p.trF) % 8 == 0 && p.N % 8 == 0) {
             static_assert(4 * 32 * TM * (32 * TN + 1) * 4 <= NS * C::STAGE, "epilogue staging exceeds LDS ring");
@@ -992,13 +1138,17 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
     } else {
         // the LDS ring is free once every wave has finished its last slab; tiles
         // whose staging exceeds it leave in row halves
-        constexpr bool whole = 4 * 32 * TM * (32 * TN + 4) * 4 <= NS * C::STAGE;
-        static_assert(whole || (TM % 2 == 0 && 4 * 16 * TM * (32 * TN + 4) * 4 <= NS * C::STAGE),
+        // (the folded-LayerNorm row table sits above the staging area)
+        constexpr int TAB = FOLD && KG == 1 ? C::BM * 8 : 0;
+        constexpr bool whole = 4 * 32 * TM * (32 * TN + 4) * 4 + TAB <= NS * C::STAGE;
+        static_assert(whole || (TM % 2 == 0 && 4 * 16 * TM * (32 * TN + 4) * 4 + TAB <= NS * C::STAGE),
                       "epilogue staging exceeds LDS ring");
         if constexpr (whole) {
             __syncthreads();
             float* wsm = (float*)smem + wid * (32 * TM) * ((EPI == EPI_GLU ? 16 * TN : 32 * TN) + 4);
-            if (kg == 0) epilogue32_lds<EPI, TM, TN>(p, acc, wsm, m0 + wm * TM * 32, n0 + wn * TN * 32, lane);
+            if (kg == 0)
+                epilogue32_lds<EPI, TM, TN>(p, acc, wsm, m0 + wm * TM * 32, n0 + wn * TN * 32, lane, fold,
+                                            ftab, wm * TM * 32);
         } else {
             constexpr int TH = TM / 2;
             float* wsm = (float*)smem + wid * (32 * TH) * ((EPI == EPI_GLU ? 16 * TN : 32 * TN) + 4);
@@ -1012,7 +1162,7 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
                 __syncthreads();
                 if (kg == 0)
                     epilogue32_lds<EPI, TH, TN>(p, part, wsm, m0 + wm * TM * 32 + hh * TH * 32, n0 + wn * TN * 32,
-                                                lane);
+                                                lane, fold, ftab, wm * TM * 32 + hh * TH * 32);
             }
         }
     }
@@ -1477,6 +1627,20 @@ static void run_f32(const GemmParams& p, hipStream_t s) {
     case EPI_RELU2_F32: RUN<TM, TN, WT, EPI_RELU2_F32>(p, s); break;            \
     default: throw std::invalid_argument("gemm: bad epilogue");                 \
     }
+// the LDS-DMA kernel also has the residual + LayerNorm-statistics epilogue
+#define PKX_EPI_SWITCH_DMA(RUN, TM, TN, WT)                                     \
+    switch (epi) {                                                              \
+    case EPI_STORE: RUN<TM, TN, WT, EPI_STORE>(p, s); break;                    \
+    case EPI_STORE_F32: RUN<TM, TN, WT, EPI_STORE_F32>(p, s); break;            \
+    case EPI_SILU: RUN<TM, TN, WT, EPI_SILU>(p, s); break;                      \
+    case EPI_RESID: RUN<TM, TN, WT, EPI_RESID>(p, s); break;                    \
+    case EPI_GLU: RUN<TM, TN, WT, EPI_GLU>(p, s); break;                        \
+    case EPI_RELU: RUN<TM, TN, WT, EPI_RELU>(p, s); break;                      \
+    case EPI_RELU_TR: RUN<TM, TN, WT, EPI_RELU_TR>(p, s); break;                \
+    case EPI_RELU2_F32: RUN<TM, TN, WT, EPI_RELU2_F32>(p, s); break;            \
+    case EPI_RESID_LN: RUN<TM, TN, WT, EPI_RESID_LN>(p, s); break;              \
+    default: throw std::invalid_argument("gemm: bad epilogue");                 \
+    }
 
 // Row/column band split of the tile grid over the 8 XCDs that minimises the
 // L2-miss bytes gn*|A| + gm*|W| (each XCD reads its A band and its W band).
@@ -1516,7 +1680,7 @@ static void run_dma(const GemmParams& p, hipStream_t s) {
 template <int TM, int TN, int WT>
 static void f16_epi(int epi, const GemmParams& p, hipStream_t s) { PKX_EPI_SWITCH(run_f16, TM, TN, WT) }
 template <int TM, int TN, int WT>
-static void dma_epi(int epi, const GemmParams& p, hipStream_t s) { PKX_EPI_SWITCH(run_dma, TM, TN, WT) }
+static void dma_epi(int epi, const GemmParams& p, hipStream_t s) { PKX_EPI_SWITCH_DMA(run_dma, TM, TN, WT) }
 // 128 x 64 tiles with two K groups (eight waves): long-K products whose grid is
 // about one tile per CU
 template <int WT>
@@ -1527,6 +1691,7 @@ static bool dma_kg2(int epi, const GemmParams& p, hipStream_t s) {
     case EPI_STORE_F32: run_dma<2, 1, WT, EPI_STORE_F32, DMA_NS, 2>(p, s); return true;
     case EPI_RESID: run_dma<2, 1, WT, EPI_RESID, DMA_NS, 2>(p, s); return true;
     case EPI_SILU: run_dma<2, 1, WT, EPI_SILU, DMA_NS, 2>(p, s); return true;
+    case EPI_RESID_LN: run_dma<2, 1, WT, EPI_RESID_LN, DMA_NS, 2>(p, s); return true;
     default: return false;
     }
 }
@@ -1550,6 +1715,17 @@ void launch_gemm(Precision prec, int wtype, int epi, const GemmParams& p, hipStr
                 "gemm: fused conv-module epilogue needs the f16 path, N % 64 == 0, K % 64 == 0, ldy % 8 == 0");
         require(p.dw_w && p.dw_scale && p.dw_shift && p.T >= 1, "gemm: fused conv-module epilogue parameters");
     }
+    // the LDS-DMA kernel (f16 activations, K % 64 == 0) carries the LayerNorm folding
+    const bool dma_ok = prec == PREC_F16 && p.K % 64 == 0 && p.ldy % 8 == 0 &&
+                        (wtype == GT_F16 || wtype == GT_Q8_0 || wtype == GT_Q4_K);
+    if (epi == EPI_RESID_LN)
+        require(dma_ok && p.N % 32 == 0 && p.ln_g && p.ln_h && p.ln_stats,
+                "gemm: residual + LayerNorm statistics needs the f16 path, N % 32 == 0 and its outputs");
+    if (p.fold_stats)
+        require(dma_ok && p.fold_c1 && p.fold_groups >= 2 && p.fold_groups <= 32 &&
+                    (p.fold_groups & (p.fold_groups - 1)) == 0 &&
+                    (epi == EPI_STORE || epi == EPI_SILU || epi == EPI_GLU || epi == EPI_GLU_DW),
+                "gemm: a folded LayerNorm needs the f16 path, 2..32 (a power of two) statistics groups and a STORE / SILU / GLU epilogue");
     if (epi == EPI_GLU_DW) {
         // 64 x 128 tiles (56 output rows, 64 channels) on a 2-stage ring, three
         // workgroups per CU: the overlapping row tiles outnumber two slots per CU
@@ -1561,8 +1737,7 @@ void launch_gemm(Precision prec, int wtype, int epi, const GemmParams& p, hipStr
         return;
     }
     const bool big = (int64_t)cdiv(p.M, 128) * cdiv(p.N, 128) >= 256;
-    if (prec == PREC_F16 && p.K % 64 == 0 && p.ldy % 8 == 0 &&
-        (wtype == GT_F16 || wtype == GT_Q8_0 || wtype == GT_Q4_K)) {
+    if (dma_ok) {
         // Tile shapes from sweeps over the encoder's shapes on MI355X (M = B*T' = 2000):
         // q8_0 and q4_K weights prefer 128x128 when the grid holds >= 384 of them (N >= 3072,
         // and the all-layer positional projection), 128x64 at N = 1024 (FFN2, attention
@@ -1615,6 +1790,50 @@ __global__ void dequant_q8_0_kernel(const uint8_t* src, float* dst, int64_t nblk
     const uint8_t* b = src + (i / 32) * 34;
     const f16 d = __builtin_bit_cast(f16, (uint16_t)(b[0] | (b[1] << 8)));
     dst[i] = (float)(int8_t)b[2 + (i % 32)] * (float)d;
+}
+
+// One wave per weight row n: c1 = g . w[n], c2 = b . w[n] + bias[n], with w the
+// f16 value the GEMM's in-register dequantisation produces (device layouts:
+// f16 [N][K]; q8_0 int8 [N][K] + f16 d [N][K/32], w = f16(q d); q4_K nibbles
+// [N][K/2] + float2 {scale, min} [N][K/32], w = f16(q s16 - m16)).
+__global__ void ln_fold_consts_kernel(int wtype, const uint8_t* Wq, const uint8_t* Ws, int N, int K, const float* g,
+                                      const float* b, const float* bias, float* c1, float* c2) {
+    const int n = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (n >= N) return;
+    float s1 = 0.f, s2 = 0.f;
+    for (int k = lane; k < K; k += 64) {
+        float w;
+        if (wtype == GT_F16) {
+            w = (float)((const f16*)Wq)[(int64_t)n * K + k];
+        } else if (wtype == GT_Q8_0) {
+            const float q = (float)((const int8_t*)Wq)[(int64_t)n * K + k];
+            const float d = (float)((const f16*)Ws)[(int64_t)n * (K / 32) + k / 32];
+            w = (float)(f16)(q * d);
+        } else {
+            const int l = k % 64;
+            const uint8_t byte = Wq[(int64_t)n * (K / 2) + (k / 64) * 32 + (l & 31)];
+            const float q = (float)(l < 32 ? (byte & 0xF) : (byte >> 4));
+            const float2v sm = ((const float2v*)Ws)[(int64_t)n * (K / 32) + k / 32];
+            w = (float)(f16)fmaf(q, (float)(f16)sm.x, (float)(f16)(-sm.y));
+        }
+        s1 += g[k] * w;
+        s2 += b[k] * w;
+    }
+    s1 = wave_sum(s1);
+    s2 = wave_sum(s2);
+    if (lane == 0) {
+        c1[n] = s1;
+        c2[n] = s2 + (bias ? bias[n] : 0.f);
+    }
+}
+
+void launch_ln_fold_consts(int wtype, const void* Wq, const void* Ws, int N, int K, const float* g,
+                           const float* b, const float* bias, float* c1, float* c2, hipStream_t s) {
+    require(wtype == GT_F16 || wtype == GT_Q8_0 || wtype == GT_Q4_K, "ln fold: weight type must be f16/q8_0/q4_K");
+    require(N > 0 && K > 0 && g && b && c1 && c2, "ln fold: bad arguments");
+    launch(ln_fold_consts_kernel, dim3(cdiv(N, 4)), dim3(256), 0, s, wtype, (const uint8_t*)Wq, (const uint8_t*)Ws,
+           N, K, g, b, bias, c1, c2);
+    PKX_LAUNCH_CHECK();
 }
 
 __global__ void dequant_q4_k_kernel(const uint8_t* src, float* dst, int64_t nblk) {

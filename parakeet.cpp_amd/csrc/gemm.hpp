@@ -23,7 +23,10 @@ enum Epi : int {
     // GLU + pad mask, then depthwise conv over time (K = GLU_DW_K, zero padding
     // at each item's edges) + bias + folded BatchNorm + SiLU     conformer.cpp:55-157
     EPI_GLU_DW = 8,
-    EPI_COUNT = 9
+    // EPI_RESID, then for the LayerNorm that follows: H(f16) = R * ln_g and the
+    // statistics of R over each 32-column group (mean, sum of squared deviations)
+    EPI_RESID_LN = 9,
+    EPI_COUNT = 10
 };
 
 constexpr int GLU_DW_K = 9;   // depthwise kernel size of the fused conv-module epilogue
@@ -49,7 +52,25 @@ struct GemmParams {
     const float* dw_b = nullptr;
     const float* dw_scale = nullptr;
     const float* dw_shift = nullptr;
+    // EPI_RESID_LN outputs (N % 32 == 0)
+    const float* ln_g = nullptr;   // [N] gamma of the next LayerNorm
+    void* ln_h = nullptr;          // f16 [M][N]: R * gamma
+    float* ln_stats = nullptr;     // float2 [M][N / 32]: {mean, sum of squared deviations}
+    // A LayerNorm folded into this product (EPI_STORE / SILU / GLU / GLU_DW):
+    // A = x * gamma (f16, from EPI_RESID_LN) and
+    //   y = rstd_m * (acc - mean_m * fold_c1[n]) + bias[n],
+    // fold_c1 = W . gamma, bias = W . beta + b (launch_ln_fold_consts).
+    const float* fold_stats = nullptr;   // float2 [M][fold_groups]
+    const float* fold_c1 = nullptr;
+    int fold_groups = 0;
+    float fold_eps = 1e-5f;
 };
+
+// c1[n] = sum_k g[k] w[n][k], c2[n] = sum_k b[k] w[n][k] + bias[n] for a
+// LayerNorm (g, b) folded into the product with device weight (Wq, Ws) of
+// type wtype; w is the f16 value the GEMM's dequantisation produces.
+void launch_ln_fold_consts(int wtype, const void* Wq, const void* Ws, int N, int K, const float* g,
+                           const float* b, const float* bias, float* c1, float* c2, hipStream_t s);
 
 // True when launch_gemm can run EPI_GLU_DW for this shape: the f16 MFMA path,
 // N (= 2 x channels) a multiple of 64 and K a multiple of 64.

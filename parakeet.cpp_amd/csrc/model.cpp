@@ -79,6 +79,7 @@ struct Buf {
 struct Model::Ws {
     Buf a2, a2p, a3, flat;              // subsampling maps
     Buf h, u, qkv, g, pe, p, xin, tmp;  // layer activations
+    Buf lnst;                           // row statistics for the folded LayerNorms
     Buf logits, pp;                     // heads
     int* d_valid = nullptr;             // 4 x Bcap ints: v0, v1, v2, vout
     int* h_valid = nullptr;             // pinned staging
@@ -542,6 +543,32 @@ void Model::finalize() {
             require(heads_.n_tok > 0, "joint: vocab/durations mismatch");
         }
     }
+    // LayerNorm folding (f16 path): every product involved must take the LDS-DMA
+    // kernel, i.e. f16 / q8_0 / q4_K weights with K % 64 == 0
+    {
+        auto dma = [](const DevWeight& w) {
+            return (w.gtype == GT_F16 || w.gtype == GT_Q8_0 || w.gtype == GT_Q4_K) && w.K % 64 == 0;
+        };
+        const int G = D / 32;   // row-statistics groups: a power of two up to 32
+        bool ok = f16g && D % 64 == 0 && FF % 8 == 0 && G <= 32 && (G & (G - 1)) == 0;
+        for (const LayerDev& L : layers_)
+            ok = ok && dma(L.ff1_w2) && dma(L.wo) && dma(L.pw2) && dma(L.wqkv) && dma(L.pw1) && dma(L.ff2_w1);
+        ln_fold_ = ok;
+        if (ok) {
+            for (LayerDev& L : layers_) {
+                auto consts = [&](const DevWeight& w, const float* g, const float* b, const float* bias, float*& c1,
+                                  float*& c2) {
+                    c1 = (float*)dalloc((size_t)w.N * 4);
+                    c2 = (float*)dalloc((size_t)w.N * 4);
+                    launch_ln_fold_consts(w.gtype, w.q, w.s, w.N, w.K, g, b, bias, c1, c2, nullptr);
+                };
+                consts(L.wqkv, L.att_ln_g, L.att_ln_b, L.bqkv, L.qkv_c1, L.qkv_c2);
+                consts(L.pw1, L.conv_ln_g, L.conv_ln_b, L.pw1_b, L.pw1_c1, L.pw1_c2);
+                consts(L.ff2_w1, L.ff2_ln_g, L.ff2_ln_b, L.ff2_b1, L.ff2_c1, L.ff2_c2);
+            }
+            PKX_HIP(hipDeviceSynchronize());
+        }
+    }
     host_.clear();
     finalized_ = true;
 }
@@ -648,19 +675,62 @@ void Model::gemm(const DevWeight& w, int epi, const void* A, int64_t lda, int64_
     mark(fam, false);
 }
 
+void Model::gemm_resid_ln(const DevWeight& w, const void* A, int64_t M, const float* bias, float* x, float alpha,
+                          const float* g, void* h, hipStream_t s, int fam) {
+    grow(ws_->lnst, (size_t)M * (w.N / 32) * 8);
+    GemmParams p;
+    p.A = A;
+    p.lda = w.K;
+    p.Wq = w.q;
+    p.Ws = w.s;
+    p.bias = bias;
+    p.Y = x;
+    p.ldy = w.N;
+    p.alpha = alpha;
+    p.M = (int)M;
+    p.N = w.N;
+    p.K = w.K;
+    p.ln_g = g;
+    p.ln_h = h;
+    p.ln_stats = (float*)ws_->lnst.p;
+    mark(fam, true);
+    launch_gemm(prec_, w.gtype, EPI_RESID_LN, p, s);
+    mark(fam, false);
+}
+
+GemmParams Model::fold_params(const DevWeight& w, const void* A, int64_t M, const float* c1, const float* c2,
+                              void* Y, int64_t ldy) {
+    GemmParams p;
+    p.A = A;
+    p.lda = w.K;
+    p.Wq = w.q;
+    p.Ws = w.s;
+    p.bias = c2;
+    p.Y = Y;
+    p.ldy = ldy;
+    p.M = (int)M;
+    p.N = w.N;
+    p.K = w.K;
+    p.fold_stats = (const float*)ws_->lnst.p;
+    p.fold_c1 = c1;
+    p.fold_groups = w.K / 32;
+    return p;
+}
+
 void Model::conv_front(const LayerDev& L, const void* A, int64_t M, const int* valid, int B, int T, void* Y,
-                       hipStream_t s) {
+                       hipStream_t s, bool fold) {
     const ModelConfig& c = cfg_;
     const int D = c.d_model;
     if (c.conv_kernel == GLU_DW_K && gemm_glu_dw_supported(prec_, L.pw1.gtype, L.pw1.N, L.pw1.K)) {
         // one pass: the GEMM epilogue stages GLU rows in LDS and runs the
         // depthwise conv over time on them (conformer.cpp:48-157)
         GemmParams p;
+        if (fold) p = fold_params(L.pw1, A, M, L.pw1_c1, L.pw1_c2, Y, D);
         p.A = A;
         p.lda = D;
         p.Wq = L.pw1.q;
         p.Ws = L.pw1.s;
-        p.bias = L.pw1_b;
+        p.bias = fold ? L.pw1_c2 : L.pw1_b;
         p.Y = Y;
         p.ldy = D;
         p.valid = valid;
@@ -677,12 +747,21 @@ void Model::conv_front(const LayerDev& L, const void* A, int64_t M, const int* v
         mark(KF_GEMM_PW1_GLU, false);
         return;
     }
-    // GLU output in a scratch buffer that is neither A nor Y
+    // GLU output in the FFN hidden buffer (neither A nor Y in either caller)
     Ws& w = *ws_;
-    Buf& glu = (Y == w.g.p) ? w.u : w.g;
+    Buf& glu = w.u;
     grow(glu, (size_t)M * D * (prec_ == PREC_F16 ? 2 : 4));
-    require(glu.p != A, "conv module: input aliases the GLU scratch");
-    gemm(L.pw1, EPI_GLU, A, D, M, L.pw1_b, glu.p, D, 1.f, valid, T, s, prec_, KF_GEMM_PW1_GLU);
+    require(glu.p != A && glu.p != Y, "conv module: input or output aliases the GLU scratch");
+    if (fold) {
+        GemmParams p = fold_params(L.pw1, A, M, L.pw1_c1, L.pw1_c2, glu.p, D);
+        p.valid = valid;
+        p.T = T;
+        mark(KF_GEMM_PW1_GLU, true);
+        launch_gemm(prec_, L.pw1.gtype, EPI_GLU, p, s);
+        mark(KF_GEMM_PW1_GLU, false);
+    } else {
+        gemm(L.pw1, EPI_GLU, A, D, M, L.pw1_b, glu.p, D, 1.f, valid, T, s, prec_, KF_GEMM_PW1_GLU);
+    }
     mark(KF_DWCONV, true);
     launch_dwconv_bn_silu(prec_, glu.p, Y, L.dw_w, L.dw_b, L.bn_scale, L.bn_shift, B, T, D, c.conv_kernel, s);
     mark(KF_DWCONV, false);
@@ -806,13 +885,30 @@ void Model::layer_body(int l, float* x, int B, int T, const int* d_valid, bool f
         launch_layernorm(prec_, p, s);
         mark(KF_LAYERNORM, false);
     };
+    // With ln_fold_, norm_self_att, norm_conv and norm_feed_forward2 are folded:
+    // the residual product before each leaves x * gamma (f16) and the row
+    // statistics, and the product after it applies the normalisation in its
+    // epilogue.  Buffers: h and g alternate as LayerNorm / attention / conv
+    // outputs so that no product writes what it reads.
+    const bool fold = ln_fold_ && !conv_capture_;
     // Stage A: x += 0.5 * FFN1(LN(x))
     if (!first_ln_done) ln(L.ff1_ln_g, L.ff1_ln_b);
     gemm(L.ff1_w1, EPI_SILU, w.h.p, D, M, L.ff1_b1, w.u.p, c.ff_dim, 1.f, nullptr, 1, s, prec_, KF_GEMM_FFN);
-    gemm(L.ff1_w2, EPI_RESID, w.u.p, c.ff_dim, M, L.ff1_b2, x, D, 0.5f, nullptr, 1, s, prec_, KF_GEMM_FFN);
+    if (fold) {
+        gemm_resid_ln(L.ff1_w2, w.u.p, M, L.ff1_b2, x, 0.5f, L.att_ln_g, w.h.p, s, KF_GEMM_FFN);
+    } else {
+        gemm(L.ff1_w2, EPI_RESID, w.u.p, c.ff_dim, M, L.ff1_b2, x, D, 0.5f, nullptr, 1, s, prec_, KF_GEMM_FFN);
+        ln(L.att_ln_g, L.att_ln_b);
+    }
     // Stage B: x += MHSA(LN(x))
-    ln(L.att_ln_g, L.att_ln_b);
-    gemm(L.wqkv, EPI_STORE, w.h.p, D, M, L.bqkv, w.qkv.p, 3 * D, 1.f, nullptr, 1, s, prec_, KF_GEMM_QKV);
+    if (fold) {
+        const GemmParams p = fold_params(L.wqkv, w.h.p, M, L.qkv_c1, L.qkv_c2, w.qkv.p, 3 * D);
+        mark(KF_GEMM_QKV, true);
+        launch_gemm(prec_, L.wqkv.gtype, EPI_STORE, p, s);
+        mark(KF_GEMM_QKV, false);
+    } else {
+        gemm(L.wqkv, EPI_STORE, w.h.p, D, M, L.bqkv, w.qkv.p, 3 * D, 1.f, nullptr, 1, s, prec_, KF_GEMM_QKV);
+    }
     const size_t as = prec_ == PREC_F16 ? 2 : 4;
     const int ldp = pos_all ? c.n_layers * D : D;
     const void* pl = pos_all ? (const void*)((const uint8_t*)w.p.p + (size_t)l * D * as) : w.p.p;
@@ -841,19 +937,33 @@ void Model::layer_body(int l, float* x, int B, int T, const int* d_valid, bool f
         launch_relpos_attention(prec_, a, s);
         mark(KF_ATTENTION, false);
     }
-    gemm(L.wo, EPI_RESID, w.h.p, D, M, L.bo, x, D, 1.f, nullptr, 1, s, prec_, KF_GEMM_OUT);
     // Stage C: x += conv(LN(x))
-    ln(L.conv_ln_g, L.conv_ln_b);
-    conv_front(L, w.h.p, M, d_valid, B, T, w.g.p, s);
-    if (conv_capture_) {
-        gemm(L.pw2, EPI_STORE_F32, w.g.p, D, M, L.pw2_b, conv_capture_, D, 1.f, nullptr, 1, s, prec_, KF_GEMM_PW2);
-        launch_add_f32(x, conv_capture_, M * D, s);
+    if (fold) {
+        gemm_resid_ln(L.wo, w.h.p, M, L.bo, x, 1.f, L.conv_ln_g, w.g.p, s, KF_GEMM_OUT);
+        conv_front(L, w.g.p, M, d_valid, B, T, w.h.p, s, true);
+        gemm_resid_ln(L.pw2, w.h.p, M, L.pw2_b, x, 1.f, L.ff2_ln_g, w.g.p, s, KF_GEMM_PW2);
     } else {
-        gemm(L.pw2, EPI_RESID, w.g.p, D, M, L.pw2_b, x, D, 1.f, nullptr, 1, s, prec_, KF_GEMM_PW2);
+        gemm(L.wo, EPI_RESID, w.h.p, D, M, L.bo, x, D, 1.f, nullptr, 1, s, prec_, KF_GEMM_OUT);
+        ln(L.conv_ln_g, L.conv_ln_b);
+        conv_front(L, w.h.p, M, d_valid, B, T, w.g.p, s);
+        if (conv_capture_) {
+            gemm(L.pw2, EPI_STORE_F32, w.g.p, D, M, L.pw2_b, conv_capture_, D, 1.f, nullptr, 1, s, prec_,
+                 KF_GEMM_PW2);
+            launch_add_f32(x, conv_capture_, M * D, s);
+        } else {
+            gemm(L.pw2, EPI_RESID, w.g.p, D, M, L.pw2_b, x, D, 1.f, nullptr, 1, s, prec_, KF_GEMM_PW2);
+        }
+        ln(L.ff2_ln_g, L.ff2_ln_b);
     }
     // Stage D: x += 0.5 * FFN2(LN(x)); x = LN_out(x) [fused with next layer's LN_ff1]
-    ln(L.ff2_ln_g, L.ff2_ln_b);
-    gemm(L.ff2_w1, EPI_SILU, w.h.p, D, M, L.ff2_b1, w.u.p, c.ff_dim, 1.f, nullptr, 1, s, prec_, KF_GEMM_FFN);
+    if (fold) {
+        const GemmParams p = fold_params(L.ff2_w1, w.g.p, M, L.ff2_c1, L.ff2_c2, w.u.p, c.ff_dim);
+        mark(KF_GEMM_FFN, true);
+        launch_gemm(prec_, L.ff2_w1.gtype, EPI_SILU, p, s);
+        mark(KF_GEMM_FFN, false);
+    } else {
+        gemm(L.ff2_w1, EPI_SILU, w.h.p, D, M, L.ff2_b1, w.u.p, c.ff_dim, 1.f, nullptr, 1, s, prec_, KF_GEMM_FFN);
+    }
     gemm(L.ff2_w2, EPI_RESID, w.u.p, c.ff_dim, M, L.ff2_b2, x, D, 0.5f, nullptr, 1, s, prec_, KF_GEMM_FFN);
     {
         LnParams p;

@@ -54,6 +54,11 @@ struct LayerDev {
     DevWeight pw1, pw2;
     float *pw1_b = nullptr, *pw2_b = nullptr, *dw_w = nullptr, *dw_b = nullptr;
     float *bn_scale = nullptr, *bn_shift = nullptr;
+    // LayerNorms folded into the product that follows them (f16 path):
+    // c1 = W . gamma, c2 = W . beta + b for norm_self_att -> q/k/v,
+    // norm_conv -> pointwise_conv1, norm_feed_forward2 -> feed_forward2.linear1
+    float *qkv_c1 = nullptr, *qkv_c2 = nullptr, *pw1_c1 = nullptr, *pw1_c2 = nullptr;
+    float *ff2_c1 = nullptr, *ff2_c2 = nullptr;
 };
 
 struct SubDev {
@@ -126,11 +131,19 @@ private:
     void ensure_ws(int B, int T_max);
     // pointwise_conv1 + GLU + pad mask + depthwise conv + bias + folded BN + SiLU
     // of the conv module, from the normed input A [M][D] to Y [M][D]
+    // (fold: A = x * gamma with the row statistics of gemm_resid_ln)
     void conv_front(const LayerDev& L, const void* A, int64_t M, const int* valid, int B, int T, void* Y,
-                    hipStream_t s);
+                    hipStream_t s, bool fold = false);
     void gemm(const DevWeight& w, int epi, const void* A, int64_t lda, int64_t M,
               const float* bias, void* Y, int64_t ldy, float alpha, const int* valid, int T,
               hipStream_t s, Precision prec, int fam, const float* bias2 = nullptr, int trF = 1);
+    // residual product x += alpha * (A W^T + b) that also leaves, for the
+    // LayerNorm (g) that follows, x * g in f16 (h) and the row statistics
+    void gemm_resid_ln(const DevWeight& w, const void* A, int64_t M, const float* bias, float* x, float alpha,
+                       const float* g, void* h, hipStream_t s, int fam);
+    // product of a LayerNorm folded in (A = x * gamma from gemm_resid_ln)
+    GemmParams fold_params(const DevWeight& w, const void* A, int64_t M, const float* c1, const float* c2,
+                           void* Y, int64_t ldy);
     void layer_body(int l, float* x, int B, int T, const int* d_valid, bool first_ln_done,
                     bool fuse_next_ln, bool pos_all, hipStream_t s);
     void ensure_pe(int T, hipStream_t s);
@@ -141,6 +154,7 @@ private:
     ModelConfig cfg_;
     Precision prec_;
     bool finalized_ = false;
+    bool ln_fold_ = false;   // f16 path: norm_self_att / norm_conv / norm_feed_forward2 folded into GEMMs
     std::map<std::string, HostTensor> host_;
     std::vector<void*> allocs_;
     std::vector<LayerDev> layers_;

@@ -151,8 +151,9 @@ def test_profiling_counts_and_sampling(gpu, stream):
     gm.encoder_forward(dm, [200, 120], dy, stream=stream)
     prof = gm.profile()
     assert np.array_equal(dy.numpy(stream), plain)
-    # kernel 9 on the f16 path: the depthwise conv runs inside the pw1 GEMM
-    expect = {"subsampling": 5, "layernorm": 4 * L + 1, "gemm_ffn": 4 * L, "gemm_qkv": L, "gemm_pos": 1,
+    # f16 path: the depthwise conv runs inside the pw1 GEMM (kernel 9), and
+    # norm_self_att / norm_conv / norm_feed_forward2 are folded into GEMMs
+    expect = {"subsampling": 5, "layernorm": L + 1, "gemm_ffn": 4 * L, "gemm_qkv": L, "gemm_pos": 1,
               "attention": L, "gemm_out": L, "gemm_pw1_glu": L, "dwconv": 0, "gemm_pw2": L, "pos_enc": 1}
     for fam, n in expect.items():
         ms, got_n = prof[fam]
