@@ -113,6 +113,32 @@ def test_conformer_layer(gpu, stream, name, B, T, valid):
     assert rel_l2(delta_got, delta_ref) < 3 * _tol(prec)
 
 
+@pytest.mark.parametrize("name", list(CASES))
+@pytest.mark.parametrize("offset", [0.0, 4.0])
+def test_conformer_layer_folded_layernorm(gpu, stream, name, offset):
+    """The encoder's own path through a block (no conv-module capture): on the
+    f16 path norm_self_att, norm_conv and norm_feed_forward2 are folded into
+    the neighbouring GEMMs (statistics from the residual product, the
+    normalisation in the next product's epilogue).  A per-row mean of 4 sigma
+    in the residual stream checks that the folded form keeps its accuracy when
+    the mean is large against the spread."""
+    m, om, gm, prec = _models(gpu, name)
+    D, B, T = m.cfg.d_model, 3, 77
+    valid = [77, 50, 9]
+    rng = np.random.default_rng(int(31 + offset))
+    x = (rng.normal(0, 1, (B, T, D)) + offset * (1 + rng.random((B, T, 1)))).astype(np.float32)
+    print(f"[layer-fold] {name} offset={offset}", flush=True)
+    ref = om.conformer_layer(1, x, oracle.rel_pos_encoding(T, D), valid)
+    dx = gpu.DeviceArray.from_numpy(x, stream)
+    dy = gpu.DeviceArray((B, T, D), np.float32)
+    gm.conformer_layer(1, dx, valid, dy, None, stream)
+    got = dy.numpy(stream)
+    mask = _valid_mask(B, T, valid)
+    err = rel_l2(got[mask], ref[mask])
+    print(f"  rel_l2 {err:.3e}")
+    assert err < _tol(prec), err
+
+
 @pytest.mark.parametrize("name", ["f32_dk32", "q8_dk64"])
 def test_batched_equals_per_item(gpu, stream, name):
     """tests/test_conformer_batch.cpp:103-152 on the GPU path: a full item is
@@ -161,8 +187,13 @@ def test_conformer_layer_production_shape(gpu, stream, ragged):
     dconv = gpu.DeviceArray((B, T, D), np.float32)
     gm.conformer_layer(0, dx, valid, dy, dconv, stream)
     got, got_conv = dy.numpy(stream), dconv.numpy(stream)
+    # the encoder's path (no capture): LayerNorms folded into the GEMMs
+    gm.conformer_layer(0, dx, valid, dy, None, stream)
+    got_fold = dy.numpy(stream)
     gm.close()
     mask = _valid_mask(B, T, valid)
     assert rel_l2(got[mask], ref[mask]) < 1e-2
     assert rel_l2(got_conv[mask], ref_conv[mask]) < 1e-2
     assert rel_l2(got[mask] - x[mask], ref[mask] - x[mask]) < 3e-2
+    assert rel_l2(got_fold[mask], ref[mask]) < 1e-2
+    assert rel_l2(got_fold[mask] - x[mask], ref[mask] - x[mask]) < 3e-2
