@@ -82,42 +82,68 @@ __global__ __launch_bounds__(64 * NW, 1) void relpos_attn_f16_kernel(AttnParams 
     float lrow[4] = {0.f, 0.f, 0.f, 0.f};
     const int lr = 4 * (lane >> 4), lc = lane & 15;
 
-    for (int j0 = 0; j0 < vl; j0 += AK) {
-        // ---- stage K tile, transposed V tile and the positional band in LDS ----
+    // Staging of one key tile (K rows, V as 8x8 blocks, the positional band)
+    // through registers: all of a tile's global loads are issued together, and
+    // the next tile's loads are in flight while the current tile is computed.
+    constexpr int KCH = AK * (DK / 8), VCH = (AK / 8) * (DK / 8), PCH = S::APB * (DK / 8);
+    constexpr int KPT = (KCH + NT - 1) / NT, VPT = (VCH + NT - 1) / NT, PPT = (PCH + NT - 1) / NT;
+    half8v kreg[KPT], vreg[VPT][8], preg[PPT];
+    auto load_tile = [&](int j0) {
         const int rlo = T - 1 - (i0 + AQ - 1) + j0;
-        for (int c = tid; c < AK * (DK / 8); c += NT) {
-            const int r = c / (DK / 8), col = (c % (DK / 8)) * 8;
-            const int j = j0 + r;
-            half8v kv = {};
-            if (j < T) kv = *(const half8v*)(k + (rowq + j) * a.ldk + h * DK + col);
-            *(half8v*)(sm.k + r * S::LDK + col) = kv;
+#pragma unroll
+        for (int u = 0; u < KPT; ++u) {
+            const int c = tid + NT * u, r = c / (DK / 8), col = (c % (DK / 8)) * 8, j = j0 + r;
+            kreg[u] = (c < KCH && j < T) ? *(const half8v*)(k + (rowq + j) * a.ldk + h * DK + col) : (half8v){};
         }
-        // V^T in 8 x 8 blocks: 8 row loads of 16 B, transposed in registers,
-        // 8 row stores of 16 B (keys contiguous)
-        for (int c = tid; c < (AK / 8) * (DK / 8); c += NT) {
-            const int kg = c % (AK / 8), dg = c / (AK / 8);
-            half8v rows[8];
+#pragma unroll
+        for (int u = 0; u < VPT; ++u) {
+            const int c = tid + NT * u, kg = c % (AK / 8), dg = c / (AK / 8);
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const int j = j0 + 8 * kg + e;
-                rows[e] = j < T ? *(const half8v*)(v + (rowq + j) * a.ldv + h * DK + 8 * dg) : (half8v){};
-            }
-#pragma unroll
-            for (int d = 0; d < 8; ++d) {
-                half8v col;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) col[e] = rows[e][d];
-                *(half8v*)(sm.vt + (8 * dg + d) * S::LDV + 8 * kg) = col;
+                vreg[u][e] = (c < VCH && j < T) ? *(const half8v*)(v + (rowq + j) * a.ldv + h * DK + 8 * dg)
+                                                : (half8v){};
             }
         }
-        for (int c = tid; c < S::APB * (DK / 8); c += NT) {
-            const int r = c / (DK / 8), col = (c % (DK / 8)) * 8;
-            const int pr = rlo + r;
-            half8v pv = {};
-            if (pr >= 0 && pr < P) pv = *(const half8v*)(pp + (int64_t)pr * a.ldp + h * DK + col);
-            *(half8v*)(sm.p + r * S::LDK + col) = pv;
+#pragma unroll
+        for (int u = 0; u < PPT; ++u) {
+            const int c = tid + NT * u, r = c / (DK / 8), col = (c % (DK / 8)) * 8, pr = rlo + r;
+            preg[u] = (c < PCH && pr >= 0 && pr < P) ? *(const half8v*)(pp + (int64_t)pr * a.ldp + h * DK + col)
+                                                     : (half8v){};
         }
+    };
+    auto store_tile = [&]() {
+#pragma unroll
+        for (int u = 0; u < KPT; ++u) {
+            const int c = tid + NT * u;
+            if (c < KCH) *(half8v*)(sm.k + (c / (DK / 8)) * S::LDK + (c % (DK / 8)) * 8) = kreg[u];
+        }
+        // V^T: the 8 x 8 block is transposed in registers, keys contiguous
+#pragma unroll
+        for (int u = 0; u < VPT; ++u) {
+            const int c = tid + NT * u, kg = c % (AK / 8), dg = c / (AK / 8);
+            if (c < VCH) {
+#pragma unroll
+                for (int d = 0; d < 8; ++d) {
+                    half8v col;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) col[e] = vreg[u][e][d];
+                    *(half8v*)(sm.vt + (8 * dg + d) * S::LDV + 8 * kg) = col;
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < PPT; ++u) {
+            const int c = tid + NT * u;
+            if (c < PCH) *(half8v*)(sm.p + (c / (DK / 8)) * S::LDK + (c % (DK / 8)) * 8) = preg[u];
+        }
+    };
+
+    load_tile(0);
+    for (int j0 = 0; j0 < vl; j0 += AK) {
+        store_tile();
         __syncthreads();
+        if (j0 + AK < vl) load_tile(j0 + AK);
 
         // ---- ac = qu . k^T : 16 x 64 per wave ----
         float4v sac[4];
@@ -164,10 +190,7 @@ __global__ __launch_bounds__(64 * NW, 1) void relpos_attn_f16_kernel(AttnParams 
                 tmax[r] = fmaxf(tmax[r], sv);
             }
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-#pragma unroll
-            for (int off = 1; off < 16; off <<= 1) tmax[r] = fmaxf(tmax[r], __shfl_xor(tmax[r], off, 64));
-        }
+        for (int r = 0; r < 4; ++r) tmax[r] = row16_max(tmax[r]);   // over the tile's 64 keys
         float corr[4], tsum[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -186,8 +209,7 @@ __global__ __launch_bounds__(64 * NW, 1) void relpos_attn_f16_kernel(AttnParams 
             }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-#pragma unroll
-            for (int off = 1; off < 16; off <<= 1) tsum[r] += __shfl_xor(tsum[r], off, 64);
+            tsum[r] = group_sum(tsum[r], 16);
             lrow[r] = lrow[r] * corr[r] + tsum[r];
         }
 #pragma unroll

@@ -88,6 +88,28 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// Reductions over aligned groups of n consecutive lanes (n = 1, 2, 4, 8 or 16,
+// wave-uniform), every lane of a group receiving the result: DPP steps
+// quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror
+// (each pairs a lane with one in the other half of its current group).
+template <int CTRL> __device__ __forceinline__ float dpp_get(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float group_sum(float v, int n) {
+    if (n > 1) v += dpp_get<0xB1>(v);    // quad_perm [1,0,3,2]
+    if (n > 2) v += dpp_get<0x4E>(v);    // quad_perm [2,3,0,1]
+    if (n > 4) v += dpp_get<0x141>(v);   // row_half_mirror
+    if (n > 8) v += dpp_get<0x140>(v);   // row_mirror
+    return v;
+}
+// max over the 16 lanes of each DPP row
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dpp_get<0xB1>(v));
+    v = fmaxf(v, dpp_get<0x4E>(v));
+    v = fmaxf(v, dpp_get<0x141>(v));
+    return fmaxf(v, dpp_get<0x140>(v));
+}
+
 inline int cdiv(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 __host__ __device__ __forceinline__ int cdiv_dev(int a, int b) { return (a + b - 1) / b; }
 

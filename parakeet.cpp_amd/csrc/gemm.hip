@@ -23,22 +23,6 @@ __device__ __forceinline__ int xcd_tile(int bid, int total) {
 // Wave index as a wave-uniform (scalar) value.
 __device__ __forceinline__ int wave_id_uniform() { return __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6); }
 
-// Sum over aligned groups of n consecutive lanes (n = 1, 2, 4, 8 or 16,
-// wave-uniform), every lane of a group receiving the total: DPP steps
-// quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror.
-template <int CTRL> __device__ __forceinline__ float dpp_add(float v) {
-    const int o = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false);
-    return v + __builtin_bit_cast(float, o);
-}
-__device__ __forceinline__ float group_sum(float v, int n) {
-    if (n > 1) v = dpp_add<0xB1>(v);    // quad_perm [1,0,3,2]
-    if (n > 2) v = dpp_add<0x4E>(v);    // quad_perm [2,3,0,1]
-    if (n > 4) v = dpp_add<0x141>(v);   // row_half_mirror
-    if (n > 8) v = dpp_add<0x140>(v);   // row_mirror
-    return v;
-}
-
-
 // 2-D XCD blocking: the nbm x nbn tile grid is cut into gm row bands x gn
 // column bands (gm * gn = 8), one rectangle per XCD, so an XCD's L2 sees only
 // its band of A rows and its band of weight columns (gn*|A| + gm*|W| bytes
