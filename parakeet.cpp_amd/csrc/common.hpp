@@ -70,8 +70,10 @@ inline void require(bool ok, const std::string& msg) {
     if (!ok) throw std::invalid_argument(msg);
 }
 
-__device__ __forceinline__ float silu_dev(float v) { return v / (1.0f + __expf(-v)); }
-__device__ __forceinline__ float sigmoid_dev(float v) { return 1.0f / (1.0f + __expf(-v)); }
+// v_rcp_f32 (1 ulp) instead of an IEEE division: the epilogues apply these to
+// every GEMM output; exp overflow gives rcp(inf) = 0, the correct limit.
+__device__ __forceinline__ float sigmoid_dev(float v) { return __builtin_amdgcn_rcpf(1.0f + __expf(-v)); }
+__device__ __forceinline__ float silu_dev(float v) { return v * sigmoid_dev(v); }
 
 template <typename T> __device__ __forceinline__ T to_act(float v);
 template <> __device__ __forceinline__ float to_act<float>(float v) { return v; }
