@@ -893,6 +893,20 @@ __device__ __forceinline__ void epilogue32_glu_dw(const GemmParams& p, float16v 
     constexpr int CP = CW / 2, RG = 256 / CP, NR = BM - 2 * H, RPG = (NR + RG - 1) / RG;
     static_assert(256 % CP == 0, "channel pairs must divide the workgroup");
     const int lane = tid & 63, lr = 4 * (lane >> 5), lc = lane & 31;
+    // 0) per tile row: time index and whether the GLU output is kept (row in
+    //    [0, M) and t < valid), one division per row instead of per element
+    int2* rtab = (int2*)(G + BM * LDG);
+    for (int r = tid; r < BM; r += 256) {
+        const int m = m0 + r;
+        int t = 0, keep = 0;
+        if (m >= 0 && m < p.M) {
+            const int b = m / p.T;
+            t = m - b * p.T;
+            keep = !p.valid || t < p.valid[b];
+        }
+        rtab[r] = make_int2(t, keep);
+    }
+    __syncthreads();
     // 1) GLU + pad mask into LDS
 #pragma unroll
     for (int i = 0; i < TM; ++i)
@@ -906,7 +920,6 @@ __device__ __forceinline__ void epilogue32_glu_dw(const GemmParams& p, float16v 
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int rr = wm * 32 * TM + 32 * i + 8 * (r >> 2) + lr + (r & 3);
-                const int m = m0 + rr;
                 float xa = acc[i][2 * jj][r], xg = acc[i][2 * jj + 1][r];
                 if (fold) {
                     const float2v st = ftab[rr];
@@ -914,12 +927,7 @@ __device__ __forceinline__ void epilogue32_glu_dw(const GemmParams& p, float16v 
                     xg = st.y * (xg - st.x * cg);
                 }
                 float o = (xa + ba) * sigmoid_dev(xg + bg);
-                if (m < 0 || m >= p.M) {
-                    o = 0.f;
-                } else if (p.valid) {
-                    const int b = m / p.T, t = m - b * p.T;
-                    if (t >= p.valid[b]) o = 0.f;
-                }
+                if (!rtab[rr].y) o = 0.f;
                 G[rr * LDG + wn * 16 * TN + 32 * jj + lc] = o;
             }
         }
@@ -945,7 +953,7 @@ __device__ __forceinline__ void epilogue32_glu_dw(const GemmParams& p, float16v 
     for (int q = 0; q < RPG; ++q) {
         const int r = r0 + q, m = m0 + r;
         if (r < BM - H && m < p.M) {
-            const int t = m % p.T;
+            const int t = rtab[r].x;
             float2v a = {0.f, 0.f};
 #pragma unroll
             for (int j = 0; j < K; ++j)
@@ -1107,7 +1115,8 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
     if constexpr (EPI == EPI_RELU2_F32) {
         epilogue32<EPI, f16, TM, TN>(p, acc, m0 + wm * TM * 32, n0 + wn * TN * 32, lane);
     } else if constexpr (EPI == EPI_GLU_DW) {
-        static_assert(C::BM * (32 * TN + 2) * 4 + C::BM * 8 <= NS * C::STAGE, "conv staging exceeds LDS ring");
+        static_assert(C::BM * (32 * TN + 2) * 4 + C::BM * 8 + C::BM * 8 <= NS * C::STAGE,
+                      "conv staging exceeds LDS ring");
         __syncthreads();
         epilogue32_glu_dw<TM, TN>(p, acc, (float*)smem, m0, n0, wm, wn, tid, fold, ftab);
     } else if constexpr (EPI == EPI_RELU_TR) {
