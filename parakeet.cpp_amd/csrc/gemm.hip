@@ -20,6 +20,10 @@ __device__ __forceinline__ int xcd_tile(int bid, int total) {
     return x * per + (x < rem ? x : rem) + loc;
 }
 
+// Rows of each 64-wide K slab block of a slab-major q8_0 weight (views into a
+// larger allocation keep the allocation's row count).
+__device__ __forceinline__ int q8_rows(const GemmParams& p) { return p.ldw > 0 ? p.ldw : p.N; }
+
 // Wave index as a wave-uniform (scalar) value.
 __device__ __forceinline__ int wave_id_uniform() { return __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6); }
 
@@ -218,7 +222,7 @@ __device__ __forceinline__ void nib4_to_f16(uint32_t w, int hi, half2v s2, half2
     up = (__builtin_bit_cast(half2v, b) - off2) * s2 + nm2;
 }
 
-// q8_0 device layout: int8 q[N][K] and f16 d[N][K/32]; w = d*q.
+// q8_0 device layout (slab-major): int8 q[K/64][ldw][64] and f16 d[K/64][ldw][2]; w = d*q.
 template <int BN> struct BLoad16<GT_Q8_0, BN> {
     static constexpr int NC = (BN * 4 + 255) / 256;
     int4v q[NC];
@@ -230,9 +234,10 @@ template <int BN> struct BLoad16<GT_Q8_0, BN> {
             const int c = tid + 256 * i;
             const int n = n0 + (c >> 2), k = k0 + (c & 3) * 16;
             const bool in = k < p.K && n < p.N;
-            q[i] = bload16(rq, in ? (uint32_t)((int64_t)n * p.K + k) : OOB);
+            const int L = q8_rows(p);   // slab-major: (slab, row) blocks of 64 bytes / 2 scales
+            q[i] = bload16(rq, in ? (uint32_t)(((int64_t)(k / 64) * L + n) * 64 + (k & 63)) : OOB);
             d[i] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(
-                rs, (int)(in ? (uint32_t)(((int64_t)n * (p.K / 32) + k / 32) * 2) : OOB), 0, 0);
+                rs, (int)(in ? (uint32_t)((((int64_t)(k / 64) * L + n) * 2 + ((k & 63) >> 5)) * 2) : OOB), 0, 0);
         }
     }
     __device__ void store(f16* Bs, int tid) const {
@@ -336,7 +341,11 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(GemmParams p) {
 
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, ((int64_t)(p.M - 1) * p.lda + p.K) * 2);
     int64_t wq_bytes = (int64_t)p.N * p.K * 2, ws_bytes = 0;
-    if constexpr (WT == GT_Q8_0) { wq_bytes = (int64_t)p.N * p.K; ws_bytes = (int64_t)p.N * (p.K / 32) * 2; }
+    if constexpr (WT == GT_Q8_0) {
+        const int64_t blocks = (int64_t)(p.K / 64 - 1) * q8_rows(p) + p.N;   // (slab, row) blocks reachable
+        wq_bytes = blocks * 64;
+        ws_bytes = blocks * 4;
+    }
     if constexpr (WT == GT_Q4_K) { wq_bytes = (int64_t)p.N * p.K / 2; ws_bytes = (int64_t)p.N * (p.K / 32) * 8; }
     const __amdgpu_buffer_rsrc_t rq = make_rsrc(p.Wq, wq_bytes);
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(WT == GT_F16 ? p.Wq : p.Ws, WT == GT_F16 ? wq_bytes : ws_bytes);
@@ -487,14 +496,20 @@ struct DmaSrc {
     typedef DmaCfg<TM, TN, WT> C;
     __amdgpu_buffer_rsrc_t ra, rw, rs;
     uint32_t va[C::A_INSTR], vb[C::B_INSTR], vs[C::S_INSTR > 0 ? C::S_INSTR : 1];
-    int wid;
+    int wid, L;   // L: rows per slab block of a q8_0 weight
 
     __device__ __forceinline__ void init(const GemmParams& p, int m0, int n0, int wid_, int lane) {
         wid = wid_;
         const int mb = max(m0, 0);   // tiles of the fused conv-module epilogue start H rows early
         ra = make_rsrc((const f16*)p.A + (int64_t)mb * p.lda, ((int64_t)(p.M - mb - 1) * p.lda + p.K) * 2);
-        const int64_t wrow = WT == GT_Q8_0 ? p.K : WT == GT_Q4_K ? p.K / 2 : (int64_t)p.K * 2;  // bytes per row
-        rw = make_rsrc((const uint8_t*)p.Wq + n0 * wrow, (p.N - n0) * wrow);
+        L = q8_rows(p);
+        if constexpr (WT == GT_Q8_0) {
+            // slab-major: a slab's rows n0.. are contiguous 64-byte blocks, slab stride L * 64
+            rw = make_rsrc((const uint8_t*)p.Wq + (int64_t)n0 * 64, ((int64_t)(p.K / 64 - 1) * L + (p.N - n0)) * 64);
+        } else {
+            const int64_t wrow = WT == GT_Q4_K ? p.K / 2 : (int64_t)p.K * 2;  // bytes per row
+            rw = make_rsrc((const uint8_t*)p.Wq + n0 * wrow, (p.N - n0) * wrow);
+        }
 #pragma unroll
         for (int i = 0; i < C::A_INSTR; ++i) {
             const int slot = (wid * C::A_INSTR + i) * 64 + lane;   // 1 KB block = 8 rows of 128 B
@@ -508,13 +523,13 @@ struct DmaSrc {
                 const int slot = (wid * C::B_INSTR + i) * 64 + lane;   // 16 rows of 64 B
                 const int row = slot >> 2, c = (slot & 3) ^ ((row >> 2) & 3);
                 const int n = min(row, p.N - n0 - 1);
-                vb[i] = (uint32_t)((int64_t)n * p.K + 16 * c);
+                vb[i] = (uint32_t)(n * 64 + 16 * c);
             }
-            rs = make_rsrc((const f16*)p.Ws + (int64_t)n0 * (p.K / 32), (int64_t)(p.N - n0) * (p.K / 32) * 2);
+            rs = make_rsrc((const uint8_t*)p.Ws + (int64_t)n0 * 4, ((int64_t)(p.K / 64 - 1) * L + (p.N - n0)) * 4);
 #pragma unroll
             for (int i = 0; i < C::S_INSTR; ++i) {
                 const int n = min(i * 64 + lane, p.N - n0 - 1);    // 4 B = the slab's 2 scales of a row
-                vs[i] = (uint32_t)(n * (p.K / 32) * 2);
+                vs[i] = (uint32_t)(n * 4);
             }
         } else if constexpr (WT == GT_Q4_K) {
             // 32 nibble bytes per row and slab, 16-byte chunk c stored at c ^ ((row >> 3) & 1)
@@ -556,7 +571,7 @@ struct DmaSrc {
 #pragma unroll
         for (int i = 0; i < C::A_INSTR; ++i) lds_dma16(ra, st + (wid * C::A_INSTR + i) * 1024, va[i], k0 * 2);
         uint8_t* bs = st + C::A_BYTES;
-        const int kb = WT == GT_Q8_0 ? k0 : WT == GT_Q4_K ? k0 / 2 : k0 * 2;
+        const int kb = WT == GT_Q8_0 ? (k0 / 64) * L * 64 : WT == GT_Q4_K ? k0 / 2 : k0 * 2;
 #pragma unroll
         for (int i = 0; i < C::B_INSTR; ++i) {
             if constexpr (C::B_DMA == 16) lds_dma16(rw, bs + (wid * C::B_INSTR + i) * 1024, vb[i], kb);
@@ -565,7 +580,7 @@ struct DmaSrc {
         uint8_t* ss = bs + C::B_BYTES;
         if constexpr (WT == GT_Q8_0) {
 #pragma unroll
-            for (int i = 0; i < C::S_INSTR; ++i) lds_dma4(rs, ss + i * 256, vs[i], (k0 / 32) * 2);
+            for (int i = 0; i < C::S_INSTR; ++i) lds_dma4(rs, ss + i * 256, vs[i], (k0 / 64) * L * 4);
         } else if constexpr (WT == GT_Q4_K) {
 #pragma unroll
             for (int i = 0; i < C::S_INSTR; ++i) lds_dma4(rs, ss + (wid * C::S_INSTR + i) * 256, vs[i], k0 / 4);
@@ -573,14 +588,12 @@ struct DmaSrc {
     }
 };
 
+// B fragments of one slab for the 4 substeps, bf[j][s], dequantised to f16.
 template <int TM, int TN, int WT>
-__device__ __forceinline__ void mma32_slab(const uint8_t* st, float16v (&acc)[TM][TN], int wm, int wn,
-                                           int lane) {
+__device__ __forceinline__ void b_frags32(const uint8_t* st, half8v (&bf)[TN][4], int wn, int lane) {
     typedef DmaCfg<TM, TN, WT> C;
     const int q = lane >> 5, r32 = lane & 31;
     const uint8_t* bs = st + C::A_BYTES;
-    // B fragments for the 4 substeps: bf[j][s]
-    half8v bf[TN][4];
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
         const int row = wn * TN * 32 + 32 * j + r32;
@@ -620,6 +633,39 @@ __device__ __forceinline__ void mma32_slab(const uint8_t* st, float16v (&acc)[TM
             for (int s2 = 0; s2 < 4; ++s2) bf[j][s2] = *(const half8v*)(rp + (((4 * q + s2) ^ ((row >> 1) & 7)) << 4));
         }
     }
+}
+
+// A fragments of one slab, af[i][s].
+template <int TM>
+__device__ __forceinline__ void a_frags32(const uint8_t* st, half8v (&af)[TM][4], int wm, int lane) {
+    const int q = lane >> 5, r32 = lane & 31;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        const int row = wm * TM * 32 + 32 * i + r32;
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2)
+            af[i][s2] = *(const half8v*)(st + row * 128 + (((4 * q + s2) ^ ((row >> 1) & 7)) << 4));
+    }
+}
+
+template <int TM, int TN>
+__device__ __forceinline__ void mma32_frags(const half8v (&af)[TM][4], const half8v (&bf)[TN][4],
+                                            float16v (&acc)[TM][TN]) {
+#pragma unroll
+    for (int s2 = 0; s2 < 4; ++s2)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][s2], bf[j][s2], acc[i][j], 0, 0, 0);
+}
+
+template <int TM, int TN, int WT>
+__device__ __forceinline__ void mma32_slab(const uint8_t* st, float16v (&acc)[TM][TN], int wm, int wn,
+                                           int lane) {
+    const int q = lane >> 5, r32 = lane & 31;
+    half8v bf[TN][4];
+    b_frags32<TM, TN, WT>(st, bf, wn, lane);
 #pragma unroll
     for (int s2 = 0; s2 < 4; ++s2) {
 #pragma unroll
@@ -1019,7 +1065,13 @@ struct FoldStats {
 // summed in LDS (group 0 + group 1, a fixed order) before group 0 runs the
 // epilogue.  For grids of about one tile per CU: two waves per SIMD instead of
 // one.
-template <int TM, int TN, int WT, int EPI, int NS = DMA_NS, int KG = 1>
+// PP (with KG = 2): the two K groups run in anti-phase.  A group alternates a
+// fragment phase (LDS reads of slab t's A and B fragments, the dequantisation)
+// and an MFMA phase (slab t's 16 TM TN MFMAs on those registers), group 1 one
+// phase behind group 0, every phase closed by a workgroup barrier: while the
+// waves of one group issue MFMAs, the waves of the other (on the same SIMDs)
+// issue their LDS reads and vector ALU work.
+template <int TM, int TN, int WT, int EPI, int NS = DMA_NS, int KG = 1, int PP = 0>
 __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(GemmParams p) {
     typedef DmaCfg<TM, TN, WT> C;
     static_assert(NS == 2 || NS == 3, "LDS ring depth");
@@ -1059,6 +1111,42 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
     const int nk = p.K / 64 / KG, kb = kg * nk * 64;   // slabs of this group, its first K
     DmaSrc<TM, TN, WT> src;
     src.init(p, m0, n0, wid, lane);
+    if constexpr (PP) {
+        static_assert(KG == 2 && NS == 3, "anti-phase K groups: two groups, three stages");
+        src.issue(smem, kb);
+        if (nk > 1) src.issue(smem + C::STAGE, kb + 64);
+        half8v af[TM][4], bf[TN][4];
+        // group 0 reads slab 0 in the first phase
+        if (kg == 0) {
+            if (nk > 1) wait_vmcnt<C::PER_SLAB>();
+            else wait_vmcnt<0>();
+        }
+        __builtin_amdgcn_s_barrier();
+        // group-local phase q = ph - kg: fragments of slab q/2 at even q, its MFMAs at odd q
+        for (int ph = 0; ph <= 2 * nk; ++ph) {
+            const int q = ph - kg;
+            if (q >= 0 && q < 2 * nk) {
+                const int t = q >> 1;
+                if ((q & 1) == 0) {
+                    // stage (t+2) % 3 held slab t-1, whose MFMAs ended before the last barrier
+                    if (t + 2 < nk) src.issue(smem + ((t + 2) % 3) * C::STAGE, kb + (t + 2) * 64);
+                    a_frags32<TM>(smem + (t % 3) * C::STAGE, af, wm, lane);
+                    b_frags32<TM, TN, WT>(smem + (t % 3) * C::STAGE, bf, wn, lane);
+                } else {
+                    mma32_frags<TM, TN>(af, bf, acc);
+                }
+            }
+            // the group's next fragment phase (q + 1 even) needs slab (q + 1) / 2 in LDS:
+            // this wave's part has landed once the newer slabs alone are outstanding
+            if (((q + 1) & 1) == 0 && q + 1 < 2 * nk && q + 1 >= 0) {
+                const int tn = (q + 1) >> 1;
+                const int issued = q < 0 ? min(nk - 1, 1) : min(nk - 1, (q >> 1) + 2);
+                if (issued - tn >= 1) wait_vmcnt<C::PER_SLAB>();
+                else wait_vmcnt<0>();
+            }
+            __builtin_amdgcn_s_barrier();
+        }
+    } else {
     src.issue(smem, kb);
     if (NS == 3 && nk > 1) src.issue(smem + C::STAGE, kb + 64);
     int st = 0;
@@ -1077,6 +1165,7 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
         }
         mma32_slab<TM, TN, WT>(smem + st * C::STAGE, acc, wm, wn, lane);
         st = st + 1 == NS ? 0 : st + 1;
+    }
     }
     if constexpr (KG == 2) {
         // lane-major [wave][register][lane] f32: conflict-free both ways
@@ -1158,201 +1247,6 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
                                                 lane, fold, ftab, wm * TM * 32 + hh * TH * 32);
             }
         }
-    }
-}
-
-// ===========================================================================
-// Register-direct K-split GEMM (f16 activations; f16 or q8_0 weights).
-//
-// The 4 waves of a workgroup are KS K-parts x NS = 4/KS column parts.  A wave
-// owns a (32 TM) x (32 TN) output tile over K/KS and streams its operands
-// straight from global memory into registers, PF K-slabs of 64 ahead of the
-// MFMAs: no operand is shared between waves, so the main loop has no LDS
-// traffic and no barriers.  The same K permutation as the LDS kernels
-// (lane half q holds k = 32q + 8s + e in substep s) makes every operand a
-// 16-byte load: 64 contiguous bytes of an activation row, 32 contiguous bytes
-// of a q8_0 weight row (exactly one quant block, one scale).  At the end the
-// KS partial tiles are summed through LDS in a fixed order (deterministic),
-// each wave keeping TM/KS row blocks, and leave through the LDS-staged
-// coalesced epilogue.
-// ===========================================================================
-template <int TM, int TN, int KS, int WT>
-struct SkCfg {
-    static constexpr int NS = 4 / KS;
-    static constexpr int BM = 32 * TM, BN = 32 * TN * NS;
-    static constexpr int KEEP = TM / KS;                           // row blocks a wave finalises
-    static constexpr int WCH = WT == GT_Q8_0 ? 2 : 4;              // 16-byte weight chunks per lane per slab
-    static constexpr int RED_BYTES = NS * KS * KS * KEEP * TN * 4096;
-    static constexpr int EPI_BYTES = 4 * 32 * KEEP * (32 * TN + 4) * 4;
-    static constexpr int LDS_BYTES = RED_BYTES > EPI_BYTES ? RED_BYTES : EPI_BYTES;
-    static_assert(KS == 1 || KS == 2 || KS == 4, "K split");
-    static_assert(TM % KS == 0, "each K part must finalise whole row blocks");
-};
-
-template <int TM, int TN, int KS, int WT, int EPI, int PF, int BLK = 0>
-__global__ __launch_bounds__(256, 1) void gemm_sk_kernel(GemmParams p) {
-    typedef SkCfg<TM, TN, KS, WT> C;
-    __shared__ __attribute__((aligned(16))) uint8_t smem[C::LDS_BYTES];
-    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-    const int kh = wid / C::NS, nh = wid % C::NS;
-    const int q = lane >> 5, r32 = lane & 31;
-    const int nbm = cdiv_dev(p.M, C::BM), nbn = cdiv_dev(p.N, C::BN);
-    int bm, bn;
-    xcd_tile_2d(blockIdx.x, nbm, nbn, p.xcd_gm, bm, bn);
-    const int m0 = bm * C::BM, nw0 = bn * C::BN + nh * 32 * TN;
-    const int Kw = p.K / KS, kbeg = kh * Kw, nk = Kw / 64;
-
-    const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, ((int64_t)(p.M - 1) * p.lda + p.K) * 2);
-    const int64_t wq_bytes = (int64_t)p.N * p.K * (WT == GT_Q8_0 ? 1 : 2);
-    const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.Wq, wq_bytes);
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(WT == GT_Q8_0 ? p.Ws : p.Wq,
-                                                WT == GT_Q8_0 ? (int64_t)p.N * (p.K / 32) * 2 : wq_bytes);
-    uint32_t aoff[TM], woff[TN], soff[TN];
-    if constexpr (BLK) {
-        // fragment-major blocks: (32 rows, 64 k) -> 64 lanes x 64 B, lane-major per 16 B
-        const int nks = p.K / 64;
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-            aoff[i] = (uint32_t)((((m0 / 32 + i) * nks + kbeg / 64) * 4096) + lane * 16);
-#pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            const int nb = nw0 / 32 + j;
-            woff[j] = (uint32_t)(((nb * nks + kbeg / 64) * (WT == GT_Q8_0 ? 2048 : 4096)) + lane * 16);
-            soff[j] = (uint32_t)(((nb * nks + kbeg / 64) * 128) + lane * 2);
-        }
-    } else {
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-        const int m = m0 + 32 * i + r32;
-        aoff[i] = m < p.M ? (uint32_t)(((int64_t)m * p.lda + kbeg + 32 * q) * 2) : OOB;
-    }
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-        const int n = nw0 + 32 * j + r32;
-        woff[j] = n < p.N ? (uint32_t)(((int64_t)n * p.K + kbeg + 32 * q) * (WT == GT_Q8_0 ? 1 : 2)) : OOB;
-        soff[j] = n < p.N ? (uint32_t)(((int64_t)n * (p.K / 32) + kbeg / 32 + q) * 2) : OOB;
-    }
-    }
-
-    int4v abuf[PF][TM][4];
-    int4v wbuf[PF][TN][C::WCH];
-    uint32_t sbuf[PF][TN];
-    auto load = [&](int u, int kt) {
-        const uint32_t ka = BLK ? (uint32_t)kt * 4096u : (uint32_t)kt * 128u;
-        const uint32_t kw = BLK ? (uint32_t)kt * (WT == GT_Q8_0 ? 2048u : 4096u) : (uint32_t)kt * (WT == GT_Q8_0 ? 64u : 128u);
-        const uint32_t cs = BLK ? 1024u : 16u;                          // stride between a lane's 16-byte chunks
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int c = 0; c < 4; ++c) abuf[u][i][c] = bload16(ra, aoff[i] + ka + cs * c);
-#pragma unroll
-        for (int j = 0; j < TN; ++j) {
-#pragma unroll
-            for (int c = 0; c < C::WCH; ++c) wbuf[u][j][c] = bload16(rw, woff[j] + kw + cs * c);
-            if constexpr (WT == GT_Q8_0)
-                sbuf[u][j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(
-                    rs, (int)(soff[j] + (uint32_t)kt * (BLK ? 128u : 4u)), 0, 0);
-        }
-    };
-
-    float16v acc[TM][TN];
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = (float16v){};
-
-#pragma unroll
-    for (int u = 0; u < PF; ++u) load(u, u);
-    for (int kt0 = 0; kt0 < nk; kt0 += PF) {
-#pragma unroll
-        for (int u = 0; u < PF; ++u) {
-#pragma unroll
-            for (int s2 = 0; s2 < 4; ++s2) {
-                half8v bf[TN];
-#pragma unroll
-                for (int j = 0; j < TN; ++j) {
-                    if constexpr (WT == GT_Q8_0) {
-                        const f16 dh = __builtin_bit_cast(f16, (uint16_t)sbuf[u][j]);
-                        const half2v d2 = {dh, dh};
-                        const int4v raw = wbuf[u][j][s2 >> 1];
-                        half2v h0, h1, h2, h3;
-                        i8x4_to_f16((uint32_t)raw[2 * (s2 & 1)], d2, h0, h1);
-                        i8x4_to_f16((uint32_t)raw[2 * (s2 & 1) + 1], d2, h2, h3);
-                        bf[j] = (half8v){h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
-                    } else {
-                        bf[j] = __builtin_bit_cast(half8v, wbuf[u][j][s2]);
-                    }
-                }
-#pragma unroll
-                for (int i = 0; i < TM; ++i) {
-                    const half8v af = __builtin_bit_cast(half8v, abuf[u][i][s2]);
-#pragma unroll
-                    for (int j = 0; j < TN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[j], acc[i][j], 0, 0, 0);
-                }
-            }
-            if (kt0 + u + PF < nk) load(u, kt0 + u + PF);
-        }
-    }
-
-    // ---- fixed-order sum of the KS partial tiles ----
-    float16v fin[C::KEEP][TN];
-    if constexpr (KS == 1) {
-#pragma unroll
-        for (int ii = 0; ii < C::KEEP; ++ii)
-#pragma unroll
-            for (int j = 0; j < TN; ++j) fin[ii][j] = acc[ii][j];
-    } else {
-        // slot (nh, src, dst) holds src's partial of dst's row blocks, lane-major
-        // 16-byte chunks (conflict-free writes and reads)
-        float4v* red = (float4v*)smem;
-        auto slot = [&](int src, int dst, int ii, int j, int g) {
-            return ((((nh * KS + src) * KS + dst) * C::KEEP + ii) * TN + j) * 4 * 64 + g * 64 + lane;
-        };
-#pragma unroll
-        for (int dst = 0; dst < KS; ++dst) {
-            if (dst == kh) continue;
-#pragma unroll
-            for (int ii = 0; ii < C::KEEP; ++ii)
-#pragma unroll
-                for (int j = 0; j < TN; ++j)
-#pragma unroll
-                    for (int g = 0; g < 4; ++g) {
-                        const float16v& a = acc[dst * C::KEEP + ii][j];
-                        red[slot(kh, dst, ii, j, g)] = (float4v){a[4 * g], a[4 * g + 1], a[4 * g + 2], a[4 * g + 3]};
-                    }
-        }
-        __syncthreads();
-#pragma unroll
-        for (int ii = 0; ii < C::KEEP; ++ii)
-#pragma unroll
-            for (int j = 0; j < TN; ++j) {
-                float16v sum = {};
-#pragma unroll
-                for (int src = 0; src < KS; ++src) {
-                    if (src == kh) {
-                        sum += acc[kh * C::KEEP + ii][j];
-                    } else {
-#pragma unroll
-                        for (int g = 0; g < 4; ++g) {
-                            const float4v v = red[slot(src, kh, ii, j, g)];
-                            sum[4 * g] += v[0];
-                            sum[4 * g + 1] += v[1];
-                            sum[4 * g + 2] += v[2];
-                            sum[4 * g + 3] += v[3];
-                        }
-                    }
-                }
-                fin[ii][j] = sum;
-            }
-        __syncthreads();   // the reduction slots are reused by the epilogue staging below
-    }
-    const int mw = m0 + kh * C::KEEP * 32;
-    if constexpr (EPI == EPI_RELU_TR || EPI == EPI_RELU2_F32) {
-        epilogue32<EPI, f16, C::KEEP, TN>(p, fin, mw, nw0, lane);
-    } else {
-        float* wsm = (float*)smem + wid * (32 * C::KEEP) * ((EPI == EPI_GLU ? 16 * TN : 32 * TN) + 4);
-        epilogue32_lds<EPI, C::KEEP, TN>(p, fin, wsm, mw, nw0, lane);
     }
 }
 
@@ -1457,8 +1351,9 @@ template <int BN> struct BLoad32<GT_Q8_0, BN> {
             int4v v = {};
             float s = 0.f;
             if (c < BN * 2 && n < p.N && k0 < p.K) {
-                v = *(const int4v*)(W + (int64_t)n * p.K + k0 + 16 * h);
-                s = (float)S[(int64_t)n * (p.K / 32) + k0 / 32];
+                const int64_t blk = (int64_t)(k0 / 64) * q8_rows(p) + n;   // slab-major
+                v = *(const int4v*)(W + blk * 64 + (k0 & 63) + 16 * h);
+                s = (float)S[blk * 2 + ((k0 & 63) >> 5)];
             }
             q[i] = v;
             d[i] = s;
@@ -1655,7 +1550,7 @@ static int choose_xcd_gm(const GemmParams& p, int WT, int BM, int BN) {
     return best_cost < 1e300 ? best : 1;
 }
 
-template <int TM, int TN, int WT, int EPI, int NS = DMA_NS, int KG = 1>
+template <int TM, int TN, int WT, int EPI, int NS = DMA_NS, int KG = 1, int PP = 0>
 static void run_dma(const GemmParams& p, hipStream_t s) {
     if constexpr ((EPI == EPI_GLU || EPI == EPI_GLU_DW) && TN % 2 != 0) {
         throw std::logic_error("gemm: GLU epilogue dispatched to a 64-wide tile");
@@ -1665,7 +1560,7 @@ static void run_dma(const GemmParams& p, hipStream_t s) {
         const int tiles = cdiv(p.M, sm) * cdiv(p.N, 64 * TN);
         GemmParams q = p;
         q.xcd_gm = choose_xcd_gm(p, WT, sm, 64 * TN);
-        launch((gemm_dma_kernel<TM, TN, WT, EPI, NS, KG>), dim3(tiles), dim3(256 * KG), 0, s, q);
+        launch((gemm_dma_kernel<TM, TN, WT, EPI, NS, KG, PP>), dim3(tiles), dim3(256 * KG), 0, s, q);
         PKX_LAUNCH_CHECK();
     }
 }
@@ -1787,8 +1682,9 @@ __global__ void dequant_q8_0_kernel(const uint8_t* src, float* dst, int64_t nblk
 
 // One wave per weight row n: c1 = g . w[n], c2 = b . w[n] + bias[n], with w the
 // f16 value the GEMM's in-register dequantisation produces (device layouts:
-// f16 [N][K]; q8_0 int8 [N][K] + f16 d [N][K/32], w = f16(q d); q4_K nibbles
-// [N][K/2] + float2 {scale, min} [N][K/32], w = f16(q s16 - m16)).
+// f16 [N][K]; q8_0 slab-major int8 [K/64][N][64] + f16 d [K/64][N][2],
+// w = f16(q d); q4_K nibbles [N][K/2] + float2 {scale, min} [N][K/32],
+// w = f16(q s16 - m16)).
 __global__ void ln_fold_consts_kernel(int wtype, const uint8_t* Wq, const uint8_t* Ws, int N, int K, const float* g,
                                       const float* b, const float* bias, float* c1, float* c2) {
     const int n = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -1798,9 +1694,10 @@ __global__ void ln_fold_consts_kernel(int wtype, const uint8_t* Wq, const uint8_
         float w;
         if (wtype == GT_F16) {
             w = (float)((const f16*)Wq)[(int64_t)n * K + k];
-        } else if (wtype == GT_Q8_0) {
-            const float q = (float)((const int8_t*)Wq)[(int64_t)n * K + k];
-            const float d = (float)((const f16*)Ws)[(int64_t)n * (K / 32) + k / 32];
+        } else if (wtype == GT_Q8_0) {   // slab-major, N rows per slab block
+            const int64_t blk = (int64_t)(k / 64) * N + n;
+            const float q = (float)((const int8_t*)Wq)[blk * 64 + (k & 63)];
+            const float d = (float)((const f16*)Ws)[blk * 2 + ((k & 63) >> 5)];
             w = (float)(f16)(q * d);
         } else {
             const int l = k % 64;

@@ -223,17 +223,20 @@ DevWeight build_weight(const HostTensor& t, int N, int K, bool f16_gemm, std::ve
         PKX_HIP(hipMemcpy(w.q, src, (size_t)N * K * 2, hipMemcpyHostToDevice));
         break;
     case GT_Q8_0: {
-        require(K % 32 == 0, "q8_0 weight K % 32 != 0");
+        // slab-major: block b of row n lands in slab b / 2 at (slab * N + n) * 64 + 32 (b % 2)
+        require(K % 64 == 0, "q8_0 weight: K must be a multiple of 64");
         const int nb = K / 32;
         std::vector<int8_t> q((size_t)N * K);
         std::vector<uint16_t> d((size_t)N * nb);
         for (int n = 0; n < N; ++n)
             for (int b = 0; b < nb; ++b) {
                 const uint8_t* blk = src + ((size_t)n * nb + b) * 34;
-                d[(size_t)n * nb + b] = (uint16_t)(blk[0] | (blk[1] << 8));
-                std::memcpy(&q[(size_t)n * K + (size_t)b * 32], blk + 2, 32);
+                const size_t slab = (size_t)(b / 2) * N + n;
+                d[slab * 2 + b % 2] = (uint16_t)(blk[0] | (blk[1] << 8));
+                std::memcpy(&q[slab * 64 + (size_t)(b % 2) * 32], blk + 2, 32);
             }
         w.gtype = GT_Q8_0;
+        w.ldn = N;
         w.q = dalloc(q.size());
         w.s = dalloc(d.size() * 2);
         PKX_HIP(hipMemcpy(w.q, q.data(), q.size(), hipMemcpyHostToDevice));
@@ -316,7 +319,8 @@ DevWeight Model::make_weight_rows(const std::vector<const HostTensor*>& parts, i
 }
 
 // Rows [row0, row0 + nrows) of a device weight, as a weight of its own (no copy):
-// every device layout stores rows contiguously, payload and scales alike.
+// row-major layouts by offset, the slab-major q8_0 layout by offset inside each
+// slab block (ldn stays the allocation's row count).
 DevWeight weight_rows_view(const DevWeight& w, int row0, int nrows) {
     DevWeight v = w;
     v.N = nrows;
@@ -324,9 +328,9 @@ DevWeight weight_rows_view(const DevWeight& w, int row0, int nrows) {
     switch (w.gtype) {
     case GT_F32: v.q = (uint8_t*)w.q + r * K * 4; break;
     case GT_F16: v.q = (uint8_t*)w.q + r * K * 2; break;
-    case GT_Q8_0:
-        v.q = (uint8_t*)w.q + r * K;
-        v.s = (uint8_t*)w.s + r * (K / 32) * 2;
+    case GT_Q8_0:   // slab-major: the rows' offset inside every slab block
+        v.q = (uint8_t*)w.q + r * 64;
+        v.s = (uint8_t*)w.s + r * 4;
         break;
     case GT_Q4_K:
         v.q = (uint8_t*)w.q + r * K / 2;
@@ -353,6 +357,7 @@ void linear_raw(Precision prec, const HostTensor& t, int N, int K, const float* 
         p.lda = K;
         p.Wq = w.q;
         p.Ws = w.s;
+        p.ldw = w.ldn;
         p.bias = bias;
         p.Y = y;
         p.ldy = N;
@@ -659,6 +664,7 @@ void Model::gemm(const DevWeight& w, int epi, const void* A, int64_t lda, int64_
     p.lda = lda;
     p.Wq = w.q;
     p.Ws = w.s;
+    p.ldw = w.ldn;
     p.bias = bias;
     p.bias2 = bias2;
     p.Y = Y;
@@ -683,6 +689,7 @@ void Model::gemm_resid_ln(const DevWeight& w, const void* A, int64_t M, const fl
     p.lda = w.K;
     p.Wq = w.q;
     p.Ws = w.s;
+    p.ldw = w.ldn;
     p.bias = bias;
     p.Y = x;
     p.ldy = w.N;
@@ -705,6 +712,7 @@ GemmParams Model::fold_params(const DevWeight& w, const void* A, int64_t M, cons
     p.lda = w.K;
     p.Wq = w.q;
     p.Ws = w.s;
+    p.ldw = w.ldn;
     p.bias = c2;
     p.Y = Y;
     p.ldy = ldy;
@@ -730,6 +738,7 @@ void Model::conv_front(const LayerDev& L, const void* A, int64_t M, const int* v
         p.lda = D;
         p.Wq = L.pw1.q;
         p.Ws = L.pw1.s;
+        p.ldw = L.pw1.ldn;
         p.bias = fold ? L.pw1_c2 : L.pw1_b;
         p.Y = Y;
         p.ldy = D;

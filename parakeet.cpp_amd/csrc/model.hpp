@@ -35,9 +35,14 @@ struct HostTensor {
     int64_t nelem() const { return ne[0] * ne[1] * ne[2] * ne[3]; }
 };
 
+// Device weight layouts: f32 / f16 [N][K]; q8_0 slab-major, int8 [K/64][ldn][64]
+// with f16 scales [K/64][ldn][2] (one 64-wide K slab of ldn rows is contiguous,
+// so a GEMM tile's slab of weights and of scales each stream as whole cache
+// lines); q4_K nibbles [N][K/2] with float2 {scale, min} [N][K/32].
 struct DevWeight {
     int gtype = -1;   // device storage type (GT_F32/GT_F16/GT_Q8_0/GT_Q4_K)
     int N = 0, K = 0;
+    int ldn = 0;      // q8_0: rows per slab block (N of the allocation a view points into)
     void* q = nullptr;
     void* s = nullptr;
     bool ok() const { return gtype >= 0; }
