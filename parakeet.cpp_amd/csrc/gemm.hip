@@ -20,9 +20,9 @@ __device__ __forceinline__ int xcd_tile(int bid, int total) {
     return x * per + (x < rem ? x : rem) + loc;
 }
 
-// Rows of each 64-wide K slab block of a slab-major q8_0 weight (views into a
-// larger allocation keep the allocation's row count).
-__device__ __forceinline__ int q8_rows(const GemmParams& p) { return p.ldw > 0 ? p.ldw : p.N; }
+// Rows of each 64-wide K slab block of a slab-major (q8_0 / q4_K) weight (views
+// into a larger allocation keep the allocation's row count).
+__device__ __forceinline__ int slab_rows(const GemmParams& p) { return p.ldw > 0 ? p.ldw : p.N; }
 
 // Wave index as a wave-uniform (scalar) value.
 __device__ __forceinline__ int wave_id_uniform() { return __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6); }
@@ -234,7 +234,7 @@ template <int BN> struct BLoad16<GT_Q8_0, BN> {
             const int c = tid + 256 * i;
             const int n = n0 + (c >> 2), k = k0 + (c & 3) * 16;
             const bool in = k < p.K && n < p.N;
-            const int L = q8_rows(p);   // slab-major: (slab, row) blocks of 64 bytes / 2 scales
+            const int L = slab_rows(p);   // slab-major: (slab, row) blocks of 64 bytes / 2 scales
             q[i] = bload16(rq, in ? (uint32_t)(((int64_t)(k / 64) * L + n) * 64 + (k & 63)) : OOB);
             d[i] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(
                 rs, (int)(in ? (uint32_t)((((int64_t)(k / 64) * L + n) * 2 + ((k & 63) >> 5)) * 2) : OOB), 0, 0);
@@ -263,9 +263,9 @@ template <int BN> struct BLoad16<GT_Q8_0, BN> {
     }
 };
 
-// q4_K device layout: nibbles u8 qs[N][K/2] in ggml order (per 64 elements, byte l
-// holds element l in the low and element 32+l in the high nibble) and float2
-// {d*sc, dmin*m}[N][K/32]; w = s.x*q - s.y.
+// q4_K device layout (slab-major): nibbles u8 qs[K/64][ldw][32] in ggml order
+// (per 64 elements, byte l holds element l in the low and element 32+l in the
+// high nibble) and float2 {d*sc, dmin*m}[K/64][ldw][2]; w = s.x*q - s.y.
 template <int BN> struct BLoad16<GT_Q4_K, BN> {
     static constexpr int NC = (BN * 2 + 255) / 256;
     int4v q[NC];
@@ -277,8 +277,9 @@ template <int BN> struct BLoad16<GT_Q4_K, BN> {
             const int c = tid + 256 * i;
             const int n = n0 + (c >> 1), h = c & 1;
             const bool in = k0 < p.K && n < p.N;
-            q[i] = bload16(rq, in ? (uint32_t)((int64_t)n * (p.K / 2) + k0 / 2 + 16 * h) : OOB);
-            s[i] = __builtin_bit_cast(float4v, bload16(rs, in ? (uint32_t)(((int64_t)n * (p.K / 32) + k0 / 32) * 8) : OOB));
+            const int64_t blk = (int64_t)(k0 / 64) * slab_rows(p) + n;   // slab-major
+            q[i] = bload16(rq, in ? (uint32_t)(blk * 32 + 16 * h) : OOB);
+            s[i] = __builtin_bit_cast(float4v, bload16(rs, in ? (uint32_t)(blk * 16) : OOB));
         }
     }
     __device__ void store(f16* Bs, int tid) const {
@@ -342,11 +343,15 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(GemmParams p) {
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, ((int64_t)(p.M - 1) * p.lda + p.K) * 2);
     int64_t wq_bytes = (int64_t)p.N * p.K * 2, ws_bytes = 0;
     if constexpr (WT == GT_Q8_0) {
-        const int64_t blocks = (int64_t)(p.K / 64 - 1) * q8_rows(p) + p.N;   // (slab, row) blocks reachable
+        const int64_t blocks = (int64_t)(p.K / 64 - 1) * slab_rows(p) + p.N;   // (slab, row) blocks reachable
         wq_bytes = blocks * 64;
         ws_bytes = blocks * 4;
     }
-    if constexpr (WT == GT_Q4_K) { wq_bytes = (int64_t)p.N * p.K / 2; ws_bytes = (int64_t)p.N * (p.K / 32) * 8; }
+    if constexpr (WT == GT_Q4_K) {
+        const int64_t blocks = (int64_t)(p.K / 64 - 1) * slab_rows(p) + p.N;
+        wq_bytes = blocks * 32;
+        ws_bytes = blocks * 16;
+    }
     const __amdgpu_buffer_rsrc_t rq = make_rsrc(p.Wq, wq_bytes);
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(WT == GT_F16 ? p.Wq : p.Ws, WT == GT_F16 ? wq_bytes : ws_bytes);
 
@@ -502,13 +507,13 @@ struct DmaSrc {
         wid = wid_;
         const int mb = max(m0, 0);   // tiles of the fused conv-module epilogue start H rows early
         ra = make_rsrc((const f16*)p.A + (int64_t)mb * p.lda, ((int64_t)(p.M - mb - 1) * p.lda + p.K) * 2);
-        L = q8_rows(p);
-        if constexpr (WT == GT_Q8_0) {
-            // slab-major: a slab's rows n0.. are contiguous 64-byte blocks, slab stride L * 64
-            rw = make_rsrc((const uint8_t*)p.Wq + (int64_t)n0 * 64, ((int64_t)(p.K / 64 - 1) * L + (p.N - n0)) * 64);
+        L = slab_rows(p);
+        if constexpr (WT == GT_Q8_0 || WT == GT_Q4_K) {
+            // slab-major: a slab's rows n0.. are contiguous WB-byte blocks, slab stride L * WB
+            constexpr int WB = WT == GT_Q8_0 ? 64 : 32;
+            rw = make_rsrc((const uint8_t*)p.Wq + (int64_t)n0 * WB, ((int64_t)(p.K / 64 - 1) * L + (p.N - n0)) * WB);
         } else {
-            const int64_t wrow = WT == GT_Q4_K ? p.K / 2 : (int64_t)p.K * 2;  // bytes per row
-            rw = make_rsrc((const uint8_t*)p.Wq + n0 * wrow, (p.N - n0) * wrow);
+            rw = make_rsrc((const uint8_t*)p.Wq + n0 * (int64_t)p.K * 2, (p.N - n0) * (int64_t)p.K * 2);
         }
 #pragma unroll
         for (int i = 0; i < C::A_INSTR; ++i) {
@@ -545,15 +550,15 @@ struct DmaSrc {
                     off = 16 * (((slot >> 2) & 1) ^ ((row >> 3) & 1)) + 4 * (slot & 3);
                 }
                 const int n = min(row, p.N - n0 - 1);
-                vb[i] = (uint32_t)((int64_t)n * (p.K / 2) + off);
+                vb[i] = (uint32_t)(n * 32 + off);
             }
-            // {d*sc, dmin*m} float pairs of the slab's two sub-blocks: 16 B per row
-            rs = make_rsrc((const float*)p.Ws + (int64_t)n0 * (p.K / 32) * 2, (int64_t)(p.N - n0) * (p.K / 32) * 8);
+            // {d*sc, dmin*m} float pairs of the slab's two sub-blocks: 16 B per row, slab-major
+            rs = make_rsrc((const uint8_t*)p.Ws + (int64_t)n0 * 16, ((int64_t)(p.K / 64 - 1) * L + (p.N - n0)) * 16);
 #pragma unroll
             for (int i = 0; i < C::S_INSTR; ++i) {
                 const int slot = (wid * C::S_INSTR + i) * 64 + lane;
                 const int n = min(slot >> 2, p.N - n0 - 1);
-                vs[i] = (uint32_t)(n * (p.K / 32) * 8 + 4 * (slot & 3));
+                vs[i] = (uint32_t)(n * 16 + 4 * (slot & 3));
             }
         } else {
             rs = rw;
@@ -571,7 +576,7 @@ struct DmaSrc {
 #pragma unroll
         for (int i = 0; i < C::A_INSTR; ++i) lds_dma16(ra, st + (wid * C::A_INSTR + i) * 1024, va[i], k0 * 2);
         uint8_t* bs = st + C::A_BYTES;
-        const int kb = WT == GT_Q8_0 ? (k0 / 64) * L * 64 : WT == GT_Q4_K ? k0 / 2 : k0 * 2;
+        const int kb = WT == GT_Q8_0 ? (k0 / 64) * L * 64 : WT == GT_Q4_K ? (k0 / 64) * L * 32 : k0 * 2;
 #pragma unroll
         for (int i = 0; i < C::B_INSTR; ++i) {
             if constexpr (C::B_DMA == 16) lds_dma16(rw, bs + (wid * C::B_INSTR + i) * 1024, vb[i], kb);
@@ -583,7 +588,7 @@ struct DmaSrc {
             for (int i = 0; i < C::S_INSTR; ++i) lds_dma4(rs, ss + i * 256, vs[i], (k0 / 64) * L * 4);
         } else if constexpr (WT == GT_Q4_K) {
 #pragma unroll
-            for (int i = 0; i < C::S_INSTR; ++i) lds_dma4(rs, ss + (wid * C::S_INSTR + i) * 256, vs[i], k0 / 4);
+            for (int i = 0; i < C::S_INSTR; ++i) lds_dma4(rs, ss + (wid * C::S_INSTR + i) * 256, vs[i], (k0 / 64) * L * 16);
         }
     }
 };
@@ -1351,7 +1356,7 @@ template <int BN> struct BLoad32<GT_Q8_0, BN> {
             int4v v = {};
             float s = 0.f;
             if (c < BN * 2 && n < p.N && k0 < p.K) {
-                const int64_t blk = (int64_t)(k0 / 64) * q8_rows(p) + n;   // slab-major
+                const int64_t blk = (int64_t)(k0 / 64) * slab_rows(p) + n;   // slab-major
                 v = *(const int4v*)(W + blk * 64 + (k0 & 63) + 16 * h);
                 s = (float)S[blk * 2 + ((k0 & 63) >> 5)];
             }
@@ -1384,11 +1389,10 @@ template <int BN> struct BLoad32<GT_Q4_K, BN> {
     __device__ void load(const GemmParams& p, int n0, int k0, int tid) {
         const uint8_t* W = (const uint8_t*)p.Wq;
         const float2v* S = (const float2v*)p.Ws;
-        // 32-element sub-block k0: low nibbles of bytes [k0/2, +32) if k0 % 64 == 0,
-        // else high nibbles of bytes [(k0-32)/2, +32).
+        // 32-element sub-block k0: the low nibbles of its slab block's 32 bytes if
+        // k0 % 64 == 0, else the high nibbles
         const int hi = (k0 & 32) ? 1 : 0;
         shift = hi * 4;
-        const int byte0 = (k0 - 32 * hi) / 2;
 #pragma unroll
         for (int i = 0; i < NC; ++i) {
             const int c = tid + 256 * i;
@@ -1397,8 +1401,9 @@ template <int BN> struct BLoad32<GT_Q4_K, BN> {
             int4v v = {};
             float2v sc = {0.f, 0.f};
             if (c < BN * 2 && n < p.N && k0 < p.K) {
-                v = *(const int4v*)(W + (int64_t)n * (p.K / 2) + byte0 + 16 * h);
-                sc = S[(int64_t)n * (p.K / 32) + k0 / 32];
+                const int64_t blk = (int64_t)(k0 / 64) * slab_rows(p) + n;   // slab-major
+                v = *(const int4v*)(W + blk * 32 + 16 * h);
+                sc = S[blk * 2 + hi];
             }
             q[i] = v;
             s[i] = sc;
@@ -1683,8 +1688,8 @@ __global__ void dequant_q8_0_kernel(const uint8_t* src, float* dst, int64_t nblk
 // One wave per weight row n: c1 = g . w[n], c2 = b . w[n] + bias[n], with w the
 // f16 value the GEMM's in-register dequantisation produces (device layouts:
 // f16 [N][K]; q8_0 slab-major int8 [K/64][N][64] + f16 d [K/64][N][2],
-// w = f16(q d); q4_K nibbles [N][K/2] + float2 {scale, min} [N][K/32],
-// w = f16(q s16 - m16)).
+// w = f16(q d); q4_K slab-major nibbles [K/64][N][32] + float2 {scale, min}
+// [K/64][N][2], w = f16(q s16 - m16)).
 __global__ void ln_fold_consts_kernel(int wtype, const uint8_t* Wq, const uint8_t* Ws, int N, int K, const float* g,
                                       const float* b, const float* bias, float* c1, float* c2) {
     const int n = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -1701,9 +1706,10 @@ __global__ void ln_fold_consts_kernel(int wtype, const uint8_t* Wq, const uint8_
             w = (float)(f16)(q * d);
         } else {
             const int l = k % 64;
-            const uint8_t byte = Wq[(int64_t)n * (K / 2) + (k / 64) * 32 + (l & 31)];
+            const int64_t blk = (int64_t)(k / 64) * N + n;   // slab-major, N rows per slab block
+            const uint8_t byte = Wq[blk * 32 + (l & 31)];
             const float q = (float)(l < 32 ? (byte & 0xF) : (byte >> 4));
-            const float2v sm = ((const float2v*)Ws)[(int64_t)n * (K / 32) + k / 32];
+            const float2v sm = ((const float2v*)Ws)[blk * 2 + (l >> 5)];
             w = (float)(f16)fmaf(q, (float)(f16)sm.x, (float)(f16)(-sm.y));
         }
         s1 += g[k] * w;

@@ -35,8 +35,8 @@ struct GemmParams {
     const void* A = nullptr;   // activations, row stride lda elements
     int64_t lda = 0;
     const void* Wq = nullptr;  // weight payload (device layout per type, see DevWeight)
-    const void* Ws = nullptr;  // per-block scales (q8_0: f16 [K/64][ldw][2]; q4_K: float2 [N][K/32])
-    int ldw = 0;               // q8_0: rows of each 64-wide K slab block of Wq / Ws (0: N)
+    const void* Ws = nullptr;  // per-block scales (q8_0: f16 [K/64][ldw][2]; q4_K: float2 [K/64][ldw][2])
+    int ldw = 0;               // q8_0 / q4_K: rows of each 64-wide K slab block of Wq / Ws (0: N)
     const float* bias = nullptr;
     const float* bias2 = nullptr;
     void* Y = nullptr;         // output (EPI_RESID: the f32 residual updated in place)

@@ -263,13 +263,17 @@ DevWeight build_weight(const HostTensor& t, int N, int K, bool f16_gemm, std::ve
                         s = (s6[j + 4] & 0xF) | ((s6[j - 4] >> 6) << 4);
                         m = (s6[j + 4] >> 4) | ((s6[j] >> 6) << 4);
                     }
-                    float* o = &sc[((size_t)n * (K / 32) + (size_t)b * 8 + j) * 2];
+                    // slab-major: sub-block 8b + j is half (j % 2) of slab 4b + j / 2
+                    float* o = &sc[(((size_t)(4 * b + j / 2) * N + n) * 2 + (j % 2)) * 2];
                     o[0] = d * (float)s;
                     o[1] = dmin * (float)m;
                 }
-                std::memcpy(&qs[(size_t)n * (K / 2) + (size_t)b * 128], blk + 16, 128);
+                // 32 nibble bytes per 64 elements: slab 4b + c holds bytes [32c, 32c + 32) of the block
+                for (int c = 0; c < 4; ++c)
+                    std::memcpy(&qs[((size_t)(4 * b + c) * N + n) * 32], blk + 16 + 32 * c, 32);
             }
         w.gtype = GT_Q4_K;
+        w.ldn = N;
         w.q = dalloc(qs.size());
         w.s = dalloc(sc.size() * 4);
         PKX_HIP(hipMemcpy(w.q, qs.data(), qs.size(), hipMemcpyHostToDevice));
@@ -332,9 +336,9 @@ DevWeight weight_rows_view(const DevWeight& w, int row0, int nrows) {
         v.q = (uint8_t*)w.q + r * 64;
         v.s = (uint8_t*)w.s + r * 4;
         break;
-    case GT_Q4_K:
-        v.q = (uint8_t*)w.q + r * K / 2;
-        v.s = (uint8_t*)w.s + r * (K / 32) * 8;
+    case GT_Q4_K:   // slab-major as q8_0
+        v.q = (uint8_t*)w.q + r * 32;
+        v.s = (uint8_t*)w.s + r * 16;
         break;
     default: throw std::logic_error("weight view: unknown type");
     }

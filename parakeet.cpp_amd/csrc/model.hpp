@@ -38,11 +38,12 @@ struct HostTensor {
 // Device weight layouts: f32 / f16 [N][K]; q8_0 slab-major, int8 [K/64][ldn][64]
 // with f16 scales [K/64][ldn][2] (one 64-wide K slab of ldn rows is contiguous,
 // so a GEMM tile's slab of weights and of scales each stream as whole cache
-// lines); q4_K nibbles [N][K/2] with float2 {scale, min} [N][K/32].
+// lines); q4_K slab-major too, nibbles [K/64][ldn][32] with float2
+// {scale, min} [K/64][ldn][2].
 struct DevWeight {
     int gtype = -1;   // device storage type (GT_F32/GT_F16/GT_Q8_0/GT_Q4_K)
     int N = 0, K = 0;
-    int ldn = 0;      // q8_0: rows per slab block (N of the allocation a view points into)
+    int ldn = 0;      // q8_0 / q4_K: rows per slab block (N of the allocation a view points into)
     void* q = nullptr;
     void* s = nullptr;
     bool ok() const { return gtype >= 0; }
