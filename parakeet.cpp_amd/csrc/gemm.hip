@@ -640,31 +640,6 @@ __device__ __forceinline__ void b_frags32(const uint8_t* st, half8v (&bf)[TN][4]
     }
 }
 
-// A fragments of one slab, af[i][s].
-template <int TM>
-__device__ __forceinline__ void a_frags32(const uint8_t* st, half8v (&af)[TM][4], int wm, int lane) {
-    const int q = lane >> 5, r32 = lane & 31;
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-        const int row = wm * TM * 32 + 32 * i + r32;
-#pragma unroll
-        for (int s2 = 0; s2 < 4; ++s2)
-            af[i][s2] = *(const half8v*)(st + row * 128 + (((4 * q + s2) ^ ((row >> 1) & 7)) << 4));
-    }
-}
-
-template <int TM, int TN>
-__device__ __forceinline__ void mma32_frags(const half8v (&af)[TM][4], const half8v (&bf)[TN][4],
-                                            float16v (&acc)[TM][TN]) {
-#pragma unroll
-    for (int s2 = 0; s2 < 4; ++s2)
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int j = 0; j < TN; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][s2], bf[j][s2], acc[i][j], 0, 0, 0);
-}
-
 template <int TM, int TN, int WT>
 __device__ __forceinline__ void mma32_slab(const uint8_t* st, float16v (&acc)[TM][TN], int wm, int wn,
                                            int lane) {
@@ -1070,13 +1045,7 @@ struct FoldStats {
 // summed in LDS (group 0 + group 1, a fixed order) before group 0 runs the
 // epilogue.  For grids of about one tile per CU: two waves per SIMD instead of
 // one.
-// PP (with KG = 2): the two K groups run in anti-phase.  A group alternates a
-// fragment phase (LDS reads of slab t's A and B fragments, the dequantisation)
-// and an MFMA phase (slab t's 16 TM TN MFMAs on those registers), group 1 one
-// phase behind group 0, every phase closed by a workgroup barrier: while the
-// waves of one group issue MFMAs, the waves of the other (on the same SIMDs)
-// issue their LDS reads and vector ALU work.
-template <int TM, int TN, int WT, int EPI, int NS = DMA_NS, int KG = 1, int PP = 0>
+template <int TM, int TN, int WT, int EPI, int NS = DMA_NS, int KG = 1>
 __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(GemmParams p) {
     typedef DmaCfg<TM, TN, WT> C;
     static_assert(NS == 2 || NS == 3, "LDS ring depth");
@@ -1116,42 +1085,6 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
     const int nk = p.K / 64 / KG, kb = kg * nk * 64;   // slabs of this group, its first K
     DmaSrc<TM, TN, WT> src;
     src.init(p, m0, n0, wid, lane);
-    if constexpr (PP) {
-        static_assert(KG == 2 && NS == 3, "anti-phase K groups: two groups, three stages");
-        src.issue(smem, kb);
-        if (nk > 1) src.issue(smem + C::STAGE, kb + 64);
-        half8v af[TM][4], bf[TN][4];
-        // group 0 reads slab 0 in the first phase
-        if (kg == 0) {
-            if (nk > 1) wait_vmcnt<C::PER_SLAB>();
-            else wait_vmcnt<0>();
-        }
-        __builtin_amdgcn_s_barrier();
-        // group-local phase q = ph - kg: fragments of slab q/2 at even q, its MFMAs at odd q
-        for (int ph = 0; ph <= 2 * nk; ++ph) {
-            const int q = ph - kg;
-            if (q >= 0 && q < 2 * nk) {
-                const int t = q >> 1;
-                if ((q & 1) == 0) {
-                    // stage (t+2) % 3 held slab t-1, whose MFMAs ended before the last barrier
-                    if (t + 2 < nk) src.issue(smem + ((t + 2) % 3) * C::STAGE, kb + (t + 2) * 64);
-                    a_frags32<TM>(smem + (t % 3) * C::STAGE, af, wm, lane);
-                    b_frags32<TM, TN, WT>(smem + (t % 3) * C::STAGE, bf, wn, lane);
-                } else {
-                    mma32_frags<TM, TN>(af, bf, acc);
-                }
-            }
-            // the group's next fragment phase (q + 1 even) needs slab (q + 1) / 2 in LDS:
-            // this wave's part has landed once the newer slabs alone are outstanding
-            if (((q + 1) & 1) == 0 && q + 1 < 2 * nk && q + 1 >= 0) {
-                const int tn = (q + 1) >> 1;
-                const int issued = q < 0 ? min(nk - 1, 1) : min(nk - 1, (q >> 1) + 2);
-                if (issued - tn >= 1) wait_vmcnt<C::PER_SLAB>();
-                else wait_vmcnt<0>();
-            }
-            __builtin_amdgcn_s_barrier();
-        }
-    } else {
     src.issue(smem, kb);
     if (NS == 3 && nk > 1) src.issue(smem + C::STAGE, kb + 64);
     int st = 0;
@@ -1170,7 +1103,6 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
         }
         mma32_slab<TM, TN, WT>(smem + st * C::STAGE, acc, wm, wn, lane);
         st = st + 1 == NS ? 0 : st + 1;
-    }
     }
     if constexpr (KG == 2) {
         // lane-major [wave][register][lane] f32: conflict-free both ways
@@ -1555,7 +1487,7 @@ static int choose_xcd_gm(const GemmParams& p, int WT, int BM, int BN) {
     return best_cost < 1e300 ? best : 1;
 }
 
-template <int TM, int TN, int WT, int EPI, int NS = DMA_NS, int KG = 1, int PP = 0>
+template <int TM, int TN, int WT, int EPI, int NS = DMA_NS, int KG = 1>
 static void run_dma(const GemmParams& p, hipStream_t s) {
     if constexpr ((EPI == EPI_GLU || EPI == EPI_GLU_DW) && TN % 2 != 0) {
         throw std::logic_error("gemm: GLU epilogue dispatched to a 64-wide tile");
@@ -1565,7 +1497,7 @@ static void run_dma(const GemmParams& p, hipStream_t s) {
         const int tiles = cdiv(p.M, sm) * cdiv(p.N, 64 * TN);
         GemmParams q = p;
         q.xcd_gm = choose_xcd_gm(p, WT, sm, 64 * TN);
-        launch((gemm_dma_kernel<TM, TN, WT, EPI, NS, KG, PP>), dim3(tiles), dim3(256 * KG), 0, s, q);
+        launch((gemm_dma_kernel<TM, TN, WT, EPI, NS, KG>), dim3(tiles), dim3(256 * KG), 0, s, q);
         PKX_LAUNCH_CHECK();
     }
 }
