@@ -593,68 +593,117 @@ struct DmaSrc {
     }
 };
 
-// B fragments of one slab for the 4 substeps, bf[j][s], dequantised to f16.
-template <int TM, int TN, int WT>
-__device__ __forceinline__ void b_frags32(const uint8_t* st, half8v (&bf)[TN][4], int wn, int lane) {
+// B operand of one slab for one wave in two phases: load() issues the LDS
+// reads of the raw weights (q8_0: 32 bytes and the block scale per lane and
+// 32-block; q4_K: 32 nibble bytes and the {d*sc, dmin*m} pair; f16: the four
+// 8-half fragments), convert() turns them into bf[j][s], the f16 fragment of
+// substep s.  TM x TN: the workgroup tile in 64-blocks; WTN: the wave's 32-column
+// blocks.
+template <int TM, int TN, int WT, int WTN>
+struct BSlab {
     typedef DmaCfg<TM, TN, WT> C;
-    const int q = lane >> 5, r32 = lane & 31;
-    const uint8_t* bs = st + C::A_BYTES;
+    int4v raw[WTN][WT == GT_F16 ? 4 : 2];
+    f16 dq[WTN];       // q8_0: the 32-block scale d
+    float2v sc[WTN];   // q4_K: {d*sc, dmin*m}
+    __device__ __forceinline__ void load(const uint8_t* st, int wn, int lane) {
+        const int q = lane >> 5, r32 = lane & 31;
+        const uint8_t* bs = st + C::A_BYTES;
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-        const int row = wn * TN * 32 + 32 * j + r32;
-        if constexpr (WT == GT_Q8_0) {
-            const int sw = (row >> 2) & 3;
-            const int4v raw0 = *(const int4v*)(bs + row * 64 + (((2 * q) ^ sw) << 4));
-            const int4v raw1 = *(const int4v*)(bs + row * 64 + (((2 * q + 1) ^ sw) << 4));
-            const f16 dh = *(const f16*)(bs + C::B_BYTES + row * 4 + q * 2);
-            const half2v d2 = {dh, dh};
+        for (int j = 0; j < WTN; ++j) {
+            const int row = wn * WTN * 32 + 32 * j + r32;
+            if constexpr (WT == GT_Q8_0) {
+                const int sw = (row >> 2) & 3;
+                raw[j][0] = *(const int4v*)(bs + row * 64 + (((2 * q) ^ sw) << 4));
+                raw[j][1] = *(const int4v*)(bs + row * 64 + (((2 * q + 1) ^ sw) << 4));
+                dq[j] = *(const f16*)(bs + C::B_BYTES + row * 4 + q * 2);
+            } else if constexpr (WT == GT_Q4_K) {
+                const int sw = (row >> 3) & 1;
+                raw[j][0] = *(const int4v*)(bs + row * 32 + (sw << 4));
+                raw[j][1] = *(const int4v*)(bs + row * 32 + ((sw ^ 1) << 4));
+                sc[j] = *(const float2v*)(bs + C::B_BYTES + row * 16 + q * 8);
+            } else {
+                const uint8_t* rp = bs + row * 128;
 #pragma unroll
-            for (int s2 = 0; s2 < 4; ++s2) {
-                const uint32_t w0 = (uint32_t)(s2 < 2 ? raw0[2 * s2] : raw1[2 * (s2 - 2)]);
-                const uint32_t w1 = (uint32_t)(s2 < 2 ? raw0[2 * s2 + 1] : raw1[2 * (s2 - 2) + 1]);
-                half2v h0, h1, h2, h3;
-                i8x4_to_f16(w0, d2, h0, h1);
-                i8x4_to_f16(w1, d2, h2, h3);
-                bf[j][s2] = (half8v){h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
+                for (int s2 = 0; s2 < 4; ++s2) raw[j][s2] = *(const int4v*)(rp + (((4 * q + s2) ^ ((row >> 1) & 7)) << 4));
             }
-        } else if constexpr (WT == GT_Q4_K) {
-            const int sw = (row >> 3) & 1;
-            const int4v raw0 = *(const int4v*)(bs + row * 32 + (sw << 4));
-            const int4v raw1 = *(const int4v*)(bs + row * 32 + ((sw ^ 1) << 4));
-            const float2v sm = *(const float2v*)(bs + C::B_BYTES + row * 16 + q * 8);
-            const half2v s2 = {(f16)sm.x, (f16)sm.x}, nm2 = {(f16)-sm.y, (f16)-sm.y};
-#pragma unroll
-            for (int s2i = 0; s2i < 4; ++s2i) {
-                const uint32_t w0 = (uint32_t)(s2i < 2 ? raw0[2 * s2i] : raw1[2 * (s2i - 2)]);
-                const uint32_t w1 = (uint32_t)(s2i < 2 ? raw0[2 * s2i + 1] : raw1[2 * (s2i - 2) + 1]);
-                half2v h0, h1, h2, h3;
-                nib4_to_f16(w0, q, s2, nm2, h0, h1);
-                nib4_to_f16(w1, q, s2, nm2, h2, h3);
-                bf[j][s2i] = (half8v){h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
-            }
-        } else {
-            const uint8_t* rp = bs + row * 128;
-#pragma unroll
-            for (int s2 = 0; s2 < 4; ++s2) bf[j][s2] = *(const half8v*)(rp + (((4 * q + s2) ^ ((row >> 1) & 7)) << 4));
         }
     }
-}
+    __device__ __forceinline__ void convert(half8v (&bf)[WTN][4], int lane) const {
+        const int q = lane >> 5;
+#pragma unroll
+        for (int j = 0; j < WTN; ++j) {
+            if constexpr (WT == GT_F16) {
+#pragma unroll
+                for (int s2 = 0; s2 < 4; ++s2) bf[j][s2] = __builtin_bit_cast(half8v, raw[j][s2]);
+            } else {
+                half2v m2 = {}, nm2 = {};
+                if constexpr (WT == GT_Q8_0) {
+                    m2 = (half2v){dq[j], dq[j]};
+                } else {
+                    m2 = (half2v){(f16)sc[j].x, (f16)sc[j].x};
+                    nm2 = (half2v){(f16)-sc[j].y, (f16)-sc[j].y};
+                }
+#pragma unroll
+                for (int s2 = 0; s2 < 4; ++s2) {
+                    const uint32_t w0 = (uint32_t)(s2 < 2 ? raw[j][0][2 * s2] : raw[j][1][2 * (s2 - 2)]);
+                    const uint32_t w1 = (uint32_t)(s2 < 2 ? raw[j][0][2 * s2 + 1] : raw[j][1][2 * (s2 - 2) + 1]);
+                    half2v h0, h1, h2, h3;
+                    if constexpr (WT == GT_Q8_0) {
+                        i8x4_to_f16(w0, m2, h0, h1);
+                        i8x4_to_f16(w1, m2, h2, h3);
+                    } else {
+                        nib4_to_f16(w0, q, m2, nm2, h0, h1);
+                        nib4_to_f16(w1, q, m2, nm2, h2, h3);
+                    }
+                    bf[j][s2] = (half8v){h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
+                }
+            }
+        }
+    }
+};
 
-template <int TM, int TN, int WT>
-__device__ __forceinline__ void mma32_slab(const uint8_t* st, float16v (&acc)[TM][TN], int wm, int wn,
+// One 64-deep slab of MFMAs for one wave: acc[i][j] += A block i x B block j.
+// PF: issue every LDS read of the slab (B first, then all A fragments) before
+// the dequantisation, so that the A reads land while the VALU converts B; the
+// schedule barrier keeps the compiler from sinking the A reads to their MFMAs.
+// Otherwise A fragments are read per substep (fewer registers).
+template <int TM, int TN, int WT, int WTM, int WTN, bool PF>
+__device__ __forceinline__ void mma32_slab(const uint8_t* st, float16v (&acc)[WTM][WTN], int wm, int wn,
                                            int lane) {
     const int q = lane >> 5, r32 = lane & 31;
-    half8v bf[TN][4];
-    b_frags32<TM, TN, WT>(st, bf, wn, lane);
+    BSlab<TM, TN, WT, WTN> b;
+    b.load(st, wn, lane);
+    half8v bf[WTN][4];
+    if constexpr (PF) {
+        half8v af[4][WTM];
 #pragma unroll
-    for (int s2 = 0; s2 < 4; ++s2) {
+        for (int s2 = 0; s2 < 4; ++s2)
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
-            const int row = wm * TM * 32 + 32 * i + r32;
-            const half8v af = *(const half8v*)(st + row * 128 + (((4 * q + s2) ^ ((row >> 1) & 7)) << 4));
+            for (int i = 0; i < WTM; ++i) {
+                const int row = wm * WTM * 32 + 32 * i + r32;
+                af[s2][i] = *(const half8v*)(st + row * 128 + (((4 * q + s2) ^ ((row >> 1) & 7)) << 4));
+            }
+        __builtin_amdgcn_sched_barrier(0);
+        b.convert(bf, lane);
 #pragma unroll
-            for (int j = 0; j < TN; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[j][s2], acc[i][j], 0, 0, 0);
+        for (int s2 = 0; s2 < 4; ++s2)
+#pragma unroll
+            for (int i = 0; i < WTM; ++i)
+#pragma unroll
+                for (int j = 0; j < WTN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[s2][i], bf[j][s2], acc[i][j], 0, 0, 0);
+    } else {
+        b.convert(bf, lane);
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2) {
+#pragma unroll
+            for (int i = 0; i < WTM; ++i) {
+                const int row = wm * WTM * 32 + 32 * i + r32;
+                const half8v af = *(const half8v*)(st + row * 128 + (((4 * q + s2) ^ ((row >> 1) & 7)) << 4));
+#pragma unroll
+                for (int j = 0; j < WTN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[j][s2], acc[i][j], 0, 0, 0);
+            }
         }
     }
 }
@@ -1045,9 +1094,16 @@ struct FoldStats {
 // summed in LDS (group 0 + group 1, a fixed order) before group 0 runs the
 // epilogue.  For grids of about one tile per CU: two waves per SIMD instead of
 // one.
-template <int TM, int TN, int WT, int EPI, int NS = DMA_NS, int KG = 1>
+// WL = wave layout: 0 = 2 x 2 waves of 32 TM x 32 TN each; 1 = four waves side
+// by side along N, each 64 TM rows x 16 TN columns, so that no two waves
+// dequantise the same weight rows.
+template <int TM, int TN, int WT, int EPI, int NS = DMA_NS, int KG = 1, int WL = 0>
 __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(GemmParams p) {
     typedef DmaCfg<TM, TN, WT> C;
+    static_assert(WL == 0 || (TN % 2 == 0 && EPI != EPI_GLU && EPI != EPI_GLU_DW && EPI != EPI_RELU_TR &&
+                              EPI != EPI_RELU2_F32),
+                  "wave layout 1: even TN, LDS-staged non-GLU epilogues");
+    constexpr int WTM = WL ? 2 * TM : TM, WTN = WL ? TN / 2 : TN;   // one wave's 32-blocks
     static_assert(NS == 2 || NS == 3, "LDS ring depth");
     static_assert(KG == 1 || (KG == 2 && (EPI == EPI_STORE || EPI == EPI_STORE_F32 || EPI == EPI_RESID ||
                                           EPI == EPI_SILU || EPI == EPI_RESID_LN)),
@@ -1057,7 +1113,7 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
     const int tid = threadIdx.x & 255, lane = tid & 63;
     const int wid_all = wave_id_uniform();
     const int kg = wid_all >> 2, wid = wid_all & 3;
-    const int wm = wid >> 1, wn = wid & 1;
+    const int wm = WL ? 0 : wid >> 1, wn = WL ? wid : wid & 1;
     uint8_t* smem = smem_all + kg * NS * C::STAGE;
     // The fused conv-module epilogue needs DWH rows of GLU output either side
     // of the rows it writes: its tiles overlap by 2 DWH rows.
@@ -1068,11 +1124,11 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
     xcd_tile_2d(blockIdx.x, nbm, nbn, p.xcd_gm, bm, bn);
     const int m0 = bm * SM - DWH, n0 = bn * C::BN;
 
-    float16v acc[TM][TN];
+    float16v acc[WTM][WTN];
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < WTM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = (float16v){};
+        for (int j = 0; j < WTN; ++j) acc[i][j] = (float16v){};
 
     // folded LayerNorm: the row statistics' loads go out before the DMAs (oldest
     // in the vector-memory counter) and are combined after the main loop
@@ -1101,31 +1157,31 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
             const int st2 = st + NS - 1 >= NS ? st - 1 : st + NS - 1;
             src.issue(smem + st2 * C::STAGE, kb + (kt + NS - 1) * 64);
         }
-        mma32_slab<TM, TN, WT>(smem + st * C::STAGE, acc, wm, wn, lane);
+        mma32_slab<TM, TN, WT, WTM, WTN, WL == 1>(smem + st * C::STAGE, acc, wm, wn, lane);
         st = st + 1 == NS ? 0 : st + 1;
     }
     if constexpr (KG == 2) {
         // lane-major [wave][register][lane] f32: conflict-free both ways
-        constexpr int R = TM * TN * 16;
+        constexpr int R = WTM * WTN * 16;
         static_assert(4 * R * 64 * 4 <= KG * NS * C::STAGE, "partial tile exceeds LDS");
         float* red = (float*)smem_all + wid * R * 64 + lane;
         __syncthreads();
         if (kg == 1) {
 #pragma unroll
-            for (int i = 0; i < TM; ++i)
+            for (int i = 0; i < WTM; ++i)
 #pragma unroll
-                for (int j = 0; j < TN; ++j)
+                for (int j = 0; j < WTN; ++j)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) red[((i * TN + j) * 16 + r) * 64] = acc[i][j][r];
+                    for (int r = 0; r < 16; ++r) red[((i * WTN + j) * 16 + r) * 64] = acc[i][j][r];
         }
         __syncthreads();
         if (kg == 0) {
 #pragma unroll
-            for (int i = 0; i < TM; ++i)
+            for (int i = 0; i < WTM; ++i)
 #pragma unroll
-                for (int j = 0; j < TN; ++j)
+                for (int j = 0; j < WTN; ++j)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) acc[i][j][r] += red[((i * TN + j) * 16 + r) * 64];
+                    for (int r = 0; r < 16; ++r) acc[i][j][r] += red[((i * WTN + j) * 16 + r) * 64];
         }
     }
     // folded LayerNorm: the tile's row statistics at the top of the LDS block
@@ -1159,29 +1215,29 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
         // whose staging exceeds it leave in row halves
         // (the folded-LayerNorm row table sits above the staging area)
         constexpr int TAB = FOLD && KG == 1 ? C::BM * 8 : 0;
-        constexpr bool whole = 4 * 32 * TM * (32 * TN + 4) * 4 + TAB <= NS * C::STAGE;
-        static_assert(whole || (TM % 2 == 0 && 4 * 16 * TM * (32 * TN + 4) * 4 + TAB <= NS * C::STAGE),
+        constexpr bool whole = 4 * 32 * WTM * (32 * WTN + 4) * 4 + TAB <= NS * C::STAGE;
+        static_assert(whole || (WTM % 2 == 0 && 4 * 16 * WTM * (32 * WTN + 4) * 4 + TAB <= NS * C::STAGE),
                       "epilogue staging exceeds LDS ring");
         if constexpr (whole) {
             __syncthreads();
-            float* wsm = (float*)smem + wid * (32 * TM) * ((EPI == EPI_GLU ? 16 * TN : 32 * TN) + 4);
+            float* wsm = (float*)smem + wid * (32 * WTM) * ((EPI == EPI_GLU ? 16 * WTN : 32 * WTN) + 4);
             if (kg == 0)
-                epilogue32_lds<EPI, TM, TN>(p, acc, wsm, m0 + wm * TM * 32, n0 + wn * TN * 32, lane, fold,
-                                            ftab, wm * TM * 32);
+                epilogue32_lds<EPI, WTM, WTN>(p, acc, wsm, m0 + wm * WTM * 32, n0 + wn * WTN * 32, lane, fold,
+                                              ftab, wm * WTM * 32);
         } else {
-            constexpr int TH = TM / 2;
-            float* wsm = (float*)smem + wid * (32 * TH) * ((EPI == EPI_GLU ? 16 * TN : 32 * TN) + 4);
+            constexpr int TH = WTM / 2;
+            float* wsm = (float*)smem + wid * (32 * TH) * ((EPI == EPI_GLU ? 16 * WTN : 32 * WTN) + 4);
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
-                float16v part[TH][TN];
+                float16v part[TH][WTN];
 #pragma unroll
                 for (int i = 0; i < TH; ++i)
 #pragma unroll
-                    for (int j = 0; j < TN; ++j) part[i][j] = acc[hh * TH + i][j];
+                    for (int j = 0; j < WTN; ++j) part[i][j] = acc[hh * TH + i][j];
                 __syncthreads();
                 if (kg == 0)
-                    epilogue32_lds<EPI, TH, TN>(p, part, wsm, m0 + wm * TM * 32 + hh * TH * 32, n0 + wn * TN * 32,
-                                                lane, fold, ftab, wm * TM * 32 + hh * TH * 32);
+                    epilogue32_lds<EPI, TH, WTN>(p, part, wsm, m0 + wm * WTM * 32 + hh * TH * 32,
+                                                 n0 + wn * WTN * 32, lane, fold, ftab, wm * WTM * 32 + hh * TH * 32);
             }
         }
     }
@@ -1487,7 +1543,7 @@ static int choose_xcd_gm(const GemmParams& p, int WT, int BM, int BN) {
     return best_cost < 1e300 ? best : 1;
 }
 
-template <int TM, int TN, int WT, int EPI, int NS = DMA_NS, int KG = 1>
+template <int TM, int TN, int WT, int EPI, int NS = DMA_NS, int KG = 1, int WL = 0>
 static void run_dma(const GemmParams& p, hipStream_t s) {
     if constexpr ((EPI == EPI_GLU || EPI == EPI_GLU_DW) && TN % 2 != 0) {
         throw std::logic_error("gemm: GLU epilogue dispatched to a 64-wide tile");
@@ -1497,7 +1553,7 @@ static void run_dma(const GemmParams& p, hipStream_t s) {
         const int tiles = cdiv(p.M, sm) * cdiv(p.N, 64 * TN);
         GemmParams q = p;
         q.xcd_gm = choose_xcd_gm(p, WT, sm, 64 * TN);
-        launch((gemm_dma_kernel<TM, TN, WT, EPI, NS, KG>), dim3(tiles), dim3(256 * KG), 0, s, q);
+        launch((gemm_dma_kernel<TM, TN, WT, EPI, NS, KG, WL>), dim3(tiles), dim3(256 * KG), 0, s, q);
         PKX_LAUNCH_CHECK();
     }
 }
@@ -1506,6 +1562,21 @@ template <int TM, int TN, int WT>
 static void f16_epi(int epi, const GemmParams& p, hipStream_t s) { PKX_EPI_SWITCH(run_f16, TM, TN, WT) }
 template <int TM, int TN, int WT>
 static void dma_epi(int epi, const GemmParams& p, hipStream_t s) { PKX_EPI_SWITCH_DMA(run_dma, TM, TN, WT) }
+// 128 x 128 tiles of quantised weights: the side-by-side wave layout (each
+// weight row dequantised by one wave only) with the slab's LDS reads issued up
+// front, for every epilogue that allows it
+template <int WT>
+static void dma_22q(int epi, const GemmParams& p, hipStream_t s) {
+    switch (epi) {
+    case EPI_STORE: run_dma<2, 2, WT, EPI_STORE, DMA_NS, 1, 1>(p, s); break;
+    case EPI_STORE_F32: run_dma<2, 2, WT, EPI_STORE_F32, DMA_NS, 1, 1>(p, s); break;
+    case EPI_SILU: run_dma<2, 2, WT, EPI_SILU, DMA_NS, 1, 1>(p, s); break;
+    case EPI_RESID: run_dma<2, 2, WT, EPI_RESID, DMA_NS, 1, 1>(p, s); break;
+    case EPI_RELU: run_dma<2, 2, WT, EPI_RELU, DMA_NS, 1, 1>(p, s); break;
+    case EPI_RESID_LN: run_dma<2, 2, WT, EPI_RESID_LN, DMA_NS, 1, 1>(p, s); break;
+    default: dma_epi<2, 2, WT>(epi, p, s); break;
+    }
+}
 // 128 x 64 tiles with two K groups (eight waves): long-K products whose grid is
 // about one tile per CU
 template <int WT>
@@ -1576,12 +1647,12 @@ void launch_gemm(Precision prec, int wtype, int epi, const GemmParams& p, hipStr
         if (wtype == GT_Q4_K && dma_kg2<GT_Q4_K>(epi, p, s)) return;
         if (wtype == GT_F16 && dma_kg2<GT_F16>(epi, p, s)) return;
         if (wtype == GT_Q8_0) {
-            if (t22 >= 384 || (glu && t22 >= 256)) dma_epi<2, 2, GT_Q8_0>(epi, p, s);
+            if (t22 >= 384 || (glu && t22 >= 256)) dma_22q<GT_Q8_0>(epi, p, s);
             else if (glu) dma_epi<1, 2, GT_Q8_0>(epi, p, s);
             else if (t21 >= 128) dma_epi<2, 1, GT_Q8_0>(epi, p, s);
             else dma_epi<1, 1, GT_Q8_0>(epi, p, s);
         } else if (wtype == GT_Q4_K) {
-            if (t22 >= 384 || (glu && t22 >= 256)) dma_epi<2, 2, GT_Q4_K>(epi, p, s);
+            if (t22 >= 384 || (glu && t22 >= 256)) dma_22q<GT_Q4_K>(epi, p, s);
             else if (glu) dma_epi<1, 2, GT_Q4_K>(epi, p, s);
             else if (t21 >= 128) dma_epi<2, 1, GT_Q4_K>(epi, p, s);
             else dma_epi<1, 1, GT_Q4_K>(epi, p, s);
