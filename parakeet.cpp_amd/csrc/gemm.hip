@@ -810,14 +810,35 @@ __device__ __forceinline__ void epilogue32_relu_tr(const GemmParams& p, float16v
     }
 }
 
+// The residual stream's values under one wave's output tile, loaded into
+// registers before the main loop so that the residual epilogue does not wait
+// for them: chunk t of a lane is the float4 at row rr = (lane + 64 t) / CPR,
+// column 4 ((lane + 64 t) % CPR) of the wave tile (the epilogue's own order).
+template <int WR, int CPR>
+struct ResidPre {
+    static constexpr int NT = WR * CPR / 64;
+    static_assert(NT * 64 == WR * CPR, "whole chunks per lane");
+    float4v v[NT];
+    __device__ __forceinline__ void load(const GemmParams& p, int mw, int nw, int lane) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const int c = lane + 64 * t, m = mw + c / CPR, n = nw + (c % CPR) * 4;
+            v[t] = m < p.M && n + 3 < p.N ? *(const float4v*)((const float*)p.Y + (int64_t)m * p.ldy + n)
+                                          : (float4v){0.f, 0.f, 0.f, 0.f};
+        }
+    }
+};
+
 // fold: ftab (LDS) holds {mean, rstd} of the workgroup tile's rows for a
 // folded LayerNorm, indexed from the tile's first row; trow0 is this wave's
 // first row within the tile.  (ftab is always a valid LDS address, so that its
 // loads stay LDS loads.)
+// xpre: the wave tile's residual values from ResidPre (RESID / RESID_LN), or null.
 template <int EPI, int TM, int TN>
 __device__ __forceinline__ void epilogue32_lds(const GemmParams& p, float16v (&acc)[TM][TN], float* wsm,
                                                int mw, int nw, int lane, bool fold = false,
-                                               const float2v* ftab = nullptr, int trow0 = 0) {
+                                               const float2v* ftab = nullptr, int trow0 = 0,
+                                               const float4v* xpre = nullptr) {
     constexpr int WR = 32 * TM;
     constexpr int WC = EPI == EPI_GLU ? 16 * TN : 32 * TN;   // output columns of this wave
     constexpr int LDW = WC + 4;
@@ -898,13 +919,15 @@ __device__ __forceinline__ void epilogue32_lds(const GemmParams& p, float16v (&a
         const int G = p.N / 32;
         const int cc = (lane % CPR) * 4, n = n0 + cc;   // a lane's columns are the same on every row
         const float4v g = n < p.N ? *(const float4v*)(p.ln_g + n) : (float4v){0.f, 0.f, 0.f, 0.f};
-        for (int c = lane; c < WR * CPR; c += 64) {
+#pragma unroll
+        for (int t = 0; t < WR * CPR / 64; ++t) {
+            const int c = lane + 64 * t;
             const int rr = c / CPR;
             const int m = mw + rr;
             if (m < p.M && n < p.N) {   // uniform over the 8 lanes of a group (same row, N % 32 == 0)
                 const float4v v = *(const float4v*)(wsm + rr * LDW + cc);
                 float* dst = (float*)p.Y + (int64_t)m * p.ldy + n;
-                const float4v x = *(const float4v*)dst + v;
+                const float4v x = (xpre ? xpre[t] : *(const float4v*)dst) + v;
                 *(float4v*)dst = x;
                 const half4v h = {(f16)(x[0] * g[0]), (f16)(x[1] * g[1]), (f16)(x[2] * g[2]), (f16)(x[3] * g[3])};
                 *(half4v*)((f16*)p.ln_h + (int64_t)m * p.N + n) = h;
@@ -918,14 +941,17 @@ __device__ __forceinline__ void epilogue32_lds(const GemmParams& p, float16v (&a
         }
     } else if constexpr (EPI == EPI_STORE_F32 || EPI == EPI_RESID) {
         constexpr int CPR = WC / 4;   // float4 chunks per row
-        for (int c = lane; c < WR * CPR; c += 64) {
+        static_assert(WR * CPR % 64 == 0, "whole chunks per lane");
+#pragma unroll
+        for (int t = 0; t < WR * CPR / 64; ++t) {
+            const int c = lane + 64 * t;
             const int rr = c / CPR, cc = (c % CPR) * 4;
             const int m = mw + rr, n = n0 + cc;
             if (m >= p.M) continue;
             const float4v v = *(const float4v*)(wsm + rr * LDW + cc);
             float* dst = (float*)p.Y + (int64_t)m * p.ldy + n;
             if (n + 3 < ncol) {
-                if constexpr (EPI == EPI_RESID) *(float4v*)dst = *(const float4v*)dst + v;
+                if constexpr (EPI == EPI_RESID) *(float4v*)dst = (xpre ? xpre[t] : *(const float4v*)dst) + v;
                 else *(float4v*)dst = v;
             } else {
                 for (int e = 0; e < 4 && n + e < ncol; ++e) {
@@ -1096,14 +1122,15 @@ struct FoldStats {
 // one.
 // WL = wave layout: 0 = 2 x 2 waves of 32 TM x 32 TN each; 1 = four waves side
 // by side along N, each 64 TM rows x 16 TN columns, so that no two waves
-// dequantise the same weight rows.
+// dequantise the same weight rows; 2 = the 2 x 2 layout with the slab's LDS
+// reads issued up front (as layout 1 does).
 template <int TM, int TN, int WT, int EPI, int NS = DMA_NS, int KG = 1, int WL = 0>
 __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(GemmParams p) {
     typedef DmaCfg<TM, TN, WT> C;
-    static_assert(WL == 0 || (TN % 2 == 0 && EPI != EPI_GLU && EPI != EPI_GLU_DW && EPI != EPI_RELU_TR &&
+    static_assert(WL != 1 || (TN % 2 == 0 && EPI != EPI_GLU && EPI != EPI_GLU_DW && EPI != EPI_RELU_TR &&
                               EPI != EPI_RELU2_F32),
                   "wave layout 1: even TN, LDS-staged non-GLU epilogues");
-    constexpr int WTM = WL ? 2 * TM : TM, WTN = WL ? TN / 2 : TN;   // one wave's 32-blocks
+    constexpr int WTM = WL == 1 ? 2 * TM : TM, WTN = WL == 1 ? TN / 2 : TN;   // one wave's 32-blocks
     static_assert(NS == 2 || NS == 3, "LDS ring depth");
     static_assert(KG == 1 || (KG == 2 && (EPI == EPI_STORE || EPI == EPI_STORE_F32 || EPI == EPI_RESID ||
                                           EPI == EPI_SILU || EPI == EPI_RESID_LN)),
@@ -1113,7 +1140,7 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
     const int tid = threadIdx.x & 255, lane = tid & 63;
     const int wid_all = wave_id_uniform();
     const int kg = wid_all >> 2, wid = wid_all & 3;
-    const int wm = WL ? 0 : wid >> 1, wn = WL ? wid : wid & 1;
+    const int wm = WL == 1 ? 0 : wid >> 1, wn = WL == 1 ? wid : wid & 1;
     uint8_t* smem = smem_all + kg * NS * C::STAGE;
     // The fused conv-module epilogue needs DWH rows of GLU output either side
     // of the rows it writes: its tiles overlap by 2 DWH rows.
@@ -1138,6 +1165,16 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
         if (p.fold_stats && kg == 0) fst.prefetch(p, m0, tid);
     }
 
+    // residual epilogues: the tile's residual values are loaded now (behind the
+    // statistics, ahead of the DMAs) and wait in registers for the epilogue
+    constexpr int TAB = FOLD && KG == 1 ? C::BM * 8 : 0;
+    constexpr bool whole = 4 * 32 * WTM * (32 * WTN + 4) * 4 + TAB <= NS * C::STAGE;
+    constexpr bool RPRE = (EPI == EPI_RESID || EPI == EPI_RESID_LN) && whole;
+    ResidPre<RPRE ? 32 * WTM : 64, RPRE ? 8 * WTN : 1> rpre;
+    if constexpr (RPRE) {
+        if (kg == 0) rpre.load(p, m0 + wm * WTM * 32, n0 + wn * WTN * 32, lane);
+    }
+
     const int nk = p.K / 64 / KG, kb = kg * nk * 64;   // slabs of this group, its first K
     DmaSrc<TM, TN, WT> src;
     src.init(p, m0, n0, wid, lane);
@@ -1157,7 +1194,7 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
             const int st2 = st + NS - 1 >= NS ? st - 1 : st + NS - 1;
             src.issue(smem + st2 * C::STAGE, kb + (kt + NS - 1) * 64);
         }
-        mma32_slab<TM, TN, WT, WTM, WTN, WL == 1>(smem + st * C::STAGE, acc, wm, wn, lane);
+        mma32_slab<TM, TN, WT, WTM, WTN, WL != 0>(smem + st * C::STAGE, acc, wm, wn, lane);
         st = st + 1 == NS ? 0 : st + 1;
     }
     if constexpr (KG == 2) {
@@ -1214,8 +1251,6 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
         // the LDS ring is free once every wave has finished its last slab; tiles
         // whose staging exceeds it leave in row halves
         // (the folded-LayerNorm row table sits above the staging area)
-        constexpr int TAB = FOLD && KG == 1 ? C::BM * 8 : 0;
-        constexpr bool whole = 4 * 32 * WTM * (32 * WTN + 4) * 4 + TAB <= NS * C::STAGE;
         static_assert(whole || (WTM % 2 == 0 && 4 * 16 * WTM * (32 * WTN + 4) * 4 + TAB <= NS * C::STAGE),
                       "epilogue staging exceeds LDS ring");
         if constexpr (whole) {
@@ -1223,7 +1258,7 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
             float* wsm = (float*)smem + wid * (32 * WTM) * ((EPI == EPI_GLU ? 16 * WTN : 32 * WTN) + 4);
             if (kg == 0)
                 epilogue32_lds<EPI, WTM, WTN>(p, acc, wsm, m0 + wm * WTM * 32, n0 + wn * WTN * 32, lane, fold,
-                                              ftab, wm * WTM * 32);
+                                              ftab, wm * WTM * 32, RPRE ? rpre.v : nullptr);
         } else {
             constexpr int TH = WTM / 2;
             float* wsm = (float*)smem + wid * (32 * TH) * ((EPI == EPI_GLU ? 16 * WTN : 32 * WTN) + 4);
@@ -1562,6 +1597,11 @@ template <int TM, int TN, int WT>
 static void f16_epi(int epi, const GemmParams& p, hipStream_t s) { PKX_EPI_SWITCH(run_f16, TM, TN, WT) }
 template <int TM, int TN, int WT>
 static void dma_epi(int epi, const GemmParams& p, hipStream_t s) { PKX_EPI_SWITCH_DMA(run_dma, TM, TN, WT) }
+// the 2 x 2 wave layout with the slab's LDS reads issued up front
+template <int TM, int TN, int WT, int EPI>
+static void run_dma_pf(const GemmParams& p, hipStream_t s) { run_dma<TM, TN, WT, EPI, DMA_NS, 1, 2>(p, s); }
+template <int TM, int TN, int WT>
+static void dma_epi_pf(int epi, const GemmParams& p, hipStream_t s) { PKX_EPI_SWITCH_DMA(run_dma_pf, TM, TN, WT) }
 // 128 x 128 tiles of quantised weights: the side-by-side wave layout (each
 // weight row dequantised by one wave only) with the slab's LDS reads issued up
 // front, for every epilogue that allows it
@@ -1583,11 +1623,11 @@ template <int WT>
 static bool dma_kg2(int epi, const GemmParams& p, hipStream_t s) {
     if (p.K % 128 != 0 || p.K < 2048 || (int64_t)cdiv(p.M, 128) * cdiv(p.N, 64) > 256) return false;
     switch (epi) {
-    case EPI_STORE: run_dma<2, 1, WT, EPI_STORE, DMA_NS, 2>(p, s); return true;
-    case EPI_STORE_F32: run_dma<2, 1, WT, EPI_STORE_F32, DMA_NS, 2>(p, s); return true;
-    case EPI_RESID: run_dma<2, 1, WT, EPI_RESID, DMA_NS, 2>(p, s); return true;
-    case EPI_SILU: run_dma<2, 1, WT, EPI_SILU, DMA_NS, 2>(p, s); return true;
-    case EPI_RESID_LN: run_dma<2, 1, WT, EPI_RESID_LN, DMA_NS, 2>(p, s); return true;
+    case EPI_STORE: run_dma<2, 1, WT, EPI_STORE, DMA_NS, 2, WT == GT_F16 ? 0 : 2>(p, s); return true;
+    case EPI_STORE_F32: run_dma<2, 1, WT, EPI_STORE_F32, DMA_NS, 2, WT == GT_F16 ? 0 : 2>(p, s); return true;
+    case EPI_RESID: run_dma<2, 1, WT, EPI_RESID, DMA_NS, 2, WT == GT_F16 ? 0 : 2>(p, s); return true;
+    case EPI_SILU: run_dma<2, 1, WT, EPI_SILU, DMA_NS, 2, WT == GT_F16 ? 0 : 2>(p, s); return true;
+    case EPI_RESID_LN: run_dma<2, 1, WT, EPI_RESID_LN, DMA_NS, 2, WT == GT_F16 ? 0 : 2>(p, s); return true;
     default: return false;
     }
 }
@@ -1649,12 +1689,12 @@ void launch_gemm(Precision prec, int wtype, int epi, const GemmParams& p, hipStr
         if (wtype == GT_Q8_0) {
             if (t22 >= 384 || (glu && t22 >= 256)) dma_22q<GT_Q8_0>(epi, p, s);
             else if (glu) dma_epi<1, 2, GT_Q8_0>(epi, p, s);
-            else if (t21 >= 128) dma_epi<2, 1, GT_Q8_0>(epi, p, s);
+            else if (t21 >= 128) dma_epi_pf<2, 1, GT_Q8_0>(epi, p, s);
             else dma_epi<1, 1, GT_Q8_0>(epi, p, s);
         } else if (wtype == GT_Q4_K) {
             if (t22 >= 384 || (glu && t22 >= 256)) dma_22q<GT_Q4_K>(epi, p, s);
             else if (glu) dma_epi<1, 2, GT_Q4_K>(epi, p, s);
-            else if (t21 >= 128) dma_epi<2, 1, GT_Q4_K>(epi, p, s);
+            else if (t21 >= 128) dma_epi_pf<2, 1, GT_Q4_K>(epi, p, s);
             else dma_epi<1, 1, GT_Q4_K>(epi, p, s);
         } else {
             dma_epi<1, 2, GT_F16>(epi, p, s);
