@@ -810,6 +810,30 @@ __device__ __forceinline__ void epilogue32_relu_tr(const GemmParams& p, float16v
     }
 }
 
+// Per-column epilogue constants of one wave's 32 NJ output columns (column
+// nw + 32 j + lane % 32 for block j): bias, folded-LayerNorm W*gamma, and for
+// the LayerNorm-statistics epilogue the gamma quad of the lane's copy-out
+// columns.  Loaded before the main loop so the epilogue does not wait for them.
+template <int NJ>
+struct EpiCols {
+    float b[NJ], c1[NJ];
+    float4v g;
+    __device__ __forceinline__ void load(const GemmParams& p, int nw, int lane, bool fold, bool gamma) {
+        const int lc = lane & 31;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const int n = min(nw + 32 * j + lc, p.N - 1);
+            b[j] = p.bias ? p.bias[n] : 0.f;
+            c1[j] = fold ? p.fold_c1[n] : 0.f;
+        }
+        g = (float4v){0.f, 0.f, 0.f, 0.f};
+        if (gamma) {
+            const int n = nw + (lane % (8 * NJ)) * 4;   // the copy-out columns of RESID_LN
+            if (n < p.N) g = *(const float4v*)(p.ln_g + n);
+        }
+    }
+};
+
 // The residual stream's values under one wave's output tile, loaded into
 // registers before the main loop so that the residual epilogue does not wait
 // for them: chunk t of a lane is the float4 at row rr = (lane + 64 t) / CPR,
@@ -836,8 +860,8 @@ struct ResidPre {
 // xpre: the wave tile's residual values from ResidPre (RESID / RESID_LN), or null.
 template <int EPI, int TM, int TN>
 __device__ __forceinline__ void epilogue32_lds(const GemmParams& p, float16v (&acc)[TM][TN], float* wsm,
-                                               int mw, int nw, int lane, bool fold = false,
-                                               const float2v* ftab = nullptr, int trow0 = 0,
+                                               int mw, int nw, int lane, const EpiCols<TN>& ec,
+                                               bool fold = false, const float2v* ftab = nullptr, int trow0 = 0,
                                                const float4v* xpre = nullptr) {
     constexpr int WR = 32 * TM;
     constexpr int WC = EPI == EPI_GLU ? 16 * TN : 32 * TN;   // output columns of this wave
@@ -855,11 +879,8 @@ __device__ __forceinline__ void epilogue32_lds(const GemmParams& p, float16v (&a
             }
 #pragma unroll
             for (int jj = 0; jj < TN / 2; ++jj) {
-                const int na = nw + 64 * jj + lc;
-                const float ba = p.bias ? p.bias[min(na, p.N - 1)] : 0.f;
-                const float bg = p.bias ? p.bias[min(na + 32, p.N - 1)] : 0.f;
-                const float ca = fold ? p.fold_c1[min(na, p.N - 1)] : 0.f;
-                const float cg = fold ? p.fold_c1[min(na + 32, p.N - 1)] : 0.f;
+                const float ba = ec.b[2 * jj], bg = ec.b[2 * jj + 1];
+                const float ca = ec.c1[2 * jj], cg = ec.c1[2 * jj + 1];
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int rr = 32 * i + 8 * (r >> 2) + lr + (r & 3);
@@ -888,9 +909,7 @@ __device__ __forceinline__ void epilogue32_lds(const GemmParams& p, float16v (&a
             }
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
-                const int n = nw + 32 * j + lc;
-                const float bb = p.bias ? p.bias[min(n, p.N - 1)] : 0.f;
-                const float c1 = fold ? p.fold_c1[min(n, p.N - 1)] : 0.f;
+                const float bb = ec.b[j], c1 = ec.c1[j];
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int rr = 32 * i + 8 * (r >> 2) + lr + (r & 3);
@@ -918,7 +937,7 @@ __device__ __forceinline__ void epilogue32_lds(const GemmParams& p, float16v (&a
         static_assert(CPR % 8 == 0 && 64 % CPR == 0, "RESID_LN: whole 32-column groups per wave");
         const int G = p.N / 32;
         const int cc = (lane % CPR) * 4, n = n0 + cc;   // a lane's columns are the same on every row
-        const float4v g = n < p.N ? *(const float4v*)(p.ln_g + n) : (float4v){0.f, 0.f, 0.f, 0.f};
+        const float4v g = ec.g;
 #pragma unroll
         for (int t = 0; t < WR * CPR / 64; ++t) {
             const int c = lane + 64 * t;
@@ -980,6 +999,31 @@ __device__ __forceinline__ void epilogue32_lds(const GemmParams& p, float16v (&a
     }
 }
 
+// Constants of the fused conv-module epilogue, loaded before the main loop:
+// thread tid's tile row {time index, kept} (tid < BM) and the depthwise taps,
+// bias and folded BatchNorm of its channel pair c, c + 1 (c = n0/2 + 2 (tid % CP)).
+template <int BM, int CP>
+struct DwPre {
+    int2 rt;
+    float2v wk[GLU_DW_K], db, sc, sh;
+    __device__ __forceinline__ void load(const GemmParams& p, int m0, int n0, int tid) {
+        static_assert(BM <= 256, "one tile row per thread");
+        rt = make_int2(0, 0);
+        const int m = m0 + tid;
+        if (tid < BM && m >= 0 && m < p.M) {
+            const int b = m / p.T, t = m - b * p.T;
+            rt = make_int2(t, !p.valid || t < p.valid[b]);
+        }
+        const int c = min(n0 / 2 + 2 * (tid % CP), p.N / 2 - 2);
+#pragma unroll
+        for (int j = 0; j < GLU_DW_K; ++j)
+            wk[j] = (float2v){p.dw_w[c * GLU_DW_K + j], p.dw_w[(c + 1) * GLU_DW_K + j]};
+        db = p.dw_b ? (float2v){p.dw_b[c], p.dw_b[c + 1]} : (float2v){0.f, 0.f};
+        sc = (float2v){p.dw_scale[c], p.dw_scale[c + 1]};
+        sh = (float2v){p.dw_shift[c], p.dw_shift[c + 1]};
+    }
+};
+
 // Conformer convolution module after pointwise_conv1, in one pass over the
 // tile: GLU + pad mask (rows t >= valid -> 0) staged for the whole workgroup
 // tile in LDS as f32 [64 TM rows][32 TN channels], then the depthwise conv
@@ -988,7 +1032,8 @@ __device__ __forceinline__ void epilogue32_lds(const GemmParams& p, float16v (&a
 // m0 is the tile's first GEMM row (H rows before the first row written).
 template <int TM, int TN>
 __device__ __forceinline__ void epilogue32_glu_dw(const GemmParams& p, float16v (&acc)[TM][TN], float* G, int m0,
-                                                  int n0, int wm, int wn, int tid, bool fold, const float2v* ftab) {
+                                                  int n0, int wm, int wn, int tid, bool fold, const float2v* ftab,
+                                                  const EpiCols<TN>& ec, const DwPre<64 * TM, 16 * TN>& dp) {
     static_assert(TN % 2 == 0, "GLU needs an even number of 32-column blocks");
     constexpr int BM = 64 * TM, CW = 32 * TN, LDG = CW + 2, K = GLU_DW_K, H = (K - 1) / 2;
     constexpr int CP = CW / 2, RG = 256 / CP, NR = BM - 2 * H, RPG = (NR + RG - 1) / RG;
@@ -997,27 +1042,15 @@ __device__ __forceinline__ void epilogue32_glu_dw(const GemmParams& p, float16v 
     // 0) per tile row: time index and whether the GLU output is kept (row in
     //    [0, M) and t < valid), one division per row instead of per element
     int2* rtab = (int2*)(G + BM * LDG);
-    for (int r = tid; r < BM; r += 256) {
-        const int m = m0 + r;
-        int t = 0, keep = 0;
-        if (m >= 0 && m < p.M) {
-            const int b = m / p.T;
-            t = m - b * p.T;
-            keep = !p.valid || t < p.valid[b];
-        }
-        rtab[r] = make_int2(t, keep);
-    }
+    if (tid < BM) rtab[tid] = dp.rt;
     __syncthreads();
     // 1) GLU + pad mask into LDS
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int jj = 0; jj < TN / 2; ++jj) {
-            const int na = n0 + wn * 32 * TN + 64 * jj + lc;
-            const float ba = p.bias ? p.bias[min(na, p.N - 1)] : 0.f;
-            const float bg = p.bias ? p.bias[min(na + 32, p.N - 1)] : 0.f;
-            const float ca = fold ? p.fold_c1[min(na, p.N - 1)] : 0.f;
-            const float cg = fold ? p.fold_c1[min(na + 32, p.N - 1)] : 0.f;
+            const float ba = ec.b[2 * jj], bg = ec.b[2 * jj + 1];
+            const float ca = ec.c1[2 * jj], cg = ec.c1[2 * jj + 1];
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int rr = wm * 32 * TM + 32 * i + 8 * (r >> 2) + lr + (r & 3);
@@ -1038,11 +1071,8 @@ __device__ __forceinline__ void epilogue32_glu_dw(const GemmParams& p, float16v 
     const int cp = tid % CP, g = tid / CP;
     const int cl = 2 * cp, c = n0 / 2 + cl;
     if (c >= p.N / 2) return;
-    float2v wk[K];
-#pragma unroll
-    for (int j = 0; j < K; ++j) wk[j] = (float2v){p.dw_w[c * K + j], p.dw_w[(c + 1) * K + j]};
-    const float2v db = p.dw_b ? (float2v){p.dw_b[c], p.dw_b[c + 1]} : (float2v){0.f, 0.f};
-    const float2v sc = {p.dw_scale[c], p.dw_scale[c + 1]}, sh = {p.dw_shift[c], p.dw_shift[c + 1]};
+    const float2v(&wk)[K] = dp.wk;
+    const float2v db = dp.db, sc = dp.sc, sh = dp.sh;
     const int r0 = H + g * RPG;
     float2v win[RPG + K - 1];
 #pragma unroll
@@ -1174,6 +1204,12 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
     if constexpr (RPRE) {
         if (kg == 0) rpre.load(p, m0 + wm * WTM * 32, n0 + wn * WTN * 32, lane);
     }
+    // the epilogue's per-column (and conv-module per-channel) constants
+    const bool fold = FOLD && p.fold_stats != nullptr;
+    EpiCols<WTN> ecol;
+    if (kg == 0) ecol.load(p, n0 + wn * WTN * 32, lane, fold, EPI == EPI_RESID_LN);
+    DwPre<EPI == EPI_GLU_DW ? C::BM : 64, 16 * TN> dwpre;
+    if constexpr (EPI == EPI_GLU_DW) dwpre.load(p, m0, n0, tid);
 
     const int nk = p.K / 64 / KG, kb = kg * nk * 64;   // slabs of this group, its first K
     DmaSrc<TM, TN, WT> src;
@@ -1224,7 +1260,6 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
     // folded LayerNorm: the tile's row statistics at the top of the LDS block
     // (published by the barrier before the staging below)
     float2v* ftab = (float2v*)(smem_all + KG * NS * C::STAGE) - C::BM;
-    const bool fold = FOLD && p.fold_stats != nullptr;
     if constexpr (FOLD) {
         if (fold) {
             __syncthreads();
@@ -1237,7 +1272,7 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
         static_assert(C::BM * (32 * TN + 2) * 4 + C::BM * 8 + C::BM * 8 <= NS * C::STAGE,
                       "conv staging exceeds LDS ring");
         __syncthreads();
-        epilogue32_glu_dw<TM, TN>(p, acc, (float*)smem, m0, n0, wm, wn, tid, fold, ftab);
+        epilogue32_glu_dw<TM, TN>(p, acc, (float*)smem, m0, n0, wm, wn, tid, fold, ftab, ecol, dwpre);
     } else if constexpr (EPI == EPI_RELU_TR) {
         if ((32 * TM) % p.trF == 0 && (32 * TN * p.trF) % 8 == 0 && p.N % 8 == 0) {
             static_assert(4 * 32 * TM * (32 * TN + 1) * 4 <= NS * C::STAGE, "epilogue staging exceeds LDS ring");
@@ -1257,8 +1292,8 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
             __syncthreads();
             float* wsm = (float*)smem + wid * (32 * WTM) * ((EPI == EPI_GLU ? 16 * WTN : 32 * WTN) + 4);
             if (kg == 0)
-                epilogue32_lds<EPI, WTM, WTN>(p, acc, wsm, m0 + wm * WTM * 32, n0 + wn * WTN * 32, lane, fold,
-                                              ftab, wm * WTM * 32, RPRE ? rpre.v : nullptr);
+                epilogue32_lds<EPI, WTM, WTN>(p, acc, wsm, m0 + wm * WTM * 32, n0 + wn * WTN * 32, lane, ecol,
+                                              fold, ftab, wm * WTM * 32, RPRE ? rpre.v : nullptr);
         } else {
             constexpr int TH = WTM / 2;
             float* wsm = (float*)smem + wid * (32 * TH) * ((EPI == EPI_GLU ? 16 * WTN : 32 * WTN) + 4);
@@ -1272,7 +1307,8 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
                 __syncthreads();
                 if (kg == 0)
                     epilogue32_lds<EPI, TH, WTN>(p, part, wsm, m0 + wm * WTM * 32 + hh * TH * 32,
-                                                 n0 + wn * WTN * 32, lane, fold, ftab, wm * WTM * 32 + hh * TH * 32);
+                                                 n0 + wn * WTN * 32, lane, ecol, fold, ftab,
+                                                 wm * WTM * 32 + hh * TH * 32);
             }
         }
     }
