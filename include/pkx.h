@@ -191,6 +191,39 @@ int pkx_layernorm(const float* x_dev, const float* g_dev, const float* b_dev, fl
 /* pk::rel_pos_encoding (src/pos_enc.cpp:10-34): out_dev [2T-1][D] f32. */
 int pkx_rel_pos_encoding(int T, int D, float* out_dev, void* stream);
 
+/* ---- log-mel front end --------------------------------------------------------
+ * pk::MelFrontend::compute (src/mel.hpp:33-41, src/mel.cpp:99-185) for a batch
+ * of 16 kHz mono clips, stacked to T_max as build_mel_batch does
+ * (src/model.cpp:114-146), on the device.  f64 preemphasis, radix-2 FFT,
+ * power, filterbank sum and log with the reference's f32 roundings; per-feature
+ * normalisation over each clip's first n_samples/hop frames. */
+typedef struct pkx_mel pkx_mel;
+typedef struct {
+    int n_fft, win_length, hop_length, n_mels;
+    int per_feature;      /* parakeet.preprocessor.normalize == "per_feature" */
+    float preemph, mag_power, log_zero_guard;
+} pkx_mel_config;
+
+/* MelKernel::MelKernel (src/mel.cpp:16-61): window of window_len values
+ * (centre-padded to n_fft), filterbank fb [n_mels][n_fft/2+1].  n_fft is a
+ * power of two in [64, 512]. */
+int pkx_mel_create(const pkx_mel_config* cfg, const float* window, int window_len, const float* fb,
+                   pkx_mel** out);
+/* The same from a GGUF: parakeet.preprocessor.* (src/model_loader.cpp:133-141)
+ * and the preprocessor.featurizer.window / .fb tensors. */
+int pkx_mel_load_gguf(const char* path, pkx_mel** out);
+int pkx_mel_free(pkx_mel* m);
+int pkx_mel_info(const pkx_mel* m, pkx_mel_config* cfg);
+/* Frames of an n-sample clip (src/mel.cpp:132-135): 1 + n/hop for an even n_fft,
+ * 0 for n = 0; -1 for a null handle. */
+int pkx_mel_frames(const pkx_mel* m, int n_samples);
+/* pcm_dev [B][S_stride] f32, n_samples (host) [B] <= S_stride ->
+ * mel_dev [B][n_mels][T_max] (T_max >= every clip's frames, zero-padded),
+ * T_out (host) [B] frames per clip.  Returns once the batch is computed; one
+ * handle is not re-entrant. */
+int pkx_mel_forward(pkx_mel* m, const float* pcm_dev, int B, int64_t S_stride, const int* n_samples,
+                    float* mel_dev, int T_max, int* T_out, void* stream);
+
 /* ---- profiling ----------------------------------------------------------------
  * No counterpart in the reference (its benchmarks time whole calls).
  * family_mask selects kernel families by bit (bit i = family i in the order

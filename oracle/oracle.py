@@ -55,6 +55,11 @@ def lib():
         L.orc_ctc_greedy.argtypes = [_i32, C.c_int, C.c_int, _i32]
         L.orc_tdt_joint_argmax.argtypes = [_f, C.c_int, C.c_int, _f, _f, C.c_int, _f, C.c_int,
                                            _f, _f, _f, _f, C.c_int, C.c_int, _f, _i32, _i32]
+        L.orc_mel_window.argtypes = [_f, C.c_int, C.c_int, _f]
+        L.orc_mel_frames.argtypes = [C.c_void_p, C.c_int]
+        L.orc_rfft.argtypes = [_f, C.c_int, _f, _f]
+        L.orc_mel.argtypes = [C.c_void_p, _f, _f, _f, C.c_int, _f]
+        L.orc_mel_batch.argtypes = [C.c_void_p, _f, _f, _f, C.c_int, C.c_int, _i, C.c_int, _f, _i]
         _lib = L
     return _lib
 
@@ -304,3 +309,61 @@ def valid_out_len(T, in_valid=-1):
 
 def subsampled_len(T):
     return lib().orc_subsampled_len(T)
+
+
+# ---- log-mel front end (mel.cpp, fft.cpp, model.cpp:114-146) ----------------
+
+class MelCfg(C.Structure):
+    _fields_ = [("n_fft", C.c_int), ("hop", C.c_int), ("n_mels", C.c_int), ("per_feature", C.c_int),
+                ("preemph", C.c_float), ("mag_power", C.c_float), ("log_guard", C.c_float)]
+
+
+def mel_cfg(n_fft=512, hop=160, n_mels=128, per_feature=True, preemph=0.97, mag_power=2.0,
+            log_guard=2.0 ** -24) -> MelCfg:
+    return MelCfg(n_fft, hop, n_mels, int(bool(per_feature)), preemph, mag_power, log_guard)
+
+
+def mel_window(win: np.ndarray, n_fft: int) -> np.ndarray:
+    win = np.ascontiguousarray(win, dtype=np.float32)
+    out = np.zeros(n_fft, np.float32)
+    lib().orc_mel_window(fp(win), len(win), n_fft, fp(out))
+    return out
+
+
+def mel_frames(cfg: MelCfg, S: int) -> int:
+    return lib().orc_mel_frames(C.byref(cfg), int(S))
+
+
+def rfft(x: np.ndarray):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n = len(x)
+    re, im = np.zeros(n // 2 + 1, np.float32), np.zeros(n // 2 + 1, np.float32)
+    lib().orc_rfft(fp(x), n, fp(re), fp(im))
+    return re, im
+
+
+def mel(cfg: MelCfg, window: np.ndarray, fb: np.ndarray, samples: np.ndarray) -> np.ndarray:
+    """MelFrontend::compute for one clip -> feats [n_mels][T] (window: n_fft values)."""
+    samples = np.ascontiguousarray(samples, dtype=np.float32)
+    T = mel_frames(cfg, len(samples))
+    out = np.zeros((cfg.n_mels, T), np.float32)
+    if T:
+        lib().orc_mel(C.byref(cfg), fp(np.ascontiguousarray(window, np.float32)),
+                      fp(np.ascontiguousarray(fb, np.float32)), fp(samples), len(samples), fp(out))
+    return out
+
+
+def mel_batch(cfg: MelCfg, window: np.ndarray, fb: np.ndarray, pcm: np.ndarray, n_samples, T_max=None):
+    """build_mel_batch -> ([B][n_mels][T_max] zero-padded, T per clip)."""
+    pcm = np.ascontiguousarray(pcm, dtype=np.float32)
+    ns = np.ascontiguousarray(n_samples, dtype=np.int32)
+    B, S_stride = pcm.shape
+    Ts = [mel_frames(cfg, int(s)) for s in ns]
+    if T_max is None:
+        T_max = max(Ts) if Ts else 0
+    out = np.zeros((B, cfg.n_mels, T_max), np.float32)
+    T_out = np.zeros(B, np.int32)
+    lib().orc_mel_batch(C.byref(cfg), fp(np.ascontiguousarray(window, np.float32)),
+                        fp(np.ascontiguousarray(fb, np.float32)), fp(pcm), B, S_stride, ip(ns), T_max,
+                        fp(out), T_out.ctypes.data_as(_i))
+    return out, T_out

@@ -675,3 +675,153 @@ void orc_tdt_joint_argmax(const float* enc, int T, int D, const float* Wenc,
     }
     free(ep); free(pp); free(f);
 }
+
+/* ------------------------------------------------------------------------ */
+/* Log-mel front end: mel.cpp, fft.cpp, model.cpp:114-146                   */
+/* The reference's CPU build has no FMA contraction (baseline x86-64), so    */
+/* these functions are compiled without it as well.                          */
+/* ------------------------------------------------------------------------ */
+
+void orc_mel_window(const float* win, int win_len, int n_fft, float* out) {
+    /* mel.cpp:31-46: zero-pad (n_fft - win_len)/2 on the left */
+    for (int i = 0; i < n_fft; ++i) out[i] = 0.f;
+    if (win_len == n_fft) {
+        memcpy(out, win, sizeof(float) * (size_t)n_fft);
+        return;
+    }
+    const int left = (n_fft - win_len) / 2;
+    for (int i = 0; i < win_len && left + i < n_fft; ++i)
+        if (left + i >= 0) out[left + i] = win[i];
+}
+
+int orc_mel_frames(const orc_mel_cfg* c, int S) {
+    if (S <= 0) return 0;
+    const int padded = S + 2 * (c->n_fft / 2);
+    return padded >= c->n_fft ? 1 + (padded - c->n_fft) / c->hop : 0;
+}
+
+/* fft.cpp:9-51: bit reversal, then butterfly stages with the twiddle advanced
+ * by complex multiplication (w <- w * e^{-2 pi i / len}) inside each group. */
+__attribute__((optimize("fp-contract=off")))
+static void orc_fft_inplace(double* re, double* im, int n) {
+    for (int i = 1, j = 0; i < n; ++i) {
+        int bit = n >> 1;
+        for (; j & bit; bit >>= 1) j ^= bit;
+        j ^= bit;
+        if (i < j) {
+            double t = re[i]; re[i] = re[j]; re[j] = t;
+            t = im[i]; im[i] = im[j]; im[j] = t;
+        }
+    }
+    for (int len = 2; len <= n; len <<= 1) {
+        const double ang = -2.0 * M_PI / len, wr = cos(ang), wi = sin(ang);
+        for (int i = 0; i < n; i += len) {
+            double cr = 1.0, ci = 0.0;
+            for (int k = 0; k < len / 2; ++k) {
+                const int u = i + k, v = i + k + len / 2;
+                const double tr = cr * re[v] - ci * im[v];
+                const double ti = cr * im[v] + ci * re[v];
+                re[v] = re[u] - tr;
+                im[v] = im[u] - ti;
+                re[u] = re[u] + tr;
+                im[u] = im[u] + ti;
+                const double nr = cr * wr - ci * wi, ni = cr * wi + ci * wr;
+                cr = nr;
+                ci = ni;
+            }
+        }
+    }
+}
+
+void orc_rfft(const float* in, int n, float* re, float* im) {
+    /* fft.cpp:53-74 */
+    double* br = (double*)malloc(sizeof(double) * (size_t)n);
+    double* bi = (double*)malloc(sizeof(double) * (size_t)n);
+    for (int i = 0; i < n; ++i) { br[i] = (double)in[i]; bi[i] = 0.0; }
+    orc_fft_inplace(br, bi, n);
+    for (int k = 0; k <= n / 2; ++k) { re[k] = (float)br[k]; im[k] = (float)bi[k]; }
+    free(br);
+    free(bi);
+}
+
+__attribute__((optimize("fp-contract=off")))
+int orc_mel(const orc_mel_cfg* c, const float* window, const float* fb,
+            const float* samples, int S, float* feats) {
+    const int n_fft = c->n_fft, hop = c->hop, n_mels = c->n_mels, n_bins = n_fft / 2 + 1;
+    const int T = orc_mel_frames(c, S);
+    if (T == 0) return 0;
+    /* preemphasis in f64 (mel.cpp:110-117), then the zero-padded signal
+     * (pad_mode "constant", mel.cpp:137-142) */
+    const int pad = n_fft / 2, plen = S + 2 * pad;
+    double* padded = (double*)calloc((size_t)plen, sizeof(double));
+    for (int t = 0; t < S; ++t) {
+        double x = samples[t];
+        if (c->preemph > 0.0f && t > 0) x = (double)samples[t] - (double)c->preemph * (double)samples[t - 1];
+        padded[pad + t] = x;
+    }
+    float* frame = (float*)malloc(sizeof(float) * (size_t)n_fft);
+    float* re = (float*)malloc(sizeof(float) * (size_t)n_bins);
+    float* im = (float*)malloc(sizeof(float) * (size_t)n_bins);
+    double* power = (double*)malloc(sizeof(double) * (size_t)n_bins);
+    for (int t = 0; t < T; ++t) {
+        /* MelKernel::frame_logmel (mel.cpp:63-95) */
+        const double* fin = padded + (size_t)t * hop;
+        for (int i = 0; i < n_fft; ++i) frame[i] = (float)(fin[i] * (double)window[i]);
+        orc_rfft(frame, n_fft, re, im);
+        for (int b = 0; b < n_bins; ++b) {
+            const double mag = sqrt((double)re[b] * re[b] + (double)im[b] * im[b]);
+            power[b] = c->mag_power == 1.0f ? mag : pow(mag, (double)c->mag_power);
+        }
+        for (int m = 0; m < n_mels; ++m) {
+            const float* fbm = fb + (size_t)m * n_bins;
+            double acc = 0.0;
+            for (int b = 0; b < n_bins; ++b) acc += (double)fbm[b] * power[b];
+            feats[(size_t)m * T + t] = (float)log(acc + (double)c->log_guard);
+        }
+    }
+    /* per-feature normalisation (mel.cpp:153-183): mean and unbiased std over
+     * the first S/hop frames, std += 1e-5, later frames zeroed */
+    if (c->per_feature) {
+        const int valid = S / hop < T ? S / hop : T;
+        for (int m = 0; m < n_mels; ++m) {
+            float* row = feats + (size_t)m * T;
+            double mean = 0.0, var = 0.0;
+            if (valid > 0) {
+                for (int t = 0; t < valid; ++t) mean += row[t];
+                mean /= (double)valid;
+            }
+            if (valid > 1) {
+                for (int t = 0; t < valid; ++t) {
+                    const double d = (double)row[t] - mean;
+                    var += d * d;
+                }
+                var /= (double)(valid - 1);
+            }
+            const double sd = sqrt(var) + 1e-5;
+            for (int t = 0; t < T; ++t) row[t] = t < valid ? (float)(((double)row[t] - mean) / sd) : 0.0f;
+        }
+    }
+    free(padded);
+    free(frame);
+    free(re);
+    free(im);
+    free(power);
+    return T;
+}
+
+void orc_mel_batch(const orc_mel_cfg* c, const float* window, const float* fb,
+                   const float* pcm, int B, int S_stride, const int* n_samples,
+                   int T_max, float* out, int* T_out) {
+    memset(out, 0, sizeof(float) * (size_t)B * c->n_mels * T_max);
+#pragma omp parallel for schedule(dynamic)
+    for (int b = 0; b < B; ++b) {
+        const int T = orc_mel_frames(c, n_samples[b]);
+        T_out[b] = T;
+        if (T == 0 || T > T_max) continue;
+        float* f = (float*)malloc(sizeof(float) * (size_t)c->n_mels * T);
+        orc_mel(c, window, fb, pcm + (size_t)b * S_stride, n_samples[b], f);
+        for (int m = 0; m < c->n_mels; ++m)
+            memcpy(out + ((size_t)b * c->n_mels + m) * T_max, f + (size_t)m * T, sizeof(float) * (size_t)T);
+        free(f);
+    }
+}

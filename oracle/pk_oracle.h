@@ -137,6 +137,28 @@ void orc_tdt_joint_argmax(const float* enc, int T, int D, const float* Wenc,
                           const float* Wout, const float* bout, int n_tok,
                           int n_dur, float* logits, int32_t* tok, int32_t* dur);
 
+/* ---- log-mel front end (mel.cpp, fft.cpp, model.cpp:114-146) ------------ */
+typedef struct {
+    int n_fft, hop, n_mels, per_feature;   /* per_feature: normalize == "per_feature" */
+    float preemph, mag_power, log_guard;
+} orc_mel_cfg;
+
+/* mel.cpp:25-46 -- a win_length window centre-padded to n_fft. */
+void orc_mel_window(const float* win, int win_len, int n_fft, float* out);
+/* Frames of an S-sample clip: 1 + (S + 2 (n_fft/2) - n_fft) / hop (mel.cpp:132-135). */
+int  orc_mel_frames(const orc_mel_cfg* c, int S);
+/* fft.cpp:9-74 -- radix-2 rfft of n floats (n a power of two), bins 0..n/2 as f32. */
+void orc_rfft(const float* in, int n, float* re, float* im);
+/* mel.cpp:99-185 -- MelFrontend::compute for one clip: feats [n_mels][T]
+ * (window: n_fft values, fb: [n_mels][n_fft/2+1]).  Returns T. */
+int  orc_mel(const orc_mel_cfg* c, const float* window, const float* fb,
+             const float* samples, int S, float* feats);
+/* model.cpp:119-146 -- build_mel_batch: per-clip log-mel stacked to T_max,
+ * out [B][n_mels][T_max] zero-padded, T_out[b] each clip's frame count. */
+void orc_mel_batch(const orc_mel_cfg* c, const float* window, const float* fb,
+                   const float* pcm, int B, int S_stride, const int* n_samples,
+                   int T_max, float* out, int* T_out);
+
 #ifdef __cplusplus
 }
 #endif

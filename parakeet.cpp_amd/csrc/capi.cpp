@@ -5,7 +5,12 @@
 #include <string>
 
 #include "../../include/pkx.h"
+#include "mel.hpp"
 #include "model.hpp"
+
+struct pkx_mel {
+    std::unique_ptr<pkx::MelFront> impl;
+};
 
 struct pkx_model {
     pkx_config cfg;
@@ -322,6 +327,63 @@ int pkx_model_profile_read(pkx_model* m, double* ms, int64_t* launches) {
     return guarded([&] {
         need(m, "null model");
         m->impl->profile_read(ms, launches);
+    });
+}
+
+int pkx_mel_create(const pkx_mel_config* cfg, const float* window, int window_len, const float* fb,
+                   pkx_mel** out) {
+    return guarded([&] {
+        need(cfg && out && window && fb, "null argument");
+        *out = nullptr;
+        pkx::MelConfig c;
+        c.n_fft = cfg->n_fft;
+        c.win_length = window_len;
+        c.hop = cfg->hop_length;
+        c.n_mels = cfg->n_mels;
+        c.per_feature = cfg->per_feature ? 1 : 0;
+        c.preemph = cfg->preemph;
+        c.mag_power = cfg->mag_power;
+        c.log_guard = cfg->log_zero_guard;
+        std::unique_ptr<pkx_mel> h(new pkx_mel);
+        h->impl.reset(new pkx::MelFront(c, window, window_len, fb));
+        *out = h.release();
+    });
+}
+int pkx_mel_load_gguf(const char* path, pkx_mel** out) {
+    return guarded([&] {
+        need(path && out, "null argument");
+        *out = nullptr;
+        pkx::MelConfig c;
+        std::vector<float> window, fb;
+        pkx::load_mel_gguf(path, c, window, fb);
+        std::unique_ptr<pkx_mel> h(new pkx_mel);
+        h->impl.reset(new pkx::MelFront(c, window.data(), (int)window.size(), fb.data()));
+        *out = h.release();
+    });
+}
+int pkx_mel_free(pkx_mel* m) {
+    return guarded([&] { delete m; });
+}
+int pkx_mel_info(const pkx_mel* m, pkx_mel_config* cfg) {
+    return guarded([&] {
+        need(m && cfg, "null argument");
+        const pkx::MelConfig& c = m->impl->config();
+        cfg->n_fft = c.n_fft;
+        cfg->win_length = c.win_length;
+        cfg->hop_length = c.hop;
+        cfg->n_mels = c.n_mels;
+        cfg->per_feature = c.per_feature;
+        cfg->preemph = c.preemph;
+        cfg->mag_power = c.mag_power;
+        cfg->log_zero_guard = c.log_guard;
+    });
+}
+int pkx_mel_frames(const pkx_mel* m, int n_samples) { return m ? m->impl->frames(n_samples) : -1; }
+int pkx_mel_forward(pkx_mel* m, const float* pcm, int B, int64_t S_stride, const int* n_samples, float* mel,
+                    int T_max, int* T_out, void* s) {
+    return guarded([&] {
+        need(m != nullptr, "null mel handle");
+        m->impl->forward(pcm, B, S_stride, n_samples, mel, T_max, T_out, st(s));
     });
 }
 

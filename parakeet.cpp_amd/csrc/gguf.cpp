@@ -9,6 +9,7 @@
 #include <string>
 #include <vector>
 
+#include "mel.hpp"
 #include "model.hpp"
 
 namespace pkx {
@@ -134,23 +135,26 @@ bool wanted(const std::string& n) {
            starts("joint.enc.") || starts("joint.pred.") || starts("joint.joint_net.2.");
 }
 
-}  // namespace
+struct Header {
+    std::map<std::string, KvVal> kv;
+    std::vector<TensorInfo> infos;
+    uint64_t data0 = 0;
+};
 
-std::unique_ptr<Model> load_gguf(const std::string& path, int precision) {
-    File f(path);
+Header read_header(File& f, const std::string& path) {
     require(f.get<uint32_t>() == 0x46554747u, "not a GGUF file: " + path);
     const uint32_t version = f.get<uint32_t>();
     require(version == 3 || version == 2, "unsupported GGUF version " + std::to_string(version));
     const uint64_t n_tensors = f.get<uint64_t>();
     const uint64_t n_kv = f.get<uint64_t>();
-    std::map<std::string, KvVal> kv;
+    Header h;
     for (uint64_t i = 0; i < n_kv; ++i) {
         std::string key = f.str();
         const uint32_t t = f.get<uint32_t>();
-        kv[key] = read_val(f, t);
+        h.kv[key] = read_val(f, t);
     }
-    std::vector<TensorInfo> infos((size_t)n_tensors);
-    for (auto& ti : infos) {
+    h.infos.resize((size_t)n_tensors);
+    for (auto& ti : h.infos) {
         ti.name = f.str();
         ti.n_dims = (int)f.get<uint32_t>();
         require(ti.n_dims >= 1 && ti.n_dims <= 4, "GGUF: bad n_dims");
@@ -159,8 +163,74 @@ std::unique_ptr<Model> load_gguf(const std::string& path, int precision) {
         ti.offset = f.get<uint64_t>();
     }
     uint64_t align = 32;
-    if (kv.count("general.alignment")) align = (uint64_t)kv["general.alignment"].i;
-    const uint64_t data0 = (f.tell() + align - 1) / align * align;
+    if (h.kv.count("general.alignment")) align = (uint64_t)h.kv["general.alignment"].i;
+    h.data0 = (f.tell() + align - 1) / align * align;
+    return h;
+}
+
+// an f32 or f16 tensor read as f32
+std::vector<float> read_f32_tensor(File& f, const Header& h, const TensorInfo& ti) {
+    require(ti.gtype == GT_F32 || ti.gtype == GT_F16, "GGUF: " + ti.name + " must be f32 or f16");
+    const int64_t n = ti.ne[0] * ti.ne[1] * ti.ne[2] * ti.ne[3];
+    std::vector<float> out((size_t)n);
+    f.seek(h.data0 + ti.offset);
+    if (ti.gtype == GT_F32) {
+        f.read(out.data(), sizeof(float) * (size_t)n);
+    } else {
+        std::vector<uint16_t> hb((size_t)n);
+        f.read(hb.data(), 2 * (size_t)n);
+        for (int64_t i = 0; i < n; ++i) {
+            _Float16 hv;   // exact binary16 -> binary32
+            std::memcpy(&hv, &hb[(size_t)i], 2);
+            out[(size_t)i] = (float)hv;
+        }
+    }
+    return out;
+}
+
+}  // namespace
+
+void load_mel_gguf(const std::string& path, MelConfig& c, std::vector<float>& window, std::vector<float>& fb) {
+    File f(path);
+    Header h = read_header(f, path);
+    auto has = [&](const char* k) { return h.kv.count(k) > 0; };
+    auto u = [&](const char* k, int64_t dflt) -> int64_t { return has(k) ? h.kv[k].i : dflt; };
+    auto fl = [&](const char* k, double dflt) -> double { return has(k) ? h.kv[k].d : dflt; };
+    // src/model_loader.cpp:133-141 keys and defaults
+    require(has("parakeet.preprocessor.n_mels") && has("parakeet.preprocessor.n_fft") &&
+                has("parakeet.preprocessor.win_length") && has("parakeet.preprocessor.hop_length"),
+            "GGUF: missing parakeet.preprocessor.{n_mels,n_fft,win_length,hop_length}: " + path);
+    c.n_mels = (int)u("parakeet.preprocessor.n_mels", 0);
+    c.n_fft = (int)u("parakeet.preprocessor.n_fft", 0);
+    c.win_length = (int)u("parakeet.preprocessor.win_length", 0);
+    c.hop = (int)u("parakeet.preprocessor.hop_length", 0);
+    c.preemph = (float)fl("parakeet.preprocessor.preemph", 0.0);
+    c.mag_power = (float)fl("parakeet.preprocessor.mag_power", 2.0);
+    c.log_guard = (float)fl("parakeet.preprocessor.log_zero_guard", 0.0);
+    const std::string norm = has("parakeet.preprocessor.normalize") ? h.kv["parakeet.preprocessor.normalize"].s
+                                                                    : std::string("per_feature");
+    c.per_feature = norm == "per_feature" ? 1 : 0;
+    const TensorInfo* tw = nullptr;
+    const TensorInfo* tf = nullptr;
+    for (const auto& ti : h.infos) {
+        if (ti.name == "preprocessor.featurizer.window") tw = &ti;
+        if (ti.name == "preprocessor.featurizer.fb") tf = &ti;
+    }
+    require(tw && tf, "GGUF: missing preprocessor.featurizer.window / .fb: " + path);
+    window = read_f32_tensor(f, h, *tw);
+    fb = read_f32_tensor(f, h, *tf);
+    // fb: ggml ne [n_bins, n_mels, 1] (src/mel.cpp:50-61)
+    require(tf->ne[0] == c.n_fft / 2 + 1 && tf->ne[1] == c.n_mels,
+            "GGUF: preprocessor.featurizer.fb must be [n_mels][n_fft/2+1]");
+    c.win_length = (int)window.size();
+}
+
+std::unique_ptr<Model> load_gguf(const std::string& path, int precision) {
+    File f(path);
+    Header h = read_header(f, path);
+    std::map<std::string, KvVal>& kv = h.kv;
+    const std::vector<TensorInfo>& infos = h.infos;
+    const uint64_t data0 = h.data0;
 
     auto u = [&](const char* k, int64_t dflt) -> int64_t {
         auto it = kv.find(k);

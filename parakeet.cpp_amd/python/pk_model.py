@@ -67,6 +67,15 @@ class Config:
     attn_bias: bool = True          # linear_q/k/v/out biases (110m: yes, 0.6b-v2: no)
     conv_bias: bool = True
     ff_bias: bool = True
+    # parakeet.preprocessor.* (src/model_loader.cpp:133-141; NeMo featurizer defaults)
+    sample_rate: int = 16000
+    n_fft: int = 512
+    win_length: int = 400
+    hop_length: int = 160
+    preemph: float = 0.97
+    mag_power: float = 2.0
+    normalize: str = "per_feature"
+    log_zero_guard: float = 2.0 ** -24
 
     @property
     def d_head(self):
@@ -188,6 +197,52 @@ def synth_q4_k(rng: np.random.Generator, n: int) -> np.ndarray:
     return blk.reshape(-1)
 
 
+def hann_window(n: int) -> np.ndarray:
+    """torch.hann_window(n, periodic=False): 0.5 - 0.5 cos(2 pi k / (n - 1))."""
+    k = np.arange(n, dtype=np.float64)
+    return (0.5 - 0.5 * np.cos(2.0 * np.pi * k / (n - 1))).astype(np.float32)
+
+
+def _hz_to_mel(f):
+    """Slaney's mel scale: linear below 1 kHz (200/3 Hz per mel), logarithmic above."""
+    f = np.asarray(f, dtype=np.float64)
+    f_sp, min_log_hz = 200.0 / 3, 1000.0
+    min_log_mel, logstep = min_log_hz / f_sp, np.log(6.4) / 27.0
+    return np.where(f >= min_log_hz, min_log_mel + np.log(np.maximum(f, 1e-10) / min_log_hz) / logstep, f / f_sp)
+
+
+def _mel_to_hz(m):
+    m = np.asarray(m, dtype=np.float64)
+    f_sp, min_log_hz = 200.0 / 3, 1000.0
+    min_log_mel, logstep = min_log_hz / f_sp, np.log(6.4) / 27.0
+    return np.where(m >= min_log_mel, min_log_hz * np.exp(logstep * (m - min_log_mel)), f_sp * m)
+
+
+def mel_filterbank(sr: int, n_fft: int, n_mels: int, fmin: float = 0.0, fmax=None) -> np.ndarray:
+    """Triangular filters on the Slaney mel scale with Slaney area normalisation
+    ([n_mels][n_fft/2+1] f32), the featurizer's filterbank (preprocessor.featurizer.fb)."""
+    fmax = sr / 2.0 if fmax is None else fmax
+    fft_f = np.linspace(0.0, sr / 2.0, n_fft // 2 + 1)
+    mel_f = _mel_to_hz(np.linspace(_hz_to_mel(fmin), _hz_to_mel(fmax), n_mels + 2))
+    fdiff = np.diff(mel_f)
+    ramps = mel_f[:, None] - fft_f[None, :]
+    lower = -ramps[:-2] / fdiff[:-1, None]
+    upper = ramps[2:] / fdiff[1:, None]
+    w = np.maximum(0.0, np.minimum(lower, upper))
+    w *= (2.0 / (mel_f[2:n_mels + 2] - mel_f[:n_mels]))[:, None]
+    return w.astype(np.float32)
+
+
+def add_featurizer(m: "Model"):
+    """preprocessor.featurizer.window / .fb of the config (the two buffers the
+    converter keeps from the checkpoint, docs/conversion.md:110-136)."""
+    c = m.cfg
+    m.tensors["preprocessor.featurizer.window"] = Tensor(GGML_F32, (c.win_length,), hann_window(c.win_length))
+    m.tensors["preprocessor.featurizer.fb"] = Tensor(
+        GGML_F32, (1, c.n_mels, c.n_fft // 2 + 1), mel_filterbank(c.sample_rate, c.n_fft, c.n_mels))
+    return m
+
+
 def synthesize(cfg: Config, qtype: str = "f32", seed: int = 20261201, heads: bool = True,
                bn_random: bool = False, std: float = 0.02) -> Model:
     """Seeded random-init weights of the given architecture.
@@ -246,6 +301,14 @@ def _kv_items(cfg: Config):
           (e + "xscaling", _GT_BOOL, bool(cfg.xscaling)),
           (e + "pos_emb_max_len", _GT_U32, 5000),
           ("parakeet.preprocessor.n_mels", _GT_U32, cfg.n_mels),
+          ("parakeet.preprocessor.sample_rate", _GT_U32, cfg.sample_rate),
+          ("parakeet.preprocessor.n_fft", _GT_U32, cfg.n_fft),
+          ("parakeet.preprocessor.win_length", _GT_U32, cfg.win_length),
+          ("parakeet.preprocessor.hop_length", _GT_U32, cfg.hop_length),
+          ("parakeet.preprocessor.preemph", _GT_F32, cfg.preemph),
+          ("parakeet.preprocessor.mag_power", _GT_F32, cfg.mag_power),
+          ("parakeet.preprocessor.normalize", _GT_STR, cfg.normalize),
+          ("parakeet.preprocessor.log_zero_guard", _GT_F32, cfg.log_zero_guard),
           ("parakeet.vocab_size", _GT_U32, cfg.vocab_size),
           ("parakeet.blank_id", _GT_U32, cfg.vocab_size),
           ("parakeet.joint.joint_hidden", _GT_U32, cfg.joint_hidden),

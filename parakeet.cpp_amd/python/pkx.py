@@ -29,6 +29,12 @@ class PkxError(RuntimeError):
     pass
 
 
+class MelConfig(C.Structure):
+    _fields_ = [("n_fft", C.c_int), ("win_length", C.c_int), ("hop_length", C.c_int), ("n_mels", C.c_int),
+                ("per_feature", C.c_int), ("preemph", C.c_float), ("mag_power", C.c_float),
+                ("log_zero_guard", C.c_float)]
+
+
 class Config(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("d_model", "n_layers", "n_heads", "ff_dim", "conv_kernel",
                                         "n_mels", "sub_channels", "xscaling", "vocab_size",
@@ -76,6 +82,12 @@ SIGS = {
                     _vp], C.c_int),
     "pkx_layernorm": ([_vp, _vp, _vp, _vp, C.c_int64, C.c_int, C.c_float, _vp], C.c_int),
     "pkx_rel_pos_encoding": ([C.c_int, C.c_int, _vp, _vp], C.c_int),
+    "pkx_mel_create": ([C.POINTER(MelConfig), _vp, C.c_int, _vp, C.POINTER(_vp)], C.c_int),
+    "pkx_mel_load_gguf": ([C.c_char_p, C.POINTER(_vp)], C.c_int),
+    "pkx_mel_free": ([_vp], C.c_int),
+    "pkx_mel_info": ([_vp, C.POINTER(MelConfig)], C.c_int),
+    "pkx_mel_frames": ([_vp, C.c_int], C.c_int),
+    "pkx_mel_forward": ([_vp, _vp, C.c_int, C.c_int64, _ip, _vp, C.c_int, _ip, _vp], C.c_int),
     "pkx_model_set_profiling": ([_vp, C.c_uint, C.c_int], C.c_int),
     "pkx_model_profile_read": ([_vp, C.POINTER(C.c_double), C.POINTER(C.c_int64)], C.c_int),
 }
@@ -339,3 +351,62 @@ class Model:
         n = (C.c_int64 * len(PROF_FAMILIES))()
         check(lib().pkx_model_profile_read(self.handle, ms, n))
         return {f: (ms[i], n[i]) for i, f in enumerate(PROF_FAMILIES)}
+
+
+class Mel:
+    """A device log-mel front end (pkx_mel handle): pk::MelFrontend for a batch."""
+
+    def __init__(self, handle):
+        self.handle = handle
+        cfg = MelConfig()
+        check(lib().pkx_mel_info(handle, C.byref(cfg)))
+        self.cfg = cfg
+
+    @classmethod
+    def create(cls, n_fft, win_length, hop_length, n_mels, window, fb, preemph=0.97, mag_power=2.0,
+               log_zero_guard=2.0 ** -24, per_feature=True):
+        window = np.ascontiguousarray(window, dtype=np.float32)
+        fb = np.ascontiguousarray(fb, dtype=np.float32)
+        cfg = MelConfig(n_fft, win_length, hop_length, n_mels, int(bool(per_feature)), preemph, mag_power,
+                        log_zero_guard)
+        h = _vp()
+        check(lib().pkx_mel_create(C.byref(cfg), window.ctypes.data, len(window), fb.ctypes.data, C.byref(h)))
+        return cls(h.value)
+
+    @classmethod
+    def from_model(cls, model):
+        """From a pk_model.Model carrying the preprocessor config and featurizer tensors."""
+        c = model.cfg
+        return cls.create(c.n_fft, c.win_length, c.hop_length, c.n_mels,
+                          model.tensors["preprocessor.featurizer.window"].data,
+                          model.tensors["preprocessor.featurizer.fb"].data.reshape(c.n_mels, -1),
+                          c.preemph, c.mag_power, c.log_zero_guard, c.normalize == "per_feature")
+
+    @classmethod
+    def load_gguf(cls, path):
+        h = _vp()
+        check(lib().pkx_mel_load_gguf(str(path).encode(), C.byref(h)))
+        return cls(h.value)
+
+    def frames(self, n_samples: int) -> int:
+        return lib().pkx_mel_frames(self.handle, int(n_samples))
+
+    def forward(self, pcm: DeviceArray, n_samples, out: DeviceArray, T_max: int, stream=None):
+        """pcm [B][S_stride] f32 on the device -> out [B][n_mels][T_max]; returns frames per clip."""
+        B, S_stride = pcm.shape
+        ns = np.ascontiguousarray(n_samples, dtype=np.int32)
+        T_out = np.zeros(B, np.int32)
+        check(lib().pkx_mel_forward(self.handle, pcm.ptr, B, S_stride, _iptr(ns), out.ptr, int(T_max),
+                                    _iptr(T_out), _sh(stream)))
+        return T_out
+
+    def close(self):
+        if self.handle:
+            lib().pkx_mel_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
