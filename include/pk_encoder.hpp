@@ -64,12 +64,18 @@ public:
 
     pkx_model* handle() const { return model_; }
     int precision() const { return precision_; }
+    // log-mel front end from the same GGUF (parakeet.preprocessor.* and
+    // preprocessor.featurizer.*); null if the file has none
+    pkx_mel* mel_handle() const { return mel_; }
+    const std::string& mel_error() const { return mel_err_; }
 
     struct Device;                        // stream, staging buffers, lock
     Device& device() const { return *dev_; }
 
 private:
     pkx_model* model_ = nullptr;
+    pkx_mel* mel_ = nullptr;
+    std::string mel_err_;
     ParakeetConfig cfg_;
     int precision_ = PKX_PREC_AUTO;
     std::string err_;
@@ -181,5 +187,21 @@ private:
 
 // pos_emb [2T-1][d_model] f32 (computed on the device in double, then f32).
 void rel_pos_encoding(int T, int d_model, std::vector<float>& out);
+
+// Log-mel front end (src/mel.hpp:33-41), on the device.
+class MelFrontend {
+public:
+    explicit MelFrontend(const ModelLoader& ml);
+    // samples: 16 kHz mono.  Out: feats row-major [n_mels][T] (frame-major inner = T).
+    void compute(const std::vector<float>& samples, std::vector<float>& feats, int& n_mels, int& T) const;
+
+private:
+    const ModelLoader& ml_;
+};
+
+// Per-clip log-mel of a batch of 16 kHz mono clips, zero-padded and stacked to
+// the longest clip (src/model.cpp:114-146): data [B][n_mels][T_max], valid_T
+// each clip's frame count.  All clips in one device pass.
+MelBatch build_mel_batch(const ModelLoader& ml, const std::vector<std::vector<float>>& pcms16k);
 
 }  // namespace pk

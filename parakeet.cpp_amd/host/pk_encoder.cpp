@@ -4,7 +4,9 @@
 // back.  Plain C++17; the only device interface is pkx.h.
 #include "pk_encoder.hpp"
 
+#include <algorithm>
 #include <cmath>
+#include <cstdint>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
@@ -82,6 +84,7 @@ ModelLoader::ModelLoader() = default;
 
 ModelLoader::~ModelLoader() {
     dev_.reset();
+    if (mel_) pkx_mel_free(mel_);
     if (model_) pkx_model_free(model_);
 }
 
@@ -120,6 +123,11 @@ bool ModelLoader::load(const std::string& path, int precision) {
     model_ = m;
     dev_ = std::move(dev);
     err_.clear();
+    // the front end is optional: encoder-only files carry no featurizer
+    if (pkx_mel_load_gguf(path.c_str(), &mel_) != 0) {
+        mel_ = nullptr;
+        mel_err_ = pkx_last_error();
+    }
     return true;
 }
 
@@ -405,6 +413,62 @@ void rel_pos_encoding(int T, int d_model, std::vector<float>& out) {
     const std::string msg = rc ? pkx_last_error() : "";
     pkx_free(dp);
     if (rc) throw std::runtime_error("rel_pos_encoding: " + msg);
+}
+
+}  // namespace pk
+
+namespace pk {
+
+// ---------------------------------------------------------------------------
+// MelFrontend / build_mel_batch
+// ---------------------------------------------------------------------------
+static pkx_mel* mel_of(const ModelLoader& ml) {
+    need(ml.handle() != nullptr, "model not loaded");
+    need(ml.mel_handle() != nullptr, "no log-mel front end in this model: " + ml.mel_error());
+    return ml.mel_handle();
+}
+
+MelFrontend::MelFrontend(const ModelLoader& ml) : ml_(ml) { (void)mel_of(ml); }
+
+void MelFrontend::compute(const std::vector<float>& samples, std::vector<float>& feats, int& n_mels,
+                          int& T) const {
+    MelBatch mb = build_mel_batch(ml_, {samples});
+    n_mels = mb.n_mels;
+    T = mb.valid_T[0];
+    feats.assign(mb.data.begin(), mb.data.begin() + (size_t)n_mels * T);
+}
+
+MelBatch build_mel_batch(const ModelLoader& ml, const std::vector<std::vector<float>>& pcms16k) {
+    pkx_mel* mel = mel_of(ml);
+    pkx_mel_config mc{};
+    chk(pkx_mel_info(mel, &mc), "pkx_mel_info");
+    MelBatch mb;
+    mb.B = (int)pcms16k.size();
+    mb.n_mels = mc.n_mels;
+    need(mb.B >= 1, "build_mel_batch: empty batch");
+    size_t S = 1;
+    std::vector<int> ns(mb.B);
+    for (int b = 0; b < mb.B; ++b) {
+        need(pcms16k[b].size() < (size_t)INT32_MAX, "build_mel_batch: clip too long");
+        ns[b] = (int)pcms16k[b].size();
+        S = std::max(S, pcms16k[b].size());
+        mb.T_max = std::max(mb.T_max, pkx_mel_frames(mel, ns[b]));
+    }
+    mb.valid_T.assign(mb.B, 0);
+    if (mb.T_max == 0) return mb;
+    std::vector<float> pcm((size_t)mb.B * S, 0.0f);
+    for (int b = 0; b < mb.B; ++b) std::copy(pcms16k[b].begin(), pcms16k[b].end(), pcm.begin() + (size_t)b * S);
+    ModelLoader::Device& d = ml.device();
+    std::lock_guard<std::mutex> lock(d.mu);
+    float* dpcm = (float*)d.get(d.in, pcm.size() * 4);
+    float* dout = (float*)d.get(d.out, (size_t)mb.B * mb.n_mels * mb.T_max * 4);
+    d.h2d(dpcm, pcm.data(), pcm.size() * 4);
+    chk(pkx_mel_forward(mel, dpcm, mb.B, (int64_t)S, ns.data(), dout, mb.T_max, mb.valid_T.data(), d.stream),
+        "pkx_mel_forward");
+    mb.data.resize((size_t)mb.B * mb.n_mels * mb.T_max);
+    d.d2h(mb.data.data(), dout, mb.data.size() * 4);
+    d.sync();
+    return mb;
 }
 
 }  // namespace pk

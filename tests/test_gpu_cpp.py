@@ -20,8 +20,17 @@ pytestmark = pytest.mark.gpu
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 BIN = os.path.join(ROOT, "tests", "cpp", "build")
 TESTS = ["test_subsampling", "test_subsampling_batch", "test_relpos_attention", "test_relpos_attention_batch",
-         "test_conformer", "test_conformer_batch", "test_encoder", "test_encoder_batch"]
+         "test_conformer", "test_conformer_batch", "test_encoder", "test_encoder_batch", "test_mel"]
 _FILES = {}
+
+
+def read_wav(path):
+    """16-bit mono PCM -> f32 in [-1, 1) (x / 32768, as dr_wav converts s16)."""
+    import wave
+    with wave.open(path, "rb") as w:
+        assert w.getsampwidth() == 2 and w.getnchannels() == 1 and w.getframerate() == 16000
+        a = np.frombuffer(w.readframes(w.getnframes()), dtype="<i2")
+    return (a.astype(np.float32) / np.float32(32768.0)).astype(np.float32)
 
 
 def _files(tmp_path_factory, wtype):
@@ -30,7 +39,7 @@ def _files(tmp_path_factory, wtype):
     d = tmp_path_factory.mktemp(f"cpp_{wtype}")
     cfg = pm.Config(d_model=256, n_layers=4, n_heads=4, ff_dim=1024, conv_kernel=9, n_mels=80, sub_channels=64,
                     xscaling=True, vocab_size=127, joint_hidden=64, pred_hidden=64)
-    m = pm.synthesize(cfg, wtype, bn_random=True)
+    m = pm.add_featurizer(pm.synthesize(cfg, wtype, bn_random=True))
     om = oracle.OracleModel(m)
     rng = np.random.default_rng(42)
     F, T = cfg.n_mels, 1001
@@ -54,6 +63,13 @@ def _files(tmp_path_factory, wtype):
         "enc_layer_0": y0[0], "enc_layer_mid": cap[L // 2][0], "enc_layer_last": cap[L - 1][0],
         "encoder_out": np.ascontiguousarray(enc[0].T),
     }
+    # log-mel of the speech fixture (the oracle's MelFrontend restatement)
+    pcm = read_wav(os.path.join(ROOT, "tests", "golden", "speech.wav"))
+    mcfg = oracle.mel_cfg(n_fft=cfg.n_fft, hop=cfg.hop_length, n_mels=cfg.n_mels, preemph=cfg.preemph,
+                          mag_power=cfg.mag_power, log_guard=cfg.log_zero_guard)
+    base["pcm"] = pcm
+    base["mel_pcm"] = oracle.mel(mcfg, oracle.mel_window(m.tensors["preprocessor.featurizer.window"].data, cfg.n_fft),
+                                 m.tensors["preprocessor.featurizer.fb"].data.reshape(cfg.n_mels, -1), pcm)
     mp, bp = str(d / "model.gguf"), str(d / "baseline.gguf")
     pm.write_gguf(m, mp)
     pm.write_baseline_gguf(bp, base)

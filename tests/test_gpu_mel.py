@@ -114,3 +114,27 @@ def test_mel_rejects_bad_arguments(gpu, stream, feat):
     d_pcm.free()
     d_out.free()
     mel.close()
+
+
+def test_mel_on_speech_fixtures(gpu, stream, feat):
+    """The reference's own audio fixtures (tests/fixtures/clip.wav, speech.wav),
+    batched: real speech through the device front end against the oracle."""
+    import os
+    from test_gpu_cpp import read_wav
+    root = os.path.dirname(os.path.abspath(__file__))
+    clips = [read_wav(os.path.join(root, "golden", n)) for n in ("clip.wav", "speech.wav")]
+    lens = [len(c) for c in clips]
+    print(f"[mel] speech fixtures lens={lens}", flush=True)
+    pcm = np.zeros((2, max(lens)), np.float32)
+    for b, c in enumerate(clips):
+        pcm[b, :len(c)] = c
+    win, fb = feat
+    mel = gpu.Mel.create(N_FFT, WIN, HOP, 128, win, fb)
+    cfg = oracle.mel_cfg()
+    T_max = max(oracle.mel_frames(cfg, n) for n in lens)
+    ref, _ = oracle.mel_batch(cfg, oracle.mel_window(win, N_FFT), fb, pcm, lens, T_max)
+    got, T = _run(gpu, stream, mel, pcm, lens, T_max)
+    err = np.max(np.abs(got - ref))
+    print(f"[mel] speech max abs {err:.3e}, bit-identical {float(np.mean(got == ref)):.4f}", flush=True)
+    assert err <= 1e-4
+    mel.close()
