@@ -115,6 +115,51 @@ def other_config(name, qtype, cfg_kw, lens, T_max, steps, warmup, stream):
     return out
 
 
+def pcm_in(gm, cfg, stream, steps, warmup=2):
+    """PCM-in path: the device log-mel front end (pkx_mel_forward, 16 clips of
+    10 s of 16 kHz audio -> [16][n_mels][1001]) followed by the same encoder
+    forward.  Reports the front end alone (time, RTFx, algorithmic bytes
+    against HBM) and the two together."""
+    mel = pkx.Mel.create(cfg.n_fft, cfg.win_length, cfg.hop_length, cfg.n_mels, pm.hann_window(cfg.win_length),
+                         pm.mel_filterbank(cfg.sample_rate, cfg.n_fft, cfg.n_mels))
+    S = 10 * cfg.sample_rate
+    pcm = (np.random.default_rng(11).standard_normal((B, S)) * 0.1).astype(np.float32)
+    lens = np.full(B, S, np.int32)
+    T = mel.frames(S)
+    d_pcm = pkx.DeviceArray.from_numpy(pcm, stream)
+    d_mel = pkx.DeviceArray((B, cfg.n_mels, T), np.float32)
+    d_out = pkx.DeviceArray((B, pkx.subsampled_len(T), cfg.d_model), np.float32)
+    for _ in range(warmup):
+        Tv = mel.forward(d_pcm, lens, d_mel, T, stream=stream)
+        gm.encoder_forward(d_mel, Tv, d_out, stream=stream)
+    stream.sync()
+    e0, e1 = pkx.Event(), pkx.Event()
+    e0.record(stream)
+    for _ in range(steps):
+        mel.forward(d_pcm, lens, d_mel, T, stream=stream)
+    e1.record(stream)
+    mel_ms = e0.elapsed_ms(e1) / steps
+    e0.record(stream)
+    for _ in range(steps):
+        Tv = mel.forward(d_pcm, lens, d_mel, T, stream=stream)
+        gm.encoder_forward(d_mel, Tv, d_out, stream=stream)
+    e1.record(stream)
+    both_ms = e0.elapsed_ms(e1) / steps
+    stream.sync()
+    assert np.isfinite(d_out.numpy(stream)).all()
+    for a in (d_pcm, d_mel, d_out):
+        a.free()
+    mel.close()
+    audio_s = B * S / cfg.sample_rate
+    mel_bytes = B * S * 4 + B * cfg.n_mels * T * 4            # PCM in, log-mel out (f32)
+    return {"workload": "log-mel front end + encoder, batch 16 x 10 s of 16 kHz PCM (-> %d mel frames)" % T,
+            "mel_ms": round(mel_ms, 4), "mel_rtfx": round(audio_s / (mel_ms / 1e3), 1),
+            "mel_hbm": {"achieved": round(mel_bytes / (mel_ms / 1e3) / 1e9, 1), "unit": "GB/s",
+                        "frac": round(mel_bytes / (mel_ms / 1e3) / 1e9 / PEAK_HBM_GBS, 4),
+                        "bytes": mel_bytes, "note": "call time incl. its host sync; f64 FFT + filterbank"},
+            "ms_per_step": round(both_ms, 4), "rtfx": round(audio_s / (both_ms / 1e3), 1), "steps": steps}
+
+
 def cpu_baseline(model, mel_item, budget_s=12.0):
     import oracle
     om = oracle.OracleModel(model)
@@ -241,6 +286,8 @@ def main():
                 "per_launch": "2*M*D*FF = %.3f GFLOP (M=B*T'=%d, D=%d, FF=%d)" % (
                     work["gemm_ffn"][1] / 1e9, B * Tp, cfg.d_model, cfg.ff_dim)}
 
+    pcm_line = pcm_in(gm, cfg, stream, min(args.steps, 10))
+
     audio_s = B * T_MEL * HOP_S
     rtfx = audio_s / (ms_step / 1e3)
     line = {
@@ -257,6 +304,7 @@ def main():
         "roofline": roofline,
         "kernels": kernels,
         "kernel_busy_ms_per_step": round(busy_ms, 4),
+        "pcm_in": pcm_line,
         "setup_s": round(setup_s, 1),
     }
     if not args.no_extra:

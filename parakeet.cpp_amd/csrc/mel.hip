@@ -34,15 +34,20 @@ struct MelParams {
     const float* window;       // [n_fft]
     const float* fb;           // [n_mels][n_bins]
     const double* tw;          // [n_fft - 1][2]: stage of half-length h uses rows h-1 .. 2h-2
+    const int4* span;          // [n_mels]: the filter's nonzero bins [x, y), packed offset z
+    const float* fb_packed;    // the filters' values over their spans, back to back
+    int fb_nnz;
     float* out;                // [B][n_mels][T_max]
     int T_max, n_fft, log2n, hop, n_mels, n_bins, per_feature;
     float preemph, mag_power, log_guard;
 };
 
 __global__ __launch_bounds__(256) void mel_spec_kernel(MelParams p) {
-    constexpr int FB = MEL_FRAMES_PER_BLOCK;
+    constexpr int FB = MEL_FRAMES_PER_BLOCK, RPL = MEL_MAX_NFFT / 64;
     __shared__ double2 buf[4][MEL_MAX_NFFT];
     __shared__ double pw[FB][MEL_MAX_NFFT / 2 + 1];
+    __shared__ double2 tws[MEL_MAX_NFFT];
+    __shared__ float fbs[MEL_FB_LDS];
     const int b = blockIdx.y, t0 = blockIdx.x * FB;
     const int S = p.meta[2 * b], T = p.meta[2 * b + 1];
     if (t0 >= T) return;                               // uniform over the workgroup
@@ -51,30 +56,48 @@ __global__ __launch_bounds__(256) void mel_spec_kernel(MelParams p) {
     const float* x = p.pcm + (int64_t)b * p.S_stride;
     const double pre = (double)p.preemph;
 
+    // every frame's windowed samples (src/mel.cpp:67-69) are loaded up front,
+    // one global-memory round trip for the workgroup; twiddles and the
+    // filterbank's nonzero values go to LDS
+    float fr[FB / 4][RPL];
+#pragma unroll
     for (int r = 0; r < FB / 4; ++r) {
-        const int f = 4 * r + w, t = t0 + f;
-        double2* B2 = buf[w];
-        // windowed frame (src/mel.cpp:67-69) in bit-reversed order (src/fft.cpp:14-22)
-        for (int i = lane; i < N; i += 64) {
+        const int t = t0 + 4 * r + w;
+#pragma unroll
+        for (int ii = 0; ii < RPL; ++ii) {
+            const int i = lane + 64 * ii;
             const int q = t * p.hop + i - pad;         // sample index of padded[t*hop + i]
             double v = 0.0;
-            if (t < T && q >= 0 && q < S) {
+            if (i < N && t < T && q >= 0 && q < S) {
                 v = (double)x[q];
                 if (p.preemph > 0.0f && q > 0) v = (double)x[q] - pre * (double)x[q - 1];
             }
-            const float fr = (float)(v * (double)p.window[i]);
-            const int j = (int)(__brev((unsigned)i) >> (32 - p.log2n));
-            B2[j] = make_double2((double)fr, 0.0);
+            fr[r][ii] = i < N ? (float)(v * (double)p.window[i]) : 0.0f;
+        }
+    }
+    for (int i = tid; i < N - 1; i += 256) tws[i] = make_double2(p.tw[2 * i], p.tw[2 * i + 1]);
+    const bool fb_lds = p.fb_nnz <= MEL_FB_LDS;
+    if (fb_lds)
+        for (int i = tid; i < p.fb_nnz; i += 256) fbs[i] = p.fb_packed[i];
+
+    for (int r = 0; r < FB / 4; ++r) {
+        const int f = 4 * r + w;
+        double2* B2 = buf[w];
+        // the frame in bit-reversed order (src/fft.cpp:14-22)
+#pragma unroll
+        for (int ii = 0; ii < RPL; ++ii) {
+            const int i = lane + 64 * ii;
+            if (i < N) B2[(int)(__brev((unsigned)i) >> (32 - p.log2n))] = make_double2((double)fr[r][ii], 0.0);
         }
         __syncthreads();
         // butterfly stages (src/fft.cpp:25-50)
         for (int s = 0, h = 1; s < p.log2n; ++s, h <<= 1) {
             for (int bi = lane; bi < N / 2; bi += 64) {
                 const int k = bi & (h - 1), u = ((bi >> s) << (s + 1)) + k, v = u + h;
-                const double wr = p.tw[2 * (h - 1 + k)], wi = p.tw[2 * (h - 1 + k) + 1];
+                const double2 tw = tws[h - 1 + k];
                 const double2 a = B2[u], c = B2[v];
-                const double tr = wr * c.x - wi * c.y;
-                const double ti = wr * c.y + wi * c.x;
+                const double tr = tw.x * c.x - tw.y * c.y;
+                const double ti = tw.x * c.y + tw.y * c.x;
                 B2[v] = make_double2(a.x - tr, a.y - ti);
                 B2[u] = make_double2(a.x + tr, a.y + ti);
             }
@@ -88,28 +111,20 @@ __global__ __launch_bounds__(256) void mel_spec_kernel(MelParams p) {
         }
         __syncthreads();
     }
-    // filterbank + log (src/mel.cpp:82-89): output (m, f) with f fastest, so a
-    // wave writes 16 consecutive frames of 4 bins; 8 independent f64 chains
-    // per thread, each summed in bin order
-    constexpr int PER = 8;
+    // filterbank + log (src/mel.cpp:82-89), one f64 chain per output summed
+    // in bin order over the filter's nonzero span only: every other bin would
+    // add fb * power = +-0, which leaves the sum unchanged, so the result is
+    // the reference's dense sum bit for bit.  Output (m, f) with f fastest.
     const int f = tid & (FB - 1), t = t0 + f;
-    for (int mb = (tid >> 4) * PER; mb < p.n_mels; mb += (256 / FB) * PER) {
-        double acc[PER];
-#pragma unroll
-        for (int j = 0; j < PER; ++j) acc[j] = 0.0;
-        const float* fr = p.fb + (int64_t)mb * p.n_bins;
-        for (int k = 0; k < p.n_bins; ++k) {
-            const double pk = pw[f][k];
-#pragma unroll
-            for (int j = 0; j < PER; ++j)
-                if (mb + j < p.n_mels) acc[j] += (double)fr[(int64_t)j * p.n_bins + k] * pk;
+    for (int m = tid / FB; m < p.n_mels; m += 256 / FB) {
+        const int4 sp = p.span[m];                     // {first bin, end bin, packed offset, -}
+        double acc = 0.0;
+        if (fb_lds) {
+            for (int k = sp.x; k < sp.y; ++k) acc += (double)fbs[sp.z + k - sp.x] * pw[f][k];
+        } else {
+            for (int k = sp.x; k < sp.y; ++k) acc += (double)p.fb_packed[sp.z + k - sp.x] * pw[f][k];
         }
-        if (t < T) {
-#pragma unroll
-            for (int j = 0; j < PER; ++j)
-                if (mb + j < p.n_mels)
-                    p.out[((int64_t)b * p.n_mels + mb + j) * p.T_max + t] = (float)log(acc[j] + (double)p.log_guard);
-        }
+        if (t < T) p.out[((int64_t)b * p.n_mels + m) * p.T_max + t] = (float)log(acc + (double)p.log_guard);
     }
 }
 
@@ -180,6 +195,27 @@ MelFront::MelFront(const MelConfig& c, const float* window, int win_len, const f
             ci = ni;
         }
     }
+    // each filter's nonzero span and its values packed back to back (the
+    // kernel skips the exact zeros outside the span)
+    std::vector<int4> span((size_t)c.n_mels);
+    std::vector<float> packed;
+    for (int m = 0; m < c.n_mels; ++m) {
+        int lo = n_bins_, hi = 0;
+        for (int k = 0; k < n_bins_; ++k)
+            if (fb[(size_t)m * n_bins_ + k] != 0.0f) {
+                lo = std::min(lo, k);
+                hi = k + 1;
+            }
+        if (lo >= hi) lo = hi = 0;
+        span[(size_t)m] = make_int4(lo, hi, (int)packed.size(), 0);
+        for (int k = lo; k < hi; ++k) packed.push_back(fb[(size_t)m * n_bins_ + k]);
+    }
+    fb_nnz_ = (int)packed.size();
+    PKX_HIP(hipMalloc(&d_span_, sizeof(int4) * span.size()));
+    PKX_HIP(hipMemcpy(d_span_, span.data(), sizeof(int4) * span.size(), hipMemcpyHostToDevice));
+    PKX_HIP(hipMalloc(&d_fbp_, sizeof(float) * std::max<size_t>(packed.size(), 1)));
+    if (!packed.empty())
+        PKX_HIP(hipMemcpy(d_fbp_, packed.data(), sizeof(float) * packed.size(), hipMemcpyHostToDevice));
     PKX_HIP(hipMalloc(&d_window_, sizeof(float) * (size_t)c.n_fft));
     PKX_HIP(hipMalloc(&d_fb_, sizeof(float) * (size_t)c.n_mels * n_bins_));
     PKX_HIP(hipMalloc(&d_tw_, sizeof(double) * tw.size()));
@@ -189,7 +225,7 @@ MelFront::MelFront(const MelConfig& c, const float* window, int win_len, const f
 }
 
 MelFront::~MelFront() {
-    for (void* q : {(void*)d_window_, (void*)d_fb_, (void*)d_tw_, (void*)d_meta_})
+    for (void* q : {(void*)d_window_, (void*)d_fb_, (void*)d_tw_, (void*)d_meta_, d_span_, (void*)d_fbp_})
         if (q) (void)hipFree(q);
 }
 
@@ -229,6 +265,9 @@ void MelFront::forward(const float* pcm, int B, int64_t S_stride, const int* n_s
     p.window = d_window_;
     p.fb = d_fb_;
     p.tw = d_tw_;
+    p.span = (const int4*)d_span_;
+    p.fb_packed = d_fbp_;
+    p.fb_nnz = fb_nnz_;
     p.out = out;
     p.T_max = T_max;
     p.n_fft = cfg_.n_fft;

@@ -18,7 +18,8 @@ struct MelConfig {
 };
 
 constexpr int MEL_MAX_NFFT = 512;       // LDS sizing of the FFT kernel
-constexpr int MEL_FRAMES_PER_BLOCK = 16;
+constexpr int MEL_FRAMES_PER_BLOCK = 8;
+constexpr int MEL_FB_LDS = 2048;        // filterbank nonzeros staged in LDS (more: read from L2)
 
 class MelFront {
 public:
@@ -44,6 +45,9 @@ private:
     float* d_fb_ = nullptr;
     double* d_tw_ = nullptr;            // twiddles, [n_fft - 1][2]
     int* d_meta_ = nullptr;             // per clip {samples, frames}
+    void* d_span_ = nullptr;            // int4 [n_mels]: nonzero bins of each filter, packed offset
+    float* d_fbp_ = nullptr;            // packed nonzero filter values
+    int fb_nnz_ = 0;
     int meta_cap_ = 0;
     std::vector<int> meta_;
 };
