@@ -224,6 +224,22 @@ int pkx_mel_frames(const pkx_mel* m, int n_samples);
 int pkx_mel_forward(pkx_mel* m, const float* pcm_dev, int B, int64_t S_stride, const int* n_samples,
                     float* mel_dev, int T_max, int* T_out, void* stream);
 
+/* ---- weight quantisation ------------------------------------------------------
+ * ggml_quantize_chunk for q8_0 (gtype 8) and q4_K (gtype 12) on the device,
+ * the quantisers parakeet-cli quantize runs (examples/cli/main.cpp:322-426;
+ * ggml v0.13.0 quantize_row_q8_0_ref / quantize_row_q4_K_ref, same f32
+ * operations): src_dev [n_rows][n_per_row] f32 -> dst_dev n_rows rows of
+ * blocks (n_per_row % 32 for q8_0, % 256 for q4_K). */
+int pkx_quantize(int gtype, const float* src_dev, void* dst_dev, int64_t n_rows, int64_t n_per_row, void* stream);
+/* parakeet-cli quantize <in> <out> <type> (examples/cli/main.cpp:322-426):
+ * every KV pair copied verbatim; the allowlisted f32 2-D linears (main.cpp:
+ * 279-303) with ne0 divisible by the block quantised on the device, the other
+ * allowlisted 2-D f32 tensors kept (n_skipped), everything else copied.
+ * gtype: 8 (q8_0) or 12 (q4_K), the types this encoder runs.  Counts may be
+ * NULL. */
+int pkx_quantize_gguf(const char* in_path, const char* out_path, int gtype, int* n_quantized, int* n_kept,
+                      int* n_skipped);
+
 /* ---- profiling ----------------------------------------------------------------
  * No counterpart in the reference (its benchmarks time whole calls).
  * family_mask selects kernel families by bit (bit i = family i in the order

@@ -154,7 +154,161 @@ int orc_dequantize(int type, const void* src, float* dst, int64_t n) {
     return 2;
 }
 
-static int nearest_int(float v) { return (int)lrintf(v); }
+/* ggml's quantisers (ggml v0.13.0 ggml-quants.c, the published algorithms
+ * ggml_quantize_chunk runs for parakeet-cli quantize, examples/cli/main.cpp:
+ * 322-426).  Compiled without FMA contraction. */
+static int nearest_int(float fval) {
+    /* round to nearest, ties to even, via the 1.5 * 2^23 magic constant */
+    float val = fval + 12582912.f;
+    int i;
+    memcpy(&i, &val, sizeof(int));
+    return (i & 0x007fffff) - 0x00400000;
+}
+
+/* make_qkx2_quants: affine (scale, min) fit of n values to [0, nmax] by
+ * weighted least squares over nstep+1 candidate scales; returns the scale,
+ * *the_min = -min. */
+__attribute__((optimize("fp-contract=off")))
+static float make_qkx2_quants(int n, int nmax, const float* x, const float* weights, uint8_t* L,
+                              float* the_min, uint8_t* Laux, float rmin, float rdelta, int nstep) {
+    float min = x[0], max = x[0];
+    float sum_w = weights[0];
+    float sum_x = sum_w * x[0];
+    for (int i = 1; i < n; ++i) {
+        if (x[i] < min) min = x[i];
+        if (x[i] > max) max = x[i];
+        const float w = weights[i];
+        sum_w += w;
+        sum_x += w * x[i];
+    }
+    if (min > 0) min = 0;
+    if (max == min) {
+        for (int i = 0; i < n; ++i) L[i] = 0;
+        *the_min = -min;
+        return 0.f;
+    }
+    float iscale = nmax / (max - min);
+    float scale = 1 / iscale;
+    float best_mad = 0;
+    for (int i = 0; i < n; ++i) {
+        int l = nearest_int(iscale * (x[i] - min));
+        L[i] = (uint8_t)(l < 0 ? 0 : l > nmax ? nmax : l);
+        float diff = scale * L[i] + min - x[i];
+        diff = diff * diff;
+        best_mad += weights[i] * diff;
+    }
+    for (int is = 0; is <= nstep; ++is) {
+        iscale = (rmin + rdelta * is + nmax) / (max - min);
+        float sum_l = 0, sum_l2 = 0, sum_xl = 0;
+        for (int i = 0; i < n; ++i) {
+            int l = nearest_int(iscale * (x[i] - min));
+            l = l < 0 ? 0 : l > nmax ? nmax : l;
+            Laux[i] = (uint8_t)l;
+            const float w = weights[i];
+            sum_l += w * l;
+            sum_l2 += w * l * l;
+            sum_xl += w * l * x[i];
+        }
+        const float D = sum_w * sum_l2 - sum_l * sum_l;
+        if (D > 0) {
+            float this_scale = (sum_w * sum_xl - sum_x * sum_l) / D;
+            float this_min = (sum_l2 * sum_x - sum_l * sum_xl) / D;
+            if (this_min > 0) {
+                this_min = 0;
+                this_scale = sum_xl / sum_l2;
+            }
+            float mad = 0;
+            for (int i = 0; i < n; ++i) {
+                float diff = this_scale * Laux[i] + this_min - x[i];
+                diff = diff * diff;
+                mad += weights[i] * diff;
+            }
+            if (mad < best_mad) {
+                for (int i = 0; i < n; ++i) L[i] = Laux[i];
+                best_mad = mad;
+                scale = this_scale;
+                min = this_min;
+            }
+        }
+    }
+    *the_min = -min;
+    return scale;
+}
+
+static void get_scale_min_k4(int j, const uint8_t* q, uint8_t* d, uint8_t* m) {
+    if (j < 4) {
+        *d = q[j] & 63;
+        *m = q[j + 4] & 63;
+    } else {
+        *d = (uint8_t)((q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4));
+        *m = (uint8_t)((q[j + 4] >> 4) | ((q[j - 0] >> 6) << 4));
+    }
+}
+
+/* quantize_row_q4_K_ref for one 256-value super-block */
+__attribute__((optimize("fp-contract=off")))
+static void quantize_q4_k_block(const float* x, uint8_t* blk) {
+    uint8_t L[QK_K], Laux[32], sc[12];
+    float weights[32], mins[8], scales[8];
+    float max_scale = 0, max_min = 0;
+    for (int j = 0; j < 8; ++j) {
+        float sum_x2 = 0;
+        for (int l = 0; l < 32; ++l) sum_x2 += x[32 * j + l] * x[32 * j + l];
+        const float av_x = sqrtf(sum_x2 / 32);
+        for (int l = 0; l < 32; ++l) weights[l] = av_x + fabsf(x[32 * j + l]);
+        scales[j] = make_qkx2_quants(32, 15, x + 32 * j, weights, L + 32 * j, &mins[j], Laux, -1.f, 0.1f, 20);
+        if (scales[j] > max_scale) max_scale = scales[j];
+        if (mins[j] > max_min) max_min = mins[j];
+    }
+    const float inv_scale = max_scale > 0 ? 63.f / max_scale : 0.f;
+    const float inv_min = max_min > 0 ? 63.f / max_min : 0.f;
+    memset(sc, 0, sizeof sc);
+    for (int j = 0; j < 8; ++j) {
+        uint8_t ls = (uint8_t)nearest_int(inv_scale * scales[j]);
+        uint8_t lm = (uint8_t)nearest_int(inv_min * mins[j]);
+        ls = ls < 63 ? ls : 63;
+        lm = lm < 63 ? lm : 63;
+        if (j < 4) {
+            sc[j] = ls;
+            sc[j + 4] = lm;
+        } else {
+            sc[j + 4] = (uint8_t)((ls & 0xF) | ((lm & 0xF) << 4));
+            sc[j - 4] |= (uint8_t)((ls >> 4) << 6);
+            sc[j - 0] |= (uint8_t)((lm >> 4) << 6);
+        }
+    }
+    const uint16_t dh = orc_f32_to_f16(max_scale / 63.f), mh = orc_f32_to_f16(max_min / 63.f);
+    for (int j = 0; j < 8; ++j) {
+        uint8_t s, m;
+        get_scale_min_k4(j, sc, &s, &m);
+        const float d = orc_f16_to_f32(dh) * s;
+        if (!d) continue;
+        const float dm = orc_f16_to_f32(mh) * m;
+        for (int ii = 0; ii < 32; ++ii) {
+            int l = nearest_int((x[32 * j + ii] + dm) / d);
+            L[32 * j + ii] = (uint8_t)(l < 0 ? 0 : l > 15 ? 15 : l);
+        }
+    }
+    wr_u16(blk, dh);
+    wr_u16(blk + 2, mh);
+    memcpy(blk + 4, sc, 12);
+    uint8_t* q = blk + 16;
+    for (int j = 0; j < QK_K; j += 64) {
+        for (int l = 0; l < 32; ++l) q[l] = (uint8_t)(L[j + l] | (L[j + l + 32] << 4));
+        q += 32;
+    }
+}
+
+/* quantize_row_q8_0_ref */
+__attribute__((optimize("fp-contract=off")))
+static void quantize_q8_0_block(const float* v, uint8_t* blk) {
+    float amax = 0.f;
+    for (int j = 0; j < QK8_0; j++) amax = fmaxf(amax, fabsf(v[j]));
+    const float d = amax / ((1 << 7) - 1);
+    const float id = d ? 1.0f / d : 0.0f;
+    wr_u16(blk, orc_f32_to_f16(d));
+    for (int j = 0; j < QK8_0; ++j) blk[2 + j] = (uint8_t)(int8_t)roundf(v[j] * id);
+}
 
 int orc_quantize(int type, const float* x, void* dst, int64_t n) {
     uint8_t* o = (uint8_t*)dst;
@@ -165,66 +319,12 @@ int orc_quantize(int type, const float* x, void* dst, int64_t n) {
     }
     if (type == ORC_Q8_0) {
         if (n % QK8_0) return 1;
-        for (int64_t b = 0; b < n / QK8_0; ++b) {
-            const float* v = x + b * QK8_0;
-            uint8_t* blk = o + b * Q8_0_BYTES;
-            float amax = 0.f;
-            for (int j = 0; j < QK8_0; ++j) amax = fmaxf(amax, fabsf(v[j]));
-            float d = amax / 127.f, id = d != 0.f ? 1.f / d : 0.f;
-            wr_u16(blk, orc_f32_to_f16(d));
-            for (int j = 0; j < QK8_0; ++j) blk[2 + j] = (uint8_t)(int8_t)roundf(v[j] * id);
-        }
+        for (int64_t b = 0; b < n / QK8_0; ++b) quantize_q8_0_block(x + b * QK8_0, o + b * Q8_0_BYTES);
         return 0;
     }
     if (type == ORC_Q4_K) {
-        /* Simple min/max affine fit per 32-sub-block, then 6-bit scale/min
-         * codes against the super-block d/dmin (own quantiser). */
         if (n % QK_K) return 1;
-        for (int64_t b = 0; b < n / QK_K; ++b) {
-            const float* v = x + b * QK_K;
-            uint8_t* blk = o + b * Q4_K_BYTES;
-            float scale[8], minv[8], maxs = 0.f, maxm = 0.f;
-            for (int j = 0; j < 8; ++j) {
-                float lo = v[32 * j], hi = v[32 * j];
-                for (int l = 1; l < 32; ++l) { lo = fminf(lo, v[32 * j + l]); hi = fmaxf(hi, v[32 * j + l]); }
-                if (lo > 0.f) lo = 0.f;
-                scale[j] = (hi - lo) / 15.f;
-                minv[j] = -lo;
-                maxs = fmaxf(maxs, scale[j]);
-                maxm = fmaxf(maxm, minv[j]);
-            }
-            uint16_t dh = orc_f32_to_f16(maxs / 63.f), mh = orc_f32_to_f16(maxm / 63.f);
-            float d = orc_f16_to_f32(dh), dmin = orc_f16_to_f32(mh);
-            int sc[8], mn[8];
-            for (int j = 0; j < 8; ++j) {
-                sc[j] = d > 0.f ? nearest_int(scale[j] / d) : 0;
-                mn[j] = dmin > 0.f ? nearest_int(minv[j] / dmin) : 0;
-                if (sc[j] > 63) sc[j] = 63;
-                if (mn[j] > 63) mn[j] = 63;
-                if (sc[j] < 0) sc[j] = 0;
-                if (mn[j] < 0) mn[j] = 0;
-            }
-            wr_u16(blk, dh);
-            wr_u16(blk + 2, mh);
-            uint8_t* s = blk + 4;
-            for (int j = 0; j < 4; ++j) {
-                s[j] = (uint8_t)((sc[j] & 63) | ((sc[j + 4] >> 4) << 6));
-                s[j + 4] = (uint8_t)((mn[j] & 63) | ((mn[j + 4] >> 4) << 6));
-                s[j + 8] = (uint8_t)((sc[j + 4] & 0xF) | ((mn[j + 4] & 0xF) << 4));
-            }
-            uint8_t q[QK_K];
-            for (int j = 0; j < 8; ++j) {
-                float dj = d * (float)sc[j], mj = dmin * (float)mn[j];
-                for (int l = 0; l < 32; ++l) {
-                    int qi = dj > 0.f ? nearest_int((v[32 * j + l] + mj) / dj) : 0;
-                    q[32 * j + l] = (uint8_t)(qi < 0 ? 0 : qi > 15 ? 15 : qi);
-                }
-            }
-            uint8_t* qs = blk + 16;
-            for (int c = 0; c < 4; ++c)
-                for (int l = 0; l < 32; ++l)
-                    qs[32 * c + l] = (uint8_t)(q[64 * c + l] | (q[64 * c + 32 + l] << 4));
-        }
+        for (int64_t b = 0; b < n / QK_K; ++b) quantize_q4_k_block(x + b * QK_K, o + b * Q4_K_BYTES);
         return 0;
     }
     return 2;

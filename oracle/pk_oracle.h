@@ -45,8 +45,10 @@ int64_t  orc_row_bytes(int type, int64_t ne0);
  * q4_K: 144-byte super-block {f16 d; f16 dmin; u8 scales[12]; u8 qs[128]},
  *       w = d*sc_j*q - dmin*m_j (ggml v0.13.0 block_q4_K). Returns 0 on success. */
 int      orc_dequantize(int type, const void* src, float* dst, int64_t n);
-/* Quantise n f32 values into the given type (f16, q8_0, q4_K). Any valid
- * encoding is acceptable for q4_K (only dequantisation must match ggml). */
+/* Quantise n f32 values into the given type (f16, q8_0, q4_K): ggml's
+ * quantize_row_q8_0_ref (d = f16(amax/127), q = roundf(x / (amax/127))) and
+ * quantize_row_q4_K_ref (make_qkx2_quants per 32-value sub-block, 6-bit
+ * scale/min codes against d = max_scale/63, dmin = max_min/63). */
 int      orc_quantize(int type, const float* src, void* dst, int64_t n);
 
 /* pos_enc.cpp:10-34 -- table [2T-1][d] for positions +(T-1) .. -(T-1). */

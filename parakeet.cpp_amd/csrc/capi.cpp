@@ -7,6 +7,7 @@
 #include "../../include/pkx.h"
 #include "mel.hpp"
 #include "model.hpp"
+#include "quantize.hpp"
 
 struct pkx_mel {
     std::unique_ptr<pkx::MelFront> impl;
@@ -384,6 +385,23 @@ int pkx_mel_forward(pkx_mel* m, const float* pcm, int B, int64_t S_stride, const
     return guarded([&] {
         need(m != nullptr, "null mel handle");
         m->impl->forward(pcm, B, S_stride, n_samples, mel, T_max, T_out, st(s));
+    });
+}
+
+int pkx_quantize(int gtype, const float* src, void* dst, int64_t n_rows, int64_t n_per_row, void* s) {
+    return guarded([&] {
+        need(src && dst, "null buffer");
+        pkx::quantize_rows(gtype, src, dst, n_rows, n_per_row, st(s));
+    });
+}
+int pkx_quantize_gguf(const char* in_path, const char* out_path, int gtype, int* n_quantized, int* n_kept,
+                      int* n_skipped) {
+    return guarded([&] {
+        need(in_path && out_path, "null path");
+        const pkx::QuantizeCounts c = pkx::quantize_gguf(in_path, out_path, gtype);
+        if (n_quantized) *n_quantized = c.quantized;
+        if (n_kept) *n_kept = c.kept;
+        if (n_skipped) *n_skipped = c.skipped;
     });
 }
 

@@ -2,6 +2,7 @@
 // src/model_loader.cpp:99-167): parakeet.* KV -> ModelConfig, verbatim NeMo
 // tensor names -> Model::set_tensor.  Only the tensors the encoder, the CTC
 // head and the TDT joint use are read; the file is streamed tensor by tensor.
+#include <algorithm>
 #include <cstdio>
 #include <cstring>
 #include <map>
@@ -11,6 +12,7 @@
 
 #include "mel.hpp"
 #include "model.hpp"
+#include "quantize.hpp"
 
 namespace pkx {
 namespace {
@@ -139,6 +141,8 @@ struct Header {
     std::map<std::string, KvVal> kv;
     std::vector<TensorInfo> infos;
     uint64_t data0 = 0;
+    uint64_t kv_begin = 0, kv_end = 0, n_kv = 0;   // byte range of the KV section
+    uint64_t align = 32;
 };
 
 Header read_header(File& f, const std::string& path) {
@@ -148,11 +152,14 @@ Header read_header(File& f, const std::string& path) {
     const uint64_t n_tensors = f.get<uint64_t>();
     const uint64_t n_kv = f.get<uint64_t>();
     Header h;
+    h.n_kv = n_kv;
+    h.kv_begin = f.tell();
     for (uint64_t i = 0; i < n_kv; ++i) {
         std::string key = f.str();
         const uint32_t t = f.get<uint32_t>();
         h.kv[key] = read_val(f, t);
     }
+    h.kv_end = f.tell();
     h.infos.resize((size_t)n_tensors);
     for (auto& ti : h.infos) {
         ti.name = f.str();
@@ -164,6 +171,8 @@ Header read_header(File& f, const std::string& path) {
     }
     uint64_t align = 32;
     if (h.kv.count("general.alignment")) align = (uint64_t)h.kv["general.alignment"].i;
+    require(align > 0 && (align & (align - 1)) == 0, "GGUF: general.alignment must be a power of two");
+    h.align = align;
     h.data0 = (f.tell() + align - 1) / align * align;
     return h;
 }
@@ -275,6 +284,156 @@ std::unique_ptr<Model> load_gguf(const std::string& path, int precision) {
     }
     m->finalize();
     return m;
+}
+
+}  // namespace pkx
+
+namespace pkx {
+
+bool is_quantizable_name(const std::string& n) {
+    // examples/cli/main.cpp:279-303
+    if (n == "encoder.pre_encode.out.weight" || n == "joint.enc.weight" || n == "joint.pred.weight") return true;
+    const std::string prefix = "encoder.layers.";
+    if (n.compare(0, prefix.size(), prefix) != 0) return false;
+    size_t i = prefix.size();
+    const size_t start = i;
+    while (i < n.size() && n[i] >= '0' && n[i] <= '9') ++i;
+    if (i == start || i >= n.size() || n[i] != '.') return false;
+    const std::string rest = n.substr(i + 1);
+    for (const char* r : {"feed_forward1.linear1.weight", "feed_forward1.linear2.weight",
+                          "feed_forward2.linear1.weight", "feed_forward2.linear2.weight",
+                          "self_attn.linear_q.weight", "self_attn.linear_k.weight", "self_attn.linear_v.weight",
+                          "self_attn.linear_out.weight", "self_attn.linear_pos.weight"})
+        if (rest == r) return true;
+    return false;
+}
+
+namespace {
+struct Out {
+    FILE* f = nullptr;
+    std::string path;
+    explicit Out(const std::string& p) : f(std::fopen(p.c_str(), "wb")), path(p) {
+        require(f != nullptr, "cannot create " + p);
+    }
+    ~Out() { if (f) std::fclose(f); }
+    void write(const void* p, size_t n) { require(std::fwrite(p, 1, n, f) == n, "write failed: " + path); }
+    template <typename T> void put(T v) { write(&v, sizeof v); }
+    void str(const std::string& s) { put<uint64_t>(s.size()); write(s.data(), s.size()); }
+    void pad_to(uint64_t align) {
+        const long pos = std::ftell(f);
+        const uint64_t padn = ((uint64_t)pos + align - 1) / align * align - (uint64_t)pos;
+        static const char zeros[256] = {};
+        for (uint64_t k = 0; k < padn; k += 256) write(zeros, (size_t)std::min<uint64_t>(256, padn - k));
+    }
+};
+}  // namespace
+
+QuantizeCounts quantize_gguf(const std::string& in_path, const std::string& out_path, int gtype) {
+    require(gtype == GT_Q8_0 || gtype == GT_Q4_K, "quantize: type must be q8_0 or q4_K");
+    require(in_path != out_path, "quantize: output must differ from input");
+    const int64_t block = gtype == GT_Q8_0 ? 32 : 256, bbytes = gtype == GT_Q8_0 ? 34 : 144;
+    File f(in_path);
+    Header h = read_header(f, in_path);
+    struct Plan {
+        TensorInfo out;
+        bool quant = false;
+        int64_t src_bytes = 0, dst_bytes = 0;
+    };
+    QuantizeCounts cnt;
+    std::vector<Plan> plan(h.infos.size());
+    uint64_t off = 0;
+    for (size_t i = 0; i < h.infos.size(); ++i) {
+        const TensorInfo& ti = h.infos[i];
+        Plan& p = plan[i];
+        p.out = ti;
+        p.src_bytes = tensor_bytes(ti);
+        require(p.src_bytes >= 0, "GGUF: unsupported type " + std::to_string(ti.gtype) + " for tensor " + ti.name);
+        if (is_quantizable_name(ti.name) && ti.gtype == GT_F32) {
+            const bool two_d = ti.ne[2] == 1 && ti.ne[3] == 1 && ti.ne[0] >= 32 && ti.ne[1] >= 32;
+            if (two_d && ti.ne[0] % block == 0) p.quant = true;
+            else if (two_d) ++cnt.skipped;
+        }
+        if (p.quant) {
+            p.out.gtype = gtype;
+            p.out.n_dims = 2;
+            p.dst_bytes = ti.ne[0] / block * bbytes * ti.ne[1];
+            ++cnt.quantized;
+        } else {
+            p.dst_bytes = p.src_bytes;
+            ++cnt.kept;
+        }
+        p.out.offset = off;
+        off = (off + (uint64_t)p.dst_bytes + h.align - 1) / h.align * h.align;
+    }
+    Out o(out_path);
+    o.put<uint32_t>(0x46554747u);
+    o.put<uint32_t>(3);
+    o.put<uint64_t>(h.infos.size());
+    o.put<uint64_t>(h.n_kv);
+    {   // every KV pair verbatim
+        std::vector<uint8_t> kvb((size_t)(h.kv_end - h.kv_begin));
+        f.seek(h.kv_begin);
+        if (!kvb.empty()) f.read(kvb.data(), kvb.size());
+        if (!kvb.empty()) o.write(kvb.data(), kvb.size());
+    }
+    for (const Plan& p : plan) {
+        o.str(p.out.name);
+        o.put<uint32_t>((uint32_t)p.out.n_dims);
+        for (int d = 0; d < p.out.n_dims; ++d) o.put<uint64_t>((uint64_t)p.out.ne[d]);
+        o.put<uint32_t>((uint32_t)p.out.gtype);
+        o.put<uint64_t>(p.out.offset);
+    }
+    o.pad_to(h.align);
+    const long data_start = std::ftell(o.f);
+    hipStream_t s = nullptr;
+    PKX_HIP(hipStreamCreate(&s));
+    void *dsrc = nullptr, *ddst = nullptr;
+    size_t cap_src = 0, cap_dst = 0;
+    std::vector<uint8_t> buf, qbuf;
+    try {
+        for (size_t i = 0; i < plan.size(); ++i) {
+            const Plan& p = plan[i];
+            const uint64_t pos = (uint64_t)(std::ftell(o.f) - data_start);
+            require(pos <= p.out.offset, "quantize: layout error");
+            static const char zeros[256] = {};
+            for (uint64_t k = pos; k < p.out.offset; k += 256)
+                o.write(zeros, (size_t)std::min<uint64_t>(256, p.out.offset - k));
+            buf.resize((size_t)p.src_bytes);
+            f.seek(h.data0 + h.infos[i].offset);
+            if (!buf.empty()) f.read(buf.data(), buf.size());
+            if (!p.quant) {
+                if (!buf.empty()) o.write(buf.data(), buf.size());
+                continue;
+            }
+            if ((size_t)p.src_bytes > cap_src) {
+                if (dsrc) PKX_HIP(hipFree(dsrc));
+                dsrc = nullptr;
+                PKX_HIP(hipMalloc(&dsrc, (size_t)p.src_bytes));
+                cap_src = (size_t)p.src_bytes;
+            }
+            if ((size_t)p.dst_bytes > cap_dst) {
+                if (ddst) PKX_HIP(hipFree(ddst));
+                ddst = nullptr;
+                PKX_HIP(hipMalloc(&ddst, (size_t)p.dst_bytes));
+                cap_dst = (size_t)p.dst_bytes;
+            }
+            PKX_HIP(hipMemcpyAsync(dsrc, buf.data(), (size_t)p.src_bytes, hipMemcpyHostToDevice, s));
+            quantize_rows(gtype, (const float*)dsrc, ddst, h.infos[i].ne[1], h.infos[i].ne[0], s);
+            qbuf.resize((size_t)p.dst_bytes);
+            PKX_HIP(hipMemcpyAsync(qbuf.data(), ddst, (size_t)p.dst_bytes, hipMemcpyDeviceToHost, s));
+            PKX_HIP(hipStreamSynchronize(s));
+            o.write(qbuf.data(), qbuf.size());
+        }
+    } catch (...) {
+        if (dsrc) (void)hipFree(dsrc);
+        if (ddst) (void)hipFree(ddst);
+        (void)hipStreamDestroy(s);
+        throw;
+    }
+    if (dsrc) PKX_HIP(hipFree(dsrc));
+    if (ddst) PKX_HIP(hipFree(ddst));
+    PKX_HIP(hipStreamDestroy(s));
+    return cnt;
 }
 
 }  // namespace pkx

@@ -88,6 +88,8 @@ SIGS = {
     "pkx_mel_info": ([_vp, C.POINTER(MelConfig)], C.c_int),
     "pkx_mel_frames": ([_vp, C.c_int], C.c_int),
     "pkx_mel_forward": ([_vp, _vp, C.c_int, C.c_int64, _ip, _vp, C.c_int, _ip, _vp], C.c_int),
+    "pkx_quantize": ([C.c_int, _vp, _vp, C.c_int64, C.c_int64, _vp], C.c_int),
+    "pkx_quantize_gguf": ([C.c_char_p, C.c_char_p, C.c_int, _ip, _ip, _ip], C.c_int),
     "pkx_model_set_profiling": ([_vp, C.c_uint, C.c_int], C.c_int),
     "pkx_model_profile_read": ([_vp, C.POINTER(C.c_double), C.POINTER(C.c_int64)], C.c_int),
 }
@@ -410,3 +412,17 @@ class Mel:
             self.close()
         except Exception:
             pass
+
+
+def quantize(gtype, src: DeviceArray, dst: DeviceArray, n_rows, n_per_row, stream=None):
+    """ggml_quantize_chunk on the device: src [n_rows][n_per_row] f32 -> dst (raw blocks)."""
+    check(lib().pkx_quantize(int(gtype), src.ptr, dst.ptr, int(n_rows), int(n_per_row), _sh(stream)))
+
+
+def quantize_gguf(in_path, out_path, qtype: str):
+    """parakeet-cli quantize: returns (quantized, kept, skipped) tensor counts."""
+    gt = {"q8_0": 8, "q4_k": 12}[qtype.lower()]
+    nq, nk, ns = C.c_int(), C.c_int(), C.c_int()
+    check(lib().pkx_quantize_gguf(str(in_path).encode(), str(out_path).encode(), gt, C.byref(nq), C.byref(nk),
+                                  C.byref(ns)))
+    return nq.value, nk.value, ns.value
