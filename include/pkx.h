@@ -191,6 +191,20 @@ int pkx_layernorm(const float* x_dev, const float* g_dev, const float* b_dev, fl
 /* pk::rel_pos_encoding (src/pos_enc.cpp:10-34): out_dev [2T-1][D] f32. */
 int pkx_rel_pos_encoding(int T, int D, float* out_dev, void* stream);
 
+/* ---- greedy transducer decode ---------------------------------------------------
+ * transducer_greedy_batch (src/transducer_batch.cpp:24-213): the batched greedy
+ * TDT (n_durations > 0, frame advance = durations[argmax of the duration
+ * logits]) or RNNT (n_durations = 0) decode over the model's prediction
+ * network (src/prediction.cpp) and joint (src/joint.cpp), on the device.
+ * enc_dev [B][T_max][d_model] f32 (the encoder output, time-major), T_valid
+ * (host) frames per item.  Outputs (host, [B][cap] each, NULL to skip): token
+ * ids, NeMo frame / max_prob confidence / span per token (src/decode_types.hpp);
+ * counts (host) [B] tokens per item.  A decode needing more than cap tokens
+ * for an item is an error. */
+int pkx_transducer_greedy(pkx_model* m, const float* enc_dev, int B, int T_max, const int* T_valid,
+                          const int32_t* durations, int n_durations, int blank_id, int max_symbols, int cap,
+                          int32_t* ids, int32_t* frames, float* conf, int32_t* span, int* counts, void* stream);
+
 /* ---- log-mel front end --------------------------------------------------------
  * pk::MelFrontend::compute (src/mel.hpp:33-41, src/mel.cpp:99-185) for a batch
  * of 16 kHz mono clips, stacked to T_max as build_mel_batch does

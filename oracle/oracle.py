@@ -55,6 +55,9 @@ def lib():
         L.orc_ctc_greedy.argtypes = [_i32, C.c_int, C.c_int, _i32]
         L.orc_tdt_joint_argmax.argtypes = [_f, C.c_int, C.c_int, _f, _f, C.c_int, _f, C.c_int,
                                            _f, _f, _f, _f, C.c_int, C.c_int, _f, _i32, _i32]
+        L.orc_lstm_step.argtypes = [C.c_void_p, C.c_int32, C.c_int, _f, _f, _f, _f, _f]
+        L.orc_transducer_greedy.argtypes = [C.c_void_p, _f, C.c_int, _i32, C.c_int, C.c_int, C.c_int, _i32,
+                                            _i32, _f, _i32, C.c_int]
         L.orc_mel_window.argtypes = [_f, C.c_int, C.c_int, _f]
         L.orc_mel_frames.argtypes = [C.c_void_p, C.c_int]
         L.orc_rfft.argtypes = [_f, C.c_int, _f, _f]
@@ -367,3 +370,76 @@ def mel_batch(cfg: MelCfg, window: np.ndarray, fb: np.ndarray, pcm: np.ndarray, 
                         fp(np.ascontiguousarray(fb, np.float32)), fp(pcm), B, S_stride, ip(ns), T_max,
                         fp(out), T_out.ctypes.data_as(_i))
     return out, T_out
+
+
+# ---- greedy transducer decode (prediction.cpp, joint.cpp, tdt.cpp) ------------
+
+class TransducerW(C.Structure):
+    _fields_ = [("H", C.c_int), ("L", C.c_int), ("V1", C.c_int), ("embed", _f),
+                ("w_ih", _f * 4), ("w_hh", _f * 4), ("b_ih", _f * 4), ("b_hh", _f * 4),
+                ("Hj", C.c_int), ("D", C.c_int), ("Vp", C.c_int),
+                ("jenc_w", _f), ("jenc_b", _f), ("jpred_w", _f), ("jpred_b", _f), ("jout_w", _f), ("jout_b", _f)]
+
+
+class Transducer:
+    """Prediction net + joint of a pk_model.Model (dequantised to f32)."""
+
+    def __init__(self, model):
+        c = model.cfg
+        t = model.tensors
+
+        def f32(name):
+            tt = t[name]
+            if tt.gtype == 0:
+                return np.ascontiguousarray(tt.data, dtype=np.float32).reshape(-1)
+            n = int(np.prod(tt.shape))
+            out = np.zeros(n, np.float32)
+            assert lib().orc_dequantize(tt.gtype, np.ascontiguousarray(tt.data).ctypes.data, fp(out), n) == 0
+            return out
+
+        self._keep = []
+
+        def keep(a):
+            self._keep.append(a)
+            return fp(a)
+
+        w = TransducerW()
+        w.H, w.L, w.V1 = c.pred_hidden, c.pred_rnn_layers, c.vocab_size + 1
+        w.embed = keep(f32("decoder.prediction.embed.weight"))
+        for l in range(c.pred_rnn_layers):
+            s = "decoder.prediction.dec_rnn.lstm.%s_l" + str(l)
+            w.w_ih[l] = keep(f32(s % "weight_ih"))
+            w.w_hh[l] = keep(f32(s % "weight_hh"))
+            w.b_ih[l] = keep(f32(s % "bias_ih"))
+            w.b_hh[l] = keep(f32(s % "bias_hh"))
+        w.Hj, w.D = c.joint_hidden, c.d_model
+        w.Vp = c.vocab_size + 1 + len(c.tdt_durations)
+        w.jenc_w, w.jenc_b = keep(f32("joint.enc.weight")), keep(f32("joint.enc.bias"))
+        w.jpred_w, w.jpred_b = keep(f32("joint.pred.weight")), keep(f32("joint.pred.bias"))
+        w.jout_w, w.jout_b = keep(f32("joint.joint_net.2.weight")), keep(f32("joint.joint_net.2.bias"))
+        self.w = w
+        self.cfg = c
+
+    def lstm_step(self, token, is_sos, h, c):
+        H, L = self.w.H, self.w.L
+        h = np.ascontiguousarray(h, np.float32).reshape(L, H)
+        c = np.ascontiguousarray(c, np.float32).reshape(L, H)
+        ho, co, g = np.zeros((L, H), np.float32), np.zeros((L, H), np.float32), np.zeros(H, np.float32)
+        lib().orc_lstm_step(C.byref(self.w), int(token), int(bool(is_sos)), fp(h), fp(c), fp(ho), fp(co), fp(g))
+        return g, ho, co
+
+    def greedy(self, enc, durations=None, blank_id=None, max_symbols=10):
+        """enc [T][D] -> (ids, frames, conf, span); durations None/() = RNNT (then the joint's
+        output has no duration logits: build the model with tdt_durations=())."""
+        enc = np.ascontiguousarray(enc, np.float32)
+        T = enc.shape[0]
+        durations = np.ascontiguousarray([] if durations is None else durations, np.int32)
+        blank = self.cfg.vocab_size if blank_id is None else blank_id
+        cap = max(1, T * max_symbols)
+        ids, fr, sp = (np.zeros(cap, np.int32) for _ in range(3))
+        cf = np.zeros(cap, np.float32)
+        n = lib().orc_transducer_greedy(C.byref(self.w), fp(enc), T, durations.ctypes.data_as(_i32),
+                                        len(durations), blank, max_symbols, ids.ctypes.data_as(_i32),
+                                        fr.ctypes.data_as(_i32), fp(cf), sp.ctypes.data_as(_i32), cap)
+        assert n >= 0
+        return ids[:n].copy(), fr[:n].copy(), cf[:n].copy(), sp[:n].copy()

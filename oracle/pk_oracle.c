@@ -777,6 +777,123 @@ void orc_tdt_joint_argmax(const float* enc, int T, int D, const float* Wenc,
 }
 
 /* ------------------------------------------------------------------------ */
+/* Greedy transducer decode: prediction.cpp, joint.cpp, tdt.cpp,            */
+/* transducer_batch.cpp, decode_common.hpp                                   */
+/* ------------------------------------------------------------------------ */
+
+static float orc_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }   /* ggml_sigmoid */
+
+void orc_lstm_step(const orc_transducer* m, int32_t token, int is_sos, const float* h_in, const float* c_in,
+                   float* h_out, float* c_out, float* g_out) {
+    const int H = m->H;
+    float* x = fbuf((size_t)H);
+    float* za = fbuf((size_t)4 * H);
+    float* zb = fbuf((size_t)4 * H);
+    for (int j = 0; j < H; ++j) x[j] = is_sos ? 0.0f : m->embed[(size_t)token * H + j];
+    for (int l = 0; l < m->L; ++l) {
+        orc_linear(x, 1, H, m->w_ih[l], 4 * H, m->b_ih[l], za);            /* W_ih x + b_ih */
+        orc_linear(h_in + (size_t)l * H, 1, H, m->w_hh[l], 4 * H, m->b_hh[l], zb);   /* W_hh h + b_hh */
+        for (int j = 0; j < H; ++j) {
+            const float zi = za[j] + zb[j], zf = za[H + j] + zb[H + j];
+            const float zg = za[2 * H + j] + zb[2 * H + j], zo = za[3 * H + j] + zb[3 * H + j];
+            const float c = orc_sigmoid(zf) * c_in[(size_t)l * H + j] + orc_sigmoid(zi) * tanhf(zg);
+            c_out[(size_t)l * H + j] = c;
+            h_out[(size_t)l * H + j] = orc_sigmoid(zo) * tanhf(c);
+        }
+        for (int j = 0; j < H; ++j) x[j] = h_out[(size_t)l * H + j];
+    }
+    memcpy(g_out, h_out + (size_t)(m->L - 1) * H, sizeof(float) * (size_t)H);
+    free(x); free(za); free(zb);
+}
+
+static int orc_argmax_first(const float* a, int n) {         /* decode_common.hpp:5-9 */
+    int best = 0;
+    float bv = a[0];
+    for (int i = 1; i < n; ++i) if (a[i] > bv) { bv = a[i]; best = i; }
+    return best;
+}
+
+static float orc_max_prob_conf(const float* a, int n, int k) {   /* decode_common.hpp:12-20 */
+    float mx = a[0];
+    for (int i = 1; i < n; ++i) if (a[i] > mx) mx = a[i];
+    double den = 0.0;
+    for (int i = 0; i < n; ++i) den += exp((double)a[i] - (double)mx);
+    const double p = exp((double)a[k] - (double)mx) / den, N = (double)n;
+    return (float)((N * p - 1.0) / (N - 1.0));
+}
+
+int orc_transducer_greedy(const orc_transducer* m, const float* enc, int T, const int32_t* durations, int n_dur,
+                          int blank_id, int max_symbols, int32_t* ids, int32_t* frames, float* conf,
+                          int32_t* span, int cap) {
+    const int H = m->H, L = m->L, Hj = m->Hj, Vp = m->Vp;
+    const int tc = n_dur > 0 ? Vp - n_dur : Vp;
+    float* ep = fbuf((size_t)(T > 0 ? T : 1) * Hj);
+    if (T > 0) orc_linear(enc, T, m->D, m->jenc_w, Hj, m->jenc_b, ep);       /* joint.cpp:37-63 */
+    float *ch = fbuf((size_t)L * H), *cc = fbuf((size_t)L * H);              /* committed state */
+    float *oh = fbuf((size_t)L * H), *oc = fbuf((size_t)L * H);              /* step output */
+    float *g = fbuf((size_t)H), *pp = fbuf((size_t)Hj), *f = fbuf((size_t)Hj), *lg = fbuf((size_t)Vp);
+    memset(ch, 0, sizeof(float) * (size_t)L * H);
+    memset(cc, 0, sizeof(float) * (size_t)L * H);
+    int n = 0, t = 0, emitted_any = 0, g_valid = 0, overflow = 0;
+    int32_t last = blank_id;
+#define ORC_JOINT()                                                            \
+    do {                                                                       \
+        orc_linear(g, 1, H, m->jpred_w, Hj, m->jpred_b, pp);                   \
+        for (int h = 0; h < Hj; ++h) {                                         \
+            const float s = ep[(size_t)t * Hj + h] + pp[h];                    \
+            f[h] = s > 0.f ? s : 0.f;                                          \
+        }                                                                      \
+        orc_linear(f, 1, Hj, m->jout_w, Vp, m->jout_b, lg);                    \
+    } while (0)
+#define ORC_EMIT(K, SPAN)                                                      \
+    do {                                                                       \
+        if (n >= cap) { overflow = 1; break; }                                 \
+        ids[n] = (K); frames[n] = t; conf[n] = orc_max_prob_conf(lg, tc, (K)); \
+        span[n] = (SPAN); ++n;                                                 \
+        last = (K); emitted_any = 1; g_valid = 0;                              \
+        memcpy(ch, oh, sizeof(float) * (size_t)L * H);                         \
+        memcpy(cc, oc, sizeof(float) * (size_t)L * H);                         \
+    } while (0)
+    while (t < T && !overflow) {
+        if (n_dur > 0) {                                        /* tdt.cpp:40-112 */
+            int symbols = 0, need_loop = 1;
+            while (need_loop && symbols < max_symbols && !overflow) {
+                if (!g_valid) {
+                    orc_lstm_step(m, last, !emitted_any, ch, cc, oh, oc, g);
+                    g_valid = 1;
+                }
+                ORC_JOINT();
+                const int k = orc_argmax_first(lg, tc), dk = orc_argmax_first(lg + tc, n_dur);
+                const int skip = durations[dk];
+                if (k != blank_id) ORC_EMIT(k, skip);
+                symbols += 1;
+                t += skip;
+                need_loop = skip == 0;
+            }
+            if (symbols == max_symbols) t += 1;
+        } else {                                                /* RNNT: advance-by-1 */
+            int symbols = 0;
+            for (;;) {
+                if (!g_valid) {
+                    orc_lstm_step(m, last, !emitted_any, ch, cc, oh, oc, g);
+                    g_valid = 1;
+                }
+                ORC_JOINT();
+                const int k = orc_argmax_first(lg, Vp);
+                if (k == blank_id) { t += 1; break; }
+                ORC_EMIT(k, 1);
+                if (overflow) break;
+                if (++symbols >= max_symbols) { t += 1; break; }
+            }
+        }
+    }
+#undef ORC_JOINT
+#undef ORC_EMIT
+    free(ep); free(ch); free(cc); free(oh); free(oc); free(g); free(pp); free(f); free(lg);
+    return overflow ? -1 : n;
+}
+
+/* ------------------------------------------------------------------------ */
 /* Log-mel front end: mel.cpp, fft.cpp, model.cpp:114-146                   */
 /* The reference's CPU build has no FMA contraction (baseline x86-64), so    */
 /* these functions are compiled without it as well.                          */

@@ -139,6 +139,32 @@ void orc_tdt_joint_argmax(const float* enc, int T, int D, const float* Wenc,
                           const float* Wout, const float* bout, int n_tok,
                           int n_dur, float* logits, int32_t* tok, int32_t* dur);
 
+/* ---- greedy transducer decode (prediction.cpp, joint.cpp, tdt.cpp,
+ *      transducer_batch.cpp, decode_common.hpp) ------------------------------ */
+typedef struct {
+    int H, L, V1;                     /* pred_hidden, LSTM layers (<= 4), embedding rows (vocab+1) */
+    const float* embed;               /* [V1][H] */
+    const float *w_ih[4], *w_hh[4];   /* [4H][H] per layer, gates (i, f, g, o) */
+    const float *b_ih[4], *b_hh[4];   /* [4H] */
+    int Hj, D, Vp;                    /* joint hidden, encoder width, vocab + 1 + n_durations */
+    const float *jenc_w, *jenc_b;     /* [Hj][D], [Hj] */
+    const float *jpred_w, *jpred_b;   /* [Hj][H], [Hj] */
+    const float *jout_w, *jout_b;     /* [Vp][Hj], [Vp] */
+} orc_transducer;
+
+/* prediction.cpp:47-109 -- one stacked-LSTM step: x = embed[token] (zeros
+ * for SOS), per layer z = (W_ih x + b_ih) + (W_hh h + b_hh),
+ * c' = sigmoid(f) c + sigmoid(i) tanh(g), h' = sigmoid(o) tanh(c').
+ * h_in/c_in/h_out/c_out [L][H]; g_out = top-layer h'. */
+void orc_lstm_step(const orc_transducer* m, int32_t token, int is_sos, const float* h_in, const float* c_in,
+                   float* h_out, float* c_out, float* g_out);
+/* tdt.cpp:8-118 (n_dur > 0) / rnnt greedy (n_dur == 0) for one item, enc
+ * [T][D]: emitted ids with NeMo's per-token frame, max_prob confidence and
+ * span (decode_types.hpp).  Returns the count, -1 if cap is exceeded. */
+int orc_transducer_greedy(const orc_transducer* m, const float* enc, int T, const int32_t* durations, int n_dur,
+                          int blank_id, int max_symbols, int32_t* ids, int32_t* frames, float* conf,
+                          int32_t* span, int cap);
+
 /* ---- log-mel front end (mel.cpp, fft.cpp, model.cpp:114-146) ------------ */
 typedef struct {
     int n_fft, hop, n_mels, per_feature;   /* per_feature: normalize == "per_feature" */

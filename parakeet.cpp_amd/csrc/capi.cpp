@@ -331,6 +331,15 @@ int pkx_model_profile_read(pkx_model* m, double* ms, int64_t* launches) {
     });
 }
 
+int pkx_transducer_greedy(pkx_model* m, const float* enc, int B, int T_max, const int* T_valid,
+                          const int32_t* durations, int n_durations, int blank_id, int max_symbols, int cap,
+                          int32_t* ids, int32_t* frames, float* conf, int32_t* span, int* counts, void* s) {
+    return guarded([&] {
+        need(m && enc, "null argument");
+        m->impl->transducer_greedy(enc, B, T_max, T_valid, durations, n_durations, blank_id, max_symbols, cap, ids,
+                                   frames, conf, span, counts, st(s));
+    });
+}
 int pkx_mel_create(const pkx_mel_config* cfg, const float* window, int window_len, const float* fb,
                    pkx_mel** out) {
     return guarded([&] {

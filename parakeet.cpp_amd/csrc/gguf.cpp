@@ -134,6 +134,7 @@ int64_t tensor_bytes(const TensorInfo& t) {
 bool wanted(const std::string& n) {
     auto starts = [&](const char* p) { return n.compare(0, std::strlen(p), p) == 0; };
     return starts("encoder.") || starts("ctc_decoder.") || starts("decoder.decoder_layers.") ||
+           starts("decoder.prediction.") ||
            starts("joint.enc.") || starts("joint.pred.") || starts("joint.joint_net.2.");
 }
 

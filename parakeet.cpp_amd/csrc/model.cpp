@@ -550,6 +550,45 @@ void Model::finalize() {
             heads_.n_dur = c.n_durations;
             heads_.n_tok = V - c.n_durations;
             require(heads_.n_tok > 0, "joint: vocab/durations mismatch");
+            // prediction network (prediction.cpp): layers counted from the tensors
+            const HostTensor* emb = find("decoder.prediction.embed.weight");
+            if (emb) {
+                const std::string pre = "decoder.prediction.dec_rnn.lstm.";
+                int L = 0;
+                while (L < 4 && find(pre + "weight_ih_l" + std::to_string(L))) ++L;
+                require(L >= 1, "prediction net: no LSTM layers");
+                require(!find(pre + "weight_ih_l4"), "prediction net: at most 4 LSTM layers");
+                pred_.H = P;
+                pred_.V1 = (int)(emb->nelem() / P);
+                require(pred_.V1 * (int64_t)P == emb->nelem(), "prediction net: embedding width != pred_hidden");
+                pred_.embed = upload_f32(*emb);
+                for (int l = 0; l < L; ++l) {
+                    const std::string s = std::to_string(l);
+                    const std::vector<float> wih = to_f32(need(pre + "weight_ih_l" + s));
+                    const std::vector<float> whh = to_f32(need(pre + "weight_hh_l" + s));
+                    const std::vector<float> bih = to_f32(need(pre + "bias_ih_l" + s));
+                    const std::vector<float> bhh = to_f32(need(pre + "bias_hh_l" + s));
+                    require(wih.size() == (size_t)4 * P * P && whh.size() == wih.size() && bih.size() == (size_t)4 * P &&
+                                bhh.size() == bih.size(),
+                            "prediction net: layer " + s + " must be [4H][H] with [4H] biases");
+                    HostTensor cat;
+                    cat.gtype = GT_F32;
+                    cat.n_dims = 2;
+                    cat.ne[0] = 2 * P;
+                    cat.ne[1] = 4 * P;
+                    cat.bytes.resize((size_t)8 * P * 2 * P * 4);
+                    float* cw = (float*)cat.bytes.data();
+                    for (int r = 0; r < 4 * P; ++r) {
+                        std::memcpy(cw + (size_t)r * 2 * P, wih.data() + (size_t)r * P, sizeof(float) * P);
+                        std::memcpy(cw + (size_t)r * 2 * P + P, whh.data() + (size_t)r * P, sizeof(float) * P);
+                    }
+                    pred_.wcat[l] = make_weight(cat, 4 * P, 2 * P, false);
+                    std::vector<float> bs((size_t)4 * P);
+                    for (size_t i = 0; i < bs.size(); ++i) bs[i] = bih[i] + bhh[i];
+                    pred_.bsum[l] = upload_f32(bs);
+                }
+                pred_.L = L;
+            }
         }
     }
     // LayerNorm folding (f16 path): every product involved must take the LDS-DMA

@@ -81,6 +81,17 @@ struct HeadsDev {
     int n_tok = 0, n_dur = 0;
 };
 
+// RNNT/TDT prediction network on the device (prediction.hpp:27-50): the
+// stacked LSTM with each layer's [W_ih | W_hh] concatenated along K, so one
+// f32 product gives z = W_ih x + W_hh h; biases summed.
+struct PredDev {
+    int H = 0, L = 0, V1 = 0;
+    float* embed = nullptr;            // [V1][H]
+    DevWeight wcat[4];                 // [4H][2H]
+    float* bsum[4] = {};               // b_ih + b_hh, [4H]
+    bool ok() const { return L > 0; }
+};
+
 // Per-kernel-family timing collected when profiling is enabled.
 enum KFam : int {
     KF_SUBSAMPLING = 0, KF_LAYERNORM, KF_GEMM_FFN, KF_GEMM_QKV, KF_GEMM_POS, KF_ATTENTION,
@@ -121,6 +132,14 @@ public:
     void ctc_forward(const float* enc, int64_t M, float* logprobs, int32_t* argmax, hipStream_t s);
     void tdt_joint_argmax(const float* enc, int64_t M, const float* g, float* logits, int32_t* tok,
                           int32_t* dur, hipStream_t s);
+    bool has_decoder() const { return pred_.ok() && heads_.jout.ok(); }
+    // transducer_greedy_batch (transducer_batch.cpp:24-213): greedy TDT
+    // (n_dur > 0, skip = durations[argmax]) or RNNT decode of B utterances in
+    // lockstep rounds; enc [B][T_max][d_model] f32 device, T_valid host.
+    // Outputs (host) per item b: counts[b] tokens in ids/frames/conf/span[b*cap ...].
+    void transducer_greedy(const float* enc, int B, int T_max, const int* T_valid, const int32_t* durations,
+                           int n_dur, int blank_id, int max_symbols, int cap, int32_t* ids, int32_t* frames,
+                           float* conf, int32_t* span, int* counts, hipStream_t s);
     void set_profiling(unsigned family_mask, int stride);
     void profile_read(double* ms_per_family, int64_t* launches_per_family);
 
@@ -167,6 +186,7 @@ private:
     SubDev sub_;
     DevWeight wpos_all_;   // linear_pos of all layers, [L*D][D]; layers_[l].wpos are row views
     HeadsDev heads_;
+    PredDev pred_;
     std::unique_ptr<Ws> ws_;
     float* conv_capture_ = nullptr;   // conformer_layer_forward's conv-module output
     struct ProfHook;

@@ -63,6 +63,7 @@ class Config:
     tdt_durations: tuple = (0, 1, 2, 3, 4)
     joint_hidden: int = 640
     pred_hidden: int = 640
+    pred_rnn_layers: int = 2
     arch: str = "hybrid_tdt_ctc"
     attn_bias: bool = True          # linear_q/k/v/out biases (110m: yes, 0.6b-v2: no)
     conv_bias: bool = True
@@ -233,6 +234,23 @@ def mel_filterbank(sr: int, n_fft: int, n_mels: int, fmin: float = 0.0, fmax=Non
     return w.astype(np.float32)
 
 
+def add_prediction(m: "Model", seed: int = 20261201, std: float = 0.1):
+    """The RNNT/TDT prediction network (NeMo RNNTDecoder: Embedding(vocab+1,
+    pred_hidden) + stacked LSTM, prediction.hpp:27-50), seeded like synthesize()."""
+    c = m.cfg
+    P, V1 = c.pred_hidden, c.vocab_size + 1
+    specs = [("decoder.prediction.embed.weight", (V1, P))]
+    for l in range(c.pred_rnn_layers):
+        s = f"decoder.prediction.dec_rnn.lstm.%s_l{l}"
+        specs += [(s % "weight_ih", (4 * P, P)), (s % "weight_hh", (4 * P, P)),
+                  (s % "bias_ih", (4 * P,)), (s % "bias_hh", (4 * P,))]
+    for name, shape in specs:
+        rng = np.random.default_rng(seed ^ fnv1a64(name))
+        a = rng.normal(0, std if "embed" not in name else 1.0, int(np.prod(shape)))
+        m.tensors[name] = Tensor(GGML_F32, shape, np.ascontiguousarray(a, dtype=np.float32).reshape(shape))
+    return m
+
+
 def add_featurizer(m: "Model"):
     """preprocessor.featurizer.window / .fb of the config (the two buffers the
     converter keeps from the checkpoint, docs/conversion.md:110-136)."""
@@ -313,6 +331,7 @@ def _kv_items(cfg: Config):
           ("parakeet.blank_id", _GT_U32, cfg.vocab_size),
           ("parakeet.joint.joint_hidden", _GT_U32, cfg.joint_hidden),
           ("parakeet.decoder.pred_hidden", _GT_U32, cfg.pred_hidden),
+          ("parakeet.decoder.pred_rnn_layers", _GT_U32, cfg.pred_rnn_layers),
           ("parakeet.tdt.durations", _GT_ARR, (_GT_I32, list(cfg.tdt_durations)))]
     return kv
 

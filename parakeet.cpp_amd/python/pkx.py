@@ -89,6 +89,9 @@ SIGS = {
     "pkx_mel_frames": ([_vp, C.c_int], C.c_int),
     "pkx_mel_forward": ([_vp, _vp, C.c_int, C.c_int64, _ip, _vp, C.c_int, _ip, _vp], C.c_int),
     "pkx_quantize": ([C.c_int, _vp, _vp, C.c_int64, C.c_int64, _vp], C.c_int),
+    "pkx_transducer_greedy": ([_vp, _vp, C.c_int, C.c_int, _ip, C.POINTER(C.c_int32), C.c_int, C.c_int, C.c_int,
+                               C.c_int, C.POINTER(C.c_int32), C.POINTER(C.c_int32), _f, C.POINTER(C.c_int32), _ip,
+                               _vp], C.c_int),
     "pkx_quantize_gguf": ([C.c_char_p, C.c_char_p, C.c_int, _ip, _ip, _ip], C.c_int),
     "pkx_model_set_profiling": ([_vp, C.c_uint, C.c_int], C.c_int),
     "pkx_model_profile_read": ([_vp, C.POINTER(C.c_double), C.POINTER(C.c_int64)], C.c_int),
@@ -296,6 +299,24 @@ class Model:
                                         C.byref(tout), _iptr(vo),
                                         capture.ptr if capture is not None else None, _sh(stream)))
         return tout.value, vo
+
+    def transducer_greedy(self, enc: DeviceArray, T_valid, durations=(), blank_id=None, max_symbols=10,
+                          cap=None, stream=None):
+        """enc [B][T_max][D] f32 on the device -> per item (ids, frames, conf, span)."""
+        B, T_max, _ = enc.shape
+        cap = cap or T_max * max_symbols
+        blank = self.cfg.vocab_size if blank_id is None else blank_id
+        tv = np.ascontiguousarray(T_valid, dtype=np.int32)
+        du = np.ascontiguousarray(durations, dtype=np.int32)
+        ids, fr, sp = (np.zeros((B, cap), np.int32) for _ in range(3))
+        cf = np.zeros((B, cap), np.float32)
+        cnt = np.zeros(B, np.int32)
+        i32 = C.POINTER(C.c_int32)
+        check(lib().pkx_transducer_greedy(self.handle, enc.ptr, B, T_max, _iptr(tv), du.ctypes.data_as(i32),
+                                          len(du), blank, max_symbols, cap, ids.ctypes.data_as(i32),
+                                          fr.ctypes.data_as(i32), cf.ctypes.data_as(_f), sp.ctypes.data_as(i32),
+                                          _iptr(cnt), _sh(stream)))
+        return [(ids[b, :cnt[b]], fr[b, :cnt[b]], cf[b, :cnt[b]], sp[b, :cnt[b]]) for b in range(B)]
 
     def subsampling_forward(self, mel: DeviceArray, valid_T, out: DeviceArray,
                             mask_mode=MASK_BATCHED, stream=None):

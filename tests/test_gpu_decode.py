@@ -1,0 +1,62 @@
+"""Greedy transducer decode on the device (pkx_transducer_greedy) against the
+oracle's restatement of the per-item loops (tdt.cpp / the RNNT loop, which
+transducer_batch.cpp reproduces in lockstep).  Bar: identical token ids,
+frames and spans per item (the argmax decisions), confidence within 1e-5.
+The joint's output weights are scaled up so that the decisions have margins
+far above f32 rounding (the device sums the products in another order)."""
+import numpy as np
+import pytest
+
+import oracle
+import pk_model as pm
+
+pytestmark = pytest.mark.gpu
+
+
+def _model(durations, seed=7):
+    cfg = pm.Config(d_model=96, n_layers=1, n_heads=2, ff_dim=192, n_mels=64, sub_channels=16, vocab_size=40,
+                    joint_hidden=80, pred_hidden=72, pred_rnn_layers=2, tdt_durations=tuple(durations))
+    m = pm.add_prediction(pm.synthesize(cfg, "f32", heads=True, seed=seed), seed=seed)
+    for n in ("joint.joint_net.2.weight", "joint.joint_net.2.bias"):
+        t = m.tensors[n]
+        m.tensors[n] = pm.Tensor(t.gtype, t.shape, (t.data * 60.0).astype(np.float32))
+    return cfg, m
+
+
+@pytest.mark.parametrize("kind,max_symbols", [("tdt", 10), ("tdt", 2), ("rnnt", 10), ("rnnt", 1)])
+def test_greedy_decode_matches_oracle(gpu, stream, kind, max_symbols):
+    durations = (0, 1, 2, 3, 4) if kind == "tdt" else ()
+    cfg, m = _model(durations)
+    gm = gpu.Model.from_tensors(m)
+    tr = oracle.Transducer(m)
+    rng = np.random.default_rng(11)
+    T_valid = [60, 1, 37, 0, 59, 12]
+    B, T_max = len(T_valid), 60
+    enc = rng.standard_normal((B, T_max, cfg.d_model)).astype(np.float32)
+    print(f"[decode] {kind} max_symbols={max_symbols} T={T_valid}", flush=True)
+    d_enc = gpu.DeviceArray.from_numpy(enc, stream)
+    got = gm.transducer_greedy(d_enc, T_valid, durations=durations, max_symbols=max_symbols, stream=stream)
+    total = 0
+    for b in range(B):
+        ids, fr, cf, sp = tr.greedy(enc[b, :T_valid[b]], durations=durations, max_symbols=max_symbols)
+        g_ids, g_fr, g_cf, g_sp = got[b]
+        total += len(ids)
+        assert np.array_equal(g_ids, ids), (b, g_ids[:20], ids[:20])
+        assert np.array_equal(g_fr, fr) and np.array_equal(g_sp, sp)
+        assert np.max(np.abs(g_cf - cf), initial=0.0) <= 1e-5
+        assert np.all(ids < cfg.vocab_size)
+    print(f"[decode] {total} tokens identical", flush=True)
+    assert total > 20
+    d_enc.free()
+
+
+def test_decode_rejects_bad_arguments(gpu, stream):
+    cfg, m = _model((0, 1, 2, 3, 4))
+    gm = gpu.Model.from_tensors(m)
+    enc = np.zeros((1, 4, cfg.d_model), np.float32)
+    d_enc = gpu.DeviceArray.from_numpy(enc, stream)
+    with pytest.raises(gpu.PkxError, match="durations"):
+        gm.transducer_greedy(d_enc, [4], durations=(0, 1), stream=stream)
+    with pytest.raises(gpu.PkxError, match="T_valid"):
+        gm.transducer_greedy(d_enc, [5], durations=(0, 1, 2, 3, 4), stream=stream)
+    d_enc.free()
