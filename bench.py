@@ -160,6 +160,22 @@ def pcm_in(gm, cfg, stream, steps, warmup=2):
             "ms_per_step": round(both_ms, 4), "rtfx": round(audio_s / (both_ms / 1e3), 1), "steps": steps}
 
 
+def greedy_decode(gm, cfg, stream, d_enc, valid_out, reps=3):
+    """Batched greedy TDT decode (prediction LSTM + joint + rule, device) of the
+    encoder output: 16 items x 125 frames, 0.6B decoder shape (2-layer LSTM 640,
+    joint 640, 1024 tokens + blank + 5 durations); wall time per batch."""
+    d = tuple(cfg.tdt_durations)
+    gm.transducer_greedy(d_enc, valid_out, durations=d, stream=stream)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        out = gm.transducer_greedy(d_enc, valid_out, durations=d, stream=stream)
+    ms = (time.perf_counter() - t0) * 1e3 / reps
+    toks = int(sum(len(o[0]) for o in out))
+    audio_s = B * T_MEL * HOP_S
+    return {"workload": "greedy TDT decode of the encoder output, batch 16 x 125 frames (random-init decoder)",
+            "ms": round(ms, 3), "rtfx": round(audio_s / (ms / 1e3), 1), "tokens": toks, "reps": reps}
+
+
 def cpu_baseline(model, mel_item, budget_s=12.0):
     import oracle
     om = oracle.OracleModel(model)
@@ -195,7 +211,7 @@ def main():
 
     cfg = pm.Config(**CFG)
     t0 = time.perf_counter()
-    model = pm.synthesize(cfg, "q8_0", heads=False)
+    model = pm.add_prediction(pm.synthesize(cfg, "q8_0", heads=True))
     gm = pkx.Model.from_tensors(model, pkx.PREC_AUTO)
     assert gm.precision == pkx.PREC_F16
     setup_s = time.perf_counter() - t0
@@ -287,6 +303,8 @@ def main():
                     work["gemm_ffn"][1] / 1e9, B * Tp, cfg.d_model, cfg.ff_dim)}
 
     pcm_line = pcm_in(gm, cfg, stream, min(args.steps, 10))
+    _, vo_dec = gm.encoder_forward(d_mel, valid, d_out, stream=stream)
+    dec_line = greedy_decode(gm, cfg, stream, d_out, vo_dec)
 
     audio_s = B * T_MEL * HOP_S
     rtfx = audio_s / (ms_step / 1e3)
@@ -305,6 +323,7 @@ def main():
         "kernels": kernels,
         "kernel_busy_ms_per_step": round(busy_ms, 4),
         "pcm_in": pcm_line,
+        "decode": dec_line,
         "setup_s": round(setup_s, 1),
     }
     if not args.no_extra:

@@ -2,24 +2,27 @@
 // (src/transducer_batch.cpp:24-213) with the prediction net of
 // src/prediction.cpp:118-178 and the joint of src/joint.cpp:37-63,106-143.
 //
-// All B items advance in lockstep rounds.  One round:
-//   per LSTM layer l: z = [x_l | h_l] . [W_ih | W_hh]^T + (b_ih + b_hh)   (f32 GEMM)
-//                     lstm_cell_kernel: c' = s(f) c + s(i) tanh(g), h' = s(o) tanh(c')
-//   pp = W_pred g + b_pred                                                (f32 GEMM)
-//   joint_relu_kernel: f = ReLU(enc_proj[t_b] + pp)
-//   logits = W_out f + b_out                                              (f32 GEMM)
+// All B items advance in lockstep rounds; one round is L + 3 launches:
+//   lstm layer l (dec_mv_kernel<MV_LSTM>): z = [x_l | h_l] . [W_ih | W_hh]^T
+//       + (b_ih + b_hh) for the 4 gate rows of each hidden unit, then the
+//       cell c' = s(f) c + s(i) tanh(g), h' = s(o) tanh(c') in the same kernel
+//   joint (dec_mv_kernel<MV_JOINT>): f = ReLU(enc_proj[t_b] + W_pred g + b_pred)
+//   logits (dec_mv_kernel<MV_PLAIN>): W_out f + b_out
 //   greedy_rule_kernel: argmaxes, the TDT / RNNT rule of the per-item loops,
-//                       token records, state commit on emit.
-// Every round recomputes the LSTM for all items: from an unchanged committed
-// state it reproduces the same g bit for bit (the reference's g_valid cache
-// skips that recomputation, with the same result).  The host launches rounds
-// in chunks and reads the active flags between chunks; rounds after the last
-// item finished change nothing (the rule kernel returns for inactive items).
+//       token records, state commit on emit.
+// The matvecs are weight-streaming: each workgroup owns a few output rows,
+// keeps the B input vectors in LDS and reads its rows of W once per round for
+// all items (f32 weights; the quantisable joint projections are dequantised
+// to f32 at load).  Every round recomputes the LSTM for all items: from an
+// unchanged committed state it reproduces the same g bit for bit (the
+// reference's g_valid cache skips that recomputation, with the same result).
+// The host launches rounds in chunks and reads the active flags between
+// chunks; rounds after the last item finished change nothing.
 //
-// Device state (ws): X_l [B][2H] holds [x_l | committed h_l] for layer l
-// (x_0 = embedding of the last token, zeros before the first emission; x_l =
-// this round's h'_{l-1}), so a commit writes straight into the next round's
-// GEMM operand.
+// Device state: X_l [B][2H] holds [x_l | committed h_l] for layer l (x_0 =
+// embedding of the last token, zeros before the first emission; x_l = this
+// round's h'_{l-1}), so a commit writes straight into the next round's input.
+#include <algorithm>
 #include <cmath>
 #include <vector>
 
@@ -40,32 +43,100 @@ struct DecState {
 
 __device__ __forceinline__ float sigmoid_ref(float x) { return 1.0f / (1.0f + expf(-x)); }   // ggml_sigmoid
 
-// z [B][4H] -> out_h/out_c [B][H]; h' also into the next layer's x (or g)
-__global__ void lstm_cell_kernel(const float* z, const float* c_in, float* out_h, float* out_c, float* x_next,
-                                 int ld_next, int B, int H) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (int64_t)B * H) return;
-    const int b = (int)(i / H), j = (int)(i - (int64_t)b * H);
-    const float* zr = z + (int64_t)b * 4 * H;
-    const float zi = zr[j], zf = zr[H + j], zg = zr[2 * H + j], zo = zr[3 * H + j];
-    const float c = sigmoid_ref(zf) * c_in[i] + sigmoid_ref(zi) * tanhf(zg);
-    const float h = sigmoid_ref(zo) * tanhf(c);
-    out_c[i] = c;
-    out_h[i] = h;
-    x_next[(int64_t)b * ld_next + j] = h;
-}
+enum { MV_LSTM = 0, MV_JOINT = 1, MV_PLAIN = 2 };
+constexpr int MV_ITEMS = 16;   // items per LDS pass
 
-// f[b][:] = ReLU(enc_proj[b][clamp(t_b)][:] + pp[b][:])
-__global__ void joint_relu_kernel(const float* ep, int T_max, const float* pp, float* f, DecState st, int B, int Hj) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (int64_t)B * Hj) return;
-    const int b = (int)(i / Hj), h = (int)(i - (int64_t)b * Hj);
-    int t = st.t[b];
-    const int T = st.T[b];
-    t = t > T - 1 ? T - 1 : t;   // inactive / boundary items (their logits are not used)
-    t = t < 0 ? 0 : t;
-    const float s = ep[((int64_t)b * T_max + t) * Hj + h] + pp[i];
-    f[i] = s > 0.f ? s : 0.f;
+struct MvArgs {
+    const float* x;   // [B][ldx], K used
+    int ldx, K, B;
+    const float* W;   // [rows][K] f32
+    const float* bias;
+    int n_out;        // MV_LSTM: hidden units H (rows g*H + u); else output rows
+    float* y;         // MV_JOINT / MV_PLAIN: [B][n_out]
+    // MV_LSTM
+    const float* c_in;
+    float *out_h, *out_c, *x_next;
+    int ld_next;
+    // MV_JOINT
+    const float* ep;
+    int T_max;
+};
+
+// One wave per output unit (MV_LSTM: the 4 gate rows of a hidden unit; else
+// one row); lanes stride K in float4, the B items' inputs come from LDS.
+template <int MODE>
+__global__ __launch_bounds__(256) void dec_mv_kernel(MvArgs a, DecState st) {
+    constexpr int G = MODE == MV_LSTM ? 4 : 1;
+    extern __shared__ float xs[];   // [MV_ITEMS][K]
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int u = blockIdx.x * 4 + w;   // this wave's unit / row
+    for (int m0 = 0; m0 < a.B; m0 += MV_ITEMS) {
+        const int mc = min(MV_ITEMS, a.B - m0);
+        __syncthreads();
+        for (int i = threadIdx.x; i < mc * (a.K / 4); i += 256) {
+            const int m = i / (a.K / 4), k4 = i - m * (a.K / 4);
+            *(float4v*)(xs + m * a.K + 4 * k4) = *(const float4v*)(a.x + (int64_t)(m0 + m) * a.ldx + 4 * k4);
+        }
+        __syncthreads();
+        if (u >= a.n_out) continue;
+        float acc[MV_ITEMS][G];
+#pragma unroll
+        for (int m = 0; m < MV_ITEMS; ++m)
+#pragma unroll
+            for (int g = 0; g < G; ++g) acc[m][g] = 0.f;
+        for (int k = 4 * lane; k < a.K; k += 256) {
+            float4v wv[G];
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+                wv[g] = *(const float4v*)(a.W + (int64_t)(MODE == MV_LSTM ? g * a.n_out + u : u) * a.K + k);
+#pragma unroll
+            for (int m = 0; m < MV_ITEMS; ++m) {
+                if (m < mc) {
+                    const float4v xv = *(const float4v*)(xs + m * a.K + k);
+#pragma unroll
+                    for (int g = 0; g < G; ++g)
+                        acc[m][g] += (wv[g][0] * xv[0] + wv[g][1] * xv[1]) + (wv[g][2] * xv[2] + wv[g][3] * xv[3]);
+                }
+            }
+        }
+        // butterfly sums: every lane ends with every (item, gate) total
+#pragma unroll
+        for (int m = 0; m < MV_ITEMS; ++m)
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+                for (int o = 32; o > 0; o >>= 1) acc[m][g] += __shfl_xor(acc[m][g], o, 64);
+        // lane m finishes item m0 + m
+        float z[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            z[g] = 0.f;
+#pragma unroll
+            for (int m = 0; m < MV_ITEMS; ++m)
+                if (m == lane) z[g] = acc[m][g];
+        }
+        if (lane >= mc) continue;
+        const int b = m0 + lane;
+        if constexpr (MODE == MV_LSTM) {
+            const int H = a.n_out;
+            const float zi = z[0] + a.bias[u], zf = z[1] + a.bias[H + u];
+            const float zg = z[2] + a.bias[2 * H + u], zo = z[3] + a.bias[3 * H + u];
+            const int64_t i = (int64_t)b * H + u;
+            const float c = sigmoid_ref(zf) * a.c_in[i] + sigmoid_ref(zi) * tanhf(zg);
+            const float h = sigmoid_ref(zo) * tanhf(c);
+            a.out_c[i] = c;
+            a.out_h[i] = h;
+            a.x_next[(int64_t)b * a.ld_next + u] = h;
+        } else if constexpr (MODE == MV_JOINT) {
+            int t = st.t[b];
+            const int T = st.T[b];
+            t = t > T - 1 ? T - 1 : t;   // inactive / boundary items (their logits are not used)
+            t = t < 0 ? 0 : t;
+            const float v = a.ep[((int64_t)b * a.T_max + t) * a.n_out + u] + (z[0] + a.bias[u]);
+            a.y[(int64_t)b * a.n_out + u] = v > 0.f ? v : 0.f;
+        } else {
+            a.y[(int64_t)b * a.n_out + u] = z[0] + a.bias[u];
+        }
+    }
 }
 
 __device__ __forceinline__ void argmax_first(float& v, int& k) {
@@ -78,6 +149,34 @@ __device__ __forceinline__ void argmax_first(float& v, int& k) {
             k = ok;
         }
     }
+}
+
+// workgroup-wide argmax (first max) over a[0, n)
+__device__ __forceinline__ int block_argmax(const float* a, int n, float& vmax, float* rv, int* rk) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    float v = -INFINITY;
+    int k = 0x7fffffff;
+    for (int i = threadIdx.x; i < n; i += 256)
+        if (a[i] > v || (a[i] == v && i < k)) {
+            v = a[i];
+            k = i;
+        }
+    argmax_first(v, k);
+    __syncthreads();
+    if (lane == 0) {
+        rv[w] = v;
+        rk[w] = k;
+    }
+    __syncthreads();
+    v = rv[0];
+    k = rk[0];
+    for (int j = 1; j < 4; ++j)
+        if (rv[j] > v || (rv[j] == v && rk[j] < k)) {
+            v = rv[j];
+            k = rk[j];
+        }
+    vmax = v;
+    return k < n ? k : 0;   // no value above -inf (NaN logits): index 0, as the scalar loop
 }
 
 struct RuleArgs {
@@ -93,67 +192,58 @@ struct RuleArgs {
     float* confs;
 };
 
-// one wave per item: the per-item rule of transducer_batch.cpp:128-205
+// one workgroup per item: the per-item rule of transducer_batch.cpp:128-205
 __global__ __launch_bounds__(256) void greedy_rule_kernel(RuleArgs a, DecState st) {
-    const int lane = threadIdx.x & 63, b = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (b >= a.B || !st.active[b]) return;
+    __shared__ float rv[4];
+    __shared__ int rk[4];
+    __shared__ double rd[4];
+    const int b = blockIdx.x, tid = threadIdx.x;
+    if (!st.active[b]) return;   // uniform over the workgroup
     const float* lz = a.logits + (int64_t)b * a.Vp;
-    float v = -INFINITY;
-    int k = 0x7fffffff;
-    for (int i = lane; i < a.n_tok; i += 64)
-        if (lz[i] > v || (lz[i] == v && i < k)) {
-            v = lz[i];
-            k = i;
-        }
-    argmax_first(v, k);
+    float v;
+    const int k = block_argmax(lz, a.n_tok, v, rv, rk);
     int dk = 0;
     if (a.n_dur > 0) {
-        float dv = -INFINITY;
-        int di = 0x7fffffff;
-        for (int i = lane; i < a.n_dur; i += 64)
-            if (lz[a.n_tok + i] > dv || (lz[a.n_tok + i] == dv && i < di)) {
-                dv = lz[a.n_tok + i];
-                di = i;
-            }
-        argmax_first(dv, di);
-        dk = di < a.n_dur ? di : 0;   // no value above -inf (NaN logits): index 0, as the scalar loop
+        float dv;
+        dk = block_argmax(lz + a.n_tok, a.n_dur, dv, rv, rk);
     }
-    if (k >= a.n_tok) k = 0;
     const bool emit = k != a.blank;
-    // max_prob confidence of the emitted token (decode_common.hpp:12-20), f64
     double den = 0.0;
     if (emit) {
-        for (int i = lane; i < a.n_tok; i += 64) den += exp((double)lz[i] - (double)v);
+        // max_prob confidence of the emitted token (decode_common.hpp:12-20), f64
+        for (int i = tid; i < a.n_tok; i += 256) den += exp((double)lz[i] - (double)v);
         for (int o = 32; o > 0; o >>= 1) den += __shfl_xor(den, o, 64);
-    }
-    const int t0 = st.t[b];
-    if (emit) {
+        if ((tid & 63) == 0) rd[tid >> 6] = den;
+        __syncthreads();
+        den = (rd[0] + rd[1]) + (rd[2] + rd[3]);
         // commit: the step's (h', c') become the item's state; the token's
         // embedding is the next step's layer-0 input
         for (int l = 0; l < a.L; ++l)
-            for (int j = lane; j < a.H; j += 64) {
+            for (int j = tid; j < a.H; j += 256) {
                 a.X[l][(int64_t)b * 2 * a.H + a.H + j] = a.oh[l][(int64_t)b * a.H + j];
                 a.cc[l][(int64_t)b * a.H + j] = a.oc[l][(int64_t)b * a.H + j];
             }
-        for (int j = lane; j < a.H; j += 64) a.X[0][(int64_t)b * 2 * a.H + j] = a.embed[(int64_t)k * a.H + j];
+        for (int j = tid; j < a.H; j += 256) a.X[0][(int64_t)b * 2 * a.H + j] = a.embed[(int64_t)k * a.H + j];
     }
-    if (lane != 0) return;
-    int t = t0, sym = st.sym[b];
-    if (a.n_dur > 0) {
-        const int skip = a.durations[dk];
-        if (emit) {
-            const int n = st.count[b];
-            if (n < a.cap) {
-                const double p = 1.0 / den, N = (double)a.n_tok;   // exp(v - v) / den
-                a.ids[(int64_t)b * a.cap + n] = k;
-                a.frames[(int64_t)b * a.cap + n] = t;
-                a.confs[(int64_t)b * a.cap + n] = (float)((N * p - 1.0) / (N - 1.0));
-                a.spans[(int64_t)b * a.cap + n] = skip;
-                st.count[b] = n + 1;
-            } else {
-                *st.overflow = 1;
-            }
+    if (tid != 0) return;
+    int t = st.t[b], sym = st.sym[b];
+    const int skip = a.n_dur > 0 ? a.durations[dk] : 1;
+    if (emit) {
+        const int n = st.count[b];
+        if (n < a.cap) {
+            const double p = 1.0 / den, N = (double)a.n_tok;   // exp(v - v) / den
+            a.ids[(int64_t)b * a.cap + n] = k;
+            a.frames[(int64_t)b * a.cap + n] = t;
+            a.confs[(int64_t)b * a.cap + n] = (float)((N * p - 1.0) / (N - 1.0));
+            a.spans[(int64_t)b * a.cap + n] = skip;
+            st.count[b] = n + 1;
+        } else {
+            *st.overflow = 1;
         }
+    }
+    if (a.n_dur > 0) {
+        // symbols_added += 1; t += skip; the frame is done unless skip == 0 and
+        // symbols < max_symbols; a frame ended by max_symbols advances by 1
         sym += 1;
         t += skip;
         if (!(skip == 0 && sym < a.max_symbols)) {
@@ -161,25 +251,11 @@ __global__ __launch_bounds__(256) void greedy_rule_kernel(RuleArgs a, DecState s
             sym = 0;
         }
     } else if (!emit) {
+        t += 1;   // RNNT blank: next frame
+        sym = 0;
+    } else if (++sym >= a.max_symbols) {
         t += 1;
         sym = 0;
-    } else {
-        const int n = st.count[b];
-        if (n < a.cap) {
-            const double p = 1.0 / den, N = (double)a.n_tok;
-            a.ids[(int64_t)b * a.cap + n] = k;
-            a.frames[(int64_t)b * a.cap + n] = t;
-            a.confs[(int64_t)b * a.cap + n] = (float)((N * p - 1.0) / (N - 1.0));
-            a.spans[(int64_t)b * a.cap + n] = 1;
-            st.count[b] = n + 1;
-        } else {
-            *st.overflow = 1;
-        }
-        sym += 1;
-        if (sym >= a.max_symbols) {
-            t += 1;
-            sym = 0;
-        }
     }
     st.t[b] = t;
     st.sym[b] = sym;
@@ -212,6 +288,8 @@ void Model::transducer_greedy(const float* enc, int B, int T_max, const int* T_v
     const int n_tok = Vp - n_dur;
     require(blank_id >= 0 && blank_id < n_tok && blank_id < pred_.V1, "decode: blank_id outside the token range");
     require(n_tok <= pred_.V1, "decode: joint tokens exceed the embedding rows");
+    require(H % 4 == 0 && Hj % 4 == 0, "decode: pred_hidden and joint_hidden must be multiples of 4");
+    require((size_t)MV_ITEMS * 2 * H * 4 <= 160 * 1024, "decode: pred_hidden too large for the LDS input stage");
     for (int b = 0; b < B; ++b) require(T_valid[b] >= 0 && T_valid[b] <= T_max, "decode: T_valid outside [0, T_max]");
     for (int i = 0; i < n_dur; ++i) require(durations && durations[i] >= 0, "decode: durations must be >= 0");
 
@@ -227,9 +305,7 @@ void Model::transducer_greedy(const float* enc, int B, int T_max, const int* T_v
         PKX_HIP(hipMemsetAsync(X[l], 0, sizeof(float) * B * 2 * H, s));   // SOS input, zero state
         PKX_HIP(hipMemsetAsync(cc[l], 0, sizeof(float) * B * H, s));
     }
-    float* z = m.get<float>((size_t)B * 4 * H);
     float* g = m.get<float>((size_t)B * H);
-    float* pp = m.get<float>((size_t)B * Hj);
     float* f = m.get<float>((size_t)B * Hj);
     float* lg = m.get<float>((size_t)B * Vp);
     int* ints = m.get<int>((size_t)6 * B + 1);
@@ -277,21 +353,53 @@ void Model::transducer_greedy(const float* enc, int B, int T_max, const int* T_v
     ra.spans = d_sp;
     ra.confs = d_cf;
 
+    const size_t lds_max = (size_t)MV_ITEMS * std::max(2 * H, std::max(H, Hj)) * sizeof(float);
+    for (const void* fn : {(const void*)dec_mv_kernel<MV_LSTM>, (const void*)dec_mv_kernel<MV_JOINT>,
+                           (const void*)dec_mv_kernel<MV_PLAIN>})
+        PKX_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_max));
     auto round = [&]() {
         for (int l = 0; l < L; ++l) {
-            gemm(pred_.wcat[l], EPI_STORE_F32, X[l], 2 * H, B, pred_.bsum[l], z, 4 * H, 1.f, nullptr, 1, s,
-                 PREC_F32, -1);
-            float* xn = l + 1 < L ? X[l + 1] : g;
-            launch(lstm_cell_kernel, dim3(cdiv((int64_t)B * H, 256)), dim3(256), 0, s, (const float*)z,
-                   (const float*)cc[l], oh[l], oc[l], xn, l + 1 < L ? 2 * H : H, B, H);
+            MvArgs a{};
+            a.x = X[l];
+            a.ldx = 2 * H;
+            a.K = 2 * H;
+            a.B = B;
+            a.W = pred_.wcat[l];
+            a.bias = pred_.bsum[l];
+            a.n_out = H;
+            a.c_in = cc[l];
+            a.out_h = oh[l];
+            a.out_c = oc[l];
+            a.x_next = l + 1 < L ? X[l + 1] : g;
+            a.ld_next = l + 1 < L ? 2 * H : H;
+            launch(dec_mv_kernel<MV_LSTM>, dim3(cdiv(H, 4)), dim3(256), (uint32_t)(MV_ITEMS * 2 * H * 4), s, a, st);
             PKX_LAUNCH_CHECK();
         }
-        gemm(heads_.jpred, EPI_STORE_F32, g, H, B, heads_.jpred_b, pp, Hj, 1.f, nullptr, 1, s, PREC_F32, -1);
-        launch(joint_relu_kernel, dim3(cdiv((int64_t)B * Hj, 256)), dim3(256), 0, s, (const float*)ep, T_max,
-               (const float*)pp, f, st, B, Hj);
+        MvArgs j{};
+        j.x = g;
+        j.ldx = H;
+        j.K = H;
+        j.B = B;
+        j.W = pred_.jpred;
+        j.bias = heads_.jpred_b;
+        j.n_out = Hj;
+        j.y = f;
+        j.ep = ep;
+        j.T_max = T_max;
+        launch(dec_mv_kernel<MV_JOINT>, dim3(cdiv(Hj, 4)), dim3(256), (uint32_t)(MV_ITEMS * H * 4), s, j, st);
         PKX_LAUNCH_CHECK();
-        gemm(heads_.jout, EPI_STORE_F32, f, Hj, B, heads_.jout_b, lg, Vp, 1.f, nullptr, 1, s, PREC_F32, -1);
-        launch(greedy_rule_kernel, dim3(cdiv(B, 4)), dim3(256), 0, s, ra, st);
+        MvArgs o{};
+        o.x = f;
+        o.ldx = Hj;
+        o.K = Hj;
+        o.B = B;
+        o.W = pred_.jout;
+        o.bias = heads_.jout_b;
+        o.n_out = Vp;
+        o.y = lg;
+        launch(dec_mv_kernel<MV_PLAIN>, dim3(cdiv(Vp, 4)), dim3(256), (uint32_t)(MV_ITEMS * Hj * 4), s, o, st);
+        PKX_LAUNCH_CHECK();
+        launch(greedy_rule_kernel, dim3(B), dim3(256), 0, s, ra, st);
         PKX_LAUNCH_CHECK();
     };
 

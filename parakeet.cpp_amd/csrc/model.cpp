@@ -169,8 +169,42 @@ static std::vector<float> to_f32(const HostTensor& t) {
     } else if (t.gtype == GT_F16) {
         const uint16_t* h = (const uint16_t*)t.bytes.data();
         for (int64_t i = 0; i < n; ++i) v[(size_t)i] = half_bits_to_float(h[i]);
+    } else if (t.gtype == GT_Q8_0) {
+        // ggml block_q8_0 {f16 d; i8 q[32]}: w = d * q (exact in f32)
+        require(n % 32 == 0 && (int64_t)t.bytes.size() == n / 32 * 34, "q8_0 tensor size");
+        for (int64_t b = 0; b < n / 32; ++b) {
+            const uint8_t* blk = t.bytes.data() + b * 34;
+            const float d = half_bits_to_float((uint16_t)(blk[0] | (blk[1] << 8)));
+            for (int j = 0; j < 32; ++j) v[(size_t)(b * 32 + j)] = d * (float)(int8_t)blk[2 + j];
+        }
+    } else if (t.gtype == GT_Q4_K) {
+        // ggml block_q4_K {f16 d, dmin; u8 scales[12]; u8 qs[128]}: w = d*sc*q - dmin*m
+        require(n % 256 == 0 && (int64_t)t.bytes.size() == n / 256 * 144, "q4_K tensor size");
+        for (int64_t b = 0; b < n / 256; ++b) {
+            const uint8_t* blk = t.bytes.data() + b * 144;
+            const float d = half_bits_to_float((uint16_t)(blk[0] | (blk[1] << 8)));
+            const float dmin = half_bits_to_float((uint16_t)(blk[2] | (blk[3] << 8)));
+            const uint8_t* sc = blk + 4;
+            const uint8_t* qs = blk + 16;
+            for (int j = 0; j < 8; ++j) {
+                int s6, m6;
+                if (j < 4) {
+                    s6 = sc[j] & 63;
+                    m6 = sc[j + 4] & 63;
+                } else {
+                    s6 = (sc[j + 4] & 0xF) | ((sc[j - 4] >> 6) << 4);
+                    m6 = (sc[j + 4] >> 4) | ((sc[j] >> 6) << 4);
+                }
+                const float dj = d * (float)s6, mj = dmin * (float)m6;
+                for (int l = 0; l < 32; ++l) {
+                    const uint8_t byte = qs[32 * (j / 2) + l];
+                    const int q = (j & 1) ? (byte >> 4) : (byte & 0xF);
+                    v[(size_t)(b * 256 + 32 * j + l)] = dj * (float)q - mj;
+                }
+            }
+        }
     } else {
-        throw std::invalid_argument("expected an f32/f16 vector tensor");
+        throw std::invalid_argument("expected an f32/f16/q8_0/q4_K tensor");
     }
     return v;
 }
@@ -571,23 +605,20 @@ void Model::finalize() {
                     require(wih.size() == (size_t)4 * P * P && whh.size() == wih.size() && bih.size() == (size_t)4 * P &&
                                 bhh.size() == bih.size(),
                             "prediction net: layer " + s + " must be [4H][H] with [4H] biases");
-                    HostTensor cat;
-                    cat.gtype = GT_F32;
-                    cat.n_dims = 2;
-                    cat.ne[0] = 2 * P;
-                    cat.ne[1] = 4 * P;
-                    cat.bytes.resize((size_t)8 * P * 2 * P * 4);
-                    float* cw = (float*)cat.bytes.data();
+                    std::vector<float> cat((size_t)4 * P * 2 * P);
                     for (int r = 0; r < 4 * P; ++r) {
-                        std::memcpy(cw + (size_t)r * 2 * P, wih.data() + (size_t)r * P, sizeof(float) * P);
-                        std::memcpy(cw + (size_t)r * 2 * P + P, whh.data() + (size_t)r * P, sizeof(float) * P);
+                        std::memcpy(cat.data() + (size_t)r * 2 * P, wih.data() + (size_t)r * P, sizeof(float) * P);
+                        std::memcpy(cat.data() + (size_t)r * 2 * P + P, whh.data() + (size_t)r * P,
+                                    sizeof(float) * P);
                     }
-                    pred_.wcat[l] = make_weight(cat, 4 * P, 2 * P, false);
+                    pred_.wcat[l] = upload_f32(cat);
                     std::vector<float> bs((size_t)4 * P);
                     for (size_t i = 0; i < bs.size(); ++i) bs[i] = bih[i] + bhh[i];
                     pred_.bsum[l] = upload_f32(bs);
                 }
                 pred_.L = L;
+                pred_.jpred = upload_f32(*jp);   // f32 copies (dequantised) for the decode matvecs
+                pred_.jout = upload_f32(*jo);
             }
         }
     }

@@ -87,8 +87,10 @@ struct HeadsDev {
 struct PredDev {
     int H = 0, L = 0, V1 = 0;
     float* embed = nullptr;            // [V1][H]
-    DevWeight wcat[4];                 // [4H][2H]
+    float* wcat[4] = {};               // [4H][2H] f32 row-major
     float* bsum[4] = {};               // b_ih + b_hh, [4H]
+    float* jpred = nullptr;            // joint.pred.weight as f32 [Hj][H]
+    float* jout = nullptr;             // joint.joint_net.2.weight as f32 [Vp][Hj]
     bool ok() const { return L > 0; }
 };
 

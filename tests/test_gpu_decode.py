@@ -13,20 +13,21 @@ import pk_model as pm
 pytestmark = pytest.mark.gpu
 
 
-def _model(durations, seed=7):
-    cfg = pm.Config(d_model=96, n_layers=1, n_heads=2, ff_dim=192, n_mels=64, sub_channels=16, vocab_size=40,
-                    joint_hidden=80, pred_hidden=72, pred_rnn_layers=2, tdt_durations=tuple(durations))
-    m = pm.add_prediction(pm.synthesize(cfg, "f32", heads=True, seed=seed), seed=seed)
+def _model(durations, seed=7, qtype="f32"):
+    cfg = pm.Config(d_model=128, n_layers=1, n_heads=2, ff_dim=256, n_mels=64, sub_channels=16, vocab_size=40,
+                    joint_hidden=128, pred_hidden=64, pred_rnn_layers=2, tdt_durations=tuple(durations))
+    m = pm.add_prediction(pm.synthesize(cfg, qtype, heads=True, seed=seed), seed=seed)
     for n in ("joint.joint_net.2.weight", "joint.joint_net.2.bias"):
         t = m.tensors[n]
         m.tensors[n] = pm.Tensor(t.gtype, t.shape, (t.data * 60.0).astype(np.float32))
     return cfg, m
 
 
-@pytest.mark.parametrize("kind,max_symbols", [("tdt", 10), ("tdt", 2), ("rnnt", 10), ("rnnt", 1)])
-def test_greedy_decode_matches_oracle(gpu, stream, kind, max_symbols):
+@pytest.mark.parametrize("kind,max_symbols,qtype", [("tdt", 10, "f32"), ("tdt", 2, "f32"), ("rnnt", 10, "f32"),
+                                                     ("rnnt", 1, "f32"), ("tdt", 10, "q8_0")])
+def test_greedy_decode_matches_oracle(gpu, stream, kind, max_symbols, qtype):
     durations = (0, 1, 2, 3, 4) if kind == "tdt" else ()
-    cfg, m = _model(durations)
+    cfg, m = _model(durations, qtype=qtype)
     gm = gpu.Model.from_tensors(m)
     tr = oracle.Transducer(m)
     rng = np.random.default_rng(11)
