@@ -188,6 +188,23 @@ private:
 // pos_emb [2T-1][d_model] f32 (computed on the device in double, then f32).
 void rel_pos_encoding(int T, int d_model, std::vector<float>& out);
 
+// Per-emitted-token metadata (src/decode_types.hpp:25-30).
+struct TokenInfo {
+    int32_t id;
+    int32_t frame;
+    float conf;
+    int32_t span;
+};
+
+// Batched greedy transducer decode (src/transducer_batch.hpp:12-20) over the
+// model's prediction network and joint, on the device.  encs[n]: row-major
+// [T[n]][enc_hidden]; durations empty -> RNNT, else TDT.  Outputs per item:
+// ids[n] and, if toks != nullptr, TokenInfo[n].
+void transducer_greedy_batch(const ModelLoader& ml, const std::vector<std::vector<float>>& encs,
+                             const std::vector<int>& T, int enc_hidden, const std::vector<int32_t>& durations,
+                             int blank_id, int max_symbols, std::vector<std::vector<int32_t>>& ids,
+                             std::vector<std::vector<TokenInfo>>* toks);
+
 // Log-mel front end (src/mel.hpp:33-41), on the device.
 class MelFrontend {
 public:

@@ -472,3 +472,52 @@ MelBatch build_mel_batch(const ModelLoader& ml, const std::vector<std::vector<fl
 }
 
 }  // namespace pk
+
+namespace pk {
+
+// ---------------------------------------------------------------------------
+// transducer_greedy_batch
+// ---------------------------------------------------------------------------
+void transducer_greedy_batch(const ModelLoader& ml, const std::vector<std::vector<float>>& encs,
+                             const std::vector<int>& T, int enc_hidden, const std::vector<int32_t>& durations,
+                             int blank_id, int max_symbols, std::vector<std::vector<int32_t>>& ids,
+                             std::vector<std::vector<TokenInfo>>* toks) {
+    need(ml.handle() != nullptr, "model not loaded");
+    const int N = (int)encs.size();
+    need(N >= 1 && (int)T.size() == N, "transducer_greedy_batch: encs / T size mismatch");
+    need(enc_hidden == ml.config().d_model, "transducer_greedy_batch: enc_hidden != d_model");
+    int T_max = 1;
+    for (int n = 0; n < N; ++n) {
+        need(T[n] >= 0 && encs[n].size() >= (size_t)T[n] * enc_hidden, "transducer_greedy_batch: enc too short");
+        T_max = std::max(T_max, T[n]);
+    }
+    // stack to [N][T_max][enc_hidden] (rows past T[n] are never read)
+    std::vector<float> stacked((size_t)N * T_max * enc_hidden, 0.0f);
+    for (int n = 0; n < N; ++n)
+        std::copy(encs[n].begin(), encs[n].begin() + (size_t)T[n] * enc_hidden,
+                  stacked.begin() + (size_t)n * T_max * enc_hidden);
+    const int cap = T_max * std::max(max_symbols, 1);
+    std::vector<int32_t> id((size_t)N * cap), fr((size_t)N * cap), sp((size_t)N * cap);
+    std::vector<float> cf((size_t)N * cap);
+    std::vector<int> cnt(N);
+    ModelLoader::Device& d = ml.device();
+    std::lock_guard<std::mutex> lock(d.mu);
+    float* denc = (float*)d.get(d.in, stacked.size() * 4);
+    d.h2d(denc, stacked.data(), stacked.size() * 4);
+    chk(pkx_transducer_greedy(ml.handle(), denc, N, T_max, T.data(), durations.data(), (int)durations.size(),
+                              blank_id, max_symbols, cap, id.data(), fr.data(), cf.data(), sp.data(), cnt.data(),
+                              d.stream),
+        "pkx_transducer_greedy");
+    ids.assign(N, {});
+    if (toks) toks->assign(N, {});
+    for (int n = 0; n < N; ++n) {
+        ids[n].assign(id.begin() + (size_t)n * cap, id.begin() + (size_t)n * cap + cnt[n]);
+        if (toks)
+            for (int i = 0; i < cnt[n]; ++i) {
+                const size_t j = (size_t)n * cap + i;
+                (*toks)[n].push_back(TokenInfo{id[j], fr[j], cf[j], sp[j]});
+            }
+    }
+}
+
+}  // namespace pk

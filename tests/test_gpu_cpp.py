@@ -20,7 +20,8 @@ pytestmark = pytest.mark.gpu
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 BIN = os.path.join(ROOT, "tests", "cpp", "build")
 TESTS = ["test_subsampling", "test_subsampling_batch", "test_relpos_attention", "test_relpos_attention_batch",
-         "test_conformer", "test_conformer_batch", "test_encoder", "test_encoder_batch", "test_mel"]
+         "test_conformer", "test_conformer_batch", "test_encoder", "test_encoder_batch", "test_mel",
+         "test_transducer_greedy_batch"]
 _FILES = {}
 
 
@@ -39,7 +40,10 @@ def _files(tmp_path_factory, wtype):
     d = tmp_path_factory.mktemp(f"cpp_{wtype}")
     cfg = pm.Config(d_model=256, n_layers=4, n_heads=4, ff_dim=1024, conv_kernel=9, n_mels=80, sub_channels=64,
                     xscaling=True, vocab_size=127, joint_hidden=64, pred_hidden=64)
-    m = pm.add_featurizer(pm.synthesize(cfg, wtype, bn_random=True))
+    m = pm.add_featurizer(pm.add_prediction(pm.synthesize(cfg, wtype, bn_random=True)))
+    for n in ("joint.joint_net.2.weight", "joint.joint_net.2.bias"):   # decision margins far above f32 rounding
+        t = m.tensors[n]
+        m.tensors[n] = pm.Tensor(t.gtype, t.shape, (t.data * 60.0).astype(np.float32))
     om = oracle.OracleModel(m)
     rng = np.random.default_rng(42)
     F, T = cfg.n_mels, 1001
@@ -68,6 +72,15 @@ def _files(tmp_path_factory, wtype):
     mcfg = oracle.mel_cfg(n_fft=cfg.n_fft, hop=cfg.hop_length, n_mels=cfg.n_mels, preemph=cfg.preemph,
                           mag_power=cfg.mag_power, log_guard=cfg.log_zero_guard)
     base["pcm"] = pcm
+    # greedy TDT decode of a ragged batch of encoder outputs (the oracle's per-item loop)
+    tr = oracle.Transducer(m)
+    dT = np.array([40, 23, 9], np.int32)
+    denc = rng.standard_normal((3, 40, cfg.d_model)).astype(np.float32)
+    base["dec_enc"], base["dec_T"] = denc, dT
+    base["dec_durations"] = np.array(cfg.tdt_durations, np.int32)
+    for n in range(3):
+        ids, fr, _, sp = tr.greedy(denc[n, :dT[n]], cfg.tdt_durations)
+        base[f"dec_ids_{n}"], base[f"dec_frames_{n}"], base[f"dec_spans_{n}"] = ids, fr, sp
     base["mel_pcm"] = oracle.mel(mcfg, oracle.mel_window(m.tensors["preprocessor.featurizer.window"].data, cfg.n_fft),
                                  m.tensors["preprocessor.featurizer.fb"].data.reshape(cfg.n_mels, -1), pcm)
     mp, bp = str(d / "model.gguf"), str(d / "baseline.gguf")
