@@ -48,6 +48,15 @@ def lib():
         L.orc_conformer_layer.argtypes = [C.c_void_p, _f, C.c_int, C.c_int, _f, _i, _f, _f]
         L.orc_valid_out_len.argtypes = [C.c_int, C.c_int]
         L.orc_subsampled_len.argtypes = [C.c_int]
+        L.orc_valid_out_len_c.argtypes = [C.c_int, C.c_int, C.c_int]
+        L.orc_subsampled_len_c.argtypes = [C.c_int, C.c_int]
+        L.orc_stream_new.restype = C.c_void_p
+        L.orc_stream_new.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                     C.c_int]
+        L.orc_stream_free.argtypes = [C.c_void_p]
+        L.orc_stream_reset.argtypes = [C.c_void_p]
+        L.orc_stream_step.argtypes = [C.c_void_p, _f, C.c_int, C.c_int, _f]
+        L.orc_stream_chunk_len.argtypes = [C.c_void_p, C.c_int]
         L.orc_subsampling.argtypes = [C.c_void_p, _f, C.c_int, C.c_int, C.c_int, _i, C.c_int, _f, _i]
         L.orc_encoder_forward.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int, _f, C.c_int,
                                           C.c_int, C.c_int, _i, C.c_int, _f, _i, _f]
@@ -155,12 +164,14 @@ class OrcLayer(C.Structure):
             "conv_ln_g", "conv_ln_b", "pw1_w", "pw1_b", "dw_w", "dw_b",
             "bn_g", "bn_b", "bn_mean", "bn_var", "pw2_w", "pw2_b",
             "ff2_ln_g", "ff2_ln_b", "ff2_w1", "ff2_b1", "ff2_w2", "ff2_b2",
-            "out_ln_g", "out_ln_b")]
+            "out_ln_g", "out_ln_b")] + [
+        (n, C.c_int) for n in ("conv_causal", "conv_ln", "att_limited", "att_left", "att_right")]
 
 
 class OrcSub(C.Structure):
     _fields_ = [("C", C.c_int), ("D", C.c_int)] + [
-        (n, _f) for n in ("w0", "b0", "w2", "b2", "w3", "b3", "w5", "b5", "w6", "b6", "wout", "bout")]
+        (n, _f) for n in ("w0", "b0", "w2", "b2", "w3", "b3", "w5", "b5", "w6", "b6", "wout", "bout")] + [
+        ("causal", C.c_int)]
 
 
 _LAYER_MAP = {
@@ -212,8 +223,15 @@ class OracleModel:
             for field_name, suffix in _LAYER_MAP.items():
                 a = self.w.get(f"encoder.layers.{i}.{suffix}")
                 setattr(L, field_name, fp(a) if a is not None else None)
+            L.conv_causal = int(bool(getattr(cfg, "conv_causal", False)))
+            L.conv_ln = int(getattr(cfg, "conv_norm_type", "batch_norm") == "layer_norm")
+            L.att_limited = int(getattr(cfg, "att_context_style", "regular") == "chunked_limited"
+                                and getattr(cfg, "att_context_right", -1) >= 0)
+            L.att_left = int(getattr(cfg, "att_context_left", -1))
+            L.att_right = int(getattr(cfg, "att_context_right", -1))
         self.sub = OrcSub()
         self.sub.C, self.sub.D = cfg.sub_channels, cfg.d_model
+        self.sub.causal = int(bool(getattr(cfg, "causal_downsampling", False)))
         for field_name, suffix in _SUB_MAP.items():
             setattr(self.sub, field_name, fp(self.w["encoder.pre_encode." + suffix]))
 
@@ -246,7 +264,7 @@ class OracleModel:
     def subsampling(self, mel, valid_in=None, stage_masks=True):
         mel = f32(mel)
         B, F, T = mel.shape
-        Tp = lib().orc_subsampled_len(T)
+        Tp = lib().orc_subsampled_len_c(T, self.sub.causal)
         out = np.empty((B, Tp, self.cfg.d_model), dtype=np.float32)
         vo = np.zeros(B, dtype=np.int32)
         lib().orc_subsampling(C.cast(C.pointer(self.sub), C.c_void_p), fp(mel), B, F, T,
@@ -257,7 +275,7 @@ class OracleModel:
     def encoder(self, mel, valid_in=None, stage_masks=True, capture=False):
         mel = f32(mel)
         B, F, T = mel.shape
-        Tp = lib().orc_subsampled_len(T)
+        Tp = lib().orc_subsampled_len_c(T, self.sub.causal)
         D = self.cfg.d_model
         out = np.empty((B, Tp, D), dtype=np.float32)
         vo = np.zeros(B, dtype=np.int32)
@@ -297,6 +315,60 @@ class OracleModel:
                                    fp(f32(Wp)), fp(f32(bp)), fp(f32(Wo)), fp(f32(bo)), n_tok, n_dur,
                                    fp(logits), tok.ctypes.data_as(_i32), dur.ctypes.data_as(_i32))
         return logits, tok, dur
+
+
+class Stream:
+    """StreamingEncoder (streaming_encoder.hpp:33-95) over an OracleModel of a
+    streaming configuration: step() takes one mel window [n_mels][n] and
+    returns the kept frames [n_valid][D]."""
+
+    def __init__(self, om: OracleModel):
+        cfg = om.cfg
+        self.om = om
+        self.cfg = cfg
+        self.chunk_first = int(cfg.stream_chunk_size[0])
+        self.chunk = int(cfg.stream_chunk_size[1] if len(cfg.stream_chunk_size) > 1 else 16)
+        self.pre_cache = int(cfg.stream_pre_encode_cache_size[1]
+                             if len(cfg.stream_pre_encode_cache_size) > 1 else 9)
+        self.valid_out_len = int(cfg.stream_valid_out_len)
+        self.cache_len = int(cfg.stream_last_channel_cache_size)
+        self.h = lib().orc_stream_new(C.cast(C.pointer(om.sub), C.c_void_p), C.cast(om.layers, C.c_void_p),
+                                      cfg.n_layers, 1 if cfg.xscaling else 0, cfg.n_mels, self.cache_len,
+                                      int(cfg.stream_drop_extra_pre_encoded), self.valid_out_len)
+
+    def reset(self):
+        lib().orc_stream_reset(self.h)
+
+    def step(self, mel_window, is_last=False):
+        w = f32(mel_window)
+        F, n = w.shape
+        tc = lib().orc_stream_chunk_len(self.h, n)
+        out = np.empty((max(tc, 1), self.cfg.d_model), dtype=np.float32)
+        nv = lib().orc_stream_step(self.h, fp(w), n, 1 if is_last else 0, fp(out))
+        return out[:nv].copy()
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().orc_stream_free(self.h)
+            self.h = None
+
+
+def stream_windows(T, chunk_first, chunk, pre_cache):
+    """The CacheAwareStreamingAudioBuffer chunk schedule (tests/test_streaming_encoder.cpp:68-99):
+    (lo, hi, is_last) mel windows, the first without overlap, later ones with
+    pre_cache frames of the previous window in front."""
+    out = []
+    idx, first = 0, True
+    while idx < T:
+        size = chunk_first if first else chunk
+        hi = min(idx + size, T)
+        if hi - idx <= 0:
+            break
+        lo = idx if first else max(0, idx - pre_cache)
+        out.append((lo, hi, hi >= T))
+        idx += size
+        first = False
+    return out
 
 
 def ctc_greedy(argmax, blank_id):

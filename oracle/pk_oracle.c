@@ -441,6 +441,8 @@ void orc_relpos_attention(const orc_layer* L, const float* x, int B, int T,
     const int D = L->D, H = L->H, dk = D / H, P = 2 * T - 1;
     const int64_t M = (int64_t)B * T;
     const float scale = 1.0f / sqrtf((float)dk);
+    const int chunk = L->att_limited ? L->att_right + 1 : 1;   /* relpos_attention.cpp:30-38 */
+    const int left_chunks = L->att_limited ? L->att_left / chunk : 0;
     float* q = fbuf((size_t)M * D);
     float* k = fbuf((size_t)M * D);
     float* v = fbuf((size_t)M * D);
@@ -474,6 +476,10 @@ void orc_relpos_attention(const orc_layer* L, const float* x, int B, int T,
                     double mx = -INFINITY;
                     for (int j = 0; j < T; ++j) {
                         if (j >= vl) { sc[j] = -INFINITY; continue; }   /* :252-277 key mask */
+                        if (L->att_limited) {                 /* :252-270 chunked-limited window */
+                            const int diff = i / chunk - j / chunk;
+                            if (diff < 0 || diff > left_chunks) { sc[j] = -INFINITY; continue; }
+                        }
                         const float* kr = k + ((size_t)b * T + j) * D + (size_t)h * dk;
                         /* rel_shift (:226-238): bd_shift[i][j] = bd[i][T-1-i+j] */
                         const float* pr = p + (size_t)(T - 1 - i + j) * D + (size_t)h * dk;
@@ -501,12 +507,13 @@ void orc_relpos_attention(const orc_layer* L, const float* x, int B, int T,
 }
 
 /* ------------------------------------------------------------------------ */
-/* Conv module: conformer.cpp:38-164 (batch_norm variant, symmetric pad)     */
+/* Conv module: conformer.cpp:38-164 (symmetric or causal depthwise pad,    */
+/* batch_norm or layer_norm between the depthwise conv and SiLU)             */
 /* ------------------------------------------------------------------------ */
 
 void orc_conv_module(const orc_layer* L, const float* c, int B, int T,
                      const int* valid, float* out) {
-    const int D = L->D, K = L->K, pad = (K - 1) / 2;
+    const int D = L->D, K = L->K, pad = L->conv_causal ? K - 1 : (K - 1) / 2;   /* :100-116 */
     const int64_t M = (int64_t)B * T;
     float* y = fbuf((size_t)M * 2 * D);
     float* g = fbuf((size_t)M * D);
@@ -523,7 +530,7 @@ void orc_conv_module(const orc_layer* L, const float* c, int B, int T,
             g[m * D + ch] = (t < vl) ? a * sigmoid_f(gate) : 0.f;
         }
     }
-    for (int ch = 0; ch < D; ++ch) {                           /* :134-154 BN fold */
+    for (int ch = 0; ch < D && !L->conv_ln; ++ch) {            /* :134-154 BN fold */
         bsc[ch] = L->bn_g[ch] / sqrtf(L->bn_var[ch] + 1e-5f);
         bsh[ch] = L->bn_b[ch] - L->bn_mean[ch] * bsc[ch];
     }
@@ -538,10 +545,18 @@ void orc_conv_module(const orc_layer* L, const float* c, int B, int T,
                     acc += L->dw_w[ch * K + kk] * g[((size_t)b * T + ts) * D + ch];
                 }
                 if (L->dw_b) acc += L->dw_b[ch];
+                if (L->conv_ln) {                              /* normalised below */
+                    n[((size_t)b * T + t) * D + ch] = acc;
+                    continue;
+                }
                 float nv = acc * bsc[ch];
                 nv = nv + bsh[ch];
                 n[((size_t)b * T + t) * D + ch] = silu_f(nv);
             }
+    if (L->conv_ln) {                                          /* :128-133 norm over channels, SiLU */
+        orc_layer_norm(n, M, D, L->bn_g, L->bn_b, 1e-5f, n);
+        for (int64_t i = 0; i < M * D; ++i) n[i] = silu_f(n[i]);
+    }
     orc_linear(n, M, D, L->pw2_w, D, L->pw2_b, out);          /* :158-162 */
     free(y); free(g); free(n); free(bsc); free(bsh);
 }
@@ -594,31 +609,36 @@ void orc_conformer_layer(const orc_layer* L, const float* x, int B, int T,
 /* Subsampling: subsampling.cpp:25-46, :48-240, :242-386                     */
 /* ------------------------------------------------------------------------ */
 
-int orc_subsampled_len(int T) {
+/* all_paddings = 2 (symmetric) or 3 (causal: 2 before, 1 after), k 3, s 2 */
+int orc_subsampled_len_c(int T, int causal) {
     int t = T;
-    for (int s = 0; s < 3; ++s) t = (t + 2 - 3) / 2 + 1;
+    for (int s = 0; s < 3; ++s) t = (t + (causal ? 3 : 2) - 3) / 2 + 1;
     return t;
 }
 
-int orc_valid_out_len(int T, int in_valid) {
+int orc_valid_out_len_c(int T, int in_valid, int causal) {
     int v = in_valid >= 0 ? in_valid : T - 1;
-    for (int s = 0; s < 3; ++s) v = (v + 2 - 3) / 2 + 1;
+    for (int s = 0; s < 3; ++s) v = (v + (causal ? 3 : 2) - 3) / 2 + 1;
     return v;
 }
 
-/* 3x3 stride-2 pad-1 depthwise conv over a channels-last [Ti][Fi][C] map,
- * reading rows t >= vmask as zero; output channels-last [To][Fo][C] + bias. */
-static void dw3x3s2(const float* in, int Ti, int Fi, int C, int vmask,
+int orc_subsampled_len(int T) { return orc_subsampled_len_c(T, 0); }
+int orc_valid_out_len(int T, int in_valid) { return orc_valid_out_len_c(T, in_valid, 0); }
+
+/* 3x3 stride-2 depthwise conv (pad pl before each axis) over a channels-last
+ * [Ti][Fi][C] map, reading rows t >= vmask as zero; output channels-last
+ * [To][Fo][C] + bias. */
+static void dw3x3s2(const float* in, int Ti, int Fi, int C, int vmask, int pl,
                     const float* w, const float* bias, float* out, int To, int Fo) {
     for (int t = 0; t < To; ++t)
         for (int f = 0; f < Fo; ++f)
             for (int c = 0; c < C; ++c) {
                 float acc = 0.f;
                 for (int kh = 0; kh < 3; ++kh) {
-                    const int ti = 2 * t - 1 + kh;
+                    const int ti = 2 * t - pl + kh;
                     if (ti < 0 || ti >= Ti || ti >= vmask) continue;
                     for (int kw = 0; kw < 3; ++kw) {
-                        const int fi = 2 * f - 1 + kw;
+                        const int fi = 2 * f - pl + kw;
                         if (fi < 0 || fi >= Fi) continue;
                         acc += w[c * 9 + kh * 3 + kw] * in[((size_t)ti * Fi + fi) * C + c];
                     }
@@ -631,14 +651,18 @@ int orc_subsampling(const orc_subsampling_w* S, const float* mel, int B, int F,
                     int T, const int* valid_in, int stage_masks, float* out,
                     int* valid_out) {
     const int C = S->C, D = S->D;
-    const int T1 = (T - 1) / 2 + 1, F1 = (F - 1) / 2 + 1;
-    const int T2 = (T1 - 1) / 2 + 1, F2 = (F1 - 1) / 2 + 1;
-    const int T3 = (T2 - 1) / 2 + 1, F3 = (F2 - 1) / 2 + 1;
+    /* causal (subsampling.cpp:81-99): pad 2 before / 1 after on time and
+     * feature axes, per-stage input time masks on every path (:100-147, :283-300) */
+    const int cz = S->causal, pl = cz ? 2 : 1, ap = cz ? 3 : 2;
+    if (cz) stage_masks = 1;
+    const int T1 = (T + ap - 3) / 2 + 1, F1 = (F + ap - 3) / 2 + 1;
+    const int T2 = (T1 + ap - 3) / 2 + 1, F2 = (F1 + ap - 3) / 2 + 1;
+    const int T3 = (T2 + ap - 3) / 2 + 1, F3 = (F2 + ap - 3) / 2 + 1;
     float* flat = fbuf((size_t)B * T3 * C * F3);
     for (int b = 0; b < B; ++b) {
         const int v0 = valid_in ? valid_in[b] : T - 1;
-        const int v1 = (v0 + 2 - 3) / 2 + 1, v2 = (v1 + 2 - 3) / 2 + 1;
-        const int vo = orc_valid_out_len(T, valid_in ? valid_in[b] : -1);
+        const int v1 = (v0 + ap - 3) / 2 + 1, v2 = (v1 + ap - 3) / 2 + 1;
+        const int vo = orc_valid_out_len_c(T, valid_in ? valid_in[b] : -1, cz);
         valid_out[b] = vo > T3 ? T3 : vo;
         const int m0 = stage_masks ? v0 : T, m1 = stage_masks ? v1 : T1, m2 = stage_masks ? v2 : T2;
         const float* mb = mel + (size_t)b * F * T;
@@ -654,10 +678,10 @@ int orc_subsampling(const orc_subsampling_w* S, const float* mel, int B, int F,
                 for (int c = 0; c < C; ++c) {
                     float acc = 0.f;
                     for (int kh = 0; kh < 3; ++kh) {
-                        const int ti = 2 * t - 1 + kh;
+                        const int ti = 2 * t - pl + kh;
                         if (ti < 0 || ti >= T || ti >= m0) continue;
                         for (int kw = 0; kw < 3; ++kw) {
-                            const int fi = 2 * f - 1 + kw;
+                            const int fi = 2 * f - pl + kw;
                             if (fi < 0 || fi >= F) continue;
                             acc += S->w0[c * 9 + kh * 3 + kw] * mb[(size_t)fi * T + ti];
                         }
@@ -666,11 +690,11 @@ int orc_subsampling(const orc_subsampling_w* S, const float* mel, int B, int F,
                     a1[((size_t)t * F1 + f) * C + c] = acc > 0.f ? acc : 0.f;
                 }
         /* conv.2 depthwise + bias, conv.3 pointwise + bias + ReLU (:159-192) */
-        dw3x3s2(a1, T1, F1, C, m1, S->w2, S->b2, a2, T2, F2);
+        dw3x3s2(a1, T1, F1, C, m1, pl, S->w2, S->b2, a2, T2, F2);
         orc_linear(a2, (int64_t)T2 * F2, C, S->w3, C, S->b3, a2p);
         for (size_t i = 0; i < (size_t)T2 * F2 * C; ++i) a2p[i] = a2p[i] > 0.f ? a2p[i] : 0.f;
         /* conv.5 depthwise + bias, conv.6 pointwise + bias + ReLU */
-        dw3x3s2(a2p, T2, F2, C, m2, S->w5, S->b5, a3, T3, F3);
+        dw3x3s2(a2p, T2, F2, C, m2, pl, S->w5, S->b5, a3, T3, F3);
         orc_linear(a3, (int64_t)T3 * F3, C, S->w6, C, S->b6, a3p);
         for (size_t i = 0; i < (size_t)T3 * F3 * C; ++i) a3p[i] = a3p[i] > 0.f ? a3p[i] : 0.f;
         /* flatten channel-major per time step (idx c*F'+f, :194-202) + mask (:204-230) */
@@ -695,7 +719,7 @@ int orc_encoder_forward(const orc_subsampling_w* S, const orc_layer* layers,
                         int F, int T, const int* valid_in, int stage_masks,
                         float* out, int* valid_out, float* capture) {
     const int D = S->D;
-    const int Tp = orc_subsampled_len(T);
+    const int Tp = orc_subsampled_len_c(T, S->causal);
     const size_t MD = (size_t)B * Tp * D;
     float* x = fbuf(MD);
     float* y = fbuf(MD);
@@ -714,6 +738,186 @@ int orc_encoder_forward(const orc_subsampling_w* S, const orc_layer* layers,
     memcpy(out, x, MD * sizeof(float));
     free(x); free(y); free(pe);
     return Tp;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Cache-aware streaming encoder: streaming_encoder.cpp:29-96 (state),       */
+/* :98-338 (one layer with its caches), :340-462 (step)                      */
+/* ------------------------------------------------------------------------ */
+
+struct orc_stream {
+    const orc_subsampling_w* S;
+    const orc_layer* layers;
+    int n_layers, xscaling, F, D, K;
+    int cache_len, drop_extra, valid_out_len;
+    int step, clc_len;
+    float* cache_ch;   /* [L][cache_len][D]: norm_self_att outputs of earlier frames */
+    float* cache_t;    /* [L][K-1][D]: GLU outputs of earlier frames */
+};
+
+orc_stream* orc_stream_new(const orc_subsampling_w* S, const orc_layer* layers, int n_layers,
+                           int xscaling, int F, int cache_len, int drop_extra, int valid_out_len) {
+    orc_stream* st = (orc_stream*)calloc(1, sizeof(orc_stream));
+    st->S = S; st->layers = layers; st->n_layers = n_layers; st->xscaling = xscaling;
+    st->F = F; st->D = S->D; st->K = layers[0].K;
+    st->cache_len = cache_len; st->drop_extra = drop_extra; st->valid_out_len = valid_out_len;
+    st->cache_ch = fbuf((size_t)n_layers * cache_len * st->D);
+    st->cache_t = fbuf((size_t)n_layers * (st->K - 1) * st->D);
+    orc_stream_reset(st);
+    return st;
+}
+
+void orc_stream_free(orc_stream* st) {
+    if (!st) return;
+    free(st->cache_ch); free(st->cache_t); free(st);
+}
+
+void orc_stream_reset(orc_stream* st) {                       /* :72-79 zeros */
+    st->step = 0; st->clc_len = 0;
+    memset(st->cache_ch, 0, sizeof(float) * (size_t)st->n_layers * st->cache_len * st->D);
+    memset(st->cache_t, 0, sizeof(float) * (size_t)st->n_layers * (st->K - 1) * st->D);
+}
+
+int orc_stream_chunk_len(const orc_stream* st, int n) {      /* :350-366 */
+    const int drop = st->step != 0 ? st->drop_extra : 0;
+    const int tc = orc_subsampled_len_c(n, 1) - drop;
+    return tc < 0 ? 0 : tc;
+}
+
+/* One conformer layer of the chunk x [Tc][D] with its caches; out [Tc][D]. */
+static void stream_layer(const orc_layer* L, const float* x, int Tc, const float* pe, int CL, int clc,
+                         float* cache_ch, float* cache_t, float* out) {
+    const int D = L->D, H = L->H, dk = D / H, K = L->K, LP = K - 1, FF = L->FF;
+    const int Tk = CL + Tc, P = 2 * Tk - 1;
+    const size_t MD = (size_t)Tc * D;
+    const float scale = 1.0f / sqrtf((float)dk);
+    float* r = fbuf(MD);
+    float* t1 = fbuf(MD);
+    float* t2 = fbuf(MD);
+    float* ain = fbuf(MD);
+    /* stage A (:139-144): r = x + 0.5 FFN1(LN(x)); attn_in = norm_self_att(r) */
+    orc_layer_norm(x, Tc, D, L->ff1_ln_g, L->ff1_ln_b, 1e-5f, t1);
+    ffn(t1, Tc, D, FF, L->ff1_w1, L->ff1_b1, L->ff1_w2, L->ff1_b2, t2);
+    for (size_t i = 0; i < MD; ++i) r[i] = x[i] + t2[i] * 0.5f;
+    orc_layer_norm(r, Tc, D, L->att_ln_g, L->att_ln_b, 1e-5f, ain);
+    /* stage B (:146-245): K/V over [cache ; attn_in], Q over attn_in */
+    float* kv = fbuf((size_t)Tk * D);
+    memcpy(kv, cache_ch, sizeof(float) * (size_t)CL * D);
+    memcpy(kv + (size_t)CL * D, ain, sizeof(float) * MD);
+    float* q = fbuf(MD);
+    float* k = fbuf((size_t)Tk * D);
+    float* v = fbuf((size_t)Tk * D);
+    float* p = fbuf((size_t)P * D);
+    float* ctx = fbuf(MD);
+    orc_linear(ain, Tc, D, L->wq, D, L->bq, q);
+    orc_linear(kv, Tk, D, L->wk, D, L->bk, k);
+    orc_linear(kv, Tk, D, L->wv, D, L->bv, v);
+    orc_linear(pe, P, D, L->wpos, D, NULL, p);
+    /* mask (:196-222): leading cache_len - clc keys empty; chunked-limited
+     * window over key kj and query cache_len + qi */
+    const int chunk = L->att_right + 1, left_chunks = chunk > 0 ? L->att_left / chunk : 0;
+    const int empty = CL - clc;
+    double* sc = (double*)malloc(sizeof(double) * (size_t)Tk);
+    for (int h = 0; h < H; ++h)
+        for (int i = 0; i < Tc; ++i) {
+            const float* qr = q + (size_t)i * D + (size_t)h * dk;
+            double mx = -INFINITY;
+            for (int j = 0; j < Tk; ++j) {
+                const int cq = (CL + i) / chunk, ck = j / chunk, diff = cq - ck;
+                if (j < empty || diff < 0 || diff > left_chunks) { sc[j] = -INFINITY; continue; }
+                /* rel_shift of a [Tc][P] score block (:180-190): column Tc-1-i+j */
+                const float* kr = k + (size_t)j * D + (size_t)h * dk;
+                const float* pr = p + (size_t)(Tc - 1 - i + j) * D + (size_t)h * dk;
+                float ac = 0.f, bd = 0.f;
+                for (int c = 0; c < dk; ++c) {
+                    ac += (qr[c] + L->pos_bias_u[h * dk + c]) * kr[c];
+                    bd += (qr[c] + L->pos_bias_v[h * dk + c]) * pr[c];
+                }
+                sc[j] = (double)((ac + bd) * scale);
+                if (sc[j] > mx) mx = sc[j];
+            }
+            double den = 0.0;
+            for (int j = 0; j < Tk; ++j) { sc[j] = exp(sc[j] - mx); den += sc[j]; }
+            for (int c = 0; c < dk; ++c) {
+                double acc = 0.0;
+                for (int j = 0; j < Tk; ++j) acc += sc[j] * v[(size_t)j * D + (size_t)h * dk + c];
+                ctx[(size_t)i * D + (size_t)h * dk + c] = (float)(acc / den);
+            }
+        }
+    free(sc);
+    orc_linear(ctx, Tc, D, L->wo, D, L->bo, t2);
+    for (size_t i = 0; i < MD; ++i) r[i] += t2[i];
+    /* next attention cache (:247-266): the last CL rows of [cache ; attn_in] */
+    memcpy(cache_ch, kv + (size_t)Tc * D, sizeof(float) * (size_t)CL * D);
+    /* stage C (:268-330): conv module over [conv cache ; GLU] */
+    orc_layer_norm(r, Tc, D, L->conv_ln_g, L->conv_ln_b, 1e-5f, t1);
+    float* y = fbuf((size_t)Tc * 2 * D);
+    orc_linear(t1, Tc, D, L->pw1_w, 2 * D, L->pw1_b, y);
+    float* dwin = fbuf((size_t)(LP + Tc) * D);
+    memcpy(dwin, cache_t, sizeof(float) * (size_t)LP * D);
+    for (int t = 0; t < Tc; ++t)
+        for (int ch = 0; ch < D; ++ch)
+            dwin[(size_t)(LP + t) * D + ch] = y[(size_t)t * 2 * D + ch] * sigmoid_f(y[(size_t)t * 2 * D + D + ch]);
+    memcpy(cache_t, dwin + (size_t)Tc * D, sizeof(float) * (size_t)LP * D);
+    for (int t = 0; t < Tc; ++t)
+        for (int ch = 0; ch < D; ++ch) {
+            float acc = 0.f;
+            for (int kk = 0; kk < K; ++kk) acc += L->dw_w[ch * K + kk] * dwin[(size_t)(t + kk) * D + ch];
+            if (L->dw_b) acc += L->dw_b[ch];
+            t2[(size_t)t * D + ch] = acc;
+        }
+    if (L->conv_ln) {
+        orc_layer_norm(t2, Tc, D, L->bn_g, L->bn_b, 1e-5f, t2);
+    } else {
+        for (int t = 0; t < Tc; ++t)
+            for (int ch = 0; ch < D; ++ch) {
+                const float sc1 = L->bn_g[ch] / sqrtf(L->bn_var[ch] + 1e-5f);
+                const float sh1 = L->bn_b[ch] - L->bn_mean[ch] * sc1;
+                t2[(size_t)t * D + ch] = t2[(size_t)t * D + ch] * sc1 + sh1;
+            }
+    }
+    for (size_t i = 0; i < MD; ++i) t2[i] = silu_f(t2[i]);
+    orc_linear(t2, Tc, D, L->pw2_w, D, L->pw2_b, t1);
+    for (size_t i = 0; i < MD; ++i) r[i] += t1[i];
+    /* stage D (:332-337) */
+    orc_layer_norm(r, Tc, D, L->ff2_ln_g, L->ff2_ln_b, 1e-5f, t1);
+    ffn(t1, Tc, D, FF, L->ff2_w1, L->ff2_b1, L->ff2_w2, L->ff2_b2, t2);
+    for (size_t i = 0; i < MD; ++i) r[i] += t2[i] * 0.5f;
+    orc_layer_norm(r, Tc, D, L->out_ln_g, L->out_ln_b, 1e-5f, out);
+    free(r); free(t1); free(t2); free(ain); free(kv); free(q); free(k); free(v); free(p); free(ctx);
+    free(y); free(dwin);
+}
+
+int orc_stream_step(orc_stream* st, const float* mel, int n, int is_last, float* out) {
+    const int D = st->D, CL = st->cache_len;
+    const int drop = st->step != 0 ? st->drop_extra : 0;
+    const int Tsub = orc_subsampled_len_c(n, 1);
+    const int Tc = orc_stream_chunk_len(st, n);
+    if (Tc == 0) { st->step += 1; return 0; }                 /* :367-371 */
+    float* sx = fbuf((size_t)Tsub * D);
+    int vo = 0;
+    orc_subsampling(st->S, mel, 1, st->F, n, &n, 1, sx, &vo);   /* whole window is audio */
+    float* x = fbuf((size_t)Tc * D);
+    float* y = fbuf((size_t)Tc * D);
+    memcpy(x, sx + (size_t)drop * D, sizeof(float) * (size_t)Tc * D);
+    if (st->xscaling) {
+        const float s = sqrtf((float)D);
+        for (size_t i = 0; i < (size_t)Tc * D; ++i) x[i] *= s;
+    }
+    const int Pn = Tc + CL;                                    /* :376-381 */
+    float* pe = fbuf((size_t)(2 * Pn - 1) * D);
+    orc_rel_pos_encoding(Pn, D, pe);
+    for (int l = 0; l < st->n_layers; ++l) {
+        stream_layer(&st->layers[l], x, Tc, pe, CL, st->clc_len, st->cache_ch + (size_t)l * CL * D,
+                     st->cache_t + (size_t)l * (st->K - 1) * D, y);
+        float* tmp = x; x = y; y = tmp;
+    }
+    st->clc_len = st->clc_len + Tc < CL ? st->clc_len + Tc : CL;  /* :447-448 */
+    st->step += 1;
+    const int valid = is_last ? Tc : (st->valid_out_len < Tc ? st->valid_out_len : Tc);
+    memcpy(out, x, sizeof(float) * (size_t)valid * D);
+    free(sx); free(x); free(y); free(pe);
+    return valid;
 }
 
 /* ------------------------------------------------------------------------ */

@@ -77,6 +77,11 @@ typedef struct {
     const float *pw2_w, *pw2_b;                         /* [D][D], [D] */
     const float *ff2_ln_g, *ff2_ln_b, *ff2_w1, *ff2_b1, *ff2_w2, *ff2_b2;
     const float *out_ln_g, *out_ln_b;
+    /* streaming-model variants (model_loader.cpp:110-121); zero = offline model */
+    int conv_causal;                /* depthwise conv left pad K-1, no right pad */
+    int conv_ln;                    /* conv_norm_type "layer_norm" (bn_g/bn_b as gamma/beta) */
+    int att_limited;                /* att_context_style "chunked_limited" */
+    int att_left, att_right;        /* att_context_size [left, right] */
 } orc_layer;
 
 /* dw_striding subsampling weights (torch layouts == GGUF memory order). */
@@ -88,6 +93,7 @@ typedef struct {
     const float *w5, *b5;          /* conv.5  depthwise */
     const float *w6, *b6;          /* conv.6  pointwise */
     const float *wout, *bout;      /* out     [D][C*F'], [D] */
+    int causal;                    /* causal_downsampling: pad 2 before, 1 after on both axes */
 } orc_subsampling_w;
 
 /* relpos_attention.cpp:162-306 (batched) / :40-160 (B=1).  x is the already
@@ -105,9 +111,11 @@ void orc_conformer_layer(const orc_layer* L, const float* x, int B, int T,
                          const float* pe, const int* valid, float* out,
                          float* conv_out);
 
-/* subsampling.cpp:25-46 */
+/* subsampling.cpp:25-46 (all_paddings 2; _c: 3 when causal) */
 int  orc_valid_out_len(int T, int in_valid);
 int  orc_subsampled_len(int T);
+int  orc_valid_out_len_c(int T, int in_valid, int causal);
+int  orc_subsampled_len_c(int T, int causal);
 
 /* subsampling.cpp:48-240 (stage_masks=1, batched semantics) and :242-386
  * (stage_masks=0, scalar semantics).  mel [B][F][T]; valid_in[b] is the entry
@@ -122,6 +130,22 @@ int  orc_encoder_forward(const orc_subsampling_w* S, const orc_layer* layers,
                          int n_layers, int xscaling, const float* mel, int B,
                          int F, int T, const int* valid_in, int stage_masks,
                          float* out, int* valid_out, float* capture);
+
+/* ---- cache-aware streaming encoder (streaming_encoder.cpp) ---------------- */
+/* StreamingEncoder state (streaming_encoder.hpp:55-95): per layer the
+ * attention cache of norm_self_att outputs [cache_len][D] and the depthwise
+ * conv cache of GLU outputs [K-1][D], time-major, zero at reset. */
+typedef struct orc_stream orc_stream;
+orc_stream* orc_stream_new(const orc_subsampling_w* S, const orc_layer* layers, int n_layers,
+                           int xscaling, int F, int cache_len, int drop_extra, int valid_out_len);
+void orc_stream_free(orc_stream* st);
+void orc_stream_reset(orc_stream* st);
+/* StreamingEncoder::step (streaming_encoder.cpp:340-462): mel window [F][n]
+ * (pre-encode overlap included); writes the kept frames [n_valid][D] to out
+ * (capacity: the window's subsampled length) and returns n_valid. */
+int  orc_stream_step(orc_stream* st, const float* mel, int n, int is_last, float* out);
+/* The chunk output length before the valid slice (0 when the window is too short). */
+int  orc_stream_chunk_len(const orc_stream* st, int n);
 
 /* ctc_decoder.cpp:34-116 -- log_softmax(enc . W^T + b) over V, enc [T][D]
  * time-major; argmax with first-max tie-break (search.cpp:57-61). */

@@ -77,16 +77,48 @@ class Config:
     mag_power: float = 2.0
     normalize: str = "per_feature"
     log_zero_guard: float = 2.0 ** -24
+    # cache-aware streaming models (src/model_loader.cpp:110-131; the
+    # parakeet_realtime_eou_120m-v1 values are conv_norm_type "layer_norm",
+    # causal subsampling and conv, att_context [70, 1] "chunked_limited",
+    # chunk [9, 16], pre-encode cache [0, 9], cache 70, valid_out_len 2, drop 2)
+    conv_norm_type: str = "batch_norm"
+    causal_downsampling: bool = False
+    conv_causal: bool = False
+    att_context_style: str = "regular"
+    att_context_left: int = -1
+    att_context_right: int = -1
+    stream_chunk_size: tuple = (9, 16)
+    stream_shift_size: tuple = (9, 16)
+    stream_pre_encode_cache_size: tuple = (0, 9)
+    stream_last_channel_cache_size: int = 70
+    stream_valid_out_len: int = 2
+    stream_drop_extra_pre_encoded: int = 2
 
     @property
     def d_head(self):
         return self.d_model // self.n_heads
 
+    @property
+    def streaming(self):
+        return self.att_context_style != "regular"
+
     def sub_feat(self):
         f = self.n_mels
+        ap = 3 if self.causal_downsampling else 2
         for _ in range(3):
-            f = (f - 1) // 2 + 1
+            f = (f + ap - 3) // 2 + 1
         return f
+
+
+def eou_config(**kw) -> "Config":
+    """The cache-aware streaming model's architecture (parakeet_realtime_eou_120m-v1:
+    512 / 17 layers / 8 heads, ff 2048, conv 9, 256 subsampling channels, 128 mel)."""
+    base = dict(d_model=512, n_layers=17, n_heads=8, ff_dim=2048, conv_kernel=9, n_mels=128,
+                sub_channels=256, xscaling=False, vocab_size=1026, tdt_durations=(), arch="rnnt",
+                conv_norm_type="layer_norm", causal_downsampling=True, conv_causal=True,
+                att_context_style="chunked_limited", att_context_left=70, att_context_right=1)
+    base.update(kw)
+    return Config(**base)
 
 
 @dataclass
@@ -134,9 +166,10 @@ def _layer_names(cfg: Config, i: int):
             (p + "conv.depthwise_conv.weight", (D, 1, K), "w"),
             (p + "conv.pointwise_conv2.weight", (D, D, 1), "w"),
             (p + "conv.batch_norm.weight", (D,), "ln_g"),
-            (p + "conv.batch_norm.bias", (D,), "ln_b"),
-            (p + "conv.batch_norm.running_mean", (D,), "bn_mean"),
-            (p + "conv.batch_norm.running_var", (D,), "bn_var")]
+            (p + "conv.batch_norm.bias", (D,), "ln_b")]
+    if cfg.conv_norm_type != "layer_norm":
+        out += [(p + "conv.batch_norm.running_mean", (D,), "bn_mean"),
+                (p + "conv.batch_norm.running_var", (D,), "bn_var")]
     if cfg.conv_bias:
         out += [(p + "conv.pointwise_conv1.bias", (2 * D,), "b"),
                 (p + "conv.depthwise_conv.bias", (D,), "b"),
@@ -313,7 +346,7 @@ def _kv_items(cfg: Config):
           (e + "feat_in", _GT_U32, cfg.n_mels), (e + "d_model", _GT_U32, cfg.d_model),
           (e + "n_layers", _GT_U32, cfg.n_layers), (e + "n_heads", _GT_U32, cfg.n_heads),
           (e + "ff_dim", _GT_U32, cfg.ff_dim), (e + "conv_kernel", _GT_U32, cfg.conv_kernel),
-          (e + "conv_norm_type", _GT_STR, "batch_norm"),
+          (e + "conv_norm_type", _GT_STR, cfg.conv_norm_type),
           (e + "subsampling_factor", _GT_U32, 8),
           (e + "subsampling_conv_channels", _GT_U32, cfg.sub_channels),
           (e + "xscaling", _GT_BOOL, bool(cfg.xscaling)),
@@ -333,6 +366,20 @@ def _kv_items(cfg: Config):
           ("parakeet.decoder.pred_hidden", _GT_U32, cfg.pred_hidden),
           ("parakeet.decoder.pred_rnn_layers", _GT_U32, cfg.pred_rnn_layers),
           ("parakeet.tdt.durations", _GT_ARR, (_GT_I32, list(cfg.tdt_durations)))]
+    if cfg.streaming:       # scripts/convert_parakeet_to_gguf.py:176-222
+        st = "parakeet.streaming."
+        kv += [(e + "att_context_left", _GT_I32, cfg.att_context_left),
+               (e + "att_context_right", _GT_I32, cfg.att_context_right),
+               (e + "att_context_style", _GT_STR, cfg.att_context_style),
+               (e + "causal_downsampling", _GT_BOOL, bool(cfg.causal_downsampling)),
+               (e + "conv_causal", _GT_BOOL, bool(cfg.conv_causal)),
+               (st + "chunk_size", _GT_ARR, (_GT_I32, list(cfg.stream_chunk_size))),
+               (st + "shift_size", _GT_ARR, (_GT_I32, list(cfg.stream_shift_size))),
+               (st + "cache_drop_size", _GT_I32, 0),
+               (st + "last_channel_cache_size", _GT_I32, cfg.stream_last_channel_cache_size),
+               (st + "valid_out_len", _GT_I32, cfg.stream_valid_out_len),
+               (st + "pre_encode_cache_size", _GT_ARR, (_GT_I32, list(cfg.stream_pre_encode_cache_size))),
+               (st + "drop_extra_pre_encoded", _GT_I32, cfg.stream_drop_extra_pre_encoded)]
     return kv
 
 
