@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define PKX_ABI_VERSION 1
+#define PKX_ABI_VERSION 2
 
 typedef struct pkx_model pkx_model;
 
@@ -63,6 +63,15 @@ typedef struct {
     int xscaling;        /* parakeet.encoder.xscaling */
     int vocab_size;      /* parakeet.vocab_size (CTC/TDT heads: vocab_size + 1 tokens) */
     int n_durations;     /* len(parakeet.tdt.durations), 0 if no TDT head */
+    /* cache-aware streaming models (src/model_loader.cpp:110-131); all zero
+     * (att_left/att_right -1) for offline models */
+    int conv_ln;         /* parakeet.encoder.conv_norm_type == "layer_norm" */
+    int causal_sub;      /* parakeet.encoder.causal_downsampling */
+    int conv_causal;     /* parakeet.encoder.conv_causal */
+    int att_limited;     /* att_context_style == "chunked_limited" and att_right >= 0 */
+    int att_left, att_right;
+    int stream_chunk_first, stream_chunk, stream_pre_cache;   /* parakeet.streaming.*: mel frames */
+    int stream_cache_len, stream_valid_out_len, stream_drop_extra;
 } pkx_config;
 
 /* ---- status ---------------------------------------------------------------- */
@@ -204,6 +213,34 @@ int pkx_rel_pos_encoding(int T, int D, float* out_dev, void* stream);
 int pkx_transducer_greedy(pkx_model* m, const float* enc_dev, int B, int T_max, const int* T_valid,
                           const int32_t* durations, int n_durations, int blank_id, int max_symbols, int cap,
                           int32_t* ids, int32_t* frames, float* conf, int32_t* span, int* counts, void* stream);
+
+/* ---- cache-aware streaming encoder --------------------------------------------
+ * pk::StreamingEncoder (src/streaming_encoder.hpp:33-95, .cpp:340-462) for
+ * models with a streaming configuration (pkx_config.att_limited and the causal
+ * flags; the GGUF's parakeet.streaming.* keys), for n_streams streams advanced
+ * together (each its own caches; all take windows of the same length).  The
+ * model must outlive the handle; one handle is not re-entrant. */
+typedef struct pkx_streaming pkx_streaming;
+/* StreamingEncoder::StreamingEncoder + reset(): windows of at most max_window
+ * mel frames (pre-encode overlap included; at most 255). */
+int pkx_streaming_create(pkx_model* m, int n_streams, int max_window, void* stream, pkx_streaming** out);
+int pkx_streaming_free(pkx_streaming* st);
+/* StreamingEncoder::reset (:72-79): zero caches, step 0. */
+int pkx_streaming_reset(pkx_streaming* st, void* stream);
+/* chunk_size_first / chunk_size / pre_encode_cache_size / valid_out_len /
+ * step_num (streaming_encoder.hpp:62-67); NULL outputs are skipped. */
+int pkx_streaming_info(const pkx_streaming* st, int* chunk_first, int* chunk, int* pre_cache, int* valid_out_len,
+                       int* step);
+/* Encoder frames the next step yields for a window of n mel frames (before the
+ * valid slice): the subsampled length minus the drop of every step after the
+ * first (:350-366); -1 for a null handle. */
+int pkx_streaming_chunk_len(const pkx_streaming* st, int n_mel_frames);
+/* StreamingEncoder::step for every stream: mel_dev [n_streams][n_mels][n]
+ * f32; out_dev [n_streams][chunk_len][d_model] f32 receives every chunk frame,
+ * of which the first *n_valid are the step's output (valid_out_len mid-stream,
+ * all on the last chunk: keep_all_outputs). */
+int pkx_streaming_step(pkx_streaming* st, const float* mel_dev, int n_mel_frames, int is_last, float* out_dev,
+                       int* n_valid, void* stream);
 
 /* ---- log-mel front end --------------------------------------------------------
  * pk::MelFrontend::compute (src/mel.hpp:33-41, src/mel.cpp:99-185) for a batch

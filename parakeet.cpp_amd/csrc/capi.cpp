@@ -19,6 +19,11 @@ struct pkx_model {
     std::unique_ptr<pkx::Model> impl;
 };
 
+struct pkx_streaming {
+    pkx::Model* model;
+    std::unique_ptr<pkx::StreamState> st;
+};
+
 namespace {
 thread_local std::string g_last_error;
 
@@ -55,6 +60,18 @@ pkx::ModelConfig to_internal(const pkx_config& c) {
     m.xscaling = c.xscaling;
     m.vocab_size = c.vocab_size;
     m.n_durations = c.n_durations;
+    m.conv_ln = c.conv_ln;
+    m.causal_sub = c.causal_sub;
+    m.conv_causal = c.conv_causal;
+    m.att_limited = c.att_limited;
+    m.att_left = c.att_left;
+    m.att_right = c.att_right;
+    m.stream_chunk_first = c.stream_chunk_first;
+    m.stream_chunk = c.stream_chunk;
+    m.stream_pre_cache = c.stream_pre_cache;
+    m.stream_cache_len = c.stream_cache_len;
+    m.stream_valid_out_len = c.stream_valid_out_len;
+    m.stream_drop_extra = c.stream_drop_extra;
     return m;
 }
 
@@ -70,6 +87,18 @@ pkx_config to_public(const pkx::ModelConfig& m) {
     c.xscaling = m.xscaling;
     c.vocab_size = m.vocab_size;
     c.n_durations = m.n_durations;
+    c.conv_ln = m.conv_ln;
+    c.causal_sub = m.causal_sub;
+    c.conv_causal = m.conv_causal;
+    c.att_limited = m.att_limited;
+    c.att_left = m.att_left;
+    c.att_right = m.att_right;
+    c.stream_chunk_first = m.stream_chunk_first;
+    c.stream_chunk = m.stream_chunk;
+    c.stream_pre_cache = m.stream_pre_cache;
+    c.stream_cache_len = m.stream_cache_len;
+    c.stream_valid_out_len = m.stream_valid_out_len;
+    c.stream_drop_extra = m.stream_drop_extra;
     return c;
 }
 }  // namespace
@@ -338,6 +367,44 @@ int pkx_transducer_greedy(pkx_model* m, const float* enc, int B, int T_max, cons
         need(m && enc, "null argument");
         m->impl->transducer_greedy(enc, B, T_max, T_valid, durations, n_durations, blank_id, max_symbols, cap, ids,
                                    frames, conf, span, counts, st(s));
+    });
+}
+int pkx_streaming_create(pkx_model* m, int n_streams, int max_window, void* s, pkx_streaming** out) {
+    return guarded([&] {
+        need(m && out, "null argument");
+        *out = nullptr;
+        std::unique_ptr<pkx_streaming> h(new pkx_streaming);
+        h->model = m->impl.get();
+        h->st = h->model->stream_create(n_streams, max_window, st(s));
+        *out = h.release();
+    });
+}
+int pkx_streaming_free(pkx_streaming* h) {
+    return guarded([&] { delete h; });
+}
+int pkx_streaming_reset(pkx_streaming* h, void* s) {
+    return guarded([&] {
+        need(h, "null argument");
+        h->model->stream_reset(*h->st, st(s));
+    });
+}
+int pkx_streaming_info(const pkx_streaming* h, int* chunk_first, int* chunk, int* pre_cache, int* valid_out_len,
+                       int* step) {
+    return guarded([&] {
+        need(h, "null argument");
+        const pkx::ModelConfig& c = h->model->config();
+        if (chunk_first) *chunk_first = c.stream_chunk_first;
+        if (chunk) *chunk = c.stream_chunk;
+        if (pre_cache) *pre_cache = c.stream_pre_cache;
+        if (valid_out_len) *valid_out_len = c.stream_valid_out_len;
+        if (step) *step = h->st->step;
+    });
+}
+int pkx_streaming_chunk_len(const pkx_streaming* h, int n) { return h ? h->model->stream_chunk_len(*h->st, n) : -1; }
+int pkx_streaming_step(pkx_streaming* h, const float* mel, int n, int is_last, float* out, int* n_valid, void* s) {
+    return guarded([&] {
+        need(h && mel && out && n_valid, "null argument");
+        *n_valid = h->model->stream_step(*h->st, mel, n, is_last != 0, out, st(s));
     });
 }
 int pkx_mel_create(const pkx_mel_config* cfg, const float* window, int window_len, const float* fb,

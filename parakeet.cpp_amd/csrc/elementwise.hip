@@ -216,14 +216,15 @@ void launch_dwconv_bn_silu(Precision prec, const void* in, void* out, const floa
 // Subsampling convs (H = time, W = feature; ggml conv layout [W,H,C,N]).
 // ---------------------------------------------------------------------------
 // Depthwise 3x3 stride-2 conv (+bias) on a channels-last map [B][Ti][Fi][C],
-// rows t >= vmask[b] read as zero.  A thread owns 8 channels (16-byte loads
+// rows t >= vmask[b] read as zero; pl = zero padding before each axis (1
+// symmetric, 2 causal, subsampling.cpp:81-99).  A thread owns 8 channels (16-byte loads
 // and stores, 32 threads cover 256 channels contiguously) and a set of output
 // columns of one output row; the 3x3 window loads hit L1/L2 for the 2.25x
 // overlap between neighbouring outputs.
 template <typename T>
 __global__ __launch_bounds__(256) void sub_dwconv_kernel(const T* in, const int* vmask, const float* w,
                                                          const float* bias, T* out, int Ti, int Fi,
-                                                         int C, int To, int Fo) {
+                                                         int C, int To, int Fo, int pl) {
     constexpr int V = 16 / sizeof(T);                  // channels per thread
     const int to = blockIdx.x, b = blockIdx.y;
     const int groups = C / V, lanes_f = blockDim.x / groups;
@@ -243,11 +244,11 @@ __global__ __launch_bounds__(256) void sub_dwconv_kernel(const T* in, const int*
         for (int e = 0; e < V; ++e) acc[e] = bb[e];
 #pragma unroll
         for (int kh = 0; kh < 3; ++kh) {
-            const int ti = 2 * to - 1 + kh;
+            const int ti = 2 * to - pl + kh;
             if (ti < 0 || ti >= Ti || ti >= vlim) continue;
 #pragma unroll
             for (int kw = 0; kw < 3; ++kw) {
-                const int fi = 2 * fo - 1 + kw;
+                const int fi = 2 * fo - pl + kw;
                 if (fi < 0 || fi >= Fi) continue;
                 const T* src = in + (((int64_t)b * Ti + ti) * Fi + fi) * C + c0;
                 T x[V];
@@ -272,20 +273,22 @@ __global__ __launch_bounds__(256) void sub_dwconv_kernel(const T* in, const int*
 // staged in LDS (zero-padded, masked at t >= valid0).  One thread per channel
 // walks the feature axis with a sliding 3-column window of conv0 values, so
 // each conv0 value is computed once per block (the row shared by the two
-// output rows included).
+// output rows included).  pl = zero padding before each axis: 1 symmetric
+// (the rows and columns above), 2 causal (subsampling.cpp:81-99: conv0 rows
+// 2 t2 - 2 .. 2 t2 + 2, mel rows 4 t2 - 6 .. 4 t2 + 4).
 template <typename T>
 __global__ __launch_bounds__(256) void sub_stage1_kernel(const float* mel, const int* valid0, const int* valid1,
                                                          const float* w0, const float* b0, const float* w2,
                                                          const float* b2, T* out, int F, int Tn, int C, int T1,
-                                                         int F1, int T2, int F2) {
-    extern __shared__ float mp[];                 // [11][4 F2 + 5]: mel columns -1 .. 4 F2 + 3
+                                                         int F1, int T2, int F2, int pl) {
+    extern __shared__ float mp[];                 // [11][4 F2 + 5]: mel columns 2 - 3 pl .. 4 F2 + 4 - 3 pl
     const int b = blockIdx.y, t2a = 2 * blockIdx.x;
     const int FP = 4 * F2 + 5;
     const int v0 = valid0 ? valid0[b] : Tn;
     const int v1 = valid1 ? valid1[b] : T1;
     for (int idx = threadIdx.x; idx < 11 * FP; idx += blockDim.x) {
-        const int j = idx / FP, fi = idx % FP - 1;
-        const int t = 4 * t2a - 3 + j;
+        const int j = idx / FP, fi = idx % FP - (3 * pl - 2);
+        const int t = 4 * t2a - 3 * pl + j;
         float v = 0.f;
         if (t >= 0 && t < Tn && t < v0 && fi >= 0 && fi < F) v = mel[((int64_t)b * F + fi) * Tn + t];
         mp[idx] = v;
@@ -294,7 +297,7 @@ __global__ __launch_bounds__(256) void sub_stage1_kernel(const float* mel, const
     bool rowok[5];
 #pragma unroll
     for (int r = 0; r < 5; ++r) {
-        const int t1 = 2 * t2a - 1 + r;
+        const int t1 = 2 * t2a - pl + r;
         rowok[r] = t1 >= 0 && t1 < T1 && t1 < v1;
     }
     const bool has_b = t2a + 1 < T2;
@@ -308,16 +311,17 @@ __global__ __launch_bounds__(256) void sub_stage1_kernel(const float* mel, const
         const float bc0 = b0[c], bc2 = b2[c];
         float prev[5];
 #pragma unroll
-        for (int r = 0; r < 5; ++r) prev[r] = 0.f;    // conv0 column f1 = -1 is padding
+        for (int r = 0; r < 5; ++r) prev[r] = 0.f;    // conv0 column f1 = -pl is padding
         for (int f2 = 0; f2 < F2; ++f2) {
-            // mel columns 4 f2 - 1 .. 4 f2 + 3 (LDS columns 4 f2 .. 4 f2 + 4) of the 11 rows
+            // mel columns 4 f2 + 2 - 3 pl .. 4 f2 + 6 - 3 pl (LDS columns 4 f2 .. 4 f2 + 4)
             float m[11][5];
 #pragma unroll
             for (int j = 0; j < 11; ++j)
 #pragma unroll
                 for (int q = 0; q < 5; ++q) m[j][q] = mp[j * FP + 4 * f2 + q];
-            float ca[5], cb[5];                       // conv0 columns f1 = 2 f2, 2 f2 + 1
-            const bool fa = 2 * f2 < F1, fb = 2 * f2 + 1 < F1;
+            float ca[5], cb[5];                       // conv0 columns f1 = 2 f2 - pl + 1, 2 f2 - pl + 2
+            const int f1a = 2 * f2 - pl + 1;
+            const bool fa = f1a >= 0 && f1a < F1, fb = f1a + 1 >= 0 && f1a + 1 < F1;
 #pragma unroll
             for (int r = 0; r < 5; ++r) {
                 float sa = bc0, sb = bc0;
@@ -347,31 +351,34 @@ __global__ __launch_bounds__(256) void sub_stage1_kernel(const float* mel, const
 
 void launch_sub_stage1(Precision prec, const float* mel, const int* valid0, const int* valid1, const float* w0,
                        const float* b0, const float* w2, const float* b2, void* out, int B, int F, int T, int C,
-                       hipStream_t s) {
-    const int T1 = (T - 1) / 2 + 1, F1 = (F - 1) / 2 + 1;
-    const int T2 = (T1 - 1) / 2 + 1, F2 = (F1 - 1) / 2 + 1;
+                       hipStream_t s, bool causal) {
+    const int T1 = sub_stage_len(T, causal), F1 = sub_stage_len(F, causal);
+    const int T2 = sub_stage_len(T1, causal), F2 = sub_stage_len(F1, causal);
+    const int pl = causal ? 2 : 1;
     const dim3 grid(cdiv(T2, 2), B);
     const int bs = C >= 256 ? 256 : ((C + 63) / 64) * 64;
     const uint32_t shm = 11u * (uint32_t)(4 * F2 + 5) * 4u;   // 4 F2 + 5 >= F + 2 covers the zero padding
     if (prec == PREC_F16)
         launch(sub_stage1_kernel<f16>, grid, dim3(bs), shm, s, mel, valid0, valid1, w0, b0, w2, b2, (f16*)out, F, T,
-               C, T1, F1, T2, F2);
+               C, T1, F1, T2, F2, pl);
     else
         launch(sub_stage1_kernel<float>, grid, dim3(bs), shm, s, mel, valid0, valid1, w0, b0, w2, b2, (float*)out,
-               F, T, C, T1, F1, T2, F2);
+               F, T, C, T1, F1, T2, F2, pl);
     PKX_LAUNCH_CHECK();
 }
 
 void launch_sub_dwconv(Precision prec, const void* in, const int* vmask, const float* w,
-                       const float* bias, void* out, int B, int Ti, int Fi, int C, hipStream_t s) {
-    const int To = (Ti - 1) / 2 + 1, Fo = (Fi - 1) / 2 + 1;
+                       const float* bias, void* out, int B, int Ti, int Fi, int C, hipStream_t s, bool causal) {
+    const int To = sub_stage_len(Ti, causal), Fo = sub_stage_len(Fi, causal), pl = causal ? 2 : 1;
     require(C % 8 == 0 && C <= 2048, "subsampling: channels must be a multiple of 8 and at most 2048");
     const dim3 grid(To, B);
     const int bs = 256;
     if (prec == PREC_F16)
-        launch(sub_dwconv_kernel<f16>, grid, dim3(bs), 0, s, (const f16*)in, vmask, w, bias, (f16*)out, Ti, Fi, C, To, Fo);
+        launch(sub_dwconv_kernel<f16>, grid, dim3(bs), 0, s, (const f16*)in, vmask, w, bias, (f16*)out, Ti, Fi, C, To,
+               Fo, pl);
     else
-        launch(sub_dwconv_kernel<float>, grid, dim3(bs), 0, s, (const float*)in, vmask, w, bias, (float*)out, Ti, Fi, C, To, Fo);
+        launch(sub_dwconv_kernel<float>, grid, dim3(bs), 0, s, (const float*)in, vmask, w, bias, (float*)out, Ti, Fi,
+               C, To, Fo, pl);
     PKX_LAUNCH_CHECK();
 }
 

@@ -31,17 +31,23 @@ void launch_dwconv_bn_silu(Precision prec, const void* in, void* out, const floa
                            const float* dw_bias, const float* bn_scale, const float* bn_shift,
                            int B, int T, int D, int K, hipStream_t s);
 
+// Output length of one k3 s2 subsampling stage: all_paddings 2, or 3 when
+// causal (2 before, 1 after; subsampling.cpp:25-46).
+inline int sub_stage_len(int t, bool causal) { return (t + (causal ? 3 : 2) - 3) / 2 + 1; }
+
 // Subsampling conv.0 (subsampling.cpp:143-157: Conv2d(1->C, 3x3, s2, p1) + bias
 // + ReLU over mel [B][F][T] f32, frames t >= valid0[b] zero when valid0 is set),
 // the stage mask on its rows (t1 >= valid1[b] zero) and the first depthwise
 // conv (subsampling.cpp:168-184), fused; output channels-last [B][T2][F2][C].
+// causal: CausalConv2D padding (2 before, 1 after on both axes).
 void launch_sub_stage1(Precision prec, const float* mel, const int* valid0, const int* valid1, const float* w0,
                        const float* b0, const float* w2, const float* b2, void* out, int B, int F, int T, int C,
-                       hipStream_t s);
+                       hipStream_t s, bool causal = false);
 // Subsampling depthwise 3x3 s2 p1 + bias (subsampling.cpp:168-184), channels-last,
 // input time rows t >= vmask[b] read as zero when vmask != nullptr.
 void launch_sub_dwconv(Precision prec, const void* in, const int* vmask, const float* w,
-                       const float* bias, void* out, int B, int Ti, int Fi, int C, hipStream_t s);
+                       const float* bias, void* out, int B, int Ti, int Fi, int C, hipStream_t s,
+                       bool causal = false);
 
 // pos_enc.cpp:10-34 in f64, stored as the activation type: [2T-1][D].
 void launch_rel_pos_encoding(Precision prec, void* out, int T, int D, hipStream_t s);

@@ -263,12 +263,28 @@ std::unique_ptr<Model> load_gguf(const std::string& path, int precision) {
     c.vocab_size = (int)u("parakeet.vocab_size", 0);
     if (kv.count("parakeet.tdt.durations")) c.n_durations = (int)kv["parakeet.tdt.durations"].arr.size();
     require(c.d_model > 0 && c.vocab_size > 0, "GGUF: missing parakeet.encoder.d_model / parakeet.vocab_size");
-    require(s("parakeet.encoder.conv_norm_type", "batch_norm") == "batch_norm",
-            "conv_norm_type=layer_norm (streaming models) is not supported by this encoder");
-    require(s("parakeet.encoder.att_context_style", "regular") == "regular",
-            "chunked_limited attention (streaming models) is not supported by this encoder");
-    require(u("parakeet.encoder.causal_downsampling", 0) == 0 && u("parakeet.encoder.conv_causal", 0) == 0,
-            "causal subsampling / depthwise conv (streaming models) is not supported by this encoder");
+    const std::string cnt = s("parakeet.encoder.conv_norm_type", "batch_norm");
+    require(cnt == "batch_norm" || cnt == "layer_norm", "conv_norm_type must be batch_norm or layer_norm");
+    c.conv_ln = cnt == "layer_norm";
+    c.causal_sub = (int)u("parakeet.encoder.causal_downsampling", 0);
+    c.conv_causal = (int)u("parakeet.encoder.conv_causal", 0);
+    c.att_left = (int)u("parakeet.encoder.att_context_left", -1);
+    c.att_right = (int)u("parakeet.encoder.att_context_right", -1);
+    const std::string style = s("parakeet.encoder.att_context_style", "regular");
+    c.att_limited = style == "chunked_limited" && c.att_right >= 0;
+    if (style != "regular") {
+        // streaming_encoder.cpp:38-55: [0] for the first chunk, [1] after
+        auto arr = [&](const char* k, int idx, int dflt) -> int {
+            auto it = kv.find(k);
+            return it == kv.end() || (int)it->second.arr.size() <= idx ? dflt : (int)it->second.arr[(size_t)idx];
+        };
+        c.stream_chunk_first = arr("parakeet.streaming.chunk_size", 0, 9);
+        c.stream_chunk = arr("parakeet.streaming.chunk_size", 1, 16);
+        c.stream_pre_cache = arr("parakeet.streaming.pre_encode_cache_size", 1, 9);
+        c.stream_cache_len = (int)u("parakeet.streaming.last_channel_cache_size", 0);
+        c.stream_valid_out_len = (int)u("parakeet.streaming.valid_out_len", 0);
+        c.stream_drop_extra = (int)u("parakeet.streaming.drop_extra_pre_encoded", 0);
+    }
     const int64_t sf = u("parakeet.encoder.subsampling_factor", 8);
     require(sf == 8, "only dw_striding x8 subsampling is supported");
 

@@ -56,15 +56,15 @@ static int64_t row_bytes(int gtype, int64_t K) {
     }
 }
 
-int subsampled_len(int T) {
+int subsampled_len(int T, bool causal) {
     int t = T;
-    for (int s = 0; s < 3; ++s) t = (t + 2 - 3) / 2 + 1;
+    for (int s = 0; s < 3; ++s) t = sub_stage_len(t, causal);
     return t;
 }
 
-int valid_out_len(int T, int in_valid) {
+int valid_out_len(int T, int in_valid, bool causal) {
     int v = in_valid >= 0 ? in_valid : T - 1;
-    for (int s = 0; s < 3; ++s) v = (v + 2 - 3) / 2 + 1;
+    for (int s = 0; s < 3; ++s) v = sub_stage_len(v, causal);
     return v;
 }
 
@@ -501,7 +501,12 @@ void Model::finalize() {
             L.dw_w = upload_f32(dw);
         }
         L.dw_b = optb(cv + "depthwise_conv.bias");
-        {
+        if (c.conv_ln) {
+            // conv_norm_type "layer_norm": LayerNorm over channels with the
+            // batch_norm.weight / .bias tensors as gamma / beta (conformer.cpp:128-133)
+            L.cn_g = upload_f32(need(cv + "batch_norm.weight"));
+            L.cn_b = upload_f32(need(cv + "batch_norm.bias"));
+        } else {
             // BatchNorm fold, exactly conformer.cpp:144-147 (f32).
             std::vector<float> g = to_f32(need(cv + "batch_norm.weight")),
                                bb = to_f32(need(cv + "batch_norm.bias")),
@@ -539,7 +544,7 @@ void Model::finalize() {
     {
         const std::string p = "encoder.pre_encode.";
         int F = c.n_mels;
-        for (int s = 0; s < 3; ++s) F = (F - 1) / 2 + 1;
+        for (int s = 0; s < 3; ++s) F = sub_stage_len(F, c.causal_sub != 0);
         sub_.w0 = upload_f32(need(p + "conv.0.weight"));
         sub_.b0 = upload_f32(need(p + "conv.0.bias"));
         sub_.w2 = upload_f32(need(p + "conv.2.weight"));
@@ -853,8 +858,9 @@ void Model::conv_front(const LayerDev& L, const void* A, int64_t M, const int* v
 void Model::ensure_ws(int B, int T_max) {
     const ModelConfig& c = cfg_;
     const size_t as = prec_ == PREC_F16 ? 2 : 4;
-    const int T1 = (T_max - 1) / 2 + 1, T2 = (T1 - 1) / 2 + 1, T3 = (T2 - 1) / 2 + 1;
-    const int F1 = (c.n_mels - 1) / 2 + 1, F2 = (F1 - 1) / 2 + 1, F3 = (F2 - 1) / 2 + 1;
+    const bool cz = c.causal_sub != 0;
+    const int T1 = sub_stage_len(T_max, cz), T2 = sub_stage_len(T1, cz), T3 = sub_stage_len(T2, cz);
+    const int F1 = sub_stage_len(c.n_mels, cz), F2 = sub_stage_len(F1, cz), F3 = sub_stage_len(F2, cz);
     const size_t C = c.sub_channels, D = c.d_model, M = (size_t)B * T3, P = 2 * (size_t)T3 - 1;
     Ws& w = *ws_;
     // (the conv0 map, B x T1 x F1 x C, is never materialised: see launch_sub_stage1)
@@ -908,22 +914,29 @@ void* Model::cast_to_act(const float* x, int64_t n, hipStream_t s) {
 // ---------------------------------------------------------------------------
 int Model::subsampling_forward(const float* mel, int B, int T_max, const int* valid_T,
                                bool stage_masks, float* out, int* valid_out, hipStream_t s,
-                               bool apply_xscaling) {
+                               bool apply_xscaling, bool whole_frames) {
     require(finalized_, "model not finalized");
     require(B > 0 && T_max > 0, "subsampling: empty batch");
     ensure_ws(B, T_max);
     const ModelConfig& c = cfg_;
     const int C = c.sub_channels, F = c.n_mels;
-    const int T1 = (T_max - 1) / 2 + 1, T2 = (T1 - 1) / 2 + 1, T3 = (T2 - 1) / 2 + 1;
-    const int F1 = (F - 1) / 2 + 1, F2 = (F1 - 1) / 2 + 1, F3 = (F2 - 1) / 2 + 1;
+    // causal (CausalConv2D): pad 2 before / 1 after, and the per-stage input
+    // masks on every path (subsampling.cpp:100-147, :283-300)
+    const bool cz = c.causal_sub != 0;
+    if (cz) stage_masks = true;
+    const int T1 = sub_stage_len(T_max, cz), T2 = sub_stage_len(T1, cz), T3 = sub_stage_len(T2, cz);
+    const int F1 = sub_stage_len(F, cz), F2 = sub_stage_len(F1, cz), F3 = sub_stage_len(F2, cz);
+    (void)T1;
+    (void)F1;
     std::vector<int> v0(B), v1(B), v2(B), vo(B);
     for (int b = 0; b < B; ++b) {
         const int vt = valid_T ? valid_T[b] : T_max;
         require(vt >= 1 && vt <= T_max, "valid_T out of range");
-        v0[b] = vt - 1;                                 // offline T-1 entry convention
-        v1[b] = (v0[b] + 2 - 3) / 2 + 1;
-        v2[b] = (v1[b] + 2 - 3) / 2 + 1;
-        const int vv = valid_out_len(T_max, v0[b]);
+        // offline T-1 entry convention; a streaming window is audio to its last frame
+        v0[b] = whole_frames ? vt : vt - 1;
+        v1[b] = sub_stage_len(v0[b], cz);
+        v2[b] = sub_stage_len(v1[b], cz);
+        const int vv = valid_out_len(T_max, v0[b], cz);
         vo[b] = vv > T3 ? T3 : vv;
         if (valid_out) valid_out[b] = vo[b];
     }
@@ -934,9 +947,10 @@ int Model::subsampling_forward(const float* mel, int B, int T_max, const int* va
     const int Bc = w.Bcap;
     mark(KF_SUBSAMPLING, true);
     launch_sub_stage1(prec_, mel, stage_masks ? dv : nullptr, stage_masks ? dv + Bc : nullptr, sub_.w0, sub_.b0,
-                      sub_.w2, sub_.b2, w.a2.p, B, F, T_max, C, s);
+                      sub_.w2, sub_.b2, w.a2.p, B, F, T_max, C, s, cz);
     gemm(sub_.w3, EPI_RELU, w.a2.p, C, (int64_t)B * T2 * F2, sub_.b3, w.a2p.p, C, 1.f, nullptr, 1, s, prec_, -1);
-    launch_sub_dwconv(prec_, w.a2p.p, stage_masks ? dv + 2 * Bc : nullptr, sub_.w5, sub_.b5, w.a3.p, B, T2, F2, C, s);
+    launch_sub_dwconv(prec_, w.a2p.p, stage_masks ? dv + 2 * Bc : nullptr, sub_.w5, sub_.b5, w.a3.p, B, T2, F2, C, s,
+                      cz);
     gemm(sub_.w6, EPI_RELU_TR, w.a3.p, C, (int64_t)B * T3 * F3, sub_.b6, w.flat.p, 0, 1.f, dv + 3 * Bc, T3, s,
          prec_, -1, nullptr, F3);
     const float xs = (apply_xscaling && c.xscaling) ? std::sqrt((float)c.d_model) : 1.0f;  // encoder.cpp:122-124
@@ -951,6 +965,9 @@ int Model::subsampling_forward(const float* mel, int B, int T_max, const int* va
 // ---------------------------------------------------------------------------
 void Model::layer_body(int l, float* x, int B, int T, const int* d_valid, bool first_ln_done,
                        bool fuse_next_ln, bool pos_all, hipStream_t s) {
+    require(!cfg_.conv_ln && !cfg_.conv_causal && !cfg_.att_limited,
+            "offline forward of a cache-aware streaming model (layer_norm / causal conv / chunked-limited "
+            "attention) is not implemented: use the streaming encoder");
     const ModelConfig& c = cfg_;
     const LayerDev& L = layers_[l];
     const int D = c.d_model, H = c.n_heads, dk = D / H;
@@ -1121,6 +1138,9 @@ void Model::conformer_layer_forward(int layer, const float* x, int B, int T, con
 
 void Model::relpos_attention_forward(int layer, const float* x, int B, int T, const int* valid,
                                      float* out, hipStream_t s) {
+    require(!cfg_.conv_ln && !cfg_.conv_causal && !cfg_.att_limited,
+            "offline forward of a cache-aware streaming model (layer_norm / causal conv / chunked-limited "
+            "attention) is not implemented: use the streaming encoder");
     require(finalized_, "model not finalized");
     require(layer >= 0 && layer < cfg_.n_layers, "layer index out of range");
     ensure_ws(B, 8 * T);
@@ -1166,6 +1186,9 @@ void Model::relpos_attention_forward(int layer, const float* x, int B, int T, co
 
 void Model::conv_module_forward(int layer, const float* cin, int B, int T, const int* valid, float* out,
                                 hipStream_t s) {
+    require(!cfg_.conv_ln && !cfg_.conv_causal && !cfg_.att_limited,
+            "offline forward of a cache-aware streaming model (layer_norm / causal conv / chunked-limited "
+            "attention) is not implemented: use the streaming encoder");
     require(finalized_, "model not finalized");
     require(layer >= 0 && layer < cfg_.n_layers, "layer index out of range");
     ensure_ws(B, 8 * T);

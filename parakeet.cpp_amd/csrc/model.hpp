@@ -25,6 +25,14 @@ struct ModelConfig {
     int n_mels = 0, sub_channels = 0;
     int xscaling = 0;
     int vocab_size = 0, n_durations = 0;
+    // cache-aware streaming models (model_loader.cpp:110-131); zeros = offline
+    int conv_ln = 0;              // conv_norm_type "layer_norm"
+    int causal_sub = 0;           // causal_downsampling
+    int conv_causal = 0;          // causal depthwise conv
+    int att_limited = 0;          // att_context_style "chunked_limited" (att_right >= 0)
+    int att_left = -1, att_right = -1;
+    int stream_chunk_first = 0, stream_chunk = 0, stream_pre_cache = 0;   // mel frames
+    int stream_cache_len = 0, stream_valid_out_len = 0, stream_drop_extra = 0;
 };
 
 struct HostTensor {
@@ -60,6 +68,7 @@ struct LayerDev {
     DevWeight pw1, pw2;
     float *pw1_b = nullptr, *pw2_b = nullptr, *dw_w = nullptr, *dw_b = nullptr;
     float *bn_scale = nullptr, *bn_shift = nullptr;
+    float *cn_g = nullptr, *cn_b = nullptr;   // conv_norm_type "layer_norm": gamma, beta
     // LayerNorms folded into the product that follows them (f16 path):
     // c1 = W . gamma, c2 = W . beta + b for norm_self_att -> q/k/v,
     // norm_conv -> pointwise_conv1, norm_feed_forward2 -> feed_forward2.linear1
@@ -94,6 +103,30 @@ struct PredDev {
     bool ok() const { return L > 0; }
 };
 
+// State of a group of cache-aware streams advanced in lockstep
+// (StreamingEncoder, streaming_encoder.hpp:33-95).  The attention cache holds
+// the projected keys and values of the last cache_len frames (the reference
+// keeps norm_self_att outputs and projects them again every chunk; the
+// projection is linear, so caching its result gives the same keys and values
+// without recomputing cache_len rows per layer and chunk) in a ring per layer
+// and stream; the conv cache holds the last K-1 GLU outputs.  Device buffers
+// are owned here and sized at creation.
+struct StreamState {
+    int B = 0, max_window = 0, tc_max = 0, tsub_max = 0;
+    int CL = 0, LP = 0, np = 0;
+    int step = 0, clc = 0, head = 0;   // chunks taken, valid cache frames, ring start
+    float* kc = nullptr;               // [L][B][CL][D] keys
+    float* vc = nullptr;               // [L][B][CL][D] values
+    float* cc = nullptr;               // [L][B][LP][D] GLU history, oldest first
+    float* ppos = nullptr;             // [L][np][D] linear_pos of the table rows for
+                                       // distances CL+tc_max-1 .. -(tc_max-1)
+    float* sub = nullptr;              // [B][tsub_max][D] subsampled window
+    float* x = nullptr;                // [B][tc_max][D] residual stream
+    void *h = nullptr, *u = nullptr, *qkv = nullptr, *g = nullptr;   // activations
+    std::vector<void*> allocs;
+    ~StreamState();
+};
+
 // Per-kernel-family timing collected when profiling is enabled.
 enum KFam : int {
     KF_SUBSAMPLING = 0, KF_LAYERNORM, KF_GEMM_FFN, KF_GEMM_QKV, KF_GEMM_POS, KF_ATTENTION,
@@ -122,9 +155,11 @@ public:
     // subsampling masking (subsampling.cpp:109-147) or the scalar one.
     int encoder_forward(const float* mel, int B, int T_max, const int* valid_T, bool stage_masks,
                         float* out, int* valid_out, float* capture, hipStream_t s);
+    // whole_frames: every one of valid_T[b] mel frames is audio (a streaming
+    // window), instead of the offline T-1 convention
     int subsampling_forward(const float* mel, int B, int T_max, const int* valid_T,
                             bool stage_masks, float* out, int* valid_out, hipStream_t s,
-                            bool apply_xscaling = false);
+                            bool apply_xscaling = false, bool whole_frames = false);
     void conformer_layer_forward(int layer, const float* x, int B, int T, const int* valid,
                                  float* out, float* conv_out, hipStream_t s);
     void relpos_attention_forward(int layer, const float* x, int B, int T, const int* valid,
@@ -142,6 +177,18 @@ public:
     void transducer_greedy(const float* enc, int B, int T_max, const int* T_valid, const int32_t* durations,
                            int n_dur, int blank_id, int max_symbols, int cap, int32_t* ids, int32_t* frames,
                            float* conf, int32_t* span, int* counts, hipStream_t s);
+    // Cache-aware streaming encoder (streaming_encoder.cpp) for models with a
+    // streaming configuration: n_streams streams advanced together, windows of
+    // at most max_window mel frames.
+    std::unique_ptr<StreamState> stream_create(int n_streams, int max_window, hipStream_t s);
+    void stream_reset(StreamState& st, hipStream_t s);
+    // Frames a window of n mel frames yields before the valid slice (0: none).
+    int stream_chunk_len(const StreamState& st, int n) const;
+    // StreamingEncoder::step (streaming_encoder.cpp:340-462) for every stream:
+    // mel [B][n_mels][n] f32 device (pre-encode overlap included); out
+    // [B][stream_chunk_len][D] f32 device receives all chunk frames; returns
+    // the number kept (valid_out_len mid-stream, all when is_last).
+    int stream_step(StreamState& st, const float* mel, int n, bool is_last, float* out, hipStream_t s);
     void set_profiling(unsigned family_mask, int stride);
     void profile_read(double* ms_per_family, int64_t* launches_per_family);
 
@@ -218,8 +265,8 @@ void linear_raw(Precision prec, const HostTensor& t, int N, int K, const float* 
 // GGUF v3 reader: fills a Model with the encoder (+ head) tensors and config.
 std::unique_ptr<Model> load_gguf(const std::string& path, int precision);
 
-// subsampling.cpp:25-46 arithmetic
-int subsampled_len(int T);
-int valid_out_len(int T, int in_valid);
+// subsampling.cpp:25-46 arithmetic (all_paddings 2; 3 when causal)
+int subsampled_len(int T, bool causal = false);
+int valid_out_len(int T, int in_valid, bool causal = false);
 
 }  // namespace pkx

@@ -38,7 +38,10 @@ class MelConfig(C.Structure):
 class Config(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("d_model", "n_layers", "n_heads", "ff_dim", "conv_kernel",
                                         "n_mels", "sub_channels", "xscaling", "vocab_size",
-                                        "n_durations")]
+                                        "n_durations", "conv_ln", "causal_sub", "conv_causal",
+                                        "att_limited", "att_left", "att_right", "stream_chunk_first",
+                                        "stream_chunk", "stream_pre_cache", "stream_cache_len",
+                                        "stream_valid_out_len", "stream_drop_extra")]
 
 
 SIGS = {
@@ -93,6 +96,12 @@ SIGS = {
                                C.c_int, C.POINTER(C.c_int32), C.POINTER(C.c_int32), _f, C.POINTER(C.c_int32), _ip,
                                _vp], C.c_int),
     "pkx_quantize_gguf": ([C.c_char_p, C.c_char_p, C.c_int, _ip, _ip, _ip], C.c_int),
+    "pkx_streaming_create": ([_vp, C.c_int, C.c_int, _vp, C.POINTER(_vp)], C.c_int),
+    "pkx_streaming_free": ([_vp], C.c_int),
+    "pkx_streaming_reset": ([_vp, _vp], C.c_int),
+    "pkx_streaming_info": ([_vp, _ip, _ip, _ip, _ip, _ip], C.c_int),
+    "pkx_streaming_chunk_len": ([_vp, C.c_int], C.c_int),
+    "pkx_streaming_step": ([_vp, _vp, C.c_int, C.c_int, _vp, _ip, _vp], C.c_int),
     "pkx_model_set_profiling": ([_vp, C.c_uint, C.c_int], C.c_int),
     "pkx_model_profile_read": ([_vp, C.POINTER(C.c_double), C.POINTER(C.c_int64)], C.c_int),
 }
@@ -257,6 +266,18 @@ class Model:
         c = model.cfg
         cfg = Config(c.d_model, c.n_layers, c.n_heads, c.ff_dim, c.conv_kernel, c.n_mels,
                      c.sub_channels, int(c.xscaling), c.vocab_size, len(c.tdt_durations))
+        cfg.att_left, cfg.att_right = -1, -1
+        if getattr(c, "streaming", False):
+            cfg.conv_ln = int(c.conv_norm_type == "layer_norm")
+            cfg.causal_sub = int(bool(c.causal_downsampling))
+            cfg.conv_causal = int(bool(c.conv_causal))
+            cfg.att_limited = int(c.att_context_style == "chunked_limited" and c.att_context_right >= 0)
+            cfg.att_left, cfg.att_right = c.att_context_left, c.att_context_right
+            cfg.stream_chunk_first, cfg.stream_chunk = c.stream_chunk_size[0], c.stream_chunk_size[-1]
+            cfg.stream_pre_cache = c.stream_pre_encode_cache_size[-1]
+            cfg.stream_cache_len = c.stream_last_channel_cache_size
+            cfg.stream_valid_out_len = c.stream_valid_out_len
+            cfg.stream_drop_extra = c.stream_drop_extra_pre_encoded
         h = _vp()
         check(lib().pkx_model_create(C.byref(cfg), precision, C.byref(h)))
         try:
@@ -374,6 +395,52 @@ class Model:
         n = (C.c_int64 * len(PROF_FAMILIES))()
         check(lib().pkx_model_profile_read(self.handle, ms, n))
         return {f: (ms[i], n[i]) for i, f in enumerate(PROF_FAMILIES)}
+
+
+class Streaming:
+    """Cache-aware streaming encoder (pkx_streaming handle): pk::StreamingEncoder
+    for n_streams streams advanced together."""
+
+    def __init__(self, model: "Model", n_streams=1, max_window=25, stream=None):
+        self.model = model                     # kept alive: the handle points into it
+        h = _vp()
+        check(lib().pkx_streaming_create(model.handle, int(n_streams), int(max_window), _sh(stream), C.byref(h)))
+        self.handle = h.value
+        self.n_streams = int(n_streams)
+        v = [C.c_int() for _ in range(5)]
+        check(lib().pkx_streaming_info(self.handle, *[C.byref(x) for x in v]))
+        self.chunk_first, self.chunk, self.pre_cache, self.valid_out_len, _ = (x.value for x in v)
+
+    @property
+    def step_num(self):
+        v = C.c_int()
+        check(lib().pkx_streaming_info(self.handle, None, None, None, None, C.byref(v)))
+        return v.value
+
+    def reset(self, stream=None):
+        check(lib().pkx_streaming_reset(self.handle, _sh(stream)))
+
+    def chunk_len(self, n):
+        return lib().pkx_streaming_chunk_len(self.handle, int(n))
+
+    def step(self, mel: DeviceArray, out: DeviceArray, is_last=False, stream=None):
+        """mel [S][n_mels][n] -> out [S][chunk_len][D] (device); returns the kept frame count."""
+        S, F, n = mel.shape
+        nv = C.c_int()
+        check(lib().pkx_streaming_step(self.handle, mel.ptr, int(n), 1 if is_last else 0, out.ptr, C.byref(nv),
+                                       _sh(stream)))
+        return nv.value
+
+    def close(self):
+        if self.handle:
+            lib().pkx_streaming_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 class Mel:

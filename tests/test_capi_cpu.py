@@ -58,7 +58,7 @@ def test_length_arithmetic_matches_oracle():
         print(' '.join(str(L.pkx_valid_out_len(t, -1)) for t in range(1, 3001)))
         print(' '.join(str(L.pkx_valid_out_len(3000, v)) for v in range(0, 3001, 7)))
     """).split("\n")
-    assert out[0] == "1"
+    assert out[0] == "2"
     assert [int(x) for x in out[1].split()] == [oracle.subsampled_len(t) for t in range(1, 3001)]
     assert [int(x) for x in out[2].split()] == [oracle.valid_out_len(t) for t in range(1, 3001)]
     assert [int(x) for x in out[3].split()] == [oracle.valid_out_len(3000, v) for v in range(0, 3001, 7)]
@@ -150,11 +150,9 @@ def test_gguf_writer_layout(tmp_path):
         assert f.read(t.nbytes()) == np.ascontiguousarray(t.data).tobytes()
 
 
-@pytest.mark.parametrize("key,val", [("parakeet.encoder.conv_norm_type", "layer_norm"),
-                                     ("parakeet.encoder.att_context_style", "chunked_limited")])
-def test_gguf_loader_rejects_streaming_models(tmp_path, key, val):
-    """Streaming (cache-aware) checkpoints are out of scope: the loader refuses
-    them from the KV block, before any device allocation."""
+def test_gguf_loader_rejects_unknown_conv_norm(tmp_path):
+    """conv_norm_type other than batch_norm / layer_norm (conformer.cpp:279-280)
+    is refused from the KV block, before any device allocation."""
     if not os.path.exists(LIB):
         pytest.skip("libpkx.so not built")
     cfg = pm.Config(d_model=64, n_layers=1, n_heads=4, ff_dim=128, n_mels=24, sub_channels=16, vocab_size=31,
@@ -162,11 +160,11 @@ def test_gguf_loader_rejects_streaming_models(tmp_path, key, val):
     m = pm.synthesize(cfg, "f32")
     path = tmp_path / "s.gguf"
     # later duplicate keys overwrite earlier ones in the reader's map
-    pm.write_gguf(m, str(path), extra_kv=[(key, 8, val)])
+    pm.write_gguf(m, str(path), extra_kv=[("parakeet.encoder.conv_norm_type", 8, "group_norm")])
     out = _run(f"""
         import ctypes as C, pkx
         L = pkx.lib()
         h = C.c_void_p()
         print(L.pkx_model_load_gguf({str(path)!r}.encode(), -1, C.byref(h)), L.pkx_last_error().decode())
     """).strip()
-    assert out.startswith("1 ") and "streaming" in out
+    assert out.startswith("1 ") and "conv_norm_type" in out
