@@ -176,6 +176,59 @@ def greedy_decode(gm, cfg, stream, d_enc, valid_out, reps=3):
             "ms": round(ms, 3), "rtfx": round(audio_s / (ms / 1e3), 1), "tokens": toks, "reps": reps}
 
 
+def streaming(stream, n_streams=64, steps=50, warmup=5):
+    """Cache-aware streaming encoder (pkx_streaming_step): the streaming model's
+    shape (17 blocks, d_model 512, 8 heads, ff 2048, causal, att_context [70, 1],
+    q8_0 linears), n_streams streams in lockstep, steady-state windows of
+    9 + 16 mel frames (160 ms of new audio, 2 encoder frames per stream and
+    step).  Reports per-step latency, stream RTFx, and the step's HBM bytes
+    (device weights once + per stream the f32 key/value rings and conv
+    history) against 8 TB/s."""
+    cfg = pm.eou_config()
+    model = pm.synthesize(cfg, "q8_0", heads=False)
+    gm = pkx.Model.from_tensors(model, pkx.PREC_AUTO)
+    S, W = n_streams, 25
+    st = pkx.Streaming(gm, n_streams=S, max_window=W, stream=stream)
+    rng = np.random.default_rng(3)
+    d_first = pkx.DeviceArray.from_numpy(rng.normal(0, 1, (S, cfg.n_mels, 9)).astype(np.float32), stream)
+    d_win = pkx.DeviceArray.from_numpy(rng.normal(0, 1, (S, cfg.n_mels, W)).astype(np.float32), stream)
+    d_out = pkx.DeviceArray((S, st.chunk_len(9), cfg.d_model), np.float32)
+    st.step(d_first, d_out, stream=stream)
+    for _ in range(warmup):
+        st.step(d_win, d_out, stream=stream)
+    stream.sync()
+    e0, e1 = pkx.Event(), pkx.Event()
+    e0.record(stream)
+    for _ in range(steps):
+        st.step(d_win, d_out, stream=stream)
+    e1.record(stream)
+    ms = e0.elapsed_ms(e1) / steps
+    stream.sync()
+    assert np.isfinite(d_out.numpy(stream)).all(), "non-finite streaming output"
+    gm.set_profiling(True)
+    n_prof = 5
+    for _ in range(n_prof):
+        st.step(d_win, d_out, stream=stream)
+    prof = gm.profile()
+    gm.set_profiling(False)
+    D, FF, L, CL, LP, C = cfg.d_model, cfg.ff_dim, cfg.n_layers, 70, cfg.conv_kernel - 1, cfg.sub_channels
+    n_w = L * (4 * D * FF + 7 * D * D) + D * C * cfg.sub_feat() + 2 * C * C
+    w_bytes = n_w * 34 / 32                                   # q8_0: 32 int8 + one f16 scale per block
+    state_bytes = S * L * (2 * CL * D * 4 + 2 * 2 * D * 4 + 2 * LP * D * 4)
+    total = w_bytes + state_bytes
+    audio_s = S * 16 * HOP_S
+    st.close()
+    fams = {f: {"launches_per_step": round(n / n_prof, 1), "us_per_step": round(t / n_prof * 1e3, 1)}
+            for f, (t, n) in prof.items() if n}
+    return {"workload": "cache-aware streaming encoder, 17 blocks d_model 512 q8_0 (streaming model shape), "
+                        "%d streams x windows of 9 + 16 mel frames (2 encoder frames per stream and step)" % S,
+            "ms_per_step": round(ms, 4), "rtfx": round(audio_s / (ms / 1e3), 1),
+            "hbm": {"bytes_per_step": int(total), "weights": int(w_bytes), "stream_state": int(state_bytes),
+                    "achieved": round(total / (ms / 1e3) / 1e9, 1), "unit": "GB/s",
+                    "frac": round(total / (ms / 1e3) / 1e9 / PEAK_HBM_GBS, 4)},
+            "kernels": fams, "steps": steps}
+
+
 def cpu_baseline(model, mel_item, budget_s=12.0):
     import oracle
     om = oracle.OracleModel(model)
@@ -305,6 +358,7 @@ def main():
     pcm_line = pcm_in(gm, cfg, stream, min(args.steps, 10))
     _, vo_dec = gm.encoder_forward(d_mel, valid, d_out, stream=stream)
     dec_line = greedy_decode(gm, cfg, stream, d_out, vo_dec)
+    stream_line = streaming(stream)
 
     audio_s = B * T_MEL * HOP_S
     rtfx = audio_s / (ms_step / 1e3)
@@ -324,6 +378,7 @@ def main():
         "kernel_busy_ms_per_step": round(busy_ms, 4),
         "pcm_in": pcm_line,
         "decode": dec_line,
+        "streaming": stream_line,
         "setup_s": round(setup_s, 1),
     }
     if not args.no_extra:

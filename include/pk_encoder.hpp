@@ -34,6 +34,14 @@
 
 namespace pk {
 
+// Cache-aware streaming schedule (src/model_loader.hpp:15-26): the [first,
+// later] values of the chunk arrays.
+struct StreamingCfg {
+    bool present = false;
+    std::vector<int32_t> chunk_size, shift_size, pre_encode_cache_size;
+    int32_t last_channel_cache_size = 0, valid_out_len = 0, drop_extra_pre_encoded = 0;
+};
+
 // Encoder fields of the reference's ParakeetConfig (src/model_loader.hpp:27-52).
 struct ParakeetConfig {
     int feat_in = 0;                     // n_mels
@@ -46,6 +54,12 @@ struct ParakeetConfig {
     bool xscaling = true;
     int vocab_size = 0;
     int n_durations = 0;                 // len(tdt.durations); 0 without a TDT head
+    std::string conv_norm_type = "batch_norm";
+    int32_t att_context_left = -1, att_context_right = -1;
+    std::string att_context_style = "regular";
+    bool causal_downsampling = false;
+    bool conv_causal = false;
+    StreamingCfg streaming;
 };
 
 class ModelLoader {
@@ -204,6 +218,44 @@ void transducer_greedy_batch(const ModelLoader& ml, const std::vector<std::vecto
                              const std::vector<int>& T, int enc_hidden, const std::vector<int32_t>& durations,
                              int blank_id, int max_symbols, std::vector<std::vector<int32_t>>& ids,
                              std::vector<std::vector<TokenInfo>>* toks);
+
+// Cache-aware streaming FastConformer encoder (src/streaming_encoder.hpp:33-95)
+// on the device: per-layer attention and conv caches carried across chunks,
+// so the concatenated chunk outputs are the offline limited-context encoder's
+// frames.  One stream per object (the C ABI advances several together).
+class StreamingEncoder {
+public:
+    explicit StreamingEncoder(const ModelLoader& ml);
+    ~StreamingEncoder();
+    StreamingEncoder(const StreamingEncoder&) = delete;
+    StreamingEncoder& operator=(const StreamingEncoder&) = delete;
+
+    // Zero the caches and the step counter (a fresh stream).
+    void reset();
+    // One mel window row-major [n_mels][n_mel_frames] (pre-encode overlap
+    // included) -> the chunk's valid frames row-major [valid][d_model];
+    // is_last keeps every produced frame (keep_all_outputs).
+    std::vector<float> step(const std::vector<float>& mel_chunk_frames, int n_mel_frames, bool is_last,
+                            int& n_valid_out);
+    std::vector<float> step(const std::vector<float>& mel_chunk_frames, int n_mel_frames) {
+        int v = 0;
+        return step(mel_chunk_frames, n_mel_frames, false, v);
+    }
+
+    int chunk_size_first() const { return chunk_first_; }   // mel frames, step 0
+    int chunk_size() const { return chunk_main_; }          // mel frames, later steps
+    int pre_encode_cache_size() const { return pre_cache_; }
+    int valid_out_len() const { return valid_out_len_; }
+    int step_num() const;
+
+private:
+    const ModelLoader& ml_;
+    pkx_streaming* st_ = nullptr;
+    void* mel_dev_ = nullptr;
+    void* out_dev_ = nullptr;
+    int d_model_ = 0, n_mels_ = 0, max_window_ = 0;
+    int chunk_first_ = 0, chunk_main_ = 0, pre_cache_ = 0, valid_out_len_ = 0;
+};
 
 // Log-mel front end (src/mel.hpp:33-41), on the device.
 class MelFrontend {

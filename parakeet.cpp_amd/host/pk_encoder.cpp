@@ -119,6 +119,22 @@ bool ModelLoader::load(const std::string& path, int precision) {
     cfg_.xscaling = c.xscaling != 0;
     cfg_.vocab_size = c.vocab_size;
     cfg_.n_durations = c.n_durations;
+    cfg_.conv_norm_type = c.conv_ln ? "layer_norm" : "batch_norm";
+    cfg_.att_context_left = c.att_left;
+    cfg_.att_context_right = c.att_right;
+    cfg_.att_context_style = c.att_limited ? "chunked_limited" : "regular";
+    cfg_.causal_downsampling = c.causal_sub != 0;
+    cfg_.conv_causal = c.conv_causal != 0;
+    cfg_.streaming = StreamingCfg();
+    if (c.att_limited) {
+        cfg_.streaming.present = true;
+        cfg_.streaming.chunk_size = {c.stream_chunk_first, c.stream_chunk};
+        cfg_.streaming.shift_size = {c.stream_chunk_first, c.stream_chunk};
+        cfg_.streaming.pre_encode_cache_size = {0, c.stream_pre_cache};
+        cfg_.streaming.last_channel_cache_size = c.stream_cache_len;
+        cfg_.streaming.valid_out_len = c.stream_valid_out_len;
+        cfg_.streaming.drop_extra_pre_encoded = c.stream_drop_extra;
+    }
     precision_ = prec;
     model_ = m;
     dev_ = std::move(dev);
@@ -426,6 +442,65 @@ static pkx_mel* mel_of(const ModelLoader& ml) {
     need(ml.handle() != nullptr, "model not loaded");
     need(ml.mel_handle() != nullptr, "no log-mel front end in this model: " + ml.mel_error());
     return ml.mel_handle();
+}
+
+// ---------------------------------------------------------------------------
+// StreamingEncoder (streaming_encoder.hpp:33-95) over pkx_streaming_*
+// ---------------------------------------------------------------------------
+StreamingEncoder::StreamingEncoder(const ModelLoader& ml) : ml_(ml) {
+    need(ml.handle() != nullptr, "StreamingEncoder: model not loaded");
+    need(ml.config().streaming.present, "StreamingEncoder requires a streaming model");
+    d_model_ = ml.config().d_model;
+    n_mels_ = ml.config().feat_in;
+    int pc = 0, ch = 0, cf = 0, vo = 0;
+    ModelLoader::Device& d = ml.device();
+    std::lock_guard<std::mutex> lock(d.mu);
+    // the longest window the schedule produces: pre-encode overlap + a later chunk
+    max_window_ = std::max(ml.config().streaming.chunk_size[0],
+                           ml.config().streaming.pre_encode_cache_size[1] + ml.config().streaming.chunk_size[1]);
+    chk(pkx_streaming_create(ml.handle(), 1, max_window_, d.stream, &st_), "pkx_streaming_create");
+    chk(pkx_streaming_info(st_, &cf, &ch, &pc, &vo, nullptr), "pkx_streaming_info");
+    chunk_first_ = cf;
+    chunk_main_ = ch;
+    pre_cache_ = pc;
+    valid_out_len_ = vo;
+    chk(pkx_malloc(&mel_dev_, (size_t)n_mels_ * max_window_ * 4), "pkx_malloc");
+    chk(pkx_malloc(&out_dev_, (size_t)pkx_streaming_chunk_len(st_, max_window_) * d_model_ * 4), "pkx_malloc");
+}
+
+StreamingEncoder::~StreamingEncoder() {
+    if (st_) pkx_streaming_free(st_);
+    if (mel_dev_) pkx_free(mel_dev_);
+    if (out_dev_) pkx_free(out_dev_);
+}
+
+void StreamingEncoder::reset() {
+    ModelLoader::Device& d = ml_.device();
+    std::lock_guard<std::mutex> lock(d.mu);
+    chk(pkx_streaming_reset(st_, d.stream), "pkx_streaming_reset");
+    d.sync();
+}
+
+int StreamingEncoder::step_num() const {
+    int s = 0;
+    chk(pkx_streaming_info(st_, nullptr, nullptr, nullptr, nullptr, &s), "pkx_streaming_info");
+    return s;
+}
+
+std::vector<float> StreamingEncoder::step(const std::vector<float>& mel, int n, bool is_last, int& n_valid_out) {
+    need((int64_t)mel.size() == (int64_t)n_mels_ * n, "StreamingEncoder::step: mel size != n_mels * n_mel_frames");
+    need(n >= 1 && n <= max_window_, "StreamingEncoder::step: window longer than the schedule's");
+    ModelLoader::Device& d = ml_.device();
+    std::lock_guard<std::mutex> lock(d.mu);
+    d.h2d(mel_dev_, mel.data(), mel.size() * 4);
+    int nv = 0;
+    chk(pkx_streaming_step(st_, (const float*)mel_dev_, n, is_last ? 1 : 0, (float*)out_dev_, &nv, d.stream),
+        "pkx_streaming_step");
+    std::vector<float> out((size_t)nv * d_model_);
+    if (nv) d.d2h(out.data(), out_dev_, out.size() * 4);
+    d.sync();
+    n_valid_out = nv;
+    return out;
 }
 
 MelFrontend::MelFrontend(const ModelLoader& ml) : ml_(ml) { (void)mel_of(ml); }

@@ -90,6 +90,45 @@ def _files(tmp_path_factory, wtype):
     return _FILES[wtype]
 
 
+def _files_eou(tmp_path_factory, wtype):
+    """A cache-aware streaming model and its baselines: the mel, the oracle's
+    streamed encoder output (stream_encoder_out) and its offline encoder output
+    with every frame valid (encoder_out), both [d_model][T']."""
+    key = "eou_" + wtype
+    if key in _FILES:
+        return _FILES[key]
+    d = tmp_path_factory.mktemp(f"cpp_{key}")
+    cfg = pm.eou_config(d_model=256, n_layers=3, n_heads=4, ff_dim=512, n_mels=64, sub_channels=64)
+    m = pm.synthesize(cfg, wtype, heads=False, std=0.05)
+    om = oracle.OracleModel(m)
+    rng = np.random.default_rng(17)
+    T = 137
+    mel = rng.standard_normal((cfg.n_mels, T)).astype(np.float32)
+    st = oracle.Stream(om)
+    outs = [st.step(mel[:, lo:hi], is_last=last) for lo, hi, last in oracle.stream_windows(T, 9, 16, 9)]
+    stream = np.concatenate(outs)
+    off, _ = om.encoder(mel[None], valid_in=[T])
+    mp, bp, sp = str(d / "eou.gguf"), str(d / "baseline_eou.gguf"), str(d / "baseline_eou_stream.gguf")
+    pm.write_gguf(m, mp)
+    pm.write_baseline_gguf(bp, {"mel": mel, "encoder_out": np.ascontiguousarray(off[0].T)})
+    pm.write_baseline_gguf(sp, {"stream_encoder_out": np.ascontiguousarray(stream.T)})
+    _FILES[key] = (mp, bp, sp)
+    return _FILES[key]
+
+
+@pytest.mark.parametrize("wtype", ["f32", "q8_0"])
+def test_cpp_streaming_encoder(tmp_path_factory, wtype):
+    exe = os.path.join(BIN, "test_streaming_encoder")
+    assert os.path.exists(exe), f"{exe} not built (make -C tests/cpp)"
+    mp, bp, sp = _files_eou(tmp_path_factory, wtype)
+    env = dict(os.environ, PARAKEET_TEST_GGUF_EOU=mp, PARAKEET_TEST_BASELINE_EOU=bp,
+               PARAKEET_TEST_BASELINE_EOU_STREAM=sp)
+    print(f"[cpp] test_streaming_encoder {wtype}", flush=True)
+    r = subprocess.run([exe], env=env, capture_output=True, text=True, timeout=120)
+    print(r.stderr)
+    assert r.returncode == 0, r.stdout + r.stderr
+
+
 @pytest.mark.parametrize("wtype", ["f32", "q8_0"])
 @pytest.mark.parametrize("name", TESTS)
 def test_cpp(tmp_path_factory, wtype, name):
