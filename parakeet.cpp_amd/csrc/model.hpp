@@ -115,8 +115,8 @@ struct StreamState {
     int B = 0, max_window = 0, tc_max = 0, tsub_max = 0;
     int CL = 0, LP = 0, np = 0;
     int step = 0, clc = 0, head = 0;   // chunks taken, valid cache frames, ring start
-    float* kc = nullptr;               // [L][B][CL][D] keys
-    float* vc = nullptr;               // [L][B][CL][D] values
+    void* kc = nullptr;                // [L][B][CL][D] keys, activation type
+    void* vc = nullptr;                // [L][B][CL][D] values, activation type
     float* cc = nullptr;               // [L][B][LP][D] GLU history, oldest first
     float* ppos = nullptr;             // [L][np][D] linear_pos of the table rows for
                                        // distances CL+tc_max-1 .. -(tc_max-1)

@@ -21,8 +21,8 @@ namespace {
 
 struct StreamAttnParams {
     const void* qkv;       // [M][3D] act: q | k | v (biases applied), row b*Tc + i
-    float* kc;             // [B][CL][D] this layer's key ring
-    float* vc;             // [B][CL][D] value ring
+    void* kc;              // [B][CL][D] act: this layer's key ring
+    void* vc;              // [B][CL][D] act: value ring
     const float* ppos;     // [np][D] positional projections, row r <-> distance CL + tc_max - 1 - r
     const float* bias_u;   // [D]
     const float* bias_v;   // [D]
@@ -31,53 +31,101 @@ struct StreamAttnParams {
     float scale;
 };
 
-// One workgroup per (stream, head), 256 threads.  LDS: the chunk's q + u,
-// q + v, k, v rows (f32, [Tc][dk] each) and the score block [Tc][CL + Tc].
-template <typename T>
+// LDS floats of one stream_attn_kernel workgroup: keys and values of the
+// Tk = CL + Tc frames and the NPB = CL + 2 Tc - 1 positional rows the chunk
+// reads, rows padded to dk + 1 (consecutive rows start in consecutive banks),
+// q + u and q + v [Tc][dk], scores [Tc][Tk].
+inline int stream_attn_lds_floats(int Tc, int CL, int dk) {
+    const int Tk = CL + Tc, npb = CL + 2 * Tc - 1;
+    return (2 * Tk + npb) * (dk + 1) + 2 * Tc * dk + Tc * Tk;
+}
+
+// One workgroup per (stream, head), 256 threads.  Everything the chunk reads
+// is staged in LDS with coalesced loads first (ring rows in logical order,
+// the chunk's own keys / values, the positional band); a thread then owns a
+// (query, key) score, a wave a softmax row, a thread a (query, channel) output.
+// DK > 0: the head width at compile time (dot products fully unrolled, so the
+// LDS reads of a score issue back to back); DK = 0 reads it from p.dk.
+template <typename T, int DK>
 __global__ __launch_bounds__(256) void stream_attn_kernel(StreamAttnParams p) {
     extern __shared__ float sm[];
-    const int b = blockIdx.x, h = blockIdx.y, dk = p.dk, D = p.D, Tc = p.Tc, CL = p.CL;
-    const int Tk = CL + Tc;
-    float* qu = sm;
-    float* qv = qu + Tc * dk;
-    float* kn = qv + Tc * dk;
-    float* vn = kn + Tc * dk;
-    float* sc = vn + Tc * dk;                    // [Tc][Tk]
+    const int b = blockIdx.x, h = blockIdx.y, dk = DK > 0 ? DK : p.dk, D = p.D, Tc = p.Tc, CL = p.CL;
+    const int Tk = CL + Tc, npb = CL + 2 * Tc - 1, ld = dk + 1;
+    float* ks = sm;                              // [Tk][ld]
+    float* vs = ks + Tk * ld;                    // [Tk][ld]
+    float* ps = vs + Tk * ld;                    // [npb][ld]: row j <-> distance CL + Tc - 1 - j
+    float* qu = ps + npb * ld;                   // [Tc][dk]
+    float* qv = qu + Tc * dk;                    // [Tc][dk]
+    float* sc = qv + Tc * dk;                    // [Tc][Tk]
     const T* qkv = (const T*)p.qkv;
+    T* kring = (T*)p.kc + (int64_t)b * CL * D + h * dk;
+    T* vring = (T*)p.vc + (int64_t)b * CL * D + h * dk;
+    // 16-byte loads (dk % 8 == 0, D % 8 == 0), several in flight per thread
+    constexpr int VE = 16 / sizeof(T);
+    const int vpr = dk / VE;
+#pragma unroll 4
+    for (int e = threadIdx.x; e < Tk * vpr; e += blockDim.x) {
+        const int r = e / vpr, c0 = (e % vpr) * VE;
+        const T *sk, *sv;
+        if (r < CL) {
+            const int64_t o = (int64_t)((p.head + r) % CL) * D + c0;
+            sk = kring + o;
+            sv = vring + o;
+        } else {
+            const T* row = qkv + (int64_t)(b * Tc + r - CL) * 3 * D + h * dk + c0;
+            sk = row + D;
+            sv = row + 2 * D;
+        }
+        T xk[VE], xv[VE];
+        *(int4v*)xk = *(const int4v*)sk;
+        *(int4v*)xv = *(const int4v*)sv;
+#pragma unroll
+        for (int q = 0; q < VE; ++q) {
+            ks[r * ld + c0 + q] = (float)xk[q];
+            vs[r * ld + c0 + q] = (float)xv[q];
+        }
+    }
+    const int prow0 = p.tc_max - Tc;             // global row of band row 0 (distance CL + Tc - 1)
+    const int vpp = dk / 4;
+#pragma unroll 4
+    for (int e = threadIdx.x; e < npb * vpp; e += blockDim.x) {
+        const int r = e / vpp, c0 = (e % vpp) * 4;
+        float x[4];
+        *(int4v*)x = *(const int4v*)(p.ppos + (int64_t)(prow0 + r) * D + h * dk + c0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) ps[r * ld + c0 + q] = x[q];
+    }
     for (int e = threadIdx.x; e < Tc * dk; e += blockDim.x) {
         const int i = e / dk, c = e % dk;
-        const T* row = qkv + (int64_t)(b * Tc + i) * 3 * D + h * dk + c;
-        const float q = (float)row[0];
+        const float q = (float)qkv[(int64_t)(b * Tc + i) * 3 * D + h * dk + c];
         qu[e] = q + p.bias_u[h * dk + c];
         qv[e] = q + p.bias_v[h * dk + c];
-        kn[e] = (float)row[D];
-        vn[e] = (float)row[2 * D];
     }
     __syncthreads();
-    const float* kring = p.kc + (int64_t)b * CL * D + h * dk;
-    const float* vring = p.vc + (int64_t)b * CL * D + h * dk;
     const int empty = CL - p.clc;
-    const int rmax = CL + p.tc_max - 1;          // ppos row of distance 0 is rmax
     for (int e = threadIdx.x; e < Tc * Tk; e += blockDim.x) {
         const int i = e / Tk, kj = e % Tk;
         const int diff = (CL + i) / p.chunk - kj / p.chunk;
         float s = -INFINITY;
         if (kj >= empty && diff >= 0 && diff <= p.left_chunks) {
-            const float* kr = kj < CL ? kring + (int64_t)((p.head + kj) % CL) * D : kn + (kj - CL) * dk;
-            const float* pr = p.ppos + (int64_t)(rmax - (CL + i - kj)) * D + h * dk;
+            // rel_shift of the [Tc][2 Tk - 1] block: column Tc - 1 - i + kj
+            const float* kr = ks + kj * ld;
+            const float* pr = ps + (Tc - 1 - i + kj) * ld;
             const float* a = qu + i * dk;
-            const float* c2 = qv + i * dk;
+            const float* a2 = qv + i * dk;
             float ac = 0.f, bd = 0.f;
+#pragma unroll 16
             for (int c = 0; c < dk; ++c) {
                 ac += a[c] * kr[c];
-                bd += c2[c] * pr[c];
+                bd += a2[c] * pr[c];
             }
             s = (ac + bd) * p.scale;
         }
         sc[e] = s;
     }
     __syncthreads();
-    // softmax per query row, one wave per row
+    // softmax per query row, one wave per row (the query's own frame is
+    // always visible, so no row is empty)
     const int wid = threadIdx.x / 64, lane = threadIdx.x % 64;
     for (int i = wid; i < Tc; i += blockDim.x / 64) {
         float* r = sc + i * Tk;
@@ -100,23 +148,18 @@ __global__ __launch_bounds__(256) void stream_attn_kernel(StreamAttnParams p) {
         const int i = e / dk, c = e % dk;
         const float* r = sc + i * Tk;
         float acc = 0.f;
-        for (int kj = 0; kj < CL; ++kj) {
-            const float pj = r[kj];
-            if (pj != 0.f) acc += pj * vring[(int64_t)((p.head + kj) % CL) * D + c];
-        }
-        for (int q = 0; q < Tc; ++q) acc += r[CL + q] * vn[q * dk + c];
+#pragma unroll 8
+        for (int kj = 0; kj < Tk; ++kj) acc += r[kj] * vs[kj * ld + c];
         out[(int64_t)(b * Tc + i) * D + h * dk + c] = to_act<T>(acc);
     }
-    __syncthreads();
-    // the chunk's frames take the ring slots of the oldest ones: logical
-    // order [cache[Tc:] ; chunk] with the ring start moved by Tc (host side)
-    float* kw = p.kc + (int64_t)b * CL * D + h * dk;
-    float* vw = p.vc + (int64_t)b * CL * D + h * dk;
+    // the chunk's frames take the ring slots of the oldest ones (every ring
+    // read above went through LDS before the barrier): logical order
+    // [cache[Tc:] ; chunk] with the ring start moved by Tc on the host
     for (int e = threadIdx.x; e < Tc * dk; e += blockDim.x) {
         const int q = e / dk, c = e % dk;
         const int64_t slot = (int64_t)((p.head + q) % CL) * D + c;
-        kw[slot] = kn[e];
-        vw[slot] = vn[e];
+        kring[slot] = to_act<T>(ks[(CL + q) * ld + c]);
+        vring[slot] = to_act<T>(vs[(CL + q) * ld + c]);
     }
 }
 
@@ -197,6 +240,74 @@ __global__ __launch_bounds__(256) void stream_conv_kernel(StreamConvParams p) {
         }
 }
 
+// The common shape (K taps known at compile time, Tc <= TCM): every global
+// load of a channel (taps, history, chunk) is issued before any arithmetic,
+// the history update is written from registers.
+template <typename T, int K, int TCM>
+__global__ __launch_bounds__(256) void stream_conv_kernel_k(StreamConvParams p) {
+    extern __shared__ float dwo[];               // [TCM][D]
+    constexpr int LP = K - 1;
+    const int b = blockIdx.x, D = p.D, Tc = p.Tc;
+    const T* glu = (const T*)p.glu + (int64_t)b * Tc * D;
+    float* hist = p.cc + (int64_t)b * LP * D;
+    T* out = (T*)p.out + (int64_t)b * Tc * D;
+    for (int c = threadIdx.x; c < D; c += blockDim.x) {
+        float wk[K], seq[LP + TCM];
+#pragma unroll
+        for (int k = 0; k < K; ++k) wk[k] = p.w[(int64_t)c * K + k];
+#pragma unroll
+        for (int u = 0; u < LP; ++u) seq[u] = hist[(int64_t)u * D + c];
+#pragma unroll
+        for (int t = 0; t < TCM; ++t) seq[LP + t] = t < Tc ? (float)glu[(int64_t)t * D + c] : 0.f;
+        const float bias = p.dw_b ? p.dw_b[c] : 0.f;
+#pragma unroll
+        for (int t = 0; t < TCM; ++t) {
+            if (t < Tc) {
+                float acc = 0.f;
+#pragma unroll
+                for (int k = 0; k < K; ++k) acc += wk[k] * seq[t + k];
+                dwo[t * D + c] = acc + bias;
+            }
+        }
+        // history <- the last LP entries of [history ; chunk]
+#pragma unroll
+        for (int j = 0; j < LP; ++j) {
+#pragma unroll
+            for (int t = 0; t <= TCM; ++t)
+                if (t == Tc) hist[(int64_t)j * D + c] = seq[j + t];
+        }
+    }
+    __syncthreads();
+    const int wid = threadIdx.x / 64, lane = threadIdx.x % 64, nw = blockDim.x / 64;
+    for (int t = wid; t < Tc; t += nw) {
+        const float* r = dwo + t * D;
+        T* o = out + (int64_t)t * D;
+        if (p.ln) {
+            float s = 0.f;
+            for (int c = lane; c < D; c += 64) s += r[c];
+            const float mean = wave_sum(s) / D;
+            float s2 = 0.f;
+            for (int c = lane; c < D; c += 64) {
+                const float d = r[c] - mean;
+                s2 += d * d;
+            }
+            const float rstd = 1.0f / sqrtf(wave_sum(s2) / D + 1e-5f);
+            for (int c = lane; c < D; c += 64) {
+                float y = (r[c] - mean) * rstd;
+                y = y * p.g[c] + p.beta[c];
+                o[c] = to_act<T>(y / (1.0f + __expf(-y)));
+            }
+        } else {
+            for (int c = lane; c < D; c += 64) {
+                const float y = r[c] * p.g[c] + p.beta[c];
+                o[c] = to_act<T>(y / (1.0f + __expf(-y)));
+            }
+        }
+    }
+}
+
+constexpr int SC_TCM = 8;   // chunk frames of the compile-time conv path
+
 }  // namespace
 
 StreamState::~StreamState() {
@@ -211,11 +322,16 @@ std::unique_ptr<StreamState> Model::stream_create(int n_streams, int max_window,
     require(n_streams >= 1 && max_window >= 1, "streaming encoder: n_streams and max_window must be positive");
     require(c.conv_kernel >= 2, "streaming encoder: conv kernel must have at least 2 taps");
     const int D = c.d_model, dk = D / c.n_heads;
-    require(dk <= 256 && D % 8 == 0 && D <= 2048, "streaming encoder: d_model above 2048 or head width above 256");
-    // LDS beyond the default 64 KiB: attention up to (4 dk + CL + 32) x 32
-    // floats, conv SC_FRAMES x D floats (both checked per launch)
-    for (const void* fn : {(const void*)stream_attn_kernel<f16>, (const void*)stream_attn_kernel<float>,
-                           (const void*)stream_conv_kernel<f16>, (const void*)stream_conv_kernel<float>})
+    require(dk <= 256 && dk % 8 == 0 && D % 8 == 0 && D <= 2048,
+            "streaming encoder: d_model above 2048, or head width above 256 or not a multiple of 8");
+    // LDS beyond the default 64 KiB (attention: stream_attn_lds_floats, conv:
+    // SC_FRAMES x D floats)
+    for (const void* fn : {(const void*)stream_attn_kernel<f16, 0>, (const void*)stream_attn_kernel<float, 0>,
+                           (const void*)stream_attn_kernel<f16, 64>, (const void*)stream_attn_kernel<float, 64>,
+                           (const void*)stream_attn_kernel<f16, 128>, (const void*)stream_attn_kernel<float, 128>,
+                           (const void*)stream_conv_kernel<f16>, (const void*)stream_conv_kernel<float>,
+                           (const void*)stream_conv_kernel_k<f16, 9, SC_TCM>,
+                           (const void*)stream_conv_kernel_k<float, 9, SC_TCM>})
         PKX_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
     std::unique_ptr<StreamState> st(new StreamState());
     st->B = n_streams;
@@ -226,6 +342,8 @@ std::unique_ptr<StreamState> Model::stream_create(int n_streams, int max_window,
     st->LP = c.conv_kernel - 1;
     require(st->tc_max <= st->CL, "streaming encoder: a window yields more frames than the attention cache holds");
     require(st->tc_max <= 32, "streaming encoder: at most 32 encoder frames per chunk (max_window <= 255)");
+    require(stream_attn_lds_floats(st->tc_max, st->CL, dk) * 4 <= 160 * 1024,
+            "streaming encoder: attention cache x head width too large for one workgroup's LDS");
     st->np = st->CL + 2 * st->tc_max - 1;
     const size_t as = prec_ == PREC_F16 ? 2 : 4, L = (size_t)c.n_layers, B = (size_t)n_streams;
     const size_t M = B * (size_t)st->tc_max;
@@ -235,8 +353,8 @@ std::unique_ptr<StreamState> Model::stream_create(int n_streams, int max_window,
         st->allocs.push_back(q);
         return q;
     };
-    st->kc = (float*)al(L * B * st->CL * D * 4);
-    st->vc = (float*)al(L * B * st->CL * D * 4);
+    st->kc = al(L * B * st->CL * D * as);
+    st->vc = al(L * B * st->CL * D * as);
     st->cc = (float*)al(L * B * st->LP * D * 4);
     st->ppos = (float*)al(L * st->np * D * 4);
     st->sub = (float*)al(B * st->tsub_max * D * 4);
@@ -262,8 +380,9 @@ std::unique_ptr<StreamState> Model::stream_create(int n_streams, int max_window,
 void Model::stream_reset(StreamState& st, hipStream_t s) {
     const ModelConfig& c = cfg_;
     const size_t L = (size_t)c.n_layers, B = (size_t)st.B, D = (size_t)c.d_model;
-    PKX_HIP(hipMemsetAsync(st.kc, 0, L * B * st.CL * D * 4, s));
-    PKX_HIP(hipMemsetAsync(st.vc, 0, L * B * st.CL * D * 4, s));
+    const size_t as = prec_ == PREC_F16 ? 2 : 4;
+    PKX_HIP(hipMemsetAsync(st.kc, 0, L * B * st.CL * D * as, s));
+    PKX_HIP(hipMemsetAsync(st.vc, 0, L * B * st.CL * D * as, s));
     PKX_HIP(hipMemsetAsync(st.cc, 0, L * B * st.LP * D * 4, s));
     st.step = 0;
     st.clc = 0;
@@ -292,34 +411,51 @@ int Model::stream_step(StreamState& st, const float* mel, int n, bool is_last, f
     const int Tsub = subsampling_forward(mel, B, n, vn.data(), true, st.sub, nullptr, s, true, true);
     PKX_HIP(hipMemcpy2DAsync(st.x, (size_t)Tc * D * 4, st.sub + (size_t)drop * D, (size_t)Tsub * D * 4,
                              (size_t)Tc * D * 4, (size_t)B, hipMemcpyDeviceToDevice, s));
-    auto ln = [&](const float* g, const float* b, void* y, float* y32) {
+    auto ln = [&](const float* g, const float* b, void* y, float* y32, const float* g2 = nullptr,
+                  const float* b2 = nullptr) {
         LnParams p;
         p.x = st.x;
         p.g = g;
         p.b = b;
         p.y = y;
         p.y_f32 = y32;
+        p.g2 = g2;
+        p.b2 = b2;
         p.M = M;
         p.D = D;
         mark(KF_LAYERNORM, true);
         launch_layernorm(prec_, p, s);
         mark(KF_LAYERNORM, false);
     };
-    const size_t LB = (size_t)B;
+    const size_t LB = (size_t)B, as = prec_ == PREC_F16 ? 2 : 4;
+    // f16 path: norm_self_att, norm_conv and norm_feed_forward2 folded into the
+    // products after them, as in the offline forward (the residual product
+    // before each leaves x * gamma and the row statistics); norm_out fused with
+    // the next layer's norm_feed_forward1.
+    const bool fold = ln_fold_;
+    ln(layers_[0].ff1_ln_g, layers_[0].ff1_ln_b, st.h, nullptr);
     for (int l = 0; l < c.n_layers; ++l) {
         const LayerDev& L = layers_[(size_t)l];
-        // A: x += 0.5 FFN1(LN(x))
-        ln(L.ff1_ln_g, L.ff1_ln_b, st.h, nullptr);
+        // A: x += 0.5 FFN1(LN(x))   (h holds LN_ff1(x))
         gemm(L.ff1_w1, EPI_SILU, st.h, D, M, L.ff1_b1, st.u, c.ff_dim, 1.f, nullptr, 1, s, prec_, KF_GEMM_FFN);
-        gemm(L.ff1_w2, EPI_RESID, st.u, c.ff_dim, M, L.ff1_b2, st.x, D, 0.5f, nullptr, 1, s, prec_, KF_GEMM_FFN);
         // B: x += MHSA(LN(x)) over [cache ; chunk]
-        ln(L.att_ln_g, L.att_ln_b, st.h, nullptr);
-        gemm(L.wqkv, EPI_STORE, st.h, D, M, L.bqkv, st.qkv, 3 * D, 1.f, nullptr, 1, s, prec_, KF_GEMM_QKV);
+        if (fold) {
+            gemm_resid_ln(L.ff1_w2, st.u, M, L.ff1_b2, st.x, 0.5f, L.att_ln_g, st.h, s, KF_GEMM_FFN);
+            const GemmParams p = fold_params(L.wqkv, st.h, M, L.qkv_c1, L.qkv_c2, st.qkv, 3 * D);
+            mark(KF_GEMM_QKV, true);
+            launch_gemm(prec_, L.wqkv.gtype, EPI_STORE, p, s);
+            mark(KF_GEMM_QKV, false);
+        } else {
+            gemm(L.ff1_w2, EPI_RESID, st.u, c.ff_dim, M, L.ff1_b2, st.x, D, 0.5f, nullptr, 1, s, prec_,
+                 KF_GEMM_FFN);
+            ln(L.att_ln_g, L.att_ln_b, st.h, nullptr);
+            gemm(L.wqkv, EPI_STORE, st.h, D, M, L.bqkv, st.qkv, 3 * D, 1.f, nullptr, 1, s, prec_, KF_GEMM_QKV);
+        }
         {
             StreamAttnParams a;
             a.qkv = st.qkv;
-            a.kc = st.kc + (size_t)l * LB * st.CL * D;
-            a.vc = st.vc + (size_t)l * LB * st.CL * D;
+            a.kc = (uint8_t*)st.kc + (size_t)l * LB * st.CL * D * as;
+            a.vc = (uint8_t*)st.vc + (size_t)l * LB * st.CL * D * as;
             a.ppos = st.ppos + (size_t)l * st.np * D;
             a.bias_u = L.pos_u;
             a.bias_v = L.pos_v;
@@ -334,20 +470,33 @@ int Model::stream_step(StreamState& st, const float* mel, int n, bool is_last, f
             a.D = D;
             a.dk = dk;
             a.scale = 1.0f / std::sqrt((float)dk);
-            const uint32_t shm = (uint32_t)(4 * Tc * dk + Tc * (st.CL + Tc)) * 4u;
-            require(shm <= 160u * 1024u, "streaming encoder: attention cache too long for LDS");
+            const uint32_t shm = (uint32_t)stream_attn_lds_floats(Tc, st.CL, dk) * 4u;
             mark(KF_ATTENTION, true);
-            if (prec_ == PREC_F16)
-                launch(stream_attn_kernel<f16>, dim3(B, H), dim3(256), shm, s, a);
-            else
-                launch(stream_attn_kernel<float>, dim3(B, H), dim3(256), shm, s, a);
+            const dim3 grid(B, H);
+            if (prec_ == PREC_F16) {
+                if (dk == 64) launch(stream_attn_kernel<f16, 64>, grid, dim3(256), shm, s, a);
+                else if (dk == 128) launch(stream_attn_kernel<f16, 128>, grid, dim3(256), shm, s, a);
+                else launch(stream_attn_kernel<f16, 0>, grid, dim3(256), shm, s, a);
+            } else {
+                if (dk == 64) launch(stream_attn_kernel<float, 64>, grid, dim3(256), shm, s, a);
+                else if (dk == 128) launch(stream_attn_kernel<float, 128>, grid, dim3(256), shm, s, a);
+                else launch(stream_attn_kernel<float, 0>, grid, dim3(256), shm, s, a);
+            }
             PKX_LAUNCH_CHECK();
             mark(KF_ATTENTION, false);
         }
-        gemm(L.wo, EPI_RESID, st.g, D, M, L.bo, st.x, D, 1.f, nullptr, 1, s, prec_, KF_GEMM_OUT);
         // C: x += conv(LN(x)) with the causal depthwise conv over [history ; chunk]
-        ln(L.conv_ln_g, L.conv_ln_b, st.h, nullptr);
-        gemm(L.pw1, EPI_GLU, st.h, D, M, L.pw1_b, st.g, D, 1.f, nullptr, 1, s, prec_, KF_GEMM_PW1_GLU);
+        if (fold) {
+            gemm_resid_ln(L.wo, st.g, M, L.bo, st.x, 1.f, L.conv_ln_g, st.h, s, KF_GEMM_OUT);
+            GemmParams p = fold_params(L.pw1, st.h, M, L.pw1_c1, L.pw1_c2, st.g, D);
+            mark(KF_GEMM_PW1_GLU, true);
+            launch_gemm(prec_, L.pw1.gtype, EPI_GLU, p, s);
+            mark(KF_GEMM_PW1_GLU, false);
+        } else {
+            gemm(L.wo, EPI_RESID, st.g, D, M, L.bo, st.x, D, 1.f, nullptr, 1, s, prec_, KF_GEMM_OUT);
+            ln(L.conv_ln_g, L.conv_ln_b, st.h, nullptr);
+            gemm(L.pw1, EPI_GLU, st.h, D, M, L.pw1_b, st.g, D, 1.f, nullptr, 1, s, prec_, KF_GEMM_PW1_GLU);
+        }
         {
             StreamConvParams q;
             q.glu = st.g;
@@ -363,19 +512,36 @@ int Model::stream_step(StreamState& st, const float* mel, int n, bool is_last, f
             q.K = c.conv_kernel;
             const uint32_t shm = (uint32_t)(SC_FRAMES * D) * 4u;
             mark(KF_DWCONV, true);
-            if (prec_ == PREC_F16)
+            if (c.conv_kernel == 9 && Tc <= SC_TCM) {
+                if (prec_ == PREC_F16)
+                    launch(stream_conv_kernel_k<f16, 9, SC_TCM>, dim3(B), dim3(256), shm, s, q);
+                else
+                    launch(stream_conv_kernel_k<float, 9, SC_TCM>, dim3(B), dim3(256), shm, s, q);
+            } else if (prec_ == PREC_F16) {
                 launch(stream_conv_kernel<f16>, dim3(B), dim3(256), shm, s, q);
-            else
+            } else {
                 launch(stream_conv_kernel<float>, dim3(B), dim3(256), shm, s, q);
+            }
             PKX_LAUNCH_CHECK();
             mark(KF_DWCONV, false);
         }
-        gemm(L.pw2, EPI_RESID, st.h, D, M, L.pw2_b, st.x, D, 1.f, nullptr, 1, s, prec_, KF_GEMM_PW2);
-        // D: x += 0.5 FFN2(LN(x)); x = norm_out(x)
-        ln(L.ff2_ln_g, L.ff2_ln_b, st.h, nullptr);
-        gemm(L.ff2_w1, EPI_SILU, st.h, D, M, L.ff2_b1, st.u, c.ff_dim, 1.f, nullptr, 1, s, prec_, KF_GEMM_FFN);
+        // D: x += 0.5 FFN2(LN(x)); x = norm_out(x) (+ the next layer's LN_ff1 into h)
+        if (fold) {
+            gemm_resid_ln(L.pw2, st.h, M, L.pw2_b, st.x, 1.f, L.ff2_ln_g, st.g, s, KF_GEMM_PW2);
+            const GemmParams p = fold_params(L.ff2_w1, st.g, M, L.ff2_c1, L.ff2_c2, st.u, c.ff_dim);
+            mark(KF_GEMM_FFN, true);
+            launch_gemm(prec_, L.ff2_w1.gtype, EPI_SILU, p, s);
+            mark(KF_GEMM_FFN, false);
+        } else {
+            gemm(L.pw2, EPI_RESID, st.h, D, M, L.pw2_b, st.x, D, 1.f, nullptr, 1, s, prec_, KF_GEMM_PW2);
+            ln(L.ff2_ln_g, L.ff2_ln_b, st.h, nullptr);
+            gemm(L.ff2_w1, EPI_SILU, st.h, D, M, L.ff2_b1, st.u, c.ff_dim, 1.f, nullptr, 1, s, prec_, KF_GEMM_FFN);
+        }
         gemm(L.ff2_w2, EPI_RESID, st.u, c.ff_dim, M, L.ff2_b2, st.x, D, 0.5f, nullptr, 1, s, prec_, KF_GEMM_FFN);
-        ln(L.out_ln_g, L.out_ln_b, nullptr, st.x);
+        if (l + 1 < c.n_layers)
+            ln(L.out_ln_g, L.out_ln_b, st.h, st.x, layers_[(size_t)l + 1].ff1_ln_g, layers_[(size_t)l + 1].ff1_ln_b);
+        else
+            ln(L.out_ln_g, L.out_ln_b, nullptr, st.x);
     }
     PKX_HIP(hipMemcpyAsync(out, st.x, (size_t)M * D * 4, hipMemcpyDeviceToDevice, s));
     st.clc = st.clc + Tc < st.CL ? st.clc + Tc : st.CL;   // streaming_encoder.cpp:447-448

@@ -21,6 +21,7 @@ CASES = {
     "f32": (dict(d_model=128, n_heads=4, ff_dim=256), "f32", 0, 1e-4),
     "f16": (dict(d_model=128, n_heads=2, ff_dim=256), "f16", 1, 1e-2),
     "q8_0": (dict(d_model=256, n_heads=4, ff_dim=512), "q8_0", 1, 1e-2),
+    "f16_dk128": (dict(d_model=256, n_heads=2, ff_dim=512), "f16", 1, 1e-2),
 }
 
 
