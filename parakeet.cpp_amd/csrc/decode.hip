@@ -45,6 +45,7 @@ __device__ __forceinline__ float sigmoid_ref(float x) { return 1.0f / (1.0f + ex
 
 enum { MV_LSTM = 0, MV_JOINT = 1, MV_PLAIN = 2 };
 constexpr int MV_ITEMS = 16;   // items per LDS pass
+constexpr int MV_KMAX = 8;     // K <= 256 MV_KMAX: a wave holds its whole weight rows in registers
 
 struct MvArgs {
     const float* x;   // [B][ldx], K used
@@ -70,6 +71,17 @@ __global__ __launch_bounds__(256) void dec_mv_kernel(MvArgs a, DecState st) {
     extern __shared__ float xs[];   // [MV_ITEMS][K]
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int u = blockIdx.x * 4 + w;   // this wave's unit / row
+    // the wave's weight rows, all loads in flight at once, kept for every item pass
+    float4v wv[MV_KMAX][G];
+#pragma unroll
+    for (int ki = 0; ki < MV_KMAX; ++ki) {
+        const int k = 4 * lane + 256 * ki;
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+            wv[ki][g] = (u < a.n_out && k < a.K)
+                            ? *(const float4v*)(a.W + (int64_t)(MODE == MV_LSTM ? g * a.n_out + u : u) * a.K + k)
+                            : float4v{0.f, 0.f, 0.f, 0.f};
+    }
     for (int m0 = 0; m0 < a.B; m0 += MV_ITEMS) {
         const int mc = min(MV_ITEMS, a.B - m0);
         __syncthreads();
@@ -84,18 +96,18 @@ __global__ __launch_bounds__(256) void dec_mv_kernel(MvArgs a, DecState st) {
         for (int m = 0; m < MV_ITEMS; ++m)
 #pragma unroll
             for (int g = 0; g < G; ++g) acc[m][g] = 0.f;
-        for (int k = 4 * lane; k < a.K; k += 256) {
-            float4v wv[G];
 #pragma unroll
-            for (int g = 0; g < G; ++g)
-                wv[g] = *(const float4v*)(a.W + (int64_t)(MODE == MV_LSTM ? g * a.n_out + u : u) * a.K + k);
+        for (int ki = 0; ki < MV_KMAX; ++ki) {
+            const int k = 4 * lane + 256 * ki;
+            if (k >= a.K) break;
 #pragma unroll
             for (int m = 0; m < MV_ITEMS; ++m) {
                 if (m < mc) {
                     const float4v xv = *(const float4v*)(xs + m * a.K + k);
 #pragma unroll
                     for (int g = 0; g < G; ++g)
-                        acc[m][g] += (wv[g][0] * xv[0] + wv[g][1] * xv[1]) + (wv[g][2] * xv[2] + wv[g][3] * xv[3]);
+                        acc[m][g] += (wv[ki][g][0] * xv[0] + wv[ki][g][1] * xv[1]) +
+                                     (wv[ki][g][2] * xv[2] + wv[ki][g][3] * xv[3]);
                 }
             }
         }
@@ -290,6 +302,7 @@ void Model::transducer_greedy(const float* enc, int B, int T_max, const int* T_v
     require(n_tok <= pred_.V1, "decode: joint tokens exceed the embedding rows");
     require(H % 4 == 0 && Hj % 4 == 0, "decode: pred_hidden and joint_hidden must be multiples of 4");
     require((size_t)MV_ITEMS * 2 * H * 4 <= 160 * 1024, "decode: pred_hidden too large for the LDS input stage");
+    require(2 * H <= 256 * MV_KMAX && Hj <= 256 * MV_KMAX, "decode: pred_hidden above 1024 or joint_hidden above 2048");
     for (int b = 0; b < B; ++b) require(T_valid[b] >= 0 && T_valid[b] <= T_max, "decode: T_valid outside [0, T_max]");
     for (int i = 0; i < n_dur; ++i) require(durations && durations[i] >= 0, "decode: durations must be >= 0");
 

@@ -426,6 +426,12 @@ class Streaming:
     def step(self, mel: DeviceArray, out: DeviceArray, is_last=False, stream=None):
         """mel [S][n_mels][n] -> out [S][chunk_len][D] (device); returns the kept frame count."""
         S, F, n = mel.shape
+        if S != self.n_streams or F != self.model.cfg.n_mels or np.dtype(mel.dtype) != np.float32:
+            raise PkxError(f"streaming step: mel must be [{self.n_streams}][{self.model.cfg.n_mels}][n], got {mel.shape}")
+        tc = self.chunk_len(n)
+        if tc > 0 and (out.shape[0] != S or out.shape[1] < tc or out.shape[2] != self.model.cfg.d_model
+                       or np.dtype(out.dtype) != np.float32):
+            raise PkxError(f"streaming step: out must be f32 [{S}][>={tc}][{self.model.cfg.d_model}], got {out.shape}")
         nv = C.c_int()
         check(lib().pkx_streaming_step(self.handle, mel.ptr, int(n), 1 if is_last else 0, out.ptr, C.byref(nv),
                                        _sh(stream)))

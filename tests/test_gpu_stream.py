@@ -166,3 +166,22 @@ def test_streaming_model_from_gguf(gpu, stream, tmp_path):
         outs.append(np.concatenate(res, axis=1))
         st.close()
     assert np.array_equal(outs[0], outs[1])
+
+
+def test_streaming_binding_checks_shapes(gpu, stream):
+    """The device buffers' sizes cannot cross the C ABI, so the binding checks
+    them before the call: a window for the wrong number of streams or an output
+    too short for the chunk is refused without a launch."""
+    cfg, m, om, gm, tol = _models(gpu, "f32")
+    st = gpu.Streaming(gm, n_streams=2, max_window=25, stream=stream)
+    one = gpu.DeviceArray((1, cfg.n_mels, 9), np.float32)
+    out = gpu.DeviceArray((2, 2, cfg.d_model), np.float32)
+    with pytest.raises(gpu.PkxError, match="mel must be"):
+        st.step(one, out, stream=stream)
+    two = gpu.DeviceArray.from_numpy(np.zeros((2, cfg.n_mels, 9), np.float32), stream)
+    short = gpu.DeviceArray((2, 1, cfg.d_model), np.float32)
+    with pytest.raises(gpu.PkxError, match="out must be"):
+        st.step(two, short, stream=stream)
+    assert st.step_num == 0
+    assert st.step(two, out, stream=stream) == 2
+    st.close()
