@@ -1725,6 +1725,8 @@ void launch_gemm(Precision prec, int wtype, int epi, const GemmParams& p, hipStr
         if (wtype == GT_Q8_0) {
             if (t22 >= 384 || (glu && t22 >= 256)) dma_22q<GT_Q8_0>(epi, p, s);
             else if (glu) dma_epi<1, 2, GT_Q8_0>(epi, p, s);
+            // few rows (a streaming step: M = streams x chunk frames): the most workgroups
+            else if (p.M <= 512 && (int64_t)cdiv(p.M, 64) * cdiv(p.N, 64) <= 512) dma_epi<1, 1, GT_Q8_0>(epi, p, s);
             else if (t21 >= 128) dma_epi_pf<2, 1, GT_Q8_0>(epi, p, s);
             else dma_epi<1, 1, GT_Q8_0>(epi, p, s);
         } else if (wtype == GT_Q4_K) {
