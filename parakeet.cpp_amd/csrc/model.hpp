@@ -118,7 +118,7 @@ struct StreamState {
     void* kc = nullptr;                // [L][B][CL][D] keys, activation type
     void* vc = nullptr;                // [L][B][CL][D] values, activation type
     float* cc = nullptr;               // [L][B][LP][D] GLU history, oldest first
-    float* ppos = nullptr;             // [L][np][D] linear_pos of the table rows for
+    void* ppos = nullptr;              // [L][np][D] act: linear_pos of the table rows for
                                        // distances CL+tc_max-1 .. -(tc_max-1)
     float* sub = nullptr;              // [B][tsub_max][D] subsampled window
     float* x = nullptr;                // [B][tc_max][D] residual stream

@@ -23,7 +23,7 @@ struct StreamAttnParams {
     const void* qkv;       // [M][3D] act: q | k | v (biases applied), row b*Tc + i
     void* kc;              // [B][CL][D] act: this layer's key ring
     void* vc;              // [B][CL][D] act: value ring
-    const float* ppos;     // [np][D] positional projections, row r <-> distance CL + tc_max - 1 - r
+    const void* ppos;      // [np][D] act: positional projections, row r <-> distance CL + tc_max - 1 - r
     const float* bias_u;   // [D]
     const float* bias_v;   // [D]
     void* out;             // [M][D] act
@@ -31,13 +31,14 @@ struct StreamAttnParams {
     float scale;
 };
 
-// LDS floats of one stream_attn_kernel workgroup: keys and values of the
+// LDS bytes of one stream_attn_kernel workgroup: keys and values of the
 // Tk = CL + Tc frames and the NPB = CL + 2 Tc - 1 positional rows the chunk
-// reads, rows padded to dk + 1 (consecutive rows start in consecutive banks),
-// q + u and q + v [Tc][dk], scores [Tc][Tk].
-inline int stream_attn_lds_floats(int Tc, int CL, int dk) {
+// reads, in the activation type (as bytes), rows padded by 4 bytes
+// (consecutive rows start in consecutive banks); q + u and q + v [Tc][dk]
+// and the scores [Tc][Tk] in f32.
+inline int stream_attn_lds_bytes(int Tc, int CL, int dk, int as) {
     const int Tk = CL + Tc, npb = CL + 2 * Tc - 1;
-    return (2 * Tk + npb) * (dk + 1) + 2 * Tc * dk + Tc * Tk;
+    return (2 * Tk + npb) * (dk + 4 / as) * as + (2 * Tc * dk + Tc * Tk) * 4;
 }
 
 // One workgroup per (stream, head), 256 threads.  Everything the chunk reads
@@ -50,13 +51,13 @@ template <typename T, int DK>
 __global__ __launch_bounds__(256) void stream_attn_kernel(StreamAttnParams p) {
     extern __shared__ float sm[];
     const int b = blockIdx.x, h = blockIdx.y, dk = DK > 0 ? DK : p.dk, D = p.D, Tc = p.Tc, CL = p.CL;
-    const int Tk = CL + Tc, npb = CL + 2 * Tc - 1, ld = dk + 1;
-    float* ks = sm;                              // [Tk][ld]
-    float* vs = ks + Tk * ld;                    // [Tk][ld]
-    float* ps = vs + Tk * ld;                    // [npb][ld]: row j <-> distance CL + Tc - 1 - j
-    float* qu = ps + npb * ld;                   // [Tc][dk]
+    const int Tk = CL + Tc, npb = CL + 2 * Tc - 1, ld = dk + 4 / (int)sizeof(T);
+    float* qu = sm;                              // [Tc][dk]
     float* qv = qu + Tc * dk;                    // [Tc][dk]
     float* sc = qv + Tc * dk;                    // [Tc][Tk]
+    T* ks = (T*)(sc + Tc * Tk);                  // [Tk][ld]
+    T* vs = ks + Tk * ld;                        // [Tk][ld]
+    T* ps = vs + Tk * ld;                        // [npb][ld]: row j <-> distance CL + Tc - 1 - j
     const T* qkv = (const T*)p.qkv;
     T* kring = (T*)p.kc + (int64_t)b * CL * D + h * dk;
     T* vring = (T*)p.vc + (int64_t)b * CL * D + h * dk;
@@ -81,19 +82,19 @@ __global__ __launch_bounds__(256) void stream_attn_kernel(StreamAttnParams p) {
         *(int4v*)xv = *(const int4v*)sv;
 #pragma unroll
         for (int q = 0; q < VE; ++q) {
-            ks[r * ld + c0 + q] = (float)xk[q];
-            vs[r * ld + c0 + q] = (float)xv[q];
+            ks[r * ld + c0 + q] = xk[q];
+            vs[r * ld + c0 + q] = xv[q];
         }
     }
     const int prow0 = p.tc_max - Tc;             // global row of band row 0 (distance CL + Tc - 1)
-    const int vpp = dk / 4;
+    const T* ppos = (const T*)p.ppos;
 #pragma unroll 4
-    for (int e = threadIdx.x; e < npb * vpp; e += blockDim.x) {
-        const int r = e / vpp, c0 = (e % vpp) * 4;
-        float x[4];
-        *(int4v*)x = *(const int4v*)(p.ppos + (int64_t)(prow0 + r) * D + h * dk + c0);
+    for (int e = threadIdx.x; e < npb * vpr; e += blockDim.x) {
+        const int r = e / vpr, c0 = (e % vpr) * VE;
+        T x[VE];
+        *(int4v*)x = *(const int4v*)(ppos + (int64_t)(prow0 + r) * D + h * dk + c0);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) ps[r * ld + c0 + q] = x[q];
+        for (int q = 0; q < VE; ++q) ps[r * ld + c0 + q] = x[q];
     }
     for (int e = threadIdx.x; e < Tc * dk; e += blockDim.x) {
         const int i = e / dk, c = e % dk;
@@ -109,15 +110,15 @@ __global__ __launch_bounds__(256) void stream_attn_kernel(StreamAttnParams p) {
         float s = -INFINITY;
         if (kj >= empty && diff >= 0 && diff <= p.left_chunks) {
             // rel_shift of the [Tc][2 Tk - 1] block: column Tc - 1 - i + kj
-            const float* kr = ks + kj * ld;
-            const float* pr = ps + (Tc - 1 - i + kj) * ld;
+            const T* kr = ks + kj * ld;
+            const T* pr = ps + (Tc - 1 - i + kj) * ld;
             const float* a = qu + i * dk;
             const float* a2 = qv + i * dk;
             float ac = 0.f, bd = 0.f;
 #pragma unroll 16
             for (int c = 0; c < dk; ++c) {
-                ac += a[c] * kr[c];
-                bd += a2[c] * pr[c];
+                ac += a[c] * (float)kr[c];
+                bd += a2[c] * (float)pr[c];
             }
             s = (ac + bd) * p.scale;
         }
@@ -149,7 +150,7 @@ __global__ __launch_bounds__(256) void stream_attn_kernel(StreamAttnParams p) {
         const float* r = sc + i * Tk;
         float acc = 0.f;
 #pragma unroll 8
-        for (int kj = 0; kj < Tk; ++kj) acc += r[kj] * vs[kj * ld + c];
+        for (int kj = 0; kj < Tk; ++kj) acc += r[kj] * (float)vs[kj * ld + c];
         out[(int64_t)(b * Tc + i) * D + h * dk + c] = to_act<T>(acc);
     }
     // the chunk's frames take the ring slots of the oldest ones (every ring
@@ -158,8 +159,8 @@ __global__ __launch_bounds__(256) void stream_attn_kernel(StreamAttnParams p) {
     for (int e = threadIdx.x; e < Tc * dk; e += blockDim.x) {
         const int q = e / dk, c = e % dk;
         const int64_t slot = (int64_t)((p.head + q) % CL) * D + c;
-        kring[slot] = to_act<T>(ks[(CL + q) * ld + c]);
-        vring[slot] = to_act<T>(vs[(CL + q) * ld + c]);
+        kring[slot] = ks[(CL + q) * ld + c];
+        vring[slot] = vs[(CL + q) * ld + c];
     }
 }
 
@@ -324,7 +325,7 @@ std::unique_ptr<StreamState> Model::stream_create(int n_streams, int max_window,
     const int D = c.d_model, dk = D / c.n_heads;
     require(dk <= 256 && dk % 8 == 0 && D % 8 == 0 && D <= 2048,
             "streaming encoder: d_model above 2048, or head width above 256 or not a multiple of 8");
-    // LDS beyond the default 64 KiB (attention: stream_attn_lds_floats, conv:
+    // LDS beyond the default 64 KiB (attention: stream_attn_lds_bytes, conv:
     // SC_FRAMES x D floats)
     for (const void* fn : {(const void*)stream_attn_kernel<f16, 0>, (const void*)stream_attn_kernel<float, 0>,
                            (const void*)stream_attn_kernel<f16, 64>, (const void*)stream_attn_kernel<float, 64>,
@@ -342,7 +343,7 @@ std::unique_ptr<StreamState> Model::stream_create(int n_streams, int max_window,
     st->LP = c.conv_kernel - 1;
     require(st->tc_max <= st->CL, "streaming encoder: a window yields more frames than the attention cache holds");
     require(st->tc_max <= 32, "streaming encoder: at most 32 encoder frames per chunk (max_window <= 255)");
-    require(stream_attn_lds_floats(st->tc_max, st->CL, dk) * 4 <= 160 * 1024,
+    require(stream_attn_lds_bytes(st->tc_max, st->CL, dk, prec_ == PREC_F16 ? 2 : 4) <= 160 * 1024,
             "streaming encoder: attention cache x head width too large for one workgroup's LDS");
     st->np = st->CL + 2 * st->tc_max - 1;
     const size_t as = prec_ == PREC_F16 ? 2 : 4, L = (size_t)c.n_layers, B = (size_t)n_streams;
@@ -356,7 +357,7 @@ std::unique_ptr<StreamState> Model::stream_create(int n_streams, int max_window,
     st->kc = al(L * B * st->CL * D * as);
     st->vc = al(L * B * st->CL * D * as);
     st->cc = (float*)al(L * B * st->LP * D * 4);
-    st->ppos = (float*)al(L * st->np * D * 4);
+    st->ppos = al(L * st->np * D * as);
     st->sub = (float*)al(B * st->tsub_max * D * 4);
     st->x = (float*)al(M * D * 4);
     st->h = al(M * D * as);
@@ -370,7 +371,7 @@ std::unique_ptr<StreamState> Model::stream_create(int n_streams, int max_window,
     void* pe = al((size_t)(2 * Pn - 1) * D * as);
     launch_rel_pos_encoding(prec_, pe, Pn, D, s);
     for (int l = 0; l < c.n_layers; ++l)
-        gemm(layers_[(size_t)l].wpos, EPI_STORE_F32, pe, D, st->np, nullptr, st->ppos + (size_t)l * st->np * D, D,
+        gemm(layers_[(size_t)l].wpos, EPI_STORE, pe, D, st->np, nullptr, (uint8_t*)st->ppos + (size_t)l * st->np * D * as, D,
              1.f, nullptr, 1, s, prec_, KF_GEMM_POS);
     stream_reset(*st, s);
     PKX_HIP(hipStreamSynchronize(s));
@@ -456,7 +457,7 @@ int Model::stream_step(StreamState& st, const float* mel, int n, bool is_last, f
             a.qkv = st.qkv;
             a.kc = (uint8_t*)st.kc + (size_t)l * LB * st.CL * D * as;
             a.vc = (uint8_t*)st.vc + (size_t)l * LB * st.CL * D * as;
-            a.ppos = st.ppos + (size_t)l * st.np * D;
+            a.ppos = (const uint8_t*)st.ppos + (size_t)l * st.np * D * as;
             a.bias_u = L.pos_u;
             a.bias_v = L.pos_v;
             a.out = st.g;
@@ -470,7 +471,7 @@ int Model::stream_step(StreamState& st, const float* mel, int n, bool is_last, f
             a.D = D;
             a.dk = dk;
             a.scale = 1.0f / std::sqrt((float)dk);
-            const uint32_t shm = (uint32_t)stream_attn_lds_floats(Tc, st.CL, dk) * 4u;
+            const uint32_t shm = (uint32_t)stream_attn_lds_bytes(Tc, st.CL, dk, (int)as);
             mark(KF_ATTENTION, true);
             const dim3 grid(B, H);
             if (prec_ == PREC_F16) {
