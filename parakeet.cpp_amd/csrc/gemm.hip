@@ -1658,6 +1658,13 @@ static void dma_22q(int epi, const GemmParams& p, hipStream_t s) {
 template <int WT>
 static bool dma_kg2(int epi, const GemmParams& p, hipStream_t s) {
     if (p.K % 128 != 0 || p.K < 2048 || (int64_t)cdiv(p.M, 128) * cdiv(p.N, 64) > 256) return false;
+    if (WT != GT_F16 && p.M <= 512) {
+        switch (epi) {
+        case EPI_RESID: run_dma<1, 1, WT, EPI_RESID, DMA_NS, 2, 0>(p, s); return true;
+        case EPI_RESID_LN: run_dma<1, 1, WT, EPI_RESID_LN, DMA_NS, 2, 0>(p, s); return true;
+        default: break;
+        }
+    }
     switch (epi) {
     case EPI_STORE: run_dma<2, 1, WT, EPI_STORE, DMA_NS, 2, WT == GT_F16 ? 0 : 2>(p, s); return true;
     case EPI_STORE_F32: run_dma<2, 1, WT, EPI_STORE_F32, DMA_NS, 2, WT == GT_F16 ? 0 : 2>(p, s); return true;

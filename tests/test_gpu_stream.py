@@ -22,6 +22,8 @@ CASES = {
     "f16": (dict(d_model=128, n_heads=2, ff_dim=256), "f16", 1, 1e-2),
     "q8_0": (dict(d_model=256, n_heads=4, ff_dim=512), "q8_0", 1, 1e-2),
     "f16_dk128": (dict(d_model=256, n_heads=2, ff_dim=512), "f16", 1, 1e-2),
+    # K = 2048 in linear2: the two-K-group products at few rows
+    "q8_0_ff2048": (dict(d_model=256, n_heads=4, ff_dim=2048), "q8_0", 1, 1e-2),
 }
 
 
