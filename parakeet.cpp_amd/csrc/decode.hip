@@ -85,9 +85,26 @@ __global__ __launch_bounds__(256) void dec_mv_kernel(MvArgs a, DecState st) {
     for (int m0 = 0; m0 < a.B; m0 += MV_ITEMS) {
         const int mc = min(MV_ITEMS, a.B - m0);
         __syncthreads();
-        for (int i = threadIdx.x; i < mc * (a.K / 4); i += 256) {
-            const int m = i / (a.K / 4), k4 = i - m * (a.K / 4);
-            *(float4v*)(xs + m * a.K + 4 * k4) = *(const float4v*)(a.x + (int64_t)(m0 + m) * a.ldx + 4 * k4);
+        // the items' inputs into LDS, eight 16-byte loads in flight per thread
+        const int n4 = mc * (a.K / 4);
+        for (int i0 = threadIdx.x; i0 < n4; i0 += 256 * 8) {
+            float4v v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int i = i0 + 256 * j;
+                if (i < n4) {
+                    const int m = i / (a.K / 4), k4 = i - m * (a.K / 4);
+                    v[j] = *(const float4v*)(a.x + (int64_t)(m0 + m) * a.ldx + 4 * k4);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int i = i0 + 256 * j;
+                if (i < n4) {
+                    const int m = i / (a.K / 4), k4 = i - m * (a.K / 4);
+                    *(float4v*)(xs + m * a.K + 4 * k4) = v[j];
+                }
+            }
         }
         __syncthreads();
         if (u >= a.n_out) continue;
