@@ -128,20 +128,44 @@ __global__ __launch_bounds__(256) void dec_mv_kernel(MvArgs a, DecState st) {
                 }
             }
         }
-        // butterfly sums: every lane ends with every (item, gate) total
-#pragma unroll
-        for (int m = 0; m < MV_ITEMS; ++m)
-#pragma unroll
-            for (int g = 0; g < G; ++g)
-                for (int o = 32; o > 0; o >>= 1) acc[m][g] += __shfl_xor(acc[m][g], o, 64);
         // lane m finishes item m0 + m
         float z[G];
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            z[g] = 0.f;
+        if constexpr (G * MV_ITEMS == 64) {
+            // recursive halving over the 64 (item, gate) sums: at each step a
+            // lane keeps half of its values and adds its partner's copy of
+            // them, so lane L ends with the total of value L = 4 m + g
+            float t[64];
 #pragma unroll
             for (int m = 0; m < MV_ITEMS; ++m)
-                if (m == lane) z[g] = acc[m][g];
+#pragma unroll
+                for (int g = 0; g < G; ++g) t[m * G + g] = acc[m][g];
+#pragma unroll
+            for (int step = 0; step < 6; ++step) {
+                const int o = 32 >> step;
+                const bool hi = (lane & o) != 0;
+#pragma unroll
+                for (int i = 0; i < (32 >> step); ++i) {
+                    const float send = hi ? t[i] : t[i + o];
+                    const float keep = hi ? t[i + o] : t[i];
+                    t[i] = keep + __shfl_xor(send, o, 64);
+                }
+            }
+#pragma unroll
+            for (int g = 0; g < G; ++g) z[g] = __shfl(t[0], (lane & (MV_ITEMS - 1)) * G + g, 64);
+        } else {
+            // butterfly sums: every lane ends with every item total
+#pragma unroll
+            for (int m = 0; m < MV_ITEMS; ++m)
+#pragma unroll
+                for (int g = 0; g < G; ++g)
+                    for (int o = 32; o > 0; o >>= 1) acc[m][g] += __shfl_xor(acc[m][g], o, 64);
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                z[g] = 0.f;
+#pragma unroll
+                for (int m = 0; m < MV_ITEMS; ++m)
+                    if (m == lane) z[g] = acc[m][g];
+            }
         }
         if (lane >= mc) continue;
         const int b = m0 + lane;
