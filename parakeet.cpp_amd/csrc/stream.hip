@@ -312,7 +312,7 @@ constexpr int SC_TCM = 8;   // chunk frames of the compile-time conv path
 }  // namespace
 
 StreamState::~StreamState() {
-    for (void* q : allocs) hipFree(q);
+    for (void* q : allocs) (void)hipFree(q);
 }
 
 std::unique_ptr<StreamState> Model::stream_create(int n_streams, int max_window, hipStream_t s) {
