@@ -61,3 +61,30 @@ def test_decode_rejects_bad_arguments(gpu, stream):
     with pytest.raises(gpu.PkxError, match="T_valid"):
         gm.transducer_greedy(d_enc, [5], durations=(0, 1, 2, 3, 4), stream=stream)
     d_enc.free()
+
+
+def test_greedy_decode_more_items_than_one_pass(gpu, stream):
+    """21 items: the matvec kernels take the items in passes of 16 through LDS
+    (the second pass reuses the weight rows the wave holds in registers)."""
+    durations = (0, 1, 2, 3, 4)
+    cfg, m = _model(durations, seed=9)
+    gm = gpu.Model.from_tensors(m)
+    tr = oracle.Transducer(m)
+    rng = np.random.default_rng(21)
+    T_valid = [int(t) for t in rng.integers(0, 41, 21)]
+    B, T_max = len(T_valid), 40
+    enc = rng.standard_normal((B, T_max, cfg.d_model)).astype(np.float32)
+    print(f"[decode] B={B} T={T_valid}", flush=True)
+    d_enc = gpu.DeviceArray.from_numpy(enc, stream)
+    got = gm.transducer_greedy(d_enc, T_valid, durations=durations, max_symbols=10, stream=stream)
+    total = 0
+    for b in range(B):
+        ids, fr, cf, sp = tr.greedy(enc[b, :T_valid[b]], durations=durations, max_symbols=10)
+        g_ids, g_fr, g_cf, g_sp = got[b]
+        total += len(ids)
+        assert np.array_equal(g_ids, ids), (b, g_ids[:20], ids[:20])
+        assert np.array_equal(g_fr, fr) and np.array_equal(g_sp, sp)
+        assert np.max(np.abs(g_cf - cf), initial=0.0) <= 1e-5
+    print(f"[decode] {total} tokens identical over {B} items", flush=True)
+    assert total > 20
+    d_enc.free()
