@@ -23,12 +23,16 @@ import pk_model as pm  # noqa: E402
 import pkx  # noqa: E402
 
 PEAK_F16_TFLOPS = 2500.0   # MI355X dense f16/bf16 MFMA
+PEAK_F32_TFLOPS = 157.3    # MI355X dense f32 MFMA
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 
 # 0.6B shape (parakeet-tdt-0.6b-v2: no linear/conv biases)
 CFG = dict(d_model=1024, n_layers=24, n_heads=8, ff_dim=4096, conv_kernel=9, n_mels=128,
            sub_channels=256, xscaling=False, vocab_size=1024, attn_bias=False, ff_bias=False,
            conv_bias=False)
+# 110M shape (parakeet-tdt_ctc-110m: linear and conv biases present)
+CFG110 = dict(d_model=512, n_layers=17, n_heads=8, ff_dim=2048, conv_kernel=9, n_mels=80,
+              sub_channels=256, xscaling=False, vocab_size=1024)
 B, T_MEL, HOP_S = 16, 1000, 0.01
 
 
@@ -39,7 +43,8 @@ def family_work(cfg, B, Tp):
     return {
         "gemm_ffn": ("TFLOP/s", 2.0 * M * D * FF),
         "gemm_qkv": ("TFLOP/s", 2.0 * M * D * 3 * D),
-        "gemm_pos": ("TFLOP/s", 2.0 * P * D * D),
+        # one launch projects the positional table for all L layers ([L*D][D] weight)
+        "gemm_pos": ("TFLOP/s", 2.0 * P * D * (cfg.n_layers * D)),
         "gemm_out": ("TFLOP/s", 2.0 * M * D * D),
         # pointwise_conv1 (+ GLU, and with kernel 9 the depthwise conv + BN + SiLU in its epilogue)
         "gemm_pw1_glu": ("TFLOP/s", 2.0 * M * D * 2 * D),
@@ -68,10 +73,10 @@ def layernorm_bytes(cfg, B, Tp, launches):
     return ((3 * L + 1) * single + (L - 1) * fused + last) / launches
 
 
-def other_config(name, qtype, cfg_kw, lens, T_max, steps, warmup, stream):
+def other_config(name, qtype, cfg_kw, lens, T_max, steps, warmup, stream, base=None):
     """The other benchmark shapes, same measurement (one GPU, inputs resident,
     FFN GEMM sampled with per-dispatch events inside the timed region)."""
-    kw = dict(CFG)
+    kw = dict(CFG if base is None else base)
     kw.update(cfg_kw)
     cfg = pm.Config(**kw)
     model = pm.synthesize(cfg, qtype, heads=False)
@@ -103,11 +108,14 @@ def other_config(name, qtype, cfg_kw, lens, T_max, steps, warmup, stream):
     M = Bc * Tp
     ffn_flop = 2.0 * M * cfg.d_model * cfg.ff_dim
     ffn_tf = ffn_flop / (ffn_ms / 1e3 / ffn_n) / 1e12
+    f32 = gm.precision == pkx.PREC_F32
+    peak = PEAK_F32_TFLOPS if f32 else PEAK_F16_TFLOPS
     audio_s = float(np.sum(lens)) * HOP_S
-    out = {"workload": name, "ms_per_step": round(ms, 4), "rtfx": round(audio_s / (ms / 1e3), 1),
+    out = {"workload": name, "dtype": "f32" if f32 else "f16", "ms_per_step": round(ms, 4),
+           "rtfx": round(audio_s / (ms / 1e3), 1),
            "frames_per_s": round(float(np.sum(vo)) / (ms / 1e3), 1),
            "gemm_ffn": {"avg_us": round(ffn_ms / ffn_n * 1e3, 2), "achieved": round(ffn_tf, 2),
-                        "unit": "TFLOP/s", "frac": round(ffn_tf / PEAK_F16_TFLOPS, 4)},
+                        "unit": "TFLOP/s", "peak": peak, "frac": round(ffn_tf / peak, 4)},
            "steps": steps}
     d_mel.free()
     d_out.free()
@@ -231,24 +239,42 @@ def streaming(stream, n_streams=256, steps=50, warmup=5):
             "kernels": fams, "steps": steps}
 
 
-def cpu_baseline(model, mel_item, budget_s=12.0):
+def cpu_model_name():
+    """The host CPU's model name (what lscpu prints as "Model name")."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(model, mel, valid):
+    """The oracle (C restatement of the reference encoder, OpenMP over rows and
+    heads) on the benchmarked workload itself: the whole B x 1000-frame batch,
+    once with every host thread this process may use and once with 8 threads
+    (the reference's default, kDefaultThreads in src/ggml_graph.cpp:47)."""
     import oracle
     om = oracle.OracleModel(model)
-    threads = oracle.get_threads()
-    om.encoder(mel_item[:, :, :200])                         # warm-up (page in weights)
-    n, t0 = 0, time.perf_counter()
-    while True:
-        om.encoder(mel_item)
-        n += 1
+    n_all = oracle.get_threads()
+    om.encoder(mel[:1, :, :200], np.array([199]))               # warm-up (page in weights)
+    runs = []
+    for threads in (n_all, 8):
+        oracle.set_threads(threads)
+        t0 = time.perf_counter()
+        om.encoder(mel, valid - 1)
         el = time.perf_counter() - t0
-        if el > budget_s or n >= 8:
-            break
-    audio = n * mel_item.shape[2] * HOP_S
-    return {"value": round(audio / el, 3), "unit": "RTFx (audio s / wall s)", "cores": threads,
-            "kind": "port",
-            "sample": f"{n} x 1 clip of {mel_item.shape[2]} frames (10 s), same 0.6B q8_0 weights "
-                      f"dequantised to f32, C restatement of the reference encoder (ggml absent), "
-                      f"{el:.1f} s wall, OpenMP {threads} threads"}
+        audio = mel.shape[0] * mel.shape[2] * HOP_S
+        runs.append({"threads": threads, "value": round(audio / el, 3), "wall_s": round(el, 2)})
+    oracle.set_threads(n_all)
+    return {"value": runs[0]["value"], "unit": "RTFx (audio s / wall s)", "cores": n_all, "kind": "port",
+            "cpu_model": cpu_model_name(), "nproc": os.cpu_count(), "runs": runs,
+            "sample": f"the benchmarked batch ({mel.shape[0]} x {mel.shape[2]} frames = "
+                      f"{mel.shape[0] * mel.shape[2] * HOP_S:.0f} s of audio), same 0.6B q8_0 weights "
+                      f"dequantised to f32, C restatement of the reference encoder (ggml absent); "
+                      f"{runs[0]['wall_s']} s at {n_all} threads, {runs[1]['wall_s']} s at 8 threads"}
 
 
 def main():
@@ -362,6 +388,14 @@ def main():
                 "per_launch": "2*M*D*FF = %.3f GFLOP (M=B*T'=%d, D=%d, FF=%d)" % (
                     work["gemm_ffn"][1] / 1e9, B * Tp, cfg.d_model, cfg.ff_dim)}
 
+    lnk = kernels.get("layernorm", {})
+    roofline_hbm = {"bound": "hbm", "kernel": "layernorm (norm_out fused with the next block's "
+                                              "norm_feed_forward1; layer 0's norm_feed_forward1)",
+                    "achieved": lnk.get("achieved"), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                    "frac": lnk.get("frac"), "traffic": None, "avg_us": lnk.get("avg_us"),
+                    "per_launch": "f32 residual read (+ f32 write back) + f16 normalised rows: %.1f MB average" % (
+                        layernorm_bytes(cfg, B, Tp, cfg.n_layers + 1) / 1e6)}
+
     pcm_line = pcm_in(gm, cfg, stream, min(args.steps, 10))
     _, vo_dec = gm.encoder_forward(d_mel, valid, d_out, stream=stream)
     dec_line = greedy_decode(gm, cfg, stream, d_out, vo_dec)
@@ -381,6 +415,7 @@ def main():
                    "global_batch": B, "seq_len": T_MEL, "parallelism": "none (1 GPU)"},
         "frames_per_s": round(B * Tp / (ms_step / 1e3), 1),
         "roofline": roofline,
+        "roofline_hbm": roofline_hbm,
         "kernels": kernels,
         "kernel_busy_ms_per_step": round(busy_ms, 4),
         "pcm_in": pcm_line,
@@ -398,9 +433,14 @@ def main():
                          dict(n_layers=42), np.full(8, 3000, dtype=np.int32), 3000, 5, 1, stream),
             other_config("0.6B q4_K weights, batch 16 x 10 s", "q4_k", {}, np.full(16, 1000, dtype=np.int32), 1000,
                          10, 2, stream),
+            # the 110M shape in f32 (f32 MFMA 16x16x4; FFN against the f32 peak)
+            other_config("110M shape f32 (17 blocks, d_model 512, 8 heads x 64, ff 2048, 80-mel), batch 1 x 10 s",
+                         "f32", {}, np.full(1, 1000, dtype=np.int32), 1000, 20, 3, stream, base=CFG110),
+            other_config("110M shape f32, batch 16 x 10 s", "f32", {}, np.full(16, 1000, dtype=np.int32), 1000,
+                         10, 2, stream, base=CFG110),
         ]
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(model, mel[:1].copy())
+        line["cpu_baseline"] = cpu_baseline(model, mel, valid)
     print(json.dumps(line))
 
 

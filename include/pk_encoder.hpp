@@ -34,32 +34,47 @@
 
 namespace pk {
 
-// Cache-aware streaming schedule (src/model_loader.hpp:15-26): the [first,
-// later] values of the chunk arrays.
+// Cache-aware streaming schedule (src/model_loader.hpp:15-26), filled for
+// models whose att_context_style is not "regular".
 struct StreamingCfg {
+    std::vector<int32_t> chunk_size;
+    std::vector<int32_t> shift_size;
+    std::vector<int32_t> pre_encode_cache_size;
+    int32_t cache_drop_size = 0;
+    int32_t last_channel_cache_size = 0;
+    int32_t valid_out_len = 0;
+    int32_t drop_extra_pre_encoded = 0;
     bool present = false;
-    std::vector<int32_t> chunk_size, shift_size, pre_encode_cache_size;
-    int32_t last_channel_cache_size = 0, valid_out_len = 0, drop_extra_pre_encoded = 0;
 };
 
-// Encoder fields of the reference's ParakeetConfig (src/model_loader.hpp:27-52).
+// The reference's ParakeetConfig, field for field (src/model_loader.hpp:27-52),
+// read from the same GGUF keys with the same defaults
+// (src/model_loader.cpp:99-156).
 struct ParakeetConfig {
-    int feat_in = 0;                     // n_mels
-    int d_model = 0;
-    int n_layers = 0;
-    int n_heads = 0;
-    int ff_dim = 0;
-    int conv_kernel = 0;
-    int subsampling_conv_channels = 0;
+    std::string arch;
+    // encoder
+    uint32_t feat_in = 0, d_model = 0, n_layers = 0, n_heads = 0, ff_dim = 0, conv_kernel = 0;
+    std::string conv_norm_type;
+    uint32_t subsampling_factor = 0, subsampling_conv_channels = 0, pos_emb_max_len = 5000;
     bool xscaling = true;
-    int vocab_size = 0;
-    int n_durations = 0;                 // len(tdt.durations); 0 without a TDT head
-    std::string conv_norm_type = "batch_norm";
+    // cache-aware streaming / causal configuration
     int32_t att_context_left = -1, att_context_right = -1;
     std::string att_context_style = "regular";
     bool causal_downsampling = false;
     bool conv_causal = false;
     StreamingCfg streaming;
+    // preprocessor
+    uint32_t sample_rate = 16000, n_mels = 0, n_fft = 0, win_length = 0, hop_length = 0;
+    float preemph = 0.0f, mag_power = 2.0f, log_zero_guard = 0.0f;
+    std::string normalize;
+    // transducer (optional)
+    uint32_t pred_hidden = 0, pred_rnn_layers = 0, joint_hidden = 0;
+    std::string joint_activation;
+    std::vector<int32_t> tdt_durations;
+    uint32_t max_symbols = 10;
+    // vocab
+    uint32_t vocab_size = 0, blank_id = 0;
+    std::vector<std::string> tokenizer_pieces;
 };
 
 class ModelLoader {
@@ -74,6 +89,7 @@ public:
     bool load(const std::string& path) { return load(path, PKX_PREC_AUTO); }
     bool load(const std::string& path, int precision);
     const ParakeetConfig& config() const { return cfg_; }
+    const std::vector<std::string>& tokenizer_pieces() const { return cfg_.tokenizer_pieces; }
     const std::string& last_error() const { return err_; }
 
     pkx_model* handle() const { return model_; }
@@ -162,8 +178,8 @@ class ConformerLayer {
 public:
     ConformerLayer(const ModelLoader& ml, int layer_idx);
 
-    // x [T][d_model]; pos_emb [pos_len = 2T-1][d_model] must be
-    // rel_pos_encoding(T, d_model) (the device path regenerates that table);
+    // x [T][d_model]; pos_emb [pos_len = 2T-1][d_model], used as given (e.g.
+    // rel_pos_encoding(T, d_model), or a table computed elsewhere in f32);
     // out [T][d_model].
     void forward(const std::vector<float>& x, int T, const std::vector<float>& pos_emb,
                  int pos_len, int valid_len, std::vector<float>& out) const;
@@ -210,10 +226,40 @@ struct TokenInfo {
     int32_t span;
 };
 
+// The prediction network (src/prediction.hpp:52-105) and joint
+// (src/joint.hpp:27-80) of a loaded model.  Their weights are uploaded by the
+// ModelLoader (prediction LSTM, joint enc / pred / output projections); these
+// objects name them for transducer_greedy_batch, which runs every step on the
+// device.  The reference's per-step host methods (forward, step, step_logits)
+// have no counterpart here.
+class PredictionNet {
+public:
+    explicit PredictionNet(const ModelLoader& ml);
+    const ModelLoader& loader() const { return ml_; }
+
+private:
+    const ModelLoader& ml_;
+};
+
+class Joint {
+public:
+    explicit Joint(const ModelLoader& ml);
+    const ModelLoader& loader() const { return ml_; }
+
+private:
+    const ModelLoader& ml_;
+};
+
 // Batched greedy transducer decode (src/transducer_batch.hpp:12-20) over the
 // model's prediction network and joint, on the device.  encs[n]: row-major
 // [T[n]][enc_hidden]; durations empty -> RNNT, else TDT.  Outputs per item:
-// ids[n] and, if toks != nullptr, TokenInfo[n].
+// ids[n] and, if toks != nullptr, TokenInfo[n].  pred and joint must come from
+// the same loader.
+void transducer_greedy_batch(const PredictionNet& pred, const Joint& joint,
+                             const std::vector<std::vector<float>>& encs, const std::vector<int>& T,
+                             int enc_hidden, const std::vector<int32_t>& durations, int blank_id, int max_symbols,
+                             std::vector<std::vector<int32_t>>& ids, std::vector<std::vector<TokenInfo>>* toks);
+// The same with the loader named directly.
 void transducer_greedy_batch(const ModelLoader& ml, const std::vector<std::vector<float>>& encs,
                              const std::vector<int>& T, int enc_hidden, const std::vector<int32_t>& durations,
                              int blank_id, int max_symbols, std::vector<std::vector<int32_t>>& ids,

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define PKX_ABI_VERSION 2
+#define PKX_ABI_VERSION 3
 
 typedef struct pkx_model pkx_model;
 
@@ -102,6 +102,18 @@ int pkx_event_elapsed_ms(float* ms, void* start, void* stop);   /* synchronises 
  * encoder, CTC-head and TDT-joint tensors.  precision: PKX_PREC_*. */
 int pkx_model_load_gguf(const char* path, int precision, pkx_model** out);
 
+/* Every key-value pair of a GGUF v3 header, in file order: the KV half of
+ * gguf_init_from_file that pk::ModelLoader::load reads ParakeetConfig from
+ * (src/model_loader.cpp:99-156).  visit(user, key, type, elem_type, n, data):
+ * type is the GGUF value type (4 u32, 5 i32, 6 f32, 7 bool, 8 string, 9 array,
+ * ...); elem_type is the element type of an array and equals type for a
+ * scalar; n is the element count (1 for a scalar); data points to n packed
+ * little-endian values (bools as one byte), or to n pkx_gguf_str for strings.
+ * Pointers are valid only during the call. */
+typedef struct { const char* s; size_t n; } pkx_gguf_str;
+typedef void (*pkx_gguf_kv_fn)(void* user, const char* key, int type, int elem_type, uint64_t n, const void* data);
+int pkx_gguf_read_kv(const char* path, pkx_gguf_kv_fn visit, void* user);
+
 /* Build a handle from tensors supplied one by one (same names, ggml ne order
  * and raw bytes as in a GGUF), then pkx_model_finalize(). */
 int pkx_model_create(const pkx_config* cfg, int precision, pkx_model** out);
@@ -150,17 +162,21 @@ int pkx_subsampling_forward(pkx_model* m, const float* mel_dev, int B, int T_max
 /* pk::ConformerLayer::forward / forward_with_conv (src/conformer.cpp:426-516)
  * and build_graph_batched (:285-353).  x_dev, out_dev [B][T][d_model] f32
  * (may alias); valid host [B] (NULL = T); conv_out_dev NULL or [B][T][d_model]
- * receives the conv-module output.  The rel-pos table is computed internally
- * (pk::rel_pos_encoding). */
+ * receives the conv-module output.  pos_emb_dev is the caller's relative
+ * positional table [2T-1][d_model] f32 (the reference's pos_emb argument,
+ * src/conformer.hpp:70-91), used as given; NULL computes
+ * pk::rel_pos_encoding(T, d_model) on the device. */
 int pkx_conformer_layer_forward(pkx_model* m, int layer, const float* x_dev, int B, int T,
-                                const int* valid, float* out_dev, float* conv_out_dev,
-                                void* stream);
+                                const int* valid, const float* pos_emb_dev, float* out_dev,
+                                float* conv_out_dev, void* stream);
 
 /* pk::RelPosAttention::forward / build_graph_batched
  * (src/relpos_attention.cpp:162-306, :308-333): x_dev is the already
- * normalised input [B][T][d_model]. */
+ * normalised input [B][T][d_model]; pos_emb_dev as for
+ * pkx_conformer_layer_forward (src/relpos_attention.hpp:52-55). */
 int pkx_relpos_attention_forward(pkx_model* m, int layer, const float* x_dev, int B, int T,
-                                 const int* valid, float* out_dev, void* stream);
+                                 const int* valid, const float* pos_emb_dev, float* out_dev,
+                                 void* stream);
 
 /* pk::ConformerLayer::conv_module_forward (src/conformer.cpp:518-543) and
  * build_conv_module (:38-164): c_dev = norm_conv(residual). */

@@ -181,6 +181,23 @@ int pkx_model_load_gguf(const char* path, int precision, pkx_model** out) {
     });
 }
 
+int pkx_gguf_read_kv(const char* path, pkx_gguf_kv_fn fn, void* user) {
+    return guarded([&] {
+        need(path && fn, "null argument");
+        std::vector<pkx_gguf_str> tmp;
+        pkx::read_gguf_kv(path, [&](const std::string& key, int type, int et, uint64_t n, const void* raw,
+                                    const std::vector<std::string>* strs) {
+            if (strs) {
+                tmp.resize(strs->size());
+                for (size_t i = 0; i < strs->size(); ++i) tmp[i] = pkx_gguf_str{(*strs)[i].data(), (*strs)[i].size()};
+                fn(user, key.c_str(), type, et, n, tmp.data());
+            } else {
+                fn(user, key.c_str(), type, et, n, raw);
+            }
+        });
+    });
+}
+
 int pkx_model_create(const pkx_config* cfg, int precision, pkx_model** out) {
     return guarded([&] {
         need(cfg && out, "null argument");
@@ -263,18 +280,18 @@ int pkx_subsampling_forward(pkx_model* m, const float* mel, int B, int T_max, co
 }
 
 int pkx_conformer_layer_forward(pkx_model* m, int layer, const float* x, int B, int T, const int* valid,
-                                float* out, float* conv_out, void* s) {
+                                const float* pos_emb, float* out, float* conv_out, void* s) {
     return guarded([&] {
         need(m && x && out, "null argument");
-        m->impl->conformer_layer_forward(layer, x, B, T, valid, out, conv_out, st(s));
+        m->impl->conformer_layer_forward(layer, x, B, T, valid, pos_emb, out, conv_out, st(s));
     });
 }
 
 int pkx_relpos_attention_forward(pkx_model* m, int layer, const float* x, int B, int T, const int* valid,
-                                 float* out, void* s) {
+                                 const float* pos_emb, float* out, void* s) {
     return guarded([&] {
         need(m && x && out, "null argument");
-        m->impl->relpos_attention_forward(layer, x, B, T, valid, out, st(s));
+        m->impl->relpos_attention_forward(layer, x, B, T, valid, pos_emb, out, st(s));
     });
 }
 

@@ -200,6 +200,42 @@ std::vector<float> read_f32_tensor(File& f, const Header& h, const TensorInfo& t
 
 }  // namespace
 
+// Every KV pair of the header, in file order, with its value in raw form: the
+// key-value half of gguf_init_from_file that pk::ModelLoader::load reads its
+// ParakeetConfig from (src/model_loader.cpp:99-156).
+void read_gguf_kv(const std::string& path, const KvVisitor& visit) {
+    File f(path);
+    require(f.get<uint32_t>() == 0x46554747u, "not a GGUF file: " + path);
+    const uint32_t version = f.get<uint32_t>();
+    require(version == 3 || version == 2, "unsupported GGUF version " + std::to_string(version));
+    (void)f.get<uint64_t>();   // tensor count
+    const uint64_t n_kv = f.get<uint64_t>();
+    std::vector<uint8_t> raw;
+    std::vector<std::string> strs;
+    for (uint64_t i = 0; i < n_kv; ++i) {
+        const std::string key = f.str();
+        const uint32_t t = f.get<uint32_t>();
+        uint32_t et = t;
+        uint64_t n = 1;
+        if (t == KV_ARR) {
+            et = f.get<uint32_t>();
+            n = f.get<uint64_t>();
+        }
+        strs.clear();
+        if (et == KV_STR) {
+            require(n < (1ull << 24), "GGUF: string array too long");
+            for (uint64_t k = 0; k < n; ++k) strs.push_back(f.str());
+            visit(key, (int)t, (int)et, n, nullptr, &strs);
+        } else {
+            const size_t es = scalar_size(et);
+            require(es > 0 && n < (1ull << 28), "GGUF: bad KV value type in " + key);
+            raw.resize((size_t)(n * es));
+            if (!raw.empty()) f.read(raw.data(), raw.size());
+            visit(key, (int)t, (int)et, n, raw.data(), nullptr);
+        }
+    }
+}
+
 void load_mel_gguf(const std::string& path, MelConfig& c, std::vector<float>& window, std::vector<float>& fb) {
     File f(path);
     Header h = read_header(f, path);

@@ -897,9 +897,10 @@ void Model::stage_valid(const std::vector<int>* v[4], hipStream_t s) {
     PKX_HIP(hipEventRecord(w.staged, s));
 }
 
-void Model::ensure_pe(int T, hipStream_t s) {
+void Model::ensure_pe(int T, hipStream_t s, const float* given) {
     mark(KF_POS_ENC, true);
-    launch_rel_pos_encoding(prec_, ws_->pe.p, T, cfg_.d_model, s);
+    if (given) launch_cast_f32(prec_, given, ws_->pe.p, (int64_t)(2 * T - 1) * cfg_.d_model, s);
+    else launch_rel_pos_encoding(prec_, ws_->pe.p, T, cfg_.d_model, s);
     mark(KF_POS_ENC, false);
 }
 
@@ -1108,7 +1109,7 @@ int Model::encoder_forward(const float* mel, int B, int T_max, const int* valid_
     return T3;
 }
 
-void Model::conformer_layer_forward(int layer, const float* x, int B, int T, const int* valid,
+void Model::conformer_layer_forward(int layer, const float* x, int B, int T, const int* valid, const float* pos,
                                     float* out, float* conv_out, hipStream_t s) {
     require(finalized_, "model not finalized");
     require(layer >= 0 && layer < cfg_.n_layers, "layer index out of range");
@@ -1123,7 +1124,7 @@ void Model::conformer_layer_forward(int layer, const float* x, int B, int T, con
         const std::vector<int>* slots[4] = {&v, &v, &v, &v};
         stage_valid(slots, s);
     }
-    ensure_pe(T, s);
+    ensure_pe(T, s, pos);
     const size_t MD = (size_t)B * T * cfg_.d_model;
     if (out != x) PKX_HIP(hipMemcpyAsync(out, x, MD * 4, hipMemcpyDeviceToDevice, s));
     conv_capture_ = conv_out;
@@ -1136,7 +1137,7 @@ void Model::conformer_layer_forward(int layer, const float* x, int B, int T, con
     conv_capture_ = nullptr;
 }
 
-void Model::relpos_attention_forward(int layer, const float* x, int B, int T, const int* valid,
+void Model::relpos_attention_forward(int layer, const float* x, int B, int T, const int* valid, const float* pos,
                                      float* out, hipStream_t s) {
     require(!cfg_.conv_ln && !cfg_.conv_causal && !cfg_.att_limited,
             "offline forward of a cache-aware streaming model (layer_norm / causal conv / chunked-limited "
@@ -1153,7 +1154,7 @@ void Model::relpos_attention_forward(int layer, const float* x, int B, int T, co
         const std::vector<int>* slots[4] = {&v, &v, &v, &v};
         stage_valid(slots, s);
     }
-    ensure_pe(T, s);
+    ensure_pe(T, s, pos);
     const ModelConfig& c = cfg_;
     const LayerDev& L = layers_[layer];
     const int D = c.d_model, H = c.n_heads, dk = D / H;

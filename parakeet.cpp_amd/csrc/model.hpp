@@ -8,6 +8,7 @@
 // is folded once at upload instead of per call (conformer.cpp:134-154), and a
 // grow-only workspace holds every activation of a forward.
 #pragma once
+#include <functional>
 #include <map>
 #include <memory>
 #include <string>
@@ -160,9 +161,11 @@ public:
     int subsampling_forward(const float* mel, int B, int T_max, const int* valid_T,
                             bool stage_masks, float* out, int* valid_out, hipStream_t s,
                             bool apply_xscaling = false, bool whole_frames = false);
-    void conformer_layer_forward(int layer, const float* x, int B, int T, const int* valid,
+    // pos: the caller's positional table [2T-1][D] f32 (device), or null for
+    // rel_pos_encoding(T, D) computed here
+    void conformer_layer_forward(int layer, const float* x, int B, int T, const int* valid, const float* pos,
                                  float* out, float* conv_out, hipStream_t s);
-    void relpos_attention_forward(int layer, const float* x, int B, int T, const int* valid,
+    void relpos_attention_forward(int layer, const float* x, int B, int T, const int* valid, const float* pos,
                                   float* out, hipStream_t s);
     void conv_module_forward(int layer, const float* c, int B, int T, const int* valid, float* out,
                              hipStream_t s);
@@ -220,7 +223,9 @@ private:
                            void* Y, int64_t ldy);
     void layer_body(int l, float* x, int B, int T, const int* d_valid, bool first_ln_done,
                     bool fuse_next_ln, bool pos_all, hipStream_t s);
-    void ensure_pe(int T, hipStream_t s);
+    // positional table of T' frames in ws_->pe (act dtype): computed, or the
+    // caller's f32 table cast
+    void ensure_pe(int T, hipStream_t s, const float* given = nullptr);
     void stage_valid(const std::vector<int>* v[4], hipStream_t s);
     void mark(int fam, bool begin);
     void* cast_to_act(const float* x, int64_t n, hipStream_t s);
@@ -264,6 +269,14 @@ void linear_raw(Precision prec, const HostTensor& t, int N, int K, const float* 
 
 // GGUF v3 reader: fills a Model with the encoder (+ head) tensors and config.
 std::unique_ptr<Model> load_gguf(const std::string& path, int precision);
+
+// Every KV pair of a GGUF header in file order: type (GGUF numbering), element
+// type (arrays; = type for scalars), element count, and either the packed raw
+// values (numbers, bools) or the strings.
+typedef std::function<void(const std::string& key, int type, int elem_type, uint64_t n, const void* raw,
+                           const std::vector<std::string>* strs)>
+    KvVisitor;
+void read_gguf_kv(const std::string& path, const KvVisitor& visit);
 
 // subsampling.cpp:25-46 arithmetic (all_paddings 2; 3 when causal)
 int subsampled_len(int T, bool causal = false);

@@ -9,6 +9,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <stdexcept>
 
@@ -24,25 +25,143 @@ void need(bool ok, const std::string& msg) {
     if (!ok) throw std::invalid_argument(msg);
 }
 
-// The positional table the device regenerates (src/pos_enc.cpp:10-34):
-// row p is position T-1-p; columns 2i/2i+1 hold sin/cos of pos * 10000^(-2i/d),
-// evaluated in double and stored as f32.  Spot-checks rows 0, T-1 and 2T-2 of
-// a caller's table so a different table is refused rather than ignored.
+// The caller's positional table is used as given (uploaded with the input),
+// as the reference's graph takes pos_emb as a leaf (src/conformer.cpp:359-424):
+// only its shape is checked, [pos_len = 2T-1][d_model].
 void check_pos_emb(const std::vector<float>& pe, int T, int pos_len, int d) {
     need(T >= 1 && pos_len == 2 * T - 1, "pos_emb: pos_len must be 2T-1");
     need(pe.size() == (size_t)pos_len * d, "pos_emb: size must be pos_len * d_model");
-    const double neg_log = -std::log(10000.0) / d;
-    for (int p : {0, T - 1, 2 * T - 2}) {
-        const double pos = (double)(T - 1 - p);
-        for (int i = 0; i < d / 2; ++i) {
-            const double ang = pos * std::exp((double)(2 * i) * neg_log);
-            const float s = (float)std::sin(ang), c = (float)std::cos(ang);
-            const float gs = pe[(size_t)p * d + 2 * i], gc = pe[(size_t)p * d + 2 * i + 1];
-            need(std::fabs(gs - s) <= 1e-5f + 1e-5f * std::fabs(s) && std::fabs(gc - c) <= 1e-5f + 1e-5f * std::fabs(c),
-                 "pos_emb: table differs from rel_pos_encoding(T, d_model); the device path "
-                 "only supports the standard table");
-        }
+}
+
+// One GGUF KV value as read through pkx_gguf_read_kv.
+struct Kv {
+    int type = 0, elem = 0;
+    std::vector<uint8_t> raw;            // packed little-endian numbers / bools
+    std::vector<std::string> strs;       // strings
+    uint64_t n = 0;
+};
+
+void collect_kv(void* user, const char* key, int type, int elem, uint64_t n, const void* data) {
+    auto& kv = *static_cast<std::map<std::string, Kv>*>(user);
+    Kv v;
+    v.type = type;
+    v.elem = elem;
+    v.n = n;
+    if (elem == 8) {   // GGUF string
+        const pkx_gguf_str* s = static_cast<const pkx_gguf_str*>(data);
+        for (uint64_t i = 0; i < n; ++i) v.strs.emplace_back(s[i].s, s[i].n);
+    } else {
+        const size_t es = elem == 0 || elem == 1 || elem == 7 ? 1 : elem == 2 || elem == 3 ? 2
+                        : elem == 10 || elem == 11 || elem == 12 ? 8 : 4;
+        v.raw.assign(static_cast<const uint8_t*>(data), static_cast<const uint8_t*>(data) + n * es);
     }
+    kv[key] = std::move(v);
+}
+
+int64_t kv_int_at(const Kv& v, uint64_t i) {
+    const uint8_t* p = v.raw.data();
+    switch (v.elem) {
+    case 0: case 7: return p[i];
+    case 1: return (int8_t)p[i];
+    case 2: { uint16_t x; std::memcpy(&x, p + 2 * i, 2); return x; }
+    case 3: { int16_t x; std::memcpy(&x, p + 2 * i, 2); return x; }
+    case 4: { uint32_t x; std::memcpy(&x, p + 4 * i, 4); return x; }
+    case 5: { int32_t x; std::memcpy(&x, p + 4 * i, 4); return x; }
+    case 10: { uint64_t x; std::memcpy(&x, p + 8 * i, 8); return (int64_t)x; }
+    case 11: { int64_t x; std::memcpy(&x, p + 8 * i, 8); return x; }
+    default: return 0;
+    }
+}
+
+// ParakeetConfig from the GGUF header: the keys and defaults of
+// pk::ModelLoader::load (src/model_loader.cpp:99-156).
+bool read_config(const std::string& path, ParakeetConfig& c) {
+    std::map<std::string, Kv> kv;
+    if (pkx_gguf_read_kv(path.c_str(), collect_kv, &kv) != 0) return false;
+    auto find = [&](const char* k) -> const Kv* {
+        auto it = kv.find(k);
+        return it == kv.end() || it->second.n == 0 ? nullptr : &it->second;
+    };
+    auto u32 = [&](const char* k, uint32_t d = 0) -> uint32_t {
+        const Kv* v = find(k);
+        return v && v->elem != 8 && v->elem != 6 ? (uint32_t)kv_int_at(*v, 0) : d;
+    };
+    auto i32 = [&](const char* k, int32_t d = 0) -> int32_t {
+        const Kv* v = find(k);
+        return v && v->elem != 8 && v->elem != 6 ? (int32_t)kv_int_at(*v, 0) : d;
+    };
+    auto f32 = [&](const char* k, float d = 0.0f) -> float {
+        const Kv* v = find(k);
+        if (!v || v->elem != 6) return d;
+        float x;
+        std::memcpy(&x, v->raw.data(), 4);
+        return x;
+    };
+    auto bln = [&](const char* k, bool d = false) -> bool {
+        const Kv* v = find(k);
+        return v && v->elem == 7 ? v->raw[0] != 0 : d;
+    };
+    auto str = [&](const char* k, const char* d = "") -> std::string {
+        const Kv* v = find(k);
+        return v && v->type == 8 ? v->strs[0] : std::string(d);
+    };
+    auto i32_arr = [&](const char* k) -> std::vector<int32_t> {
+        std::vector<int32_t> out;
+        auto it = kv.find(k);
+        if (it != kv.end() && it->second.type == 9 && it->second.elem == 5)
+            for (uint64_t i = 0; i < it->second.n; ++i) out.push_back((int32_t)kv_int_at(it->second, i));
+        return out;
+    };
+    c.arch = str("parakeet.arch");
+    c.feat_in = u32("parakeet.encoder.feat_in");
+    c.d_model = u32("parakeet.encoder.d_model");
+    c.n_layers = u32("parakeet.encoder.n_layers");
+    c.n_heads = u32("parakeet.encoder.n_heads");
+    c.ff_dim = u32("parakeet.encoder.ff_dim");
+    c.conv_kernel = u32("parakeet.encoder.conv_kernel");
+    c.conv_norm_type = str("parakeet.encoder.conv_norm_type", "batch_norm");
+    c.subsampling_factor = u32("parakeet.encoder.subsampling_factor");
+    c.subsampling_conv_channels = u32("parakeet.encoder.subsampling_conv_channels");
+    c.xscaling = bln("parakeet.encoder.xscaling", true);
+    c.pos_emb_max_len = u32("parakeet.encoder.pos_emb_max_len", 5000);
+    c.att_context_left = i32("parakeet.encoder.att_context_left", -1);
+    c.att_context_right = i32("parakeet.encoder.att_context_right", -1);
+    c.att_context_style = str("parakeet.encoder.att_context_style", "regular");
+    c.causal_downsampling = bln("parakeet.encoder.causal_downsampling", false);
+    c.conv_causal = bln("parakeet.encoder.conv_causal", false);
+    c.streaming = StreamingCfg();
+    if (c.att_context_style != "regular") {
+        StreamingCfg& s = c.streaming;
+        s.chunk_size = i32_arr("parakeet.streaming.chunk_size");
+        s.shift_size = i32_arr("parakeet.streaming.shift_size");
+        s.pre_encode_cache_size = i32_arr("parakeet.streaming.pre_encode_cache_size");
+        s.cache_drop_size = i32("parakeet.streaming.cache_drop_size", 0);
+        s.last_channel_cache_size = i32("parakeet.streaming.last_channel_cache_size", 0);
+        s.valid_out_len = i32("parakeet.streaming.valid_out_len", 0);
+        s.drop_extra_pre_encoded = i32("parakeet.streaming.drop_extra_pre_encoded", 0);
+        s.present = true;
+    }
+    c.sample_rate = u32("parakeet.preprocessor.sample_rate", 16000);
+    c.n_mels = u32("parakeet.preprocessor.n_mels");
+    c.n_fft = u32("parakeet.preprocessor.n_fft");
+    c.win_length = u32("parakeet.preprocessor.win_length");
+    c.hop_length = u32("parakeet.preprocessor.hop_length");
+    c.preemph = f32("parakeet.preprocessor.preemph", 0.0f);
+    c.mag_power = f32("parakeet.preprocessor.mag_power", 2.0f);
+    c.normalize = str("parakeet.preprocessor.normalize", "per_feature");
+    c.log_zero_guard = f32("parakeet.preprocessor.log_zero_guard", 0.0f);
+    c.pred_hidden = u32("parakeet.decoder.pred_hidden");
+    c.pred_rnn_layers = u32("parakeet.decoder.pred_rnn_layers");
+    c.joint_hidden = u32("parakeet.joint.joint_hidden");
+    c.joint_activation = str("parakeet.joint.activation");
+    c.max_symbols = u32("parakeet.decoding.max_symbols", 10);
+    c.vocab_size = u32("parakeet.vocab_size");
+    c.blank_id = u32("parakeet.blank_id");
+    c.tdt_durations = i32_arr("parakeet.tdt.durations");
+    auto tp = kv.find("parakeet.tokenizer.pieces");
+    c.tokenizer_pieces.clear();
+    if (tp != kv.end() && tp->second.type == 9 && tp->second.elem == 8) c.tokenizer_pieces = tp->second.strs;
+    return true;
 }
 
 }  // namespace
@@ -54,7 +173,7 @@ struct ModelLoader::Device {
     };
     void* stream = nullptr;
     std::mutex mu;
-    Buf in, out, aux, cap, meta;
+    Buf in, out, aux, cap, meta, pos;
 
     void* get(Buf& b, size_t bytes) {
         if (bytes == 0) bytes = 1;
@@ -71,7 +190,7 @@ struct ModelLoader::Device {
     void d2h(void* dst, const void* src, size_t bytes) { chk(pkx_memcpy_d2h(dst, src, bytes, stream), "d2h"); }
     void sync() { chk(pkx_stream_synchronize(stream), "synchronize"); }
     ~Device() {
-        for (Buf* b : {&in, &out, &aux, &cap, &meta})
+        for (Buf* b : {&in, &out, &aux, &cap, &meta, &pos})
             if (b->p) pkx_free(b->p);
         if (stream) pkx_stream_destroy(stream);
     }
@@ -109,32 +228,14 @@ bool ModelLoader::load(const std::string& path, int precision) {
         pkx_model_free(m);
         return false;
     }
-    cfg_.feat_in = c.n_mels;
-    cfg_.d_model = c.d_model;
-    cfg_.n_layers = c.n_layers;
-    cfg_.n_heads = c.n_heads;
-    cfg_.ff_dim = c.ff_dim;
-    cfg_.conv_kernel = c.conv_kernel;
-    cfg_.subsampling_conv_channels = c.sub_channels;
-    cfg_.xscaling = c.xscaling != 0;
-    cfg_.vocab_size = c.vocab_size;
-    cfg_.n_durations = c.n_durations;
-    cfg_.conv_norm_type = c.conv_ln ? "layer_norm" : "batch_norm";
-    cfg_.att_context_left = c.att_left;
-    cfg_.att_context_right = c.att_right;
-    cfg_.att_context_style = c.att_limited ? "chunked_limited" : "regular";
-    cfg_.causal_downsampling = c.causal_sub != 0;
-    cfg_.conv_causal = c.conv_causal != 0;
-    cfg_.streaming = StreamingCfg();
-    if (c.att_limited) {
-        cfg_.streaming.present = true;
-        cfg_.streaming.chunk_size = {c.stream_chunk_first, c.stream_chunk};
-        cfg_.streaming.shift_size = {c.stream_chunk_first, c.stream_chunk};
-        cfg_.streaming.pre_encode_cache_size = {0, c.stream_pre_cache};
-        cfg_.streaming.last_channel_cache_size = c.stream_cache_len;
-        cfg_.streaming.valid_out_len = c.stream_valid_out_len;
-        cfg_.streaming.drop_extra_pre_encoded = c.stream_drop_extra;
+    ParakeetConfig pc;
+    if (!read_config(path, pc)) {
+        err_ = std::string("gguf KV read failed: ") + path + ": " + pkx_last_error();
+        std::fprintf(stderr, "[pk] %s\n", err_.c_str());
+        pkx_model_free(m);
+        return false;
     }
+    cfg_ = std::move(pc);
     precision_ = prec;
     model_ = m;
     dev_ = std::move(dev);
@@ -169,7 +270,7 @@ void Encoder::forward(const std::vector<float>& mel, int n_mels, int T, std::vec
 void Encoder::forward_capture(const std::vector<float>& mel, int n_mels, int T, std::vector<float>& enc_out,
                               int& d_model, int& Tout, const std::vector<int>& capture_layers,
                               std::vector<std::vector<float>>& layer_outs) const {
-    need(n_mels == ml_.config().feat_in, "Encoder::forward: n_mels does not match the model");
+    need(n_mels == (int)ml_.config().feat_in, "Encoder::forward: n_mels does not match the model");
     need(T >= 1 && mel.size() == (size_t)n_mels * T, "Encoder::forward: mel must be [n_mels][T]");
     for (int l : capture_layers) need(l >= 0 && l < n_layers_, "Encoder::forward_capture: layer out of range");
     ModelLoader::Device& d = dev_of(ml_);
@@ -207,7 +308,7 @@ void Encoder::forward_batch(const MelBatch& mels, std::vector<std::vector<float>
                             int& Tout, std::vector<int>& valid_Tout) const {
     const int B = mels.B, F = mels.n_mels, T = mels.T_max, D = d_model_;
     need(B >= 1 && T >= 1, "Encoder::forward_batch: empty batch");
-    need(F == ml_.config().feat_in, "Encoder::forward_batch: n_mels does not match the model");
+    need(F == (int)ml_.config().feat_in, "Encoder::forward_batch: n_mels does not match the model");
     need(mels.data.size() == (size_t)B * F * T, "Encoder::forward_batch: data must be [B][n_mels][T_max]");
     need(mels.valid_T.size() == (size_t)B, "Encoder::forward_batch: valid_T must have B entries");
     ModelLoader::Device& d = dev_of(ml_);
@@ -269,7 +370,7 @@ void Subsampling::forward(const std::vector<float>& mel, int n_mels, int T, std:
 
 void Subsampling::forward(const std::vector<float>& mel, int n_mels, int T, std::vector<float>& out, int& Tout,
                           int& d_model, int& valid_len, int in_valid_frames) const {
-    need(n_mels == ml_.config().feat_in, "Subsampling::forward: n_mels does not match the model");
+    need(n_mels == (int)ml_.config().feat_in, "Subsampling::forward: n_mels does not match the model");
     need(T >= 1 && mel.size() == (size_t)n_mels * T, "Subsampling::forward: mel must be [n_mels][T]");
     need(in_valid_frames <= T - 1,
          "Subsampling::forward: in_valid_frames > T-1 is a streaming window (not in this offline build)");
@@ -295,7 +396,7 @@ void Subsampling::forward(const std::vector<float>& mel, int n_mels, int T, std:
 void Subsampling::forward_batch(const float* mel, int n_mels, int T, int B, const std::vector<int>& valid_in,
                                 std::vector<float>& out, int& Tp, std::vector<int>& valid_out) const {
     need(mel != nullptr && B >= 1 && T >= 1, "Subsampling::forward_batch: empty batch");
-    need(n_mels == ml_.config().feat_in, "Subsampling::forward_batch: n_mels does not match the model");
+    need(n_mels == (int)ml_.config().feat_in, "Subsampling::forward_batch: n_mels does not match the model");
     need(valid_in.size() == (size_t)B, "Subsampling::forward_batch: valid_in must have B entries");
     std::vector<int> vT(B);
     for (int b = 0; b < B; ++b) {
@@ -331,7 +432,8 @@ namespace {
 enum class Unit { Layer, Attention, Conv };
 
 void run_unit(const ModelLoader& ml, Unit u, int layer, const std::vector<float>& x, int T, int B,
-              const std::vector<int>& valid, std::vector<float>& out, std::vector<float>* conv_out) {
+              const std::vector<int>& valid, std::vector<float>& out, std::vector<float>* conv_out,
+              const std::vector<float>* pos_emb = nullptr) {
     const int D = ml.config().d_model;
     need(T >= 1 && B >= 1 && x.size() == (size_t)B * T * D, "input must be [B][T][d_model]");
     need(valid.size() == (size_t)B, "valid_len must have B entries");
@@ -342,14 +444,16 @@ void run_unit(const ModelLoader& ml, Unit u, int layer, const std::vector<float>
     float* dx = (float*)d.get(d.in, n * 4);
     float* dy = (float*)d.get(d.out, n * 4);
     float* dc = conv_out ? (float*)d.get(d.aux, n * 4) : nullptr;
+    float* dpe = pos_emb ? (float*)d.get(d.pos, pos_emb->size() * 4) : nullptr;
     d.h2d(dx, x.data(), n * 4);
+    if (pos_emb) d.h2d(dpe, pos_emb->data(), pos_emb->size() * 4);
     switch (u) {
     case Unit::Layer:
-        chk(pkx_conformer_layer_forward(ml.handle(), layer, dx, B, T, valid.data(), dy, dc, d.stream),
+        chk(pkx_conformer_layer_forward(ml.handle(), layer, dx, B, T, valid.data(), dpe, dy, dc, d.stream),
             "pkx_conformer_layer_forward");
         break;
     case Unit::Attention:
-        chk(pkx_relpos_attention_forward(ml.handle(), layer, dx, B, T, valid.data(), dy, d.stream),
+        chk(pkx_relpos_attention_forward(ml.handle(), layer, dx, B, T, valid.data(), dpe, dy, d.stream),
             "pkx_relpos_attention_forward");
         break;
     case Unit::Conv:
@@ -371,20 +475,20 @@ void run_unit(const ModelLoader& ml, Unit u, int layer, const std::vector<float>
 ConformerLayer::ConformerLayer(const ModelLoader& ml, int layer_idx)
     : ml_(ml), layer_idx_(layer_idx), d_model_(ml.config().d_model) {
     need(ml.handle() != nullptr, "ConformerLayer: model not loaded");
-    need(layer_idx >= 0 && layer_idx < ml.config().n_layers, "ConformerLayer: layer index out of range");
+    need(layer_idx >= 0 && layer_idx < (int)ml.config().n_layers, "ConformerLayer: layer index out of range");
 }
 
 void ConformerLayer::forward(const std::vector<float>& x, int T, const std::vector<float>& pos_emb, int pos_len,
                              int valid_len, std::vector<float>& out) const {
     check_pos_emb(pos_emb, T, pos_len, d_model_);
-    run_unit(ml_, Unit::Layer, layer_idx_, x, T, 1, {valid_len}, out, nullptr);
+    run_unit(ml_, Unit::Layer, layer_idx_, x, T, 1, {valid_len}, out, nullptr, &pos_emb);
 }
 
 void ConformerLayer::forward_with_conv(const std::vector<float>& x, int T, const std::vector<float>& pos_emb,
                                        int pos_len, int valid_len, std::vector<float>& out,
                                        std::vector<float>& conv_out) const {
     check_pos_emb(pos_emb, T, pos_len, d_model_);
-    run_unit(ml_, Unit::Layer, layer_idx_, x, T, 1, {valid_len}, out, &conv_out);
+    run_unit(ml_, Unit::Layer, layer_idx_, x, T, 1, {valid_len}, out, &conv_out, &pos_emb);
 }
 
 void ConformerLayer::conv_module_forward(const std::vector<float>& conv_in, int T, int valid_len,
@@ -395,25 +499,25 @@ void ConformerLayer::conv_module_forward(const std::vector<float>& conv_in, int 
 void ConformerLayer::forward_batch(const std::vector<float>& x, int T, int B, const std::vector<float>& pos_emb,
                                    int pos_len, const std::vector<int>& valid_len, std::vector<float>& out) const {
     check_pos_emb(pos_emb, T, pos_len, d_model_);
-    run_unit(ml_, Unit::Layer, layer_idx_, x, T, B, valid_len, out, nullptr);
+    run_unit(ml_, Unit::Layer, layer_idx_, x, T, B, valid_len, out, nullptr, &pos_emb);
 }
 
 RelPosAttention::RelPosAttention(const ModelLoader& ml, int layer_idx)
     : ml_(ml), layer_idx_(layer_idx), d_model_(ml.config().d_model) {
     need(ml.handle() != nullptr, "RelPosAttention: model not loaded");
-    need(layer_idx >= 0 && layer_idx < ml.config().n_layers, "RelPosAttention: layer index out of range");
+    need(layer_idx >= 0 && layer_idx < (int)ml.config().n_layers, "RelPosAttention: layer index out of range");
 }
 
 void RelPosAttention::forward(const std::vector<float>& x, int T, const std::vector<float>& pos_emb, int pos_len,
                               int valid_len, std::vector<float>& out) const {
     check_pos_emb(pos_emb, T, pos_len, d_model_);
-    run_unit(ml_, Unit::Attention, layer_idx_, x, T, 1, {valid_len}, out, nullptr);
+    run_unit(ml_, Unit::Attention, layer_idx_, x, T, 1, {valid_len}, out, nullptr, &pos_emb);
 }
 
 void RelPosAttention::forward_batch(const std::vector<float>& x, int T, int B, const std::vector<float>& pos_emb,
                                     int pos_len, const std::vector<int>& valid_len, std::vector<float>& out) const {
     check_pos_emb(pos_emb, T, pos_len, d_model_);
-    run_unit(ml_, Unit::Attention, layer_idx_, x, T, B, valid_len, out, nullptr);
+    run_unit(ml_, Unit::Attention, layer_idx_, x, T, B, valid_len, out, nullptr, &pos_emb);
 }
 
 // ---------------------------------------------------------------------------
@@ -560,7 +664,7 @@ void transducer_greedy_batch(const ModelLoader& ml, const std::vector<std::vecto
     need(ml.handle() != nullptr, "model not loaded");
     const int N = (int)encs.size();
     need(N >= 1 && (int)T.size() == N, "transducer_greedy_batch: encs / T size mismatch");
-    need(enc_hidden == ml.config().d_model, "transducer_greedy_batch: enc_hidden != d_model");
+    need(enc_hidden == (int)ml.config().d_model, "transducer_greedy_batch: enc_hidden != d_model");
     int T_max = 1;
     for (int n = 0; n < N; ++n) {
         need(T[n] >= 0 && encs[n].size() >= (size_t)T[n] * enc_hidden, "transducer_greedy_batch: enc too short");
@@ -593,6 +697,20 @@ void transducer_greedy_batch(const ModelLoader& ml, const std::vector<std::vecto
                 (*toks)[n].push_back(TokenInfo{id[j], fr[j], cf[j], sp[j]});
             }
     }
+}
+
+PredictionNet::PredictionNet(const ModelLoader& ml) : ml_(ml) {
+    need(ml.handle() != nullptr, "PredictionNet: model not loaded");
+}
+
+Joint::Joint(const ModelLoader& ml) : ml_(ml) { need(ml.handle() != nullptr, "Joint: model not loaded"); }
+
+void transducer_greedy_batch(const PredictionNet& pred, const Joint& joint,
+                             const std::vector<std::vector<float>>& encs, const std::vector<int>& T,
+                             int enc_hidden, const std::vector<int32_t>& durations, int blank_id, int max_symbols,
+                             std::vector<std::vector<int32_t>>& ids, std::vector<std::vector<TokenInfo>>* toks) {
+    need(&pred.loader() == &joint.loader(), "transducer_greedy_batch: pred and joint of different models");
+    transducer_greedy_batch(pred.loader(), encs, T, enc_hidden, durations, blank_id, max_symbols, ids, toks);
 }
 
 }  // namespace pk

@@ -365,7 +365,11 @@ def _kv_items(cfg: Config):
           ("parakeet.joint.joint_hidden", _GT_U32, cfg.joint_hidden),
           ("parakeet.decoder.pred_hidden", _GT_U32, cfg.pred_hidden),
           ("parakeet.decoder.pred_rnn_layers", _GT_U32, cfg.pred_rnn_layers),
-          ("parakeet.tdt.durations", _GT_ARR, (_GT_I32, list(cfg.tdt_durations)))]
+          ("parakeet.joint.activation", _GT_STR, "relu"),
+          ("parakeet.decoding.max_symbols", _GT_U32, 10),
+          ("parakeet.tdt.durations", _GT_ARR, (_GT_I32, list(cfg.tdt_durations))),
+          # SentencePiece pieces: synthetic ones, one per token id (blank excluded)
+          ("parakeet.tokenizer.pieces", _GT_ARR, (_GT_STR, ["<unk>"] + [f"▁t{i}" for i in range(1, cfg.vocab_size)]))]
     if cfg.streaming:       # scripts/convert_parakeet_to_gguf.py:176-222
         st = "parakeet.streaming."
         kv += [(e + "att_context_left", _GT_I32, cfg.att_context_left),

@@ -74,9 +74,9 @@ SIGS = {
     "pkx_compact_channels_first": ([_vp, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp, _vp], C.c_int),
     "pkx_subsampling_forward": ([_vp, _vp, C.c_int, C.c_int, _ip, C.c_int, _vp, _ip, _ip, _vp],
                                 C.c_int),
-    "pkx_conformer_layer_forward": ([_vp, C.c_int, _vp, C.c_int, C.c_int, _ip, _vp, _vp, _vp],
+    "pkx_conformer_layer_forward": ([_vp, C.c_int, _vp, C.c_int, C.c_int, _ip, _vp, _vp, _vp, _vp],
                                     C.c_int),
-    "pkx_relpos_attention_forward": ([_vp, C.c_int, _vp, C.c_int, C.c_int, _ip, _vp, _vp], C.c_int),
+    "pkx_relpos_attention_forward": ([_vp, C.c_int, _vp, C.c_int, C.c_int, _ip, _vp, _vp, _vp], C.c_int),
     "pkx_conv_module_forward": ([_vp, C.c_int, _vp, C.c_int, C.c_int, _ip, _vp, _vp], C.c_int),
     "pkx_ctc_forward": ([_vp, _vp, C.c_int64, _vp, _vp, _vp], C.c_int),
     "pkx_tdt_joint_argmax": ([_vp, _vp, C.c_int64, _vp, _vp, _vp, _vp, _vp], C.c_int),
@@ -350,17 +350,21 @@ class Model:
         return tout.value, vo
 
     def conformer_layer(self, layer, x: DeviceArray, valid, out: DeviceArray,
-                        conv_out: DeviceArray = None, stream=None):
+                        conv_out: DeviceArray = None, stream=None, pos_emb: DeviceArray = None):
+        """pos_emb: the caller's [2T-1][d_model] f32 table, or None for rel_pos_encoding(T, d_model)."""
         B, T, D = x.shape
         v = None if valid is None else np.ascontiguousarray(valid, dtype=np.int32)
-        check(lib().pkx_conformer_layer_forward(self.handle, layer, x.ptr, B, T, _iptr(v), out.ptr,
+        check(lib().pkx_conformer_layer_forward(self.handle, layer, x.ptr, B, T, _iptr(v),
+                                                pos_emb.ptr if pos_emb is not None else None, out.ptr,
                                                 conv_out.ptr if conv_out is not None else None,
                                                 _sh(stream)))
 
-    def relpos_attention(self, layer, x: DeviceArray, valid, out: DeviceArray, stream=None):
+    def relpos_attention(self, layer, x: DeviceArray, valid, out: DeviceArray, stream=None,
+                         pos_emb: DeviceArray = None):
         B, T, D = x.shape
         v = None if valid is None else np.ascontiguousarray(valid, dtype=np.int32)
-        check(lib().pkx_relpos_attention_forward(self.handle, layer, x.ptr, B, T, _iptr(v), out.ptr,
+        check(lib().pkx_relpos_attention_forward(self.handle, layer, x.ptr, B, T, _iptr(v),
+                                                 pos_emb.ptr if pos_emb is not None else None, out.ptr,
                                                  _sh(stream)))
 
     def conv_module(self, layer, c: DeviceArray, valid, out: DeviceArray, stream=None):
@@ -429,9 +433,9 @@ class Streaming:
         if S != self.n_streams or F != self.model.cfg.n_mels or np.dtype(mel.dtype) != np.float32:
             raise PkxError(f"streaming step: mel must be [{self.n_streams}][{self.model.cfg.n_mels}][n], got {mel.shape}")
         tc = self.chunk_len(n)
-        if tc > 0 and (out.shape[0] != S or out.shape[1] < tc or out.shape[2] != self.model.cfg.d_model
-                       or np.dtype(out.dtype) != np.float32):
-            raise PkxError(f"streaming step: out must be f32 [{S}][>={tc}][{self.model.cfg.d_model}], got {out.shape}")
+        # the device writes one packed [S][tc][D] block, so the row count must be tc exactly
+        if tc > 0 and (tuple(out.shape) != (S, tc, self.model.cfg.d_model) or np.dtype(out.dtype) != np.float32):
+            raise PkxError(f"streaming step: out must be f32 [{S}][{tc}][{self.model.cfg.d_model}], got {out.shape}")
         nv = C.c_int()
         check(lib().pkx_streaming_step(self.handle, mel.ptr, int(n), 1 if is_last else 0, out.ptr, C.byref(nv),
                                        _sh(stream)))

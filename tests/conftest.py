@@ -42,3 +42,40 @@ def gpu():
 @pytest.fixture(scope="session")
 def stream(gpu):
     return gpu.Stream()
+
+
+def tie_excluded(ref_logits, rel=1e-6):
+    """Frames whose reference top-2 logits are an exact f32 tie up to rel*|max|:
+    the only frames on the f32 path where the first-max argmax
+    (src/decode_common.hpp:5-9, src/search.cpp:57-61) may legitimately differ."""
+    top2 = np.sort(np.asarray(ref_logits, dtype=np.float64), axis=-1)[..., -2:]
+    return (top2[..., 1] - top2[..., 0]) <= rel * np.maximum(np.abs(top2[..., 1]), 1e-30)
+
+
+def argmax_identical(got_ids, ref_ids, ref_logits, label, rel=1e-6):
+    """Asserts ids are identical on every frame except exact f32 ties; prints the
+    number of excluded frames.  Returns that number."""
+    ex = tie_excluded(ref_logits, rel)
+    got_ids, ref_ids = np.asarray(got_ids), np.asarray(ref_ids)
+    bad = (got_ids != ref_ids) & ~ex
+    print(f"  [{label}] argmax: {int(ex.sum())} of {ex.size} frames excluded as f32 ties, "
+          f"{int((got_ids != ref_ids).sum())} differ", flush=True)
+    assert not bad.any(), (label, np.flatnonzero(bad)[:10])
+    return int(ex.sum())
+
+
+def argmax_within_error(got_ids, ref_ids, ref_logits, got_logits, label, max_frac=0.01):
+    """Reduced-precision (F16 mode) argmax bar: a frame may differ only where the
+    reference's top-2 margin is within twice the measured logit error of that
+    frame, and such frames are at most max_frac of all.  Returns (excusable, differ)."""
+    ref_logits = np.asarray(ref_logits, dtype=np.float64)
+    err = np.abs(np.asarray(got_logits, dtype=np.float64) - ref_logits).max(axis=-1)
+    top2 = np.sort(ref_logits, axis=-1)[..., -2:]
+    excusable = (top2[..., 1] - top2[..., 0]) <= 2.0 * err
+    differ = np.asarray(got_ids) != np.asarray(ref_ids)
+    print(f"  [{label}] argmax: {int(differ.sum())} of {differ.size} frames differ, "
+          f"{int(excusable.sum())} within twice the logit error "
+          f"(max logit error {float(err.max()):.2e})", flush=True)
+    assert not (differ & ~excusable).any(), (label, np.flatnonzero(differ & ~excusable)[:10])
+    assert excusable.mean() <= max_frac, (label, float(excusable.mean()))
+    return int(excusable.sum()), int(differ.sum())

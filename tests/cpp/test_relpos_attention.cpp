@@ -27,11 +27,18 @@ int main() {
     bool ok = pktest::compare(out, ref, "relpos_attention", 2e-2f, 2e-2f);
     ok = pktest::compare_rel_l2(out, ref, "relpos_attention", pktest::bar_for(ml.precision())) && ok;
 
-    // a table other than rel_pos_encoding(T, d) is refused, not silently replaced
-    std::vector<float> bad = pos;
-    bad[1] += 0.5f;
+    // The baseline table is rel_pos_encoding(T, d) perturbed by up to 5e-4 (a
+    // table computed in f32 elsewhere, as NeMo's is): it is used as given, so
+    // the exact table yields a different output.
+    std::vector<float> exact;
+    pk::rel_pos_encoding(T, D, exact);
+    std::vector<float> out_exact;
+    attn.forward(x, T, exact, pos_len, valid_len, out_exact);
+    if (out_exact == out) { std::fprintf(stderr, "caller's pos_emb not used\n"); ok = false; }
+    // a table of the wrong shape is refused
     bool refused = false;
-    try { attn.forward(x, T, bad, pos_len, valid_len, out); } catch (const std::invalid_argument&) { refused = true; }
-    if (!refused) { std::fprintf(stderr, "non-standard pos_emb accepted\n"); ok = false; }
+    std::vector<float> short_tab(pos.begin(), pos.end() - D);
+    try { attn.forward(x, T, short_tab, pos_len, valid_len, out); } catch (const std::invalid_argument&) { refused = true; }
+    if (!refused) { std::fprintf(stderr, "pos_emb of the wrong size accepted\n"); ok = false; }
     return ok ? 0 : 1;
 }

@@ -24,10 +24,13 @@ int main() {
         T[n] = Tb[n];
         encs[n].assign(enc.begin() + (size_t)n * T_max * D, enc.begin() + (size_t)n * T_max * D + (size_t)T[n] * D);
     }
-    const int blank = ml.config().vocab_size;
+    const int blank = (int)ml.config().blank_id;
+    // the reference's call shape: prediction net and joint of the loaded model
+    pk::PredictionNet pred(ml);
+    pk::Joint joint(ml);
     std::vector<std::vector<int32_t>> ids;
     std::vector<std::vector<pk::TokenInfo>> toks;
-    pk::transducer_greedy_batch(ml, encs, T, D, durs, blank, 10, ids, &toks);
+    pk::transducer_greedy_batch(pred, joint, encs, T, D, durs, blank, (int)ml.config().max_symbols, ids, &toks);
     bool ok = true;
     for (int n = 0; n < N; ++n) {
         std::vector<int32_t> ref_ids, ref_fr, ref_sp;

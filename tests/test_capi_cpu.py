@@ -58,7 +58,7 @@ def test_length_arithmetic_matches_oracle():
         print(' '.join(str(L.pkx_valid_out_len(t, -1)) for t in range(1, 3001)))
         print(' '.join(str(L.pkx_valid_out_len(3000, v)) for v in range(0, 3001, 7)))
     """).split("\n")
-    assert out[0] == "2"
+    assert out[0] == "3"
     assert [int(x) for x in out[1].split()] == [oracle.subsampled_len(t) for t in range(1, 3001)]
     assert [int(x) for x in out[2].split()] == [oracle.valid_out_len(t) for t in range(1, 3001)]
     assert [int(x) for x in out[3].split()] == [oracle.valid_out_len(3000, v) for v in range(0, 3001, 7)]
@@ -168,3 +168,58 @@ def test_gguf_loader_rejects_unknown_conv_norm(tmp_path):
         print(L.pkx_model_load_gguf({str(path)!r}.encode(), -1, C.byref(h)), L.pkx_last_error().decode())
     """).strip()
     assert out.startswith("1 ") and "conv_norm_type" in out
+
+
+def test_gguf_kv_reader(tmp_path):
+    """pkx_gguf_read_kv hands every KV pair of a GGUF header to the visitor in
+    file order with the GGUF type codes and raw values (the KV half of
+    gguf_init_from_file that ModelLoader::load reads, src/model_loader.cpp:99-156);
+    host-only, no device call."""
+    if not os.path.exists(LIB):
+        pytest.skip("libpkx.so not built")
+    cfg = pm.Config(d_model=64, n_layers=1, n_heads=2, ff_dim=128, n_mels=16, sub_channels=8, vocab_size=7,
+                    joint_hidden=16, pred_hidden=16)
+    path = str(tmp_path / "kv.gguf")
+    pm.write_gguf(pm.synthesize(cfg, "f32"), path)
+    out = _run(f"""
+        import ctypes as C, pkx
+        L = pkx.lib()
+        class S(C.Structure):
+            _fields_ = [("s", C.c_char_p), ("n", C.c_size_t)]
+        FN = C.CFUNCTYPE(None, C.c_void_p, C.c_char_p, C.c_int, C.c_int, C.c_uint64, C.c_void_p)
+        L.pkx_gguf_read_kv.argtypes = [C.c_char_p, FN, C.c_void_p]
+        seen = []
+        def visit(user, key, t, et, n, data):
+            if et == 8:
+                arr = C.cast(data, C.POINTER(S))
+                val = [arr[i].s[:arr[i].n].decode() for i in range(n)]
+            elif et == 4:
+                val = list(C.cast(data, C.POINTER(C.c_uint32))[:n])
+            elif et == 5:
+                val = list(C.cast(data, C.POINTER(C.c_int32))[:n])
+            elif et == 6:
+                val = list(C.cast(data, C.POINTER(C.c_float))[:n])
+            elif et == 7:
+                val = [bool(b) for b in C.cast(data, C.POINTER(C.c_uint8))[:n]]
+            else:
+                val = None
+            seen.append((key.decode(), t, et, n, val))
+        cb = FN(visit)
+        assert L.pkx_gguf_read_kv({path!r}.encode(), cb, None) == 0
+        for k, t, et, n, v in seen:
+            print(repr((k, t, et, n, v if n < 20 else (v[:3], len(v)))))
+        assert L.pkx_gguf_read_kv(b"/nonexistent.gguf", cb, None) != 0
+        print("ERR", L.pkx_last_error().decode())
+    """)
+    rows = [eval(l) for l in out.splitlines() if l.startswith("(")]
+    kv = {r[0]: r for r in rows}
+    assert [r[0] for r in rows][:2] == ["general.architecture", "parakeet.arch"]
+    assert kv["parakeet.arch"][4] == ["hybrid_tdt_ctc"] and kv["parakeet.arch"][1] == 8
+    assert kv["parakeet.encoder.d_model"][1:] == (4, 4, 1, [64])
+    assert kv["parakeet.encoder.xscaling"][4] == [False]
+    assert kv["parakeet.tdt.durations"][1:] == (9, 5, 5, [0, 1, 2, 3, 4])
+    assert abs(kv["parakeet.preprocessor.preemph"][4][0] - 0.97) < 1e-7
+    assert kv["parakeet.tokenizer.pieces"][1:4] == (9, 8, 7)
+    assert kv["parakeet.tokenizer.pieces"][4] == ["<unk>", "\u2581t1", "\u2581t2", "\u2581t3", "\u2581t4",
+                                                  "\u2581t5", "\u2581t6"]
+    assert "cannot open" in out.splitlines()[-1]

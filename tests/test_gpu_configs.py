@@ -7,22 +7,18 @@
 * 1.1B shape (q8_0, d = 1024, 8 heads, FFN 4096) at batch 8 x 30 s: one
   block at T' = 375, and the long-T stress shape T' = 3750 through the
   relative-position attention alone (batch 1).
-Bars: relative L2 1e-2 over valid frames (F16 path); argmax identical on
-frames whose top-2 logit margin exceeds the f16 rounding scale.
+Bars: relative L2 1e-2 over valid frames (F16 path); the joint (f32 for
+every weight type) fed the same encoder output gives identical argmax ids on
+every frame but exact f32 ties.
 """
 import numpy as np
 import pytest
 
 import oracle
 import pk_model as pm
-from conftest import rel_l2
+from conftest import argmax_identical, rel_l2
 
 pytestmark = pytest.mark.gpu
-
-
-def _margin_ok(logits, am, margin=2e-3):
-    top2 = np.sort(logits, axis=1)[:, -2:]
-    return (top2[:, 1] - top2[:, 0]) > margin * np.maximum(1.0, np.abs(top2[:, 1]))
 
 
 def _cfg06(n_layers, **kw):
@@ -70,11 +66,8 @@ def test_f16_ragged_batch_with_tdt_joint(gpu, stream):
     gm.tdt_joint(de, Mv, dg, dl, dt, dd, stream)
     tok, dur = dt.numpy(stream), dd.numpy(stream)
     n_tok = V - len(cfg.tdt_durations)
-    ok_t = _margin_ok(lg_ref[:, :n_tok], tok_ref)
-    ok_d = _margin_ok(lg_ref[:, n_tok:], dur_ref)
-    assert ok_t.mean() > 0.9
-    assert np.array_equal(tok[ok_t], tok_ref[ok_t])
-    assert np.array_equal(dur[ok_d], dur_ref[ok_d])
+    argmax_identical(tok, tok_ref, lg_ref[:, :n_tok], "c3 joint tokens")
+    argmax_identical(dur, dur_ref, lg_ref[:, n_tok:], "c3 joint durations")
     gm.close()
 
 

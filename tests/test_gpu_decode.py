@@ -88,3 +88,38 @@ def test_greedy_decode_more_items_than_one_pass(gpu, stream):
     print(f"[decode] {total} tokens identical over {B} items", flush=True)
     assert total > 20
     d_enc.free()
+
+
+def test_greedy_decode_production_shape(gpu, stream):
+    """The 0.6B decoder's shape: 2-layer LSTM of 640 (K = 1280 in the gate
+    products, several register slabs per lane), joint 640, 1024 tokens + blank +
+    5 durations (1030 outputs, not a multiple of 4), encoder width 1024, and 17
+    ragged items (more than one LDS pass of 16)."""
+    durations = (0, 1, 2, 3, 4)
+    cfg = pm.Config(d_model=1024, n_layers=1, n_heads=8, ff_dim=256, n_mels=64, sub_channels=16, vocab_size=1024,
+                    joint_hidden=640, pred_hidden=640, pred_rnn_layers=2, tdt_durations=durations)
+    m = pm.add_prediction(pm.synthesize(cfg, "q8_0", heads=True, seed=640), seed=640)
+    for n in ("joint.joint_net.2.weight", "joint.joint_net.2.bias"):
+        t = m.tensors[n]
+        m.tensors[n] = pm.Tensor(t.gtype, t.shape, (t.data * 60.0).astype(np.float32))
+    gm = gpu.Model.from_tensors(m)
+    tr = oracle.Transducer(m)
+    rng = np.random.default_rng(17)
+    T_valid = [125, 125, 3, 0, 64, 125, 99, 1, 125, 17, 80, 125, 42, 125, 7, 110, 125]
+    B, T_max = len(T_valid), 125
+    enc = rng.standard_normal((B, T_max, cfg.d_model)).astype(np.float32)
+    print(f"[decode] production shape B={B} T={T_valid}", flush=True)
+    d_enc = gpu.DeviceArray.from_numpy(enc, stream)
+    got = gm.transducer_greedy(d_enc, T_valid, durations=durations, max_symbols=10, stream=stream)
+    total = 0
+    for b in range(B):
+        ids, fr, cf, sp = tr.greedy(enc[b, :T_valid[b]], durations=durations, max_symbols=10)
+        g_ids, g_fr, g_cf, g_sp = got[b]
+        total += len(ids)
+        assert np.array_equal(g_ids, ids), (b, g_ids[:20], ids[:20])
+        assert np.array_equal(g_fr, fr) and np.array_equal(g_sp, sp)
+        assert np.max(np.abs(g_cf - cf), initial=0.0) <= 1e-5
+    print(f"[decode] {total} tokens identical over {B} items", flush=True)
+    assert total > 100
+    d_enc.free()
+    gm.close()

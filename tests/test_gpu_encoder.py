@@ -1,12 +1,13 @@
 """Encoder-level parity through the C ABI vs the CPU oracle: subsampling
 (batched and scalar masking), the full encoder per layer, and the CTC / TDT
-argmax heads (token ids identical)."""
+argmax heads (token ids identical on every frame but exact f32 ties; the
+heads compute in f32 for every weight type)."""
 import numpy as np
 import pytest
 
 import oracle
 import pk_model as pm
-from conftest import rel_l2
+from conftest import argmax_identical, rel_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -86,12 +87,6 @@ def test_encoder_per_layer(gpu, stream, name, T, valid_T):
     assert rel_l2(got[mask], ref[mask]) < _tol(prec)
 
 
-def _margin_ok(logits, idx):
-    """True where the top-1 beats the runner-up by more than 1e-3 (ties flagged)."""
-    s = np.sort(logits, axis=-1)
-    return (s[..., -1] - s[..., -2]) > 1e-3
-
-
 @pytest.mark.parametrize("name", ["f32", "q8_0"])
 def test_ctc_head(gpu, stream, name):
     m, om, gm, prec = _models(gpu, name)
@@ -106,11 +101,10 @@ def test_ctc_head(gpu, stream, name):
     gm.ctc(de, T, dlp, dam, stream)
     lp, am = dlp.numpy(stream), dam.numpy(stream)
     assert np.abs(lp - lp_ref).max() < 1e-4
-    ok = _margin_ok(lp_ref, am_ref)
-    assert np.array_equal(am[ok], am_ref[ok])
-    assert ok.mean() > 0.9
-    assert np.array_equal(oracle.ctc_greedy(am, m.cfg.vocab_size), oracle.ctc_greedy(am_ref, m.cfg.vocab_size)) \
-        or not ok.all()
+    # the head runs in f32 for every weight type: identical ids but for exact f32 ties
+    n_ex = argmax_identical(am, am_ref, lp_ref, f"ctc {name}")
+    if n_ex == 0:
+        assert np.array_equal(oracle.ctc_greedy(am, m.cfg.vocab_size), oracle.ctc_greedy(am_ref, m.cfg.vocab_size))
 
 
 @pytest.mark.parametrize("name", ["f32", "q8_0", "q4_k"])
@@ -129,10 +123,8 @@ def test_tdt_joint_argmax(gpu, stream, name):
     lg, tok, dur = dl.numpy(stream), dt.numpy(stream), dd.numpy(stream)
     assert rel_l2(lg, lg_ref) < 1e-5
     n_tok = V - len(m.cfg.tdt_durations)
-    ok_t = _margin_ok(lg_ref[:, :n_tok], tok_ref)
-    ok_d = _margin_ok(lg_ref[:, n_tok:], dur_ref)
-    assert np.array_equal(tok[ok_t], tok_ref[ok_t])
-    assert np.array_equal(dur[ok_d], dur_ref[ok_d])
+    argmax_identical(tok, tok_ref, lg_ref[:, :n_tok], f"joint tokens {name}")
+    argmax_identical(dur, dur_ref, lg_ref[:, n_tok:], f"joint durations {name}")
 
 
 def test_profiling_counts_and_sampling(gpu, stream):

@@ -184,6 +184,63 @@ def test_streaming_binding_checks_shapes(gpu, stream):
     short = gpu.DeviceArray((2, 1, cfg.d_model), np.float32)
     with pytest.raises(gpu.PkxError, match="out must be"):
         st.step(two, short, stream=stream)
+    # an output with more rows than the chunk would put the second stream's
+    # frames at the wrong offset (the device writes one packed [S][tc][D] block)
+    long_out = gpu.DeviceArray((2, 5, cfg.d_model), np.float32)
+    with pytest.raises(gpu.PkxError, match="out must be"):
+        st.step(two, long_out, stream=stream)
     assert st.step_num == 0
     assert st.step(two, out, stream=stream) == 2
     st.close()
+
+
+# Schedules and variants beyond the streaming model's own: chunks of 72 mel
+# frames (9 encoder frames per step, more than the compile-time conv kernel's
+# 8, so the generic causal conv and a 9-row attention chunk run), the
+# BatchNorm conv norm, and a depthwise kernel of 5.
+VARIANTS = {
+    "f16_tc9_batchnorm": (dict(d_model=128, n_heads=2, ff_dim=256, conv_norm_type="batch_norm",
+                               stream_chunk_size=(9, 72), stream_shift_size=(9, 72), stream_valid_out_len=9,
+                               att_context_right=8), "f16", 1, 1e-2, 81),
+    "f32_tc9": (dict(d_model=128, n_heads=4, ff_dim=256, stream_chunk_size=(9, 72), stream_shift_size=(9, 72),
+                     stream_valid_out_len=9, att_context_right=8), "f32", 0, 1e-4, 81),
+    "f32_k5": (dict(d_model=128, n_heads=4, ff_dim=256, conv_kernel=5), "f32", 0, 1e-4, 25),
+    "q8_0_k5_batchnorm": (dict(d_model=256, n_heads=4, ff_dim=512, conv_kernel=5, conv_norm_type="batch_norm"),
+                          "q8_0", 1, 1e-2, 25),
+}
+
+
+@pytest.mark.parametrize("name", list(VARIANTS))
+def test_streaming_variants_match_oracle(gpu, stream, name):
+    kw, qt, prec, tol, max_window = VARIANTS[name]
+    cfg = _cfg(kw)
+    m = pm.synthesize(cfg, qt, heads=False, std=0.05, bn_random=True)
+    om = oracle.OracleModel(m)
+    gm = gpu.Model.from_tensors(m, precision=prec)
+    S, T = 2, 200
+    rng = np.random.default_rng(21)
+    mels = rng.normal(0, 1, (S, cfg.n_mels, T)).astype(np.float32)
+    st = gpu.Streaming(gm, n_streams=S, max_window=max_window, stream=stream)
+    refs = [oracle.Stream(om) for _ in range(S)]
+    windows = oracle.stream_windows(T, st.chunk_first, st.chunk, st.pre_cache)
+    tcs = sorted({st.chunk_len(hi - lo) for lo, hi, _ in windows})
+    print(f"[stream] {name}: {S} streams, {len(windows)} chunks, chunk lengths {tcs}", flush=True)
+    worst = 0.0
+    for k, (lo, hi, last) in enumerate(windows):
+        tc = st.chunk_len(hi - lo)
+        d_mel = gpu.DeviceArray.from_numpy(np.ascontiguousarray(mels[:, :, lo:hi]), stream)
+        out = gpu.DeviceArray((S, max(tc, 1), cfg.d_model), np.float32)
+        nv = st.step(d_mel, out, is_last=last, stream=stream)
+        got = out.numpy(stream)
+        for s in range(S):
+            ref = refs[s].step(mels[s, :, lo:hi], is_last=last)
+            assert nv == ref.shape[0], (k, nv, ref.shape)
+            if nv:
+                err = rel_l2(got[s, :nv], ref)
+                worst = max(worst, err)
+                assert err < tol, (name, k, s, err)
+    print(f"[stream]   worst chunk rel_l2 {worst:.2e}", flush=True)
+    if "tc9" in name:
+        assert max(tcs) > 8
+    st.close()
+    gm.close()
