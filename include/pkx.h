@@ -196,6 +196,22 @@ int pkx_ctc_forward(pkx_model* m, const float* enc_dev, int64_t M, float* logpro
 int pkx_tdt_joint_argmax(pkx_model* m, const float* enc_dev, int64_t M, const float* g_dev,
                          float* logits_dev, int32_t* tok_dev, int32_t* dur_dev, void* stream);
 
+/* No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops or harnesses that forbid
+ * hipMalloc).  pkx_tdt_joint_argmax with the same kernels and results, its
+ * scratch (the prediction projection [joint_hidden] and the joint hidden
+ * activations [M][joint_hidden], f32) held in a fixed per-GPU device array of
+ * PKX_JOINT_NOALLOC_MAX_FLOATS floats (16 MiB, kept until the process ends)
+ * instead of the model's grow-only workspace.  Calls no hipMalloc / hipFree.
+ * Fails (nonzero, message in pkx_last_error) when
+ * M > (PKX_JOINT_NOALLOC_MAX_FLOATS - joint_hidden rounded up to 64) /
+ * joint_hidden, i.e. 6552 frames at joint_hidden 640.  Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (any stream, any
+ * model handle) race. */
+#define PKX_JOINT_NOALLOC_MAX_FLOATS (4u << 20)
+int pkx_tdt_joint_argmax_noalloc(pkx_model* m, const float* enc_dev, int64_t M, const float* g_dev,
+                                 float* logits_dev, int32_t* tok_dev, int32_t* dur_dev, void* stream);
+
 /* ---- kernel-level entry points (ggml ops the encoder issues) ---------------- */
 
 /* Dequantise n raw ggml-layout elements (q8_0 / q4_K / f16) to f32, bit-exact

@@ -2,6 +2,7 @@
 // exceptions and reports them through a thread-local last-error string, the
 // same no-throw convention as the reference C API (src/parakeet_capi.cpp:207-225).
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "../../include/pkx.h"
@@ -24,6 +25,12 @@ struct pkx_streaming {
     std::unique_ptr<pkx::StreamState> st;
 };
 
+// Fixed device scratch of pkx_tdt_joint_argmax_noalloc: one copy per GPU,
+// held until the process ends.  Host code never passes the symbol's name as an
+// address (it is a host-side stand-in there); joint_scratch() finds each GPU's
+// copy with hipGetSymbolAddress and that address is used from then on.
+static __device__ __align__(256) float scratch[PKX_JOINT_NOALLOC_MAX_FLOATS];
+
 namespace {
 thread_local std::string g_last_error;
 
@@ -43,6 +50,26 @@ int guarded(F&& f) {
 }
 
 hipStream_t st(void* s) { return (hipStream_t)s; }
+
+constexpr int kMaxDevices = 64;
+
+// Device address of this GPU's copy of `scratch` (below the namespace), looked
+// up with hipGetSymbolAddress once per device with that device current.
+
+float* joint_scratch() {
+    static std::mutex mu;
+    static float* ptr[kMaxDevices] = {};
+    int dev = 0;
+    PKX_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) throw std::invalid_argument("device index out of range");
+    std::lock_guard<std::mutex> lock(mu);
+    if (!ptr[dev]) {
+        void* p = nullptr;
+        PKX_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        ptr[dev] = (float*)p;
+    }
+    return ptr[dev];
+}
 
 void need(bool ok, const char* what) {
     if (!ok) throw std::invalid_argument(what);
@@ -315,6 +342,24 @@ int pkx_tdt_joint_argmax(pkx_model* m, const float* enc, int64_t M, const float*
     return guarded([&] {
         need(m && enc && g && logits && tok && dur, "null argument");
         m->impl->tdt_joint_argmax(enc, M, g, logits, tok, dur, st(s));
+    });
+}
+
+int pkx_tdt_joint_argmax_noalloc(pkx_model* m, const float* enc, int64_t M, const float* g, float* logits,
+                                 int32_t* tok, int32_t* dur, void* s) {
+    return guarded([&] {
+        need(m && enc && g && logits && tok && dur, "null argument");
+        need(m->impl->has_joint(), "model has no TDT joint");
+        const int64_t Hj = m->impl->joint_hidden();
+        need(M >= 1, "joint: no frames");
+        // scratch layout: pp [Hj] at 0, hid [M][Hj] from the next 256-byte boundary
+        const int64_t hid_off = (Hj + 63) / 64 * 64;
+        need(M <= ((int64_t)PKX_JOINT_NOALLOC_MAX_FLOATS - hid_off) / Hj,
+             "pkx_tdt_joint_argmax_noalloc: M frames need more than the fixed scratch array of "
+             "PKX_JOINT_NOALLOC_MAX_FLOATS floats (at most (PKX_JOINT_NOALLOC_MAX_FLOATS - joint_hidden) / "
+             "joint_hidden frames); use pkx_tdt_joint_argmax");
+        float* sc = joint_scratch();
+        m->impl->tdt_joint_argmax_in(enc, M, g, logits, tok, dur, sc, sc + hid_off, st(s));
     });
 }
 

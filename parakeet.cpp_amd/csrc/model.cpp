@@ -1229,12 +1229,21 @@ void Model::tdt_joint_argmax(const float* enc, int64_t M, const float* g, float*
     Ws& w = *ws_;
     grow(w.pp, (size_t)Hj * 4);
     grow(w.logits, (size_t)M * Hj * 4);
-    gemm(heads_.jpred, EPI_STORE_F32, g, heads_.jpred.K, 1, heads_.jpred_b, w.pp.p, Hj, 1.f, nullptr, 1, s,
-         PREC_F32, -1);
-    gemm(heads_.jenc, EPI_RELU2_F32, enc, cfg_.d_model, M, heads_.jenc_b, w.logits.p, Hj, 1.f, nullptr, 1, s,
-         PREC_F32, -1, (const float*)w.pp.p);
-    gemm(heads_.jout, EPI_STORE_F32, w.logits.p, Hj, M, heads_.jout_b, logits, heads_.jout.N, 1.f, nullptr, 1, s,
-         PREC_F32, -1);
+    tdt_joint_argmax_in(enc, M, g, logits, tok, dur, (float*)w.pp.p, (float*)w.logits.p, s);
+}
+
+void Model::tdt_joint_argmax_in(const float* enc, int64_t M, const float* g, float* logits, int32_t* tok,
+                                int32_t* dur, float* pp, float* hid, hipStream_t s) {
+    require(finalized_ && heads_.jout.ok(), "model has no TDT joint");
+    require(M >= 1, "joint: no frames");
+    const int Hj = heads_.jenc.N;
+    // every element of pp and hid read below is written first by these products
+    gemm(heads_.jpred, EPI_STORE_F32, g, heads_.jpred.K, 1, heads_.jpred_b, pp, Hj, 1.f, nullptr, 1, s, PREC_F32,
+         -1);
+    gemm(heads_.jenc, EPI_RELU2_F32, enc, cfg_.d_model, M, heads_.jenc_b, hid, Hj, 1.f, nullptr, 1, s, PREC_F32, -1,
+         pp);
+    gemm(heads_.jout, EPI_STORE_F32, hid, Hj, M, heads_.jout_b, logits, heads_.jout.N, 1.f, nullptr, 1, s, PREC_F32,
+         -1);
     launch_split_argmax(logits, M, heads_.n_tok, heads_.n_dur, tok, dur, s);
 }
 

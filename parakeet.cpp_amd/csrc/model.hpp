@@ -172,6 +172,12 @@ public:
     void ctc_forward(const float* enc, int64_t M, float* logprobs, int32_t* argmax, hipStream_t s);
     void tdt_joint_argmax(const float* enc, int64_t M, const float* g, float* logits, int32_t* tok,
                           int32_t* dur, hipStream_t s);
+    // The same products on caller-provided device scratch (allocates nothing):
+    // pp [joint_hidden] and hid [M][joint_hidden] f32, both fully written before
+    // they are read.
+    void tdt_joint_argmax_in(const float* enc, int64_t M, const float* g, float* logits, int32_t* tok,
+                             int32_t* dur, float* pp, float* hid, hipStream_t s);
+    int joint_hidden() const { return heads_.jout.ok() ? heads_.jenc.N : 0; }
     bool has_decoder() const { return pred_.ok() && heads_.jout.ok(); }
     // transducer_greedy_batch (transducer_batch.cpp:24-213): greedy TDT
     // (n_dur > 0, skip = durations[argmax]) or RNNT decode of B utterances in

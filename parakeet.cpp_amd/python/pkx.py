@@ -80,6 +80,7 @@ SIGS = {
     "pkx_conv_module_forward": ([_vp, C.c_int, _vp, C.c_int, C.c_int, _ip, _vp, _vp], C.c_int),
     "pkx_ctc_forward": ([_vp, _vp, C.c_int64, _vp, _vp, _vp], C.c_int),
     "pkx_tdt_joint_argmax": ([_vp, _vp, C.c_int64, _vp, _vp, _vp, _vp, _vp], C.c_int),
+    "pkx_tdt_joint_argmax_noalloc": ([_vp, _vp, C.c_int64, _vp, _vp, _vp, _vp, _vp], C.c_int),
     "pkx_dequantize": ([C.c_int, _vp, _vp, C.c_int64, _vp], C.c_int),
     "pkx_linear": ([C.c_int, C.c_int, C.c_int, C.c_int, _vp, C.c_size_t, _vp, _vp, C.c_int64, _vp,
                     _vp], C.c_int),
@@ -380,6 +381,12 @@ class Model:
                   dur: DeviceArray, stream=None):
         check(lib().pkx_tdt_joint_argmax(self.handle, enc.ptr, M, g.ptr, logits.ptr, tok.ptr, dur.ptr,
                                          _sh(stream)))
+
+    def tdt_joint_noalloc(self, enc: DeviceArray, M, g: DeviceArray, logits: DeviceArray, tok: DeviceArray,
+                          dur: DeviceArray, stream=None):
+        """pkx_tdt_joint_argmax_noalloc: the same joint on the library's fixed per-GPU scratch."""
+        check(lib().pkx_tdt_joint_argmax_noalloc(self.handle, enc.ptr, M, g.ptr, logits.ptr, tok.ptr, dur.ptr,
+                                                 _sh(stream)))
 
     def set_profiling(self, families=True, stride=1):
         """families: True (all), False/None (off), or an iterable of PROF_FAMILIES names;
