@@ -1198,7 +1198,7 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
     // residual epilogues: the tile's residual values are loaded now (behind the
     // statistics, ahead of the DMAs) and wait in registers for the epilogue
     constexpr int TAB = FOLD && KG == 1 ? C::BM * 8 : 0;
-    constexpr bool whole = 4 * 32 * WTM * (32 * WTN + 4) * 4 + TAB <= NS * C::STAGE;
+    constexpr bool whole = 4 * 32 * WTM * (32 * WTN + 4) * 4 + TAB <= KG * NS * C::STAGE;
     constexpr bool RPRE = (EPI == EPI_RESID || EPI == EPI_RESID_LN) && whole;
     ResidPre<RPRE ? 32 * WTM : 64, RPRE ? 8 * WTN : 1> rpre;
     if constexpr (RPRE) {
@@ -1286,7 +1286,7 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
         // the LDS ring is free once every wave has finished its last slab; tiles
         // whose staging exceeds it leave in row halves
         // (the folded-LayerNorm row table sits above the staging area)
-        static_assert(whole || (WTM % 2 == 0 && 4 * 16 * WTM * (32 * WTN + 4) * 4 + TAB <= NS * C::STAGE),
+        static_assert(whole || (WTM % 2 == 0 && 4 * 16 * WTM * (32 * WTN + 4) * 4 + TAB <= KG * NS * C::STAGE),
                       "epilogue staging exceeds LDS ring");
         if constexpr (whole) {
             __syncthreads();

@@ -85,6 +85,13 @@ struct Model::Ws {
     int* h_valid = nullptr;             // pinned staging
     int Bcap = 0;
     hipEvent_t staged = nullptr;
+    ~Ws() {
+        for (Buf* b : {&a2, &a2p, &a3, &flat, &h, &u, &qkv, &g, &pe, &p, &xin, &tmp, &lnst, &logits, &pp})
+            if (b->p) (void)hipFree(b->p);
+        if (d_valid) (void)hipFree(d_valid);
+        if (h_valid) (void)hipHostFree(h_valid);
+        if (staged) (void)hipEventDestroy(staged);
+    }
 };
 
 static void grow(Buf& b, size_t bytes) {
@@ -112,14 +119,7 @@ Model::Model(const ModelConfig& cfg, int precision) : cfg_(cfg), ws_(new Ws) {
 Model::~Model() {
     auto fr = [](void* p) { if (p) (void)hipFree(p); };
     for (void* p : allocs_) fr(p);
-    if (ws_) {
-        for (Buf* b : {&ws_->a2, &ws_->a2p, &ws_->a3, &ws_->flat, &ws_->h, &ws_->u, &ws_->qkv,
-                       &ws_->g, &ws_->pe, &ws_->p, &ws_->xin, &ws_->tmp, &ws_->logits, &ws_->pp})
-            fr(b->p);
-        fr(ws_->d_valid);
-        if (ws_->h_valid) (void)hipHostFree(ws_->h_valid);
-        if (ws_->staged) (void)hipEventDestroy(ws_->staged);
-    }
+    ws_.reset();
     if (tl_launch_hook && tl_launch_hook == (LaunchHook*)prof_hook_.get()) tl_launch_hook = nullptr;
     for (auto& e : prof_ev_) {
         (void)hipEventDestroy(e.first);
@@ -876,7 +876,7 @@ void Model::ensure_ws(int B, int T_max) {
     grow(w.p, P * D * c.n_layers * as);   // all layers' positional projections
     grow(w.tmp, M * D * 4);
     if (B > w.Bcap) {
-        if (w.d_valid) PKX_HIP(hipFree(w.d_valid));
+            if (w.d_valid) PKX_HIP(hipFree(w.d_valid));
         if (w.h_valid) PKX_HIP(hipHostFree(w.h_valid));
         w.d_valid = nullptr;
         w.h_valid = nullptr;
@@ -916,19 +916,19 @@ void* Model::cast_to_act(const float* x, int64_t n, hipStream_t s) {
 int Model::subsampling_forward(const float* mel, int B, int T_max, const int* valid_T,
                                bool stage_masks, float* out, int* valid_out, hipStream_t s,
                                bool apply_xscaling, bool whole_frames) {
+    const int T3 = stage_lengths(B, T_max, valid_T, valid_out, s, whole_frames);
+    subsampling_kernels(mel, B, T_max, stage_masks, out, s, apply_xscaling);
+    return T3;
+}
+
+// Per-item valid lengths of every subsampling stage (host arithmetic,
+// subsampling.cpp:25-46) staged to the device; returns T'.
+int Model::stage_lengths(int B, int T_max, const int* valid_T, int* valid_out, hipStream_t s, bool whole_frames) {
     require(finalized_, "model not finalized");
     require(B > 0 && T_max > 0, "subsampling: empty batch");
     ensure_ws(B, T_max);
-    const ModelConfig& c = cfg_;
-    const int C = c.sub_channels, F = c.n_mels;
-    // causal (CausalConv2D): pad 2 before / 1 after, and the per-stage input
-    // masks on every path (subsampling.cpp:100-147, :283-300)
-    const bool cz = c.causal_sub != 0;
-    if (cz) stage_masks = true;
+    const bool cz = cfg_.causal_sub != 0;
     const int T1 = sub_stage_len(T_max, cz), T2 = sub_stage_len(T1, cz), T3 = sub_stage_len(T2, cz);
-    const int F1 = sub_stage_len(F, cz), F2 = sub_stage_len(F1, cz), F3 = sub_stage_len(F2, cz);
-    (void)T1;
-    (void)F1;
     std::vector<int> v0(B), v1(B), v2(B), vo(B);
     for (int b = 0; b < B; ++b) {
         const int vt = valid_T ? valid_T[b] : T_max;
@@ -943,6 +943,22 @@ int Model::subsampling_forward(const float* mel, int B, int T_max, const int* va
     }
     const std::vector<int>* slots[4] = {&v0, &v1, &v2, &vo};
     stage_valid(slots, s);
+    return T3;
+}
+
+// The subsampling kernels on lengths staged by stage_lengths.
+void Model::subsampling_kernels(const float* mel, int B, int T_max, bool stage_masks, float* out, hipStream_t s,
+                                bool apply_xscaling) {
+    const ModelConfig& c = cfg_;
+    const int C = c.sub_channels, F = c.n_mels;
+    // causal (CausalConv2D): pad 2 before / 1 after, and the per-stage input
+    // masks on every path (subsampling.cpp:100-147, :283-300)
+    const bool cz = c.causal_sub != 0;
+    if (cz) stage_masks = true;
+    const int T1 = sub_stage_len(T_max, cz), T2 = sub_stage_len(T1, cz), T3 = sub_stage_len(T2, cz);
+    const int F1 = sub_stage_len(F, cz), F2 = sub_stage_len(F1, cz), F3 = sub_stage_len(F2, cz);
+    (void)T1;
+    (void)F1;
     Ws& w = *ws_;
     const int* dv = w.d_valid;
     const int Bc = w.Bcap;
@@ -958,7 +974,6 @@ int Model::subsampling_forward(const float* mel, int B, int T_max, const int* va
     gemm(sub_.out, EPI_STORE_F32, w.flat.p, (int64_t)C * F3, (int64_t)B * T3, sub_.bout, out, c.d_model, xs,
          nullptr, 1, s, prec_, -1);
     mark(KF_SUBSAMPLING, false);
-    return T3;
 }
 
 // ---------------------------------------------------------------------------
@@ -1090,9 +1105,16 @@ void Model::layer_body(int l, float* x, int B, int T, const int* d_valid, bool f
 // ---------------------------------------------------------------------------
 int Model::encoder_forward(const float* mel, int B, int T_max, const int* valid_T, bool stage_masks,
                            float* out, int* valid_out, float* capture, hipStream_t s) {
-    std::vector<int> vo(B);
-    const int T3 = subsampling_forward(mel, B, T_max, valid_T, stage_masks, out, vo.data(), s, true);
-    if (valid_out) std::memcpy(valid_out, vo.data(), sizeof(int) * B);
+    const int T3 = stage_lengths(B, T_max, valid_T, valid_out, s, false);
+    encoder_kernels(mel, B, T_max, T3, stage_masks, out, capture, s);
+    return T3;
+}
+
+// subsampling -> xscaling -> positional table -> blocks, on lengths staged by
+// stage_lengths (encoder.cpp:97-167)
+void Model::encoder_kernels(const float* mel, int B, int T_max, int T3, bool stage_masks, float* out,
+                            float* capture, hipStream_t s) {
+    subsampling_kernels(mel, B, T_max, stage_masks, out, s, true);
     const int* dvalid = ws_->d_valid + 3 * ws_->Bcap;
     ensure_pe(T3, s);
     const int L = cfg_.n_layers;
@@ -1106,7 +1128,6 @@ int Model::encoder_forward(const float* mel, int B, int T_max, const int* valid_
         if (capture)
             PKX_HIP(hipMemcpyAsync(capture + (size_t)l * MD, out, MD * 4, hipMemcpyDeviceToDevice, s));
     }
-    return T3;
 }
 
 void Model::conformer_layer_forward(int layer, const float* x, int B, int T, const int* valid, const float* pos,

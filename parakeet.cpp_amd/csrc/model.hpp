@@ -227,6 +227,11 @@ private:
     // product of a LayerNorm folded in (A = x * gamma from gemm_resid_ln)
     GemmParams fold_params(const DevWeight& w, const void* A, int64_t M, const float* c1, const float* c2,
                            void* Y, int64_t ldy);
+    int stage_lengths(int B, int T_max, const int* valid_T, int* valid_out, hipStream_t s, bool whole_frames);
+    void subsampling_kernels(const float* mel, int B, int T_max, bool stage_masks, float* out, hipStream_t s,
+                             bool apply_xscaling);
+    void encoder_kernels(const float* mel, int B, int T_max, int T3, bool stage_masks, float* out, float* capture,
+                         hipStream_t s);
     void layer_body(int l, float* x, int B, int T, const int* d_valid, bool first_ln_done,
                     bool fuse_next_ln, bool pos_all, hipStream_t s);
     // positional table of T' frames in ws_->pe (act dtype): computed, or the
