@@ -186,16 +186,22 @@ __global__ __launch_bounds__(64 * NW, 1) void relpos_attn_f16_kernel(AttnParams 
                 const float bd = sm.g[w][ii * S::LDG + 15 - ii + jj];   // bd[i][T-1-i+j]
                 float sv = (sac[jt][r] + bd) * scale;
                 if (j0 + jj >= vl) sv = -INFINITY;
+                if (a.chunk > 0) {
+                    const int dc = (i0w + ii) / a.chunk - (j0 + jj) / a.chunk;
+                    if (dc < 0 || dc > a.left_chunks) sv = -INFINITY;
+                }
                 s[jt][r] = sv;
                 tmax[r] = fmaxf(tmax[r], sv);
             }
 #pragma unroll
         for (int r = 0; r < 4; ++r) tmax[r] = row16_max(tmax[r]);   // over the tile's 64 keys
         float corr[4], tsum[4];
+        float msub[4];   // the running max, 0 while every key so far is masked (no -inf - -inf)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const float mnew = fmaxf(mrow[r], tmax[r]);
-            corr[r] = __expf(mrow[r] - mnew);   // exp(-inf) = 0 on the first tile
+            msub[r] = mnew == -INFINITY ? 0.f : mnew;
+            corr[r] = __expf(mrow[r] - msub[r]);   // exp(-inf) = 0 on the first tile
             mrow[r] = mnew;
             tsum[r] = 0.f;
         }
@@ -203,7 +209,7 @@ __global__ __launch_bounds__(64 * NW, 1) void relpos_attn_f16_kernel(AttnParams 
         for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float e = __expf(s[jt][r] - mrow[r]);
+                const float e = __expf(s[jt][r] - msub[r]);
                 tsum[r] += e;
                 sm.prob[w][(lr + r) * S::LDP + 16 * jt + lc] = (f16)e;
             }
@@ -284,7 +290,11 @@ __global__ __launch_bounds__(64) void relpos_attn_f32_kernel(AttnParams a, int d
             ac += qu[c] * kr[c];
             bd += qv[c] * pr[c];
         }
-        const float s = (ac + bd) * a.scale;
+        float s = (ac + bd) * a.scale;
+        if (a.chunk > 0) {
+            const int dc = i / a.chunk - j / a.chunk;
+            if (dc < 0 || dc > a.left_chunks) s = -INFINITY;   // key i itself is always seen
+        }
         sc[j] = s;
         mx = fmaxf(mx, s);
     }

@@ -15,6 +15,9 @@ struct AttnParams {
     void* out = nullptr;      int64_t ldo = 0;   // ctx [B*T][.]
     int B = 0, T = 0, H = 0, dk = 0;
     float scale = 1.0f;
+    // chunked-limited window (relpos_attention.cpp:252-275), 0 = off: query i
+    // sees key j only if 0 <= i / chunk - j / chunk <= left_chunks
+    int chunk = 0, left_chunks = 0;
 };
 
 void launch_relpos_attention(Precision prec, const AttnParams& a, hipStream_t s);

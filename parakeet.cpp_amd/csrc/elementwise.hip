@@ -56,7 +56,8 @@ template <> __device__ __forceinline__ void store4<f16>(f16* p, const float4v& v
     *(half4v*)p = h;
 }
 
-// MODE 0: y = LN(x); MODE 1: y_f32 = LN(x), y = LN2(y_f32); MODE 2: y_f32 = LN(x).
+// MODE 0: y = LN(x); MODE 1: y_f32 = LN(x), y = LN2(y_f32); MODE 2: y_f32 = LN(x);
+// MODE 3: y = silu(LN(x)).
 template <int NV, typename OutT, int MODE>
 __global__ __launch_bounds__(256) void layernorm_kernel(LnParams p) {
     const int lane = threadIdx.x & 63;
@@ -71,7 +72,7 @@ __global__ __launch_bounds__(256) void layernorm_kernel(LnParams p) {
         ld_row4<NV>(b2, p.b2, lane, p.D);
     }
     ln_row<NV>(v, lane, p.D, g1, b1, p.eps);
-    if constexpr (MODE != 0) {
+    if constexpr (MODE == 1 || MODE == 2) {
         float* yr = p.y_f32 + row * p.D;
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
@@ -80,6 +81,12 @@ __global__ __launch_bounds__(256) void layernorm_kernel(LnParams p) {
         }
         if constexpr (MODE == 2) return;
         else ln_row<NV>(v, lane, p.D, g2, b2, p.eps);
+    }
+    if constexpr (MODE == 3) {
+#pragma unroll
+        for (int i = 0; i < NV; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[i][e] = silu_dev(v[i][e]);
     }
     OutT* yo = (OutT*)p.y + row * p.D;
 #pragma unroll
@@ -92,7 +99,9 @@ __global__ __launch_bounds__(256) void layernorm_kernel(LnParams p) {
 template <int NV, typename OutT>
 static void ln_go(const LnParams& p, hipStream_t s) {
     const dim3 grid(cdiv(p.M, 4));
-    if (p.y_f32 && p.y)
+    if (p.silu)
+        launch((layernorm_kernel<NV, OutT, 3>), grid, dim3(256), 0, s, p);
+    else if (p.y_f32 && p.y)
         launch((layernorm_kernel<NV, OutT, 1>), grid, dim3(256), 0, s, p);
     else if (p.y_f32)
         launch((layernorm_kernel<NV, OutT, 2>), grid, dim3(256), 0, s, p);
@@ -113,6 +122,7 @@ static void ln_nv(const LnParams& p, hipStream_t s) {
 
 void launch_layernorm(Precision prec, const LnParams& p, hipStream_t s) {
     require(p.D % 4 == 0, "layernorm: D must be a multiple of 4");
+    require(!p.silu || (p.y && !p.y_f32), "layernorm: the SiLU output is the activation-type y only");
     if (p.M == 0) return;
     if (prec == PREC_F16) ln_nv<f16>(p, s);
     else ln_nv<float>(p, s);
@@ -120,24 +130,26 @@ void launch_layernorm(Precision prec, const LnParams& p, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------
-// Depthwise conv1d + bias + folded BatchNorm + SiLU, sliding window over time
-// in registers: a thread owns 16 bytes of channels (8 f16 / 4 f32) and TT
-// output frames, loading TT + K - 1 input frames once.
+// Depthwise conv1d + bias (+ folded BatchNorm + SiLU), sliding window over
+// time in registers: a thread owns 16 bytes of channels (8 f16 / 4 f32) and TT
+// output frames, loading TT + K - 1 input frames once.  padl zero frames
+// precede each item ((K-1)/2 symmetric, K-1 causal, conformer.cpp:81-120).
+// BNSILU: y = silu((conv + b) * scale + shift) in the input type; otherwise
+// y = conv + b in f32 (the LayerNorm conv norm follows in its own pass).
 // ---------------------------------------------------------------------------
-template <typename T, int K, int TT>
-__global__ __launch_bounds__(256) void dwconv_bn_silu_kernel(const T* in, T* out, const float* w,
-                                                             const float* dwb, const float* sc,
-                                                             const float* sh, int Tn, int D) {
+template <typename T, typename OutT, int K, int TT, bool BNSILU>
+__global__ __launch_bounds__(256) void dwconv_kernel(const T* in, OutT* out, const float* w, const float* dwb,
+                                                     const float* sc, const float* sh, int Tn, int D, int padl) {
     constexpr int VEC = 16 / sizeof(T);
     const int c0 = (blockIdx.x * blockDim.x + threadIdx.x) * VEC;
     if (c0 >= D) return;
     const int t0 = blockIdx.y * TT, b = blockIdx.z;
-    constexpr int PAD = (K - 1) / 2, NW = TT + K - 1;
+    constexpr int NW = TT + K - 1;
     const T* base = in + (int64_t)b * Tn * D + c0;
     float win[NW][VEC];
 #pragma unroll
     for (int r = 0; r < NW; ++r) {
-        const int t = t0 - PAD + r;
+        const int t = t0 - padl + r;
         T x[VEC];
         if (t >= 0 && t < Tn) {
             *(int4v*)x = *(const int4v*)(base + (int64_t)t * D);
@@ -154,61 +166,73 @@ __global__ __launch_bounds__(256) void dwconv_bn_silu_kernel(const T* in, T* out
 #pragma unroll
         for (int k = 0; k < K; ++k) wk[e][k] = w[(c0 + e) * K + k];
         bias[e] = dwb ? dwb[c0 + e] : 0.f;
-        scale[e] = sc[c0 + e];
-        shift[e] = sh[c0 + e];
+        scale[e] = BNSILU ? sc[c0 + e] : 1.f;
+        shift[e] = BNSILU ? sh[c0 + e] : 0.f;
     }
-    T* ob = out + (int64_t)b * Tn * D + c0;
+    OutT* ob = out + (int64_t)b * Tn * D + c0;
 #pragma unroll
     for (int tt = 0; tt < TT; ++tt) {
         const int t = t0 + tt;
         if (t >= Tn) break;
-        T o[VEC];
+        OutT o[VEC];
 #pragma unroll
         for (int e = 0; e < VEC; ++e) {
             float acc = 0.f;
 #pragma unroll
             for (int k = 0; k < K; ++k) acc += wk[e][k] * win[tt + k][e];
-            const float y = (acc + bias[e]) * scale[e] + shift[e];
-            o[e] = to_act<T>(silu_dev(y));
+            if constexpr (BNSILU) o[e] = to_act<OutT>(silu_dev((acc + bias[e]) * scale[e] + shift[e]));
+            else o[e] = acc + bias[e];
         }
-        *(int4v*)(ob + (int64_t)t * D) = *(const int4v*)o;
+        OutT* dst = ob + (int64_t)t * D;
+        if constexpr (sizeof(OutT) * VEC == 16) {
+            *(int4v*)dst = *(const int4v*)o;
+        } else {
+#pragma unroll
+            for (int h = 0; h < (int)(sizeof(OutT) * VEC / 16); ++h) ((int4v*)dst)[h] = ((const int4v*)o)[h];
+        }
     }
 }
 
 template <typename ET, int K>
 static void dw_go(const void* in, void* out, const float* w, const float* dwb, const float* sc,
-                  const float* sh, int B, int Tn, int D, hipStream_t s) {
+                  const float* sh, int B, int Tn, int D, int padl, hipStream_t s) {
     // one wave per (64 channel vectors, 4 frames, item): enough waves in flight
     // to cover the load latency of this small pass (B*T*D/2048 waves)
     constexpr int TT = 4, VEC = 16 / sizeof(ET);
     const int nvec = D / VEC;
     const int bs = 64;
     const dim3 grid(cdiv(nvec, bs), cdiv(Tn, TT), B);
-    launch((dwconv_bn_silu_kernel<ET, K, TT>), grid, dim3(bs), 0, s, (const ET*)in, (ET*)out, w, dwb, sc, sh, Tn,
-           D);
+    if (sc)
+        launch((dwconv_kernel<ET, ET, K, TT, true>), grid, dim3(bs), 0, s, (const ET*)in, (ET*)out, w, dwb, sc, sh,
+               Tn, D, padl);
+    else
+        launch((dwconv_kernel<ET, float, K, TT, false>), grid, dim3(bs), 0, s, (const ET*)in, (float*)out, w, dwb,
+               sc, sh, Tn, D, padl);
 }
 
 template <typename ET>
 static void dw_k(const void* in, void* out, const float* w, const float* dwb, const float* sc,
-                 const float* sh, int B, int Tn, int D, int K, hipStream_t s) {
+                 const float* sh, int B, int Tn, int D, int K, int padl, hipStream_t s) {
     switch (K) {
-    case 3: dw_go<ET, 3>(in, out, w, dwb, sc, sh, B, Tn, D, s); break;
-    case 5: dw_go<ET, 5>(in, out, w, dwb, sc, sh, B, Tn, D, s); break;
-    case 7: dw_go<ET, 7>(in, out, w, dwb, sc, sh, B, Tn, D, s); break;
-    case 9: dw_go<ET, 9>(in, out, w, dwb, sc, sh, B, Tn, D, s); break;
-    case 15: dw_go<ET, 15>(in, out, w, dwb, sc, sh, B, Tn, D, s); break;
-    case 31: dw_go<ET, 31>(in, out, w, dwb, sc, sh, B, Tn, D, s); break;
+    case 3: dw_go<ET, 3>(in, out, w, dwb, sc, sh, B, Tn, D, padl, s); break;
+    case 5: dw_go<ET, 5>(in, out, w, dwb, sc, sh, B, Tn, D, padl, s); break;
+    case 7: dw_go<ET, 7>(in, out, w, dwb, sc, sh, B, Tn, D, padl, s); break;
+    case 9: dw_go<ET, 9>(in, out, w, dwb, sc, sh, B, Tn, D, padl, s); break;
+    case 15: dw_go<ET, 15>(in, out, w, dwb, sc, sh, B, Tn, D, padl, s); break;
+    case 31: dw_go<ET, 31>(in, out, w, dwb, sc, sh, B, Tn, D, padl, s); break;
     default: throw std::invalid_argument("dwconv: unsupported kernel size");
     }
 }
 
-void launch_dwconv_bn_silu(Precision prec, const void* in, void* out, const float* w,
-                           const float* dw_bias, const float* bn_scale, const float* bn_shift,
-                           int B, int T, int D, int K, hipStream_t s) {
+void launch_dwconv(Precision prec, const void* in, void* out, const float* w, const float* dw_bias,
+                   const float* bn_scale, const float* bn_shift, int B, int T, int D, int K, bool causal,
+                   hipStream_t s) {
     if (B == 0 || T == 0) return;
     require(D % 8 == 0, "dwconv: D must be a multiple of 8");
-    if (prec == PREC_F16) dw_k<f16>(in, out, w, dw_bias, bn_scale, bn_shift, B, T, D, K, s);
-    else dw_k<float>(in, out, w, dw_bias, bn_scale, bn_shift, B, T, D, K, s);
+    require((bn_scale == nullptr) == (bn_shift == nullptr), "dwconv: BatchNorm scale and shift go together");
+    const int padl = causal ? K - 1 : (K - 1) / 2;
+    if (prec == PREC_F16) dw_k<f16>(in, out, w, dw_bias, bn_scale, bn_shift, B, T, D, K, padl, s);
+    else dw_k<float>(in, out, w, dw_bias, bn_scale, bn_shift, B, T, D, K, padl, s);
     PKX_LAUNCH_CHECK();
 }
 

@@ -21,15 +21,19 @@ struct LnParams {
     int64_t M = 0;
     int D = 0;
     float eps = 1e-5f;
+    bool silu = false;   // y = silu(LN(x; g, b)): the conv module's LayerNorm conv norm (conformer.cpp:126-133, :157)
 };
 void launch_layernorm(Precision prec, const LnParams& p, hipStream_t s);
 
-// Conv module middle (conformer.cpp:81-157): depthwise conv (K taps, symmetric
-// pad (K-1)/2, cross-correlation) + bias, folded BatchNorm scale/shift, SiLU.
-// in/out [B][T][D] activation type; w [D][K].
-void launch_dwconv_bn_silu(Precision prec, const void* in, void* out, const float* w,
-                           const float* dw_bias, const float* bn_scale, const float* bn_shift,
-                           int B, int T, int D, int K, hipStream_t s);
+// Conv module middle (conformer.cpp:81-157): depthwise conv (K taps,
+// cross-correlation; zero padding (K-1)/2 both sides, or K-1 before only when
+// causal, conformer.cpp:100-120) + bias, then with bn_scale/bn_shift the
+// folded BatchNorm and SiLU into `out` in the activation type, or without them
+// the raw conv + bias into `out` as f32 (for the LayerNorm conv norm).
+// in [B][T][D] activation type; w [D][K].
+void launch_dwconv(Precision prec, const void* in, void* out, const float* w, const float* dw_bias,
+                   const float* bn_scale, const float* bn_shift, int B, int T, int D, int K, bool causal,
+                   hipStream_t s);
 
 // Output length of one k3 s2 subsampling stage: all_paddings 2, or 3 when
 // causal (2 before, 1 after; subsampling.cpp:25-46).

@@ -808,7 +808,9 @@ void Model::conv_front(const LayerDev& L, const void* A, int64_t M, const int* v
                        hipStream_t s, bool fold) {
     const ModelConfig& c = cfg_;
     const int D = c.d_model;
-    if (c.conv_kernel == GLU_DW_K && gemm_glu_dw_supported(prec_, L.pw1.gtype, L.pw1.N, L.pw1.K)) {
+    // the one-pass epilogue is the symmetric-padding, BatchNorm conv module
+    if (c.conv_kernel == GLU_DW_K && !c.conv_ln && !c.conv_causal &&
+        gemm_glu_dw_supported(prec_, L.pw1.gtype, L.pw1.N, L.pw1.K)) {
         // one pass: the GEMM epilogue stages GLU rows in LDS and runs the
         // depthwise conv over time on them (conformer.cpp:48-157)
         GemmParams p;
@@ -851,7 +853,25 @@ void Model::conv_front(const LayerDev& L, const void* A, int64_t M, const int* v
         gemm(L.pw1, EPI_GLU, A, D, M, L.pw1_b, glu.p, D, 1.f, valid, T, s, prec_, KF_GEMM_PW1_GLU);
     }
     mark(KF_DWCONV, true);
-    launch_dwconv_bn_silu(prec_, glu.p, Y, L.dw_w, L.dw_b, L.bn_scale, L.bn_shift, B, T, D, c.conv_kernel, s);
+    if (c.conv_ln) {
+        // conv_norm_type "layer_norm": depthwise conv + bias in f32, then the
+        // LayerNorm over channels + SiLU (conformer.cpp:126-133, :157)
+        grow(w.tmp, (size_t)M * D * 4);
+        launch_dwconv(prec_, glu.p, w.tmp.p, L.dw_w, L.dw_b, nullptr, nullptr, B, T, D, c.conv_kernel,
+                      c.conv_causal != 0, s);
+        LnParams lp;
+        lp.x = (const float*)w.tmp.p;
+        lp.g = L.cn_g;
+        lp.b = L.cn_b;
+        lp.y = Y;
+        lp.M = M;
+        lp.D = D;
+        lp.silu = true;
+        launch_layernorm(prec_, lp, s);
+    } else {
+        launch_dwconv(prec_, glu.p, Y, L.dw_w, L.dw_b, L.bn_scale, L.bn_shift, B, T, D, c.conv_kernel,
+                      c.conv_causal != 0, s);
+    }
     mark(KF_DWCONV, false);
 }
 
@@ -895,6 +915,15 @@ void Model::stage_valid(const std::vector<int>* v[4], hipStream_t s) {
         std::memcpy(w.h_valid + (size_t)k * w.Bcap, v[k]->data(), v[k]->size() * sizeof(int));
     PKX_HIP(hipMemcpyAsync(w.d_valid, w.h_valid, sizeof(int) * 4 * (size_t)w.Bcap, hipMemcpyHostToDevice, s));
     PKX_HIP(hipEventRecord(w.staged, s));
+}
+
+// The chunked-limited window of a streaming model (relpos_attention.cpp:252-275):
+// chunks of att_right + 1 frames, a query sees its own chunk and
+// att_left / chunk_size chunks before it.
+void Model::att_window(AttnParams& a) const {
+    if (!cfg_.att_limited) return;
+    a.chunk = cfg_.att_right + 1;
+    a.left_chunks = cfg_.att_left / a.chunk;
 }
 
 void Model::ensure_pe(int T, hipStream_t s, const float* given) {
@@ -981,9 +1010,6 @@ void Model::subsampling_kernels(const float* mel, int B, int T_max, bool stage_m
 // ---------------------------------------------------------------------------
 void Model::layer_body(int l, float* x, int B, int T, const int* d_valid, bool first_ln_done,
                        bool fuse_next_ln, bool pos_all, hipStream_t s) {
-    require(!cfg_.conv_ln && !cfg_.conv_causal && !cfg_.att_limited,
-            "offline forward of a cache-aware streaming model (layer_norm / causal conv / chunked-limited "
-            "attention) is not implemented: use the streaming encoder");
     const ModelConfig& c = cfg_;
     const LayerDev& L = layers_[l];
     const int D = c.d_model, H = c.n_heads, dk = D / H;
@@ -1049,6 +1075,7 @@ void Model::layer_body(int l, float* x, int B, int T, const int* d_valid, bool f
         a.H = H;
         a.dk = dk;
         a.scale = 1.0f / std::sqrt((float)dk);
+        att_window(a);
         mark(KF_ATTENTION, true);
         launch_relpos_attention(prec_, a, s);
         mark(KF_ATTENTION, false);
@@ -1160,9 +1187,6 @@ void Model::conformer_layer_forward(int layer, const float* x, int B, int T, con
 
 void Model::relpos_attention_forward(int layer, const float* x, int B, int T, const int* valid, const float* pos,
                                      float* out, hipStream_t s) {
-    require(!cfg_.conv_ln && !cfg_.conv_causal && !cfg_.att_limited,
-            "offline forward of a cache-aware streaming model (layer_norm / causal conv / chunked-limited "
-            "attention) is not implemented: use the streaming encoder");
     require(finalized_, "model not finalized");
     require(layer >= 0 && layer < cfg_.n_layers, "layer index out of range");
     ensure_ws(B, 8 * T);
@@ -1202,15 +1226,13 @@ void Model::relpos_attention_forward(int layer, const float* x, int B, int T, co
     a.H = H;
     a.dk = dk;
     a.scale = 1.0f / std::sqrt((float)dk);
+    att_window(a);
     launch_relpos_attention(prec_, a, s);
     gemm(L.wo, EPI_STORE_F32, w.h.p, D, M, L.bo, out, D, 1.f, nullptr, 1, s, prec_, KF_GEMM_OUT);
 }
 
 void Model::conv_module_forward(int layer, const float* cin, int B, int T, const int* valid, float* out,
                                 hipStream_t s) {
-    require(!cfg_.conv_ln && !cfg_.conv_causal && !cfg_.att_limited,
-            "offline forward of a cache-aware streaming model (layer_norm / causal conv / chunked-limited "
-            "attention) is not implemented: use the streaming encoder");
     require(finalized_, "model not finalized");
     require(layer >= 0 && layer < cfg_.n_layers, "layer index out of range");
     ensure_ws(B, 8 * T);

@@ -237,6 +237,7 @@ private:
     // positional table of T' frames in ws_->pe (act dtype): computed, or the
     // caller's f32 table cast
     void ensure_pe(int T, hipStream_t s, const float* given = nullptr);
+    void att_window(AttnParams& a) const;
     void stage_valid(const std::vector<int>* v[4], hipStream_t s);
     void mark(int fam, bool begin);
     void* cast_to_act(const float* x, int64_t n, hipStream_t s);

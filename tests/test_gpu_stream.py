@@ -135,11 +135,6 @@ def test_streaming_needs_streaming_model(gpu, stream):
     gm = gpu.Model.from_tensors(pm.synthesize(cfg, "f32", heads=False), precision=0)
     with pytest.raises(gpu.PkxError, match="streaming configuration"):
         gpu.Streaming(gm, 1, 25, stream=stream)
-    # and the offline forward refuses a streaming model
-    _, _, _, gs, _ = _models(gpu, "f32")
-    x = gpu.DeviceArray((1, 20, 128), np.float32)
-    with pytest.raises(gpu.PkxError, match="streaming encoder"):
-        gs.conformer_layer(0, x, [20], x, stream=stream)
 
 
 def test_streaming_model_from_gguf(gpu, stream, tmp_path):
