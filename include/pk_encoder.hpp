@@ -2,19 +2,34 @@
 // the gfx950 kernels behind the pkx C ABI (pkx.h).
 //
 // Same class names, method names, argument meaning and layouts as the
-// reference's host API for this path, so code written against it (the
-// transcribe paths in src/model.cpp, the CLI bench, the tests) compiles
-// against this header unchanged:
-//   pk::ModelLoader       src/model_loader.hpp:53-83 (load + config only)
+// reference's host API for this path, so the encoder calls of code written
+// against it (the transcribe paths in src/model.cpp, the CLI bench, the layer
+// tests) compile against this header.  Deviations, each because nothing here
+// uses ggml:
+//   * ModelLoader has no tensor(), ggml_ctx(), realize_weights() or
+//     weights_realized() (the weights live on the device, not in a ggml
+//     context); it adds load(path, precision), last_error(), handle(),
+//     precision(), mel_handle() and device().
+//   * The ggml graph builders (build_graph, build_graph_batched) have no
+//     counterpart; their batched semantics are forward_batch() overloads.
+//   * PredictionNet and Joint keep only their constructors: the reference's
+//     per-step host methods (forward, step, step_logits) do not exist, since
+//     transducer_greedy_batch runs every step on the device.
+//   * A failing forward throws std::runtime_error (the reference asserts).
+// Classes and their reference declarations:
+//   pk::ModelLoader       src/model_loader.hpp:53-83
+//   pk::ParakeetConfig    src/model_loader.hpp:27-52 (same fields and types)
 //   pk::MelBatch          src/encoder.hpp:17-23
 //   pk::Encoder           src/encoder.hpp:25-62
 //   pk::Subsampling       src/subsampling.hpp:11-76
 //   pk::ConformerLayer    src/conformer.hpp:48-110
 //   pk::RelPosAttention   src/relpos_attention.hpp:31-66
 //   pk::rel_pos_encoding  src/pos_enc.hpp:20
-// The ggml graph builders (build_graph, build_graph_batched) have no
-// counterpart: nothing here builds a graph.  Their batched semantics are
-// offered as forward_batch() overloads on host vectors instead.
+//   pk::PredictionNet, pk::Joint, pk::transducer_greedy_batch
+//                         src/prediction.hpp:51-53, src/joint.hpp:29-31,
+//                         src/transducer_batch.hpp:12-20
+//   pk::StreamingEncoder  src/streaming_encoder.hpp:33-95
+//   pk::MelFrontend       src/mel.hpp:31 (whole-clip front end)
 //
 // Errors: ModelLoader::load returns false (message in last_error() and on
 // stderr), like the reference.  A failing forward throws std::runtime_error
