@@ -104,6 +104,19 @@ __device__ __forceinline__ float group_sum(float v, int n) {
     if (n > 8) v += dpp_get<0x140>(v);   // row_mirror
     return v;
 }
+// Sum over a whole wave, every lane receiving it: DPP within each row of 16
+// lanes, then the four row sums read with v_readlane (no LDS round trips, as
+// the ds_bpermute steps of wave_sum take).  Every lane of the wave must be
+// active.
+__device__ __forceinline__ float wave_sum_full(float v) {
+    v = group_sum(v, 16);
+    const int vi = __builtin_bit_cast(int, v);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 48));
+    return (r0 + r1) + (r2 + r3);
+}
 // max over the 16 lanes of each DPP row
 __device__ __forceinline__ float row16_max(float v) {
     v = fmaxf(v, dpp_get<0xB1>(v));

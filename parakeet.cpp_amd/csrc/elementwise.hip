@@ -7,6 +7,8 @@ namespace pkx {
 
 // ---------------------------------------------------------------------------
 // LayerNorm: one wave per row, the row held in registers (NV float4 per lane).
+// A wave past the last row returns as a whole, so every reducing wave has all
+// 64 lanes active.
 // ---------------------------------------------------------------------------
 // gamma/beta are loaded by the caller before the row statistics are formed,
 // so their memory latency overlaps the reductions instead of following them.
@@ -19,7 +21,7 @@ __device__ __forceinline__ void ln_row(float4v (&v)[NV], int lane, int D, const 
         const int c = (lane + 64 * i) * 4;
         if (c < D) s += (v[i][0] + v[i][1]) + (v[i][2] + v[i][3]);
     }
-    const float mean = wave_sum(s) / (float)D;
+    const float mean = wave_sum_full(s) / (float)D;
     float s2 = 0.f;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
@@ -33,7 +35,7 @@ __device__ __forceinline__ void ln_row(float4v (&v)[NV], int lane, int D, const 
             }
         }
     }
-    const float rs = 1.0f / sqrtf(wave_sum(s2) / (float)D + eps);
+    const float rs = 1.0f / sqrtf(wave_sum_full(s2) / (float)D + eps);
 #pragma unroll
     for (int i = 0; i < NV; ++i)
 #pragma unroll
