@@ -1676,6 +1676,29 @@ static bool dma_kg2(int epi, const GemmParams& p, hipStream_t s) {
 }
 template <int TM, int TN, int WT>
 static void f32_epi(int epi, const GemmParams& p, hipStream_t s) { PKX_EPI_SWITCH(run_f32, TM, TN, WT) }
+// tiles narrower than 64 columns per wave pair: every epilogue but GLU (which
+// pairs 32-column input and gate groups inside a wave's 64 columns)
+template <int TM, int TN, int WT>
+static void f32_epi_narrow(int epi, const GemmParams& p, hipStream_t s) {
+    switch (epi) {
+    case EPI_STORE: run_f32<TM, TN, WT, EPI_STORE>(p, s); break;
+    case EPI_STORE_F32: run_f32<TM, TN, WT, EPI_STORE_F32>(p, s); break;
+    case EPI_SILU: run_f32<TM, TN, WT, EPI_SILU>(p, s); break;
+    case EPI_RESID: run_f32<TM, TN, WT, EPI_RESID>(p, s); break;
+    case EPI_RELU: run_f32<TM, TN, WT, EPI_RELU>(p, s); break;
+    case EPI_RELU_TR: run_f32<TM, TN, WT, EPI_RELU_TR>(p, s); break;
+    case EPI_RELU2_F32: run_f32<TM, TN, WT, EPI_RELU2_F32>(p, s); break;
+    default: throw std::invalid_argument("gemm: bad epilogue");
+    }
+}
+// shape 0: 64x128 tiles; 1: 32x64; 2: 32x32 (GLU keeps 64-column wave tiles: 32x128)
+template <int WT>
+static void f32_shape(int shape, int epi, const GemmParams& p, hipStream_t s) {
+    if (shape == 0) f32_epi<2, 4, WT>(epi, p, s);
+    else if (epi == EPI_GLU) f32_epi<1, 4, WT>(epi, p, s);
+    else if (shape == 1) f32_epi_narrow<1, 2, WT>(epi, p, s);
+    else f32_epi_narrow<1, 1, WT>(epi, p, s);
+}
 
 bool gemm_glu_dw_supported(Precision prec, int wtype, int N, int K) {
     return prec == PREC_F16 && N % 64 == 0 && K % 64 == 0 &&
@@ -1752,11 +1775,16 @@ void launch_gemm(Precision prec, int wtype, int epi, const GemmParams& p, hipStr
         default: throw std::invalid_argument("gemm(f16): weight type must be f16/q8_0/q4_K");
         }
     } else {
+        // 64x128 tiles while they fill the chip; a single utterance (M = T' ~ 125)
+        // gives only 8-32 of them, so smaller tiles buy workgroups there
+        const int64_t t24 = (int64_t)cdiv(p.M, 64) * cdiv(p.N, 128);
+        const int64_t t12 = (int64_t)cdiv(p.M, 32) * cdiv(p.N, 64);
+        const int shape = t24 >= 256 ? 0 : t12 >= 256 ? 1 : 2;
         switch (wtype) {
-        case GT_F32: f32_epi<2, 4, GT_F32>(epi, p, s); break;
-        case GT_F16: f32_epi<2, 4, GT_F16>(epi, p, s); break;
-        case GT_Q8_0: f32_epi<2, 4, GT_Q8_0>(epi, p, s); break;
-        case GT_Q4_K: f32_epi<2, 4, GT_Q4_K>(epi, p, s); break;
+        case GT_F32: f32_shape<GT_F32>(shape, epi, p, s); break;
+        case GT_F16: f32_shape<GT_F16>(shape, epi, p, s); break;
+        case GT_Q8_0: f32_shape<GT_Q8_0>(shape, epi, p, s); break;
+        case GT_Q4_K: f32_shape<GT_Q4_K>(shape, epi, p, s); break;
         default: throw std::invalid_argument("gemm(f32): unknown weight type");
         }
     }
