@@ -13,242 +13,358 @@
 // K / V^T / band staging needs block-wide barriers.
 #include "attention.hpp"
 
+#include <type_traits>
+
 namespace pkx {
 
-// ---------------------------------------------------------------------------
-// f16 MFMA kernel.  NW waves per block, 16 query rows per wave (AQ = 16 NW).
-// ---------------------------------------------------------------------------
 constexpr int AK = 64;   // keys per tile
 
-template <int DK, int NW>
-struct AttnSmem {
-    static constexpr int AQ = 16 * NW;
-    static constexpr int APB = (AQ + AK - 1 + 15) / 16 * 16;  // positional band rows per key tile
-    static constexpr int LDK = DK + 8;   // K and P rows (halves)
-    static constexpr int LDV = AK + 8;   // transposed V rows (halves)
-    static constexpr int LDG = 80;       // band product (floats)
-    static constexpr int LDP = AK + 8;   // probabilities (halves)
-    f16 k[AK * LDK];
-    f16 vt[DK * LDV];
-    f16 p[APB * LDK];
-    float g[NW][16 * LDG];
-    f16 prob[NW][16 * LDP];
+// ---------------------------------------------------------------------------
+// f16 MFMA kernel, key-split: 8 waves per block in two key groups.  Waves 0-3
+// take the even 64-key tiles, waves 4-7 the odd ones, each wave the same 16
+// query rows as its partner; the two online-softmax states are merged once at
+// the end.  A 64-query block therefore keeps two waves per SIMD busy, and a
+// short sequence (T' <= 128) costs each wave a single key tile.  K, the
+// positional band and V^T are staged for both tiles of a step at once; their
+// 16-byte chunks are XOR-swizzled within each 256-byte LDS line, so 16
+// consecutive rows read at one logical chunk hit 16 distinct bank quads
+// without row padding.
+// ---------------------------------------------------------------------------
+template <int DK>
+struct KsSmem {
+    static constexpr int AQ = 64;                   // queries per block
+    static constexpr int NCH = DK / 8;              // 16-byte chunks per K / band row
+    static constexpr int BROWS = AQ + 2 * AK;       // band rows per step (AQ + 2 AK - 1 used)
+    static constexpr int LDG = 84;                  // G row (floats): row groups 4 apart land 16 banks apart
+    static constexpr int LDP = AK + 8;              // probability row (halves)
+    f16 k[2 * AK * DK];       // [group][key][DK]
+    f16 vt[2 * DK * AK];      // [group][dim][key]
+    f16 p[BROWS * DK];        // band rows of the step
+    float g[8][16 * LDG];     // per wave: G, then its probabilities (f16)
 };
 
-template <int DK, int NW>
-__global__ __launch_bounds__(64 * NW, 1) void relpos_attn_f16_kernel(AttnParams a) {
-    static_assert(DK % 32 == 0, "head dim must be a multiple of 32");
-    typedef AttnSmem<DK, NW> S;
-    constexpr int AQ = S::AQ, NT = 64 * NW;
+// stored position of logical 16-byte chunk c in row r of a swizzled array
+// with nch chunks per row (rows shorter than 256 bytes share an LDS line)
+__device__ __forceinline__ int swz(int r, int c, int nch) { return c ^ ((r / (16 / nch)) % nch); }
+
+template <int DK, bool LONG>
+__global__ __launch_bounds__(512, 1) void relpos_attn_ks_kernel(AttnParams a) {
+    static_assert(DK == 32 || DK == 64 || DK == 128, "head dim");
+    typedef KsSmem<DK> S;
+    constexpr int AQ = S::AQ, NCH = S::NCH, NT = 512, NKC = DK / 32, NDT = DK / 16;
     __shared__ __attribute__((aligned(16))) S sm;
+    static_assert(sizeof(S) <= 160 * 1024, "LDS");
+    static_assert(8 * (NDT * 2 + 4) * 64 * 4 <= sizeof(sm.k) + sizeof(sm.vt), "merge area");
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int b = blockIdx.z, h = blockIdx.y, i0 = blockIdx.x * AQ;
+    const int grp = w >> 2, wq = w & 3;
     const int T = a.T, P = 2 * T - 1;
+    // work order (head, item, query block), query block fastest, each XCD a
+    // contiguous run: the blocks of one item share K and V, those of one head
+    // the positional band, in the XCD's L2
+    const int nq = (T + AQ - 1) / AQ;
+    const int wid = xcd_tile(blockIdx.x, nq * a.B * a.H);
+    const int b = (wid / nq) % a.B, h = wid / (nq * a.B), i0 = (wid % nq) * AQ;
     const int vl = a.valid ? a.valid[b] : T;
-    const int i0w = i0 + 16 * w;
-    const float scale = a.scale;
+    const int i0w = i0 + 16 * wq;
+    const int lr = 4 * (lane >> 4), lc = lane & 15;
     const f16* q = (const f16*)a.q;
     const f16* k = (const f16*)a.k;
     const f16* v = (const f16*)a.v;
     const f16* pp = (const f16*)a.p;
     const int64_t rowq = (int64_t)b * T;
+    const int nit = (vl + 2 * AK - 1) / (2 * AK);   // steps of 128 keys (<= 1 unless LONG)
 
-    // Query fragments (A operand of v_mfma_f32_16x16x32_f16): row lane%16,
-    // k = 32*kc + 8*(lane/16) + [0..7].  pos_bias_u/v added in f32.
-    constexpr int NKC = DK / 32;
-    half8v qu[NKC], qv[NKC];
-    {
-        const int i = i0w + (lane & 15);
-#pragma unroll
-        for (int kc = 0; kc < NKC; ++kc) {
-            const int c0 = 32 * kc + 8 * (lane >> 4);
-            half8v x = {};
-            if (i < T) x = *(const half8v*)(q + (rowq + i) * a.ldq + h * DK + c0);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float xf = (float)x[e];
-                qu[kc][e] = (f16)(xf + a.bias_u[h * DK + c0 + e]);
-                qv[kc][e] = (f16)(xf + a.bias_v[h * DK + c0 + e]);
-            }
-        }
-    }
-
-    constexpr int NDT = DK / 16;
-    float4v o[NDT];
-#pragma unroll
-    for (int d = 0; d < NDT; ++d) o[d] = (float4v){0.f, 0.f, 0.f, 0.f};
-    float mrow[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-    float lrow[4] = {0.f, 0.f, 0.f, 0.f};
-    const int lr = 4 * (lane >> 4), lc = lane & 15;
-
-    // Staging of one key tile (K rows, V as 8x8 blocks, the positional band)
-    // through registers: all of a tile's global loads are issued together, and
-    // the next tile's loads are in flight while the current tile is computed.
-    constexpr int KCH = AK * (DK / 8), VCH = (AK / 8) * (DK / 8), PCH = S::APB * (DK / 8);
-    constexpr int KPT = (KCH + NT - 1) / NT, VPT = (VCH + NT - 1) / NT, PPT = (PCH + NT - 1) / NT;
-    half8v kreg[KPT], vreg[VPT][8], preg[PPT];
-    auto load_tile = [&](int j0) {
-        const int rlo = T - 1 - (i0 + AQ - 1) + j0;
-#pragma unroll
-        for (int u = 0; u < KPT; ++u) {
-            const int c = tid + NT * u, r = c / (DK / 8), col = (c % (DK / 8)) * 8, j = j0 + r;
-            kreg[u] = (c < KCH && j < T) ? *(const half8v*)(k + (rowq + j) * a.ldk + h * DK + col) : (half8v){};
-        }
+    // V of a step: 8 x 8 blocks (8 keys x 8 dims) through registers, lanes
+    // along the dims so that 16 lanes read one whole row; transposed on the
+    // way into LDS (V^T rows are dims, keys contiguous)
+    constexpr int VCH = (2 * AK / 8) * NCH, VPT = (VCH + NT - 1) / NT;
+    half8v vreg[VPT][8];
+    auto load_v = [&](int jb) {
 #pragma unroll
         for (int u = 0; u < VPT; ++u) {
-            const int c = tid + NT * u, kg = c % (AK / 8), dg = c / (AK / 8);
+            const int c = tid + NT * u, kg = c / NCH, dg = c % NCH;
+            const f16* src = v + (rowq + jb + 8 * kg) * a.ldv + h * DK + 8 * dg;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int j = j0 + 8 * kg + e;
-                vreg[u][e] = (c < VCH && j < T) ? *(const half8v*)(v + (rowq + j) * a.ldv + h * DK + 8 * dg)
-                                                : (half8v){};
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < PPT; ++u) {
-            const int c = tid + NT * u, r = c / (DK / 8), col = (c % (DK / 8)) * 8, pr = rlo + r;
-            preg[u] = (c < PCH && pr >= 0 && pr < P) ? *(const half8v*)(pp + (int64_t)pr * a.ldp + h * DK + col)
-                                                     : (half8v){};
+            for (int e = 0; e < 8; ++e)
+                vreg[u][e] = (c < VCH && jb + 8 * kg + e < T) ? *(const half8v*)(src + (int64_t)e * a.ldv) : (half8v){};
         }
     };
-    auto store_tile = [&]() {
-#pragma unroll
-        for (int u = 0; u < KPT; ++u) {
-            const int c = tid + NT * u;
-            if (c < KCH) *(half8v*)(sm.k + (c / (DK / 8)) * S::LDK + (c % (DK / 8)) * 8) = kreg[u];
-        }
-        // V^T: the 8 x 8 block is transposed in registers, keys contiguous
+    auto store_v = [&]() {
 #pragma unroll
         for (int u = 0; u < VPT; ++u) {
-            const int c = tid + NT * u, kg = c % (AK / 8), dg = c / (AK / 8);
+            const int c = tid + NT * u, kg = c / NCH, dg = c % NCH;
+            const int g = kg / (AK / 8), kc8 = kg % (AK / 8);
             if (c < VCH) {
 #pragma unroll
                 for (int d = 0; d < 8; ++d) {
                     half8v col;
 #pragma unroll
                     for (int e = 0; e < 8; ++e) col[e] = vreg[u][e][d];
-                    *(half8v*)(sm.vt + (8 * dg + d) * S::LDV + 8 * kg) = col;
+                    const int row = 8 * dg + d;
+                    *(half8v*)(sm.vt + (g * DK + row) * AK + swz(row, kc8, AK / 8) * 8) = col;
                 }
             }
+        }
+    };
+    // K and the positional band of a step through registers (long sequences:
+    // the next step's loads are in flight while this one is computed)
+    constexpr int KCH = 2 * AK * NCH, PCH = S::BROWS * NCH;
+    constexpr int KPT = LONG ? (KCH + NT - 1) / NT : 1, PPT = LONG ? (PCH + NT - 1) / NT : 1;
+    half8v kreg[KPT], preg[PPT];
+    auto load_kp = [&](int jb) {
+        const int rlo = T - 1 - (i0 + AQ - 1) + jb;
+#pragma unroll
+        for (int u = 0; u < KPT; ++u) {
+            const int c = tid + NT * u, r = c / NCH, j = jb + r;
+            kreg[u] = (c < KCH && j < T) ? *(const half8v*)(k + (rowq + j) * a.ldk + h * DK + (c % NCH) * 8)
+                                         : (half8v){};
         }
 #pragma unroll
         for (int u = 0; u < PPT; ++u) {
-            const int c = tid + NT * u;
-            if (c < PCH) *(half8v*)(sm.p + (c / (DK / 8)) * S::LDK + (c % (DK / 8)) * 8) = preg[u];
+            const int c = tid + NT * u, pr = rlo + c / NCH;
+            preg[u] = (c < PCH && pr >= 0 && pr < P) ? *(const half8v*)(pp + (int64_t)pr * a.ldp + h * DK + (c % NCH) * 8)
+                                                     : (half8v){};
+        }
+    };
+    auto store_kp = [&]() {
+#pragma unroll
+        for (int u = 0; u < KPT; ++u) {
+            const int c = tid + NT * u, r = c / NCH;   // r: 0..127 = group * 64 + key
+            if (c < KCH) *(half8v*)(sm.k + r * DK + swz(r, c % NCH, NCH) * 8) = kreg[u];
+        }
+#pragma unroll
+        for (int u = 0; u < PPT; ++u) {
+            const int c = tid + NT * u, r = c / NCH;
+            if (c < PCH) *(half8v*)(sm.p + r * DK + swz(r, c % NCH, NCH) * 8) = preg[u];
+        }
+    };
+    // A single step (T' <= 128): K and the band go straight into LDS by DMA,
+    // 16 bytes per lane, the swizzle applied through each lane's source
+    // chunk; rows past T' or outside the band's 2T'-1 positions read past the
+    // buffer's end (negative rows wrap above it) and arrive as zeros.
+    auto dma_kp = [&]() {
+        const __amdgpu_buffer_rsrc_t rk = make_rsrc(k + rowq * a.ldk + h * DK, ((int64_t)(T - 1) * a.ldk + DK) * 2);
+        const __amdgpu_buffer_rsrc_t rp = make_rsrc(pp + h * DK, ((int64_t)(P - 1) * a.ldp + DK) * 2);
+        const int rlo = T - 1 - (i0 + AQ - 1);
+        constexpr int KI = KCH / 64, PI = PCH / 64;   // 1-KB instructions per array
+        for (int ii = w; ii < KI; ii += 8) {
+            const int o = ii * 1024 + 16 * lane, r = o / (DK * 2), t = (o % (DK * 2)) / 16;
+            lds_dma16(rk, (uint8_t*)sm.k + ii * 1024, (uint32_t)((r * a.ldk + swz(r, t, NCH) * 8) * 2), 0);
+        }
+        for (int ii = w; ii < PI; ii += 8) {
+            const int o = ii * 1024 + 16 * lane, r = o / (DK * 2), t = (o % (DK * 2)) / 16;
+            const int64_t off = ((int64_t)(rlo + r) * a.ldp + swz(r, t, NCH) * 8) * 2;
+            lds_dma16(rp, (uint8_t*)sm.p + ii * 1024, off < 0 ? OOB : (uint32_t)off, 0);
         }
     };
 
-    load_tile(0);
-    for (int j0 = 0; j0 < vl; j0 += AK) {
-        store_tile();
-        __syncthreads();
-        if (j0 + AK < vl) load_tile(j0 + AK);
-
-        // ---- ac = qu . k^T : 16 x 64 per wave ----
-        float4v sac[4];
+    // the query rows and position biases first: they return ahead of the
+    // staging loads issued next (vector memory returns in order)
+    half8v qx[NKC];
+    float4v bq[NKC][4];   // bias_u, bias_u, bias_v, bias_v halves of each fragment's 8 columns
+    {
+        const int i = i0w + lc;
 #pragma unroll
-        for (int jt = 0; jt < 4; ++jt) {
-            sac[jt] = (float4v){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int kc = 0; kc < NKC; ++kc) {
-                const half8v kf = *(const half8v*)(sm.k + (16 * jt + lc) * S::LDK + 32 * kc + 8 * (lane >> 4));
-                sac[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qu[kc], kf, sac[jt], 0, 0, 0);
-            }
+        for (int kc = 0; kc < NKC; ++kc) {
+            const int c0 = h * DK + 32 * kc + 8 * (lane >> 4);
+            qx[kc] = i < T ? *(const half8v*)(q + (rowq + i) * a.ldq + c0) : (half8v){};
+            bq[kc][0] = *(const float4v*)(a.bias_u + c0);
+            bq[kc][1] = *(const float4v*)(a.bias_u + c0 + 4);
+            bq[kc][2] = *(const float4v*)(a.bias_v + c0);
+            bq[kc][3] = *(const float4v*)(a.bias_v + c0 + 4);
         }
-        // ---- band product G = qv . p_band^T : 16 x 80, band rows start at AQ - 16 - 16 w ----
-        {
-            const int pb = AQ - 16 - 16 * w;
+    }
+    if (nit > 0) {
+        if constexpr (LONG) load_kp(0);
+        else dma_kp();
+        load_v(0);
+    }
+
+    // Query fragments (A operand of v_mfma_f32_16x16x32_f16): row lane%16,
+    // k = 32*kc + 8*(lane/16) + [0..7].  pos_bias_u/v added in f32.
+    half8v qu[NKC], qv[NKC];
+#pragma unroll
+    for (int kc = 0; kc < NKC; ++kc)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float xf = (float)qx[kc][e];
+            qu[kc][e] = (f16)(xf + bq[kc][e >> 2][e & 3]);
+            qv[kc][e] = (f16)(xf + bq[kc][2 + (e >> 2)][e & 3]);
+        }
+    // scores in log2 units: exp(scale * x) = exp2(scale * log2(e) * x)
+    const float sl2 = a.scale * 1.4426950408889634f;
+    // chunk of each of this lane's query rows (chunked-limited window)
+    int qch[4] = {0, 0, 0, 0};
+    if (a.chunk > 0) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) qch[r] = (i0w + lr + r) / a.chunk;
+    }
+
+    float4v o[NDT];
+#pragma unroll
+    for (int d = 0; d < NDT; ++d) o[d] = (float4v){0.f, 0.f, 0.f, 0.f};
+    float mrow[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    float lrow[4] = {0.f, 0.f, 0.f, 0.f};
+    float* gw = sm.g[w];
+    f16* probw = (f16*)gw;
+    const f16* kt = sm.k + grp * AK * DK;
+    const f16* vtt = sm.vt + grp * DK * AK;
+    const int pb = AQ - 16 - 16 * wq + AK * grp;   // this wave's first band row
+
+    for (int s = 0; s < nit; ++s) {
+        if constexpr (LONG) store_kp();
+        store_v();
+        __builtin_amdgcn_s_waitcnt(0);   // this wave's DMAs have landed
+        __syncthreads();
+        if (s + 1 < nit) {
+            if constexpr (LONG) load_kp(2 * AK * (s + 1));
+            load_v(2 * AK * (s + 1));
+        }
+        const int j0 = 2 * AK * s + AK * grp;
+        if (j0 < vl) {
+            // ---- ac = qu . k^T : 16 x 64 ----
+            float4v sac[4];
+#pragma unroll
+            for (int jt = 0; jt < 4; ++jt) {
+                sac[jt] = (float4v){0.f, 0.f, 0.f, 0.f};
+                const int r = 16 * jt + lc;
+#pragma unroll
+                for (int kc = 0; kc < NKC; ++kc) {
+                    const half8v kf = *(const half8v*)(kt + r * DK + swz(r, 4 * kc + (lane >> 4), NCH) * 8);
+                    sac[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qu[kc], kf, sac[jt], 0, 0, 0);
+                }
+            }
+            // ---- band product G = qv . p_band^T : 16 x 80 ----
 #pragma unroll
             for (int gt = 0; gt < 5; ++gt) {
                 float4v g = {0.f, 0.f, 0.f, 0.f};
+                const int r = pb + 16 * gt + lc;
 #pragma unroll
                 for (int kc = 0; kc < NKC; ++kc) {
-                    const half8v pf = *(const half8v*)(sm.p + (pb + 16 * gt + lc) * S::LDK + 32 * kc + 8 * (lane >> 4));
+                    const half8v pf = *(const half8v*)(sm.p + r * DK + swz(r, 4 * kc + (lane >> 4), NCH) * 8);
                     g = __builtin_amdgcn_mfma_f32_16x16x32_f16(qv[kc], pf, g, 0, 0, 0);
                 }
 #pragma unroll
-                for (int r = 0; r < 4; ++r) sm.g[w][(lr + r) * S::LDG + 16 * gt + lc] = g[r];
+                for (int rr = 0; rr < 4; ++rr) gw[(lr + rr) * S::LDG + 16 * gt + lc] = g[rr];
             }
-        }
-        // each wave reads back only its own G rows: a wave-local barrier suffices
-        __builtin_amdgcn_s_waitcnt(0xc07f);
-        __builtin_amdgcn_wave_barrier();
+            // the wave reads back only its own G rows
+            __builtin_amdgcn_s_waitcnt(0xc07f);
+            __builtin_amdgcn_wave_barrier();
 
-        // ---- scores, rel_shift gather, key mask, online softmax ----
-        float s[4][4];
-        float tmax[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+            // ---- scores (rel_shift gather bd[i][j] = G[i][15 - i + j]), masks, online softmax ----
+            const bool kmask = j0 + AK > vl, cmask = a.chunk > 0;
+            int kch[4] = {0, 0, 0, 0};
+            if (cmask) {
 #pragma unroll
-        for (int jt = 0; jt < 4; ++jt)
+                for (int jt = 0; jt < 4; ++jt) kch[jt] = (j0 + 16 * jt + lc) / a.chunk;
+            }
+            float sc[4][4];
+            float tmax[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int ii = lr + r, jj = 16 * jt + lc;
-                const float bd = sm.g[w][ii * S::LDG + 15 - ii + jj];   // bd[i][T-1-i+j]
-                float sv = (sac[jt][r] + bd) * scale;
-                if (j0 + jj >= vl) sv = -INFINITY;
-                if (a.chunk > 0) {
-                    const int dc = (i0w + ii) / a.chunk - (j0 + jj) / a.chunk;
-                    if (dc < 0 || dc > a.left_chunks) sv = -INFINITY;
+            for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int ii = lr + r, jj = 16 * jt + lc;
+                    float sv = (sac[jt][r] + gw[ii * S::LDG + 15 - ii + jj]) * sl2;
+                    if (kmask && j0 + jj >= vl) sv = -INFINITY;
+                    if (cmask) {
+                        const int dc = qch[r] - kch[jt];
+                        if (dc < 0 || dc > a.left_chunks) sv = -INFINITY;
+                    }
+                    sc[jt][r] = sv;
+                    tmax[r] = fmaxf(tmax[r], sv);
                 }
-                s[jt][r] = sv;
-                tmax[r] = fmaxf(tmax[r], sv);
-            }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) tmax[r] = row16_max(tmax[r]);   // over the tile's 64 keys
-        float corr[4], tsum[4];
-        float msub[4];   // the running max, 0 while every key so far is masked (no -inf - -inf)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const float mnew = fmaxf(mrow[r], tmax[r]);
-            msub[r] = mnew == -INFINITY ? 0.f : mnew;
-            corr[r] = __expf(mrow[r] - msub[r]);   // exp(-inf) = 0 on the first tile
-            mrow[r] = mnew;
-            tsum[r] = 0.f;
-        }
-#pragma unroll
-        for (int jt = 0; jt < 4; ++jt)
+            float corr[4], msub[4], tsum[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float e = __expf(s[jt][r] - msub[r]);
-                tsum[r] += e;
-                sm.prob[w][(lr + r) * S::LDP + 16 * jt + lc] = (f16)e;
+                const float mnew = fmaxf(mrow[r], row16_max(tmax[r]));
+                msub[r] = mnew == -INFINITY ? 0.f : mnew;   // no -inf - -inf while every key so far is masked
+                corr[r] = __builtin_amdgcn_exp2f(mrow[r] - msub[r]);
+                mrow[r] = mnew;
+                tsum[r] = 0.f;
             }
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            tsum[r] = group_sum(tsum[r], 16);
-            lrow[r] = lrow[r] * corr[r] + tsum[r];
-        }
+            for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
-        for (int d = 0; d < NDT; ++d)
+                for (int r = 0; r < 4; ++r) {
+                    const float e = __builtin_amdgcn_exp2f(sc[jt][r] - msub[r]);
+                    tsum[r] += e;
+                    probw[(lr + r) * S::LDP + 16 * jt + lc] = (f16)e;
+                }
 #pragma unroll
-            for (int r = 0; r < 4; ++r) o[d][r] *= corr[r];
-        // the probabilities are wave-private too
-        __builtin_amdgcn_s_waitcnt(0xc07f);
-        __builtin_amdgcn_wave_barrier();
+            for (int r = 0; r < 4; ++r) lrow[r] = lrow[r] * corr[r] + group_sum(tsum[r], 16);
+            if (s > 0) {
+#pragma unroll
+                for (int d = 0; d < NDT; ++d)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) o[d][r] *= corr[r];
+            }
+            __builtin_amdgcn_s_waitcnt(0xc07f);
+            __builtin_amdgcn_wave_barrier();
 
-        // ---- o += prob . v : A = prob (16 x 64 keys), B = v^T rows ----
+            // ---- o += prob . v : A = prob (16 x 64 keys), B = v^T rows ----
 #pragma unroll
-        for (int kc = 0; kc < 2; ++kc) {
-            const half8v pf = *(const half8v*)(sm.prob[w] + lc * S::LDP + 32 * kc + 8 * (lane >> 4));
+            for (int kc = 0; kc < 2; ++kc) {
+                const half8v pf = *(const half8v*)(probw + lc * S::LDP + 32 * kc + 8 * (lane >> 4));
 #pragma unroll
-            for (int d = 0; d < NDT; ++d) {
-                const half8v vf = *(const half8v*)(sm.vt + (16 * d + lc) * S::LDV + 32 * kc + 8 * (lane >> 4));
-                o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf, vf, o[d], 0, 0, 0);
+                for (int d = 0; d < NDT; ++d) {
+                    const int r = 16 * d + lc;
+                    const half8v vf = *(const half8v*)(vtt + r * AK + swz(r, 4 * kc + (lane >> 4), AK / 8) * 8);
+                    o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf, vf, o[d], 0, 0, 0);
+                }
             }
         }
-        __syncthreads();   // the next tile's staging overwrites K, V^T and the band
+        __syncthreads();   // the next step's staging overwrites K, V^T and the band
     }
 
-    // ---- normalise, zero padded query rows, merge heads into ctx[b*T+i][h*DK+c] ----
+    // ---- merge the two key groups (K / V^T area reused): group 0 finishes
+    // rows r = 0, 1 of each lane's four, group 1 rows 2, 3; each hands the
+    // other half of its state over ----
+    constexpr int MR = NDT * 2 + 4;   // floats per lane handed over: o of two rows, m and l
+    float* hand = (float*)sm.k + (grp * 4 + wq) * MR * 64 + lane;
+    const float* take = (float*)sm.k + ((1 - grp) * 4 + wq) * MR * 64 + lane;
+    f16* stage = (f16*)sm.g[wq];   // the 16 output rows of query block wq (f16, DK wide)
+    auto give = [&](auto R) {
+        constexpr int r0 = decltype(R)::value;
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+#pragma unroll
+            for (int d = 0; d < NDT; ++d) hand[(d * 2 + rr) * 64] = o[d][r0 + rr];
+            hand[(NDT * 2 + rr) * 64] = mrow[r0 + rr];
+            hand[(NDT * 2 + 2 + rr) * 64] = lrow[r0 + rr];
+        }
+    };
+    auto keep = [&](auto R) {
+        constexpr int r0 = decltype(R)::value;
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+            const int r = r0 + rr;
+            const float m1 = take[(NDT * 2 + rr) * 64], l1 = take[(NDT * 2 + 2 + rr) * 64];
+            const float m = fmaxf(mrow[r], m1);
+            const float c0 = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mrow[r] - m);
+            const float c1 = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - m);
+            const float l = lrow[r] * c0 + l1 * c1;
+            const int i = i0w + lr + r;
+            const float inv = (i < vl && l > 0.f) ? 1.0f / l : 0.f;   // padded query rows are zero
+#pragma unroll
+            for (int d = 0; d < NDT; ++d)
+                stage[(lr + r) * DK + 16 * d + lc] = (f16)((o[d][r] * c0 + take[(d * 2 + rr) * 64] * c1) * inv);
+        }
+    };
+    if (grp == 0) give(std::integral_constant<int, 2>{});
+    else give(std::integral_constant<int, 0>{});
+    __syncthreads();
+    if (grp == 0) keep(std::integral_constant<int, 0>{});
+    else keep(std::integral_constant<int, 2>{});
+    __syncthreads();
+    // ---- store: wave (wq, grp) writes rows 8 grp .. 8 grp + 7 of block wq in 16-byte chunks ----
     f16* out = (f16*)a.out;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int i = i0w + lr + r;
-        if (i >= T) continue;
-        const float inv = (i < vl && lrow[r] > 0.f) ? 1.0f / lrow[r] : 0.f;
-#pragma unroll
-        for (int d = 0; d < NDT; ++d)
-            out[(rowq + i) * a.ldo + h * DK + 16 * d + lc] = (f16)(o[d][r] * inv);
+    for (int u = 0; u < (8 * NCH + 63) / 64; ++u) {
+        const int c = lane + 64 * u, r = 8 * grp + c / NCH, i = i0w + r;
+        if (c < 8 * NCH && i < T)
+            *(half8v*)(out + (rowq + i) * a.ldo + h * DK + (c % NCH) * 8) = *(const half8v*)(stage + r * DK + (c % NCH) * 8);
     }
 }
 
@@ -318,16 +434,19 @@ __global__ __launch_bounds__(64) void relpos_attn_f32_kernel(AttnParams a, int d
 void launch_relpos_attention(Precision prec, const AttnParams& a, hipStream_t s) {
     require(a.T > 0 && a.B > 0 && a.H > 0, "attention: empty shape");
     if (prec == PREC_F16) {
-        // 32 queries (2 waves) per block: twice the blocks of a 64-query tiling
-        // and an LDS footprint that lets two blocks share a CU.
-        constexpr int NW = 4;
-        const dim3 grid(cdiv(a.T, 16 * NW), a.H, a.B);
+        // 64 queries per block, two key groups of four waves; sequences of at
+        // most 128 frames take a single step whose K and band arrive by DMA
+        const dim3 grid(cdiv(a.T, 64) * a.H * a.B);
+        const bool lng = a.T > 2 * AK;
         if (a.dk == 128) {
-            launch(relpos_attn_f16_kernel<128, NW>, grid, dim3(64 * NW), 0, s, a);
+            if (lng) launch(relpos_attn_ks_kernel<128, true>, grid, dim3(512), 0, s, a);
+            else launch(relpos_attn_ks_kernel<128, false>, grid, dim3(512), 0, s, a);
         } else if (a.dk == 64) {
-            launch(relpos_attn_f16_kernel<64, NW>, grid, dim3(64 * NW), 0, s, a);
+            if (lng) launch(relpos_attn_ks_kernel<64, true>, grid, dim3(512), 0, s, a);
+            else launch(relpos_attn_ks_kernel<64, false>, grid, dim3(512), 0, s, a);
         } else if (a.dk == 32) {
-            launch(relpos_attn_f16_kernel<32, NW>, grid, dim3(64 * NW), 0, s, a);
+            if (lng) launch(relpos_attn_ks_kernel<32, true>, grid, dim3(512), 0, s, a);
+            else launch(relpos_attn_ks_kernel<32, false>, grid, dim3(512), 0, s, a);
         } else {
             throw std::invalid_argument("attention(f16): head dim must be 32, 64 or 128");
         }

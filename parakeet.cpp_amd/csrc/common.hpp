@@ -104,6 +104,29 @@ __device__ __forceinline__ float group_sum(float v, int n) {
     if (n > 8) v += dpp_get<0x140>(v);   // row_mirror
     return v;
 }
+// XCD-aware block order: the hardware dispatches block b to XCD b % 8;
+// xcd_tile gives each XCD a contiguous range of work positions (a bijection
+// on [0, total)), so neighbouring work items share one XCD's L2.
+__device__ __forceinline__ int xcd_tile(int bid, int total) {
+    const int per = total / 8, rem = total % 8;
+    const int x = bid % 8, loc = bid / 8;
+    return x * per + (x < rem ? x : rem) + loc;
+}
+
+// Raw buffer resources: loads at offsets at or past num_records return zero,
+// so an offset pushed to OOB (or a negative one, read as unsigned) is a
+// zero fill with no branch.
+constexpr uint32_t OOB = 0x80000000u;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+    const int n = bytes > 0x7fffffff ? 0x7fffffff : (int)bytes;
+    return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, n, 0x00020000);
+}
+// Buffer load of 16 bytes per lane straight into LDS: lane L's data lands at
+// lds + 16 L; soff is wave-uniform.
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds, uint32_t voff, int soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
+}
+
 // Sum over a whole wave, every lane receiving it: DPP within each row of 16
 // lanes, then the four row sums read with v_readlane (no LDS round trips, as
 // the ds_bpermute steps of wave_sum take).  Every lane of the wave must be

@@ -11,14 +11,6 @@
 
 namespace pkx {
 
-// ---------------------------------------------------------------------------
-// XCD-aware tile order: hardware dispatches block b to XCD b % 8.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ int xcd_tile(int bid, int total) {
-    const int per = total / 8, rem = total % 8;
-    const int x = bid % 8, loc = bid / 8;
-    return x * per + (x < rem ? x : rem) + loc;
-}
 
 // Rows of each 64-wide K slab block of a slab-major (q8_0 / q4_K) weight (views
 // into a larger allocation keep the allocation's row count).
@@ -139,12 +131,6 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, float4v (&acc)[TM]
 // ===========================================================================
 constexpr int BK16 = 64;
 constexpr int LDK16 = BK16 + 8;   // +16 B row pad: 8 consecutive rows cover all banks
-constexpr uint32_t OOB = 0x80000000u;
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
-    const int n = bytes > 0x7fffffff ? 0x7fffffff : (int)bytes;
-    return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, n, 0x00020000);
-}
 __device__ __forceinline__ int4v bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
 }
@@ -482,11 +468,8 @@ struct DmaCfg {
     static_assert(A_BYTES % 4096 == 0 && B_BYTES % 1024 == 0, "tile must split into equal parts per wave");
 };
 
-// Buffer load of 16 (4) bytes per lane straight into LDS: lane L's data lands
-// at lds + 16 L (4 L); soff is wave-uniform.
-__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds, uint32_t voff, int soff) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
-}
+// Buffer load of 4 bytes per lane straight into LDS: lane L's data lands at
+// lds + 4 L; soff is wave-uniform (lds_dma16 in common.hpp moves 16 bytes).
 __device__ __forceinline__ void lds_dma4(__amdgpu_buffer_rsrc_t r, uint8_t* lds, uint32_t voff, int soff) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 4, voff, soff, 0, 0);
 }
