@@ -64,6 +64,41 @@ def test_subsampling(gpu, stream, name, mask_mode, T, valid_T):
     assert rel_l2(got[mask], ref[mask]) < _tol(prec)
 
 
+# F16 subsampling at the production channel count (a multiple of 64): conv0
+# runs on the matrix cores there (f16 mel and weights, f32 accumulation, the
+# conv0 map staged in f16), so it is checked on its own against the oracle.
+SUB_F16 = {
+    "128mel_c256": dict(d_model=256, n_heads=2, ff_dim=512, n_mels=128, sub_channels=256),
+    "80mel_c256": dict(d_model=256, n_heads=2, ff_dim=512, n_mels=80, sub_channels=256),
+    "80mel_c192": dict(d_model=256, n_heads=2, ff_dim=512, n_mels=80, sub_channels=192),
+}
+_SUB = {}
+
+
+@pytest.mark.parametrize("name", list(SUB_F16))
+@pytest.mark.parametrize("mask_mode", [0, 1])
+@pytest.mark.parametrize("T,valid_T", [(1000, [1000, 1000]), (333, [333, 200, 17]), (9, [9, 2])])
+def test_subsampling_f16_production_channels(gpu, stream, name, mask_mode, T, valid_T):
+    if name not in _SUB:
+        m = pm.synthesize(pm.Config(n_layers=1, conv_kernel=9, **SUB_F16[name]), "q8_0", heads=False, bn_random=True)
+        _SUB[name] = (m, oracle.OracleModel(m), gpu.Model.from_tensors(m, 1))
+    m, om, gm = _SUB[name]
+    B, F = len(valid_T), m.cfg.n_mels
+    mel = _mel(B, F, T, valid_T, T + 1)
+    print(f"[sub16] {name} mask={mask_mode} T={T} valid={valid_T}", flush=True)
+    ref, vo_ref = om.subsampling(mel, np.array(valid_T) - 1, stage_masks=(mask_mode == 0))
+    Tp = oracle.subsampled_len(T)
+    dm = gpu.DeviceArray.from_numpy(mel, stream)
+    dy = gpu.DeviceArray((B, Tp, m.cfg.d_model), np.float32)
+    tp, vo = gm.subsampling_forward(dm, valid_T, dy, mask_mode, stream)
+    got = dy.numpy(stream)
+    assert tp == Tp and list(vo) == list(vo_ref)
+    mask = np.arange(Tp)[None, :] < vo[:, None]
+    err = rel_l2(got[mask], ref[mask])
+    print(f"[sub16]   rel_l2 {err:.2e}", flush=True)
+    assert err < 1e-2
+
+
 @pytest.mark.parametrize("name", list(CASES))
 @pytest.mark.parametrize("T,valid_T", [(400, [400]), (320, [320, 201])])
 def test_encoder_per_layer(gpu, stream, name, T, valid_T):
