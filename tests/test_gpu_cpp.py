@@ -127,6 +127,44 @@ def _files_eou(tmp_path_factory, wtype):
     return _FILES[key]
 
 
+def _files_eou_offline(tmp_path_factory, wtype):
+    """The streaming model's offline baselines for Encoder::forward_capture:
+    the mel, the oracle's whole-sequence encoder output [d_model][T'] and the
+    layer 0 / mid / last captures [T'][d_model], at the forward path's entry
+    valid length T - 1 (src/encoder.cpp:30-95)."""
+    key = "eou_off_" + wtype
+    if key in _FILES:
+        return _FILES[key]
+    mp, _, _ = _files_eou(tmp_path_factory, wtype)
+    d = tmp_path_factory.mktemp(f"cpp_{key}")
+    cfg = pm.eou_config(d_model=256, n_layers=3, n_heads=4, ff_dim=512, n_mels=64, sub_channels=64)
+    m = pm.synthesize(cfg, wtype, heads=False, std=0.05)
+    om = oracle.OracleModel(m)
+    rng = np.random.default_rng(23)
+    T = 161
+    mel = rng.standard_normal((cfg.n_mels, T)).astype(np.float32)
+    off, _, cap = om.encoder(mel[None], valid_in=[T - 1], capture=True)
+    L = cfg.n_layers
+    bp = str(d / "baseline_eou_offline.gguf")
+    pm.write_baseline_gguf(bp, {"mel": mel, "encoder_out": np.ascontiguousarray(off[0].T),
+                                "enc_layer_0": cap[0][0], "enc_layer_mid": cap[L // 2][0],
+                                "enc_layer_last": cap[L - 1][0]})
+    _FILES[key] = (mp, bp)
+    return _FILES[key]
+
+
+@pytest.mark.parametrize("wtype", ["f32", "q8_0"])
+def test_cpp_encoder_eou(tmp_path_factory, wtype):
+    exe = os.path.join(BIN, "test_encoder_eou")
+    assert os.path.exists(exe), f"{exe} not built (make -C tests/cpp)"
+    mp, bp = _files_eou_offline(tmp_path_factory, wtype)
+    env = dict(os.environ, PARAKEET_TEST_GGUF_EOU=mp, PARAKEET_TEST_BASELINE_EOU=bp)
+    print(f"[cpp] test_encoder_eou {wtype}", flush=True)
+    r = subprocess.run([exe], env=env, capture_output=True, text=True, timeout=120)
+    print(r.stderr)
+    assert r.returncode == 0, r.stdout + r.stderr
+
+
 @pytest.mark.parametrize("wtype", ["f32", "q8_0"])
 def test_cpp_streaming_encoder(tmp_path_factory, wtype):
     exe = os.path.join(BIN, "test_streaming_encoder")
