@@ -1648,11 +1648,12 @@ static void dma_22q(int epi, const GemmParams& p, hipStream_t s) {
     default: dma_epi<2, 2, WT>(epi, p, s); break;
     }
 }
-// 128 x 64 tiles with two K groups (eight waves): long-K products whose grid is
-// about one tile per CU
+// 128 x 64 tiles with two K groups (eight waves): products of K >= 1024 whose
+// grid is about one tile per CU (FFN linear2 at K = 4096; attention out and
+// pw2 at K = 1024, where the split takes 0.3 - 0.9 us off a 14 - 15 us launch)
 template <int WT>
 static bool dma_kg2(int epi, const GemmParams& p, hipStream_t s) {
-    if (p.K % 128 != 0 || p.K < 2048 || (int64_t)cdiv(p.M, 128) * cdiv(p.N, 64) > 256) return false;
+    if (p.K % 128 != 0 || p.K < 1024 || (int64_t)cdiv(p.M, 128) * cdiv(p.N, 64) > 256) return false;
     if (WT != GT_F16 && p.M <= 512) {
         switch (epi) {
         case EPI_RESID: run_dma<1, 1, WT, EPI_RESID, DMA_NS, 2, 0>(p, s); return true;

@@ -96,7 +96,7 @@ def test_rel_pos_encoding(gpu, stream, T, D):
 
 @pytest.mark.parametrize("gtype", [pm.GGML_F16, pm.GGML_Q8_0, pm.GGML_Q4_K])
 @pytest.mark.parametrize("M,N,K", [(1000, 3072, 512), (2000, 4096, 256), (333, 2048, 1024), (129, 320, 1280),
-                                   (2000, 1024, 4096), (700, 1000, 2048)])
+                                   (2000, 1024, 4096), (700, 1000, 2048), (2000, 3072, 1024), (1900, 2880, 512)])
 def test_linear_tile_shapes(gpu, stream, gtype, M, N, K):
     """f16 path at shapes that select each MFMA tile (64x64, 128x64, 128x128,
     and 128x64 with two K groups for long K) and leave partial tiles on both
