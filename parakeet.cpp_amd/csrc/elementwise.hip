@@ -12,9 +12,10 @@ namespace pkx {
 // ---------------------------------------------------------------------------
 // gamma/beta are loaded by the caller before the row statistics are formed,
 // so their memory latency overlaps the reductions instead of following them.
+// Returns the row's {mean, rstd}.
 template <int NV>
-__device__ __forceinline__ void ln_row(float4v (&v)[NV], int lane, int D, const float4v (&gg)[NV],
-                                       const float4v (&bb)[NV], float eps) {
+__device__ __forceinline__ float2v ln_row(float4v (&v)[NV], int lane, int D, const float4v (&gg)[NV],
+                                          const float4v (&bb)[NV], float eps) {
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
@@ -40,6 +41,7 @@ __device__ __forceinline__ void ln_row(float4v (&v)[NV], int lane, int D, const 
     for (int i = 0; i < NV; ++i)
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[i][e] = (v[i][e] * rs) * gg[i][e] + bb[i][e];
+    return (float2v){mean, rs};
 }
 
 template <int NV>
@@ -59,21 +61,27 @@ template <> __device__ __forceinline__ void store4<f16>(f16* p, const float4v& v
 }
 
 // MODE 0: y = LN(x); MODE 1: y_f32 = LN(x), y = LN2(y_f32); MODE 2: y_f32 = LN(x);
-// MODE 3: y = silu(LN(x)).
+// MODE 3: y = silu(LN(x)); MODE 4: y = LN2(LN(x)) and LN's per-row {mean, rstd}
+// in rows, x unchanged (the consumer of LN(x) recomputes it from the two).
 template <int NV, typename OutT, int MODE>
 __global__ __launch_bounds__(256) void layernorm_kernel(LnParams p) {
+    constexpr bool TWO = MODE == 1 || MODE == 4;
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= p.M) return;
-    float4v v[NV], g1[NV], b1[NV], g2[MODE == 1 ? NV : 1], b2[MODE == 1 ? NV : 1];
+    float4v v[NV], g1[NV], b1[NV], g2[TWO ? NV : 1], b2[TWO ? NV : 1];
     ld_row4<NV>(v, p.x + row * p.D, lane, p.D);
     ld_row4<NV>(g1, p.g, lane, p.D);
     ld_row4<NV>(b1, p.b, lane, p.D);
-    if constexpr (MODE == 1) {
+    if constexpr (TWO) {
         ld_row4<NV>(g2, p.g2, lane, p.D);
         ld_row4<NV>(b2, p.b2, lane, p.D);
     }
-    ln_row<NV>(v, lane, p.D, g1, b1, p.eps);
+    const float2v st = ln_row<NV>(v, lane, p.D, g1, b1, p.eps);
+    if constexpr (MODE == 4) {
+        if (lane == 0) ((float2v*)p.rows)[row] = st;
+        ln_row<NV>(v, lane, p.D, g2, b2, p.eps);
+    }
     if constexpr (MODE == 1 || MODE == 2) {
         float* yr = p.y_f32 + row * p.D;
 #pragma unroll
@@ -107,6 +115,8 @@ static void ln_go(const LnParams& p, hipStream_t s) {
         launch((layernorm_kernel<NV, OutT, 1>), grid, dim3(256), 0, s, p);
     else if (p.y_f32)
         launch((layernorm_kernel<NV, OutT, 2>), grid, dim3(256), 0, s, p);
+    else if (p.rows)
+        launch((layernorm_kernel<NV, OutT, 4>), grid, dim3(256), 0, s, p);
     else
         launch((layernorm_kernel<NV, OutT, 0>), grid, dim3(256), 0, s, p);
 }
@@ -125,6 +135,8 @@ static void ln_nv(const LnParams& p, hipStream_t s) {
 void launch_layernorm(Precision prec, const LnParams& p, hipStream_t s) {
     require(p.D % 4 == 0, "layernorm: D must be a multiple of 4");
     require(!p.silu || (p.y && !p.y_f32), "layernorm: the SiLU output is the activation-type y only");
+    require(!p.rows || (p.y && !p.y_f32 && !p.silu && p.g2 && p.b2),
+            "layernorm: row statistics go with the two-LayerNorm activation output only");
     if (p.M == 0) return;
     if (prec == PREC_F16) ln_nv<f16>(p, s);
     else ln_nv<float>(p, s);

@@ -22,6 +22,9 @@ struct LnParams {
     int D = 0;
     float eps = 1e-5f;
     bool silu = false;   // y = silu(LN(x; g, b)): the conv module's LayerNorm conv norm (conformer.cpp:126-133, :157)
+    // with g2 / b2 and y (no y_f32): y = LN2(LN(x)) and LN's {mean, rstd} per
+    // row (float2 [M]); x is left as it is
+    float* rows = nullptr;
 };
 void launch_layernorm(Precision prec, const LnParams& p, hipStream_t s);
 

@@ -802,11 +802,12 @@ __device__ __forceinline__ void epilogue32_relu_tr(const GemmParams& p, float16v
 // Per-column epilogue constants of one wave's 32 NJ output columns (column
 // nw + 32 j + lane % 32 for block j): bias, folded-LayerNorm W*gamma, and for
 // the LayerNorm-statistics epilogue the gamma quad of the lane's copy-out
-// columns.  Loaded before the main loop so the epilogue does not wait for them.
+// columns (and the gamma / beta quads of a LayerNorm applied to the residual).
+// Loaded before the main loop so the epilogue does not wait for them.
 template <int NJ>
 struct EpiCols {
     float b[NJ], c1[NJ];
-    float4v g;
+    float4v g, rg, rb;
     __device__ __forceinline__ void load(const GemmParams& p, int nw, int lane, bool fold, bool gamma) {
         const int lc = lane & 31;
 #pragma unroll
@@ -815,10 +816,16 @@ struct EpiCols {
             b[j] = p.bias ? p.bias[n] : 0.f;
             c1[j] = fold ? p.fold_c1[n] : 0.f;
         }
-        g = (float4v){0.f, 0.f, 0.f, 0.f};
+        g = rg = rb = (float4v){0.f, 0.f, 0.f, 0.f};
         if (gamma) {
             const int n = nw + (lane % (8 * NJ)) * 4;   // the copy-out columns of RESID_LN
-            if (n < p.N) g = *(const float4v*)(p.ln_g + n);
+            if (n < p.N) {
+                g = *(const float4v*)(p.ln_g + n);
+                if (p.res_rows) {
+                    rg = *(const float4v*)(p.res_g + n);
+                    rb = *(const float4v*)(p.res_b + n);
+                }
+            }
         }
     }
 };
@@ -827,17 +834,22 @@ struct EpiCols {
 // registers before the main loop so that the residual epilogue does not wait
 // for them: chunk t of a lane is the float4 at row rr = (lane + 64 t) / CPR,
 // column 4 ((lane + 64 t) % CPR) of the wave tile (the epilogue's own order).
-template <int WR, int CPR>
+// RS: also the rows' {mean, rstd} of a LayerNorm applied to the residual.
+template <int WR, int CPR, bool RS = false>
 struct ResidPre {
     static constexpr int NT = WR * CPR / 64;
     static_assert(NT * 64 == WR * CPR, "whole chunks per lane");
     float4v v[NT];
+    float2v rs[RS ? NT : 1];
     __device__ __forceinline__ void load(const GemmParams& p, int mw, int nw, int lane) {
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             const int c = lane + 64 * t, m = mw + c / CPR, n = nw + (c % CPR) * 4;
             v[t] = m < p.M && n + 3 < p.N ? *(const float4v*)((const float*)p.Y + (int64_t)m * p.ldy + n)
                                           : (float4v){0.f, 0.f, 0.f, 0.f};
+            if constexpr (RS) {
+                if (p.res_rows) rs[t] = m < p.M ? ((const float2v*)p.res_rows)[m] : (float2v){0.f, 0.f};
+            }
         }
     }
 };
@@ -846,12 +858,13 @@ struct ResidPre {
 // folded LayerNorm, indexed from the tile's first row; trow0 is this wave's
 // first row within the tile.  (ftab is always a valid LDS address, so that its
 // loads stay LDS loads.)
-// xpre: the wave tile's residual values from ResidPre (RESID / RESID_LN), or null.
+// xpre: the wave tile's residual values from ResidPre (RESID / RESID_LN), or null;
+// xrs: with xpre, the rows' {mean, rstd} for a LayerNorm applied to the residual.
 template <int EPI, int TM, int TN>
 __device__ __forceinline__ void epilogue32_lds(const GemmParams& p, float16v (&acc)[TM][TN], float* wsm,
                                                int mw, int nw, int lane, const EpiCols<TN>& ec,
                                                bool fold = false, const float2v* ftab = nullptr, int trow0 = 0,
-                                               const float4v* xpre = nullptr) {
+                                               const float4v* xpre = nullptr, const float2v* xrs = nullptr) {
     constexpr int WR = 32 * TM;
     constexpr int WC = EPI == EPI_GLU ? 16 * TN : 32 * TN;   // output columns of this wave
     constexpr int LDW = WC + 4;
@@ -935,7 +948,13 @@ __device__ __forceinline__ void epilogue32_lds(const GemmParams& p, float16v (&a
             if (m < p.M && n < p.N) {   // uniform over the 8 lanes of a group (same row, N % 32 == 0)
                 const float4v v = *(const float4v*)(wsm + rr * LDW + cc);
                 float* dst = (float*)p.Y + (int64_t)m * p.ldy + n;
-                const float4v x = (xpre ? xpre[t] : *(const float4v*)dst) + v;
+                float4v x = xpre ? xpre[t] : *(const float4v*)dst;
+                if (p.res_rows) {   // the stream before a LayerNorm whose output was not stored
+                    const float2v rs = xrs ? xrs[t] : ((const float2v*)p.res_rows)[m];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) x[e] = ((x[e] - rs.x) * rs.y) * ec.rg[e] + ec.rb[e];
+                }
+                x += v;
                 *(float4v*)dst = x;
                 const half4v h = {(f16)(x[0] * g[0]), (f16)(x[1] * g[1]), (f16)(x[2] * g[2]), (f16)(x[3] * g[3])};
                 *(half4v*)((f16*)p.ln_h + (int64_t)m * p.N + n) = h;
@@ -1189,7 +1208,7 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
     constexpr int TAB = FOLD && KG == 1 ? C::BM * 8 : 0;
     constexpr bool whole = 4 * 32 * WTM * (32 * WTN + 4) * 4 + TAB <= KG * NS * C::STAGE;
     constexpr bool RPRE = (EPI == EPI_RESID || EPI == EPI_RESID_LN) && whole;
-    ResidPre<RPRE ? 32 * WTM : 64, RPRE ? 8 * WTN : 1> rpre;
+    ResidPre<RPRE ? 32 * WTM : 64, RPRE ? 8 * WTN : 1, EPI == EPI_RESID_LN && RPRE> rpre;
     if constexpr (RPRE) {
         if (kg == 0) rpre.load(p, m0 + wm * WTM * 32, n0 + wn * WTN * 32, lane);
     }
@@ -1282,7 +1301,8 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
             float* wsm = (float*)smem + wid * (32 * WTM) * ((EPI == EPI_GLU ? 16 * WTN : 32 * WTN) + 4);
             if (kg == 0)
                 epilogue32_lds<EPI, WTM, WTN>(p, acc, wsm, m0 + wm * WTM * 32, n0 + wn * WTN * 32, lane, ecol,
-                                              fold, ftab, wm * WTM * 32, RPRE ? rpre.v : nullptr);
+                                              fold, ftab, wm * WTM * 32, RPRE ? rpre.v : nullptr,
+                                              RPRE && EPI == EPI_RESID_LN && p.res_rows ? rpre.rs : nullptr);
         } else {
             constexpr int TH = WTM / 2;
             float* wsm = (float*)smem + wid * (32 * TH) * ((EPI == EPI_GLU ? 16 * WTN : 32 * WTN) + 4);
@@ -1719,6 +1739,9 @@ void launch_gemm(Precision prec, int wtype, int epi, const GemmParams& p, hipStr
     if (epi == EPI_RESID_LN)
         require(dma_ok && p.N % 32 == 0 && p.ln_g && p.ln_h && p.ln_stats,
                 "gemm: residual + LayerNorm statistics needs the f16 path, N % 32 == 0 and its outputs");
+    if (p.res_rows)
+        require(epi == EPI_RESID_LN && p.res_g && p.res_b,
+                "gemm: a LayerNorm on the residual goes with EPI_RESID_LN and needs its gamma and beta");
     if (p.fold_stats)
         require(dma_ok && p.fold_c1 && p.fold_groups >= 2 && p.fold_groups <= 32 &&
                     (p.fold_groups & (p.fold_groups - 1)) == 0 &&

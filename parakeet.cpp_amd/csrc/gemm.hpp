@@ -57,6 +57,13 @@ struct GemmParams {
     const float* ln_g = nullptr;   // [N] gamma of the next LayerNorm
     void* ln_h = nullptr;          // f16 [M][N]: R * gamma
     float* ln_stats = nullptr;     // float2 [M][N / 32]: {mean, sum of squared deviations}
+    // EPI_RESID_LN: the residual read is LN(R) rather than R, with R's per-row
+    // {mean, rstd} in res_rows (float2 [M]) and the LayerNorm's gamma / beta in
+    // res_g / res_b [N]: R holds the stream before a LayerNorm whose output was
+    // not stored, and the update writes the normalised stream plus the product
+    const float* res_rows = nullptr;
+    const float* res_g = nullptr;
+    const float* res_b = nullptr;
     // A LayerNorm folded into this product (EPI_STORE / SILU / GLU / GLU_DW):
     // A = x * gamma (f16, from EPI_RESID_LN) and
     //   y = rstd_m * (acc - mean_m * fold_c1[n]) + bias[n],

@@ -80,13 +80,14 @@ struct Model::Ws {
     Buf a2, a2p, a3, flat;              // subsampling maps
     Buf h, u, qkv, g, pe, p, xin, tmp;  // layer activations
     Buf lnst;                           // row statistics for the folded LayerNorms
+    Buf lnrows;                         // norm_out's per-row {mean, rstd} (not stored norm_out output)
     Buf logits, pp;                     // heads
     int* d_valid = nullptr;             // 4 x Bcap ints: v0, v1, v2, vout
     int* h_valid = nullptr;             // pinned staging
     int Bcap = 0;
     hipEvent_t staged = nullptr;
     ~Ws() {
-        for (Buf* b : {&a2, &a2p, &a3, &flat, &h, &u, &qkv, &g, &pe, &p, &xin, &tmp, &lnst, &logits, &pp})
+        for (Buf* b : {&a2, &a2p, &a3, &flat, &h, &u, &qkv, &g, &pe, &p, &xin, &tmp, &lnst, &lnrows, &logits, &pp})
             if (b->p) (void)hipFree(b->p);
         if (d_valid) (void)hipFree(d_valid);
         if (h_valid) (void)hipHostFree(h_valid);
@@ -761,9 +762,13 @@ void Model::gemm(const DevWeight& w, int epi, const void* A, int64_t lda, int64_
 }
 
 void Model::gemm_resid_ln(const DevWeight& w, const void* A, int64_t M, const float* bias, float* x, float alpha,
-                          const float* g, void* h, hipStream_t s, int fam) {
+                          const float* g, void* h, hipStream_t s, int fam, const float* res_rows,
+                          const float* res_g, const float* res_b) {
     grow(ws_->lnst, (size_t)M * (w.N / 32) * 8);
     GemmParams p;
+    p.res_rows = res_rows;
+    p.res_g = res_g;
+    p.res_b = res_b;
     p.A = A;
     p.lda = w.K;
     p.Wq = w.q;
@@ -1033,12 +1038,20 @@ void Model::layer_body(int l, float* x, int B, int T, const int* d_valid, bool f
     // epilogue.  Buffers: h and g alternate as LayerNorm / attention / conv
     // outputs so that no product writes what it reads.
     const bool fold = ln_fold_ && !conv_capture_;
+    // x may hold the previous block's stream before its norm_out (whose
+    // per-row statistics are staged): FFN1 linear2 then adds to norm_out(x)
+    const bool out_ln_in = first_ln_done && out_ln_pending_;
+    out_ln_pending_ = false;
     // Stage A: x += 0.5 * FFN1(LN(x))
     if (!first_ln_done) ln(L.ff1_ln_g, L.ff1_ln_b);
     gemm(L.ff1_w1, EPI_SILU, w.h.p, D, M, L.ff1_b1, w.u.p, c.ff_dim, 1.f, nullptr, 1, s, prec_, KF_GEMM_FFN);
     if (fold) {
-        gemm_resid_ln(L.ff1_w2, w.u.p, M, L.ff1_b2, x, 0.5f, L.att_ln_g, w.h.p, s, KF_GEMM_FFN);
+        const LayerDev* P = out_ln_in ? &layers_[l - 1] : nullptr;
+        gemm_resid_ln(L.ff1_w2, w.u.p, M, L.ff1_b2, x, 0.5f, L.att_ln_g, w.h.p, s, KF_GEMM_FFN,
+                      P ? (const float*)ws_->lnrows.p : nullptr, P ? P->out_ln_g : nullptr,
+                      P ? P->out_ln_b : nullptr);
     } else {
+        require(!out_ln_in, "norm_out left pending for a block that does not take it");
         gemm(L.ff1_w2, EPI_RESID, w.u.p, c.ff_dim, M, L.ff1_b2, x, D, 0.5f, nullptr, 1, s, prec_, KF_GEMM_FFN);
         ln(L.att_ln_g, L.att_ln_b);
     }
@@ -1118,6 +1131,16 @@ void Model::layer_body(int l, float* x, int B, int T, const int* d_valid, bool f
             p.g2 = layers_[l + 1].ff1_ln_g;
             p.b2 = layers_[l + 1].ff1_ln_b;
             p.y = w.h.p;
+            if (fold) {
+                // x keeps the stream before norm_out: the next block's FFN1
+                // linear2 (a residual + statistics product) applies norm_out
+                // from its per-row statistics as it adds, so the f32 stream is
+                // not written twice
+                grow(ws_->lnrows, (size_t)M * 8);
+                p.y_f32 = nullptr;
+                p.rows = (float*)ws_->lnrows.p;
+                out_ln_pending_ = true;
+            }
         }
         p.M = M;
         p.D = D;
@@ -1150,10 +1173,22 @@ void Model::encoder_kernels(const float* mel, int B, int T_max, int T3, bool sta
     if (pos_all)
         gemm(wpos_all_, EPI_STORE, ws_->pe.p, cfg_.d_model, 2 * (int64_t)T3 - 1, nullptr, ws_->p.p,
              (int64_t)L * cfg_.d_model, 1.f, nullptr, 1, s, prec_, KF_GEMM_POS);
+    out_ln_pending_ = false;
     for (int l = 0; l < L; ++l) {
         layer_body(l, out, B, T3, dvalid, l > 0, l + 1 < L, pos_all, s);
-        if (capture)
+        if (capture && out_ln_pending_) {
+            // the block's output is norm_out of what x holds
+            LnParams p;
+            p.x = out;
+            p.g = layers_[l].out_ln_g;
+            p.b = layers_[l].out_ln_b;
+            p.y_f32 = capture + (size_t)l * MD;
+            p.M = (int64_t)B * T3;
+            p.D = cfg_.d_model;
+            launch_layernorm(prec_, p, s);
+        } else if (capture) {
             PKX_HIP(hipMemcpyAsync(capture + (size_t)l * MD, out, MD * 4, hipMemcpyDeviceToDevice, s));
+        }
     }
 }
 
@@ -1176,6 +1211,7 @@ void Model::conformer_layer_forward(int layer, const float* x, int B, int T, con
     const size_t MD = (size_t)B * T * cfg_.d_model;
     if (out != x) PKX_HIP(hipMemcpyAsync(out, x, MD * 4, hipMemcpyDeviceToDevice, s));
     conv_capture_ = conv_out;
+    out_ln_pending_ = false;
     try {
         layer_body(layer, out, B, T, ws_->d_valid + 3 * ws_->Bcap, false, false, false, s);
     } catch (...) {

@@ -222,8 +222,11 @@ private:
               hipStream_t s, Precision prec, int fam, const float* bias2 = nullptr, int trF = 1);
     // residual product x += alpha * (A W^T + b) that also leaves, for the
     // LayerNorm (g) that follows, x * g in f16 (h) and the row statistics
+    // (res_rows: x holds the stream before a LayerNorm (res_g, res_b) whose
+    // output was not stored; the product adds to that LayerNorm's output)
     void gemm_resid_ln(const DevWeight& w, const void* A, int64_t M, const float* bias, float* x, float alpha,
-                       const float* g, void* h, hipStream_t s, int fam);
+                       const float* g, void* h, hipStream_t s, int fam, const float* res_rows = nullptr,
+                       const float* res_g = nullptr, const float* res_b = nullptr);
     // product of a LayerNorm folded in (A = x * gamma from gemm_resid_ln)
     GemmParams fold_params(const DevWeight& w, const void* A, int64_t M, const float* c1, const float* c2,
                            void* Y, int64_t ldy);
@@ -246,6 +249,9 @@ private:
     Precision prec_;
     bool finalized_ = false;
     bool ln_fold_ = false;   // f16 path: norm_self_att / norm_conv / norm_feed_forward2 folded into GEMMs
+    // layer_body left x before its norm_out, with that LayerNorm's per-row
+    // {mean, rstd} in the workspace (the next block's FFN1 linear2 applies it)
+    bool out_ln_pending_ = false;
     std::map<std::string, HostTensor> host_;
     std::vector<void*> allocs_;
     std::vector<LayerDev> layers_;

@@ -122,6 +122,57 @@ def test_encoder_per_layer(gpu, stream, name, T, valid_T):
     assert rel_l2(got[mask], ref[mask]) < _tol(prec)
 
 
+_STRONG = {}
+
+
+@pytest.mark.parametrize("name", ["q8_0", "f16", "q8_0_d512"])
+def test_encoder_strong_layernorms(gpu, stream, name):
+    """LayerNorm gains far from 1 and large shifts on norm_out and
+    norm_feed_forward1 (the fused norm_out + next-block LayerNorm pass), and a
+    feed_forward2 bias that puts each row's mean at several sigma before
+    norm_out: a dropped or misplaced gamma / beta term, or a cancellation in a
+    variance, shows in every layer's output.  The forward without capture
+    gives the same output bit for bit."""
+    if name not in _STRONG:
+        kw, wt = (dict(d_model=512, n_heads=4, ff_dim=1024, n_mels=80), "q8_0") if name == "q8_0_d512" \
+            else CASES[name][:2]
+        cfg = pm.Config(n_layers=4, conv_kernel=9, sub_channels=32, vocab_size=127, joint_hidden=64,
+                        pred_hidden=64, **kw)
+        m = pm.synthesize(cfg, wt, bn_random=True)
+        rng = np.random.default_rng(77)
+        D = cfg.d_model
+        for i in range(cfg.n_layers):
+            p = f"encoder.layers.{i}."
+            for nm in ("norm_out", "norm_feed_forward1"):
+                m.tensors[p + nm + ".weight"].data[:] = rng.uniform(0.4, 2.5, D)
+                m.tensors[p + nm + ".bias"].data[:] = rng.normal(0, 0.7, D)
+            m.tensors[p + "feed_forward2.linear2.bias"].data[:] = 8.0 + rng.normal(0, 0.3, D)
+        _STRONG[name] = (m, oracle.OracleModel(m), gpu.Model.from_tensors(m, 1))
+    m, om, gm = _STRONG[name]
+    T, valid_T = 320, [320, 201]
+    B, F, D, L = len(valid_T), m.cfg.n_mels, m.cfg.d_model, m.cfg.n_layers
+    mel = _mel(B, F, T, valid_T, 17)
+    print(f"[enc-strong] {name} T={T} valid={valid_T}", flush=True)
+    ref, vo_ref, cap_ref = om.encoder(mel, np.array(valid_T) - 1, capture=True)
+    Tp = oracle.subsampled_len(T)
+    dm = gpu.DeviceArray.from_numpy(mel, stream)
+    dy = gpu.DeviceArray((B, Tp, D), np.float32)
+    dcap = gpu.DeviceArray((L, B, Tp, D), np.float32)
+    tp, vo = gm.encoder_forward(dm, valid_T, dy, capture=dcap, stream=stream)
+    got, cap = dy.numpy(stream), dcap.numpy(stream)
+    assert tp == Tp and list(vo) == list(vo_ref)
+    mask = np.arange(Tp)[None, :] < vo[:, None]
+    for l in range(L):
+        err = rel_l2(cap[l][mask], cap_ref[l][mask])
+        print(f"  layer {l}: rel_l2 {err:.3e}")
+        assert err < 1e-2, (l, err)
+    # without capture the same forward (no extra LayerNorm passes) gives the same output
+    dy2 = gpu.DeviceArray((B, Tp, D), np.float32)
+    gm.encoder_forward(dm, valid_T, dy2, stream=stream)
+    assert np.array_equal(dy2.numpy(stream), got)
+    assert rel_l2(got[mask], ref[mask]) < 1e-2
+
+
 @pytest.mark.parametrize("name", ["f32", "q8_0"])
 def test_ctc_head(gpu, stream, name):
     m, om, gm, prec = _models(gpu, name)
