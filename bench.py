@@ -63,13 +63,16 @@ def layernorm_bytes(cfg, B, Tp, launches):
     stream and write f16; norm_out is fused with the next layer's
     norm_feed_forward1 (and also writes the f32 stream back), the last one f32
     only.  Folded (L + 1 launches): only layer 0's norm_feed_forward1 and the
-    norm_out passes remain."""
+    norm_out passes remain, and a norm_out fused with the next
+    norm_feed_forward1 reads the f32 stream and writes the f16 operand and the
+    per-row statistics (the next block's FFN1 linear2 applies norm_out)."""
     D, L, M = cfg.d_model, cfg.n_layers, B * Tp
     single = M * D * (4 + 2)
-    fused = M * D * (4 + 4 + 2)
     last = M * D * (4 + 4)
     if launches == L + 1:
+        fused = M * D * (4 + 2) + M * 8
         return (single + (L - 1) * fused + last) / launches
+    fused = M * D * (4 + 4 + 2)
     return ((3 * L + 1) * single + (L - 1) * fused + last) / launches
 
 
@@ -393,7 +396,8 @@ def main():
                                               "norm_feed_forward1; layer 0's norm_feed_forward1)",
                     "achieved": lnk.get("achieved"), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                     "frac": lnk.get("frac"), "traffic": None, "avg_us": lnk.get("avg_us"),
-                    "per_launch": "f32 residual read (+ f32 write back) + f16 normalised rows: %.1f MB average" % (
+                    "per_launch": "f32 residual read + f16 normalised rows (+ f32 write of the last norm_out, "
+                                  "per-row statistics of the others): %.1f MB average" % (
                         layernorm_bytes(cfg, B, Tp, cfg.n_layers + 1) / 1e6)}
 
     pcm_line = pcm_in(gm, cfg, stream, min(args.steps, 10))
