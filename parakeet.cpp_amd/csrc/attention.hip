@@ -145,12 +145,19 @@ __global__ __launch_bounds__(512, 1) void relpos_attn_ks_kernel(AttnParams a) {
     // buffer's end (negative rows wrap above it) and arrive as zeros.
     auto dma_kp = [&]() {
         const __amdgpu_buffer_rsrc_t rk = make_rsrc(k + rowq * a.ldk + h * DK, ((int64_t)(T - 1) * a.ldk + DK) * 2);
+        const __amdgpu_buffer_rsrc_t rv = make_rsrc(v + rowq * a.ldv + h * DK, ((int64_t)(T - 1) * a.ldv + DK) * 2);
         const __amdgpu_buffer_rsrc_t rp = make_rsrc(pp + h * DK, ((int64_t)(P - 1) * a.ldp + DK) * 2);
         const int rlo = T - 1 - (i0 + AQ - 1);
         constexpr int KI = KCH / 64, PI = PCH / 64;   // 1-KB instructions per array
         for (int ii = w; ii < KI; ii += 8) {
             const int o = ii * 1024 + 16 * lane, r = o / (DK * 2), t = (o % (DK * 2)) / 16;
             lds_dma16(rk, (uint8_t*)sm.k + ii * 1024, (uint32_t)((r * a.ldk + swz(r, t, NCH) * 8) * 2), 0);
+        }
+        // V in its own layout ([key][dim], swizzled like K); P.V reads it with
+        // transposing LDS loads
+        for (int ii = w; ii < KI; ii += 8) {
+            const int o = ii * 1024 + 16 * lane, r = o / (DK * 2), t = (o % (DK * 2)) / 16;
+            lds_dma16(rv, (uint8_t*)sm.vt + ii * 1024, (uint32_t)((r * a.ldv + swz(r, t, NCH) * 8) * 2), 0);
         }
         for (int ii = w; ii < PI; ii += 8) {
             const int o = ii * 1024 + 16 * lane, r = o / (DK * 2), t = (o % (DK * 2)) / 16;
@@ -160,25 +167,44 @@ __global__ __launch_bounds__(512, 1) void relpos_attn_ks_kernel(AttnParams a) {
     };
 
     // the query rows and position biases first: they return ahead of the
-    // staging loads issued next (vector memory returns in order)
+    // staging loads issued next (vector memory returns in order).  The head's
+    // biases [bias_u | bias_v] (2 DK floats) take one 16-byte load per lane
+    // and reach the lanes that add them through the wave's G scratch: the
+    // per-CU load path carries 1 KB per wave instead of 16.
+    constexpr int BL = DK / 4;   // lanes per bias vector
     half8v qx[NKC];
-    float4v bq[NKC][4];   // bias_u, bias_u, bias_v, bias_v halves of each fragment's 8 columns
+    float4v bl = {0.f, 0.f, 0.f, 0.f};
     {
         const int i = i0w + lc;
 #pragma unroll
         for (int kc = 0; kc < NKC; ++kc) {
             const int c0 = h * DK + 32 * kc + 8 * (lane >> 4);
             qx[kc] = i < T ? *(const half8v*)(q + (rowq + i) * a.ldq + c0) : (half8v){};
-            bq[kc][0] = *(const float4v*)(a.bias_u + c0);
-            bq[kc][1] = *(const float4v*)(a.bias_u + c0 + 4);
-            bq[kc][2] = *(const float4v*)(a.bias_v + c0);
-            bq[kc][3] = *(const float4v*)(a.bias_v + c0 + 4);
         }
+        if (lane < 2 * BL) bl = *(const float4v*)((lane < BL ? a.bias_u : a.bias_v) + h * DK + 4 * (lane % BL));
     }
     if (nit > 0) {
-        if constexpr (LONG) load_kp(0);
-        else dma_kp();
-        load_v(0);
+        if constexpr (LONG) {
+            load_kp(0);
+            load_v(0);
+        } else {
+            dma_kp();
+        }
+    }
+    float4v bq[NKC][4];   // bias_u, bias_u, bias_v, bias_v halves of each fragment's 8 columns
+    {
+        float4v* bs = (float4v*)sm.g[w];
+        if (lane < 2 * BL) bs[lane] = bl;
+        __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): the wave's bias writes are done
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int kc = 0; kc < NKC; ++kc) {
+            const int c4 = (32 * kc + 8 * (lane >> 4)) / 4;
+            bq[kc][0] = bs[c4];
+            bq[kc][1] = bs[c4 + 1];
+            bq[kc][2] = bs[BL + c4];
+            bq[kc][3] = bs[BL + c4 + 1];
+        }
     }
 
     // Query fragments (A operand of v_mfma_f32_16x16x32_f16): row lane%16,
@@ -209,17 +235,21 @@ __global__ __launch_bounds__(512, 1) void relpos_attn_ks_kernel(AttnParams a) {
     float* gw = sm.g[w];
     f16* probw = (f16*)gw;
     const f16* kt = sm.k + grp * AK * DK;
-    const f16* vtt = sm.vt + grp * DK * AK;
+    const f16* vtt = sm.vt + grp * DK * AK;   // V^T (long) or V (one step) of this group's keys
     const int pb = AQ - 16 - 16 * wq + AK * grp;   // this wave's first band row
 
     for (int s = 0; s < nit; ++s) {
-        if constexpr (LONG) store_kp();
-        store_v();
+        if constexpr (LONG) {
+            store_kp();
+            store_v();
+        }
         __builtin_amdgcn_s_waitcnt(0);   // this wave's DMAs have landed
         __syncthreads();
-        if (s + 1 < nit) {
-            if constexpr (LONG) load_kp(2 * AK * (s + 1));
-            load_v(2 * AK * (s + 1));
+        if constexpr (LONG) {
+            if (s + 1 < nit) {
+                load_kp(2 * AK * (s + 1));
+                load_v(2 * AK * (s + 1));
+            }
         }
         const int j0 = 2 * AK * s + AK * grp;
         if (j0 < vl) {
@@ -309,8 +339,27 @@ __global__ __launch_bounds__(512, 1) void relpos_attn_ks_kernel(AttnParams a) {
                 const half8v pf = *(const half8v*)(probw + lc * S::LDP + 32 * kc + 8 * (lane >> 4));
 #pragma unroll
                 for (int d = 0; d < NDT; ++d) {
-                    const int r = 16 * d + lc;
-                    const half8v vf = *(const half8v*)(vtt + r * AK + swz(r, 4 * kc + (lane >> 4), AK / 8) * 8);
+                    half8v vf;
+                    if constexpr (LONG) {
+                        const int r = 16 * d + lc;
+                        vf = *(const half8v*)(vtt + r * AK + swz(r, 4 * kc + (lane >> 4), AK / 8) * 8);
+                    } else {
+                        // B[key][dim] for keys 32 kc + 8 (lane / 16) + 0..7, dim 16 d + lane % 16:
+                        // in each 16-lane group, lane 4 j + q points at key j (and j + 4) and
+                        // dims 16 d + 4 q .. + 3; the transposing load hands lane i the
+                        // four keys' values of dim 16 d + i
+                        const int kr = 32 * kc + 8 * (lane >> 4) + (lc >> 2);
+                        const int dc = 16 * d + 4 * (lc & 3);             // first dim of the 8-byte piece
+                        const int r0 = kr, r1 = kr + 4;
+                        const f16* p0 = vtt + r0 * DK + swz(r0, dc / 8, NCH) * 8 + (dc & 7);
+                        const f16* p1 = vtt + r1 * DK + swz(r1, dc / 8, NCH) * 8 + (dc & 7);
+                        typedef __fp16 fp4 __attribute__((ext_vector_type(4)));
+                        const half4v v0 = __builtin_bit_cast(half4v, __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                                                                         (__attribute__((address_space(3))) fp4*)p0));
+                        const half4v v1 = __builtin_bit_cast(half4v, __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                                                                         (__attribute__((address_space(3))) fp4*)p1));
+                        vf = (half8v){v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+                    }
                     o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf, vf, o[d], 0, 0, 0);
                 }
             }
