@@ -10,7 +10,7 @@
 // 64-key tile the needed positional rows form one band of 79 rows, computed
 // as a 16x80 MFMA product into LDS and gathered along the diagonal.  Each
 // wave's G rows and probabilities are private to it, so only the shared
-// K / V^T / band staging needs block-wide barriers.
+// K / V / band staging needs block-wide barriers.
 #include "attention.hpp"
 
 #include <type_traits>
@@ -24,11 +24,11 @@ constexpr int AK = 64;   // keys per tile
 // take the even 64-key tiles, waves 4-7 the odd ones, each wave the same 16
 // query rows as its partner; the two online-softmax states are merged once at
 // the end.  A 64-query block therefore keeps two waves per SIMD busy, and a
-// short sequence (T' <= 128) costs each wave a single key tile.  K, the
-// positional band and V^T are staged for both tiles of a step at once; their
-// 16-byte chunks are XOR-swizzled within each 256-byte LDS line, so 16
-// consecutive rows read at one logical chunk hit 16 distinct bank quads
-// without row padding.
+// short sequence (T' <= 128) costs each wave a single key tile.  K, V and the
+// positional band are staged for both tiles of a step at once; their 16-byte
+// chunks are XOR-swizzled within each 256-byte LDS line, so 16 consecutive
+// rows read at one logical chunk hit 16 distinct bank quads without row
+// padding.  P.V reads V with transposing LDS loads (ds_read_b64_tr_b16).
 // ---------------------------------------------------------------------------
 template <int DK>
 struct KsSmem {
@@ -38,7 +38,7 @@ struct KsSmem {
     static constexpr int LDG = 84;                  // G row (floats): row groups 4 apart land 16 banks apart
     static constexpr int LDP = AK + 8;              // probability row (halves)
     f16 k[2 * AK * DK];       // [group][key][DK]
-    f16 vt[2 * DK * AK];      // [group][dim][key]
+    f16 vt[2 * AK * DK];      // V: [group][key][DK]
     f16 p[BROWS * DK];        // band rows of the step
     float g[8][16 * LDG];     // per wave: G, then its probabilities (f16)
 };
@@ -75,50 +75,20 @@ __global__ __launch_bounds__(512, 1) void relpos_attn_ks_kernel(AttnParams a) {
     const int64_t rowq = (int64_t)b * T;
     const int nit = (vl + 2 * AK - 1) / (2 * AK);   // steps of 128 keys (<= 1 unless LONG)
 
-    // V of a step: 8 x 8 blocks (8 keys x 8 dims) through registers, lanes
-    // along the dims so that 16 lanes read one whole row; transposed on the
-    // way into LDS (V^T rows are dims, keys contiguous)
-    constexpr int VCH = (2 * AK / 8) * NCH, VPT = (VCH + NT - 1) / NT;
-    half8v vreg[VPT][8];
-    auto load_v = [&](int jb) {
-#pragma unroll
-        for (int u = 0; u < VPT; ++u) {
-            const int c = tid + NT * u, kg = c / NCH, dg = c % NCH;
-            const f16* src = v + (rowq + jb + 8 * kg) * a.ldv + h * DK + 8 * dg;
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-                vreg[u][e] = (c < VCH && jb + 8 * kg + e < T) ? *(const half8v*)(src + (int64_t)e * a.ldv) : (half8v){};
-        }
-    };
-    auto store_v = [&]() {
-#pragma unroll
-        for (int u = 0; u < VPT; ++u) {
-            const int c = tid + NT * u, kg = c / NCH, dg = c % NCH;
-            const int g = kg / (AK / 8), kc8 = kg % (AK / 8);
-            if (c < VCH) {
-#pragma unroll
-                for (int d = 0; d < 8; ++d) {
-                    half8v col;
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) col[e] = vreg[u][e][d];
-                    const int row = 8 * dg + d;
-                    *(half8v*)(sm.vt + (g * DK + row) * AK + swz(row, kc8, AK / 8) * 8) = col;
-                }
-            }
-        }
-    };
-    // K and the positional band of a step through registers (long sequences:
-    // the next step's loads are in flight while this one is computed)
+    // K, V and the positional band of a step through registers (long
+    // sequences: the next step's loads are in flight while this one is
+    // computed); V keeps its own layout, P.V reads it with transposing loads
     constexpr int KCH = 2 * AK * NCH, PCH = S::BROWS * NCH;
     constexpr int KPT = LONG ? (KCH + NT - 1) / NT : 1, PPT = LONG ? (PCH + NT - 1) / NT : 1;
-    half8v kreg[KPT], preg[PPT];
+    half8v kreg[KPT], vreg[KPT], preg[PPT];
     auto load_kp = [&](int jb) {
         const int rlo = T - 1 - (i0 + AQ - 1) + jb;
 #pragma unroll
         for (int u = 0; u < KPT; ++u) {
             const int c = tid + NT * u, r = c / NCH, j = jb + r;
-            kreg[u] = (c < KCH && j < T) ? *(const half8v*)(k + (rowq + j) * a.ldk + h * DK + (c % NCH) * 8)
-                                         : (half8v){};
+            const bool in = c < KCH && j < T;
+            kreg[u] = in ? *(const half8v*)(k + (rowq + j) * a.ldk + h * DK + (c % NCH) * 8) : (half8v){};
+            vreg[u] = in ? *(const half8v*)(v + (rowq + j) * a.ldv + h * DK + (c % NCH) * 8) : (half8v){};
         }
 #pragma unroll
         for (int u = 0; u < PPT; ++u) {
@@ -131,7 +101,10 @@ __global__ __launch_bounds__(512, 1) void relpos_attn_ks_kernel(AttnParams a) {
 #pragma unroll
         for (int u = 0; u < KPT; ++u) {
             const int c = tid + NT * u, r = c / NCH;   // r: 0..127 = group * 64 + key
-            if (c < KCH) *(half8v*)(sm.k + r * DK + swz(r, c % NCH, NCH) * 8) = kreg[u];
+            if (c < KCH) {
+                *(half8v*)(sm.k + r * DK + swz(r, c % NCH, NCH) * 8) = kreg[u];
+                *(half8v*)(sm.vt + r * DK + swz(r, c % NCH, NCH) * 8) = vreg[u];
+            }
         }
 #pragma unroll
         for (int u = 0; u < PPT; ++u) {
@@ -184,12 +157,8 @@ __global__ __launch_bounds__(512, 1) void relpos_attn_ks_kernel(AttnParams a) {
         if (lane < 2 * BL) bl = *(const float4v*)((lane < BL ? a.bias_u : a.bias_v) + h * DK + 4 * (lane % BL));
     }
     if (nit > 0) {
-        if constexpr (LONG) {
-            load_kp(0);
-            load_v(0);
-        } else {
-            dma_kp();
-        }
+        if constexpr (LONG) load_kp(0);
+        else dma_kp();
     }
     float4v bq[NKC][4];   // bias_u, bias_u, bias_v, bias_v halves of each fragment's 8 columns
     {
@@ -235,21 +204,15 @@ __global__ __launch_bounds__(512, 1) void relpos_attn_ks_kernel(AttnParams a) {
     float* gw = sm.g[w];
     f16* probw = (f16*)gw;
     const f16* kt = sm.k + grp * AK * DK;
-    const f16* vtt = sm.vt + grp * DK * AK;   // V^T (long) or V (one step) of this group's keys
+    const f16* vtt = sm.vt + grp * DK * AK;   // V of this group's keys ([key][dim], swizzled)
     const int pb = AQ - 16 - 16 * wq + AK * grp;   // this wave's first band row
 
     for (int s = 0; s < nit; ++s) {
-        if constexpr (LONG) {
-            store_kp();
-            store_v();
-        }
+        if constexpr (LONG) store_kp();
         __builtin_amdgcn_s_waitcnt(0);   // this wave's DMAs have landed
         __syncthreads();
         if constexpr (LONG) {
-            if (s + 1 < nit) {
-                load_kp(2 * AK * (s + 1));
-                load_v(2 * AK * (s + 1));
-            }
+            if (s + 1 < nit) load_kp(2 * AK * (s + 1));
         }
         const int j0 = 2 * AK * s + AK * grp;
         if (j0 < vl) {
@@ -339,35 +302,29 @@ __global__ __launch_bounds__(512, 1) void relpos_attn_ks_kernel(AttnParams a) {
                 const half8v pf = *(const half8v*)(probw + lc * S::LDP + 32 * kc + 8 * (lane >> 4));
 #pragma unroll
                 for (int d = 0; d < NDT; ++d) {
-                    half8v vf;
-                    if constexpr (LONG) {
-                        const int r = 16 * d + lc;
-                        vf = *(const half8v*)(vtt + r * AK + swz(r, 4 * kc + (lane >> 4), AK / 8) * 8);
-                    } else {
-                        // B[key][dim] for keys 32 kc + 8 (lane / 16) + 0..7, dim 16 d + lane % 16:
-                        // in each 16-lane group, lane 4 j + q points at key j (and j + 4) and
-                        // dims 16 d + 4 q .. + 3; the transposing load hands lane i the
-                        // four keys' values of dim 16 d + i
-                        const int kr = 32 * kc + 8 * (lane >> 4) + (lc >> 2);
-                        const int dc = 16 * d + 4 * (lc & 3);             // first dim of the 8-byte piece
-                        const int r0 = kr, r1 = kr + 4;
-                        const f16* p0 = vtt + r0 * DK + swz(r0, dc / 8, NCH) * 8 + (dc & 7);
-                        const f16* p1 = vtt + r1 * DK + swz(r1, dc / 8, NCH) * 8 + (dc & 7);
-                        typedef __fp16 fp4 __attribute__((ext_vector_type(4)));
-                        const half4v v0 = __builtin_bit_cast(half4v, __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-                                                                         (__attribute__((address_space(3))) fp4*)p0));
-                        const half4v v1 = __builtin_bit_cast(half4v, __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-                                                                         (__attribute__((address_space(3))) fp4*)p1));
-                        vf = (half8v){v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-                    }
+                    // B[key][dim] for keys 32 kc + 8 (lane / 16) + 0..7, dim 16 d + lane % 16:
+                    // in each 16-lane group, lane 4 j + q points at key j (and j + 4) and
+                    // dims 16 d + 4 q .. + 3; the transposing load hands lane i the four
+                    // keys' values of dim 16 d + i
+                    const int kr = 32 * kc + 8 * (lane >> 4) + (lc >> 2);
+                    const int dc = 16 * d + 4 * (lc & 3);             // first dim of the 8-byte piece
+                    const int r0 = kr, r1 = kr + 4;
+                    const f16* p0 = vtt + r0 * DK + swz(r0, dc / 8, NCH) * 8 + (dc & 7);
+                    const f16* p1 = vtt + r1 * DK + swz(r1, dc / 8, NCH) * 8 + (dc & 7);
+                    typedef __fp16 fp4 __attribute__((ext_vector_type(4)));
+                    const half4v v0 = __builtin_bit_cast(half4v, __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                                                                     (__attribute__((address_space(3))) fp4*)p0));
+                    const half4v v1 = __builtin_bit_cast(half4v, __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                                                                     (__attribute__((address_space(3))) fp4*)p1));
+                    const half8v vf = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
                     o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf, vf, o[d], 0, 0, 0);
                 }
             }
         }
-        __syncthreads();   // the next step's staging overwrites K, V^T and the band
+        __syncthreads();   // the next step's staging overwrites K, V and the band
     }
 
-    // ---- merge the two key groups (K / V^T area reused): group 0 finishes
+    // ---- merge the two key groups (K / V area reused): group 0 finishes
     // rows r = 0, 1 of each lane's four, group 1 rows 2, 3; each hands the
     // other half of its state over ----
     constexpr int MR = NDT * 2 + 4;   // floats per lane handed over: o of two rows, m and l
