@@ -54,7 +54,6 @@ __global__ __launch_bounds__(512, 1) void relpos_attn_ks_kernel(AttnParams a) {
     constexpr int AQ = S::AQ, NCH = S::NCH, NT = 512, NKC = DK / 32, NDT = DK / 16;
     __shared__ __attribute__((aligned(16))) S sm;
     static_assert(sizeof(S) <= 160 * 1024, "LDS");
-    static_assert(8 * (NDT * 2 + 4) * 64 * 4 <= sizeof(sm.k) + sizeof(sm.vt), "merge area");
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int grp = w >> 2, wq = w & 3;
@@ -321,32 +320,50 @@ __global__ __launch_bounds__(512, 1) void relpos_attn_ks_kernel(AttnParams a) {
                 }
             }
         }
-        __syncthreads();   // the next step's staging overwrites K, V and the band
+        if (s + 1 < nit) __syncthreads();   // the next step's staging overwrites K, V and the band
     }
 
-    // ---- merge the two key groups (K / V area reused): group 0 finishes
-    // rows r = 0, 1 of each lane's four, group 1 rows 2, 3; each hands the
-    // other half of its state over ----
-    constexpr int MR = NDT * 2 + 4;   // floats per lane handed over: o of two rows, m and l
-    float* hand = (float*)sm.k + (grp * 4 + wq) * MR * 64 + lane;
-    const float* take = (float*)sm.k + ((1 - grp) * 4 + wq) * MR * 64 + lane;
-    f16* stage = (f16*)sm.g[wq];   // the 16 output rows of query block wq (f16, DK wide)
+    // ---- merge the two key groups: group 0 finishes rows r = 0, 1 of each
+    // lane's four, group 1 rows 2, 3.  Each wave leaves the other half of its
+    // state in its own G area (no other wave reads it: no barrier before),
+    // as 16-byte chunks [chunk][lane]; after one barrier it finishes its half
+    // from its partner's area and stages the output rows in the K area (free
+    // once every wave is past its products) ----
+    constexpr int MR4 = (NDT * 2 + 4) / 4;   // float4 per lane handed over: o of two rows, m and l
+    static_assert(MR4 * 64 * 16 <= sizeof(sm.g[0]) && 4 * 16 * DK * 2 <= sizeof(sm.k), "merge areas");
+    float4v* hand = (float4v*)sm.g[w] + lane;
+    const float4v* take = (const float4v*)sm.g[w ^ 4] + lane;   // the partner: same query rows, other keys
+    f16* stage = (f16*)sm.k + wq * 16 * DK;   // the 16 output rows of query block wq (f16, DK wide)
     auto give = [&](auto R) {
         constexpr int r0 = decltype(R)::value;
+        float x[MR4 * 4];
 #pragma unroll
-        for (int rr = 0; rr < 2; ++rr) {
-#pragma unroll
-            for (int d = 0; d < NDT; ++d) hand[(d * 2 + rr) * 64] = o[d][r0 + rr];
-            hand[(NDT * 2 + rr) * 64] = mrow[r0 + rr];
-            hand[(NDT * 2 + 2 + rr) * 64] = lrow[r0 + rr];
+        for (int d = 0; d < NDT; ++d) {
+            x[2 * d] = o[d][r0];
+            x[2 * d + 1] = o[d][r0 + 1];
         }
+        x[2 * NDT] = mrow[r0];
+        x[2 * NDT + 1] = mrow[r0 + 1];
+        x[2 * NDT + 2] = lrow[r0];
+        x[2 * NDT + 3] = lrow[r0 + 1];
+#pragma unroll
+        for (int c = 0; c < MR4; ++c) hand[c * 64] = (float4v){x[4 * c], x[4 * c + 1], x[4 * c + 2], x[4 * c + 3]};
     };
     auto keep = [&](auto R) {
         constexpr int r0 = decltype(R)::value;
+        float y[MR4 * 4];
+#pragma unroll
+        for (int c = 0; c < MR4; ++c) {
+            const float4v t = take[c * 64];
+            y[4 * c] = t[0];
+            y[4 * c + 1] = t[1];
+            y[4 * c + 2] = t[2];
+            y[4 * c + 3] = t[3];
+        }
 #pragma unroll
         for (int rr = 0; rr < 2; ++rr) {
             const int r = r0 + rr;
-            const float m1 = take[(NDT * 2 + rr) * 64], l1 = take[(NDT * 2 + 2 + rr) * 64];
+            const float m1 = y[2 * NDT + rr], l1 = y[2 * NDT + 2 + rr];
             const float m = fmaxf(mrow[r], m1);
             const float c0 = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mrow[r] - m);
             const float c1 = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - m);
@@ -355,7 +372,7 @@ __global__ __launch_bounds__(512, 1) void relpos_attn_ks_kernel(AttnParams a) {
             const float inv = (i < vl && l > 0.f) ? 1.0f / l : 0.f;   // padded query rows are zero
 #pragma unroll
             for (int d = 0; d < NDT; ++d)
-                stage[(lr + r) * DK + 16 * d + lc] = (f16)((o[d][r] * c0 + take[(d * 2 + rr) * 64] * c1) * inv);
+                stage[(lr + r) * DK + 16 * d + lc] = (f16)((o[d][r] * c0 + y[2 * d + rr] * c1) * inv);
         }
     };
     if (grp == 0) give(std::integral_constant<int, 2>{});
