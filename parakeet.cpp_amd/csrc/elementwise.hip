@@ -3,6 +3,8 @@
 // 16-byte (f32) / 8-byte (f16) vector accesses along the channel dim.
 #include "elementwise.hpp"
 
+#include <type_traits>
+
 namespace pkx {
 
 // ---------------------------------------------------------------------------
@@ -320,16 +322,24 @@ __global__ __launch_bounds__(256) void sub_stage1_kernel(const float* mel, const
                                                          const float* b2, T* out, int F, int Tn, int C, int T1,
                                                          int F1, int T2, int F2, int pl) {
     extern __shared__ float mp[];                 // [11][4 F2 + 5]: mel columns 2 - 3 pl .. 4 F2 + 4 - 3 pl
+    // f16 output: the mel tile is staged as f16 (rows of FPH halves, even so
+    // that column pairs are 4-byte aligned) and conv0 runs as packed f16
+    // products with f32 accumulation (v_dot2_f32_f16)
+    constexpr bool H = std::is_same<T, f16>::value;
     const int b = blockIdx.y, t2a = 2 * blockIdx.x;
-    const int FP = 4 * F2 + 5;
+    const int FP = 4 * F2 + 5, FPH = FP + 1;
+    f16* mh = (f16*)mp;
     const int v0 = valid0 ? valid0[b] : Tn;
     const int v1 = valid1 ? valid1[b] : T1;
+    // time fastest across the threads: mel is [B][F][T], so 11 consecutive
+    // threads read one feature's 44 contiguous bytes
     for (int idx = threadIdx.x; idx < 11 * FP; idx += blockDim.x) {
-        const int j = idx / FP, fi = idx % FP - (3 * pl - 2);
+        const int j = idx % 11, q = idx / 11, fi = q - (3 * pl - 2);
         const int t = 4 * t2a - 3 * pl + j;
         float v = 0.f;
         if (t >= 0 && t < Tn && t < v0 && fi >= 0 && fi < F) v = mel[((int64_t)b * F + fi) * Tn + t];
-        mp[idx] = v;
+        if constexpr (H) mh[j * FPH + q] = (f16)v;
+        else mp[j * FP + q] = v;
     }
     __syncthreads();
     bool rowok[5];
@@ -347,31 +357,64 @@ __global__ __launch_bounds__(256) void sub_stage1_kernel(const float* mel, const
             k2[e] = w2[c * 9 + e];
         }
         const float bc0 = b0[c], bc2 = b2[c];
+        // f16 taps: (kw 0, kw 1) of each row, (kh 0, kh 1) at kw 2, and kw 2 of kh 2
+        half2v w01[3], w2v;
+#pragma unroll
+        for (int kh = 0; kh < 3; ++kh) w01[kh] = (half2v){(f16)k0[kh * 3], (f16)k0[kh * 3 + 1]};
+        w2v = (half2v){(f16)k0[2], (f16)k0[5]};
+        const float w22 = (float)(f16)k0[8];
         float prev[5];
 #pragma unroll
         for (int r = 0; r < 5; ++r) prev[r] = 0.f;    // conv0 column f1 = -pl is padding
         for (int f2 = 0; f2 < F2; ++f2) {
             // mel columns 4 f2 + 2 - 3 pl .. 4 f2 + 6 - 3 pl (LDS columns 4 f2 .. 4 f2 + 4)
-            float m[11][5];
-#pragma unroll
-            for (int j = 0; j < 11; ++j)
-#pragma unroll
-                for (int q = 0; q < 5; ++q) m[j][q] = mp[j * FP + 4 * f2 + q];
             float ca[5], cb[5];                       // conv0 columns f1 = 2 f2 - pl + 1, 2 f2 - pl + 2
             const int f1a = 2 * f2 - pl + 1;
             const bool fa = f1a >= 0 && f1a < F1, fb = f1a + 1 >= 0 && f1a + 1 < F1;
+            if constexpr (H) {
+                half2v p01[11], p23[11];
+                f16 m4[11];
 #pragma unroll
-            for (int r = 0; r < 5; ++r) {
-                float sa = bc0, sb = bc0;
+                for (int j = 0; j < 11; ++j) {
+                    const f16* row = mh + j * FPH + 4 * f2;
+                    p01[j] = *(const half2v*)row;
+                    p23[j] = *(const half2v*)(row + 2);
+                    m4[j] = row[4];
+                }
 #pragma unroll
-                for (int kh = 0; kh < 3; ++kh)
+                for (int r = 0; r < 5; ++r) {
+                    float sa = bc0, sb = bc0;
 #pragma unroll
-                    for (int kw = 0; kw < 3; ++kw) {
-                        sa += k0[kh * 3 + kw] * m[2 * r + kh][kw];
-                        sb += k0[kh * 3 + kw] * m[2 * r + kh][2 + kw];
+                    for (int kh = 0; kh < 3; ++kh) {
+                        sa = __builtin_amdgcn_fdot2(p01[2 * r + kh], w01[kh], sa, false);
+                        sb = __builtin_amdgcn_fdot2(p23[2 * r + kh], w01[kh], sb, false);
                     }
-                ca[r] = (rowok[r] && fa && sa > 0.f) ? sa : 0.f;
-                cb[r] = (rowok[r] && fb && sb > 0.f) ? sb : 0.f;
+                    sa = __builtin_amdgcn_fdot2((half2v){p23[2 * r][0], p23[2 * r + 1][0]}, w2v, sa, false);
+                    sb = __builtin_amdgcn_fdot2((half2v){m4[2 * r], m4[2 * r + 1]}, w2v, sb, false);
+                    sa += w22 * (float)p23[2 * r + 2][0];
+                    sb += w22 * (float)m4[2 * r + 2];
+                    ca[r] = (rowok[r] && fa && sa > 0.f) ? sa : 0.f;
+                    cb[r] = (rowok[r] && fb && sb > 0.f) ? sb : 0.f;
+                }
+            } else {
+                float m[11][5];
+#pragma unroll
+                for (int j = 0; j < 11; ++j)
+#pragma unroll
+                    for (int q = 0; q < 5; ++q) m[j][q] = mp[j * FP + 4 * f2 + q];
+#pragma unroll
+                for (int r = 0; r < 5; ++r) {
+                    float sa = bc0, sb = bc0;
+#pragma unroll
+                    for (int kh = 0; kh < 3; ++kh)
+#pragma unroll
+                        for (int kw = 0; kw < 3; ++kw) {
+                            sa += k0[kh * 3 + kw] * m[2 * r + kh][kw];
+                            sb += k0[kh * 3 + kw] * m[2 * r + kh][2 + kw];
+                        }
+                    ca[r] = (rowok[r] && fa && sa > 0.f) ? sa : 0.f;
+                    cb[r] = (rowok[r] && fb && sb > 0.f) ? sb : 0.f;
+                }
             }
             float oa = bc2, ob = bc2;
 #pragma unroll
@@ -395,7 +438,9 @@ void launch_sub_stage1(Precision prec, const float* mel, const int* valid0, cons
     const int pl = causal ? 2 : 1;
     const dim3 grid(cdiv(T2, 2), B);
     const int bs = C >= 256 ? 256 : ((C + 63) / 64) * 64;
-    const uint32_t shm = 11u * (uint32_t)(4 * F2 + 5) * 4u;   // 4 F2 + 5 >= F + 2 covers the zero padding
+    // 4 F2 + 5 >= F + 2 covers the zero padding; f32 tile [11][FP] (the f16
+    // tile [11][FP + 1] fits in it)
+    const uint32_t shm = 11u * (uint32_t)(4 * F2 + 5) * 4u;
     if (prec == PREC_F16)
         launch(sub_stage1_kernel<f16>, grid, dim3(bs), shm, s, mel, valid0, valid1, w0, b0, w2, b2, (f16*)out, F, T,
                C, T1, F1, T2, F2, pl);
