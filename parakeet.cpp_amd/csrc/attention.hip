@@ -8,9 +8,9 @@
 // keys are streamed in tiles of 64 with an online softmax, and the shifted
 // term uses the identity bd_shift[i][j] = bd[i][T-1-i+j]: for a 16-query x
 // 64-key tile the needed positional rows form one band of 79 rows, computed
-// as a 16x80 MFMA product into LDS and gathered along the diagonal.  Each
-// wave's G rows and probabilities are private to it, so only the shared
-// K / V / band staging needs block-wide barriers.
+// as an 80x16 MFMA product into LDS and gathered along the diagonal.  Each
+// wave's G area is private to it, so only the shared K / V / band staging
+// needs block-wide barriers.
 #include "attention.hpp"
 
 #include <type_traits>
@@ -24,28 +24,49 @@ constexpr int AK = 64;   // keys per tile
 // take the even 64-key tiles, waves 4-7 the odd ones, each wave the same 16
 // query rows as its partner; the two online-softmax states are merged once at
 // the end.  A 64-query block therefore keeps two waves per SIMD busy, and a
-// short sequence (T' <= 128) costs each wave a single key tile.  K, V and the
+// short sequence (T' <= 128) costs each wave a single key tile.  The products
+// are formed transposed (keys x queries, dims x queries): each lane holds
+// the scores of one query, so the softmax reduces over its own registers and
+// the three other lanes of that query, and its probabilities are already the
+// B operand of O^T = V^T . P^T, with no pass through LDS.  K, V and the
 // positional band are staged for both tiles of a step at once; their 16-byte
 // chunks are XOR-swizzled within each 256-byte LDS line, so 16 consecutive
 // rows read at one logical chunk hit 16 distinct bank quads without row
-// padding.  P.V reads V with transposing LDS loads (ds_read_b64_tr_b16).
+// padding.  V^T fragments come from V with transposing LDS loads
+// (ds_read_b64_tr_b16).
 // ---------------------------------------------------------------------------
 template <int DK>
 struct KsSmem {
     static constexpr int AQ = 64;                   // queries per block
     static constexpr int NCH = DK / 8;              // 16-byte chunks per K / band row
     static constexpr int BROWS = AQ + 2 * AK;       // band rows per step (AQ + 2 AK - 1 used)
-    static constexpr int LDG = 84;                  // G row (floats): row groups 4 apart land 16 banks apart
-    static constexpr int LDP = AK + 8;              // probability row (halves)
-    f16 k[2 * AK * DK];       // [group][key][DK]
-    f16 vt[2 * AK * DK];      // V: [group][key][DK]
-    f16 p[BROWS * DK];        // band rows of the step
-    float g[8][16 * LDG];     // per wave: G, then its probabilities (f16)
+    static constexpr int KI = 2 * AK * NCH / 64;    // 1-KB DMA instructions for K (and for V)
+    static constexpr int PI = (BROWS * NCH / 64 + 7) / 8 * 8;   // for the band, rounded to the 8 waves
+    static constexpr int LDG = 84;                  // G^T row (floats)
+    f16 k[2 * AK * DK];       // K: [group][key][DK]
+    f16 vs[2 * AK * DK];      // V: [group][key][DK]
+    f16 p[PI * 512];          // band rows of the step (rows past BROWS unused)
+    float g[8][16 * LDG];     // per wave: G^T as [query][band row]
 };
 
 // stored position of logical 16-byte chunk c in row r of a swizzled array
 // with nch chunks per row (rows shorter than 256 bytes share an LDS line)
 __device__ __forceinline__ int swz(int r, int c, int nch) { return c ^ ((r / (16 / nch)) % nch); }
+
+// max / sum over the four 16-lane groups of a wave (lanes l, l^16, l^32, l^48);
+// every lane of the four gets the same value
+__device__ __forceinline__ float xg_max(float x) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float xg_sum(float x) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
 
 template <int DK, bool LONG>
 __global__ __launch_bounds__(512, 1) void relpos_attn_ks_kernel(AttnParams a) {
@@ -54,8 +75,10 @@ __global__ __launch_bounds__(512, 1) void relpos_attn_ks_kernel(AttnParams a) {
     constexpr int AQ = S::AQ, NCH = S::NCH, NT = 512, NKC = DK / 32, NDT = DK / 16;
     __shared__ __attribute__((aligned(16))) S sm;
     static_assert(sizeof(S) <= 160 * 1024, "LDS");
+    static_assert(S::KI % 8 == 0 && S::PI % 8 == 0, "DMA instructions split evenly over the waves");
 
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int grp = w >> 2, wq = w & 3;
     const int T = a.T, P = 2 * T - 1;
     // work order (head, item, query block), query block fastest, each XCD a
@@ -66,7 +89,7 @@ __global__ __launch_bounds__(512, 1) void relpos_attn_ks_kernel(AttnParams a) {
     const int b = (wid / nq) % a.B, h = wid / (nq * a.B), i0 = (wid % nq) * AQ;
     const int vl = a.valid ? a.valid[b] : T;
     const int i0w = i0 + 16 * wq;
-    const int lr = 4 * (lane >> 4), lc = lane & 15;
+    const int lg = lane >> 4, lc = lane & 15;   // lane group; lane in group = this lane's query
     const f16* q = (const f16*)a.q;
     const f16* k = (const f16*)a.k;
     const f16* v = (const f16*)a.v;
@@ -76,7 +99,7 @@ __global__ __launch_bounds__(512, 1) void relpos_attn_ks_kernel(AttnParams a) {
 
     // K, V and the positional band of a step through registers (long
     // sequences: the next step's loads are in flight while this one is
-    // computed); V keeps its own layout, P.V reads it with transposing loads
+    // computed)
     constexpr int KCH = 2 * AK * NCH, PCH = S::BROWS * NCH;
     constexpr int KPT = LONG ? (KCH + NT - 1) / NT : 1, PPT = LONG ? (PCH + NT - 1) / NT : 1;
     half8v kreg[KPT], vreg[KPT], preg[PPT];
@@ -102,7 +125,7 @@ __global__ __launch_bounds__(512, 1) void relpos_attn_ks_kernel(AttnParams a) {
             const int c = tid + NT * u, r = c / NCH;   // r: 0..127 = group * 64 + key
             if (c < KCH) {
                 *(half8v*)(sm.k + r * DK + swz(r, c % NCH, NCH) * 8) = kreg[u];
-                *(half8v*)(sm.vt + r * DK + swz(r, c % NCH, NCH) * 8) = vreg[u];
+                *(half8v*)(sm.vs + r * DK + swz(r, c % NCH, NCH) * 8) = vreg[u];
             }
         }
 #pragma unroll
@@ -111,30 +134,18 @@ __global__ __launch_bounds__(512, 1) void relpos_attn_ks_kernel(AttnParams a) {
             if (c < PCH) *(half8v*)(sm.p + r * DK + swz(r, c % NCH, NCH) * 8) = preg[u];
         }
     };
-    // A single step (T' <= 128): K and the band go straight into LDS by DMA,
-    // 16 bytes per lane, the swizzle applied through each lane's source
-    // chunk; rows past T' or outside the band's 2T'-1 positions read past the
-    // buffer's end (negative rows wrap above it) and arrive as zeros.
-    auto dma_kp = [&]() {
-        const __amdgpu_buffer_rsrc_t rk = make_rsrc(k + rowq * a.ldk + h * DK, ((int64_t)(T - 1) * a.ldk + DK) * 2);
-        const __amdgpu_buffer_rsrc_t rv = make_rsrc(v + rowq * a.ldv + h * DK, ((int64_t)(T - 1) * a.ldv + DK) * 2);
-        const __amdgpu_buffer_rsrc_t rp = make_rsrc(pp + h * DK, ((int64_t)(P - 1) * a.ldp + DK) * 2);
-        const int rlo = T - 1 - (i0 + AQ - 1);
-        constexpr int KI = KCH / 64, PI = PCH / 64;   // 1-KB instructions per array
-        for (int ii = w; ii < KI; ii += 8) {
-            const int o = ii * 1024 + 16 * lane, r = o / (DK * 2), t = (o % (DK * 2)) / 16;
-            lds_dma16(rk, (uint8_t*)sm.k + ii * 1024, (uint32_t)((r * a.ldk + swz(r, t, NCH) * 8) * 2), 0);
-        }
-        // V in its own layout ([key][dim], swizzled like K); P.V reads it with
-        // transposing LDS loads
-        for (int ii = w; ii < KI; ii += 8) {
-            const int o = ii * 1024 + 16 * lane, r = o / (DK * 2), t = (o % (DK * 2)) / 16;
-            lds_dma16(rv, (uint8_t*)sm.vt + ii * 1024, (uint32_t)((r * a.ldv + swz(r, t, NCH) * 8) * 2), 0);
-        }
-        for (int ii = w; ii < PI; ii += 8) {
-            const int o = ii * 1024 + 16 * lane, r = o / (DK * 2), t = (o % (DK * 2)) / 16;
-            const int64_t off = ((int64_t)(rlo + r) * a.ldp + swz(r, t, NCH) * 8) * 2;
-            lds_dma16(rp, (uint8_t*)sm.p + ii * 1024, off < 0 ? OOB : (uint32_t)off, 0);
+    // A single step (T' <= 128): K, the band and V go straight into LDS by
+    // DMA, 16 bytes per lane, the swizzle applied through each lane's source
+    // chunk, the same number of instructions from every wave; rows past T' or
+    // outside the band's 2T'-1 positions read past the buffer's end (negative
+    // rows wrap above it) and arrive as zeros.
+    constexpr int KPW = S::KI / 8, PPW = S::PI / 8;   // DMA instructions per wave
+    auto dma_rows = [&](__amdgpu_buffer_rsrc_t r, f16* dst, int64_t ld, int row0, int per_wave) {
+        for (int u = 0; u < per_wave; ++u) {
+            const int ii = w + 8 * u;
+            const int o = ii * 1024 + 16 * lane, rr = o / (DK * 2), t = (o % (DK * 2)) / 16;
+            const int64_t off = ((int64_t)(row0 + rr) * ld + swz(rr, t, NCH) * 8) * 2;
+            lds_dma16(r, (uint8_t*)dst + ii * 1024, off < 0 ? OOB : (uint32_t)off, 0);
         }
     };
 
@@ -150,14 +161,22 @@ __global__ __launch_bounds__(512, 1) void relpos_attn_ks_kernel(AttnParams a) {
         const int i = i0w + lc;
 #pragma unroll
         for (int kc = 0; kc < NKC; ++kc) {
-            const int c0 = h * DK + 32 * kc + 8 * (lane >> 4);
+            const int c0 = h * DK + 32 * kc + 8 * lg;
             qx[kc] = i < T ? *(const half8v*)(q + (rowq + i) * a.ldq + c0) : (half8v){};
         }
         if (lane < 2 * BL) bl = *(const float4v*)((lane < BL ? a.bias_u : a.bias_v) + h * DK + 4 * (lane % BL));
     }
-    if (nit > 0) {
-        if constexpr (LONG) load_kp(0);
-        else dma_kp();
+    __builtin_amdgcn_sched_barrier(0);   // these loads stay ahead of the staging
+    // issued whatever the item's length (an item with no valid frame still
+    // waits for them below), so that the waits in between count a fixed
+    // number of younger loads
+    if constexpr (LONG) {
+        load_kp(0);
+    } else {
+        // K and the band now, V once K has landed
+        dma_rows(make_rsrc(k + rowq * a.ldk + h * DK, ((int64_t)(T - 1) * a.ldk + DK) * 2), sm.k, a.ldk, 0, KPW);
+        dma_rows(make_rsrc(pp + h * DK, ((int64_t)(P - 1) * a.ldp + DK) * 2), sm.p, a.ldp, T - 1 - (i0 + AQ - 1),
+                 PPW);
     }
     float4v bq[NKC][4];   // bias_u, bias_u, bias_v, bias_v halves of each fragment's 8 columns
     {
@@ -167,7 +186,7 @@ __global__ __launch_bounds__(512, 1) void relpos_attn_ks_kernel(AttnParams a) {
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
         for (int kc = 0; kc < NKC; ++kc) {
-            const int c4 = (32 * kc + 8 * (lane >> 4)) / 4;
+            const int c4 = (32 * kc + 8 * lg) / 4;
             bq[kc][0] = bs[c4];
             bq[kc][1] = bs[c4 + 1];
             bq[kc][2] = bs[BL + c4];
@@ -175,7 +194,7 @@ __global__ __launch_bounds__(512, 1) void relpos_attn_ks_kernel(AttnParams a) {
         }
     }
 
-    // Query fragments (A operand of v_mfma_f32_16x16x32_f16): row lane%16,
+    // Query fragments (B operand of v_mfma_f32_16x16x32_f16): query lane%16,
     // k = 32*kc + 8*(lane/16) + [0..7].  pos_bias_u/v added in f32.
     half8v qu[NKC], qv[NKC];
 #pragma unroll
@@ -188,169 +207,187 @@ __global__ __launch_bounds__(512, 1) void relpos_attn_ks_kernel(AttnParams a) {
         }
     // scores in log2 units: exp(scale * x) = exp2(scale * log2(e) * x)
     const float sl2 = a.scale * 1.4426950408889634f;
-    // chunk of each of this lane's query rows (chunked-limited window)
-    int qch[4] = {0, 0, 0, 0};
+    // the keys this lane's query sees: [jlo, jhi), the valid frames and, with
+    // a chunked-limited window, the chunks qc - left_chunks .. qc of the
+    // query's chunk qc (j / chunk in that range <=> j in the interval)
+    int jlo = 0, jhi = vl;
     if (a.chunk > 0) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) qch[r] = (i0w + lr + r) / a.chunk;
+        const int qc = (i0w + lc) / a.chunk;
+        jlo = max(0, (qc - a.left_chunks) * a.chunk);
+        jhi = min(vl, (qc + 1) * a.chunk);
     }
 
+    // O^T fragments: o[d][r] = output of query lane%16, dim 16 d + 4 (lane/16) + r
     float4v o[NDT];
 #pragma unroll
     for (int d = 0; d < NDT; ++d) o[d] = (float4v){0.f, 0.f, 0.f, 0.f};
-    float mrow[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-    float lrow[4] = {0.f, 0.f, 0.f, 0.f};
+    float mrow = -INFINITY;   // running max of this lane's query (the same in its four lanes)
+    float lrow = 0.f;         // this lane's part of the running denominator (its 16 keys per tile)
     float* gw = sm.g[w];
-    f16* probw = (f16*)gw;
     const f16* kt = sm.k + grp * AK * DK;
-    const f16* vtt = sm.vt + grp * DK * AK;   // V of this group's keys ([key][dim], swizzled)
+    const f16* vst = sm.vs + grp * AK * DK;         // V of this group's keys ([key][dim], swizzled)
     const int pb = AQ - 16 - 16 * wq + AK * grp;   // this wave's first band row
+    float4v sac[4];    // S^T: sac[jt][r] = score of this lane's query, key 16 jt + 4 (lane/16) + r
+    half4v pr[4];      // its probabilities
 
-    for (int s = 0; s < nit; ++s) {
-        if constexpr (LONG) store_kp();
-        __builtin_amdgcn_s_waitcnt(0);   // this wave's DMAs have landed
-        __syncthreads();
-        if constexpr (LONG) {
-            if (s + 1 < nit) load_kp(2 * AK * (s + 1));
+    // ---- S^T = k . qu^T : 64 x 16 ----
+    auto qk = [&]() {
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt) {
+            sac[jt] = (float4v){0.f, 0.f, 0.f, 0.f};
+            const int r = 16 * jt + lc;
+#pragma unroll
+            for (int kc = 0; kc < NKC; ++kc) {
+                const half8v kf = *(const half8v*)(kt + r * DK + swz(r, 4 * kc + lg, NCH) * 8);
+                sac[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qu[kc], sac[jt], 0, 0, 0);
+            }
         }
-        const int j0 = 2 * AK * s + AK * grp;
-        if (j0 < vl) {
-            // ---- ac = qu . k^T : 16 x 64 ----
-            float4v sac[4];
+    };
+    // ---- band product G^T = p_band . qv^T : 80 x 16, into the wave's G area
+    // as [query][band row] (one 16-byte write per lane and 16-row block) ----
+    auto band = [&]() {
 #pragma unroll
-            for (int jt = 0; jt < 4; ++jt) {
-                sac[jt] = (float4v){0.f, 0.f, 0.f, 0.f};
-                const int r = 16 * jt + lc;
+        for (int gt = 0; gt < 5; ++gt) {
+            float4v g = {0.f, 0.f, 0.f, 0.f};
+            const int r = pb + 16 * gt + lc;
 #pragma unroll
-                for (int kc = 0; kc < NKC; ++kc) {
-                    const half8v kf = *(const half8v*)(kt + r * DK + swz(r, 4 * kc + (lane >> 4), NCH) * 8);
-                    sac[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qu[kc], kf, sac[jt], 0, 0, 0);
-                }
+            for (int kc = 0; kc < NKC; ++kc) {
+                const half8v pf = *(const half8v*)(sm.p + r * DK + swz(r, 4 * kc + lg, NCH) * 8);
+                g = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf, qv[kc], g, 0, 0, 0);
             }
-            // ---- band product G = qv . p_band^T : 16 x 80 ----
+            *(float4v*)(gw + lc * S::LDG + 16 * gt + 4 * lg) = g;
+        }
+        // the wave reads back only its own G area
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        __builtin_amdgcn_wave_barrier();
+    };
+    // ---- scores (rel_shift gather bd[i][j] = G[i][15 - i + j]), masks, online softmax ----
+    auto softmax = [&](int s, int j0) {
+        float sc[4][4];
+        float tmax = -INFINITY;
+        const float* grow = gw + lc * S::LDG + 15 - lc + 4 * lg;
 #pragma unroll
-            for (int gt = 0; gt < 5; ++gt) {
-                float4v g = {0.f, 0.f, 0.f, 0.f};
-                const int r = pb + 16 * gt + lc;
-#pragma unroll
-                for (int kc = 0; kc < NKC; ++kc) {
-                    const half8v pf = *(const half8v*)(sm.p + r * DK + swz(r, 4 * kc + (lane >> 4), NCH) * 8);
-                    g = __builtin_amdgcn_mfma_f32_16x16x32_f16(qv[kc], pf, g, 0, 0, 0);
-                }
-#pragma unroll
-                for (int rr = 0; rr < 4; ++rr) gw[(lr + rr) * S::LDG + 16 * gt + lc] = g[rr];
-            }
-            // the wave reads back only its own G rows
-            __builtin_amdgcn_s_waitcnt(0xc07f);
-            __builtin_amdgcn_wave_barrier();
-
-            // ---- scores (rel_shift gather bd[i][j] = G[i][15 - i + j]), masks, online softmax ----
-            const bool kmask = j0 + AK > vl, cmask = a.chunk > 0;
-            int kch[4] = {0, 0, 0, 0};
-            if (cmask) {
-#pragma unroll
-                for (int jt = 0; jt < 4; ++jt) kch[jt] = (j0 + 16 * jt + lc) / a.chunk;
-            }
-            float sc[4][4];
-            float tmax[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-#pragma unroll
-            for (int jt = 0; jt < 4; ++jt)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int ii = lr + r, jj = 16 * jt + lc;
-                    float sv = (sac[jt][r] + gw[ii * S::LDG + 15 - ii + jj]) * sl2;
-                    if (kmask && j0 + jj >= vl) sv = -INFINITY;
-                    if (cmask) {
-                        const int dc = qch[r] - kch[jt];
-                        if (dc < 0 || dc > a.left_chunks) sv = -INFINITY;
-                    }
-                    sc[jt][r] = sv;
-                    tmax[r] = fmaxf(tmax[r], sv);
-                }
-            float corr[4], msub[4], tsum[4];
+        for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float mnew = fmaxf(mrow[r], row16_max(tmax[r]));
-                msub[r] = mnew == -INFINITY ? 0.f : mnew;   // no -inf - -inf while every key so far is masked
-                corr[r] = __builtin_amdgcn_exp2f(mrow[r] - msub[r]);
-                mrow[r] = mnew;
-                tsum[r] = 0.f;
+                // the mask is added (x + -inf = -inf for the finite scores), not
+                // selected: a select lets the compiler move each G read behind
+                // a branch of its own
+                const int j = j0 + 16 * jt + 4 * lg + r;
+                const float sv = (sac[jt][r] + grow[16 * jt + r]) * sl2 + ((j < jlo || j >= jhi) ? -INFINITY : 0.f);
+                sc[jt][r] = sv;
+                tmax = fmaxf(tmax, sv);
             }
+        const float mnew = fmaxf(mrow, xg_max(tmax));
+        const float msub = mnew == -INFINITY ? 0.f : mnew;   // no -inf - -inf while every key so far is masked
+        const float corr = __builtin_amdgcn_exp2f(mrow - msub);
+        mrow = mnew;
+        float tsum = 0.f;
 #pragma unroll
-            for (int jt = 0; jt < 4; ++jt)
+        for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const float e = __builtin_amdgcn_exp2f(sc[jt][r] - msub[r]);
-                    tsum[r] += e;
-                    probw[(lr + r) * S::LDP + 16 * jt + lc] = (f16)e;
-                }
-#pragma unroll
-            for (int r = 0; r < 4; ++r) lrow[r] = lrow[r] * corr[r] + group_sum(tsum[r], 16);
-            if (s > 0) {
-#pragma unroll
-                for (int d = 0; d < NDT; ++d)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) o[d][r] *= corr[r];
+            for (int r = 0; r < 4; ++r) {
+                const float e = __builtin_amdgcn_exp2f(sc[jt][r] - msub);
+                tsum += e;
+                pr[jt][r] = (f16)e;
             }
-            __builtin_amdgcn_s_waitcnt(0xc07f);
-            __builtin_amdgcn_wave_barrier();
-
-            // ---- o += prob . v : A = prob (16 x 64 keys), B = v^T rows ----
+        lrow = lrow * corr + tsum;
+        if (s > 0) {
 #pragma unroll
-            for (int kc = 0; kc < 2; ++kc) {
-                const half8v pf = *(const half8v*)(probw + lc * S::LDP + 32 * kc + 8 * (lane >> 4));
+            for (int d = 0; d < NDT; ++d) o[d] *= corr;
+        }
+    };
+    // ---- O^T += v^T . prob^T : per 32-key block kc, MFMA k slot 8 (lane/16) + e
+    // stands for key 32 kc + 4 (lane/16) + e (e < 4) or 32 kc + 16 + 4 (lane/16)
+    // + e - 4, the keys whose probabilities this lane holds ----
+    auto pv = [&]() {
 #pragma unroll
-                for (int d = 0; d < NDT; ++d) {
-                    // B[key][dim] for keys 32 kc + 8 (lane / 16) + 0..7, dim 16 d + lane % 16:
-                    // in each 16-lane group, lane 4 j + q points at key j (and j + 4) and
-                    // dims 16 d + 4 q .. + 3; the transposing load hands lane i the four
-                    // keys' values of dim 16 d + i
-                    const int kr = 32 * kc + 8 * (lane >> 4) + (lc >> 2);
-                    const int dc = 16 * d + 4 * (lc & 3);             // first dim of the 8-byte piece
-                    const int r0 = kr, r1 = kr + 4;
-                    const f16* p0 = vtt + r0 * DK + swz(r0, dc / 8, NCH) * 8 + (dc & 7);
-                    const f16* p1 = vtt + r1 * DK + swz(r1, dc / 8, NCH) * 8 + (dc & 7);
-                    typedef __fp16 fp4 __attribute__((ext_vector_type(4)));
-                    const half4v v0 = __builtin_bit_cast(half4v, __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-                                                                     (__attribute__((address_space(3))) fp4*)p0));
-                    const half4v v1 = __builtin_bit_cast(half4v, __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-                                                                     (__attribute__((address_space(3))) fp4*)p1));
-                    const half8v vf = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-                    o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf, vf, o[d], 0, 0, 0);
-                }
+        for (int kc = 0; kc < 2; ++kc) {
+            const half8v pf = {pr[2 * kc][0], pr[2 * kc][1], pr[2 * kc][2], pr[2 * kc][3],
+                               pr[2 * kc + 1][0], pr[2 * kc + 1][1], pr[2 * kc + 1][2], pr[2 * kc + 1][3]};
+#pragma unroll
+            for (int d = 0; d < NDT; ++d) {
+                // A[dim][key] for dims 16 d + lane % 16: in each 16-lane group, lane
+                // 4 j + q points at key base + j and dims 16 d + 4 q .. + 3; the
+                // transposing load hands lane i the four keys' values of dim 16 d + i
+                const int kr = 32 * kc + 4 * lg + (lc >> 2);
+                const int dc = 16 * d + 4 * (lc & 3);
+                const int r1 = kr + 16;
+                const f16* p0 = vst + kr * DK + swz(kr, dc / 8, NCH) * 8 + (dc & 7);
+                const f16* p1 = vst + r1 * DK + swz(r1, dc / 8, NCH) * 8 + (dc & 7);
+                typedef __fp16 fp4 __attribute__((ext_vector_type(4)));
+                const half4v v0 = __builtin_bit_cast(half4v, __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                                                                 (__attribute__((address_space(3))) fp4*)p0));
+                const half4v v1 = __builtin_bit_cast(half4v, __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                                                                 (__attribute__((address_space(3))) fp4*)p1));
+                const half8v vf = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+                o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf, o[d], 0, 0, 0);
             }
         }
-        if (s + 1 < nit) __syncthreads();   // the next step's staging overwrites K, V and the band
+    };
+
+    if constexpr (LONG) {
+        for (int s = 0; s < nit; ++s) {
+            store_kp();
+            __builtin_amdgcn_s_waitcnt(0);   // this wave's stores have landed
+            __syncthreads();
+            if (s + 1 < nit) load_kp(2 * AK * (s + 1));
+            const int j0 = 2 * AK * s + AK * grp;
+            if (j0 < vl) {
+                qk();
+                band();
+                softmax(s, j0);
+                pv();
+            }
+            if (s + 1 < nit) __syncthreads();   // the next step's staging overwrites K, V and the band
+        }
+    } else {
+        // K, then the band, then V: each wait leaves the younger DMAs in flight
+        // and a bare s_barrier publishes every wave's share
+        const int j0 = AK * grp;
+        wait_vmcnt<PPW>();
+        __builtin_amdgcn_s_barrier();
+        dma_rows(make_rsrc(v + rowq * a.ldv + h * DK, ((int64_t)(T - 1) * a.ldv + DK) * 2), sm.vs, a.ldv, 0, KPW);
+        if (j0 < vl) qk();
+        wait_vmcnt<KPW>();
+        __builtin_amdgcn_s_barrier();
+        if (j0 < vl) {
+            band();
+            softmax(0, j0);
+        }
+        wait_vmcnt<0>();
+        __builtin_amdgcn_s_barrier();
+        if (j0 < vl) pv();
     }
 
-    // ---- merge the two key groups: group 0 finishes rows r = 0, 1 of each
-    // lane's four, group 1 rows 2, 3.  Each wave leaves the other half of its
-    // state in its own G area (no other wave reads it: no barrier before),
-    // as 16-byte chunks [chunk][lane]; after one barrier it finishes its half
-    // from its partner's area and stages the output rows in the K area (free
-    // once every wave is past its products) ----
-    constexpr int MR4 = (NDT * 2 + 4) / 4;   // float4 per lane handed over: o of two rows, m and l
-    static_assert(MR4 * 64 * 16 <= sizeof(sm.g[0]) && 4 * 16 * DK * 2 <= sizeof(sm.k), "merge areas");
+    // ---- merge the two key groups: group 0 finishes the dims of the first
+    // NDT / 2 blocks d, group 1 the rest.  Each wave leaves the other half of
+    // its state in its own G area (no other wave reads it: no barrier
+    // before), as 16-byte chunks [chunk][lane]; after one barrier it finishes
+    // its half from its partner's area and stores it, 8 bytes per lane and
+    // block (the four lanes of a query cover 32 contiguous bytes) ----
+    constexpr int NH = NDT / 2;
+    constexpr int MR4 = (4 * NH + 2 + 3) / 4;   // float4 per lane handed over: o of NH blocks, m and l
+    static_assert(MR4 * 64 * 16 <= sizeof(sm.g[0]), "merge area");
+    lrow = xg_sum(lrow);
     float4v* hand = (float4v*)sm.g[w] + lane;
-    const float4v* take = (const float4v*)sm.g[w ^ 4] + lane;   // the partner: same query rows, other keys
-    f16* stage = (f16*)sm.k + wq * 16 * DK;   // the 16 output rows of query block wq (f16, DK wide)
-    auto give = [&](auto R) {
-        constexpr int r0 = decltype(R)::value;
+    const float4v* take = (const float4v*)sm.g[w ^ 4] + lane;   // the partner: same queries, other keys
+    auto give = [&](auto D0) {
+        constexpr int d0 = decltype(D0)::value;
         float x[MR4 * 4];
 #pragma unroll
-        for (int d = 0; d < NDT; ++d) {
-            x[2 * d] = o[d][r0];
-            x[2 * d + 1] = o[d][r0 + 1];
-        }
-        x[2 * NDT] = mrow[r0];
-        x[2 * NDT + 1] = mrow[r0 + 1];
-        x[2 * NDT + 2] = lrow[r0];
-        x[2 * NDT + 3] = lrow[r0 + 1];
+        for (int e = 0; e < MR4 * 4; ++e) x[e] = 0.f;
+#pragma unroll
+        for (int dd = 0; dd < NH; ++dd)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) x[4 * dd + r] = o[d0 + dd][r];
+        x[4 * NH] = mrow;
+        x[4 * NH + 1] = lrow;
 #pragma unroll
         for (int c = 0; c < MR4; ++c) hand[c * 64] = (float4v){x[4 * c], x[4 * c + 1], x[4 * c + 2], x[4 * c + 3]};
     };
-    auto keep = [&](auto R) {
-        constexpr int r0 = decltype(R)::value;
+    auto keep = [&](auto D0) {
+        constexpr int d0 = decltype(D0)::value;
         float y[MR4 * 4];
 #pragma unroll
         for (int c = 0; c < MR4; ++c) {
@@ -360,35 +397,29 @@ __global__ __launch_bounds__(512, 1) void relpos_attn_ks_kernel(AttnParams a) {
             y[4 * c + 2] = t[2];
             y[4 * c + 3] = t[3];
         }
+        const float m1 = y[4 * NH], l1 = y[4 * NH + 1];
+        const float m = fmaxf(mrow, m1);
+        const float c0 = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mrow - m);
+        const float c1 = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - m);
+        const float l = lrow * c0 + l1 * c1;
+        const int i = i0w + lc;
+        const float inv = (i < vl && l > 0.f) ? 1.0f / l : 0.f;   // padded query rows are zero
+        if (i < T) {
+            f16* orow = (f16*)a.out + (rowq + i) * a.ldo + h * DK + 4 * lg;
 #pragma unroll
-        for (int rr = 0; rr < 2; ++rr) {
-            const int r = r0 + rr;
-            const float m1 = y[2 * NDT + rr], l1 = y[2 * NDT + 2 + rr];
-            const float m = fmaxf(mrow[r], m1);
-            const float c0 = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mrow[r] - m);
-            const float c1 = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - m);
-            const float l = lrow[r] * c0 + l1 * c1;
-            const int i = i0w + lr + r;
-            const float inv = (i < vl && l > 0.f) ? 1.0f / l : 0.f;   // padded query rows are zero
+            for (int dd = 0; dd < NH; ++dd) {
+                half4v hv;
 #pragma unroll
-            for (int d = 0; d < NDT; ++d)
-                stage[(lr + r) * DK + 16 * d + lc] = (f16)((o[d][r] * c0 + y[2 * d + rr] * c1) * inv);
+                for (int r = 0; r < 4; ++r) hv[r] = (f16)((o[d0 + dd][r] * c0 + y[4 * dd + r] * c1) * inv);
+                *(half4v*)(orow + 16 * (d0 + dd)) = hv;
+            }
         }
     };
-    if (grp == 0) give(std::integral_constant<int, 2>{});
+    if (grp == 0) give(std::integral_constant<int, NH>{});
     else give(std::integral_constant<int, 0>{});
     __syncthreads();
     if (grp == 0) keep(std::integral_constant<int, 0>{});
-    else keep(std::integral_constant<int, 2>{});
-    __syncthreads();
-    // ---- store: wave (wq, grp) writes rows 8 grp .. 8 grp + 7 of block wq in 16-byte chunks ----
-    f16* out = (f16*)a.out;
-#pragma unroll
-    for (int u = 0; u < (8 * NCH + 63) / 64; ++u) {
-        const int c = lane + 64 * u, r = 8 * grp + c / NCH, i = i0w + r;
-        if (c < 8 * NCH && i < T)
-            *(half8v*)(out + (rowq + i) * a.ldo + h * DK + (c % NCH) * 8) = *(const half8v*)(stage + r * DK + (c % NCH) * 8);
-    }
+    else keep(std::integral_constant<int, NH>{});
 }
 
 // ---------------------------------------------------------------------------
@@ -457,6 +488,8 @@ __global__ __launch_bounds__(64) void relpos_attn_f32_kernel(AttnParams a, int d
 void launch_relpos_attention(Precision prec, const AttnParams& a, hipStream_t s) {
     require(a.T > 0 && a.B > 0 && a.H > 0, "attention: empty shape");
     if (prec == PREC_F16) {
+        require(a.ldq % 8 == 0 && a.ldk % 8 == 0 && a.ldv % 8 == 0 && a.ldp % 8 == 0 && a.ldo % 4 == 0,
+                "attention(f16): row strides must keep 16-byte input rows and 8-byte output pieces aligned");
         // 64 queries per block, two key groups of four waves; sequences of at
         // most 128 frames take a single step whose K and band arrive by DMA
         const dim3 grid(cdiv(a.T, 64) * a.H * a.B);

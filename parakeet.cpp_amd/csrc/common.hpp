@@ -126,6 +126,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, in
 __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds, uint32_t voff, int soff) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
 }
+// s_waitcnt with only the vector-memory counter bounded (gfx9 encoding): the
+// N most recent vector-memory operations of the wave may still be in flight.
+template <int N> __device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
 
 // Sum over a whole wave, every lane receiving it: DPP within each row of 16
 // lanes, then the four row sums read with v_readlane (no LDS round trips, as
@@ -139,13 +145,6 @@ __device__ __forceinline__ float wave_sum_full(float v) {
     const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 32));
     const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 48));
     return (r0 + r1) + (r2 + r3);
-}
-// max over the 16 lanes of each DPP row
-__device__ __forceinline__ float row16_max(float v) {
-    v = fmaxf(v, dpp_get<0xB1>(v));
-    v = fmaxf(v, dpp_get<0x4E>(v));
-    v = fmaxf(v, dpp_get<0x141>(v));
-    return fmaxf(v, dpp_get<0x140>(v));
 }
 
 inline int cdiv(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }

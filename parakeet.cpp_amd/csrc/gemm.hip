@@ -445,12 +445,6 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(GemmParams p) {
 // ===========================================================================
 constexpr int DMA_NS = 3;
 
-// s_waitcnt with only the vector-memory counter bounded (gfx9 encoding).
-template <int N> __device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
-
 template <int TM, int TN, int WT>
 struct DmaCfg {
     static constexpr int BM = 64 * TM, BN = 64 * TN;      // 2x2 waves of (32 TM) x (32 TN)
