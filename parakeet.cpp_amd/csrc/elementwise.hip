@@ -146,49 +146,81 @@ void launch_layernorm(Precision prec, const LnParams& p, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------
-// Depthwise conv1d + bias (+ folded BatchNorm + SiLU), sliding window over
-// time in registers: a thread owns 16 bytes of channels (8 f16 / 4 f32) and TT
-// output frames, loading TT + K - 1 input frames once.  padl zero frames
-// precede each item ((K-1)/2 symmetric, K-1 causal, conformer.cpp:81-120).
-// BNSILU: y = silu((conv + b) * scale + shift) in the input type; otherwise
-// y = conv + b in f32 (the LayerNorm conv norm follows in its own pass).
+// Depthwise conv1d + bias (+ folded BatchNorm + SiLU) over [B][T][D]: padl
+// zero frames precede each item ((K-1)/2 symmetric, K-1 causal,
+// conformer.cpp:81-120).  BNSILU: y = silu((conv + b) * scale + shift) in the
+// input type; otherwise y = conv + b in f32 (the LayerNorm conv norm follows
+// in its own pass).  A block takes a 128-byte channel slice of TC frames: it
+// stages those frames and their K-1 halo frames once in LDS (coalesced
+// 16-byte rows, zeros outside the item), then each thread computes TC/32
+// consecutive frames of one 16-byte channel vector from a window in
+// registers.  LDS rows are padded to 160 bytes, so the 16 lanes of a read
+// group (two row groups, four rows apart) hit 16 distinct bank quads.
 // ---------------------------------------------------------------------------
-template <typename T, typename OutT, int K, int TT, bool BNSILU>
-__global__ __launch_bounds__(256) void dwconv_kernel(const T* in, OutT* out, const float* w, const float* dwb,
-                                                     const float* sc, const float* sh, int Tn, int D, int padl) {
-    constexpr int VEC = 16 / sizeof(T);
-    const int c0 = (blockIdx.x * blockDim.x + threadIdx.x) * VEC;
-    if (c0 >= D) return;
-    const int t0 = blockIdx.y * TT, b = blockIdx.z;
-    constexpr int NW = TT + K - 1;
-    const T* base = in + (int64_t)b * Tn * D + c0;
-    float win[NW][VEC];
+template <typename T, typename OutT, int K, int TC, bool BNSILU>
+__global__ __launch_bounds__(256) void dwconv_lds_kernel(const T* in, OutT* out, const float* w, const float* dwb,
+                                                         const float* sc, const float* sh, int Tn, int D, int padl) {
+    constexpr int VEC = 16 / sizeof(T);   // channels per 16-byte vector
+    constexpr int CV = 8;                 // vectors per staged row (128 bytes)
+    constexpr int RG = 256 / CV;          // row groups
+    constexpr int RT = TC / RG;           // output frames per thread
+    constexpr int NR = TC + K - 1;        // staged frames
+    static_assert(TC % RG == 0, "frames per thread");
+    __shared__ int4v tile[NR][CV + 2];
+    const int cv = threadIdx.x % CV, rg = threadIdx.x / CV;
+    const int cb = blockIdx.x * CV * VEC;   // the block's first channel
+    const int t0 = blockIdx.y * TC, b = blockIdx.z;
+    const T* base = in + (int64_t)b * Tn * D;
+    constexpr int NL = (NR * CV + 255) / 256;   // staging loads per thread, all issued before the first store
+    int4v x[NL];
 #pragma unroll
-    for (int r = 0; r < NW; ++r) {
-        const int t = t0 - padl + r;
-        T x[VEC];
-        if (t >= 0 && t < Tn) {
-            *(int4v*)x = *(const int4v*)(base + (int64_t)t * D);
-        } else {
-#pragma unroll
-            for (int e = 0; e < VEC; ++e) x[e] = (T)0.f;
-        }
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) win[r][e] = (float)x[e];
+    for (int u = 0; u < NL; ++u) {
+        const int i = threadIdx.x + 256 * u, r = i / CV, v = i % CV;
+        const int t = t0 - padl + r, c = cb + v * VEC;
+        x[u] = (int4v){0, 0, 0, 0};
+        if (i < NR * CV && t >= 0 && t < Tn && c < D) x[u] = *(const int4v*)(base + (int64_t)t * D + c);
     }
+#pragma unroll
+    for (int u = 0; u < NL; ++u) {
+        const int i = threadIdx.x + 256 * u;
+        if (i < NR * CV) tile[i / CV][i % CV] = x[u];
+    }
+    // the block's taps [CV VEC][K] and per-channel constants, one coalesced
+    // pass into LDS (per-thread scalar loads of 8 channels x K taps would
+    // take most of the kernel's time)
+    constexpr int CB = CV * VEC;
+    __shared__ float wsm[CB * K], csm[3][CB];
+    for (int i = threadIdx.x; i < CB * K; i += 256) wsm[i] = cb * K + i < D * K ? w[cb * K + i] : 0.f;
+    for (int i = threadIdx.x; i < CB; i += 256) {
+        const int c = min(cb + i, D - 1);
+        csm[0][i] = dwb ? dwb[c] : 0.f;
+        csm[1][i] = BNSILU ? sc[c] : 1.f;
+        csm[2][i] = BNSILU ? sh[c] : 0.f;
+    }
+    const int c0 = cb + cv * VEC;
+    __syncthreads();
+    if (c0 >= D) return;
     float wk[VEC][K], bias[VEC], scale[VEC], shift[VEC];
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
 #pragma unroll
-        for (int k = 0; k < K; ++k) wk[e][k] = w[(c0 + e) * K + k];
-        bias[e] = dwb ? dwb[c0 + e] : 0.f;
-        scale[e] = BNSILU ? sc[c0 + e] : 1.f;
-        shift[e] = BNSILU ? sh[c0 + e] : 0.f;
+        for (int k = 0; k < K; ++k) wk[e][k] = wsm[(cv * VEC + e) * K + k];
+        bias[e] = csm[0][cv * VEC + e];
+        scale[e] = csm[1][cv * VEC + e];
+        shift[e] = csm[2][cv * VEC + e];
+    }
+    float win[RT + K - 1][VEC];
+#pragma unroll
+    for (int r = 0; r < RT + K - 1; ++r) {
+        const int4v xr = tile[rg * RT + r][cv];
+        const T* xv = (const T*)&xr;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) win[r][e] = (float)xv[e];
     }
     OutT* ob = out + (int64_t)b * Tn * D + c0;
 #pragma unroll
-    for (int tt = 0; tt < TT; ++tt) {
-        const int t = t0 + tt;
+    for (int tt = 0; tt < RT; ++tt) {
+        const int t = t0 + rg * RT + tt;
         if (t >= Tn) break;
         OutT o[VEC];
 #pragma unroll
@@ -200,30 +232,24 @@ __global__ __launch_bounds__(256) void dwconv_kernel(const T* in, OutT* out, con
             else o[e] = acc + bias[e];
         }
         OutT* dst = ob + (int64_t)t * D;
-        if constexpr (sizeof(OutT) * VEC == 16) {
-            *(int4v*)dst = *(const int4v*)o;
-        } else {
 #pragma unroll
-            for (int h = 0; h < (int)(sizeof(OutT) * VEC / 16); ++h) ((int4v*)dst)[h] = ((const int4v*)o)[h];
-        }
+        for (int h = 0; h < (int)(sizeof(OutT) * VEC / 16); ++h) ((int4v*)dst)[h] = ((const int4v*)o)[h];
     }
 }
 
 template <typename ET, int K>
 static void dw_go(const void* in, void* out, const float* w, const float* dwb, const float* sc,
                   const float* sh, int B, int Tn, int D, int padl, hipStream_t s) {
-    // one wave per (64 channel vectors, 4 frames, item): enough waves in flight
-    // to cover the load latency of this small pass (B*T*D/2048 waves)
-    constexpr int TT = 4, VEC = 16 / sizeof(ET);
-    const int nvec = D / VEC;
-    const int bs = 64;
-    const dim3 grid(cdiv(nvec, bs), cdiv(Tn, TT), B);
+    // blocks of 64 frames x 128 bytes of channels (an encoder item of 125
+    // frames and 1024 f16 channels: 2 x 16 blocks)
+    constexpr int TC = 64, VEC = 16 / sizeof(ET);
+    const dim3 grid(cdiv(D / VEC, 8), cdiv(Tn, TC), B);
     if (sc)
-        launch((dwconv_kernel<ET, ET, K, TT, true>), grid, dim3(bs), 0, s, (const ET*)in, (ET*)out, w, dwb, sc, sh,
-               Tn, D, padl);
+        launch((dwconv_lds_kernel<ET, ET, K, TC, true>), grid, dim3(256), 0, s, (const ET*)in, (ET*)out, w, dwb, sc,
+               sh, Tn, D, padl);
     else
-        launch((dwconv_kernel<ET, float, K, TT, false>), grid, dim3(bs), 0, s, (const ET*)in, (float*)out, w, dwb,
-               sc, sh, Tn, D, padl);
+        launch((dwconv_lds_kernel<ET, float, K, TC, false>), grid, dim3(256), 0, s, (const ET*)in, (float*)out, w,
+               dwb, sc, sh, Tn, D, padl);
 }
 
 template <typename ET>
