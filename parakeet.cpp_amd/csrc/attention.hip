@@ -13,6 +13,7 @@
 // needs block-wide barriers.
 #include "attention.hpp"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace pkx {
@@ -33,7 +34,8 @@ constexpr int AK = 64;   // keys per tile
 // chunks are XOR-swizzled within each 256-byte LDS line, so 16 consecutive
 // rows read at one logical chunk hit 16 distinct bank quads without row
 // padding.  V^T fragments come from V with transposing LDS loads
-// (ds_read_b64_tr_b16).
+// (ds_read_b64_tr_b16).  A step's K, band and V arrive by DMA; the next
+// step's are issued as soon as every wave has read the current ones.
 // ---------------------------------------------------------------------------
 template <int DK>
 struct KsSmem {
@@ -68,11 +70,33 @@ __device__ __forceinline__ float xg_sum(float x) {
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-template <int DK, bool LONG>
+// ds_read_b64_tr_b16 issued from inline assembly, and the wait for it: the
+// compiler's own form of this load counts as possibly aliasing every LDS DMA
+// in flight and would drain them all before it.  lds_tr_wait<N> waits until
+// at most N LDS operations of the wave are outstanding (in-order completion,
+// so the two loads named are done) and ties their registers to the wait.
+__device__ __forceinline__ void lds_tr_b64(half4v& r, const f16* p) {
+    const uint32_t off = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const f16*)p;
+    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(off));
+}
+template <int N> __device__ __forceinline__ void lds_tr_wait(half4v& x, half4v& y) {
+    static_assert(N >= 0 && N < 16, "lgkmcnt range");
+    asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(x), "+v"(y) : "n"(N));
+}
+
+// f(integral_constant<int, I>) for I = B .. E-1
+template <int B, int E, typename F> __device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
+template <int DK>
 __global__ __launch_bounds__(512, 1) void relpos_attn_ks_kernel(AttnParams a) {
     static_assert(DK == 32 || DK == 64 || DK == 128, "head dim");
     typedef KsSmem<DK> S;
-    constexpr int AQ = S::AQ, NCH = S::NCH, NT = 512, NKC = DK / 32, NDT = DK / 16;
+    constexpr int AQ = S::AQ, NCH = S::NCH, NKC = DK / 32, NDT = DK / 16;
     __shared__ __attribute__((aligned(16))) S sm;
     static_assert(sizeof(S) <= 160 * 1024, "LDS");
     static_assert(S::KI % 8 == 0 && S::PI % 8 == 0, "DMA instructions split evenly over the waves");
@@ -95,50 +119,13 @@ __global__ __launch_bounds__(512, 1) void relpos_attn_ks_kernel(AttnParams a) {
     const f16* v = (const f16*)a.v;
     const f16* pp = (const f16*)a.p;
     const int64_t rowq = (int64_t)b * T;
-    const int nit = (vl + 2 * AK - 1) / (2 * AK);   // steps of 128 keys (<= 1 unless LONG)
+    const int nit = (vl + 2 * AK - 1) / (2 * AK);   // steps of 128 keys
 
-    // K, V and the positional band of a step through registers (long
-    // sequences: the next step's loads are in flight while this one is
-    // computed)
-    constexpr int KCH = 2 * AK * NCH, PCH = S::BROWS * NCH;
-    constexpr int KPT = LONG ? (KCH + NT - 1) / NT : 1, PPT = LONG ? (PCH + NT - 1) / NT : 1;
-    half8v kreg[KPT], vreg[KPT], preg[PPT];
-    auto load_kp = [&](int jb) {
-        const int rlo = T - 1 - (i0 + AQ - 1) + jb;
-#pragma unroll
-        for (int u = 0; u < KPT; ++u) {
-            const int c = tid + NT * u, r = c / NCH, j = jb + r;
-            const bool in = c < KCH && j < T;
-            kreg[u] = in ? *(const half8v*)(k + (rowq + j) * a.ldk + h * DK + (c % NCH) * 8) : (half8v){};
-            vreg[u] = in ? *(const half8v*)(v + (rowq + j) * a.ldv + h * DK + (c % NCH) * 8) : (half8v){};
-        }
-#pragma unroll
-        for (int u = 0; u < PPT; ++u) {
-            const int c = tid + NT * u, pr = rlo + c / NCH;
-            preg[u] = (c < PCH && pr >= 0 && pr < P) ? *(const half8v*)(pp + (int64_t)pr * a.ldp + h * DK + (c % NCH) * 8)
-                                                     : (half8v){};
-        }
-    };
-    auto store_kp = [&]() {
-#pragma unroll
-        for (int u = 0; u < KPT; ++u) {
-            const int c = tid + NT * u, r = c / NCH;   // r: 0..127 = group * 64 + key
-            if (c < KCH) {
-                *(half8v*)(sm.k + r * DK + swz(r, c % NCH, NCH) * 8) = kreg[u];
-                *(half8v*)(sm.vs + r * DK + swz(r, c % NCH, NCH) * 8) = vreg[u];
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < PPT; ++u) {
-            const int c = tid + NT * u, r = c / NCH;
-            if (c < PCH) *(half8v*)(sm.p + r * DK + swz(r, c % NCH, NCH) * 8) = preg[u];
-        }
-    };
-    // A single step (T' <= 128): K, the band and V go straight into LDS by
-    // DMA, 16 bytes per lane, the swizzle applied through each lane's source
-    // chunk, the same number of instructions from every wave; rows past T' or
-    // outside the band's 2T'-1 positions read past the buffer's end (negative
-    // rows wrap above it) and arrive as zeros.
+    // K, the band and V of a step go straight into LDS by DMA, 16 bytes per
+    // lane, the swizzle applied through each lane's source chunk, the same
+    // number of instructions from every wave; rows past T' or outside the
+    // band's 2T'-1 positions read past the buffer's end (negative rows wrap
+    // above it) and arrive as zeros.
     constexpr int KPW = S::KI / 8, PPW = S::PI / 8;   // DMA instructions per wave
     auto dma_rows = [&](__amdgpu_buffer_rsrc_t r, f16* dst, int64_t ld, int row0, int per_wave) {
         for (int u = 0; u < per_wave; ++u) {
@@ -170,14 +157,16 @@ __global__ __launch_bounds__(512, 1) void relpos_attn_ks_kernel(AttnParams a) {
     // issued whatever the item's length (an item with no valid frame still
     // waits for them below), so that the waits in between count a fixed
     // number of younger loads
-    if constexpr (LONG) {
-        load_kp(0);
-    } else {
-        // K and the band now, V once K has landed
-        dma_rows(make_rsrc(k + rowq * a.ldk + h * DK, ((int64_t)(T - 1) * a.ldk + DK) * 2), sm.k, a.ldk, 0, KPW);
-        dma_rows(make_rsrc(pp + h * DK, ((int64_t)(P - 1) * a.ldp + DK) * 2), sm.p, a.ldp, T - 1 - (i0 + AQ - 1),
-                 PPW);
-    }
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(k + rowq * a.ldk + h * DK, ((int64_t)(T - 1) * a.ldk + DK) * 2);
+    const __amdgpu_buffer_rsrc_t rp = make_rsrc(pp + h * DK, ((int64_t)(P - 1) * a.ldp + DK) * 2);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(v + rowq * a.ldv + h * DK, ((int64_t)(T - 1) * a.ldv + DK) * 2);
+    const int rlo = T - 1 - (i0 + AQ - 1);   // the band's first position at step 0
+    auto dma_k = [&](int st) { dma_rows(rk, sm.k, a.ldk, 2 * AK * st, KPW); };          // K of step st
+    auto dma_p = [&](int st) { dma_rows(rp, sm.p, a.ldp, rlo + 2 * AK * st, PPW); };    // its band
+    auto dma_v = [&](int st) { dma_rows(rv, sm.vs, a.ldv, 2 * AK * st, KPW); };         // its V
+    dma_k(0);
+    dma_p(0);
+    dma_v(0);
     float4v bq[NKC][4];   // bias_u, bias_u, bias_v, bias_v halves of each fragment's 8 columns
     {
         float4v* bs = (float4v*)sm.g[w];
@@ -305,6 +294,7 @@ __global__ __launch_bounds__(512, 1) void relpos_attn_ks_kernel(AttnParams a) {
         for (int kc = 0; kc < 2; ++kc) {
             const half8v pf = {pr[2 * kc][0], pr[2 * kc][1], pr[2 * kc][2], pr[2 * kc][3],
                                pr[2 * kc + 1][0], pr[2 * kc + 1][1], pr[2 * kc + 1][2], pr[2 * kc + 1][3]};
+            half4v v0[NDT], v1[NDT];
 #pragma unroll
             for (int d = 0; d < NDT; ++d) {
                 // A[dim][key] for dims 16 d + lane % 16: in each 16-lane group, lane
@@ -313,52 +303,58 @@ __global__ __launch_bounds__(512, 1) void relpos_attn_ks_kernel(AttnParams a) {
                 const int kr = 32 * kc + 4 * lg + (lc >> 2);
                 const int dc = 16 * d + 4 * (lc & 3);
                 const int r1 = kr + 16;
-                const f16* p0 = vst + kr * DK + swz(kr, dc / 8, NCH) * 8 + (dc & 7);
-                const f16* p1 = vst + r1 * DK + swz(r1, dc / 8, NCH) * 8 + (dc & 7);
-                typedef __fp16 fp4 __attribute__((ext_vector_type(4)));
-                const half4v v0 = __builtin_bit_cast(half4v, __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-                                                                 (__attribute__((address_space(3))) fp4*)p0));
-                const half4v v1 = __builtin_bit_cast(half4v, __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-                                                                 (__attribute__((address_space(3))) fp4*)p1));
-                const half8v vf = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-                o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf, o[d], 0, 0, 0);
+                lds_tr_b64(v0[d], vst + kr * DK + swz(kr, dc / 8, NCH) * 8 + (dc & 7));
+                lds_tr_b64(v1[d], vst + r1 * DK + swz(r1, dc / 8, NCH) * 8 + (dc & 7));
             }
+            auto mma = [&](auto D) {
+                constexpr int d = decltype(D)::value;
+                lds_tr_wait<2 * (NDT - 1 - d)>(v0[d], v1[d]);
+                const half8v vf = {v0[d][0], v0[d][1], v0[d][2], v0[d][3], v1[d][0], v1[d][1], v1[d][2], v1[d][3]};
+                o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf, o[d], 0, 0, 0);
+            };
+            static_for<0, NDT>(mma);
         }
     };
 
-    if constexpr (LONG) {
-        for (int s = 0; s < nit; ++s) {
-            store_kp();
-            __builtin_amdgcn_s_waitcnt(0);   // this wave's stores have landed
-            __syncthreads();
-            if (s + 1 < nit) load_kp(2 * AK * (s + 1));
-            const int j0 = 2 * AK * s + AK * grp;
-            if (j0 < vl) {
-                qk();
-                band();
-                softmax(s, j0);
-                pv();
-            }
-            if (s + 1 < nit) __syncthreads();   // the next step's staging overwrites K, V and the band
-        }
-    } else {
-        // K, then the band, then V: each wait leaves the younger DMAs in flight
-        // and a bare s_barrier publishes every wave's share
-        const int j0 = AK * grp;
-        wait_vmcnt<PPW>();
+    // Steps of 128 keys.  In flight at the top of a step, oldest first: its
+    // K, band and V.  The next step's K and band are issued once every wave
+    // has its scores, its V once every wave is past P.V; each wait leaves the
+    // younger DMAs in flight, and a bare s_barrier publishes every wave's
+    // share.  The last step issues nothing and is peeled off, so that every
+    // path through a step has the same loads in flight (the compiler's own
+    // waits then stay out of the way).  An item with no valid frame still
+    // waits for the first step's DMAs.
+    auto step = [&](int s, auto MORE) {
+        constexpr bool more = decltype(MORE)::value;
+        const int j0 = 2 * AK * s + AK * grp;
+        const bool act = j0 < vl;
+        wait_vmcnt<PPW + KPW>();   // K
         __builtin_amdgcn_s_barrier();
-        dma_rows(make_rsrc(v + rowq * a.ldv + h * DK, ((int64_t)(T - 1) * a.ldv + DK) * 2), sm.vs, a.ldv, 0, KPW);
-        if (j0 < vl) qk();
-        wait_vmcnt<KPW>();
+        if (act) qk();
+        wait_vmcnt<KPW>();         // the band
         __builtin_amdgcn_s_barrier();
-        if (j0 < vl) {
+        if (act) {
             band();
-            softmax(0, j0);
+            softmax(s, j0);
         }
-        wait_vmcnt<0>();
+        if constexpr (more) {
+            __builtin_amdgcn_s_barrier();   // K and the band are read
+            dma_k(s + 1);
+            dma_p(s + 1);
+            wait_vmcnt<PPW + KPW>();        // V (the next K and band behind it)
+        } else {
+            wait_vmcnt<0>();
+        }
         __builtin_amdgcn_s_barrier();
-        if (j0 < vl) pv();
-    }
+        if (act) pv();
+        if constexpr (more) {
+            __builtin_amdgcn_s_barrier();   // V is read
+            dma_v(s + 1);
+        }
+    };
+    const int nst = max(nit, 1);
+    for (int s = 0; s + 1 < nst; ++s) step(s, std::true_type{});
+    step(nst - 1, std::false_type{});
 
     // ---- merge the two key groups: group 0 finishes the dims of the first
     // NDT / 2 blocks d, group 1 the rest.  Each wave leaves the other half of
@@ -490,22 +486,16 @@ void launch_relpos_attention(Precision prec, const AttnParams& a, hipStream_t s)
     if (prec == PREC_F16) {
         require(a.ldq % 8 == 0 && a.ldk % 8 == 0 && a.ldv % 8 == 0 && a.ldp % 8 == 0 && a.ldo % 4 == 0,
                 "attention(f16): row strides must keep 16-byte input rows and 8-byte output pieces aligned");
-        // 64 queries per block, two key groups of four waves; sequences of at
-        // most 128 frames take a single step whose K and band arrive by DMA
+        // 64 queries per block, two key groups of four waves, steps of 128 keys
+        // staged by DMA (offsets within a head's band rows are 32-bit)
+        require(((int64_t)(2 * a.T - 2) * a.ldp + a.dk) * 2 < ((int64_t)1 << 31) &&
+                    ((int64_t)(a.T + 127) * std::max(a.ldk, a.ldv) + a.dk) * 2 < ((int64_t)1 << 31),
+                "attention(f16): an item's key rows or a head's positional rows span 2 GiB or more");
         const dim3 grid(cdiv(a.T, 64) * a.H * a.B);
-        const bool lng = a.T > 2 * AK;
-        if (a.dk == 128) {
-            if (lng) launch(relpos_attn_ks_kernel<128, true>, grid, dim3(512), 0, s, a);
-            else launch(relpos_attn_ks_kernel<128, false>, grid, dim3(512), 0, s, a);
-        } else if (a.dk == 64) {
-            if (lng) launch(relpos_attn_ks_kernel<64, true>, grid, dim3(512), 0, s, a);
-            else launch(relpos_attn_ks_kernel<64, false>, grid, dim3(512), 0, s, a);
-        } else if (a.dk == 32) {
-            if (lng) launch(relpos_attn_ks_kernel<32, true>, grid, dim3(512), 0, s, a);
-            else launch(relpos_attn_ks_kernel<32, false>, grid, dim3(512), 0, s, a);
-        } else {
-            throw std::invalid_argument("attention(f16): head dim must be 32, 64 or 128");
-        }
+        if (a.dk == 128) launch(relpos_attn_ks_kernel<128>, grid, dim3(512), 0, s, a);
+        else if (a.dk == 64) launch(relpos_attn_ks_kernel<64>, grid, dim3(512), 0, s, a);
+        else if (a.dk == 32) launch(relpos_attn_ks_kernel<32>, grid, dim3(512), 0, s, a);
+        else throw std::invalid_argument("attention(f16): head dim must be 32, 64 or 128");
     } else {
         const size_t smem = sizeof(float) * (2 * (size_t)a.dk + (size_t)a.T);
         require(smem <= 64 * 1024, "attention(f32): T too large for the LDS score row");

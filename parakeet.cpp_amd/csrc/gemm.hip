@@ -1088,9 +1088,15 @@ __device__ __forceinline__ void epilogue32_glu_dw(const GemmParams& p, float16v 
         if (r < BM - H && m < p.M) {
             const int t = rtab[r].x;
             float2v a = {0.f, 0.f};
+            if (t >= H && t < p.T - H) {
+                // the whole window inside the item (all but 2 H frames of it)
 #pragma unroll
-            for (int j = 0; j < K; ++j)
-                if ((unsigned)(t + j - H) < (unsigned)p.T) a += wk[j] * win[q + j];
+                for (int j = 0; j < K; ++j) a += wk[j] * win[q + j];
+            } else {
+#pragma unroll
+                for (int j = 0; j < K; ++j)
+                    if ((unsigned)(t + j - H) < (unsigned)p.T) a += wk[j] * win[q + j];
+            }
             const float2v y = (a + db) * sc + sh;
             const half2v h = {(f16)silu_dev(y[0]), (f16)silu_dev(y[1])};
             *(half2v*)((f16*)p.Y + (int64_t)m * p.ldy + c) = h;
