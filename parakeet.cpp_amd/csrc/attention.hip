@@ -37,18 +37,21 @@ constexpr int AK = 64;   // keys per tile
 // (ds_read_b64_tr_b16).  A step's K, band and V arrive by DMA; the next
 // step's are issued as soon as every wave has read the current ones.
 // ---------------------------------------------------------------------------
-template <int DK>
+template <int DK, int NQW, int NG>
 struct KsSmem {
-    static constexpr int AQ = 64;                   // queries per block
+    static constexpr int NW = NQW * NG;             // waves: NQW query blocks of 16 x NG key groups
+    static constexpr int AQ = 16 * NQW;             // queries per block
     static constexpr int NCH = DK / 8;              // 16-byte chunks per K / band row
-    static constexpr int BROWS = AQ + 2 * AK;       // band rows per step (AQ + 2 AK - 1 used)
-    static constexpr int KI = 2 * AK * NCH / 64;    // 1-KB DMA instructions for K (and for V)
-    static constexpr int PI = (BROWS * NCH / 64 + 7) / 8 * 8;   // for the band, rounded to the 8 waves
+    static constexpr int BROWS = AQ + NG * AK;      // band rows per step (AQ + NG AK - 1 used)
+    // 1-KB DMA instructions for K (and for V) and for the band, each rounded
+    // up to a multiple of the waves (rows past a step's own arrive unused)
+    static constexpr int KI = (NG * AK * NCH / 64 + NW - 1) / NW * NW;
+    static constexpr int PI = (BROWS * NCH / 64 + NW - 1) / NW * NW;
     static constexpr int LDG = 84;                  // G^T row (floats)
-    f16 k[2 * AK * DK];       // K: [group][key][DK]
-    f16 vs[2 * AK * DK];      // V: [group][key][DK]
-    f16 p[PI * 512];          // band rows of the step (rows past BROWS unused)
-    float g[8][16 * LDG];     // per wave: G^T as [query][band row]
+    f16 k[KI * 512];          // K: [group][key][DK]
+    f16 vs[KI * 512];         // V: [group][key][DK]
+    f16 p[PI * 512];          // band rows of the step
+    float g[NW][16 * LDG];    // per wave: G^T as [query][band row]
 };
 
 // stored position of logical 16-byte chunk c in row r of a swizzled array
@@ -92,18 +95,18 @@ template <int B, int E, typename F> __device__ __forceinline__ void static_for(F
     }
 }
 
-template <int DK>
-__global__ __launch_bounds__(512, 1) void relpos_attn_ks_kernel(AttnParams a) {
+template <int DK, int NQW, int NG>
+__global__ __launch_bounds__(64 * NQW * NG, 1) void relpos_attn_ks_kernel(AttnParams a) {
     static_assert(DK == 32 || DK == 64 || DK == 128, "head dim");
-    typedef KsSmem<DK> S;
-    constexpr int AQ = S::AQ, NCH = S::NCH, NKC = DK / 32, NDT = DK / 16;
+    static_assert(NG == 1 || NG == 2, "key groups");
+    typedef KsSmem<DK, NQW, NG> S;
+    constexpr int AQ = S::AQ, NCH = S::NCH, NW = S::NW, NKC = DK / 32, NDT = DK / 16, SK = NG * AK;
     __shared__ __attribute__((aligned(16))) S sm;
     static_assert(sizeof(S) <= 160 * 1024, "LDS");
-    static_assert(S::KI % 8 == 0 && S::PI % 8 == 0, "DMA instructions split evenly over the waves");
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int grp = w >> 2, wq = w & 3;
+    const int grp = w / NQW, wq = w % NQW;
     const int T = a.T, P = 2 * T - 1;
     // work order (head, item, query block), query block fastest, each XCD a
     // contiguous run: the blocks of one item share K and V, those of one head
@@ -119,17 +122,17 @@ __global__ __launch_bounds__(512, 1) void relpos_attn_ks_kernel(AttnParams a) {
     const f16* v = (const f16*)a.v;
     const f16* pp = (const f16*)a.p;
     const int64_t rowq = (int64_t)b * T;
-    const int nit = (vl + 2 * AK - 1) / (2 * AK);   // steps of 128 keys
+    const int nit = (vl + SK - 1) / SK;   // steps of SK = NG x 64 keys
 
     // K, the band and V of a step go straight into LDS by DMA, 16 bytes per
     // lane, the swizzle applied through each lane's source chunk, the same
     // number of instructions from every wave; rows past T' or outside the
     // band's 2T'-1 positions read past the buffer's end (negative rows wrap
     // above it) and arrive as zeros.
-    constexpr int KPW = S::KI / 8, PPW = S::PI / 8;   // DMA instructions per wave
+    constexpr int KPW = S::KI / NW, PPW = S::PI / NW;   // DMA instructions per wave
     auto dma_rows = [&](__amdgpu_buffer_rsrc_t r, f16* dst, int64_t ld, int row0, int per_wave) {
         for (int u = 0; u < per_wave; ++u) {
-            const int ii = w + 8 * u;
+            const int ii = w + NW * u;
             const int o = ii * 1024 + 16 * lane, rr = o / (DK * 2), t = (o % (DK * 2)) / 16;
             const int64_t off = ((int64_t)(row0 + rr) * ld + swz(rr, t, NCH) * 8) * 2;
             lds_dma16(r, (uint8_t*)dst + ii * 1024, off < 0 ? OOB : (uint32_t)off, 0);
@@ -161,9 +164,9 @@ __global__ __launch_bounds__(512, 1) void relpos_attn_ks_kernel(AttnParams a) {
     const __amdgpu_buffer_rsrc_t rp = make_rsrc(pp + h * DK, ((int64_t)(P - 1) * a.ldp + DK) * 2);
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(v + rowq * a.ldv + h * DK, ((int64_t)(T - 1) * a.ldv + DK) * 2);
     const int rlo = T - 1 - (i0 + AQ - 1);   // the band's first position at step 0
-    auto dma_k = [&](int st) { dma_rows(rk, sm.k, a.ldk, 2 * AK * st, KPW); };          // K of step st
-    auto dma_p = [&](int st) { dma_rows(rp, sm.p, a.ldp, rlo + 2 * AK * st, PPW); };    // its band
-    auto dma_v = [&](int st) { dma_rows(rv, sm.vs, a.ldv, 2 * AK * st, KPW); };         // its V
+    auto dma_k = [&](int st) { dma_rows(rk, sm.k, a.ldk, SK * st, KPW); };          // K of step st
+    auto dma_p = [&](int st) { dma_rows(rp, sm.p, a.ldp, rlo + SK * st, PPW); };    // its band
+    auto dma_v = [&](int st) { dma_rows(rv, sm.vs, a.ldv, SK * st, KPW); };         // its V
     dma_k(0);
     dma_p(0);
     dma_v(0);
@@ -326,7 +329,7 @@ __global__ __launch_bounds__(512, 1) void relpos_attn_ks_kernel(AttnParams a) {
     // waits for the first step's DMAs.
     auto step = [&](int s, auto MORE) {
         constexpr bool more = decltype(MORE)::value;
-        const int j0 = 2 * AK * s + AK * grp;
+        const int j0 = SK * s + AK * grp;
         const bool act = j0 < vl;
         wait_vmcnt<PPW + KPW>();   // K
         __builtin_amdgcn_s_barrier();
@@ -356,66 +359,81 @@ __global__ __launch_bounds__(512, 1) void relpos_attn_ks_kernel(AttnParams a) {
     for (int s = 0; s + 1 < nst; ++s) step(s, std::true_type{});
     step(nst - 1, std::false_type{});
 
-    // ---- merge the two key groups: group 0 finishes the dims of the first
+    // ---- two key groups: merged, group 0 finishing the dims of the first
     // NDT / 2 blocks d, group 1 the rest.  Each wave leaves the other half of
     // its state in its own G area (no other wave reads it: no barrier
     // before), as 16-byte chunks [chunk][lane]; after one barrier it finishes
-    // its half from its partner's area and stores it, 8 bytes per lane and
-    // block (the four lanes of a query cover 32 contiguous bytes) ----
-    constexpr int NH = NDT / 2;
-    constexpr int MR4 = (4 * NH + 2 + 3) / 4;   // float4 per lane handed over: o of NH blocks, m and l
-    static_assert(MR4 * 64 * 16 <= sizeof(sm.g[0]), "merge area");
+    // its half from its partner's area.  Stores: 8 bytes per lane and block
+    // (the four lanes of a query cover 32 contiguous bytes) ----
     lrow = xg_sum(lrow);
-    float4v* hand = (float4v*)sm.g[w] + lane;
-    const float4v* take = (const float4v*)sm.g[w ^ 4] + lane;   // the partner: same queries, other keys
-    auto give = [&](auto D0) {
-        constexpr int d0 = decltype(D0)::value;
-        float x[MR4 * 4];
-#pragma unroll
-        for (int e = 0; e < MR4 * 4; ++e) x[e] = 0.f;
-#pragma unroll
-        for (int dd = 0; dd < NH; ++dd)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) x[4 * dd + r] = o[d0 + dd][r];
-        x[4 * NH] = mrow;
-        x[4 * NH + 1] = lrow;
-#pragma unroll
-        for (int c = 0; c < MR4; ++c) hand[c * 64] = (float4v){x[4 * c], x[4 * c + 1], x[4 * c + 2], x[4 * c + 3]};
-    };
-    auto keep = [&](auto D0) {
-        constexpr int d0 = decltype(D0)::value;
-        float y[MR4 * 4];
-#pragma unroll
-        for (int c = 0; c < MR4; ++c) {
-            const float4v t = take[c * 64];
-            y[4 * c] = t[0];
-            y[4 * c + 1] = t[1];
-            y[4 * c + 2] = t[2];
-            y[4 * c + 3] = t[3];
-        }
-        const float m1 = y[4 * NH], l1 = y[4 * NH + 1];
-        const float m = fmaxf(mrow, m1);
-        const float c0 = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mrow - m);
-        const float c1 = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - m);
-        const float l = lrow * c0 + l1 * c1;
-        const int i = i0w + lc;
-        const float inv = (i < vl && l > 0.f) ? 1.0f / l : 0.f;   // padded query rows are zero
+    const int i = i0w + lc;
+    f16* orow = (f16*)a.out + (rowq + i) * a.ldo + h * DK + 4 * lg;
+    if constexpr (NG == 1) {
+        const float inv = (i < vl && lrow > 0.f) ? 1.0f / lrow : 0.f;   // padded query rows are zero
         if (i < T) {
-            f16* orow = (f16*)a.out + (rowq + i) * a.ldo + h * DK + 4 * lg;
 #pragma unroll
-            for (int dd = 0; dd < NH; ++dd) {
+            for (int d = 0; d < NDT; ++d) {
                 half4v hv;
 #pragma unroll
-                for (int r = 0; r < 4; ++r) hv[r] = (f16)((o[d0 + dd][r] * c0 + y[4 * dd + r] * c1) * inv);
-                *(half4v*)(orow + 16 * (d0 + dd)) = hv;
+                for (int r = 0; r < 4; ++r) hv[r] = (f16)(o[d][r] * inv);
+                *(half4v*)(orow + 16 * d) = hv;
             }
         }
-    };
-    if (grp == 0) give(std::integral_constant<int, NH>{});
-    else give(std::integral_constant<int, 0>{});
-    __syncthreads();
-    if (grp == 0) keep(std::integral_constant<int, 0>{});
-    else keep(std::integral_constant<int, NH>{});
+    } else {
+        constexpr int NH = NDT / 2;
+        constexpr int MR4 = (4 * NH + 2 + 3) / 4;   // float4 per lane handed over: o of NH blocks, m and l
+        static_assert(MR4 * 64 * 16 <= sizeof(sm.g[0]), "merge area");
+        float4v* hand = (float4v*)sm.g[w] + lane;
+        // the partner: same queries, other keys
+        const float4v* take = (const float4v*)sm.g[grp == 0 ? w + NQW : w - NQW] + lane;
+        auto give = [&](auto D0) {
+            constexpr int d0 = decltype(D0)::value;
+            float x[MR4 * 4];
+#pragma unroll
+            for (int e = 0; e < MR4 * 4; ++e) x[e] = 0.f;
+#pragma unroll
+            for (int dd = 0; dd < NH; ++dd)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) x[4 * dd + r] = o[d0 + dd][r];
+            x[4 * NH] = mrow;
+            x[4 * NH + 1] = lrow;
+#pragma unroll
+            for (int c = 0; c < MR4; ++c)
+                hand[c * 64] = (float4v){x[4 * c], x[4 * c + 1], x[4 * c + 2], x[4 * c + 3]};
+        };
+        auto keep = [&](auto D0) {
+            constexpr int d0 = decltype(D0)::value;
+            float y[MR4 * 4];
+#pragma unroll
+            for (int c = 0; c < MR4; ++c) {
+                const float4v t = take[c * 64];
+                y[4 * c] = t[0];
+                y[4 * c + 1] = t[1];
+                y[4 * c + 2] = t[2];
+                y[4 * c + 3] = t[3];
+            }
+            const float m1 = y[4 * NH], l1 = y[4 * NH + 1];
+            const float m = fmaxf(mrow, m1);
+            const float c0 = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mrow - m);
+            const float c1 = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - m);
+            const float l = lrow * c0 + l1 * c1;
+            const float inv = (i < vl && l > 0.f) ? 1.0f / l : 0.f;   // padded query rows are zero
+            if (i < T) {
+#pragma unroll
+                for (int dd = 0; dd < NH; ++dd) {
+                    half4v hv;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) hv[r] = (f16)((o[d0 + dd][r] * c0 + y[4 * dd + r] * c1) * inv);
+                    *(half4v*)(orow + 16 * (d0 + dd)) = hv;
+                }
+            }
+        };
+        if (grp == 0) give(std::integral_constant<int, NH>{});
+        else give(std::integral_constant<int, 0>{});
+        __syncthreads();
+        if (grp == 0) keep(std::integral_constant<int, 0>{});
+        else keep(std::integral_constant<int, NH>{});
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -491,10 +509,23 @@ void launch_relpos_attention(Precision prec, const AttnParams& a, hipStream_t s)
         require(((int64_t)(2 * a.T - 2) * a.ldp + a.dk) * 2 < ((int64_t)1 << 31) &&
                     ((int64_t)(a.T + 127) * std::max(a.ldk, a.ldv) + a.dk) * 2 < ((int64_t)1 << 31),
                 "attention(f16): an item's key rows or a head's positional rows span 2 GiB or more");
-        const dim3 grid(cdiv(a.T, 64) * a.H * a.B);
-        if (a.dk == 128) launch(relpos_attn_ks_kernel<128>, grid, dim3(512), 0, s, a);
-        else if (a.dk == 64) launch(relpos_attn_ks_kernel<64>, grid, dim3(512), 0, s, a);
-        else if (a.dk == 32) launch(relpos_attn_ks_kernel<32>, grid, dim3(512), 0, s, a);
+        // Blocks run one per CU (LDS).  When the last round of 64-query
+        // blocks would leave the chip partly idle, 96-query blocks of one key
+        // group (six waves, 1.5x the work each) are taken if they need
+        // fewer rounds by that measure (T' = 375 at batch 8: 384 -> 256).
+        int dev = 0, cus = 256;
+        PKX_HIP(hipGetDevice(&dev));
+        PKX_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+        const int64_t nb64 = (int64_t)cdiv(a.T, 64) * a.H * a.B, nb96 = (int64_t)cdiv(a.T, 96) * a.H * a.B;
+        const bool wide = 3 * ((nb96 + cus - 1) / cus) < 2 * ((nb64 + cus - 1) / cus);
+        auto go = [&](auto DKc) {
+            constexpr int D = decltype(DKc)::value;
+            if (wide) launch(relpos_attn_ks_kernel<D, 6, 1>, dim3(nb96), dim3(384), 0, s, a);
+            else launch(relpos_attn_ks_kernel<D, 4, 2>, dim3(nb64), dim3(512), 0, s, a);
+        };
+        if (a.dk == 128) go(std::integral_constant<int, 128>{});
+        else if (a.dk == 64) go(std::integral_constant<int, 64>{});
+        else if (a.dk == 32) go(std::integral_constant<int, 32>{});
         else throw std::invalid_argument("attention(f16): head dim must be 32, 64 or 128");
     } else {
         const size_t smem = sizeof(float) * (2 * (size_t)a.dk + (size_t)a.T);

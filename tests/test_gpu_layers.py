@@ -21,6 +21,7 @@ CASES = {
     "q8_dk64": (dict(d_model=256, n_heads=4, ff_dim=512), "q8_0", 1),
     "q4k_dk128": (dict(d_model=256, n_heads=2, ff_dim=512), "q4_k", 1),
     "f16_dk64": (dict(d_model=128, n_heads=2, ff_dim=256, attn_bias=False, conv_bias=False), "f16", 1),
+    "f16_dk32": (dict(d_model=128, n_heads=4, ff_dim=256), "f16", 1),
     # depthwise kernel 5: the f16 path runs GLU GEMM + separate depthwise pass
     # (kernel 9 takes the fused one-pass conv-module GEMM)
     "f16_k5": (dict(d_model=128, n_heads=2, ff_dim=256, conv_kernel=5), "f16", 1),
@@ -53,9 +54,13 @@ def _valid_mask(B, T, valid):
     return np.arange(T)[None, :] < np.asarray(valid)[:, None]
 
 
+# (16, 375): more 64-query blocks than one round of the chip holds, so the f16
+# kernel takes its 96-query single-key-group form (the 4-head cases: dk 64, 32)
 @pytest.mark.parametrize("name", list(CASES))
 @pytest.mark.parametrize("B,T,valid", [(1, 1, [1]), (2, 37, [37, 20]), (3, 70, [70, 64, 1]),
-                                       (2, 130, [130, 99])])
+                                       (2, 130, [130, 99]),
+                                       (16, 375, [375, 375, 300, 1, 129, 128, 64, 65, 200, 374, 96, 97, 250, 33,
+                                                  375, 2])])
 def test_relpos_attention(gpu, stream, name, B, T, valid):
     m, om, gm, prec = _models(gpu, name)
     D = m.cfg.d_model
