@@ -350,11 +350,13 @@ __global__ __launch_bounds__(256) void sub_stage1_kernel(const float* mel, const
     extern __shared__ float mp[];                 // [11][4 F2 + 5]: mel columns 2 - 3 pl .. 4 F2 + 4 - 3 pl
     // f16 output: the mel tile is staged as f16 (rows of FPH halves, even so
     // that column pairs are 4-byte aligned) and conv0 runs as packed f16
-    // products with f32 accumulation (v_dot2_f32_f16)
+    // products with f32 accumulation (v_dot2_f32_f16); a second tile holds
+    // vertical pairs (rows j, j + 1 of one column) for the kw = 2 taps
     constexpr bool H = std::is_same<T, f16>::value;
     const int b = blockIdx.y, t2a = 2 * blockIdx.x;
     const int FP = 4 * F2 + 5, FPH = FP + 1;
     f16* mh = (f16*)mp;
+    half2v* mv = (half2v*)(mh + 11 * FPH);        // [10][FP]
     const int v0 = valid0 ? valid0[b] : Tn;
     const int v1 = valid1 ? valid1[b] : T1;
     // time fastest across the threads: mel is [B][F][T], so 11 consecutive
@@ -368,6 +370,13 @@ __global__ __launch_bounds__(256) void sub_stage1_kernel(const float* mel, const
         else mp[j * FP + q] = v;
     }
     __syncthreads();
+    if constexpr (H) {
+        for (int idx = threadIdx.x; idx < 10 * FP; idx += blockDim.x) {
+            const int j = idx / FP, q = idx % FP;
+            mv[idx] = (half2v){mh[j * FPH + q], mh[(j + 1) * FPH + q]};
+        }
+        __syncthreads();
+    }
     bool rowok[5];
 #pragma unroll
     for (int r = 0; r < 5; ++r) {
@@ -398,7 +407,7 @@ __global__ __launch_bounds__(256) void sub_stage1_kernel(const float* mel, const
             const int f1a = 2 * f2 - pl + 1;
             const bool fa = f1a >= 0 && f1a < F1, fb = f1a + 1 >= 0 && f1a + 1 < F1;
             if constexpr (H) {
-                half2v p01[11], p23[11];
+                half2v p01[11], p23[11], v2[5], v4[5];
                 f16 m4[11];
 #pragma unroll
                 for (int j = 0; j < 11; ++j) {
@@ -408,6 +417,11 @@ __global__ __launch_bounds__(256) void sub_stage1_kernel(const float* mel, const
                     m4[j] = row[4];
                 }
 #pragma unroll
+                for (int r = 0; r < 5; ++r) {   // rows 2 r, 2 r + 1 at columns 4 f2 + 2 and 4 f2 + 4
+                    v2[r] = mv[2 * r * FP + 4 * f2 + 2];
+                    v4[r] = mv[2 * r * FP + 4 * f2 + 4];
+                }
+#pragma unroll
                 for (int r = 0; r < 5; ++r) {
                     float sa = bc0, sb = bc0;
 #pragma unroll
@@ -415,12 +429,13 @@ __global__ __launch_bounds__(256) void sub_stage1_kernel(const float* mel, const
                         sa = __builtin_amdgcn_fdot2(p01[2 * r + kh], w01[kh], sa, false);
                         sb = __builtin_amdgcn_fdot2(p23[2 * r + kh], w01[kh], sb, false);
                     }
-                    sa = __builtin_amdgcn_fdot2((half2v){p23[2 * r][0], p23[2 * r + 1][0]}, w2v, sa, false);
-                    sb = __builtin_amdgcn_fdot2((half2v){m4[2 * r], m4[2 * r + 1]}, w2v, sb, false);
+                    sa = __builtin_amdgcn_fdot2(v2[r], w2v, sa, false);
+                    sb = __builtin_amdgcn_fdot2(v4[r], w2v, sb, false);
                     sa += w22 * (float)p23[2 * r + 2][0];
                     sb += w22 * (float)m4[2 * r + 2];
-                    ca[r] = (rowok[r] && fa && sa > 0.f) ? sa : 0.f;
-                    cb[r] = (rowok[r] && fb && sb > 0.f) ? sb : 0.f;
+                    // ReLU and the masks (row, column; uniform over the block)
+                    ca[r] = rowok[r] && fa ? fmaxf(sa, 0.f) : 0.f;
+                    cb[r] = rowok[r] && fb ? fmaxf(sb, 0.f) : 0.f;
                 }
             } else {
                 float m[11][5];
@@ -464,9 +479,10 @@ void launch_sub_stage1(Precision prec, const float* mel, const int* valid0, cons
     const int pl = causal ? 2 : 1;
     const dim3 grid(cdiv(T2, 2), B);
     const int bs = C >= 256 ? 256 : ((C + 63) / 64) * 64;
-    // 4 F2 + 5 >= F + 2 covers the zero padding; f32 tile [11][FP] (the f16
-    // tile [11][FP + 1] fits in it)
-    const uint32_t shm = 11u * (uint32_t)(4 * F2 + 5) * 4u;
+    // 4 F2 + 5 >= F + 2 covers the zero padding; f32 tile [11][FP], f16 tile
+    // [11][FP + 1] followed by the vertical pairs [10][FP]
+    const uint32_t FP = 4 * F2 + 5;
+    const uint32_t shm = prec == PREC_F16 ? 11u * (FP + 1) * 2u + 10u * FP * 4u : 11u * FP * 4u;
     if (prec == PREC_F16)
         launch(sub_stage1_kernel<f16>, grid, dim3(bs), shm, s, mel, valid0, valid1, w0, b0, w2, b2, (f16*)out, F, T,
                C, T1, F1, T2, F2, pl);
