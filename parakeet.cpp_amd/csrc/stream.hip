@@ -33,36 +33,37 @@ struct StreamAttnParams {
 
 // LDS bytes of one stream_attn_kernel workgroup: keys and values of the
 // Tk = CL + Tc frames and the NPB = CL + 2 Tc - 1 positional rows the chunk
-// reads, in the activation type (as bytes), rows padded by 4 bytes
-// (consecutive rows start in consecutive banks); q + u and q + v [Tc][dk]
-// and the scores [Tc][Tk] in f32.
+// reads, in the activation type (as bytes), rows padded by 16 bytes (16-byte
+// aligned rows whose starts step through the bank quads); q + u and q + v
+// [Tc][dk] and the scores [Tc][Tk] (rounded up to 16 bytes) in f32.
 inline int stream_attn_lds_bytes(int Tc, int CL, int dk, int as) {
     const int Tk = CL + Tc, npb = CL + 2 * Tc - 1;
-    return (2 * Tk + npb) * (dk + 4 / as) * as + (2 * Tc * dk + Tc * Tk) * 4;
+    return (2 * Tk + npb) * (dk + 16 / as) * as + (2 * Tc * dk + (Tc * Tk + 3) / 4 * 4) * 4;
 }
 
 // One workgroup per (stream, head), 256 threads.  Everything the chunk reads
-// is staged in LDS with coalesced loads first (ring rows in logical order,
-// the chunk's own keys / values, the positional band); a thread then owns a
-// (query, key) score, a wave a softmax row, a thread a (query, channel) output.
-// DK > 0: the head width at compile time (dot products fully unrolled, so the
-// LDS reads of a score issue back to back); DK = 0 reads it from p.dk.
+// is staged in LDS with coalesced 16-byte loads and stores first (ring rows in
+// logical order, the chunk's own keys / values, the positional band); a
+// thread then owns a (query, key) score, read as 16-byte vectors, a wave a
+// softmax row, and a thread 16 bytes of one query's output channels.
+// DK > 0: the head width at compile time (dot products fully unrolled); DK = 0
+// reads it from p.dk.
 template <typename T, int DK>
 __global__ __launch_bounds__(256) void stream_attn_kernel(StreamAttnParams p) {
     extern __shared__ float sm[];
+    constexpr int VE = 16 / sizeof(T);           // elements per 16-byte vector
     const int b = blockIdx.x, h = blockIdx.y, dk = DK > 0 ? DK : p.dk, D = p.D, Tc = p.Tc, CL = p.CL;
-    const int Tk = CL + Tc, npb = CL + 2 * Tc - 1, ld = dk + 4 / (int)sizeof(T);
+    const int Tk = CL + Tc, npb = CL + 2 * Tc - 1, ld = dk + VE;
     float* qu = sm;                              // [Tc][dk]
     float* qv = qu + Tc * dk;                    // [Tc][dk]
     float* sc = qv + Tc * dk;                    // [Tc][Tk]
-    T* ks = (T*)(sc + Tc * Tk);                  // [Tk][ld]
+    T* ks = (T*)(sc + (Tc * Tk + 3) / 4 * 4);    // [Tk][ld]
     T* vs = ks + Tk * ld;                        // [Tk][ld]
     T* ps = vs + Tk * ld;                        // [npb][ld]: row j <-> distance CL + Tc - 1 - j
     const T* qkv = (const T*)p.qkv;
     T* kring = (T*)p.kc + (int64_t)b * CL * D + h * dk;
     T* vring = (T*)p.vc + (int64_t)b * CL * D + h * dk;
     // 16-byte loads (dk % 8 == 0, D % 8 == 0), several in flight per thread
-    constexpr int VE = 16 / sizeof(T);
     const int vpr = dk / VE;
 #pragma unroll 4
     for (int e = threadIdx.x; e < Tk * vpr; e += blockDim.x) {
@@ -77,24 +78,15 @@ __global__ __launch_bounds__(256) void stream_attn_kernel(StreamAttnParams p) {
             sk = row + D;
             sv = row + 2 * D;
         }
-        T xk[VE], xv[VE];
-        *(int4v*)xk = *(const int4v*)sk;
-        *(int4v*)xv = *(const int4v*)sv;
-#pragma unroll
-        for (int q = 0; q < VE; ++q) {
-            ks[r * ld + c0 + q] = xk[q];
-            vs[r * ld + c0 + q] = xv[q];
-        }
+        *(int4v*)(ks + r * ld + c0) = *(const int4v*)sk;
+        *(int4v*)(vs + r * ld + c0) = *(const int4v*)sv;
     }
     const int prow0 = p.tc_max - Tc;             // global row of band row 0 (distance CL + Tc - 1)
     const T* ppos = (const T*)p.ppos;
 #pragma unroll 4
     for (int e = threadIdx.x; e < npb * vpr; e += blockDim.x) {
         const int r = e / vpr, c0 = (e % vpr) * VE;
-        T x[VE];
-        *(int4v*)x = *(const int4v*)(ppos + (int64_t)(prow0 + r) * D + h * dk + c0);
-#pragma unroll
-        for (int q = 0; q < VE; ++q) ps[r * ld + c0 + q] = x[q];
+        *(int4v*)(ps + r * ld + c0) = *(const int4v*)(ppos + (int64_t)(prow0 + r) * D + h * dk + c0);
     }
     for (int e = threadIdx.x; e < Tc * dk; e += blockDim.x) {
         const int i = e / dk, c = e % dk;
@@ -115,10 +107,20 @@ __global__ __launch_bounds__(256) void stream_attn_kernel(StreamAttnParams p) {
             const float* a = qu + i * dk;
             const float* a2 = qv + i * dk;
             float ac = 0.f, bd = 0.f;
-#pragma unroll 16
-            for (int c = 0; c < dk; ++c) {
-                ac += a[c] * (float)kr[c];
-                bd += a2[c] * (float)pr[c];
+#pragma unroll 4
+            for (int c = 0; c < dk; c += VE) {
+                const int4v kk = *(const int4v*)(kr + c), pk = *(const int4v*)(pr + c);
+                const T* kx = (const T*)&kk;
+                const T* px = (const T*)&pk;
+#pragma unroll
+                for (int e4 = 0; e4 < VE; e4 += 4) {
+                    const float4v av = *(const float4v*)(a + c + e4), bv = *(const float4v*)(a2 + c + e4);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        ac += av[q] * (float)kx[e4 + q];
+                        bd += bv[q] * (float)px[e4 + q];
+                    }
+                }
             }
             s = (ac + bd) * p.scale;
         }
@@ -145,22 +147,33 @@ __global__ __launch_bounds__(256) void stream_attn_kernel(StreamAttnParams p) {
     }
     __syncthreads();
     T* out = (T*)p.out;
-    for (int e = threadIdx.x; e < Tc * dk; e += blockDim.x) {
-        const int i = e / dk, c = e % dk;
+    for (int e = threadIdx.x; e < Tc * vpr; e += blockDim.x) {
+        const int i = e / vpr, c0 = (e % vpr) * VE;
         const float* r = sc + i * Tk;
-        float acc = 0.f;
-#pragma unroll 8
-        for (int kj = 0; kj < Tk; ++kj) acc += r[kj] * (float)vs[kj * ld + c];
-        out[(int64_t)(b * Tc + i) * D + h * dk + c] = to_act<T>(acc);
+        float acc[VE];
+#pragma unroll
+        for (int q = 0; q < VE; ++q) acc[q] = 0.f;
+#pragma unroll 4
+        for (int kj = 0; kj < Tk; ++kj) {
+            const float w = r[kj];
+            const int4v vv = *(const int4v*)(vs + kj * ld + c0);
+            const T* vx = (const T*)&vv;
+#pragma unroll
+            for (int q = 0; q < VE; ++q) acc[q] += w * (float)vx[q];
+        }
+        T o[VE];
+#pragma unroll
+        for (int q = 0; q < VE; ++q) o[q] = to_act<T>(acc[q]);
+        *(int4v*)(out + (int64_t)(b * Tc + i) * D + h * dk + c0) = *(const int4v*)o;
     }
     // the chunk's frames take the ring slots of the oldest ones (every ring
     // read above went through LDS before the barrier): logical order
     // [cache[Tc:] ; chunk] with the ring start moved by Tc on the host
-    for (int e = threadIdx.x; e < Tc * dk; e += blockDim.x) {
-        const int q = e / dk, c = e % dk;
-        const int64_t slot = (int64_t)((p.head + q) % CL) * D + c;
-        kring[slot] = ks[(CL + q) * ld + c];
-        vring[slot] = vs[(CL + q) * ld + c];
+    for (int e = threadIdx.x; e < Tc * vpr; e += blockDim.x) {
+        const int q = e / vpr, c0 = (e % vpr) * VE;
+        const int64_t slot = (int64_t)((p.head + q) % CL) * D + c0;
+        *(int4v*)(kring + slot) = *(const int4v*)(ks + (CL + q) * ld + c0);
+        *(int4v*)(vring + slot) = *(const int4v*)(vs + (CL + q) * ld + c0);
     }
 }
 
