@@ -14,7 +14,6 @@
 #include "attention.hpp"
 
 #include <algorithm>
-#include <atomic>
 #include <type_traits>
 
 namespace pkx {
@@ -514,15 +513,7 @@ void launch_relpos_attention(Precision prec, const AttnParams& a, hipStream_t s)
         // blocks would leave the chip partly idle, 96-query blocks of one key
         // group (six waves, 1.5x the work each) are taken if they need
         // fewer rounds by that measure (T' = 375 at batch 8: 384 -> 256).
-        static std::atomic<int> cu_count[64];   // per device, 0 until first asked
-        int dev = 0;
-        PKX_HIP(hipGetDevice(&dev));
-        require(dev >= 0 && dev < 64, "attention: device index");
-        int cus = cu_count[dev].load(std::memory_order_relaxed);
-        if (cus == 0) {
-            PKX_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-            cu_count[dev].store(cus, std::memory_order_relaxed);
-        }
+        const int cus = device_cu_count();
         const int64_t nb64 = (int64_t)cdiv(a.T, 64) * a.H * a.B, nb96 = (int64_t)cdiv(a.T, 96) * a.H * a.B;
         const bool wide = 3 * ((nb96 + cus - 1) / cus) < 2 * ((nb64 + cus - 1) / cus);
         auto go = [&](auto DKc) {

@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 #include <hip/hip_ext.h>
 
+#include <atomic>
 #include <cstdint>
 #include <cstdio>
 #include <stdexcept>
@@ -148,6 +149,20 @@ __device__ __forceinline__ float wave_sum_full(float v) {
 }
 
 inline int cdiv(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
+
+// Compute units of the current device (asked once per device, then cached).
+inline int device_cu_count() {
+    static std::atomic<int> cache[64];   // per device, 0 until first asked
+    int dev = 0;
+    PKX_HIP(hipGetDevice(&dev));
+    require(dev >= 0 && dev < 64, "device index out of range");
+    int cus = cache[dev].load(std::memory_order_relaxed);
+    if (cus == 0) {
+        PKX_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+        cache[dev].store(cus, std::memory_order_relaxed);
+    }
+    return cus;
+}
 __host__ __device__ __forceinline__ int cdiv_dev(int a, int b) { return (a + b - 1) / b; }
 
 }  // namespace pkx

@@ -25,9 +25,8 @@ __device__ __forceinline__ int wave_id_uniform() { return __builtin_amdgcn_readf
 // over the chip instead of 8*|A| or 8*|W|).  xcd_tile gives each XCD a
 // contiguous range of positions; positions enumerate the rectangles in order,
 // each rectangle M-fastest, so the map is a bijection for any grid size.
-__device__ __forceinline__ void xcd_tile_2d(int bid, int nbm, int nbn, int gm, int& bm, int& bn) {
+__device__ __forceinline__ void xcd_rect(int k, int nbm, int nbn, int gm, int& bm, int& bn) {
     const int gn = 8 / gm;
-    int k = xcd_tile(bid, nbm * nbn);
     for (int i = 0; i < gm; ++i) {
         const int r0 = i * nbm / gm, r1 = (i + 1) * nbm / gm;
         for (int j = 0; j < gn; ++j) {
@@ -42,6 +41,9 @@ __device__ __forceinline__ void xcd_tile_2d(int bid, int nbm, int nbn, int gm, i
         }
     }
     bm = bn = 0;   // unreachable: the rectangles cover the grid
+}
+__device__ __forceinline__ void xcd_tile_2d(int bid, int nbm, int nbn, int gm, int& bm, int& bn) {
+    xcd_rect(xcd_tile(bid, nbm * nbn), nbm, nbn, gm, bm, bn);
 }
 
 // ---------------------------------------------------------------------------
@@ -1162,8 +1164,15 @@ struct FoldStats {
 // by side along N, each 64 TM rows x 16 TN columns, so that no two waves
 // dequantise the same weight rows; 2 = the 2 x 2 layout with the slab's LDS
 // reads issued up front (as layout 1 does).
+// WL = 3: layout 0 with the K range cut over p.ksplit workgroups per tile
+// (split-K across workgroups, for grids far smaller than the chip).  Each
+// workgroup writes its partial tile to p.sk_part and counts itself in
+// p.sk_cnt[tile]; the last one to arrive sums the partials in split order (the
+// same order whichever arrives last, so results are deterministic), resets the
+// counter and runs the epilogue.
 template <int TM, int TN, int WT, int EPI, int NS = DMA_NS, int KG = 1, int WL = 0>
 __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(GemmParams p) {
+    constexpr bool SPLIT = WL == 3;
     typedef DmaCfg<TM, TN, WT> C;
     static_assert(WL != 1 || (TN % 2 == 0 && EPI != EPI_GLU && EPI != EPI_GLU_DW && EPI != EPI_RELU_TR &&
                               EPI != EPI_RELU2_F32),
@@ -1185,8 +1194,16 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
     constexpr int DWH = EPI == EPI_GLU_DW ? (GLU_DW_K - 1) / 2 : 0;
     constexpr int SM = C::BM - 2 * DWH;
     const int nbm = cdiv_dev(p.M, SM), nbn = cdiv_dev(p.N, C::BN);
-    int bm, bn;
-    xcd_tile_2d(blockIdx.x, nbm, nbn, p.xcd_gm, bm, bn);
+    int bm, bn, tile = 0, split = 0;
+    if constexpr (SPLIT) {
+        // the splits of one tile are consecutive positions (one XCD)
+        const int k = xcd_tile(blockIdx.x, nbm * nbn * p.ksplit);
+        tile = k / p.ksplit;
+        split = k - tile * p.ksplit;
+        xcd_rect(tile, nbm, nbn, p.xcd_gm, bm, bn);
+    } else {
+        xcd_tile_2d(blockIdx.x, nbm, nbn, p.xcd_gm, bm, bn);
+    }
     const int m0 = bm * SM - DWH, n0 = bn * C::BN;
 
     float16v acc[WTM][WTN];
@@ -1219,7 +1236,8 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
     DwPre<EPI == EPI_GLU_DW ? C::BM : 64, 16 * TN> dwpre;
     if constexpr (EPI == EPI_GLU_DW) dwpre.load(p, m0, n0, tid);
 
-    const int nk = p.K / 64 / KG, kb = kg * nk * 64;   // slabs of this group, its first K
+    // slabs of this group, its first K
+    const int nk = SPLIT ? p.K / 64 / KG / p.ksplit : p.K / 64 / KG, kb = (split * KG + kg) * nk * 64;
     DmaSrc<TM, TN, WT> src;
     src.init(p, m0, n0, wid, lane);
     src.issue(smem, kb);
@@ -1238,7 +1256,7 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
             const int st2 = st + NS - 1 >= NS ? st - 1 : st + NS - 1;
             src.issue(smem + st2 * C::STAGE, kb + (kt + NS - 1) * 64);
         }
-        mma32_slab<TM, TN, WT, WTM, WTN, WL != 0>(smem + st * C::STAGE, acc, wm, wn, lane);
+        mma32_slab<TM, TN, WT, WTM, WTN, WL == 1 || WL == 2>(smem + st * C::STAGE, acc, wm, wn, lane);
         st = st + 1 == NS ? 0 : st + 1;
     }
     if constexpr (KG == 2) {
@@ -1263,6 +1281,59 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
                 for (int j = 0; j < WTN; ++j)
 #pragma unroll
                     for (int r = 0; r < 16; ++r) acc[i][j][r] += red[((i * WTN + j) * 16 + r) * 64];
+        }
+    }
+    if constexpr (SPLIT) {
+        static_assert(!FOLD && EPI != EPI_GLU_DW, "split-K: no folded LayerNorm");
+        // Partial tiles [tile][split][wave][register][lane], written and read
+        // with device-scope accesses (coherent across the XCDs' L2s without
+        // cache-wide write-backs or invalidations, which would also evict the
+        // weights every other workgroup is reading).
+        constexpr int R = WTM * WTN * 16;
+        const int S = p.ksplit;
+        float* part = p.sk_part + (int64_t)tile * S * (4 * R * 64) + wid * R * 64 + lane;
+        if (kg == 0) {
+#pragma unroll
+            for (int i = 0; i < WTM; ++i)
+#pragma unroll
+                for (int j = 0; j < WTN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        __hip_atomic_store(part + (int64_t)split * (4 * R * 64) + ((i * WTN + j) * 16 + r) * 64,
+                                           acc[i][j][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            wait_vmcnt<0>();   // the partial has reached the device before the count
+        }
+        __shared__ int sk_last;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            const int seen = __hip_atomic_fetch_add(p.sk_cnt + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            sk_last = seen == S - 1;
+            // every split of this tile has counted: ready for the next launch
+            if (seen == S - 1) __hip_atomic_store(p.sk_cnt + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if (!sk_last) return;
+        if (kg == 0) {
+            // the sum in split order, whichever split arrived last
+            float16v own[WTM][WTN];
+#pragma unroll
+            for (int i = 0; i < WTM; ++i)
+#pragma unroll
+                for (int j = 0; j < WTN; ++j) own[i][j] = acc[i][j];
+            for (int t = 0; t < S; ++t) {
+#pragma unroll
+                for (int i = 0; i < WTM; ++i)
+#pragma unroll
+                    for (int j = 0; j < WTN; ++j)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) {
+                            const float v = t == split ? own[i][j][r]
+                                                       : __hip_atomic_load(part + (int64_t)t * (4 * R * 64) +
+                                                                               ((i * WTN + j) * 16 + r) * 64,
+                                                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                            acc[i][j][r] = t == 0 ? v : acc[i][j][r] + v;
+                        }
+            }
         }
     }
     // folded LayerNorm: the tile's row statistics at the top of the LDS block
@@ -1668,6 +1739,30 @@ static void dma_22q(int epi, const GemmParams& p, hipStream_t s) {
     default: dma_epi<2, 2, WT>(epi, p, s); break;
     }
 }
+// Split-K across workgroups for the residual products of few rows and K >= 1024
+// (a streaming step's FFN linear2: M = streams x chunk frames, 64 x 64 tiles in
+// the tens): 64 x 64 tiles in two K groups, the K range cut over S workgroups
+// per tile (S a power of two up to 8, each K group keeping at least one 64-deep
+// slab) until the grid holds about one workgroup per CU.  On MI355X at M = 512,
+// N = 512, K = 2048: 64 tiles x 4 splits, 1.4 us faster per launch; at K = 512
+// (linear_out, pw2) and with two workgroups per CU it was slower.
+template <int WT>
+static bool dma_splitk(int epi, const GemmParams& p, hipStream_t s) {
+    if (!p.sk_part || !p.sk_cnt || p.M > 512 || p.K < 1024 || (epi != EPI_RESID && epi != EPI_RESID_LN))
+        return false;
+    const int tiles = cdiv(p.M, 64) * cdiv(p.N, 64);
+    const int cus = device_cu_count();
+    int S = 1;
+    while (S < 8 && 2 * S * tiles <= cus && p.K % (2 * S * 128) == 0) S *= 2;
+    if (S == 1 || (int64_t)tiles * S * 64 * 64 > p.sk_part_floats || tiles > p.sk_cnt_n) return false;
+    GemmParams q = p;
+    q.ksplit = S;
+    q.xcd_gm = choose_xcd_gm(p, WT, 64, 64);
+    if (epi == EPI_RESID) launch((gemm_dma_kernel<1, 1, WT, EPI_RESID, DMA_NS, 2, 3>), dim3(tiles * S), dim3(512), 0, s, q);
+    else launch((gemm_dma_kernel<1, 1, WT, EPI_RESID_LN, DMA_NS, 2, 3>), dim3(tiles * S), dim3(512), 0, s, q);
+    PKX_LAUNCH_CHECK();
+    return true;
+}
 // 128 x 64 tiles with two K groups (eight waves): products of K >= 1024 whose
 // grid is about one tile per CU (FFN linear2 at K = 4096; attention out and
 // pw2 at K = 1024, where the split takes 0.3 - 0.9 us off a 14 - 15 us launch)
@@ -1768,6 +1863,9 @@ void launch_gemm(Precision prec, int wtype, int epi, const GemmParams& p, hipStr
         const int64_t t22 = (int64_t)cdiv(p.M, 128) * cdiv(p.N, 128);
         const int64_t t21 = (int64_t)cdiv(p.M, 128) * cdiv(p.N, 64);
         const bool glu = epi == EPI_GLU || epi == EPI_GLU_DW;
+        if (wtype == GT_Q8_0 && dma_splitk<GT_Q8_0>(epi, p, s)) return;
+        if (wtype == GT_Q4_K && dma_splitk<GT_Q4_K>(epi, p, s)) return;
+        if (wtype == GT_F16 && dma_splitk<GT_F16>(epi, p, s)) return;
         if (wtype == GT_Q8_0 && dma_kg2<GT_Q8_0>(epi, p, s)) return;
         if (wtype == GT_Q4_K && dma_kg2<GT_Q4_K>(epi, p, s)) return;
         if (wtype == GT_F16 && dma_kg2<GT_F16>(epi, p, s)) return;

@@ -72,6 +72,17 @@ struct GemmParams {
     const float* fold_c1 = nullptr;
     int fold_groups = 0;
     float fold_eps = 1e-5f;
+    // Split-K across workgroups: launch_gemm cuts the K range of small grids
+    // (M <= 512 residual products) over ksplit workgroups per tile when the
+    // caller supplies this workspace: sk_part holds the partial tiles
+    // (sk_part_floats floats), sk_cnt one arrival counter per tile (sk_cnt_n
+    // ints, zero when allocated; every launch leaves them zero again).  Calls
+    // sharing one workspace must not overlap.
+    float* sk_part = nullptr;
+    int64_t sk_part_floats = 0;
+    int* sk_cnt = nullptr;
+    int sk_cnt_n = 0;
+    int ksplit = 1;            // set by launch_gemm
 };
 
 // c1[n] = sum_k g[k] w[n][k], c2[n] = sum_k b[k] w[n][k] + bias[n] for a

@@ -82,14 +82,17 @@ struct Model::Ws {
     Buf lnst;                           // row statistics for the folded LayerNorms
     Buf lnrows;                         // norm_out's per-row {mean, rstd} (not stored norm_out output)
     Buf logits, pp;                     // heads
+    Buf skpart;                         // split-K partial tiles
+    int* skcnt = nullptr;               // split-K tile counters (zero between launches)
     int* d_valid = nullptr;             // 4 x Bcap ints: v0, v1, v2, vout
     int* h_valid = nullptr;             // pinned staging
     int Bcap = 0;
     hipEvent_t staged = nullptr;
     ~Ws() {
-        for (Buf* b : {&a2, &a2p, &a3, &flat, &h, &u, &qkv, &g, &pe, &p, &xin, &tmp, &lnst, &lnrows, &logits, &pp})
+        for (Buf* b : {&a2, &a2p, &a3, &flat, &h, &u, &qkv, &g, &pe, &p, &xin, &tmp, &lnst, &lnrows, &logits, &pp, &skpart})
             if (b->p) (void)hipFree(b->p);
         if (d_valid) (void)hipFree(d_valid);
+        if (skcnt) (void)hipFree(skcnt);
         if (h_valid) (void)hipHostFree(h_valid);
         if (staged) (void)hipEventDestroy(staged);
     }
@@ -756,9 +759,28 @@ void Model::gemm(const DevWeight& w, int epi, const void* A, int64_t lda, int64_
     p.M = (int)M;
     p.N = w.N;
     p.K = w.K;
+    if (epi == EPI_RESID) splitk_ws(p, s);
     mark(fam, true);
     launch_gemm(prec, w.gtype, epi, p, s);
     mark(fam, false);
+}
+
+// 2^20 floats of partial tiles (256 64 x 64 tile splits) and 512 tile counters
+constexpr int64_t SK_FLOATS = (int64_t)1 << 20;
+constexpr int SK_TILES = 512;
+
+void Model::splitk_ws(GemmParams& p, hipStream_t s) {
+    if (p.M > 512) return;
+    if (!ws_->skcnt) {
+        grow(ws_->skpart, (size_t)SK_FLOATS * 4);
+        PKX_HIP(hipMalloc(&ws_->skcnt, SK_TILES * sizeof(int)));
+        PKX_HIP(hipMemsetAsync(ws_->skcnt, 0, SK_TILES * sizeof(int), s));
+        PKX_HIP(hipStreamSynchronize(s));
+    }
+    p.sk_part = (float*)ws_->skpart.p;
+    p.sk_part_floats = SK_FLOATS;
+    p.sk_cnt = ws_->skcnt;
+    p.sk_cnt_n = SK_TILES;
 }
 
 void Model::gemm_resid_ln(const DevWeight& w, const void* A, int64_t M, const float* bias, float* x, float alpha,
@@ -784,6 +806,7 @@ void Model::gemm_resid_ln(const DevWeight& w, const void* A, int64_t M, const fl
     p.ln_g = g;
     p.ln_h = h;
     p.ln_stats = (float*)ws_->lnst.p;
+    splitk_ws(p, s);
     mark(fam, true);
     launch_gemm(prec_, w.gtype, EPI_RESID_LN, p, s);
     mark(fam, false);

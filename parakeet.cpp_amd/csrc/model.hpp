@@ -227,6 +227,9 @@ private:
     void gemm_resid_ln(const DevWeight& w, const void* A, int64_t M, const float* bias, float* x, float alpha,
                        const float* g, void* h, hipStream_t s, int fam, const float* res_rows = nullptr,
                        const float* res_g = nullptr, const float* res_b = nullptr);
+    // split-K workspace for residual products of few rows (M <= 512), made on
+    // first use; launch_gemm decides whether to split
+    void splitk_ws(GemmParams& p, hipStream_t s);
     // product of a LayerNorm folded in (A = x * gamma from gemm_resid_ln)
     GemmParams fold_params(const DevWeight& w, const void* A, int64_t M, const float* c1, const float* c2,
                            void* Y, int64_t ldy);

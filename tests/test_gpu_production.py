@@ -15,6 +15,8 @@ oracle, through the C ABI.
 * 1.1B-shape q8_0 encoder, 42 blocks, 30 s clips (T' 375), every layer within
   1e-2 (4 of the configuration's 8 items, one of them ragged, to keep the
   oracle's share of the test near 10 s on the GPU host).
+* 0.6B shape, 3 blocks, at few rows (B 3 ragged and B 1): the split-K
+  residual products, every layer within 1e-2 and bit-identical on a repeat.
 Relative L2 is over each item's valid frames.
 """
 import time
@@ -205,6 +207,32 @@ def test_06b_full_depth_f16_ragged_tdt(gpu, stream):
     lg_e2e, tok_e2e, dur_e2e = om.tdt_joint(ref[mask], g)
     argmax_within_error(tok, tok_e2e, lg_e2e[:, :n_tok], lg[:, :n_tok], "c3 end-to-end tokens")
     argmax_within_error(dur, dur_e2e, lg_e2e[:, n_tok:], lg[:, n_tok:], "c3 end-to-end durations")
+    gm.close()
+
+
+# ---------------------------------------------------------------------------
+# Few rows (M = B*T' <= 512): the residual products of K >= 1024 (FFN linear2,
+# attention out, pw2) split K over 2 (B 3, M 375) or 8 (B 1, M 125) workgroups
+# per tile, partials summed in a fixed order
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("wtype,lens", [("q8_0", [1000, 737, 1000]), ("f16", [1000])])
+def test_06b_few_rows_split_k(gpu, stream, wtype, lens):
+    m = pm.synthesize(_cfg06(3), wtype, bn_random=True, heads=False)
+    om = oracle.OracleModel(m)
+    gm = gpu.Model.from_tensors(m, gpu.PREC_F16)
+    rng = np.random.default_rng(4000)
+    mel = rng.normal(0, 1, (len(lens), 128, 1000)).astype(np.float32)
+    for b, v in enumerate(lens):
+        mel[b, :, v:] = 0.0
+    label = f"split-K {wtype} B={len(lens)}"
+    print(f"[{label}] lens={lens}", flush=True)
+    got, _, _ = _run_encoder(gpu, stream, gm, om, mel, lens, label, 1e-2)
+    # deterministic: the same partials in the same order on a second call
+    dm = gpu.DeviceArray.from_numpy(mel, stream)
+    dy = gpu.DeviceArray(got.shape, np.float32)
+    gm.encoder_forward(dm, lens, dy, stream=stream)
+    assert np.array_equal(dy.numpy(stream), got)
+    dm.free(), dy.free()
     gm.close()
 
 
