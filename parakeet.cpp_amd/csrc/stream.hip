@@ -258,7 +258,7 @@ __global__ __launch_bounds__(256) void stream_conv_kernel(StreamConvParams p) {
 // load of a channel (taps, history, chunk) is issued before any arithmetic,
 // the history update is written from registers.
 template <typename T, int K, int TCM>
-__global__ __launch_bounds__(256) void stream_conv_kernel_k(StreamConvParams p) {
+__global__ __launch_bounds__(512) void stream_conv_kernel_k(StreamConvParams p) {
     extern __shared__ float dwo[];               // [TCM][D]
     constexpr int LP = K - 1;
     const int b = blockIdx.x, D = p.D, Tc = p.Tc;
@@ -527,10 +527,13 @@ int Model::stream_step(StreamState& st, const float* mel, int n, bool is_last, f
             const uint32_t shm = (uint32_t)(SC_FRAMES * D) * 4u;
             mark(KF_DWCONV, true);
             if (c.conv_kernel == 9 && Tc <= SC_TCM) {
+                // one stream per workgroup, one channel per thread up to 512
+                // (every load of a channel in flight at once, 8 waves per CU)
+                const uint32_t shk = (uint32_t)(SC_TCM * D) * 4u;
                 if (prec_ == PREC_F16)
-                    launch(stream_conv_kernel_k<f16, 9, SC_TCM>, dim3(B), dim3(256), shm, s, q);
+                    launch(stream_conv_kernel_k<f16, 9, SC_TCM>, dim3(B), dim3(512), shk, s, q);
                 else
-                    launch(stream_conv_kernel_k<float, 9, SC_TCM>, dim3(B), dim3(256), shm, s, q);
+                    launch(stream_conv_kernel_k<float, 9, SC_TCM>, dim3(B), dim3(512), shk, s, q);
             } else if (prec_ == PREC_F16) {
                 launch(stream_conv_kernel<f16>, dim3(B), dim3(256), shm, s, q);
             } else {
