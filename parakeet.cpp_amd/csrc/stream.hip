@@ -31,21 +31,23 @@ struct StreamAttnParams {
     float scale;
 };
 
-// LDS bytes of one stream_attn_kernel workgroup: keys and values of the
-// Tk = CL + Tc frames and the NPB = CL + 2 Tc - 1 positional rows the chunk
-// reads, in the activation type (as bytes), rows padded by 16 bytes (16-byte
-// aligned rows whose starts step through the bank quads); q + u and q + v
-// [Tc][dk] and the scores [Tc][Tk] (rounded up to 16 bytes) in f32.
+// LDS bytes of one stream_attn_kernel workgroup: the values of the Tk = CL + Tc
+// frames in the activation type, rows padded by 16 bytes (16-byte aligned rows
+// whose starts step through the bank quads); q + u and q + v [Tc][dk] and the
+// scores [Tc][Tk] (rounded up to 16 bytes) in f32.
 inline int stream_attn_lds_bytes(int Tc, int CL, int dk, int as) {
-    const int Tk = CL + Tc, npb = CL + 2 * Tc - 1;
-    return (2 * Tk + npb) * (dk + 16 / as) * as + (2 * Tc * dk + (Tc * Tk + 3) / 4 * 4) * 4;
+    const int Tk = CL + Tc;
+    // + the P.V partials: 256 threads x 16 bytes of f32 (4 or 8 floats)
+    return Tk * (dk + 16 / as) * as + (2 * Tc * dk + (Tc * Tk + 3) / 4 * 4) * 4 + 256 * (16 / as) * 4;
 }
 
-// One workgroup per (stream, head), 256 threads.  Everything the chunk reads
-// is staged in LDS with coalesced 16-byte loads and stores first (ring rows in
-// logical order, the chunk's own keys / values, the positional band); a
-// thread then owns a (query, key) score, read as 16-byte vectors, a wave a
-// softmax row, and a thread 16 bytes of one query's output channels.
+// One workgroup per (stream, head), 256 threads.  The values are staged in LDS
+// with coalesced 16-byte loads (ring rows in logical order, then the chunk's
+// own); a thread owns a (query, key) score and reads that key's row and its
+// positional row straight from memory (each one contiguous 16-byte vectors,
+// issued together), a wave a softmax row, and a thread 16 bytes of one
+// query's output channels.  Keeping only the values in LDS lets the whole
+// grid of a step (streams x heads) be resident at once.
 // DK > 0: the head width at compile time (dot products fully unrolled); DK = 0
 // reads it from p.dk.
 template <typename T, int DK>
@@ -53,40 +55,27 @@ __global__ __launch_bounds__(256) void stream_attn_kernel(StreamAttnParams p) {
     extern __shared__ float sm[];
     constexpr int VE = 16 / sizeof(T);           // elements per 16-byte vector
     const int b = blockIdx.x, h = blockIdx.y, dk = DK > 0 ? DK : p.dk, D = p.D, Tc = p.Tc, CL = p.CL;
-    const int Tk = CL + Tc, npb = CL + 2 * Tc - 1, ld = dk + VE;
+    const int Tk = CL + Tc, ld = dk + VE;
     float* qu = sm;                              // [Tc][dk]
     float* qv = qu + Tc * dk;                    // [Tc][dk]
     float* sc = qv + Tc * dk;                    // [Tc][Tk]
-    T* ks = (T*)(sc + (Tc * Tk + 3) / 4 * 4);    // [Tk][ld]
-    T* vs = ks + Tk * ld;                        // [Tk][ld]
-    T* ps = vs + Tk * ld;                        // [npb][ld]: row j <-> distance CL + Tc - 1 - j
+    T* vs = (T*)(sc + (Tc * Tk + 3) / 4 * 4);    // [Tk][ld]
     const T* qkv = (const T*)p.qkv;
     T* kring = (T*)p.kc + (int64_t)b * CL * D + h * dk;
     T* vring = (T*)p.vc + (int64_t)b * CL * D + h * dk;
+    // key row kj of [ring in logical order ; chunk]
+    auto key_row = [&](int kj) -> const T* {
+        return kj < CL ? kring + (int64_t)((p.head + kj) % CL) * D
+                       : qkv + (int64_t)(b * Tc + kj - CL) * 3 * D + D + h * dk;
+    };
     // 16-byte loads (dk % 8 == 0, D % 8 == 0), several in flight per thread
     const int vpr = dk / VE;
 #pragma unroll 4
     for (int e = threadIdx.x; e < Tk * vpr; e += blockDim.x) {
         const int r = e / vpr, c0 = (e % vpr) * VE;
-        const T *sk, *sv;
-        if (r < CL) {
-            const int64_t o = (int64_t)((p.head + r) % CL) * D + c0;
-            sk = kring + o;
-            sv = vring + o;
-        } else {
-            const T* row = qkv + (int64_t)(b * Tc + r - CL) * 3 * D + h * dk + c0;
-            sk = row + D;
-            sv = row + 2 * D;
-        }
-        *(int4v*)(ks + r * ld + c0) = *(const int4v*)sk;
+        const T* sv = r < CL ? vring + (int64_t)((p.head + r) % CL) * D + c0
+                             : qkv + (int64_t)(b * Tc + r - CL) * 3 * D + 2 * D + h * dk + c0;
         *(int4v*)(vs + r * ld + c0) = *(const int4v*)sv;
-    }
-    const int prow0 = p.tc_max - Tc;             // global row of band row 0 (distance CL + Tc - 1)
-    const T* ppos = (const T*)p.ppos;
-#pragma unroll 4
-    for (int e = threadIdx.x; e < npb * vpr; e += blockDim.x) {
-        const int r = e / vpr, c0 = (e % vpr) * VE;
-        *(int4v*)(ps + r * ld + c0) = *(const int4v*)(ppos + (int64_t)(prow0 + r) * D + h * dk + c0);
     }
     for (int e = threadIdx.x; e < Tc * dk; e += blockDim.x) {
         const int i = e / dk, c = e % dk;
@@ -95,6 +84,8 @@ __global__ __launch_bounds__(256) void stream_attn_kernel(StreamAttnParams p) {
         qv[e] = q + p.bias_v[h * dk + c];
     }
     __syncthreads();
+    // positional row of distance CL + Tc - 1 - j is ppos row tc_max - Tc + j
+    const T* pband = (const T*)p.ppos + (int64_t)(p.tc_max - Tc) * D + h * dk;
     const int empty = CL - p.clc;
     for (int e = threadIdx.x; e < Tc * Tk; e += blockDim.x) {
         const int i = e / Tk, kj = e % Tk;
@@ -102,12 +93,12 @@ __global__ __launch_bounds__(256) void stream_attn_kernel(StreamAttnParams p) {
         float s = -INFINITY;
         if (kj >= empty && diff >= 0 && diff <= p.left_chunks) {
             // rel_shift of the [Tc][2 Tk - 1] block: column Tc - 1 - i + kj
-            const T* kr = ks + kj * ld;
-            const T* pr = ps + (Tc - 1 - i + kj) * ld;
+            const T* kr = key_row(kj);
+            const T* pr = pband + (int64_t)(Tc - 1 - i + kj) * D;
             const float* a = qu + i * dk;
             const float* a2 = qv + i * dk;
             float ac = 0.f, bd = 0.f;
-#pragma unroll 4
+#pragma unroll 8
             for (int c = 0; c < dk; c += VE) {
                 const int4v kk = *(const int4v*)(kr + c), pk = *(const int4v*)(pr + c);
                 const T* kx = (const T*)&kk;
@@ -147,32 +138,67 @@ __global__ __launch_bounds__(256) void stream_attn_kernel(StreamAttnParams p) {
     }
     __syncthreads();
     T* out = (T*)p.out;
-    for (int e = threadIdx.x; e < Tc * vpr; e += blockDim.x) {
-        const int i = e / vpr, c0 = (e % vpr) * VE;
+    // P.V: the Tc x vpr output vectors, each over KS key slices (all threads
+    // busy when Tc * vpr is small); the slices' partials are summed in slice
+    // order through LDS
+    const int nvo = Tc * vpr, KS = nvo >= (int)blockDim.x ? 1 : (int)blockDim.x / nvo;
+    float* red = (float*)(vs + Tk * ld);         // [KS][nvo][VE] f32, after the values
+    for (int e = threadIdx.x; e < nvo * KS; e += blockDim.x) {
+        const int o = e % nvo, ks = e / nvo;
+        const int i = o / vpr, c0 = (o % vpr) * VE;
         const float* r = sc + i * Tk;
         float acc[VE];
 #pragma unroll
         for (int q = 0; q < VE; ++q) acc[q] = 0.f;
-#pragma unroll 4
-        for (int kj = 0; kj < Tk; ++kj) {
+        const int k0 = ks * Tk / KS, k1 = (ks + 1) * Tk / KS;
+#pragma unroll 2
+        for (int kj = k0; kj < k1; ++kj) {
             const float w = r[kj];
             const int4v vv = *(const int4v*)(vs + kj * ld + c0);
             const T* vx = (const T*)&vv;
 #pragma unroll
             for (int q = 0; q < VE; ++q) acc[q] += w * (float)vx[q];
         }
-        T o[VE];
+        if (KS == 1) {
+            T ov[VE];
 #pragma unroll
-        for (int q = 0; q < VE; ++q) o[q] = to_act<T>(acc[q]);
-        *(int4v*)(out + (int64_t)(b * Tc + i) * D + h * dk + c0) = *(const int4v*)o;
+            for (int q = 0; q < VE; ++q) ov[q] = to_act<T>(acc[q]);
+            *(int4v*)(out + (int64_t)(b * Tc + i) * D + h * dk + c0) = *(const int4v*)ov;
+        } else {
+#pragma unroll
+            for (int q = 0; q < VE; q += 4)
+                *(float4v*)(red + ((int64_t)ks * nvo + o) * VE + q) =
+                    (float4v){acc[q], acc[q + 1], acc[q + 2], acc[q + 3]};
+        }
+    }
+    if (KS > 1) {
+        __syncthreads();
+        for (int o = threadIdx.x; o < nvo; o += blockDim.x) {
+            const int i = o / vpr, c0 = (o % vpr) * VE;
+            float acc[VE];
+#pragma unroll
+            for (int q = 0; q < VE; ++q) acc[q] = red[(int64_t)o * VE + q];
+            for (int ks = 1; ks < KS; ++ks) {
+#pragma unroll
+                for (int q = 0; q < VE; q += 4) {
+                    const float4v v = *(const float4v*)(red + ((int64_t)ks * nvo + o) * VE + q);
+                    acc[q] += v[0], acc[q + 1] += v[1], acc[q + 2] += v[2], acc[q + 3] += v[3];
+                }
+            }
+            T ov[VE];
+#pragma unroll
+            for (int q = 0; q < VE; ++q) ov[q] = to_act<T>(acc[q]);
+            *(int4v*)(out + (int64_t)(b * Tc + i) * D + h * dk + c0) = *(const int4v*)ov;
+        }
     }
     // the chunk's frames take the ring slots of the oldest ones (every ring
-    // read above went through LDS before the barrier): logical order
+    // read of this workgroup is done: the key reads fed the scores before the
+    // barriers above, the value reads went through LDS): logical order
     // [cache[Tc:] ; chunk] with the ring start moved by Tc on the host
     for (int e = threadIdx.x; e < Tc * vpr; e += blockDim.x) {
         const int q = e / vpr, c0 = (e % vpr) * VE;
         const int64_t slot = (int64_t)((p.head + q) % CL) * D + c0;
-        *(int4v*)(kring + slot) = *(const int4v*)(ks + (CL + q) * ld + c0);
+        *(int4v*)(kring + slot) = *(const int4v*)(key_row(CL + q) + c0);
         *(int4v*)(vring + slot) = *(const int4v*)(vs + (CL + q) * ld + c0);
     }
 }
