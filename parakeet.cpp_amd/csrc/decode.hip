@@ -63,43 +63,51 @@ struct MvArgs {
     int T_max;
 };
 
-// One wave per output unit (MV_LSTM: the 4 gate rows of a hidden unit; else
-// one row); lanes stride K in float4, the B items' inputs come from LDS.
+// Two waves per output unit (MV_LSTM: the 4 gate rows of a hidden unit; else
+// one row), each over every other 256-wide K slab: waves 0-3 take the even
+// slabs of units 4 bx + w, waves 4-7 the odd slabs of the same units, and the
+// odd half's sums are added to the even half's through LDS (even + odd, one
+// fixed order). Lanes stride a slab in float4; the items' inputs come from LDS.
 template <int MODE>
-__global__ __launch_bounds__(256) void dec_mv_kernel(MvArgs a, DecState st) {
+__global__ __launch_bounds__(512) void dec_mv_kernel(MvArgs a, DecState st) {
     constexpr int G = MODE == MV_LSTM ? 4 : 1;
+    constexpr int KH = MV_KMAX / 2;   // slabs per wave
     extern __shared__ float xs[];   // [MV_ITEMS][K]
+    __shared__ float zodd[4][MV_ITEMS][G];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int u = blockIdx.x * 4 + w;   // this wave's unit / row
-    // the wave's weight rows, all loads in flight at once, kept for every item pass
-    float4v wv[MV_KMAX][G];
+    const int uw = w & 3, kh = w >> 2;
+    const int u = blockIdx.x * 4 + uw;   // this wave's unit / row
+    // the wave's half of the weight rows, all loads in flight at once, kept for
+    // every item pass (rows past n_out read as zero)
+    float4v wv[KH][G];
 #pragma unroll
-    for (int ki = 0; ki < MV_KMAX; ++ki) {
-        const int k = 4 * lane + 256 * ki;
+    for (int kj = 0; kj < KH; ++kj) {
+        const int k = 4 * lane + 256 * (2 * kj + kh);
 #pragma unroll
         for (int g = 0; g < G; ++g)
-            wv[ki][g] = (u < a.n_out && k < a.K)
+            wv[kj][g] = (u < a.n_out && k < a.K)
                             ? *(const float4v*)(a.W + (int64_t)(MODE == MV_LSTM ? g * a.n_out + u : u) * a.K + k)
                             : float4v{0.f, 0.f, 0.f, 0.f};
     }
     for (int m0 = 0; m0 < a.B; m0 += MV_ITEMS) {
         const int mc = min(MV_ITEMS, a.B - m0);
         __syncthreads();
-        // the items' inputs into LDS, eight 16-byte loads in flight per thread
+        // the items' inputs into LDS, twelve 16-byte loads in flight per thread
+        // (16 items at K <= 1536 in one round)
         const int n4 = mc * (a.K / 4);
-        for (int i0 = threadIdx.x; i0 < n4; i0 += 256 * 8) {
-            float4v v[8];
+        for (int i0 = threadIdx.x; i0 < n4; i0 += 512 * 12) {
+            float4v v[12];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int i = i0 + 256 * j;
+            for (int j = 0; j < 12; ++j) {
+                const int i = i0 + 512 * j;
                 if (i < n4) {
                     const int m = i / (a.K / 4), k4 = i - m * (a.K / 4);
                     v[j] = *(const float4v*)(a.x + (int64_t)(m0 + m) * a.ldx + 4 * k4);
                 }
             }
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int i = i0 + 256 * j;
+            for (int j = 0; j < 12; ++j) {
+                const int i = i0 + 512 * j;
                 if (i < n4) {
                     const int m = i / (a.K / 4), k4 = i - m * (a.K / 4);
                     *(float4v*)(xs + m * a.K + 4 * k4) = v[j];
@@ -107,24 +115,25 @@ __global__ __launch_bounds__(256) void dec_mv_kernel(MvArgs a, DecState st) {
             }
         }
         __syncthreads();
-        if (u >= a.n_out) continue;
         float acc[MV_ITEMS][G];
 #pragma unroll
         for (int m = 0; m < MV_ITEMS; ++m)
 #pragma unroll
             for (int g = 0; g < G; ++g) acc[m][g] = 0.f;
 #pragma unroll
-        for (int ki = 0; ki < MV_KMAX; ++ki) {
-            const int k = 4 * lane + 256 * ki;
-            if (k >= a.K) break;
+        for (int kj = 0; kj < KH; ++kj) {
+            const int k = 4 * lane + 256 * (2 * kj + kh);
+            if (256 * (2 * kj + kh) >= a.K) break;   // uniform over the wave
+            if (k < a.K) {
 #pragma unroll
-            for (int m = 0; m < MV_ITEMS; ++m) {
-                if (m < mc) {
-                    const float4v xv = *(const float4v*)(xs + m * a.K + k);
+                for (int m = 0; m < MV_ITEMS; ++m) {
+                    if (m < mc) {
+                        const float4v xv = *(const float4v*)(xs + m * a.K + k);
 #pragma unroll
-                    for (int g = 0; g < G; ++g)
-                        acc[m][g] += (wv[ki][g][0] * xv[0] + wv[ki][g][1] * xv[1]) +
-                                     (wv[ki][g][2] * xv[2] + wv[ki][g][3] * xv[3]);
+                        for (int g = 0; g < G; ++g)
+                            acc[m][g] += (wv[kj][g][0] * xv[0] + wv[kj][g][1] * xv[1]) +
+                                         (wv[kj][g][2] * xv[2] + wv[kj][g][3] * xv[3]);
+                    }
                 }
             }
         }
@@ -167,7 +176,16 @@ __global__ __launch_bounds__(256) void dec_mv_kernel(MvArgs a, DecState st) {
                     if (m == lane) z[g] = acc[m][g];
             }
         }
-        if (lane >= mc) continue;
+        // the odd-slab half hands its sums to the even half (every wave reaches
+        // this barrier; the next pass's staging waits behind the one above)
+        if (kh == 1 && lane < MV_ITEMS) {
+#pragma unroll
+            for (int g = 0; g < G; ++g) zodd[uw][lane][g] = z[g];
+        }
+        __syncthreads();
+        if (kh == 1 || u >= a.n_out || lane >= mc) continue;
+#pragma unroll
+        for (int g = 0; g < G; ++g) z[g] += zodd[uw][lane][g];
         const int b = m0 + lane;
         if constexpr (MODE == MV_LSTM) {
             const int H = a.n_out;
@@ -426,7 +444,7 @@ void Model::transducer_greedy(const float* enc, int B, int T_max, const int* T_v
             a.out_c = oc[l];
             a.x_next = l + 1 < L ? X[l + 1] : g;
             a.ld_next = l + 1 < L ? 2 * H : H;
-            launch(dec_mv_kernel<MV_LSTM>, dim3(cdiv(H, 4)), dim3(256), (uint32_t)(MV_ITEMS * 2 * H * 4), s, a, st);
+            launch(dec_mv_kernel<MV_LSTM>, dim3(cdiv(H, 4)), dim3(512), (uint32_t)(MV_ITEMS * 2 * H * 4), s, a, st);
             PKX_LAUNCH_CHECK();
         }
         MvArgs j{};
@@ -440,7 +458,7 @@ void Model::transducer_greedy(const float* enc, int B, int T_max, const int* T_v
         j.y = f;
         j.ep = ep;
         j.T_max = T_max;
-        launch(dec_mv_kernel<MV_JOINT>, dim3(cdiv(Hj, 4)), dim3(256), (uint32_t)(MV_ITEMS * H * 4), s, j, st);
+        launch(dec_mv_kernel<MV_JOINT>, dim3(cdiv(Hj, 4)), dim3(512), (uint32_t)(MV_ITEMS * H * 4), s, j, st);
         PKX_LAUNCH_CHECK();
         MvArgs o{};
         o.x = f;
@@ -451,7 +469,7 @@ void Model::transducer_greedy(const float* enc, int B, int T_max, const int* T_v
         o.bias = heads_.jout_b;
         o.n_out = Vp;
         o.y = lg;
-        launch(dec_mv_kernel<MV_PLAIN>, dim3(cdiv(Vp, 4)), dim3(256), (uint32_t)(MV_ITEMS * Hj * 4), s, o, st);
+        launch(dec_mv_kernel<MV_PLAIN>, dim3(cdiv(Vp, 4)), dim3(512), (uint32_t)(MV_ITEMS * Hj * 4), s, o, st);
         PKX_LAUNCH_CHECK();
         launch(greedy_rule_kernel, dim3(B), dim3(256), 0, s, ra, st);
         PKX_LAUNCH_CHECK();

@@ -118,7 +118,12 @@ def test_greedy_decode_production_shape(gpu, stream):
         total += len(ids)
         assert np.array_equal(g_ids, ids), (b, g_ids[:20], ids[:20])
         assert np.array_equal(g_fr, fr) and np.array_equal(g_sp, sp)
-        assert np.max(np.abs(g_cf - cf), initial=0.0) <= 1e-5
+        # The joint output is scaled x60 here, so logits reach a few hundred,
+        # where one f32 ulp is 1.5e-5-3e-5; device and oracle sum the K = 640
+        # products in different orders, so each logit may differ by a few ulps.
+        # The confidence (N p - 1) / (N - 1), p = 1 / sum exp(l - l_max), moves
+        # by at most ~2 max|dl| * p: 5e-5 covers two ulps at |l| ~ 256.
+        assert np.max(np.abs(g_cf - cf), initial=0.0) <= 5e-5
     print(f"[decode] {total} tokens identical over {B} items", flush=True)
     assert total > 100
     d_enc.free()
