@@ -63,15 +63,18 @@ struct MvArgs {
     int T_max;
 };
 
-// Two waves per output unit (MV_LSTM: the 4 gate rows of a hidden unit; else
-// one row), each over every other 256-wide K slab: waves 0-3 take the even
-// slabs of units 4 bx + w, waves 4-7 the odd slabs of the same units, and the
-// odd half's sums are added to the even half's through LDS (even + odd, one
-// fixed order). Lanes stride a slab in float4; the items' inputs come from LDS.
-template <int MODE>
-__global__ __launch_bounds__(512) void dec_mv_kernel(MvArgs a, DecState st) {
+// KS waves per output unit (MV_LSTM: the 4 gate rows of a hidden unit; else
+// one row). With KS = 2 each takes every other 256-wide K slab: waves 0-3 the
+// even slabs of units 4 bx + w, waves 4-7 the odd slabs of the same units, and
+// the odd half's sums are added to the even half's through LDS (even + odd,
+// one fixed order). Lanes stride a slab in float4; the items' inputs come
+// from LDS.
+template <int MODE, int KS>
+__global__ __launch_bounds__(256 * KS) void dec_mv_kernel(MvArgs a, DecState st) {
+    static_assert(KS == 1 || KS == 2, "one or two waves per unit");
     constexpr int G = MODE == MV_LSTM ? 4 : 1;
-    constexpr int KH = MV_KMAX / 2;   // slabs per wave
+    constexpr int KH = MV_KMAX / KS;   // slabs per wave
+    constexpr int NT = 256 * KS;
     extern __shared__ float xs[];   // [MV_ITEMS][K]
     __shared__ float zodd[4][MV_ITEMS][G];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -82,7 +85,7 @@ __global__ __launch_bounds__(512) void dec_mv_kernel(MvArgs a, DecState st) {
     float4v wv[KH][G];
 #pragma unroll
     for (int kj = 0; kj < KH; ++kj) {
-        const int k = 4 * lane + 256 * (2 * kj + kh);
+        const int k = 4 * lane + 256 * (KS * kj + kh);
 #pragma unroll
         for (int g = 0; g < G; ++g)
             wv[kj][g] = (u < a.n_out && k < a.K)
@@ -95,11 +98,11 @@ __global__ __launch_bounds__(512) void dec_mv_kernel(MvArgs a, DecState st) {
         // the items' inputs into LDS, twelve 16-byte loads in flight per thread
         // (16 items at K <= 1536 in one round)
         const int n4 = mc * (a.K / 4);
-        for (int i0 = threadIdx.x; i0 < n4; i0 += 512 * 12) {
+        for (int i0 = threadIdx.x; i0 < n4; i0 += NT * 12) {
             float4v v[12];
 #pragma unroll
             for (int j = 0; j < 12; ++j) {
-                const int i = i0 + 512 * j;
+                const int i = i0 + NT * j;
                 if (i < n4) {
                     const int m = i / (a.K / 4), k4 = i - m * (a.K / 4);
                     v[j] = *(const float4v*)(a.x + (int64_t)(m0 + m) * a.ldx + 4 * k4);
@@ -107,7 +110,7 @@ __global__ __launch_bounds__(512) void dec_mv_kernel(MvArgs a, DecState st) {
             }
 #pragma unroll
             for (int j = 0; j < 12; ++j) {
-                const int i = i0 + 512 * j;
+                const int i = i0 + NT * j;
                 if (i < n4) {
                     const int m = i / (a.K / 4), k4 = i - m * (a.K / 4);
                     *(float4v*)(xs + m * a.K + 4 * k4) = v[j];
@@ -122,8 +125,8 @@ __global__ __launch_bounds__(512) void dec_mv_kernel(MvArgs a, DecState st) {
             for (int g = 0; g < G; ++g) acc[m][g] = 0.f;
 #pragma unroll
         for (int kj = 0; kj < KH; ++kj) {
-            const int k = 4 * lane + 256 * (2 * kj + kh);
-            if (256 * (2 * kj + kh) >= a.K) break;   // uniform over the wave
+            const int k = 4 * lane + 256 * (KS * kj + kh);
+            if (256 * (KS * kj + kh) >= a.K) break;   // uniform over the wave
             if (k < a.K) {
 #pragma unroll
                 for (int m = 0; m < MV_ITEMS; ++m) {
@@ -178,14 +181,18 @@ __global__ __launch_bounds__(512) void dec_mv_kernel(MvArgs a, DecState st) {
         }
         // the odd-slab half hands its sums to the even half (every wave reaches
         // this barrier; the next pass's staging waits behind the one above)
-        if (kh == 1 && lane < MV_ITEMS) {
+        if constexpr (KS == 2) {
+            if (kh == 1 && lane < MV_ITEMS) {
 #pragma unroll
-            for (int g = 0; g < G; ++g) zodd[uw][lane][g] = z[g];
+                for (int g = 0; g < G; ++g) zodd[uw][lane][g] = z[g];
+            }
+            __syncthreads();
         }
-        __syncthreads();
         if (kh == 1 || u >= a.n_out || lane >= mc) continue;
+        if constexpr (KS == 2) {
 #pragma unroll
-        for (int g = 0; g < G; ++g) z[g] += zodd[uw][lane][g];
+            for (int g = 0; g < G; ++g) z[g] += zodd[uw][lane][g];
+        }
         const int b = m0 + lane;
         if constexpr (MODE == MV_LSTM) {
             const int H = a.n_out;
@@ -268,8 +275,30 @@ __global__ __launch_bounds__(256) void greedy_rule_kernel(RuleArgs a, DecState s
     __shared__ float rv[4];
     __shared__ int rk[4];
     __shared__ double rd[4];
+    __shared__ int dur_s[32];
     const int b = blockIdx.x, tid = threadIdx.x;
     if (!st.active[b]) return;   // uniform over the workgroup
+    // The item's state is read and written only by thread 0 of this workgroup:
+    // its loads go out now, beside the logits', not after the commit stores.
+    int t = 0, sym = 0, cnt = 0;
+    if (tid == 0) {
+        t = st.t[b];
+        sym = st.sym[b];
+        cnt = st.count[b];
+    }
+    if (tid < a.n_dur && tid < 32) dur_s[tid] = a.durations[tid];   // visible after block_argmax's barriers
+    // this step's (h', c') rows, loaded now and stored by the commit if the item
+    // emits (L <= 4, H <= 1024: at most 4 x 4 values of each per thread)
+    float ph[4][4], pc[4][4];
+#pragma unroll
+    for (int l = 0; l < 4; ++l)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int j = tid + 256 * r;
+            const bool ok = l < a.L && j < a.H;
+            ph[l][r] = ok ? a.oh[l][(int64_t)b * a.H + j] : 0.f;
+            pc[l][r] = ok ? a.oc[l][(int64_t)b * a.H + j] : 0.f;
+        }
     const float* lz = a.logits + (int64_t)b * a.Vp;
     float v;
     const int k = block_argmax(lz, a.n_tok, v, rv, rk);
@@ -289,18 +318,22 @@ __global__ __launch_bounds__(256) void greedy_rule_kernel(RuleArgs a, DecState s
         den = (rd[0] + rd[1]) + (rd[2] + rd[3]);
         // commit: the step's (h', c') become the item's state; the token's
         // embedding is the next step's layer-0 input
-        for (int l = 0; l < a.L; ++l)
-            for (int j = tid; j < a.H; j += 256) {
-                a.X[l][(int64_t)b * 2 * a.H + a.H + j] = a.oh[l][(int64_t)b * a.H + j];
-                a.cc[l][(int64_t)b * a.H + j] = a.oc[l][(int64_t)b * a.H + j];
+#pragma unroll
+        for (int l = 0; l < 4; ++l)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int j = tid + 256 * r;
+                if (l < a.L && j < a.H) {
+                    a.X[l][(int64_t)b * 2 * a.H + a.H + j] = ph[l][r];
+                    a.cc[l][(int64_t)b * a.H + j] = pc[l][r];
+                }
             }
         for (int j = tid; j < a.H; j += 256) a.X[0][(int64_t)b * 2 * a.H + j] = a.embed[(int64_t)k * a.H + j];
     }
     if (tid != 0) return;
-    int t = st.t[b], sym = st.sym[b];
-    const int skip = a.n_dur > 0 ? a.durations[dk] : 1;
+    const int skip = a.n_dur > 0 ? (dk < 32 ? dur_s[dk] : a.durations[dk]) : 1;
     if (emit) {
-        const int n = st.count[b];
+        const int n = cnt;
         if (n < a.cap) {
             const double p = 1.0 / den, N = (double)a.n_tok;   // exp(v - v) / den
             a.ids[(int64_t)b * a.cap + n] = k;
@@ -426,8 +459,8 @@ void Model::transducer_greedy(const float* enc, int B, int T_max, const int* T_v
     ra.confs = d_cf;
 
     const size_t lds_max = (size_t)MV_ITEMS * std::max(2 * H, std::max(H, Hj)) * sizeof(float);
-    for (const void* fn : {(const void*)dec_mv_kernel<MV_LSTM>, (const void*)dec_mv_kernel<MV_JOINT>,
-                           (const void*)dec_mv_kernel<MV_PLAIN>})
+    for (const void* fn : {(const void*)dec_mv_kernel<MV_LSTM, 2>, (const void*)dec_mv_kernel<MV_JOINT, 2>,
+                           (const void*)dec_mv_kernel<MV_PLAIN, 1>})
         PKX_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_max));
     auto round = [&]() {
         for (int l = 0; l < L; ++l) {
@@ -444,7 +477,7 @@ void Model::transducer_greedy(const float* enc, int B, int T_max, const int* T_v
             a.out_c = oc[l];
             a.x_next = l + 1 < L ? X[l + 1] : g;
             a.ld_next = l + 1 < L ? 2 * H : H;
-            launch(dec_mv_kernel<MV_LSTM>, dim3(cdiv(H, 4)), dim3(512), (uint32_t)(MV_ITEMS * 2 * H * 4), s, a, st);
+            launch(dec_mv_kernel<MV_LSTM, 2>, dim3(cdiv(H, 4)), dim3(512), (uint32_t)(MV_ITEMS * 2 * H * 4), s, a, st);
             PKX_LAUNCH_CHECK();
         }
         MvArgs j{};
@@ -458,7 +491,7 @@ void Model::transducer_greedy(const float* enc, int B, int T_max, const int* T_v
         j.y = f;
         j.ep = ep;
         j.T_max = T_max;
-        launch(dec_mv_kernel<MV_JOINT>, dim3(cdiv(Hj, 4)), dim3(512), (uint32_t)(MV_ITEMS * H * 4), s, j, st);
+        launch(dec_mv_kernel<MV_JOINT, 2>, dim3(cdiv(Hj, 4)), dim3(512), (uint32_t)(MV_ITEMS * H * 4), s, j, st);
         PKX_LAUNCH_CHECK();
         MvArgs o{};
         o.x = f;
@@ -469,7 +502,7 @@ void Model::transducer_greedy(const float* enc, int B, int T_max, const int* T_v
         o.bias = heads_.jout_b;
         o.n_out = Vp;
         o.y = lg;
-        launch(dec_mv_kernel<MV_PLAIN>, dim3(cdiv(Vp, 4)), dim3(512), (uint32_t)(MV_ITEMS * Hj * 4), s, o, st);
+        launch(dec_mv_kernel<MV_PLAIN, 1>, dim3(cdiv(Vp, 4)), dim3(256), (uint32_t)(MV_ITEMS * Hj * 4), s, o, st);
         PKX_LAUNCH_CHECK();
         launch(greedy_rule_kernel, dim3(B), dim3(256), 0, s, ra, st);
         PKX_LAUNCH_CHECK();
