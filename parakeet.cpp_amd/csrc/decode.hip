@@ -94,6 +94,24 @@ __global__ __launch_bounds__(256 * KS) void dec_mv_kernel(MvArgs a, DecState st)
     }
     for (int m0 = 0; m0 < a.B; m0 += MV_ITEMS) {
         const int mc = min(MV_ITEMS, a.B - m0);
+        // the epilogue's operands for item m0 + lane, loaded ahead of the
+        // staging so that their latency overlaps it
+        const bool epi = kh == 0 && u < a.n_out && lane < mc;
+        const int b = m0 + lane;
+        float pb[G], pc = 0.f;
+#pragma unroll
+        for (int g = 0; g < G; ++g) pb[g] = epi ? a.bias[g * a.n_out + u] : 0.f;
+        if constexpr (MODE == MV_LSTM) {
+            if (epi) pc = a.c_in[(int64_t)b * a.n_out + u];
+        } else if constexpr (MODE == MV_JOINT) {
+            if (epi) {
+                int t = st.t[b];
+                const int T = st.T[b];
+                t = t > T - 1 ? T - 1 : t;   // inactive / boundary items (their logits are not used)
+                t = t < 0 ? 0 : t;
+                pc = a.ep[((int64_t)b * a.T_max + t) * a.n_out + u];
+            }
+        }
         __syncthreads();
         // the items' inputs into LDS, twelve 16-byte loads in flight per thread
         // (16 items at K <= 1536 in one round)
@@ -188,31 +206,26 @@ __global__ __launch_bounds__(256 * KS) void dec_mv_kernel(MvArgs a, DecState st)
             }
             __syncthreads();
         }
-        if (kh == 1 || u >= a.n_out || lane >= mc) continue;
+        if (!epi) continue;
         if constexpr (KS == 2) {
 #pragma unroll
             for (int g = 0; g < G; ++g) z[g] += zodd[uw][lane][g];
         }
-        const int b = m0 + lane;
         if constexpr (MODE == MV_LSTM) {
             const int H = a.n_out;
-            const float zi = z[0] + a.bias[u], zf = z[1] + a.bias[H + u];
-            const float zg = z[2] + a.bias[2 * H + u], zo = z[3] + a.bias[3 * H + u];
+            const float zi = z[0] + pb[0], zf = z[1] + pb[1];
+            const float zg = z[2] + pb[2], zo = z[3] + pb[3];
             const int64_t i = (int64_t)b * H + u;
-            const float c = sigmoid_ref(zf) * a.c_in[i] + sigmoid_ref(zi) * tanhf(zg);
+            const float c = sigmoid_ref(zf) * pc + sigmoid_ref(zi) * tanhf(zg);
             const float h = sigmoid_ref(zo) * tanhf(c);
             a.out_c[i] = c;
             a.out_h[i] = h;
             a.x_next[(int64_t)b * a.ld_next + u] = h;
         } else if constexpr (MODE == MV_JOINT) {
-            int t = st.t[b];
-            const int T = st.T[b];
-            t = t > T - 1 ? T - 1 : t;   // inactive / boundary items (their logits are not used)
-            t = t < 0 ? 0 : t;
-            const float v = a.ep[((int64_t)b * a.T_max + t) * a.n_out + u] + (z[0] + a.bias[u]);
+            const float v = pc + (z[0] + pb[0]);
             a.y[(int64_t)b * a.n_out + u] = v > 0.f ? v : 0.f;
         } else {
-            a.y[(int64_t)b * a.n_out + u] = z[0] + a.bias[u];
+            a.y[(int64_t)b * a.n_out + u] = z[0] + pb[0];
         }
     }
 }
