@@ -73,7 +73,11 @@ inline void require(bool ok, const std::string& msg) {
 
 // v_rcp_f32 (1 ulp) instead of an IEEE division: the epilogues apply these to
 // every GEMM output; exp overflow gives rcp(inf) = 0, the correct limit.
-__device__ __forceinline__ float sigmoid_dev(float v) { return __builtin_amdgcn_rcpf(1.0f + __expf(-v)); }
+// e^-v as the bare v_exp_f32 of -v log2(e): without the denormal-range fix-up
+// of __expf, whose results only differ where 1 + e^-v rounds to 1 anyway.
+__device__ __forceinline__ float sigmoid_dev(float v) {
+    return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(v * -1.4426950408889634f));
+}
 __device__ __forceinline__ float silu_dev(float v) { return v * sigmoid_dev(v); }
 
 template <typename T> __device__ __forceinline__ T to_act(float v);

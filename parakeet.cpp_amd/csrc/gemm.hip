@@ -1395,6 +1395,363 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
 }
 
 // ===========================================================================
+// Register-B kernel (gemm_rb_kernel): only the activation tile goes through
+// LDS; the weights stream from L2 straight into registers.
+//
+// Four waves side by side along N, each owning 32 WTM rows x 32 WTN columns of
+// a (32 WTM) x (128 WTN) workgroup tile, one workgroup per CU.  A wave's
+// weight columns are its own, so each weight is loaded and dequantised once
+// per workgroup and never written to or read from LDS; the A tile (BM rows x
+// 64 K per slab) arrives by global_load_lds DMA into an NS-stage ring and is
+// read by all four waves.  LDS bytes per slab: BM*128 written + 4*BM*128 read,
+// i.e. 5/BN bytes per flop (the 128 x 128 LDS-B kernel moves about 2.4x that).
+//
+// Per slab k one barrier, then the slab k+NS-1 loads are issued (A DMA, B
+// register loads; slabs past K read out of range and return zeros, so the
+// wait counts never change), then the MFMAs of slab k run interleaved with the
+// LDS reads of A(k+1) and the dequantisation of B(k+1) into the other half of
+// the double-buffered fragments.  The lane's K order (k = 32q + 8s + e for lane
+// half q and substep s) is the LDS-B kernel's: each lane's weight bytes of a
+// slab are one contiguous 32-byte run of one q8_0 block.
+// ===========================================================================
+
+// One wave's raw weight registers for one 64-deep slab: WTN blocks of 32
+// columns; lane (q = lane / 32, c = lane % 32) holds column c of each block
+// over k = 32q .. 32q + 31 of the slab.
+template <int WT, int WTN> struct BRaw;
+
+template <int WTN> struct BRaw<GT_Q8_0, WTN> {
+    int4v q[WTN][2];
+    uint32_t d[WTN];
+    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rq, __amdgpu_buffer_rsrc_t rs, const uint32_t (&vq)[WTN],
+                                         const uint32_t (&vs)[WTN], int soq, int sos) {
+#pragma unroll
+        for (int j = 0; j < WTN; ++j) {
+            q[j][0] = __builtin_amdgcn_raw_buffer_load_b128(rq, (int)vq[j], soq, 0);
+            q[j][1] = __builtin_amdgcn_raw_buffer_load_b128(rq, (int)(vq[j] + 16), soq, 0);
+            d[j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, (int)vs[j], sos, 0);
+        }
+    }
+    __device__ __forceinline__ void convert_j(half8v (&bf)[4], int j, int) const {
+        const f16 dh = __builtin_bit_cast(f16, (uint16_t)d[j]);
+        const half2v m2 = {dh, dh};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            half2v h0, h1, h2, h3;
+            i8x4_to_f16((uint32_t)q[j][s >> 1][2 * (s & 1)], m2, h0, h1);
+            i8x4_to_f16((uint32_t)q[j][s >> 1][2 * (s & 1) + 1], m2, h2, h3);
+            bf[s] = (half8v){h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
+        }
+    }
+};
+
+// q4_K: both lane halves load the column's 32 nibble bytes (half q takes the
+// low (q = 0) or high (q = 1) nibbles) and their own {d*sc, dmin*m} pair.
+template <int WTN> struct BRaw<GT_Q4_K, WTN> {
+    int4v q[WTN][2];
+    float2v s[WTN];
+    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rq, __amdgpu_buffer_rsrc_t rs, const uint32_t (&vq)[WTN],
+                                         const uint32_t (&vs)[WTN], int soq, int sos) {
+#pragma unroll
+        for (int j = 0; j < WTN; ++j) {
+            q[j][0] = __builtin_amdgcn_raw_buffer_load_b128(rq, (int)vq[j], soq, 0);
+            q[j][1] = __builtin_amdgcn_raw_buffer_load_b128(rq, (int)(vq[j] + 16), soq, 0);
+            s[j] = __builtin_bit_cast(float2v, __builtin_amdgcn_raw_buffer_load_b64(rs, (int)vs[j], sos, 0));
+        }
+    }
+    __device__ __forceinline__ void convert_j(half8v (&bf)[4], int j, int q_half) const {
+        const half2v m2 = {(f16)s[j].x, (f16)s[j].x};
+        const half2v nm2 = {(f16)-s[j].y, (f16)-s[j].y};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            half2v h0, h1, h2, h3;
+            nib4_to_f16((uint32_t)q[j][t >> 1][2 * (t & 1)], q_half, m2, nm2, h0, h1);
+            nib4_to_f16((uint32_t)q[j][t >> 1][2 * (t & 1) + 1], q_half, m2, nm2, h2, h3);
+            bf[t] = (half8v){h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
+        }
+    }
+};
+
+// f16 weights, row-major [N][K]: the lane's 32 halves are 64 contiguous bytes.
+template <int WTN> struct BRaw<GT_F16, WTN> {
+    int4v q[WTN][4];
+    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rq, __amdgpu_buffer_rsrc_t, const uint32_t (&vq)[WTN],
+                                         const uint32_t (&)[WTN], int soq, int) {
+#pragma unroll
+        for (int j = 0; j < WTN; ++j)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) q[j][t] = __builtin_amdgcn_raw_buffer_load_b128(rq, (int)(vq[j] + 16 * t), soq, 0);
+    }
+    __device__ __forceinline__ void convert_j(half8v (&bf)[4], int j, int) const {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) bf[t] = __builtin_bit_cast(half8v, q[j][t]);
+    }
+};
+
+// Vector-memory instructions of one slab's weight loads per wave.
+template <int WT, int WTN>
+constexpr int rb_b_ops() { return WT == GT_F16 ? 4 * WTN : 3 * WTN; }
+
+template <int WTM, int WTN, int WT, int EPI, int NS, int TD = 0, bool FO = false>
+struct RbCfg {
+    static constexpr int BM = 32 * WTM, BN = 128 * WTN;
+    static constexpr int A_STAGE = BM * 128;                  // f16 [BM][64]
+    static constexpr int NA = A_STAGE / 4096;                 // 1 KB A DMAs per wave per slab
+    static constexpr int NB = rb_b_ops<WT, WTN>();
+    static constexpr int NT = TD > 0 ? 2 : 0;                 // L2 touch DMAs per wave per slab
+    static constexpr int PER_SLAB = NA + NB + NT;
+    static constexpr int NR = 4;                              // weight register sets (>= NS - 1 in flight)
+    static constexpr int U = 4;                               // loop unroll: every ring index static
+    static constexpr bool FOLD = FO && (EPI == EPI_STORE || EPI == EPI_SILU);
+    static constexpr int FOLD_BYTES = FOLD ? BM * 32 * 8 : 0; // {mean, M2} of up to 32 groups per row
+    static constexpr int TOUCH = TD > 0 ? 256 : 0;            // destination of the touch DMAs
+    static constexpr int MAIN = NS * A_STAGE + FOLD_BYTES + TOUCH;
+    static constexpr int STG_WHOLE = 4 * 32 * WTM * (32 * WTN + 4) * 4;
+    static constexpr bool WHOLE = STG_WHOLE + BM * 8 <= 160 * 1024 - 1024;
+    static constexpr int STG = WHOLE ? STG_WHOLE : STG_WHOLE / 2;
+    static constexpr int LDS = (MAIN > STG ? MAIN : STG) + BM * 8;
+    static_assert(A_STAGE % 4096 == 0, "A slab splits into 1 KB DMAs per wave");
+    static_assert(LDS <= 160 * 1024, "LDS budget");
+    static_assert(WHOLE || WTM % 2 == 0, "row-half staging needs an even WTM");
+};
+
+template <int WTM, int WTN, int WT, int EPI, int NS, int TD = 0, bool FO = false>
+__global__ __launch_bounds__(256, 1) void gemm_rb_kernel(GemmParams p) {
+    typedef RbCfg<WTM, WTN, WT, EPI, NS, TD, FO> C;
+    static_assert(NS >= 3 && NS <= 5, "ring depth");
+    static_assert(EPI == EPI_STORE || EPI == EPI_STORE_F32 || EPI == EPI_SILU || EPI == EPI_RESID ||
+                      EPI == EPI_RESID_LN,
+                  "register-B kernel: LDS-staged epilogues only");
+    constexpr int BM = C::BM, NR = C::NR;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[C::LDS];
+
+    const int tid = threadIdx.x, lane = tid & 63, wid = wave_id_uniform();
+    const int q = lane >> 5, r32 = lane & 31;
+    int bm, bn;
+    xcd_tile_2d(blockIdx.x, cdiv_dev(p.M, BM), cdiv_dev(p.N, C::BN), p.xcd_gm, bm, bn);
+    const int m0 = bm * BM, n0 = bn * C::BN, nw = n0 + wid * 32 * WTN;
+    const int nk = p.K / 64;
+
+    // folded LayerNorm (FO: p.fold_stats is set) statistics of the tile's rows:
+    // DMA into LDS first (the oldest vector-memory operations, complete by the
+    // first slab's wait)
+    constexpr bool fold = C::FOLD;
+    if constexpr (C::FOLD) {
+        if (fold) {
+            const int lc = __builtin_ctz(p.fold_groups / 2), total = BM << lc;   // 16-byte chunks
+            const __amdgpu_buffer_rsrc_t rf =
+                make_rsrc((const float2v*)p.fold_stats + (int64_t)m0 * p.fold_groups,
+                          ((int64_t)(p.M - m0) * p.fold_groups) * 8);
+            uint8_t* fl = smem + NS * C::A_STAGE;
+            for (int c0 = wid * 64; c0 < total; c0 += 256) {
+                const int ch = c0 + lane, r = ch >> lc;
+                const uint32_t off = ch < total ? (uint32_t)(min(r, p.M - 1 - m0) << (lc + 4)) + ((ch & ((1 << lc) - 1)) << 4)
+                                                : OOB;
+                lds_dma16(rf, fl + c0 * 16, off, 0);
+            }
+        }
+    }
+    EpiCols<WTN> ecol;
+    ecol.load(p, nw, lane, fold, EPI == EPI_RESID_LN);
+
+    // A: 64-column slabs of rows m0.., swizzled 16-byte chunks (as DmaSrc)
+    const __amdgpu_buffer_rsrc_t ra =
+        make_rsrc((const f16*)p.A + (int64_t)m0 * p.lda, ((int64_t)(p.M - m0 - 1) * p.lda + p.K) * 2);
+    uint32_t va[C::NA];
+#pragma unroll
+    for (int i = 0; i < C::NA; ++i) {
+        const int slot = (wid * C::NA + i) * 64 + lane;
+        const int row = slot >> 3, c = (slot & 7) ^ ((row >> 1) & 7);
+        const int m = min(m0 + row, p.M - 1) - m0;
+        va[i] = (uint32_t)(((int64_t)m * p.lda + 8 * c) * 2);
+    }
+    // weights: per block j the lane's byte offset in slab 0 (columns past N: out of range)
+    const int L = slab_rows(p);
+    __amdgpu_buffer_rsrc_t rq = make_rsrc(p.Wq, 0), rs = rq;
+    uint32_t vq[WTN], vs[WTN];
+    if constexpr (WT == GT_Q8_0 || WT == GT_Q4_K) {
+        constexpr int WB = WT == GT_Q8_0 ? 64 : 32, SB = WT == GT_Q8_0 ? 4 : 16;
+        // a view into a larger weight keeps the allocation's slab stride L: its
+        // last byte is in slab nk-1, row N-1
+        rq = make_rsrc(p.Wq, ((int64_t)(nk - 1) * L + p.N) * WB);
+        rs = make_rsrc(p.Ws, ((int64_t)(nk - 1) * L + p.N) * SB);
+#pragma unroll
+        for (int j = 0; j < WTN; ++j) {
+            const int n = nw + 32 * j + r32;
+            vq[j] = n < p.N ? (uint32_t)(n * WB + (WT == GT_Q8_0 ? 32 * q : 0)) : OOB;
+            vs[j] = n < p.N ? (uint32_t)(n * SB + (WT == GT_Q8_0 ? 2 * q : 8 * q)) : OOB;
+        }
+    } else {
+        rq = make_rsrc(p.Wq, (int64_t)p.N * p.K * 2);
+#pragma unroll
+        for (int j = 0; j < WTN; ++j) {
+            const int n = nw + 32 * j + r32;
+            vq[j] = n < p.N ? (uint32_t)(((int64_t)n * p.K + 32 * q) * 2) : OOB;
+            vs[j] = 0;
+        }
+    }
+    // scalar offsets of slab k (out of range past the last slab)
+    auto soq = [&](int k) -> int {
+        if (k >= nk) return (int)OOB;
+        return WT == GT_Q8_0 ? k * L * 64 : WT == GT_Q4_K ? k * L * 32 : k * 128;
+    };
+    auto sos = [&](int k) -> int {
+        if (k >= nk) return (int)OOB;
+        return WT == GT_Q8_0 ? k * L * 4 : WT == GT_Q4_K ? k * L * 16 : 0;
+    };
+    auto issue_a = [&](int k) {
+        uint8_t* st = smem + (k % NS) * C::A_STAGE + wid * C::NA * 1024;
+        const int so = k < nk ? k * 128 : (int)OOB;
+#pragma unroll
+        for (int i = 0; i < C::NA; ++i) lds_dma16(ra, st + i * 1024, va[i], so);
+    };
+    // L2 touch-ahead (TD > 0): slab k + TD's cache lines of this wave's A rows
+    // and weight columns are requested TD slabs early by two 4-byte DMAs into
+    // a scratch word per lane, so the slab's real loads hit in L2.  Lane
+    // addresses: line of slab 0 plus a per-slab stride.
+    const uint8_t* tb[2] = {nullptr, nullptr};
+    uint32_t ts[2] = {0, 0};
+    if constexpr (TD > 0) {
+        constexpr int RW = BM / 4;   // A rows touched per wave
+        const int cmax = p.N - 1;
+        if (lane < RW) {
+            tb[0] = (const uint8_t*)((const f16*)p.A + (int64_t)min(m0 + wid * RW + lane, p.M - 1) * p.lda);
+            ts[0] = 128;
+        } else if constexpr (WT == GT_Q8_0) {
+            tb[0] = (const uint8_t*)p.Ws + (int64_t)min(nw + 32 * ((lane - RW) & 1), cmax) * 4;
+            ts[0] = (uint32_t)L * 4;
+        } else if constexpr (WT == GT_Q4_K) {
+            tb[0] = (const uint8_t*)p.Ws + (int64_t)min(nw + 8 * ((lane - RW) & 7), cmax) * 16;
+            ts[0] = (uint32_t)L * 16;
+        } else {
+            tb[0] = (const uint8_t*)((const f16*)p.A + (int64_t)min(m0 + wid * RW + lane % RW, p.M - 1) * p.lda);
+            ts[0] = 128;
+        }
+        if constexpr (WT == GT_Q8_0) {
+            tb[1] = (const uint8_t*)p.Wq + (int64_t)min(nw + 2 * (lane & 31), cmax) * 64;
+            ts[1] = (uint32_t)L * 64;
+        } else if constexpr (WT == GT_Q4_K) {
+            tb[1] = (const uint8_t*)p.Wq + (int64_t)min(nw + 4 * (lane & 15), cmax) * 32;
+            ts[1] = (uint32_t)L * 32;
+        } else {
+            tb[1] = (const uint8_t*)p.Wq + (int64_t)min(nw + lane, cmax) * p.K * 2;
+            ts[1] = 128;
+        }
+    }
+    auto touch = [&](int k) {
+        if constexpr (TD > 0) {
+            const int kc = min(max(k, 0), nk - 1);
+            uint8_t* dst = smem + NS * C::A_STAGE + C::FOLD_BYTES;
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+                __builtin_amdgcn_global_load_lds(
+                    (const __attribute__((address_space(1))) void*)(tb[t] + (uint64_t)kc * ts[t]),
+                    (__attribute__((address_space(3))) void*)dst, 4, 0, 0);
+        }
+    };
+
+    float16v acc[WTM][WTN];
+#pragma unroll
+    for (int i = 0; i < WTM; ++i)
+#pragma unroll
+        for (int j = 0; j < WTN; ++j) acc[i][j] = (float16v){};
+
+    BRaw<WT, WTN> braw[NR];
+    half8v af[2][4][WTM], bf[2][WTN][4];
+    auto read_a = [&](half8v (&a)[4][WTM], int k) {
+        const uint8_t* st = smem + (k % NS) * C::A_STAGE;
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int i = 0; i < WTM; ++i) {
+                const int row = 32 * i + r32;
+                a[s][i] = *(const half8v*)(st + row * 128 + (((4 * q + s) ^ ((row >> 1) & 7)) << 4));
+            }
+    };
+
+    // prologue: slabs 0 .. NS-2 in flight, slab 0 in registers
+#pragma unroll
+    for (int k = 0; k < NS - 1; ++k) {
+        issue_a(k);
+        braw[k % NR].load(rq, rs, vq, vs, soq(k), sos(k));
+        touch(k - (NS - 1) + TD);
+    }
+    wait_vmcnt<(NS - 2) * C::PER_SLAB + C::NT>();
+    __builtin_amdgcn_s_barrier();
+    read_a(af[0], 0);
+#pragma unroll
+    for (int j = 0; j < WTN; ++j) braw[0].convert_j(bf[0][j], j, q);
+
+    // nk % U == 0 (checked on the host): the ring indices of slab k are u-static
+    for (int k0 = 0; k0 < nk; k0 += C::U) {
+#pragma unroll
+        for (int u = 0; u < C::U; ++u) {
+            const int k = k0 + u;
+            // slab k+1 (A in LDS from every wave, B in this wave's registers) has landed
+            wait_vmcnt<(NS - 3) * C::PER_SLAB + C::NT>();
+            __builtin_amdgcn_s_barrier();
+            issue_a(k + NS - 1);
+            braw[(u + NS - 1) % NR].load(rq, rs, vq, vs, soq(k + NS - 1), sos(k + NS - 1));
+            touch(k + TD);
+            const int cu = u & 1, nx = cu ^ 1;
+            // the MFMAs of slab k, with the next slab's A reads and weight
+            // dequantisation interleaved (one MFMA, then an LDS read or four VALU)
+            read_a(af[nx], k + 1);
+#pragma unroll
+            for (int j = 0; j < WTN; ++j) braw[(u + 1) % NR].convert_j(bf[nx][j], j, q);
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int i = 0; i < WTM; ++i)
+#pragma unroll
+                    for (int j = 0; j < WTN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[cu][s][i], bf[cu][j][s], acc[i][j], 0, 0, 0);
+#pragma unroll
+            for (int g = 0; g < 4 * WTM * WTN; ++g) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                if (g < 4 * WTM) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // LDS read
+                __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // VALU
+            }
+        }
+    }
+    wait_vmcnt<0>();
+    __syncthreads();
+
+    // folded LayerNorm: {mean, rstd} of the tile's rows at the top of LDS
+    float2v* ftab = (float2v*)(smem + C::LDS) - BM;
+    if constexpr (C::FOLD) {
+        if (fold) {
+            FoldStats<BM> fst;
+            const int lc = __builtin_ctz(p.fold_groups / 2), total = BM << lc;
+#pragma unroll
+            for (int i = 0; i < FoldStats<BM>::MAXC; ++i) {
+                const int ch = tid + 256 * i;
+                fst.c[i] = ch < total ? ((const float4v*)(smem + NS * C::A_STAGE))[ch] : (float4v){0.f, 0.f, 0.f, 0.f};
+            }
+            fst.finish(p, ftab, tid);
+            __syncthreads();
+        }
+    }
+    if constexpr (C::WHOLE) {
+        float* wsm = (float*)smem + wid * (32 * WTM) * (32 * WTN + 4);
+        epilogue32_lds<EPI, WTM, WTN>(p, acc, wsm, m0, nw, lane, ecol, fold, ftab, 0);
+    } else {
+        constexpr int TH = WTM / 2;
+        float* wsm = (float*)smem + wid * (32 * TH) * (32 * WTN + 4);
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            float16v part[TH][WTN];
+#pragma unroll
+            for (int i = 0; i < TH; ++i)
+#pragma unroll
+                for (int j = 0; j < WTN; ++j) part[i][j] = acc[hh * TH + i][j];
+            if (hh) __syncthreads();
+            epilogue32_lds<EPI, TH, WTN>(p, part, wsm, m0 + hh * TH * 32, nw, lane, ecol, fold, ftab, hh * TH * 32);
+        }
+    }
+}
+
+// ===========================================================================
 // f32 path: A f32, weights -> f32, v_mfma_f32_16x16x4_f32, BK = 32
 // ===========================================================================
 constexpr int BK32 = 32;
@@ -1709,6 +2066,20 @@ static void run_dma(const GemmParams& p, hipStream_t s) {
     }
 }
 
+template <int WTM, int WTN, int WT, int EPI, int NS, int TD = 0>
+static void run_rb(const GemmParams& p, hipStream_t s) {
+    typedef RbCfg<WTM, WTN, WT, EPI, NS, TD> C;
+    constexpr bool can_fold = EPI == EPI_STORE || EPI == EPI_SILU;
+    require(p.K % (64 * C::U) == 0, "gemm: register-B kernel needs K % 256 == 0");
+    if (p.fold_stats) require(p.fold_groups <= 32, "gemm: register-B kernel folds at most 32 statistics groups");
+    const int tiles = cdiv(p.M, C::BM) * cdiv(p.N, C::BN);
+    GemmParams q = p;
+    q.xcd_gm = choose_xcd_gm(p, WT, C::BM, C::BN);
+    if (can_fold && p.fold_stats) launch((gemm_rb_kernel<WTM, WTN, WT, EPI, NS, TD, can_fold>), dim3(tiles), dim3(256), 0, s, q);
+    else launch((gemm_rb_kernel<WTM, WTN, WT, EPI, NS, TD, false>), dim3(tiles), dim3(256), 0, s, q);
+    PKX_LAUNCH_CHECK();
+}
+
 template <int TM, int TN, int WT>
 static void f16_epi(int epi, const GemmParams& p, hipStream_t s) { PKX_EPI_SWITCH(run_f16, TM, TN, WT) }
 template <int TM, int TN, int WT>
@@ -1785,6 +2156,25 @@ static bool dma_kg2(int epi, const GemmParams& p, hipStream_t s) {
     default: return false;
     }
 }
+// Register-B kernel (128 x 256 tiles, one per CU) for the wide quantised
+// products: FFN linear1 (N = 4096), q/k/v (N = 3072) and the all-layer
+// positional projection.  On MI355X at M = 2000, K = 1024 (q8_0): 25.7 against
+// 27.8 us (FFN linear1), 25.0 against 27.7 (q/k/v, folded LayerNorm), 22.2
+// against 24.9 (positional, M = 249, N = 24576) for the LDS-B 128 x 128 tiles.
+// Grids under about 3/4 of the chip keep the LDS-B kernels.
+template <int WT>
+static bool dma_rb(int epi, const GemmParams& p, hipStream_t s) {
+    if (p.K % 256 != 0 || p.N < 2048 || (p.fold_stats && p.fold_groups > 32)) return false;
+    if (epi != EPI_STORE && epi != EPI_SILU && epi != EPI_STORE_F32) return false;
+    if ((int64_t)cdiv(p.M, 128) * cdiv(p.N, 256) * 4 < (int64_t)device_cu_count() * 3) return false;
+    switch (epi) {
+    case EPI_STORE: run_rb<4, 2, WT, EPI_STORE, 4>(p, s); break;
+    case EPI_SILU: run_rb<4, 2, WT, EPI_SILU, 4>(p, s); break;
+    default: run_rb<4, 2, WT, EPI_STORE_F32, 4>(p, s); break;
+    }
+    return true;
+}
+
 template <int TM, int TN, int WT>
 static void f32_epi(int epi, const GemmParams& p, hipStream_t s) { PKX_EPI_SWITCH(run_f32, TM, TN, WT) }
 // tiles narrower than 64 columns per wave pair: every epilogue but GLU (which
@@ -1863,6 +2253,8 @@ void launch_gemm(Precision prec, int wtype, int epi, const GemmParams& p, hipStr
         const int64_t t22 = (int64_t)cdiv(p.M, 128) * cdiv(p.N, 128);
         const int64_t t21 = (int64_t)cdiv(p.M, 128) * cdiv(p.N, 64);
         const bool glu = epi == EPI_GLU || epi == EPI_GLU_DW;
+        if (wtype == GT_Q8_0 && dma_rb<GT_Q8_0>(epi, p, s)) return;
+        if (wtype == GT_Q4_K && dma_rb<GT_Q4_K>(epi, p, s)) return;
         if (wtype == GT_Q8_0 && dma_splitk<GT_Q8_0>(epi, p, s)) return;
         if (wtype == GT_Q4_K && dma_splitk<GT_Q4_K>(epi, p, s)) return;
         if (wtype == GT_F16 && dma_splitk<GT_F16>(epi, p, s)) return;
