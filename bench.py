@@ -76,15 +76,24 @@ def layernorm_bytes(cfg, B, Tp, launches):
     return ((3 * L + 1) * single + (L - 1) * fused + last) / launches
 
 
-def other_config(name, qtype, cfg_kw, lens, T_max, steps, warmup, stream, base=None):
+def step_stats(events):
+    """Median and p90 of the per-step times between consecutive events (ms)."""
+    per = np.array([events[i].elapsed_ms(events[i + 1]) for i in range(len(events) - 1)])
+    return round(float(np.median(per)), 4), round(float(np.percentile(per, 90)), 4)
+
+
+def other_config(name, qtype, cfg_kw, lens, T_max, steps, warmup, stream, base=None, gm=None):
     """The other benchmark shapes, same measurement (one GPU, inputs resident,
-    FFN GEMM sampled with per-dispatch events inside the timed region)."""
+    FFN GEMM sampled with per-dispatch events inside the timed region).  gm: a
+    model handle to reuse (kept open); otherwise one is synthesised and closed."""
     kw = dict(CFG if base is None else base)
     kw.update(cfg_kw)
     cfg = pm.Config(**kw)
-    model = pm.synthesize(cfg, qtype, heads=False)
-    gm = pkx.Model.from_tensors(model, pkx.PREC_AUTO)
-    del model
+    own = gm is None
+    if own:
+        model = pm.synthesize(cfg, qtype, heads=False)
+        gm = pkx.Model.from_tensors(model, pkx.PREC_AUTO)
+        del model
     Bc = len(lens)
     rng = np.random.default_rng(42)
     mel = rng.standard_normal((Bc, cfg.n_mels, T_max)).astype(np.float32)
@@ -98,16 +107,21 @@ def other_config(name, qtype, cfg_kw, lens, T_max, steps, warmup, stream, base=N
         gm.encoder_forward(d_mel, valid, d_out, stream=stream)
     stream.sync()
     gm.set_profiling(["gemm_ffn"], stride=25)
-    e0, e1 = pkx.Event(), pkx.Event()
-    e0.record(stream)
+    ev = [pkx.Event() for _ in range(steps + 1)]
+    ev[0].record(stream)
     vo = None
-    for _ in range(steps):
+    for i in range(steps):
         _, vo = gm.encoder_forward(d_mel, valid, d_out, stream=stream)
-    e1.record(stream)
-    ms = e0.elapsed_ms(e1) / steps
+        ev[i + 1].record(stream)
+    ms = ev[0].elapsed_ms(ev[-1]) / steps
     stream.sync()
+    med, p90 = step_stats(ev)
     ffn_ms, ffn_n = gm.profile()["gemm_ffn"]
     gm.set_profiling(False)
+    res = d_out.numpy(stream)
+    finite = bool(all(np.isfinite(res[b, :vo[b]]).all() for b in range(Bc)))
+    if not finite:
+        raise RuntimeError("%s: non-finite encoder output" % name)
     M = Bc * Tp
     ffn_flop = 2.0 * M * cfg.d_model * cfg.ff_dim
     ffn_tf = ffn_flop / (ffn_ms / 1e3 / ffn_n) / 1e12
@@ -115,6 +129,7 @@ def other_config(name, qtype, cfg_kw, lens, T_max, steps, warmup, stream, base=N
     peak = PEAK_F32_TFLOPS if f32 else PEAK_F16_TFLOPS
     audio_s = float(np.sum(lens)) * HOP_S
     out = {"workload": name, "dtype": "f32" if f32 else "f16", "ms_per_step": round(ms, 4),
+           "ms_per_step_median": med, "ms_per_step_p90": p90, "outputs_finite": finite,
            "rtfx": round(audio_s / (ms / 1e3), 1),
            "frames_per_s": round(float(np.sum(vo)) / (ms / 1e3), 1),
            "gemm_ffn": {"avg_us": round(ffn_ms / ffn_n * 1e3, 2), "achieved": round(ffn_tf, 2),
@@ -122,7 +137,8 @@ def other_config(name, qtype, cfg_kw, lens, T_max, steps, warmup, stream, base=N
            "steps": steps}
     d_mel.free()
     d_out.free()
-    gm.close()
+    if own:
+        gm.close()
     return out
 
 
@@ -243,7 +259,20 @@ def streaming(stream, n_streams=256, steps=50, warmup=5):
 
 
 def cpu_model_name():
-    """The host CPU's model name (what lscpu prints as "Model name")."""
+    """The host CPU's model name as lscpu prints it ("Model name", with its
+    "BIOS Model name" when lscpu gives one), else /proc/cpuinfo's."""
+    import subprocess
+    names = []
+    try:
+        txt = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in txt.splitlines():
+            key, _, val = line.partition(":")
+            if key.strip() in ("Model name", "BIOS Model name") and val.strip():
+                names.append("%s: %s" % (key.strip(), val.strip()))
+    except (OSError, subprocess.SubprocessError):
+        pass
+    if names:
+        return "; ".join(names)
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
@@ -322,13 +351,14 @@ def main():
     # FFN1/FFN2 launches of the 24 blocks as the steps go by, and the event cost
     # (about 4 launches per step) stays off the rest.
     gm.set_profiling(["gemm_ffn"], stride=25)
-    e0, e1 = pkx.Event(), pkx.Event()
-    e0.record(stream)
-    for _ in range(args.steps):
+    ev = [pkx.Event() for _ in range(args.steps + 1)]
+    ev[0].record(stream)
+    for i in range(args.steps):
         gm.encoder_forward(d_mel, valid, d_out, stream=stream)
-    e1.record(stream)
-    ms_total = e0.elapsed_ms(e1)
+        ev[i + 1].record(stream)
+    ms_total = ev[0].elapsed_ms(ev[-1])
     stream.sync()
+    ms_med, ms_p90 = step_stats(ev)
     ffn_ms, ffn_n = gm.profile()["gemm_ffn"]
     ms_step = ms_total / args.steps
     out = d_out.numpy(stream)
@@ -411,6 +441,7 @@ def main():
         "metric": "encoder RTFx + HBM GB/s / MFMA util, 0.6B conformer q8_0 bs16 on 1 MI355X",
         "value": round(rtfx, 1), "unit": "RTFx (audio s / wall s)",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 4),
+        "ms_per_step_median": ms_med, "ms_per_step_p90": ms_p90,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
         "data": "synthetic (seeded N(0,1) log-mel; random-init q8_0 weights)",
         "config": {"workload": "FastConformer encoder 0.6B shape: 24 blocks, d_model 1024, 8 heads x 128, "
@@ -430,11 +461,16 @@ def main():
     if not args.no_extra:
         # the ragged f16 batch (16 clips of 2-20 s) and the 1.1B shape at 8 x 30 s
         lens = (200 + np.floor(np.random.default_rng(7).random(16) * 1801)).astype(np.int32)
+        cfg11 = pm.Config(**dict(CFG, n_layers=42))
+        gm11 = pkx.Model.from_tensors(pm.synthesize(cfg11, "q8_0", heads=False), pkx.PREC_AUTO)
         line["other_configs"] = [
             other_config("0.6B f16 weights, batch 16 ragged 2-20 s (T_max %d frames)" % int(lens.max()), "f16", {},
                          lens, int(lens.max()), 10, 2, stream),
             other_config("1.1B shape q8_0 (42 blocks), batch 8 x 30 s (3000 frames -> T'=375)", "q8_0",
-                         dict(n_layers=42), np.full(8, 3000, dtype=np.int32), 3000, 5, 1, stream),
+                         dict(n_layers=42), np.full(8, 3000, dtype=np.int32), 3000, 5, 1, stream, gm=gm11),
+            # the long-sequence stress case: 300 s per item, T' = 3750 (the O(T'^2) attention)
+            other_config("1.1B shape q8_0 (42 blocks), batch 8 x 300 s (30000 frames -> T'=3750)", "q8_0",
+                         dict(n_layers=42), np.full(8, 30000, dtype=np.int32), 30000, 2, 1, stream, gm=gm11),
             other_config("0.6B q4_K weights, batch 16 x 10 s", "q4_k", {}, np.full(16, 1000, dtype=np.int32), 1000,
                          10, 2, stream),
             # the 110M shape in f32 (f32 MFMA 16x16x4; FFN against the f32 peak)
@@ -443,6 +479,7 @@ def main():
             other_config("110M shape f32, batch 16 x 10 s", "f32", {}, np.full(16, 1000, dtype=np.int32), 1000,
                          10, 2, stream, base=CFG110),
         ]
+        gm11.close()
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(model, mel, valid)
     print(json.dumps(line))

@@ -53,6 +53,11 @@ enum { PKX_PREC_AUTO = -1, PKX_PREC_F32 = 0, PKX_PREC_F16 = 1 };
  *   SCALAR:  mask only the flattened output (Subsampling::build_graph,
  *            src/subsampling.cpp:281-300, used by Encoder::forward). */
 enum { PKX_MASK_BATCHED = 0, PKX_MASK_SCALAR = 1 };
+/* Flag or-ed into pkx_subsampling_forward's mask_mode: valid_T holds entry valid
+ * lengths as the streaming windows count them (every frame of the window is
+ * audio, src/subsampling.hpp:53-61: in_valid_frames), 1 <= valid_T[b] <= T_max,
+ * instead of true frame counts whose entry valid length is one less. */
+enum { PKX_MASK_WHOLE_FRAMES = 4 };
 
 /* Encoder hyper-parameters (the encoder fields of pk::ParakeetConfig,
  * src/model_loader.hpp:27-52; GGUF keys parakeet.encoder.*). */
@@ -83,6 +88,8 @@ const char* pkx_last_error(void);
 int pkx_device_count(int* n);
 int pkx_malloc(void** dev, size_t bytes);
 int pkx_free(void* dev);
+/* Free and total device memory of the current device (hipMemGetInfo). */
+int pkx_mem_info(size_t* free_bytes, size_t* total_bytes);
 int pkx_memcpy_h2d(void* dev_dst, const void* host_src, size_t bytes, void* stream);
 int pkx_memcpy_d2h(void* host_dst, const void* dev_src, size_t bytes, void* stream);
 int pkx_memcpy_d2d(void* dev_dst, const void* dev_src, size_t bytes, void* stream);
@@ -223,6 +230,15 @@ int pkx_dequantize(int ggml_type, const void* src_dev, float* dst_dev, int64_t n
  * F32 or F16 path.  x_dev [M][K] f32, y_dev [M][N] f32. */
 int pkx_linear(int precision, int ggml_type, int N, int K, const void* host_w, size_t nbytes,
                const float* bias_dev, const float* x_dev, int64_t M, float* y_dev, void* stream);
+
+/* y += alpha * (x . W^T + bias): the residual products of the encoder
+ * (ggml_add(r, ggml_scale(ggml_mul_mat(W, x), 0.5)), src/conformer.cpp:326-330,
+ * with alpha 0.5; alpha 1 for linear_out / pointwise_conv2) on the kernels the
+ * encoder runs them with, including the split-K path for products of at most
+ * 512 rows and K >= 1024.  y_dev [M][N] f32, read and written. */
+int pkx_linear_residual(int precision, int ggml_type, int N, int K, const void* host_w, size_t nbytes,
+                        const float* bias_dev, const float* x_dev, int64_t M, float alpha, float* y_dev,
+                        void* stream);
 
 /* LayerNorm over the last dim, f32 in/out (ggml_norm + mul + add,
  * src/conformer.cpp:300-307). */

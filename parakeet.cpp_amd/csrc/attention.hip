@@ -78,9 +78,18 @@ __device__ __forceinline__ float xg_sum(float x) {
 // in flight and would drain them all before it.  lds_tr_wait<N> waits until
 // at most N LDS operations of the wave are outstanding (in-order completion,
 // so the two loads named are done) and ties their registers to the wait.
+// Invariant: between lds_tr_b64 and the lds_tr_wait that names its register,
+// no instruction may read, copy, spill or overwrite that register (the data
+// lands asynchronously; the compiler believes it valid at the load).  The
+// destination is an in-out operand from a defined value, so the load and the
+// wait are the register's only definitions, and each value is consumed right
+// after its wait; the built code keeps the window clean (no VGPR copy or spill
+// of a transposed-load destination between the load and its s_waitcnt, read
+// from this file's gfx950 assembly).
 __device__ __forceinline__ void lds_tr_b64(half4v& r, const f16* p) {
     const uint32_t off = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const f16*)p;
-    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(off));
+    r = (half4v){};
+    asm volatile("ds_read_b64_tr_b16 %0, %1" : "+v"(r) : "v"(off));
 }
 template <int N> __device__ __forceinline__ void lds_tr_wait(half4v& x, half4v& y) {
     static_assert(N >= 0 && N < 16, "lgkmcnt range");

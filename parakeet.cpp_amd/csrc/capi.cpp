@@ -28,7 +28,8 @@ struct pkx_streaming {
 // Fixed device scratch of pkx_tdt_joint_argmax_noalloc: one copy per GPU,
 // held until the process ends.  Host code never passes the symbol's name as an
 // address (it is a host-side stand-in there); joint_scratch() finds each GPU's
-// copy with hipGetSymbolAddress and that address is used from then on.
+// copy with hipGetSymbolAddress (at model set-up, with the model's device
+// current) and that address is used from then on.
 static __device__ __align__(256) float scratch[PKX_JOINT_NOALLOC_MAX_FLOATS];
 
 namespace {
@@ -66,6 +67,10 @@ float* joint_scratch() {
     if (!ptr[dev]) {
         void* p = nullptr;
         PKX_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        // the code objects of the kernels the entry point launches, loaded now
+        // rather than at its first launch
+        pkx::gemm_module_ready();
+        pkx::elementwise_module_ready();
         ptr[dev] = (float*)p;
     }
     return ptr[dev];
@@ -144,6 +149,12 @@ int pkx_malloc(void** dev, size_t bytes) {
 int pkx_free(void* dev) {
     return guarded([&] { if (dev) PKX_HIP(hipFree(dev)); });
 }
+int pkx_mem_info(size_t* free_bytes, size_t* total_bytes) {
+    return guarded([&] {
+        need(free_bytes && total_bytes, "null out");
+        PKX_HIP(hipMemGetInfo(free_bytes, total_bytes));
+    });
+}
 int pkx_memcpy_h2d(void* dst, const void* src, size_t bytes, void* s) {
     return guarded([&] {
         PKX_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, st(s)));
@@ -200,6 +211,7 @@ int pkx_model_load_gguf(const char* path, int precision, pkx_model** out) {
         need(path && out, "null argument");
         *out = nullptr;
         std::unique_ptr<pkx::Model> impl = pkx::load_gguf(path, precision);
+        (void)joint_scratch();   // set-up: this GPU's scratch address (see pkx_model_finalize)
         pkx_model* m = new pkx_model;
         m->cfg = to_public(impl->config());
         m->precision = impl->precision();
@@ -256,6 +268,10 @@ int pkx_model_finalize(pkx_model* m) {
         need(m, "null model");
         m->impl->finalize();
         m->precision = m->impl->precision();
+        // Set-up of pkx_tdt_joint_argmax_noalloc on this GPU: the symbol lookup
+        // (the first one on a device materialises the array's storage) happens
+        // here, so that entry point itself takes no device memory.
+        (void)joint_scratch();
     });
 }
 
@@ -299,9 +315,11 @@ int pkx_subsampling_forward(pkx_model* m, const float* mel, int B, int T_max, co
                             float* out, int* T_out, int* valid_out, void* s) {
     return guarded([&] {
         need(m && mel && out, "null argument");
-        need(mask_mode == PKX_MASK_BATCHED || mask_mode == PKX_MASK_SCALAR, "bad mask_mode");
-        const int Tp = m->impl->subsampling_forward(mel, B, T_max, valid_T, mask_mode == PKX_MASK_BATCHED, out,
-                                                    valid_out, st(s), false);
+        const int base = mask_mode & ~PKX_MASK_WHOLE_FRAMES;
+        need(base == PKX_MASK_BATCHED || base == PKX_MASK_SCALAR, "bad mask_mode");
+        const int Tp = m->impl->subsampling_forward(mel, B, T_max, valid_T, base == PKX_MASK_BATCHED, out,
+                                                    valid_out, st(s), false,
+                                                    (mask_mode & PKX_MASK_WHOLE_FRAMES) != 0);
         if (T_out) *T_out = Tp;
     });
 }
@@ -382,6 +400,21 @@ int pkx_linear(int precision, int gtype, int N, int K, const void* host_w, size_
         t.ne[1] = N;
         t.bytes.assign((const uint8_t*)host_w, (const uint8_t*)host_w + nbytes);
         pkx::linear_raw((pkx::Precision)precision, t, N, K, bias, x, M, y, st(s));
+    });
+}
+
+int pkx_linear_residual(int precision, int gtype, int N, int K, const void* host_w, size_t nbytes, const float* bias,
+                        const float* x, int64_t M, float alpha, float* y, void* s) {
+    return guarded([&] {
+        need(host_w && x && y, "null argument");
+        need(precision == PKX_PREC_F32 || precision == PKX_PREC_F16, "precision must be F32 or F16");
+        pkx::HostTensor t;
+        t.gtype = gtype;
+        t.n_dims = 2;
+        t.ne[0] = K;
+        t.ne[1] = N;
+        t.bytes.assign((const uint8_t*)host_w, (const uint8_t*)host_w + nbytes);
+        pkx::linear_raw((pkx::Precision)precision, t, N, K, bias, x, M, y, st(s), true, alpha);
     });
 }
 

@@ -603,6 +603,13 @@ void launch_log_softmax_argmax(const float* logits, float* logprobs, int32_t* ar
     PKX_LAUNCH_CHECK();
 }
 
+// Loads this file's code object on the current device (the runtime loads it
+// at the first launch otherwise, taking device memory then).
+void elementwise_module_ready() {
+    hipFuncAttributes a;
+    PKX_HIP(hipFuncGetAttributes(&a, (const void*)split_argmax_kernel));
+}
+
 void launch_split_argmax(const float* logits, int64_t M, int n_tok, int n_dur, int32_t* tok,
                          int32_t* dur, hipStream_t s) {
     if (M == 0) return;

@@ -65,6 +65,7 @@ void launch_log_softmax_argmax(const float* logits, float* logprobs, int32_t* ar
                                int V, hipStream_t s);
 
 // Split argmax per row (tdt.cpp:76-79): tok = argmax[0,n_tok), dur = argmax[n_tok, n_tok+n_dur).
+void elementwise_module_ready();
 void launch_split_argmax(const float* logits, int64_t M, int n_tok, int n_dur, int32_t* tok,
                          int32_t* dur, hipStream_t s);
 

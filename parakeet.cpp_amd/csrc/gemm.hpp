@@ -100,6 +100,9 @@ bool gemm_glu_dw_supported(Precision prec, int wtype, int N, int K);
 // weights dequantised to f32).  wtype is the ggml type of the device weight.
 void launch_gemm(Precision prec, int wtype, int epi, const GemmParams& p, hipStream_t s);
 
+// Loads the GEMM file's code object on the current device.
+void gemm_module_ready();
+
 // Bit-exact dequantisation of raw ggml blocks (GGUF layout) to f32.
 void launch_dequantize(int wtype, const void* src, float* dst, int64_t n, hipStream_t s);
 

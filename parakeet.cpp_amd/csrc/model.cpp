@@ -76,6 +76,11 @@ struct Buf {
     size_t cap = 0;
 };
 
+// Split-K workspace: 2^20 floats of partial tiles (256 64 x 64 tile splits)
+// and 512 tile counters, zero between launches
+constexpr int64_t SK_FLOATS = (int64_t)1 << 20;
+constexpr int SK_TILES = 512;
+
 struct Model::Ws {
     Buf a2, a2p, a3, flat;              // subsampling maps
     Buf h, u, qkv, g, pe, p, xin, tmp;  // layer activations
@@ -384,7 +389,7 @@ DevWeight weight_rows_view(const DevWeight& w, int row0, int nrows) {
 }
 
 void linear_raw(Precision prec, const HostTensor& t, int N, int K, const float* bias, const float* x,
-                int64_t M, float* y, hipStream_t s) {
+                int64_t M, float* y, hipStream_t s, bool residual, float alpha) {
     std::vector<void*> allocs;
     try {
         const DevWeight w = build_weight(t, N, K, prec == PREC_F16, allocs);
@@ -406,7 +411,16 @@ void linear_raw(Precision prec, const HostTensor& t, int N, int K, const float* 
         p.M = (int)M;
         p.N = N;
         p.K = K;
-        launch_gemm(prec, w.gtype, EPI_STORE_F32, p, s);
+        p.alpha = residual ? alpha : 1.0f;
+        if (residual && prec == PREC_F16) {
+            // the split-K workspace the encoder's residual products use
+            p.sk_part = (float*)dalloc_into(allocs, (size_t)SK_FLOATS * 4);
+            p.sk_part_floats = SK_FLOATS;
+            p.sk_cnt = (int*)dalloc_into(allocs, SK_TILES * sizeof(int));
+            p.sk_cnt_n = SK_TILES;
+            PKX_HIP(hipMemsetAsync(p.sk_cnt, 0, SK_TILES * sizeof(int), s));
+        }
+        launch_gemm(prec, w.gtype, residual ? EPI_RESID : EPI_STORE_F32, p, s);
         PKX_HIP(hipStreamSynchronize(s));
     } catch (...) {
         (void)hipStreamSynchronize(s);
@@ -658,6 +672,12 @@ void Model::finalize() {
         }
     }
     host_.clear();
+    // split-K workspace (residual products of few rows): created here, once, so
+    // that no forward or streaming step allocates or synchronises for it
+    grow(ws_->skpart, (size_t)SK_FLOATS * 4);
+    PKX_HIP(hipMalloc(&ws_->skcnt, SK_TILES * sizeof(int)));
+    PKX_HIP(hipMemset(ws_->skcnt, 0, SK_TILES * sizeof(int)));
+    PKX_HIP(hipDeviceSynchronize());
     finalized_ = true;
 }
 
@@ -765,18 +785,8 @@ void Model::gemm(const DevWeight& w, int epi, const void* A, int64_t lda, int64_
     mark(fam, false);
 }
 
-// 2^20 floats of partial tiles (256 64 x 64 tile splits) and 512 tile counters
-constexpr int64_t SK_FLOATS = (int64_t)1 << 20;
-constexpr int SK_TILES = 512;
-
-void Model::splitk_ws(GemmParams& p, hipStream_t s) {
-    if (p.M > 512) return;
-    if (!ws_->skcnt) {
-        grow(ws_->skpart, (size_t)SK_FLOATS * 4);
-        PKX_HIP(hipMalloc(&ws_->skcnt, SK_TILES * sizeof(int)));
-        PKX_HIP(hipMemsetAsync(ws_->skcnt, 0, SK_TILES * sizeof(int), s));
-        PKX_HIP(hipStreamSynchronize(s));
-    }
+void Model::splitk_ws(GemmParams& p, hipStream_t) {
+    if (p.M > 512 || !ws_->skcnt) return;
     p.sk_part = (float*)ws_->skpart.p;
     p.sk_part_floats = SK_FLOATS;
     p.sk_cnt = ws_->skcnt;

@@ -284,9 +284,11 @@ DevWeight build_weight(const HostTensor& t, int N, int K, bool f16_gemm, std::ve
 DevWeight weight_rows_view(const DevWeight& w, int row0, int nrows);
 
 // y[M][N] = x[M][K] . W^T (+ bias) for one raw weight, f32 in/out; the weight
-// is uploaded for this call and freed after the stream drains.
+// is uploaded for this call and freed after the stream drains.  residual:
+// y += alpha (x . W^T + bias) instead (the encoder's residual product, with
+// its split-K path for few rows).
 void linear_raw(Precision prec, const HostTensor& t, int N, int K, const float* bias, const float* x,
-                int64_t M, float* y, hipStream_t s);
+                int64_t M, float* y, hipStream_t s, bool residual = false, float alpha = 1.0f);
 
 // GGUF v3 reader: fills a Model with the encoder (+ head) tensors and config.
 std::unique_ptr<Model> load_gguf(const std::string& path, int precision);

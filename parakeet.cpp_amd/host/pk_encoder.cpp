@@ -372,18 +372,21 @@ void Subsampling::forward(const std::vector<float>& mel, int n_mels, int T, std:
                           int& d_model, int& valid_len, int in_valid_frames) const {
     need(n_mels == (int)ml_.config().feat_in, "Subsampling::forward: n_mels does not match the model");
     need(T >= 1 && mel.size() == (size_t)n_mels * T, "Subsampling::forward: mel must be [n_mels][T]");
-    need(in_valid_frames <= T - 1,
-         "Subsampling::forward: in_valid_frames > T-1 is a streaming window (not in this offline build)");
+    need(in_valid_frames <= T, "Subsampling::forward: in_valid_frames must be at most T (the window's frames)");
     ModelLoader::Device& d = dev_of(ml_);
     std::lock_guard<std::mutex> lock(d.mu);
     const int Tp = pkx_subsampled_len(T), D = d_model_;
     float* dmel = (float*)d.get(d.in, mel.size() * 4);
     float* dout = (float*)d.get(d.out, (size_t)Tp * D * 4);
     d.h2d(dmel, mel.data(), mel.size() * 4);
-    // the C ABI takes true frame counts; the entry valid length is that minus one
-    const int vT = in_valid_frames < 0 ? T : in_valid_frames + 1;
+    // The C ABI takes true frame counts (entry valid length one less); a whole
+    // window (in_valid_frames == T, the streaming convention) goes as an entry
+    // valid length of its own.
+    const bool whole = in_valid_frames == T;
+    const int vT = in_valid_frames < 0 ? T : whole ? T : in_valid_frames + 1;
     int tout = 0, vo = 0;
-    chk(pkx_subsampling_forward(ml_.handle(), dmel, 1, T, &vT, PKX_MASK_SCALAR, dout, &tout, &vo, d.stream),
+    chk(pkx_subsampling_forward(ml_.handle(), dmel, 1, T, &vT, PKX_MASK_SCALAR | (whole ? PKX_MASK_WHOLE_FRAMES : 0),
+                                dout, &tout, &vo, d.stream),
         "pkx_subsampling_forward");
     out.resize((size_t)tout * D);
     d.d2h(out.data(), dout, out.size() * 4);

@@ -84,6 +84,9 @@ SIGS = {
     "pkx_dequantize": ([C.c_int, _vp, _vp, C.c_int64, _vp], C.c_int),
     "pkx_linear": ([C.c_int, C.c_int, C.c_int, C.c_int, _vp, C.c_size_t, _vp, _vp, C.c_int64, _vp,
                     _vp], C.c_int),
+    "pkx_linear_residual": ([C.c_int, C.c_int, C.c_int, C.c_int, _vp, C.c_size_t, _vp, _vp, C.c_int64,
+                             C.c_float, _vp, _vp], C.c_int),
+    "pkx_mem_info": ([C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)], C.c_int),
     "pkx_layernorm": ([_vp, _vp, _vp, _vp, C.c_int64, C.c_int, C.c_float, _vp], C.c_int),
     "pkx_rel_pos_encoding": ([C.c_int, C.c_int, _vp, _vp], C.c_int),
     "pkx_mel_create": ([C.POINTER(MelConfig), _vp, C.c_int, _vp, C.POINTER(_vp)], C.c_int),
@@ -233,6 +236,21 @@ def linear(precision, gtype, N, K, w_raw: np.ndarray, x: DeviceArray, M, y: Devi
     w_raw = np.ascontiguousarray(w_raw)
     check(lib().pkx_linear(precision, gtype, N, K, w_raw.ctypes.data, w_raw.nbytes,
                            bias.ptr if bias is not None else None, x.ptr, M, y.ptr, _sh(stream)))
+
+
+def linear_residual(precision, gtype, N, K, w_raw: np.ndarray, x: DeviceArray, M, y: DeviceArray, alpha=1.0,
+                    bias: DeviceArray = None, stream=None):
+    """y += alpha * (x . W^T + bias) on the encoder's residual-product kernels."""
+    w_raw = np.ascontiguousarray(w_raw)
+    check(lib().pkx_linear_residual(precision, gtype, N, K, w_raw.ctypes.data, w_raw.nbytes,
+                                    bias.ptr if bias is not None else None, x.ptr, M, alpha, y.ptr, _sh(stream)))
+
+
+def mem_info():
+    """(free, total) device memory in bytes."""
+    f, t = C.c_size_t(0), C.c_size_t(0)
+    check(lib().pkx_mem_info(C.byref(f), C.byref(t)))
+    return f.value, t.value
 
 
 def layernorm(x: DeviceArray, g: DeviceArray, b: DeviceArray, y: DeviceArray, M, D, eps=1e-5,

@@ -30,5 +30,28 @@ int main() {
     }
     bool ok = pktest::compare(out, ref, "subsampling", 1e-2f, 1e-2f);
     ok = pktest::compare_rel_l2(out, ref, "subsampling", pktest::bar_for(ml.precision())) && ok;
+
+    // Streaming convention: the whole window is audio (in_valid_frames = T),
+    // so every output frame is valid (src/subsampling.hpp:53-61).
+    std::vector<float> refw; std::vector<int64_t> rws;
+    std::vector<int32_t> vw;
+    if (!pktest::load_baseline(base, "subsampling_out_whole", refw, rws)) return 1;
+    if (!pktest::load_baseline_i32(base, "subsampling_valid_whole", vw) || vw.size() != 1) return 1;
+    std::vector<float> outw; int Toutw = 0, dmw = 0, validw = 0;
+    sub.forward(mel, n_mels, T, outw, Toutw, dmw, validw, T);
+    if (validw != (int)vw[0] || validw != sub.valid_out_len(T, T) || Toutw != Tout) {
+        std::fprintf(stderr, "whole window: valid %d (baseline %d, valid_out_len %d), Tout %d\n", validw, (int)vw[0],
+                     sub.valid_out_len(T, T), Toutw);
+        return 1;
+    }
+    ok = pktest::compare_rel_l2(outw, refw, "subsampling (whole window)", pktest::bar_for(ml.precision())) && ok;
+    // a count past the window is refused
+    bool threw = false;
+    try {
+        sub.forward(mel, n_mels, T, outw, Toutw, dmw, validw, T + 1);
+    } catch (const std::exception&) {
+        threw = true;
+    }
+    if (!threw) { std::fprintf(stderr, "in_valid_frames = T + 1 was accepted\n"); return 1; }
     return ok ? 0 : 1;
 }

@@ -6,7 +6,8 @@
   tokens + 5 durations) over the encoder output with per-frame argmax.
 * 1.1B shape (q8_0, d = 1024, 8 heads, FFN 4096) at batch 8 x 30 s: one
   block at T' = 375, and the long-T stress shape T' = 3750 through the
-  relative-position attention alone (batch 1).
+  relative-position attention alone (batch 1) and through a whole block
+  (batch 2, ragged).
 Bars: relative L2 1e-2 over valid frames (F16 path); the joint (f32 for
 every weight type) fed the same encoder output gives identical argmax ids on
 every frame but exact f32 ties.
@@ -114,3 +115,24 @@ def test_long_T_stress_attention(gpu, stream, model11):
     got = dy.numpy(stream)
     assert rel_l2(got[0, :3749], ref[0, :3749]) < 1e-2
     assert rel_l2(got[0, 3749:], ref[0, 3749:]) < 1e-2      # padded query row -> linear_out bias
+
+
+def test_long_T_stress_block(gpu, stream, model11):
+    """One 1.1B-shape block at T' = 3750 (300 s of audio), batch 2, ragged: the
+    O(T'^2) attention and its rel_shift inside the whole block
+    (src/relpos_attention.cpp:252-278, src/conformer.cpp:285-353)."""
+    m, om, gm = model11
+    B, T, D = 2, 3750, 1024
+    rng = np.random.default_rng(37502)
+    valid = [3750, 2811]
+    x = rng.normal(0, 1, (B, T, D)).astype(np.float32)
+    print(f"[c5-stress] block B={B} T={T} valid={valid}", flush=True)
+    ref = om.conformer_layer(0, x, oracle.rel_pos_encoding(T, D), valid)
+    dx = gpu.DeviceArray.from_numpy(x, stream)
+    dy = gpu.DeviceArray((B, T, D), np.float32)
+    gm.conformer_layer(0, dx, valid, dy, None, stream)
+    got = dy.numpy(stream)
+    mask = np.arange(T)[None, :] < np.asarray(valid)[:, None]
+    assert np.isfinite(got[mask]).all()
+    assert rel_l2(got[mask], ref[mask]) < 1e-2
+    assert rel_l2(got[mask] - x[mask], ref[mask] - x[mask]) < 3e-2

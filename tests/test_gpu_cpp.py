@@ -54,6 +54,9 @@ def _files(tmp_path_factory, wtype):
     sub, vo = om.subsampling(mel[None], None, stage_masks=False)
     Tp, D = sub.shape[1], cfg.d_model
     assert Tp == 126 and vo[0] == Tp - 1
+    # the whole-window convention (in_valid_frames = T, src/subsampling.hpp:53-61)
+    sub_w, vo_w = om.subsampling(mel[None], [T], stage_masks=False)
+    assert vo_w[0] == Tp
     pre = (sub[0] * np.float32(np.sqrt(D))).astype(np.float32)
     pe64 = oracle.rel_pos_encoding(Tp, D)
     # the layer-level baselines take a table perturbed by up to 5e-4 (a table
@@ -67,7 +70,8 @@ def _files(tmp_path_factory, wtype):
     conv_in = rng.standard_normal((Tp, D)).astype(np.float32)
     L = cfg.n_layers
     base = {
-        "mel": mel, "subsampling_out": sub[0], "pos_emb": pe, "pos_emb_f64": pe64, "enc_pre_layers": pre,
+        "mel": mel, "subsampling_out": sub[0], "subsampling_out_whole": sub_w[0],
+        "subsampling_valid_whole": np.array([vo_w[0]], np.int32), "pos_emb": pe, "pos_emb_f64": pe64, "enc_pre_layers": pre,
         "l0_attn_in": attn_in, "l0_attn_out": om.relpos_attention(0, attn_in[None], pe, valid)[0],
         "l0_conv_out": conv0[0], "l0_conv_in": conv_in,
         "l0_conv_module_out": om.conv_module(0, conv_in[None], valid)[0],

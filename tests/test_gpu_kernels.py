@@ -113,3 +113,50 @@ def test_linear_tile_shapes(gpu, stream, gtype, M, N, K):
     gpu.linear(1, gtype, N, K, raw, dx, M, dy, db, stream)
     err = rel_l2(dy.numpy(stream), ref)
     assert err < 2e-3, err
+
+
+@pytest.mark.parametrize("gtype", [pm.GGML_Q8_0, pm.GGML_F16])
+def test_residual_split_k_fresh_inputs(gpu, stream, gtype):
+    """The split-K residual product (M <= 512 rows, K >= 1024: S workgroups per
+    tile hand partial tiles to the last arriver, which sums them in split order)
+    on fresh random inputs at every call, the calls of different sizes (some
+    with a tile's splits on two XCDs), so a stale or missing partial cannot
+    repeat the previous result.  Every element is
+    checked against a float64 product of the exact f16 operands the kernel
+    multiplies (activations rounded to f16; q8_0 weights f16(d q), f16 weights
+    as stored), within the worst-case f32 summation bound of its K terms, and
+    the first element outside it fails the test."""
+    rng = _rng(2048)
+    K, alpha = 2048, 0.5
+    # (M, N): 128 64x64 tiles x 2 splits and 64 x 4 (32 positions per XCD, a
+    # tile's splits on one XCD), then 10 tiles x 8 splits and 21 x 4, whose
+    # per-XCD ranges (10, 10-11 positions) cut tiles' splits over two XCDs
+    for call, (M, N) in enumerate(((512, 1024), (200, 1024), (128, 320), (192, 448), (512, 1024))):
+        raw, wf = _weights(gtype, N, K, rng)
+        if gtype == pm.GGML_Q8_0:
+            blk = raw.reshape(-1, 34)
+            d = blk[:, :2].copy().view(np.float16).astype(np.float32).reshape(-1, 1)
+            q = blk[:, 2:].view(np.int8).astype(np.float32)
+            w16 = (d * q).astype(np.float16).astype(np.float64).reshape(N, K)
+        else:
+            w16 = wf.astype(np.float64)
+        x = rng.normal(0, 1, (M, K)).astype(np.float32)
+        b = rng.normal(0, 0.1, N).astype(np.float32)
+        y0 = rng.normal(0, 1, (M, N)).astype(np.float32)
+        x16 = x.astype(np.float16).astype(np.float64)
+        acc = x16 @ w16.T
+        ref = y0.astype(np.float64) + alpha * (acc + b)
+        # |f32 sum - exact| <= K 2^-24 sum|x w| (+ the rounding of the last adds)
+        bound = K * 2.0 ** -24 * (np.abs(x16) @ np.abs(w16).T) + 2.0 ** -22 * (np.abs(ref) + 1.0)
+        print(f"[split-k] call {call} type={gtype} M={M} N={N} K={K}", flush=True)
+        dx = gpu.DeviceArray.from_numpy(x, stream)
+        db = gpu.DeviceArray.from_numpy(b, stream)
+        dy = gpu.DeviceArray.from_numpy(y0, stream)
+        gpu.linear_residual(1, gtype, N, K, raw, dx, M, dy, alpha, db, stream)
+        got = dy.numpy(stream).astype(np.float64)
+        bad = np.abs(got - ref) > bound
+        if bad.any():
+            i, j = np.argwhere(bad)[0]
+            raise AssertionError(f"call {call}: y[{i}][{j}] = {got[i, j]!r}, float64 {ref[i, j]!r}, "
+                                 f"bound {bound[i, j]:.3g} ({int(bad.sum())} elements outside)")
+        dx.free(), db.free(), dy.free()
