@@ -1504,9 +1504,26 @@ template <int WTN> struct BRaw<GT_F16, WTN> {
     }
 };
 
+// f16 weights slab-major ([K/64][ldw][64] halves): the lane's 32 halves of a
+// slab are 64 contiguous bytes of its column's 128-byte run.
+template <int WTN> struct BRaw<GT_F16_SLAB, WTN> {
+    int4v q[WTN][4];
+    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rq, __amdgpu_buffer_rsrc_t, const uint32_t (&vq)[WTN],
+                                         const uint32_t (&)[WTN], int soq, int) {
+#pragma unroll
+        for (int j = 0; j < WTN; ++j)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) q[j][t] = __builtin_amdgcn_raw_buffer_load_b128(rq, (int)(vq[j] + 16 * t), soq, 0);
+    }
+    __device__ __forceinline__ void convert_j(half8v (&bf)[4], int j, int) const {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) bf[t] = __builtin_bit_cast(half8v, q[j][t]);
+    }
+};
+
 // Vector-memory instructions of one slab's weight loads per wave.
 template <int WT, int WTN>
-constexpr int rb_b_ops() { return WT == GT_F16 ? 4 * WTN : 3 * WTN; }
+constexpr int rb_b_ops() { return WT == GT_F16 || WT == GT_F16_SLAB ? 4 * WTN : 3 * WTN; }
 
 template <int WTM, int WTN, int WT, int EPI, int NS, int TD = 0, bool FO = false>
 struct RbCfg {
@@ -1531,9 +1548,12 @@ struct RbCfg {
     static_assert(WHOLE || WTM % 2 == 0, "row-half staging needs an even WTM");
 };
 
-template <int WTM, int WTN, int WT, int EPI, int NS, int TD = 0, bool FO = false>
-__global__ __launch_bounds__(256, 1) void gemm_rb_kernel(GemmParams p) {
+template <int WTM, int WTN, int WT, int EPI, int NS, int TD = 0, bool FO = false, bool SK = false, int OCC = 1>
+__global__ __launch_bounds__(256, OCC) void gemm_rb_kernel(GemmParams p) {
     typedef RbCfg<WTM, WTN, WT, EPI, NS, TD, FO> C;
+    static_assert(TD == 0 || WT != GT_F16_SLAB, "touch-ahead: q8_0 / q4_K / row-major f16 weights");
+    static_assert(OCC == 1 || 2 * C::LDS <= 160 * 1024, "two workgroups per CU: LDS");
+    static_assert(!SK || EPI == EPI_RESID || EPI == EPI_RESID_LN, "split-K: residual epilogues");
     static_assert(NS >= 3 && NS <= 5, "ring depth");
     static_assert(EPI == EPI_STORE || EPI == EPI_STORE_F32 || EPI == EPI_SILU || EPI == EPI_RESID ||
                       EPI == EPI_RESID_LN,
@@ -1543,10 +1563,21 @@ __global__ __launch_bounds__(256, 1) void gemm_rb_kernel(GemmParams p) {
 
     const int tid = threadIdx.x, lane = tid & 63, wid = wave_id_uniform();
     const int q = lane >> 5, r32 = lane & 31;
-    int bm, bn;
-    xcd_tile_2d(blockIdx.x, cdiv_dev(p.M, BM), cdiv_dev(p.N, C::BN), p.xcd_gm, bm, bn);
+    int bm, bn, tile = 0, split = 0;
+    const int nbm = cdiv_dev(p.M, BM), nbn = cdiv_dev(p.N, C::BN);
+    if constexpr (SK) {
+        // SK: the K range cut over p.ksplit workgroups per tile (consecutive
+        // positions), handed over as in gemm_dma_kernel's split-K
+        const int k = xcd_tile(blockIdx.x, nbm * nbn * p.ksplit);
+        tile = k / p.ksplit;
+        split = k - tile * p.ksplit;
+        xcd_rect(tile, nbm, nbn, p.xcd_gm, bm, bn);
+    } else {
+        xcd_tile_2d(blockIdx.x, nbm, nbn, p.xcd_gm, bm, bn);
+    }
     const int m0 = bm * BM, n0 = bn * C::BN, nw = n0 + wid * 32 * WTN;
-    const int nk = p.K / 64;
+    // slabs of this workgroup: [kb, kb + nk) of the K / 64
+    const int nk = SK ? p.K / 64 / p.ksplit : p.K / 64, kb = split * nk;
 
     // folded LayerNorm (FO: p.fold_stats is set) statistics of the tile's rows:
     // DMA into LDS first (the oldest vector-memory operations, complete by the
@@ -1585,12 +1616,20 @@ __global__ __launch_bounds__(256, 1) void gemm_rb_kernel(GemmParams p) {
     const int L = slab_rows(p);
     __amdgpu_buffer_rsrc_t rq = make_rsrc(p.Wq, 0), rs = rq;
     uint32_t vq[WTN], vs[WTN];
-    if constexpr (WT == GT_Q8_0 || WT == GT_Q4_K) {
+    if constexpr (WT == GT_F16_SLAB) {
+        rq = make_rsrc(p.Wq, ((int64_t)(p.K / 64 - 1) * L + p.N) * 128);
+#pragma unroll
+        for (int j = 0; j < WTN; ++j) {
+            const int n = nw + 32 * j + r32;
+            vq[j] = n < p.N ? (uint32_t)(n * 128 + 64 * q) : OOB;
+            vs[j] = 0;
+        }
+    } else if constexpr (WT == GT_Q8_0 || WT == GT_Q4_K) {
         constexpr int WB = WT == GT_Q8_0 ? 64 : 32, SB = WT == GT_Q8_0 ? 4 : 16;
         // a view into a larger weight keeps the allocation's slab stride L: its
         // last byte is in slab nk-1, row N-1
-        rq = make_rsrc(p.Wq, ((int64_t)(nk - 1) * L + p.N) * WB);
-        rs = make_rsrc(p.Ws, ((int64_t)(nk - 1) * L + p.N) * SB);
+        rq = make_rsrc(p.Wq, ((int64_t)(p.K / 64 - 1) * L + p.N) * WB);
+        rs = make_rsrc(p.Ws, ((int64_t)(p.K / 64 - 1) * L + p.N) * SB);
 #pragma unroll
         for (int j = 0; j < WTN; ++j) {
             const int n = nw + 32 * j + r32;
@@ -1606,18 +1645,20 @@ __global__ __launch_bounds__(256, 1) void gemm_rb_kernel(GemmParams p) {
             vs[j] = 0;
         }
     }
-    // scalar offsets of slab k (out of range past the last slab)
+    // scalar offsets of this workgroup's slab k (out of range past its last slab)
     auto soq = [&](int k) -> int {
         if (k >= nk) return (int)OOB;
-        return WT == GT_Q8_0 ? k * L * 64 : WT == GT_Q4_K ? k * L * 32 : k * 128;
+        const int ka = kb + k;
+        return WT == GT_Q8_0 ? ka * L * 64 : WT == GT_Q4_K ? ka * L * 32 : WT == GT_F16_SLAB ? ka * L * 128 : ka * 128;
     };
     auto sos = [&](int k) -> int {
         if (k >= nk) return (int)OOB;
-        return WT == GT_Q8_0 ? k * L * 4 : WT == GT_Q4_K ? k * L * 16 : 0;
+        const int ka = kb + k;
+        return WT == GT_Q8_0 ? ka * L * 4 : WT == GT_Q4_K ? ka * L * 16 : 0;
     };
     auto issue_a = [&](int k) {
         uint8_t* st = smem + (k % NS) * C::A_STAGE + wid * C::NA * 1024;
-        const int so = k < nk ? k * 128 : (int)OOB;
+        const int so = k < nk ? (kb + k) * 128 : (int)OOB;
 #pragma unroll
         for (int i = 0; i < C::NA; ++i) lds_dma16(ra, st + i * 1024, va[i], so);
     };
@@ -1656,7 +1697,7 @@ __global__ __launch_bounds__(256, 1) void gemm_rb_kernel(GemmParams p) {
     }
     auto touch = [&](int k) {
         if constexpr (TD > 0) {
-            const int kc = min(max(k, 0), nk - 1);
+            const int kc = kb + min(max(k, 0), nk - 1);
             uint8_t* dst = smem + NS * C::A_STAGE + C::FOLD_BYTES;
 #pragma unroll
             for (int t = 0; t < 2; ++t)
@@ -1732,6 +1773,53 @@ __global__ __launch_bounds__(256, 1) void gemm_rb_kernel(GemmParams p) {
     }
     wait_vmcnt<0>();
     __syncthreads();
+
+    if constexpr (SK) {
+        // Partial tiles [tile][split][wave][register][lane] through agent-scope
+        // atomic stores and loads, the last of the tile's workgroups to count
+        // itself summing them in split order (gemm_dma_kernel's handoff; the
+        // argument for the relaxed accesses is written there).
+        constexpr int R = WTM * WTN * 16;
+        const int S = p.ksplit;
+        float* part = p.sk_part + (int64_t)tile * S * (4 * R * 64) + wid * R * 64 + lane;
+#pragma unroll
+        for (int i = 0; i < WTM; ++i)
+#pragma unroll
+            for (int j = 0; j < WTN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    __hip_atomic_store(part + (int64_t)split * (4 * R * 64) + ((i * WTN + j) * 16 + r) * 64,
+                                       acc[i][j][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        wait_vmcnt<0>();   // the partial has reached the device before the count
+        __shared__ int sk_last;
+        __syncthreads();
+        if (tid == 0) {
+            const int seen = __hip_atomic_fetch_add(p.sk_cnt + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            sk_last = seen == S - 1;
+            if (seen == S - 1) __hip_atomic_store(p.sk_cnt + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if (!sk_last) return;
+        float16v own[WTM][WTN];
+#pragma unroll
+        for (int i = 0; i < WTM; ++i)
+#pragma unroll
+            for (int j = 0; j < WTN; ++j) own[i][j] = acc[i][j];
+        for (int t = 0; t < S; ++t) {
+#pragma unroll
+            for (int i = 0; i < WTM; ++i)
+#pragma unroll
+                for (int j = 0; j < WTN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const float v = t == split ? own[i][j][r]
+                                                   : __hip_atomic_load(part + (int64_t)t * (4 * R * 64) +
+                                                                           ((i * WTN + j) * 16 + r) * 64,
+                                                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        acc[i][j][r] = t == 0 ? v : acc[i][j][r] + v;
+                    }
+        }
+    }
 
     // folded LayerNorm: {mean, rstd} of the tile's rows at the top of LDS
     float2v* ftab = (float2v*)(smem + C::LDS) - BM;
@@ -2083,6 +2171,21 @@ static void run_dma(const GemmParams& p, hipStream_t s) {
 }
 
 template <int WTM, int WTN, int WT, int EPI, int NS, int TD = 0>
+static void run_rb_sk(const GemmParams& p, int S, hipStream_t s) {
+    typedef RbCfg<WTM, WTN, WT, EPI, NS, TD> C;
+    require(p.K % (64 * C::U * S) == 0, "gemm: register-B split-K needs K % (256 S) == 0");
+    const int tiles = cdiv(p.M, C::BM) * cdiv(p.N, C::BN);
+    require(p.sk_part && p.sk_cnt && tiles <= p.sk_cnt_n &&
+                (int64_t)tiles * S * 4 * WTM * WTN * 16 * 64 <= p.sk_part_floats,
+            "gemm: register-B split-K workspace too small");
+    GemmParams q = p;
+    q.ksplit = S;
+    q.xcd_gm = choose_xcd_gm(p, WT, C::BM, C::BN);
+    launch((gemm_rb_kernel<WTM, WTN, WT, EPI, NS, TD, false, true>), dim3(tiles * S), dim3(256), 0, s, q);
+    PKX_LAUNCH_CHECK();
+}
+
+template <int WTM, int WTN, int WT, int EPI, int NS, int TD = 0>
 static void run_rb(const GemmParams& p, hipStream_t s) {
     typedef RbCfg<WTM, WTN, WT, EPI, NS, TD> C;
     constexpr bool can_fold = EPI == EPI_STORE || EPI == EPI_SILU;
@@ -2177,12 +2280,16 @@ static bool dma_kg2(int epi, const GemmParams& p, hipStream_t s) {
 // positional projection.  On MI355X at M = 2000, K = 1024 (q8_0): 25.7 against
 // 27.8 us (FFN linear1), 25.0 against 27.7 (q/k/v, folded LayerNorm), 22.2
 // against 24.9 (positional, M = 249, N = 24576) for the LDS-B 128 x 128 tiles.
-// Grids under about 3/4 of the chip keep the LDS-B kernels.
+// Taken when the grid is one round of the chip at least 70% full, or four
+// rounds or more; in between (M = 3000: 384 tiles, a half-empty second round
+// of long workgroups) the LDS-B kernels' finer tiles win (1.1B shape at batch
+// 8 x 30 s: 14.44 against 13.82 ms per forward with the register-B kernel).
 template <int WT>
 static bool dma_rb(int epi, const GemmParams& p, hipStream_t s) {
     if (p.K % 256 != 0 || p.N < 2048 || (p.fold_stats && p.fold_groups > 32)) return false;
     if (epi != EPI_STORE && epi != EPI_SILU && epi != EPI_STORE_F32) return false;
-    if ((int64_t)cdiv(p.M, 128) * cdiv(p.N, 256) * 4 < (int64_t)device_cu_count() * 3) return false;
+    const int64_t tiles = (int64_t)cdiv(p.M, 128) * cdiv(p.N, 256), cus = device_cu_count();
+    if (!((tiles <= cus && tiles * 10 >= cus * 7) || tiles >= 4 * cus)) return false;
     switch (epi) {
     case EPI_STORE: run_rb<4, 2, WT, EPI_STORE, 4>(p, s); break;
     case EPI_SILU: run_rb<4, 2, WT, EPI_SILU, 4>(p, s); break;
