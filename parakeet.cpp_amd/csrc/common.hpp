@@ -23,9 +23,6 @@ typedef int int4v __attribute__((ext_vector_type(4)));
 
 // ggml type ids (the GGUF weight layout)
 enum GgmlType : int { GT_F32 = 0, GT_F16 = 1, GT_Q8_0 = 8, GT_Q4_K = 12 };
-// Device-only storage: f16 weights slab-major, [K/64][ldw][64] halves (the
-// register-B GEMM's layout; no GGUF counterpart)
-constexpr int GT_F16_SLAB = 1001;
 
 // Activation storage type of a compute precision mode.
 enum Precision : int { PREC_F32 = 0, PREC_F16 = 1 };

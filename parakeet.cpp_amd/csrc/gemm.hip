@@ -1504,41 +1504,22 @@ template <int WTN> struct BRaw<GT_F16, WTN> {
     }
 };
 
-// f16 weights slab-major ([K/64][ldw][64] halves): the lane's 32 halves of a
-// slab are 64 contiguous bytes of its column's 128-byte run.
-template <int WTN> struct BRaw<GT_F16_SLAB, WTN> {
-    int4v q[WTN][4];
-    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rq, __amdgpu_buffer_rsrc_t, const uint32_t (&vq)[WTN],
-                                         const uint32_t (&)[WTN], int soq, int) {
-#pragma unroll
-        for (int j = 0; j < WTN; ++j)
-#pragma unroll
-            for (int t = 0; t < 4; ++t) q[j][t] = __builtin_amdgcn_raw_buffer_load_b128(rq, (int)(vq[j] + 16 * t), soq, 0);
-    }
-    __device__ __forceinline__ void convert_j(half8v (&bf)[4], int j, int) const {
-#pragma unroll
-        for (int t = 0; t < 4; ++t) bf[t] = __builtin_bit_cast(half8v, q[j][t]);
-    }
-};
-
 // Vector-memory instructions of one slab's weight loads per wave.
 template <int WT, int WTN>
-constexpr int rb_b_ops() { return WT == GT_F16 || WT == GT_F16_SLAB ? 4 * WTN : 3 * WTN; }
+constexpr int rb_b_ops() { return WT == GT_F16 ? 4 * WTN : 3 * WTN; }
 
-template <int WTM, int WTN, int WT, int EPI, int NS, int TD = 0, bool FO = false>
+template <int WTM, int WTN, int WT, int EPI, int NS, bool FO = false>
 struct RbCfg {
     static constexpr int BM = 32 * WTM, BN = 128 * WTN;
     static constexpr int A_STAGE = BM * 128;                  // f16 [BM][64]
     static constexpr int NA = A_STAGE / 4096;                 // 1 KB A DMAs per wave per slab
     static constexpr int NB = rb_b_ops<WT, WTN>();
-    static constexpr int NT = TD > 0 ? 2 : 0;                 // L2 touch DMAs per wave per slab
-    static constexpr int PER_SLAB = NA + NB + NT;
+    static constexpr int PER_SLAB = NA + NB;
     static constexpr int NR = 4;                              // weight register sets (>= NS - 1 in flight)
     static constexpr int U = 4;                               // loop unroll: every ring index static
     static constexpr bool FOLD = FO && (EPI == EPI_STORE || EPI == EPI_SILU);
     static constexpr int FOLD_BYTES = FOLD ? BM * 32 * 8 : 0; // {mean, M2} of up to 32 groups per row
-    static constexpr int TOUCH = TD > 0 ? 256 : 0;            // destination of the touch DMAs
-    static constexpr int MAIN = NS * A_STAGE + FOLD_BYTES + TOUCH;
+    static constexpr int MAIN = NS * A_STAGE + FOLD_BYTES;
     static constexpr int STG_WHOLE = 4 * 32 * WTM * (32 * WTN + 4) * 4;
     static constexpr bool WHOLE = STG_WHOLE + BM * 8 <= 160 * 1024 - 1024;
     static constexpr int STG = WHOLE ? STG_WHOLE : STG_WHOLE / 2;
@@ -1548,58 +1529,41 @@ struct RbCfg {
     static_assert(WHOLE || WTM % 2 == 0, "row-half staging needs an even WTM");
 };
 
-template <int WTM, int WTN, int WT, int EPI, int NS, int TD = 0, bool FO = false, bool SK = false, int OCC = 1>
-__global__ __launch_bounds__(256, OCC) void gemm_rb_kernel(GemmParams p) {
-    typedef RbCfg<WTM, WTN, WT, EPI, NS, TD, FO> C;
-    static_assert(TD == 0 || WT != GT_F16_SLAB, "touch-ahead: q8_0 / q4_K / row-major f16 weights");
-    static_assert(OCC == 1 || 2 * C::LDS <= 160 * 1024, "two workgroups per CU: LDS");
-    static_assert(!SK || EPI == EPI_RESID || EPI == EPI_RESID_LN, "split-K: residual epilogues");
+template <int WTM, int WTN, int WT, int EPI, int NS, bool FO = false>
+__global__ __launch_bounds__(256, 1) void gemm_rb_kernel(GemmParams p) {
+    typedef RbCfg<WTM, WTN, WT, EPI, NS, FO> C;
     static_assert(NS >= 3 && NS <= 5, "ring depth");
-    static_assert(EPI == EPI_STORE || EPI == EPI_STORE_F32 || EPI == EPI_SILU || EPI == EPI_RESID ||
-                      EPI == EPI_RESID_LN,
-                  "register-B kernel: LDS-staged epilogues only");
+    static_assert(EPI == EPI_STORE || EPI == EPI_STORE_F32 || EPI == EPI_SILU,
+                  "register-B kernel: store / SiLU epilogues (the wide products it runs)");
     constexpr int BM = C::BM, NR = C::NR;
     __shared__ __attribute__((aligned(1024))) uint8_t smem[C::LDS];
 
     const int tid = threadIdx.x, lane = tid & 63, wid = wave_id_uniform();
     const int q = lane >> 5, r32 = lane & 31;
-    int bm, bn, tile = 0, split = 0;
-    const int nbm = cdiv_dev(p.M, BM), nbn = cdiv_dev(p.N, C::BN);
-    if constexpr (SK) {
-        // SK: the K range cut over p.ksplit workgroups per tile (consecutive
-        // positions), handed over as in gemm_dma_kernel's split-K
-        const int k = xcd_tile(blockIdx.x, nbm * nbn * p.ksplit);
-        tile = k / p.ksplit;
-        split = k - tile * p.ksplit;
-        xcd_rect(tile, nbm, nbn, p.xcd_gm, bm, bn);
-    } else {
-        xcd_tile_2d(blockIdx.x, nbm, nbn, p.xcd_gm, bm, bn);
-    }
+    int bm, bn;
+    xcd_tile_2d(blockIdx.x, cdiv_dev(p.M, BM), cdiv_dev(p.N, C::BN), p.xcd_gm, bm, bn);
     const int m0 = bm * BM, n0 = bn * C::BN, nw = n0 + wid * 32 * WTN;
-    // slabs of this workgroup: [kb, kb + nk) of the K / 64
-    const int nk = SK ? p.K / 64 / p.ksplit : p.K / 64, kb = split * nk;
+    const int nk = p.K / 64;
 
     // folded LayerNorm (FO: p.fold_stats is set) statistics of the tile's rows:
     // DMA into LDS first (the oldest vector-memory operations, complete by the
     // first slab's wait)
     constexpr bool fold = C::FOLD;
-    if constexpr (C::FOLD) {
-        if (fold) {
-            const int lc = __builtin_ctz(p.fold_groups / 2), total = BM << lc;   // 16-byte chunks
-            const __amdgpu_buffer_rsrc_t rf =
-                make_rsrc((const float2v*)p.fold_stats + (int64_t)m0 * p.fold_groups,
-                          ((int64_t)(p.M - m0) * p.fold_groups) * 8);
-            uint8_t* fl = smem + NS * C::A_STAGE;
-            for (int c0 = wid * 64; c0 < total; c0 += 256) {
-                const int ch = c0 + lane, r = ch >> lc;
-                const uint32_t off = ch < total ? (uint32_t)(min(r, p.M - 1 - m0) << (lc + 4)) + ((ch & ((1 << lc) - 1)) << 4)
-                                                : OOB;
-                lds_dma16(rf, fl + c0 * 16, off, 0);
-            }
+    if constexpr (fold) {
+        const int lc = __builtin_ctz(p.fold_groups / 2), total = BM << lc;   // 16-byte chunks
+        const __amdgpu_buffer_rsrc_t rf =
+            make_rsrc((const float2v*)p.fold_stats + (int64_t)m0 * p.fold_groups,
+                      ((int64_t)(p.M - m0) * p.fold_groups) * 8);
+        uint8_t* fl = smem + NS * C::A_STAGE;
+        for (int c0 = wid * 64; c0 < total; c0 += 256) {
+            const int ch = c0 + lane, r = ch >> lc;
+            const uint32_t off = ch < total ? (uint32_t)(min(r, p.M - 1 - m0) << (lc + 4)) + ((ch & ((1 << lc) - 1)) << 4)
+                                            : OOB;
+            lds_dma16(rf, fl + c0 * 16, off, 0);
         }
     }
     EpiCols<WTN> ecol;
-    ecol.load(p, nw, lane, fold, EPI == EPI_RESID_LN);
+    ecol.load(p, nw, lane, fold, false);
 
     // A: 64-column slabs of rows m0.., swizzled 16-byte chunks (as DmaSrc)
     const __amdgpu_buffer_rsrc_t ra =
@@ -1616,20 +1580,12 @@ __global__ __launch_bounds__(256, OCC) void gemm_rb_kernel(GemmParams p) {
     const int L = slab_rows(p);
     __amdgpu_buffer_rsrc_t rq = make_rsrc(p.Wq, 0), rs = rq;
     uint32_t vq[WTN], vs[WTN];
-    if constexpr (WT == GT_F16_SLAB) {
-        rq = make_rsrc(p.Wq, ((int64_t)(p.K / 64 - 1) * L + p.N) * 128);
-#pragma unroll
-        for (int j = 0; j < WTN; ++j) {
-            const int n = nw + 32 * j + r32;
-            vq[j] = n < p.N ? (uint32_t)(n * 128 + 64 * q) : OOB;
-            vs[j] = 0;
-        }
-    } else if constexpr (WT == GT_Q8_0 || WT == GT_Q4_K) {
+    if constexpr (WT == GT_Q8_0 || WT == GT_Q4_K) {
         constexpr int WB = WT == GT_Q8_0 ? 64 : 32, SB = WT == GT_Q8_0 ? 4 : 16;
         // a view into a larger weight keeps the allocation's slab stride L: its
         // last byte is in slab nk-1, row N-1
-        rq = make_rsrc(p.Wq, ((int64_t)(p.K / 64 - 1) * L + p.N) * WB);
-        rs = make_rsrc(p.Ws, ((int64_t)(p.K / 64 - 1) * L + p.N) * SB);
+        rq = make_rsrc(p.Wq, ((int64_t)(nk - 1) * L + p.N) * WB);
+        rs = make_rsrc(p.Ws, ((int64_t)(nk - 1) * L + p.N) * SB);
 #pragma unroll
         for (int j = 0; j < WTN; ++j) {
             const int n = nw + 32 * j + r32;
@@ -1645,66 +1601,20 @@ __global__ __launch_bounds__(256, OCC) void gemm_rb_kernel(GemmParams p) {
             vs[j] = 0;
         }
     }
-    // scalar offsets of this workgroup's slab k (out of range past its last slab)
+    // scalar offsets of slab k (out of range past the last slab)
     auto soq = [&](int k) -> int {
         if (k >= nk) return (int)OOB;
-        const int ka = kb + k;
-        return WT == GT_Q8_0 ? ka * L * 64 : WT == GT_Q4_K ? ka * L * 32 : WT == GT_F16_SLAB ? ka * L * 128 : ka * 128;
+        return WT == GT_Q8_0 ? k * L * 64 : WT == GT_Q4_K ? k * L * 32 : k * 128;
     };
     auto sos = [&](int k) -> int {
         if (k >= nk) return (int)OOB;
-        const int ka = kb + k;
-        return WT == GT_Q8_0 ? ka * L * 4 : WT == GT_Q4_K ? ka * L * 16 : 0;
+        return WT == GT_Q8_0 ? k * L * 4 : WT == GT_Q4_K ? k * L * 16 : 0;
     };
     auto issue_a = [&](int k) {
         uint8_t* st = smem + (k % NS) * C::A_STAGE + wid * C::NA * 1024;
-        const int so = k < nk ? (kb + k) * 128 : (int)OOB;
+        const int so = k < nk ? k * 128 : (int)OOB;
 #pragma unroll
         for (int i = 0; i < C::NA; ++i) lds_dma16(ra, st + i * 1024, va[i], so);
-    };
-    // L2 touch-ahead (TD > 0): slab k + TD's cache lines of this wave's A rows
-    // and weight columns are requested TD slabs early by two 4-byte DMAs into
-    // a scratch word per lane, so the slab's real loads hit in L2.  Lane
-    // addresses: line of slab 0 plus a per-slab stride.
-    const uint8_t* tb[2] = {nullptr, nullptr};
-    uint32_t ts[2] = {0, 0};
-    if constexpr (TD > 0) {
-        constexpr int RW = BM / 4;   // A rows touched per wave
-        const int cmax = p.N - 1;
-        if (lane < RW) {
-            tb[0] = (const uint8_t*)((const f16*)p.A + (int64_t)min(m0 + wid * RW + lane, p.M - 1) * p.lda);
-            ts[0] = 128;
-        } else if constexpr (WT == GT_Q8_0) {
-            tb[0] = (const uint8_t*)p.Ws + (int64_t)min(nw + 32 * ((lane - RW) & 1), cmax) * 4;
-            ts[0] = (uint32_t)L * 4;
-        } else if constexpr (WT == GT_Q4_K) {
-            tb[0] = (const uint8_t*)p.Ws + (int64_t)min(nw + 8 * ((lane - RW) & 7), cmax) * 16;
-            ts[0] = (uint32_t)L * 16;
-        } else {
-            tb[0] = (const uint8_t*)((const f16*)p.A + (int64_t)min(m0 + wid * RW + lane % RW, p.M - 1) * p.lda);
-            ts[0] = 128;
-        }
-        if constexpr (WT == GT_Q8_0) {
-            tb[1] = (const uint8_t*)p.Wq + (int64_t)min(nw + 2 * (lane & 31), cmax) * 64;
-            ts[1] = (uint32_t)L * 64;
-        } else if constexpr (WT == GT_Q4_K) {
-            tb[1] = (const uint8_t*)p.Wq + (int64_t)min(nw + 4 * (lane & 15), cmax) * 32;
-            ts[1] = (uint32_t)L * 32;
-        } else {
-            tb[1] = (const uint8_t*)p.Wq + (int64_t)min(nw + lane, cmax) * p.K * 2;
-            ts[1] = 128;
-        }
-    }
-    auto touch = [&](int k) {
-        if constexpr (TD > 0) {
-            const int kc = kb + min(max(k, 0), nk - 1);
-            uint8_t* dst = smem + NS * C::A_STAGE + C::FOLD_BYTES;
-#pragma unroll
-            for (int t = 0; t < 2; ++t)
-                __builtin_amdgcn_global_load_lds(
-                    (const __attribute__((address_space(1))) void*)(tb[t] + (uint64_t)kc * ts[t]),
-                    (__attribute__((address_space(3))) void*)dst, 4, 0, 0);
-        }
     };
 
     float16v acc[WTM][WTN];
@@ -1731,9 +1641,8 @@ __global__ __launch_bounds__(256, OCC) void gemm_rb_kernel(GemmParams p) {
     for (int k = 0; k < NS - 1; ++k) {
         issue_a(k);
         braw[k % NR].load(rq, rs, vq, vs, soq(k), sos(k));
-        touch(k - (NS - 1) + TD);
     }
-    wait_vmcnt<(NS - 2) * C::PER_SLAB + C::NT>();
+    wait_vmcnt<(NS - 2) * C::PER_SLAB>();
     __builtin_amdgcn_s_barrier();
     read_a(af[0], 0);
 #pragma unroll
@@ -1745,11 +1654,10 @@ __global__ __launch_bounds__(256, OCC) void gemm_rb_kernel(GemmParams p) {
         for (int u = 0; u < C::U; ++u) {
             const int k = k0 + u;
             // slab k+1 (A in LDS from every wave, B in this wave's registers) has landed
-            wait_vmcnt<(NS - 3) * C::PER_SLAB + C::NT>();
+            wait_vmcnt<(NS - 3) * C::PER_SLAB>();
             __builtin_amdgcn_s_barrier();
             issue_a(k + NS - 1);
             braw[(u + NS - 1) % NR].load(rq, rs, vq, vs, soq(k + NS - 1), sos(k + NS - 1));
-            touch(k + TD);
             const int cu = u & 1, nx = cu ^ 1;
             // the MFMAs of slab k, with the next slab's A reads and weight
             // dequantisation interleaved (one MFMA, then an LDS read or four VALU)
@@ -1774,67 +1682,18 @@ __global__ __launch_bounds__(256, OCC) void gemm_rb_kernel(GemmParams p) {
     wait_vmcnt<0>();
     __syncthreads();
 
-    if constexpr (SK) {
-        // Partial tiles [tile][split][wave][register][lane] through agent-scope
-        // atomic stores and loads, the last of the tile's workgroups to count
-        // itself summing them in split order (gemm_dma_kernel's handoff; the
-        // argument for the relaxed accesses is written there).
-        constexpr int R = WTM * WTN * 16;
-        const int S = p.ksplit;
-        float* part = p.sk_part + (int64_t)tile * S * (4 * R * 64) + wid * R * 64 + lane;
-#pragma unroll
-        for (int i = 0; i < WTM; ++i)
-#pragma unroll
-            for (int j = 0; j < WTN; ++j)
-#pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    __hip_atomic_store(part + (int64_t)split * (4 * R * 64) + ((i * WTN + j) * 16 + r) * 64,
-                                       acc[i][j][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        wait_vmcnt<0>();   // the partial has reached the device before the count
-        __shared__ int sk_last;
-        __syncthreads();
-        if (tid == 0) {
-            const int seen = __hip_atomic_fetch_add(p.sk_cnt + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            sk_last = seen == S - 1;
-            if (seen == S - 1) __hip_atomic_store(p.sk_cnt + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        __syncthreads();
-        if (!sk_last) return;
-        float16v own[WTM][WTN];
-#pragma unroll
-        for (int i = 0; i < WTM; ++i)
-#pragma unroll
-            for (int j = 0; j < WTN; ++j) own[i][j] = acc[i][j];
-        for (int t = 0; t < S; ++t) {
-#pragma unroll
-            for (int i = 0; i < WTM; ++i)
-#pragma unroll
-                for (int j = 0; j < WTN; ++j)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const float v = t == split ? own[i][j][r]
-                                                   : __hip_atomic_load(part + (int64_t)t * (4 * R * 64) +
-                                                                           ((i * WTN + j) * 16 + r) * 64,
-                                                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        acc[i][j][r] = t == 0 ? v : acc[i][j][r] + v;
-                    }
-        }
-    }
-
     // folded LayerNorm: {mean, rstd} of the tile's rows at the top of LDS
     float2v* ftab = (float2v*)(smem + C::LDS) - BM;
-    if constexpr (C::FOLD) {
-        if (fold) {
-            FoldStats<BM> fst;
-            const int lc = __builtin_ctz(p.fold_groups / 2), total = BM << lc;
+    if constexpr (fold) {
+        FoldStats<BM> fst;
+        const int lc = __builtin_ctz(p.fold_groups / 2), total = BM << lc;
 #pragma unroll
-            for (int i = 0; i < FoldStats<BM>::MAXC; ++i) {
-                const int ch = tid + 256 * i;
-                fst.c[i] = ch < total ? ((const float4v*)(smem + NS * C::A_STAGE))[ch] : (float4v){0.f, 0.f, 0.f, 0.f};
-            }
-            fst.finish(p, ftab, tid);
-            __syncthreads();
+        for (int i = 0; i < FoldStats<BM>::MAXC; ++i) {
+            const int ch = tid + 256 * i;
+            fst.c[i] = ch < total ? ((const float4v*)(smem + NS * C::A_STAGE))[ch] : (float4v){0.f, 0.f, 0.f, 0.f};
         }
+        fst.finish(p, ftab, tid);
+        __syncthreads();
     }
     if constexpr (C::WHOLE) {
         float* wsm = (float*)smem + wid * (32 * WTM) * (32 * WTN + 4);
@@ -2170,32 +2029,17 @@ static void run_dma(const GemmParams& p, hipStream_t s) {
     }
 }
 
-template <int WTM, int WTN, int WT, int EPI, int NS, int TD = 0>
-static void run_rb_sk(const GemmParams& p, int S, hipStream_t s) {
-    typedef RbCfg<WTM, WTN, WT, EPI, NS, TD> C;
-    require(p.K % (64 * C::U * S) == 0, "gemm: register-B split-K needs K % (256 S) == 0");
-    const int tiles = cdiv(p.M, C::BM) * cdiv(p.N, C::BN);
-    require(p.sk_part && p.sk_cnt && tiles <= p.sk_cnt_n &&
-                (int64_t)tiles * S * 4 * WTM * WTN * 16 * 64 <= p.sk_part_floats,
-            "gemm: register-B split-K workspace too small");
-    GemmParams q = p;
-    q.ksplit = S;
-    q.xcd_gm = choose_xcd_gm(p, WT, C::BM, C::BN);
-    launch((gemm_rb_kernel<WTM, WTN, WT, EPI, NS, TD, false, true>), dim3(tiles * S), dim3(256), 0, s, q);
-    PKX_LAUNCH_CHECK();
-}
-
-template <int WTM, int WTN, int WT, int EPI, int NS, int TD = 0>
+template <int WTM, int WTN, int WT, int EPI, int NS>
 static void run_rb(const GemmParams& p, hipStream_t s) {
-    typedef RbCfg<WTM, WTN, WT, EPI, NS, TD> C;
+    typedef RbCfg<WTM, WTN, WT, EPI, NS> C;
     constexpr bool can_fold = EPI == EPI_STORE || EPI == EPI_SILU;
     require(p.K % (64 * C::U) == 0, "gemm: register-B kernel needs K % 256 == 0");
     if (p.fold_stats) require(p.fold_groups <= 32, "gemm: register-B kernel folds at most 32 statistics groups");
     const int tiles = cdiv(p.M, C::BM) * cdiv(p.N, C::BN);
     GemmParams q = p;
     q.xcd_gm = choose_xcd_gm(p, WT, C::BM, C::BN);
-    if (can_fold && p.fold_stats) launch((gemm_rb_kernel<WTM, WTN, WT, EPI, NS, TD, can_fold>), dim3(tiles), dim3(256), 0, s, q);
-    else launch((gemm_rb_kernel<WTM, WTN, WT, EPI, NS, TD, false>), dim3(tiles), dim3(256), 0, s, q);
+    if (can_fold && p.fold_stats) launch((gemm_rb_kernel<WTM, WTN, WT, EPI, NS, can_fold>), dim3(tiles), dim3(256), 0, s, q);
+    else launch((gemm_rb_kernel<WTM, WTN, WT, EPI, NS, false>), dim3(tiles), dim3(256), 0, s, q);
     PKX_LAUNCH_CHECK();
 }
 
