@@ -16,6 +16,9 @@
 //     per-step host methods (forward, step, step_logits) do not exist, since
 //     transducer_greedy_batch runs every step on the device.
 //   * A failing forward throws std::runtime_error (the reference asserts).
+//   * Subsampling::forward takes in_valid_frames up to T (the whole window);
+//     a larger count is refused (the reference would report a valid length
+//     past Tout for frames the window does not have).
 // Classes and their reference declarations:
 //   pk::ModelLoader       src/model_loader.hpp:53-83
 //   pk::ParakeetConfig    src/model_loader.hpp:27-52 (same fields and types)
