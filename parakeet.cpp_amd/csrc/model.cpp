@@ -576,6 +576,11 @@ void Model::finalize() {
         sub_.b6 = upload_f32(need(p + "conv.6.bias"));
         sub_.out = make_weight(need(p + "out.weight"), D, C * F, f16g);
         sub_.bout = upload_f32(need(p + "out.bias"));
+        if (sub_tail_fused()) {
+            sub_.tail_w = dalloc(sub_tail_frag_bytes());
+            sub_tail_prepare(sub_.w3.q, sub_.w6.q, sub_.tail_w, nullptr);
+            PKX_HIP(hipDeviceSynchronize());
+        }
     }
 
     // optional heads (always on the f32 GEMM path: argmax outputs)
@@ -923,8 +928,10 @@ void Model::ensure_ws(int B, int T_max) {
     Ws& w = *ws_;
     // (the conv0 map, B x T1 x F1 x C, is never materialised: see launch_sub_stage1)
     grow(w.a2, (size_t)B * T2 * F2 * C * as);
-    grow(w.a2p, (size_t)B * T2 * F2 * C * as);
-    grow(w.a3, (size_t)B * T3 * F3 * C * as);
+    if (!sub_tail_fused()) {   // the fused tail keeps both maps on chip
+        grow(w.a2p, (size_t)B * T2 * F2 * C * as);
+        grow(w.a3, (size_t)B * T3 * F3 * C * as);
+    }
     grow(w.flat, (size_t)B * T3 * F3 * C * as);
     grow(w.h, M * D * as);
     grow(w.u, M * c.ff_dim * as);
@@ -1014,6 +1021,15 @@ int Model::stage_lengths(int B, int T_max, const int* valid_T, int* valid_out, h
 }
 
 // The subsampling kernels on lengths staged by stage_lengths.
+bool Model::sub_tail_fused() const {
+    const ModelConfig& c = cfg_;
+    const bool cz = c.causal_sub != 0;
+    const int F2 = sub_stage_len(sub_stage_len(c.n_mels, cz), cz);
+    return prec_ == PREC_F16 && sub_tail_supported(c.sub_channels, F2, cz) && sub_.w3.gtype == GT_F16 &&
+           sub_.w6.gtype == GT_F16 && sub_.w3.N == c.sub_channels && sub_.w3.K == c.sub_channels &&
+           sub_.w6.N == c.sub_channels && sub_.w6.K == c.sub_channels;
+}
+
 void Model::subsampling_kernels(const float* mel, int B, int T_max, bool stage_masks, float* out, hipStream_t s,
                                 bool apply_xscaling) {
     const ModelConfig& c = cfg_;
@@ -1032,11 +1048,17 @@ void Model::subsampling_kernels(const float* mel, int B, int T_max, bool stage_m
     mark(KF_SUBSAMPLING, true);
     launch_sub_stage1(prec_, mel, stage_masks ? dv : nullptr, stage_masks ? dv + Bc : nullptr, sub_.w0, sub_.b0,
                       sub_.w2, sub_.b2, w.a2.p, B, F, T_max, C, s, cz);
-    gemm(sub_.w3, EPI_RELU, w.a2.p, C, (int64_t)B * T2 * F2, sub_.b3, w.a2p.p, C, 1.f, nullptr, 1, s, prec_, -1);
-    launch_sub_dwconv(prec_, w.a2p.p, stage_masks ? dv + 2 * Bc : nullptr, sub_.w5, sub_.b5, w.a3.p, B, T2, F2, C, s,
-                      cz);
-    gemm(sub_.w6, EPI_RELU_TR, w.a3.p, C, (int64_t)B * T3 * F3, sub_.b6, w.flat.p, 0, 1.f, dv + 3 * Bc, T3, s,
-         prec_, -1, nullptr, F3);
+    if (sub_tail_fused()) {
+        launch_sub_tail(w.a2.p, sub_.tail_w, sub_.b3, sub_.w5, sub_.b5, sub_.b6, stage_masks ? dv + 2 * Bc : nullptr,
+                        dv + 3 * Bc, w.flat.p, B, T2, T3, s);
+    } else {
+        gemm(sub_.w3, EPI_RELU, w.a2.p, C, (int64_t)B * T2 * F2, sub_.b3, w.a2p.p, C, 1.f, nullptr, 1, s, prec_,
+             -1);
+        launch_sub_dwconv(prec_, w.a2p.p, stage_masks ? dv + 2 * Bc : nullptr, sub_.w5, sub_.b5, w.a3.p, B, T2, F2,
+                          C, s, cz);
+        gemm(sub_.w6, EPI_RELU_TR, w.a3.p, C, (int64_t)B * T3 * F3, sub_.b6, w.flat.p, 0, 1.f, dv + 3 * Bc, T3, s,
+             prec_, -1, nullptr, F3);
+    }
     const float xs = (apply_xscaling && c.xscaling) ? std::sqrt((float)c.d_model) : 1.0f;  // encoder.cpp:122-124
     gemm(sub_.out, EPI_STORE_F32, w.flat.p, (int64_t)C * F3, (int64_t)B * T3, sub_.bout, out, c.d_model, xs,
          nullptr, 1, s, prec_, -1);

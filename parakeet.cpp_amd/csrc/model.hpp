@@ -18,6 +18,7 @@
 #include "common.hpp"
 #include "elementwise.hpp"
 #include "gemm.hpp"
+#include "subsampling.hpp"
 
 namespace pkx {
 
@@ -81,6 +82,7 @@ struct SubDev {
     float *w0 = nullptr, *b0 = nullptr, *w2 = nullptr, *b2 = nullptr, *w5 = nullptr, *b5 = nullptr;
     DevWeight w3, w6, out;
     float *b3 = nullptr, *b6 = nullptr, *bout = nullptr;
+    void* tail_w = nullptr;   // conv.3 / conv.6 in MFMA fragment order (fused tail only)
 };
 
 struct HeadsDev {
@@ -236,6 +238,9 @@ private:
     int stage_lengths(int B, int T_max, const int* valid_T, int* valid_out, hipStream_t s, bool whole_frames);
     void subsampling_kernels(const float* mel, int B, int T_max, bool stage_masks, float* out, hipStream_t s,
                              bool apply_xscaling);
+    // conv.3 -> conv.5 -> conv.6 -> flatten as one kernel (launch_sub_tail):
+    // f16 mode, 256 channels, 128 mel bins, symmetric padding, f16 pointwise weights
+    bool sub_tail_fused() const;
     void encoder_kernels(const float* mel, int B, int T_max, int T3, bool stage_masks, float* out, float* capture,
                          hipStream_t s);
     void layer_body(int l, float* x, int B, int T, const int* d_valid, bool first_ln_done,
