@@ -1046,8 +1046,12 @@ void Model::subsampling_kernels(const float* mel, int B, int T_max, bool stage_m
     const int* dv = w.d_valid;
     const int Bc = w.Bcap;
     mark(KF_SUBSAMPLING, true);
-    launch_sub_stage1(prec_, mel, stage_masks ? dv : nullptr, stage_masks ? dv + Bc : nullptr, sub_.w0, sub_.b0,
-                      sub_.w2, sub_.b2, w.a2.p, B, F, T_max, C, s, cz);
+    if (prec_ == PREC_F16 && sub_stage1_mfma_supported(C, F, cz))
+        launch_sub_stage1_mfma(mel, stage_masks ? dv : nullptr, stage_masks ? dv + Bc : nullptr, sub_.w0, sub_.b0,
+                               sub_.w2, sub_.b2, w.a2.p, B, T_max, s);
+    else
+        launch_sub_stage1(prec_, mel, stage_masks ? dv : nullptr, stage_masks ? dv + Bc : nullptr, sub_.w0, sub_.b0,
+                          sub_.w2, sub_.b2, w.a2.p, B, F, T_max, C, s, cz);
     if (sub_tail_fused()) {
         launch_sub_tail(w.a2.p, sub_.tail_w, sub_.b3, sub_.w5, sub_.b5, sub_.b6, stage_masks ? dv + 2 * Bc : nullptr,
                         dv + 3 * Bc, w.flat.p, B, T2, T3, s);

@@ -4,6 +4,17 @@
 
 namespace pkx {
 
+// Subsampling stage 1 on the matrix cores (f16 mode): conv.0 (1 -> 256,
+// 3x3, stride 2, pad 1) + bias + ReLU over mel [B][128][T] f32 (frames
+// t >= valid0[b] zero when valid0 is set), the stage mask on its rows
+// (t1 >= valid1[b] zero when valid1 is set) and the depthwise conv.2 + bias;
+// output channels-last [B][T2][32][256] f16 (subsampling.cpp:143-184).  The
+// mel values and conv.0 taps are rounded to f16 (f32 accumulation), the
+// conv.0 map is kept in f32, as in launch_sub_stage1's f16 mode.
+bool sub_stage1_mfma_supported(int C, int F, bool causal);
+void launch_sub_stage1_mfma(const float* mel, const int* valid0, const int* valid1, const float* w0, const float* b0,
+                            const float* w2, const float* b2, void* out, int B, int T, hipStream_t s);
+
 // Subsampling tail, fused: conv.3 (pointwise C -> C, 1x1) + bias + ReLU,
 // the stage mask on its rows (t2 >= valid2[b] zero when valid2 is set),
 // conv.5 (depthwise 3x3, stride 2, zero padding 1) + bias, conv.6

@@ -64,9 +64,11 @@ def test_subsampling(gpu, stream, name, mask_mode, T, valid_T):
     assert rel_l2(got[mask], ref[mask]) < _tol(prec)
 
 
-# F16 subsampling at the production channel count (a multiple of 64): conv0
-# runs on the matrix cores there (f16 mel and weights, f32 accumulation, the
-# conv0 map staged in f16), so it is checked on its own against the oracle.
+# F16 subsampling at production channel counts, checked on its own against the
+# oracle.  128 mel bins with 256 channels take the matrix-core kernels
+# (launch_sub_stage1_mfma: conv.0 as an MFMA product over f16 mel taps, f32
+# accumulation; launch_sub_tail: conv.3 -> conv.5 -> conv.6 fused); 80 bins
+# and 192 channels the general kernels (conv.0 as packed f16 dot products).
 SUB_F16 = {
     "128mel_c256": dict(d_model=256, n_heads=2, ff_dim=512, n_mels=128, sub_channels=256),
     "80mel_c256": dict(d_model=256, n_heads=2, ff_dim=512, n_mels=80, sub_channels=256),
