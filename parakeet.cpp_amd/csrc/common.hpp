@@ -113,8 +113,8 @@ __device__ __forceinline__ float group_sum(float v, int n) {
 // xcd_tile gives each XCD a contiguous range of work positions (a bijection
 // on [0, total)), so neighbouring work items share one XCD's L2.
 __device__ __forceinline__ int xcd_tile(int bid, int total) {
-    const int per = total / 8, rem = total % 8;
-    const int x = bid % 8, loc = bid / 8;
+    const int per = (int)((unsigned)total >> 3), rem = total & 7;
+    const int x = bid & 7, loc = (int)((unsigned)bid >> 3);
     return x * per + (x < rem ? x : rem) + loc;
 }
 

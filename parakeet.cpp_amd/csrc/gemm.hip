@@ -16,6 +16,16 @@ namespace pkx {
 // into a larger allocation keep the allocation's row count).
 __device__ __forceinline__ int slab_rows(const GemmParams& p) { return p.ldw > 0 ? p.ldw : p.N; }
 
+// The arguments every GEMM prologue reads, pulled into SGPRs in one batch of
+// scalar loads at kernel entry.  Left to itself the compiler loads the
+// pointers the prologue uses later (residual stream, bias) only after the
+// first batch has returned: a second serialized argument fetch of ~1k cycles
+// before the first DMA is issued.
+__device__ __forceinline__ void prefetch_gemm_args(const GemmParams& p) {
+    asm volatile("" ::"s"(p.M), "s"(p.N), "s"(p.K), "s"(p.xcd_gm), "s"(p.ldw), "s"(p.A), "s"(p.lda), "s"(p.Wq),
+                 "s"(p.Ws), "s"(p.Y), "s"(p.ldy), "s"(p.bias));
+}
+
 // Wave index as a wave-uniform (scalar) value.
 __device__ __forceinline__ int wave_id_uniform() { return __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6); }
 
@@ -25,16 +35,22 @@ __device__ __forceinline__ int wave_id_uniform() { return __builtin_amdgcn_readf
 // over the chip instead of 8*|A| or 8*|W|).  xcd_tile gives each XCD a
 // contiguous range of positions; positions enumerate the rectangles in order,
 // each rectangle M-fastest, so the map is a bijection for any grid size.
+// gm and gn are powers of two, so the band edges i * nbm / gm are shifts; the
+// one division left is the split of k inside its rectangle.  (With a division
+// for every band edge this ran ~3k cycles at the start of every launch, all
+// of it before the first load: 32-bit division by a runtime value is a
+// ~40-instruction scalar / vector round trip on this hardware.)
 __device__ __forceinline__ void xcd_rect(int k, int nbm, int nbn, int gm, int& bm, int& bn) {
-    const int gn = 8 / gm;
+    const int lgm = __builtin_ctz(gm), lgn = 3 - lgm;
     for (int i = 0; i < gm; ++i) {
-        const int r0 = i * nbm / gm, r1 = (i + 1) * nbm / gm;
-        for (int j = 0; j < gn; ++j) {
-            const int c0 = j * nbn / gn, c1 = (j + 1) * nbn / gn;
-            const int sz = (r1 - r0) * (c1 - c0);
-            if (k < sz) {
-                bm = r0 + k % (r1 - r0);
-                bn = c0 + k / (r1 - r0);
+        const int r0 = (i * nbm) >> lgm, r1 = ((i + 1) * nbm) >> lgm;
+        for (int j = 0; j < (1 << lgn); ++j) {
+            const int c0 = (j * nbn) >> lgn, c1 = ((j + 1) * nbn) >> lgn;
+            const int h = r1 - r0, sz = h * (c1 - c0);
+            if (k < sz) {   // sz > 0, so h > 0
+                const int q = (int)((unsigned)k / (unsigned)h);
+                bm = r0 + (k - q * h);
+                bn = c0 + q;
                 return;
             }
             k -= sz;
@@ -837,14 +853,27 @@ struct ResidPre {
     static_assert(NT * 64 == WR * CPR, "whole chunks per lane");
     float4v v[NT];
     float2v rs[RS ? NT : 1];
+    // Raw buffer loads over the wave's rows (rows past M, and float4s reaching
+    // past N, are out of range and read zero): one offset add and one load per
+    // chunk, where guarded global loads took a branch and 64-bit address
+    // arithmetic each (~1.5k cycles before the first DMA of the product).
     __device__ __forceinline__ void load(const GemmParams& p, int mw, int nw, int lane) {
+        const int rows = min(WR, p.M - mw);   // valid rows of the wave tile (<= 0: none)
+        const __amdgpu_buffer_rsrc_t ry =
+            make_rsrc((const float*)p.Y + (int64_t)max(mw, 0) * p.ldy,
+                      rows > 0 ? ((int64_t)(rows - 1) * p.ldy + p.N) * 4 : 0);
+        __amdgpu_buffer_rsrc_t rr = ry;
+        if constexpr (RS) rr = make_rsrc((const float2v*)p.res_rows + max(mw, 0), rows > 0 ? (int64_t)rows * 8 : 0);
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            const int c = lane + 64 * t, m = mw + c / CPR, n = nw + (c % CPR) * 4;
-            v[t] = m < p.M && n + 3 < p.N ? *(const float4v*)((const float*)p.Y + (int64_t)m * p.ldy + n)
-                                          : (float4v){0.f, 0.f, 0.f, 0.f};
+            const int c = lane + 64 * t, r = c / CPR, n = nw + (c % CPR) * 4;
+            const uint32_t off = r < rows && n + 3 < p.N ? (uint32_t)((r * p.ldy + n) * 4) : OOB;
+            v[t] = __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(ry, off, 0, 0));
             if constexpr (RS) {
-                if (p.res_rows) rs[t] = m < p.M ? ((const float2v*)p.res_rows)[m] : (float2v){0.f, 0.f};
+                if (p.res_rows) {
+                    const uint32_t ro = r < rows ? (uint32_t)(r * 8) : OOB;
+                    rs[t] = __builtin_bit_cast(float2v, __builtin_amdgcn_raw_buffer_load_b64(rr, ro, 0, 0));
+                }
             }
         }
     }
@@ -1183,6 +1212,7 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
                                           EPI == EPI_SILU || EPI == EPI_RESID_LN)),
                   "K groups: LDS-staged epilogues only");
     __shared__ __attribute__((aligned(1024))) uint8_t smem_all[KG * NS * C::STAGE];
+    prefetch_gemm_args(p);
 
     const int tid = threadIdx.x & 255, lane = tid & 63;
     const int wid_all = wave_id_uniform();
