@@ -1256,15 +1256,23 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
     // statistics, ahead of the DMAs) and wait in registers for the epilogue
     constexpr int TAB = FOLD && KG == 1 ? C::BM * 8 : 0;
     constexpr bool whole = 4 * 32 * WTM * (32 * WTN + 4) * 4 + TAB <= KG * NS * C::STAGE;
+    // Two K groups on a wave tile of two 32-row blocks share the end of the
+    // tile: group g sums and runs the epilogue of row block g (the other
+    // group's partial of it comes through LDS), so both groups' waves work in
+    // the reduction and the epilogue instead of group 0's alone.
+    constexpr bool KHALF = KG == 2 && WTM == 2 && !SPLIT && whole;
+    constexpr int ER = KHALF ? 32 : 32 * WTM;   // rows of this wave's epilogue
+    const int erow = wm * WTM * 32 + (KHALF ? kg * 32 : 0);   // its first row within the tile
+    const bool epi_wave = KHALF || kg == 0;
     constexpr bool RPRE = (EPI == EPI_RESID || EPI == EPI_RESID_LN) && whole;
-    ResidPre<RPRE ? 32 * WTM : 64, RPRE ? 8 * WTN : 1, EPI == EPI_RESID_LN && RPRE> rpre;
+    ResidPre<RPRE ? ER : 64, RPRE ? 8 * WTN : 1, EPI == EPI_RESID_LN && RPRE> rpre;
     if constexpr (RPRE) {
-        if (kg == 0) rpre.load(p, m0 + wm * WTM * 32, n0 + wn * WTN * 32, lane);
+        if (epi_wave) rpre.load(p, m0 + erow, n0 + wn * WTN * 32, lane);
     }
     // the epilogue's per-column (and conv-module per-channel) constants
     const bool fold = FOLD && p.fold_stats != nullptr;
     EpiCols<WTN> ecol;
-    if (kg == 0) ecol.load(p, n0 + wn * WTN * 32, lane, fold, EPI == EPI_RESID_LN);
+    if (epi_wave) ecol.load(p, n0 + wn * WTN * 32, lane, fold, EPI == EPI_RESID_LN);
     DwPre<EPI == EPI_GLU_DW ? C::BM : 64, 16 * TN> dwpre;
     if constexpr (EPI == EPI_GLU_DW) dwpre.load(p, m0, n0, tid);
 
@@ -1291,7 +1299,28 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
         mma32_slab<TM, TN, WT, WTM, WTN, WL == 1 || WL == 2>(smem + st * C::STAGE, acc, wm, wn, lane);
         st = st + 1 == NS ? 0 : st + 1;
     }
-    if constexpr (KG == 2) {
+    // KHALF: the row block this wave finishes (its own partial plus the other
+    // group's, the same two terms as group 0 + group 1: bit-identical)
+    float16v fin[1][WTN];
+    if constexpr (KHALF) {
+        constexpr int R = WTN * 16;
+        static_assert(8 * R * 64 * 4 <= KG * NS * C::STAGE, "partial tiles exceed LDS");
+        float* give = (float*)smem_all + wid_all * R * 64 + lane;                      // region (kg, wid)
+        const float* take = (const float*)smem_all + ((1 - kg) * 4 + wid) * R * 64 + lane;   // (1-kg, wid)
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < WTN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                give[(j * 16 + r) * 64] = kg ? acc[0][j][r] : acc[1][j][r];
+                fin[0][j][r] = kg ? acc[1][j][r] : acc[0][j][r];
+            }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < WTN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) fin[0][j][r] += take[(j * 16 + r) * 64];
+    } else if constexpr (KG == 2) {
         // lane-major [wave][register][lane] f32: conflict-free both ways
         constexpr int R = WTM * WTN * 16;
         static_assert(4 * R * 64 * 4 <= KG * NS * C::STAGE, "partial tile exceeds LDS");
@@ -1413,7 +1442,14 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
         // (the folded-LayerNorm row table sits above the staging area)
         static_assert(whole || (WTM % 2 == 0 && 4 * 16 * WTM * (32 * WTN + 4) * 4 + TAB <= KG * NS * C::STAGE),
                       "epilogue staging exceeds LDS ring");
-        if constexpr (whole) {
+        if constexpr (KHALF) {
+            // eight waves' 32-row staging tiles (the size of four 64-row ones)
+            __syncthreads();
+            float* wsm = (float*)smem_all + wid_all * 32 * (32 * WTN + 4);
+            epilogue32_lds<EPI, 1, WTN>(p, fin, wsm, m0 + erow, n0 + wn * WTN * 32, lane, ecol, fold, ftab, erow,
+                                        RPRE ? rpre.v : nullptr,
+                                        RPRE && EPI == EPI_RESID_LN && p.res_rows ? rpre.rs : nullptr);
+        } else if constexpr (whole) {
             __syncthreads();
             float* wsm = (float*)smem + wid * (32 * WTM) * ((EPI == EPI_GLU ? 16 * WTN : 32 * WTN) + 4);
             if (kg == 0)
