@@ -122,7 +122,8 @@ __global__ __launch_bounds__(64 * NQW * NG, 1) void relpos_attn_ks_kernel(AttnPa
     // the positional band, in the XCD's L2
     const int nq = (T + AQ - 1) / AQ;
     const int wid = xcd_tile(blockIdx.x, nq * a.B * a.H);
-    const int b = (wid / nq) % a.B, h = wid / (nq * a.B), i0 = (wid % nq) * AQ;
+    const int ib = udiv_small(wid, nq), h = udiv_small(ib, a.B);   // wid < 2^22 (checked at launch)
+    const int b = ib - h * a.B, i0 = (wid - ib * nq) * AQ;
     const int vl = a.valid ? a.valid[b] : T;
     const int i0w = i0 + 16 * wq;
     const int lg = lane >> 4, lc = lane & 15;   // lane group; lane in group = this lane's query
@@ -524,6 +525,7 @@ void launch_relpos_attention(Precision prec, const AttnParams& a, hipStream_t s)
         // fewer rounds by that measure (T' = 375 at batch 8: 384 -> 256).
         const int cus = device_cu_count();
         const int64_t nb64 = (int64_t)cdiv(a.T, 64) * a.H * a.B, nb96 = (int64_t)cdiv(a.T, 96) * a.H * a.B;
+        require(nb64 < ((int64_t)1 << 22), "attention(f16): more than 2^22 query blocks");
         const bool wide = 3 * ((nb96 + cus - 1) / cus) < 2 * ((nb64 + cus - 1) / cus);
         auto go = [&](auto DKc) {
             constexpr int D = decltype(DKc)::value;

@@ -1044,7 +1044,7 @@ struct DwPre {
         rt = make_int2(0, 0);
         const int m = m0 + tid;
         if (tid < BM && m >= 0 && m < p.M) {
-            const int b = m / p.T, t = m - b * p.T;
+            const int b = udiv_small(m, p.T), t = m - b * p.T;   // M < 2^22 (checked at launch)
             rt = make_int2(t, !p.valid || t < p.valid[b]);
         }
         const int c = min(n0 / 2 + 2 * (tid % CP), p.N / 2 - 2);
@@ -2250,6 +2250,7 @@ void launch_gemm(Precision prec, int wtype, int epi, const GemmParams& p, hipStr
         require(gemm_glu_dw_supported(prec, wtype, p.N, p.K) && p.ldy % 8 == 0,
                 "gemm: fused conv-module epilogue needs the f16 path, N % 64 == 0, K % 64 == 0, ldy % 8 == 0");
         require(p.dw_w && p.dw_scale && p.dw_shift && p.T >= 1, "gemm: fused conv-module epilogue parameters");
+        require(p.M < (1 << 22), "gemm: fused conv-module epilogue: fewer than 2^22 rows");
     }
     // the LDS-DMA kernel (f16 activations, K % 64 == 0) carries the LayerNorm folding
     const bool dma_ok = prec == PREC_F16 && p.K % 64 == 0 && p.ldy % 8 == 0 &&
