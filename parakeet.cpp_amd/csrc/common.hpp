@@ -129,6 +129,12 @@ __device__ __forceinline__ int udiv_small(int x, int d) {
     return q;
 }
 
+// MFMA row m of a 32-row tile <-> output column.  The 32x32 accumulator gives
+// lane half q the rows 8 g + 4 q + e (register 4 g + e, e < 4); feeding row m
+// from column 16 q + 4 g + e leaves column 16 q + r in register r, so each
+// lane holds 16 consecutive columns.
+__device__ __forceinline__ int tail_col(int m) { return 16 * ((m >> 2) & 1) + 4 * (m >> 3) + (m & 3); }
+
 // Raw buffer resources: loads at offsets at or past num_records return zero,
 // so an offset pushed to OOB (or a negative one, read as unsigned) is a
 // zero fill with no branch.

@@ -1495,6 +1495,12 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
 // the double-buffered fragments.  The lane's K order (k = 32q + 8s + e for lane
 // half q and substep s) is the LDS-B kernel's: each lane's weight bytes of a
 // slab are one contiguous 32-byte run of one q8_0 block.
+//
+// The weights are the MFMA's A operand and the activations its B operand, with
+// A row rho of block j fed from weight column 32 j + tail_col(rho): lane l then
+// ends with row 32 i + l % 32 of the tile at the 16 consecutive columns
+// 32 j + 16 (l / 32) + r in register r, and the epilogue stores 16-byte pieces
+// straight from registers (no LDS staging, one {mean, rstd} per row and lane).
 // ===========================================================================
 
 // One wave's raw weight registers for one 64-deep slab: WTN blocks of 32
@@ -1574,6 +1580,68 @@ template <int WTN> struct BRaw<GT_F16, WTN> {
 template <int WT, int WTN>
 constexpr int rb_b_ops() { return WT == GT_F16 ? 4 * WTN : 3 * WTN; }
 
+// Register-B epilogue: lane l holds row 32 i + l % 32 of the tile at columns
+// nw + 32 j + 16 (l / 32) + r in acc[i][j][r].  y = alpha (acc + bias), with a
+// folded LayerNorm alpha (rstd (acc - mean c1) + bias) as two FMAs
+// (a = alpha rstd, nb = -a mean per row; c1 and alpha * bias per column from
+// ctab), SiLU for EPI_SILU (alpha 1); f16 (or f32) pieces of 16 bytes by raw
+// buffer stores, rows past M and columns past N out of range (N % 16 == 0).
+template <int EPI, int WTM, int WTN>
+__device__ __forceinline__ void epilogue_rb(const GemmParams& p, const float16v (&acc)[WTM][WTN], const float* ctab,
+                                            int m0, int nw, int lane, float alpha, bool fold, const float2v* ftab) {
+    constexpr int WC = 32 * WTN, ESZ = EPI == EPI_STORE_F32 ? 4 : 2;
+    const int r32 = lane & 31, h = lane >> 5;
+    const int rows = p.M - m0;   // >= 1
+    const __amdgpu_buffer_rsrc_t ry =
+        make_rsrc((const uint8_t*)p.Y + (int64_t)m0 * p.ldy * ESZ, ((int64_t)(rows - 1) * p.ldy + p.N) * ESZ);
+    float4v cb[WTN][4], cc[WTN][4];
+#pragma unroll
+    for (int j = 0; j < WTN; ++j)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            cb[j][t] = *(const float4v*)(ctab + 32 * j + 16 * h + 4 * t);
+            cc[j][t] = fold ? *(const float4v*)(ctab + WC + 32 * j + 16 * h + 4 * t) : (float4v){0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+    for (int i = 0; i < WTM; ++i) {
+        const int row = 32 * i + r32;
+        float a = alpha, nb = 0.f;
+        if (fold) {
+            const float2v st = ftab[row];
+            a = alpha * st.y;
+            nb = -a * st.x;
+        }
+#pragma unroll
+        for (int j = 0; j < WTN; ++j) {
+            const int n = nw + 32 * j + 16 * h;
+            const uint32_t off = row < rows && n < p.N ? (uint32_t)((row * p.ldy + n) * ESZ) : OOB;
+            float y[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float b = fold ? __builtin_fmaf(nb, cc[j][r >> 2][r & 3], cb[j][r >> 2][r & 3]) : cb[j][r >> 2][r & 3];
+                float v = __builtin_fmaf(a, acc[i][j][r], b);
+                if constexpr (EPI == EPI_SILU) v = silu_dev(v);
+                y[r] = v;
+            }
+            if constexpr (EPI == EPI_STORE_F32) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const float4v v4 = {y[4 * t], y[4 * t + 1], y[4 * t + 2], y[4 * t + 3]};
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(int4v, v4), ry, off + 16 * t, 0, 0);
+                }
+            } else {
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    half8v hv;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) hv[e] = (f16)y[8 * t + e];
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(int4v, hv), ry, off + 16 * t, 0, 0);
+                }
+            }
+        }
+    }
+}
+
 template <int WTM, int WTN, int WT, int EPI, int NS, bool FO = false>
 struct RbCfg {
     static constexpr int BM = 32 * WTM, BN = 128 * WTN;
@@ -1586,13 +1654,12 @@ struct RbCfg {
     static constexpr bool FOLD = FO && (EPI == EPI_STORE || EPI == EPI_SILU);
     static constexpr int FOLD_BYTES = FOLD ? BM * 32 * 8 : 0; // {mean, M2} of up to 32 groups per row
     static constexpr int MAIN = NS * A_STAGE + FOLD_BYTES;
-    static constexpr int STG_WHOLE = 4 * 32 * WTM * (32 * WTN + 4) * 4;
-    static constexpr bool WHOLE = STG_WHOLE + BM * 8 <= 160 * 1024 - 1024;
-    static constexpr int STG = WHOLE ? STG_WHOLE : STG_WHOLE / 2;
-    static constexpr int LDS = (MAIN > STG ? MAIN : STG) + BM * 8;
+    static constexpr int CTAB = 4 * 2 * 32 * WTN * 4;         // epilogue column constants (in the ring)
+    static constexpr int LDS = MAIN + BM * 8;
     static_assert(A_STAGE % 4096 == 0, "A slab splits into 1 KB DMAs per wave");
+    static_assert(CTAB <= NS * A_STAGE, "column constants fit the ring");
     static_assert(LDS <= 160 * 1024, "LDS budget");
-    static_assert(WHOLE || WTM % 2 == 0, "row-half staging needs an even WTM");
+    static_assert(WTN % 2 == 0, "whole 64-column groups per wave");
 };
 
 template <int WTM, int WTN, int WT, int EPI, int NS, bool FO = false>
@@ -1628,8 +1695,16 @@ __global__ __launch_bounds__(256, 1) void gemm_rb_kernel(GemmParams p) {
             lds_dma16(rf, fl + c0 * 16, off, 0);
         }
     }
-    EpiCols<WTN> ecol;
-    ecol.load(p, nw, lane, fold, false);
+    // the epilogue's column constants: {alpha * bias} and the fold's c1 of
+    // column nw + lane + 64 t (written to LDS after the main loop)
+    const float alpha = EPI == EPI_SILU ? 1.f : p.alpha;
+    float colb[WTN / 2], colc[WTN / 2];
+#pragma unroll
+    for (int t = 0; t < WTN / 2; ++t) {
+        const int n = nw + lane + 64 * t;
+        colb[t] = n < p.N && p.bias ? alpha * p.bias[n] : 0.f;
+        colc[t] = fold && n < p.N ? p.fold_c1[n] : 0.f;
+    }
 
     // A: 64-column slabs of rows m0.., swizzled 16-byte chunks (as DmaSrc)
     const __amdgpu_buffer_rsrc_t ra =
@@ -1654,7 +1729,7 @@ __global__ __launch_bounds__(256, 1) void gemm_rb_kernel(GemmParams p) {
         rs = make_rsrc(p.Ws, ((int64_t)(nk - 1) * L + p.N) * SB);
 #pragma unroll
         for (int j = 0; j < WTN; ++j) {
-            const int n = nw + 32 * j + r32;
+            const int n = nw + 32 * j + tail_col(r32);
             vq[j] = n < p.N ? (uint32_t)(n * WB + (WT == GT_Q8_0 ? 32 * q : 0)) : OOB;
             vs[j] = n < p.N ? (uint32_t)(n * SB + (WT == GT_Q8_0 ? 2 * q : 8 * q)) : OOB;
         }
@@ -1662,7 +1737,7 @@ __global__ __launch_bounds__(256, 1) void gemm_rb_kernel(GemmParams p) {
         rq = make_rsrc(p.Wq, (int64_t)p.N * p.K * 2);
 #pragma unroll
         for (int j = 0; j < WTN; ++j) {
-            const int n = nw + 32 * j + r32;
+            const int n = nw + 32 * j + tail_col(r32);
             vq[j] = n < p.N ? (uint32_t)(((int64_t)n * p.K + 32 * q) * 2) : OOB;
             vs[j] = 0;
         }
@@ -1736,7 +1811,7 @@ __global__ __launch_bounds__(256, 1) void gemm_rb_kernel(GemmParams p) {
                 for (int i = 0; i < WTM; ++i)
 #pragma unroll
                     for (int j = 0; j < WTN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[cu][s][i], bf[cu][j][s], acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[cu][j][s], af[cu][s][i], acc[i][j], 0, 0, 0);
 #pragma unroll
             for (int g = 0; g < 4 * WTM * WTN; ++g) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
@@ -1761,23 +1836,17 @@ __global__ __launch_bounds__(256, 1) void gemm_rb_kernel(GemmParams p) {
         fst.finish(p, ftab, tid);
         __syncthreads();
     }
-    if constexpr (C::WHOLE) {
-        float* wsm = (float*)smem + wid * (32 * WTM) * (32 * WTN + 4);
-        epilogue32_lds<EPI, WTM, WTN>(p, acc, wsm, m0, nw, lane, ecol, fold, ftab, 0);
-    } else {
-        constexpr int TH = WTM / 2;
-        float* wsm = (float*)smem + wid * (32 * TH) * (32 * WTN + 4);
+    // this wave's column constants (the ring is free): written and read by
+    // the wave alone
+    float* ctab = (float*)smem + wid * 2 * 32 * WTN;
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-            float16v part[TH][WTN];
-#pragma unroll
-            for (int i = 0; i < TH; ++i)
-#pragma unroll
-                for (int j = 0; j < WTN; ++j) part[i][j] = acc[hh * TH + i][j];
-            if (hh) __syncthreads();
-            epilogue32_lds<EPI, TH, WTN>(p, part, wsm, m0 + hh * TH * 32, nw, lane, ecol, fold, ftab, hh * TH * 32);
-        }
+    for (int t = 0; t < WTN / 2; ++t) {
+        ctab[lane + 64 * t] = colb[t];
+        ctab[32 * WTN + lane + 64 * t] = colc[t];
     }
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+    epilogue_rb<EPI, WTM, WTN>(p, acc, ctab, m0, nw, lane, alpha, fold, ftab);
 }
 
 // ===========================================================================
@@ -2100,6 +2169,9 @@ static void run_rb(const GemmParams& p, hipStream_t s) {
     typedef RbCfg<WTM, WTN, WT, EPI, NS> C;
     constexpr bool can_fold = EPI == EPI_STORE || EPI == EPI_SILU;
     require(p.K % (64 * C::U) == 0, "gemm: register-B kernel needs K % 256 == 0");
+    require(p.N % 16 == 0, "gemm: register-B kernel needs N % 16 == 0 (16-column stores)");
+    require((int64_t)p.M * p.ldy * (EPI == EPI_STORE_F32 ? 4 : 2) < ((int64_t)1 << 31),
+            "gemm: register-B kernel output must stay below 2 GB (32-bit store offsets)");
     if (p.fold_stats) require(p.fold_groups <= 32, "gemm: register-B kernel folds at most 32 statistics groups");
     const int tiles = cdiv(p.M, C::BM) * cdiv(p.N, C::BN);
     GemmParams q = p;
@@ -2196,7 +2268,8 @@ static bool dma_kg2(int epi, const GemmParams& p, hipStream_t s) {
 // 8 x 30 s: 14.44 against 13.82 ms per forward with the register-B kernel).
 template <int WT>
 static bool dma_rb(int epi, const GemmParams& p, hipStream_t s) {
-    if (p.K % 256 != 0 || p.N < 2048 || (p.fold_stats && p.fold_groups > 32)) return false;
+    if (p.K % 256 != 0 || p.N < 2048 || p.N % 16 != 0 || (p.fold_stats && p.fold_groups > 32)) return false;
+    if ((int64_t)p.M * p.ldy * (epi == EPI_STORE_F32 ? 4 : 2) >= ((int64_t)1 << 31)) return false;
     if (epi != EPI_STORE && epi != EPI_SILU && epi != EPI_STORE_F32) return false;
     const int64_t tiles = (int64_t)cdiv(p.M, 128) * cdiv(p.N, 256), cus = device_cu_count();
     if (!((tiles <= cus && tiles * 10 >= cus * 7) || tiles >= 4 * cus)) return false;

@@ -66,12 +66,6 @@ struct SubTailParams {
     int B, T2, T3;
 };
 
-// MFMA row m of a 32-row tile <-> map column.  The 32x32 accumulator gives
-// lane half q the rows 8 g + 4 q + e (register 4 g + e, e < 4); feeding row m
-// from column 16 q + 4 g + e leaves column 16 q + r in register r, so each
-// lane holds 16 consecutive columns of its channel.
-__device__ __forceinline__ int tail_col(int m) { return 16 * ((m >> 2) & 1) + 4 * (m >> 3) + (m & 3); }
-
 // ReLU and a wave-uniform row mask in one v_med3_f32: median(x, 0, +inf) is
 // max(x, 0), median(x, 0, 0) is 0 (fmaxf costs two v_max_f32, the mask a
 // v_cndmask more).
@@ -296,7 +290,7 @@ __global__ __launch_bounds__(TAIL_THREADS, 1) void sub_tail_kernel(SubTailParams
 // while the current one computes.
 // ---------------------------------------------------------------------------
 namespace {
-constexpr int S1_F = 128, S1_F1 = 64, S1_F2 = 32;
+constexpr int S1_F = 128, S1_F2 = 32;   // mel bins, conv.2 map columns
 constexpr int S1_THREADS = 512;
 }  // namespace
 

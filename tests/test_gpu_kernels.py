@@ -96,11 +96,13 @@ def test_rel_pos_encoding(gpu, stream, T, D):
 
 @pytest.mark.parametrize("gtype", [pm.GGML_F16, pm.GGML_Q8_0, pm.GGML_Q4_K])
 @pytest.mark.parametrize("M,N,K", [(1000, 3072, 512), (2000, 4096, 256), (333, 2048, 1024), (129, 320, 1280),
-                                   (2000, 1024, 4096), (700, 1000, 2048), (2000, 3072, 1024), (1900, 2880, 512)])
+                                   (2000, 1024, 4096), (700, 1000, 2048), (2000, 3072, 1024), (1900, 2880, 512),
+                                   (2000, 2832, 256)])
 def test_linear_tile_shapes(gpu, stream, gtype, M, N, K):
     """f16 path at shapes that select each MFMA tile (64x64, 128x64, 128x128,
-    and 128x64 with two K groups for long K) and leave partial tiles on both
-    edges."""
+    and 128x64 with two K groups for long K; the register-B 128x256 tiles) and
+    leave partial tiles on both edges (N = 2832: the last 256-column tile holds
+    16 columns, one lane half's store group of one wave)."""
     rng = _rng(M * 7 + N + K)
     raw, wf = _weights(gtype, N, K, rng)
     x = rng.normal(0, 1, (M, K)).astype(np.float32)
