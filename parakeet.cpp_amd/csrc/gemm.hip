@@ -879,81 +879,16 @@ struct ResidPre {
     }
 };
 
-// fold: ftab (LDS) holds {mean, rstd} of the workgroup tile's rows for a
-// folded LayerNorm, indexed from the tile's first row; trow0 is this wave's
-// first row within the tile.  (ftab is always a valid LDS address, so that its
-// loads stay LDS loads.)
-// xpre: the wave tile's residual values from ResidPre (RESID / RESID_LN), or null;
-// xrs: with xpre, the rows' {mean, rstd} for a LayerNorm applied to the residual.
-template <int EPI, int TM, int TN>
-__device__ __forceinline__ void epilogue32_lds(const GemmParams& p, float16v (&acc)[TM][TN], float* wsm,
-                                               int mw, int nw, int lane, const EpiCols<TN>& ec,
-                                               bool fold = false, const float2v* ftab = nullptr, int trow0 = 0,
-                                               const float4v* xpre = nullptr, const float2v* xrs = nullptr) {
-    constexpr int WR = 32 * TM;
-    constexpr int WC = EPI == EPI_GLU ? 16 * TN : 32 * TN;   // output columns of this wave
+// Step 2 of the LDS-staged epilogues: the wave's WR x WC output tile, staged
+// as f32 rows of WC + 4 floats at wsm (rows from mw, columns from nw; GLU
+// output columns from nw / 2), leaves by coalesced 16-byte stores, the
+// residual updates reading the residual stream at the same granularity
+// (xpre: those values from ResidPre, or null; xrs: with xpre, the rows'
+// {mean, rstd} for a LayerNorm applied to the residual).
+template <int EPI, int WR, int WC, int NJ>
+__device__ __forceinline__ void epilogue_lds_out(const GemmParams& p, const float* wsm, int mw, int nw, int lane,
+                                                 const EpiCols<NJ>& ec, const float4v* xpre, const float2v* xrs) {
     constexpr int LDW = WC + 4;
-    const int lr = 4 * (lane >> 5), lc = lane & 31;
-    // 1) elementwise math in registers, staged as f32
-    if constexpr (EPI == EPI_GLU) {
-        static_assert(TN % 2 == 0, "GLU needs an even number of 32-column blocks");
-#pragma unroll
-        for (int i = 0; i < TM; ++i) {
-            float2v st[16];   // folded LayerNorm {mean, rstd} of this lane's 16 rows
-            if (fold) {
-#pragma unroll
-                for (int r = 0; r < 16; ++r) st[r] = ftab[trow0 + 32 * i + 8 * (r >> 2) + lr + (r & 3)];
-            }
-#pragma unroll
-            for (int jj = 0; jj < TN / 2; ++jj) {
-                const float ba = ec.b[2 * jj], bg = ec.b[2 * jj + 1];
-                const float ca = ec.c1[2 * jj], cg = ec.c1[2 * jj + 1];
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int rr = 32 * i + 8 * (r >> 2) + lr + (r & 3);
-                    const int m = mw + rr;
-                    float xa = acc[i][2 * jj][r], xg = acc[i][2 * jj + 1][r];
-                    if (fold) {
-                        xa = st[r].y * (xa - st[r].x * ca);
-                        xg = st[r].y * (xg - st[r].x * cg);
-                    }
-                    float o = (xa + ba) * sigmoid_dev(xg + bg);
-                    if (p.valid && m < p.M) {
-                        const int b = m / p.T, t = m - b * p.T;
-                        if (t >= p.valid[b]) o = 0.f;
-                    }
-                    wsm[rr * LDW + 32 * jj + lc] = o;
-                }
-            }
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < TM; ++i) {
-            float2v st[16];   // folded LayerNorm {mean, rstd} of this lane's 16 rows
-            if (fold) {
-#pragma unroll
-                for (int r = 0; r < 16; ++r) st[r] = ftab[trow0 + 32 * i + 8 * (r >> 2) + lr + (r & 3)];
-            }
-#pragma unroll
-            for (int j = 0; j < TN; ++j) {
-                const float bb = ec.b[j], c1 = ec.c1[j];
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int rr = 32 * i + 8 * (r >> 2) + lr + (r & 3);
-                    float v = acc[i][j][r];
-                    if (fold) v = st[r].y * (v - st[r].x * c1);
-                    v += bb;
-                    if constexpr (EPI == EPI_SILU) v = silu_dev(v);
-                    else if constexpr (EPI == EPI_RELU) v = v > 0.f ? v : 0.f;
-                    else v = v * p.alpha;    // STORE, STORE_F32, RESID
-                    wsm[rr * LDW + 32 * j + lc] = v;
-                }
-            }
-        }
-    }
-    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's LDS writes are done
-    __builtin_amdgcn_wave_barrier();
-    // 2) coalesced copy-out
     const int ncol = EPI == EPI_GLU ? p.N / 2 : p.N;
     const int n0 = EPI == EPI_GLU ? nw / 2 : nw;
     if constexpr (EPI == EPI_RESID_LN) {
@@ -1030,6 +965,83 @@ __device__ __forceinline__ void epilogue32_lds(const GemmParams& p, float16v (&a
             }
         }
     }
+}
+
+// fold: ftab (LDS) holds {mean, rstd} of the workgroup tile's rows for a
+// folded LayerNorm, indexed from the tile's first row; trow0 is this wave's
+// first row within the tile.  (ftab is always a valid LDS address, so that its
+// loads stay LDS loads.)
+// xpre: the wave tile's residual values from ResidPre (RESID / RESID_LN), or null;
+// xrs: with xpre, the rows' {mean, rstd} for a LayerNorm applied to the residual.
+template <int EPI, int TM, int TN>
+__device__ __forceinline__ void epilogue32_lds(const GemmParams& p, float16v (&acc)[TM][TN], float* wsm,
+                                               int mw, int nw, int lane, const EpiCols<TN>& ec,
+                                               bool fold = false, const float2v* ftab = nullptr, int trow0 = 0,
+                                               const float4v* xpre = nullptr, const float2v* xrs = nullptr) {
+    constexpr int WR = 32 * TM;
+    constexpr int WC = EPI == EPI_GLU ? 16 * TN : 32 * TN;   // output columns of this wave
+    constexpr int LDW = WC + 4;
+    const int lr = 4 * (lane >> 5), lc = lane & 31;
+    // 1) elementwise math in registers, staged as f32
+    if constexpr (EPI == EPI_GLU) {
+        static_assert(TN % 2 == 0, "GLU needs an even number of 32-column blocks");
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            float2v st[16];   // folded LayerNorm {mean, rstd} of this lane's 16 rows
+            if (fold) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) st[r] = ftab[trow0 + 32 * i + 8 * (r >> 2) + lr + (r & 3)];
+            }
+#pragma unroll
+            for (int jj = 0; jj < TN / 2; ++jj) {
+                const float ba = ec.b[2 * jj], bg = ec.b[2 * jj + 1];
+                const float ca = ec.c1[2 * jj], cg = ec.c1[2 * jj + 1];
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int rr = 32 * i + 8 * (r >> 2) + lr + (r & 3);
+                    const int m = mw + rr;
+                    float xa = acc[i][2 * jj][r], xg = acc[i][2 * jj + 1][r];
+                    if (fold) {
+                        xa = st[r].y * (xa - st[r].x * ca);
+                        xg = st[r].y * (xg - st[r].x * cg);
+                    }
+                    float o = (xa + ba) * sigmoid_dev(xg + bg);
+                    if (p.valid && m < p.M) {
+                        const int b = m / p.T, t = m - b * p.T;
+                        if (t >= p.valid[b]) o = 0.f;
+                    }
+                    wsm[rr * LDW + 32 * jj + lc] = o;
+                }
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            float2v st[16];   // folded LayerNorm {mean, rstd} of this lane's 16 rows
+            if (fold) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) st[r] = ftab[trow0 + 32 * i + 8 * (r >> 2) + lr + (r & 3)];
+            }
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const float bb = ec.b[j], c1 = ec.c1[j];
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int rr = 32 * i + 8 * (r >> 2) + lr + (r & 3);
+                    float v = acc[i][j][r];
+                    if (fold) v = st[r].y * (v - st[r].x * c1);
+                    v += bb;
+                    if constexpr (EPI == EPI_SILU) v = silu_dev(v);
+                    else if constexpr (EPI == EPI_RELU) v = v > 0.f ? v : 0.f;
+                    else v = v * p.alpha;    // STORE, STORE_F32, RESID
+                    wsm[rr * LDW + 32 * j + lc] = v;
+                }
+            }
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's LDS writes are done
+    __builtin_amdgcn_wave_barrier();
+    epilogue_lds_out<EPI, WR, WC, TN>(p, wsm, mw, nw, lane, ec, xpre, xrs);
 }
 
 // Constants of the fused conv-module epilogue, loaded before the main loop:
@@ -1642,41 +1654,88 @@ __device__ __forceinline__ void epilogue_rb(const GemmParams& p, const float16v 
     }
 }
 
-template <int WTM, int WTN, int WT, int EPI, int NS, bool FO = false>
+// Register-B epilogue of the residual products (two K groups, each wave
+// finishing one 32-row block): lane l holds row mb + l % 32 at columns
+// nw + 32 j + 16 (l / 32) + r in acc[j][r].  alpha (acc + bias) is staged in
+// LDS (wsm: 32 rows of 32 WTN + 4 floats, four 16-byte writes per lane and
+// block) and leaves through the coalesced residual copy-out (epilogue_lds_out:
+// x += (.), and for RESID_LN x * gamma and the 32-column group statistics),
+// whose full-line stores and residual loads take a quarter of the requests of
+// 16-byte pieces on 32 rows.  ctab: the wave's 32 WTN columns of alpha * bias.
+template <int EPI, int WTN>
+__device__ __forceinline__ void epilogue_rb_resid(const GemmParams& p, const float16v (&acc)[WTN], const float* ctab,
+                                                  float* wsm, int mb, int nw, int lane, float alpha,
+                                                  const EpiCols<WTN>& ec, const float4v* xpre, const float2v* xrs) {
+    constexpr int WC = 32 * WTN, LDW = WC + 4;
+    const int r32 = lane & 31, h = lane >> 5;
+#pragma unroll
+    for (int j = 0; j < WTN; ++j) {
+        const int c = 32 * j + 16 * h;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const float4v b4 = *(const float4v*)(ctab + c + 4 * t);
+            float4v v;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = __builtin_fmaf(alpha, acc[j][4 * t + e], b4[e]);
+            *(float4v*)(wsm + r32 * LDW + c + 4 * t) = v;
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's LDS writes are done
+    __builtin_amdgcn_wave_barrier();
+    epilogue_lds_out<EPI, 32, WC, WTN>(p, wsm, mb, nw, lane, ec, xpre, xrs);
+}
+
+// KG = 2: eight waves in two groups of four; group g streams K slabs
+// [g nk, (g+1) nk) through its own ring, and after the main loop group g sums
+// and finishes row block g of the 64-row tile (the other group's partial of
+// it comes through LDS): two waves per SIMD for grids of about one tile per
+// CU.  Used with the residual epilogues on 64 x 128 tiles.
+template <int WTM, int WTN, int WT, int EPI, int NS, bool FO = false, int KG = 1>
 struct RbCfg {
-    static constexpr int BM = 32 * WTM, BN = 128 * WTN;
+    static constexpr int BM = 32 * WTM, BN = 128 * WTN, WC = 32 * WTN;
     static constexpr int A_STAGE = BM * 128;                  // f16 [BM][64]
     static constexpr int NA = A_STAGE / 4096;                 // 1 KB A DMAs per wave per slab
     static constexpr int NB = rb_b_ops<WT, WTN>();
     static constexpr int PER_SLAB = NA + NB;
     static constexpr int NR = 4;                              // weight register sets (>= NS - 1 in flight)
     static constexpr int U = 4;                               // loop unroll: every ring index static
+    static constexpr bool RESID = EPI == EPI_RESID || EPI == EPI_RESID_LN;
     static constexpr bool FOLD = FO && (EPI == EPI_STORE || EPI == EPI_SILU);
+    static constexpr int NCA = RESID ? 1 : 2;                 // column constant arrays
+    static constexpr int RING = KG * NS * A_STAGE;
     static constexpr int FOLD_BYTES = FOLD ? BM * 32 * 8 : 0; // {mean, M2} of up to 32 groups per row
-    static constexpr int MAIN = NS * A_STAGE + FOLD_BYTES;
-    static constexpr int CTAB = 4 * 2 * 32 * WTN * 4;         // epilogue column constants (in the ring)
-    static constexpr int LDS = MAIN + BM * 8;
+    static constexpr int XCH = KG == 2 ? 8 * 16 * WTN * 64 * 4 : 0;   // K-group exchange
+    static constexpr int CTAB = 4 * KG * NCA * WC * 4;        // epilogue column constants
+    static constexpr int STG = RESID ? 8 * 32 * (WC + 4) * 4 : 0;   // residual staging
+    static constexpr int AFTER = XCH + CTAB + STG;            // the post-loop regions, from offset 0
+    static constexpr int BODY = (RING > AFTER ? RING : AFTER) + FOLD_BYTES;
+    static constexpr int LDS = BODY + BM * 8;
     static_assert(A_STAGE % 4096 == 0, "A slab splits into 1 KB DMAs per wave");
-    static_assert(CTAB <= NS * A_STAGE, "column constants fit the ring");
+    static_assert(!FOLD || AFTER <= RING, "the fold statistics sit past the ring");
     static_assert(LDS <= 160 * 1024, "LDS budget");
-    static_assert(WTN % 2 == 0, "whole 64-column groups per wave");
+    static_assert(KG == 1 || KG == 2, "K groups");
+    static_assert(!RESID || (KG == 2 && WTM == 2), "residual epilogues: two K groups, one row block per group");
+    static_assert(RESID || KG == 1, "store / SiLU epilogues: one K group");
+    static_assert(!FOLD || KG == 1, "folded LayerNorm: one K group");
 };
 
-template <int WTM, int WTN, int WT, int EPI, int NS, bool FO = false>
-__global__ __launch_bounds__(256, 1) void gemm_rb_kernel(GemmParams p) {
-    typedef RbCfg<WTM, WTN, WT, EPI, NS, FO> C;
+template <int WTM, int WTN, int WT, int EPI, int NS, bool FO = false, int KG = 1>
+__global__ __launch_bounds__(256 * KG, 1) void gemm_rb_kernel(GemmParams p) {
+    typedef RbCfg<WTM, WTN, WT, EPI, NS, FO, KG> C;
     static_assert(NS >= 3 && NS <= 5, "ring depth");
-    static_assert(EPI == EPI_STORE || EPI == EPI_STORE_F32 || EPI == EPI_SILU,
-                  "register-B kernel: store / SiLU epilogues (the wide products it runs)");
-    constexpr int BM = C::BM, NR = C::NR;
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[C::LDS];
+    static_assert(EPI == EPI_STORE || EPI == EPI_STORE_F32 || EPI == EPI_SILU || C::RESID,
+                  "register-B kernel: store / SiLU / residual epilogues");
+    constexpr int BM = C::BM, NR = C::NR, WC = C::WC;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem_all[C::LDS];
 
-    const int tid = threadIdx.x, lane = tid & 63, wid = wave_id_uniform();
+    const int tid = threadIdx.x, lane = tid & 63, wid_all = wave_id_uniform();
+    const int kg = wid_all >> 2, wid = wid_all & 3;
     const int q = lane >> 5, r32 = lane & 31;
+    uint8_t* smem = smem_all + kg * NS * C::A_STAGE;   // this group's ring
     int bm, bn;
     xcd_tile_2d(blockIdx.x, cdiv_dev(p.M, BM), cdiv_dev(p.N, C::BN), p.xcd_gm, bm, bn);
-    const int m0 = bm * BM, n0 = bn * C::BN, nw = n0 + wid * 32 * WTN;
-    const int nk = p.K / 64;
+    const int m0 = bm * BM, n0 = bn * C::BN, nw = n0 + wid * WC;
+    const int nkt = p.K / 64, nk = nkt / KG, kb = kg * nk;   // slabs: all, this group's, its first
 
     // folded LayerNorm (FO: p.fold_stats is set) statistics of the tile's rows:
     // DMA into LDS first (the oldest vector-memory operations, complete by the
@@ -1687,7 +1746,7 @@ __global__ __launch_bounds__(256, 1) void gemm_rb_kernel(GemmParams p) {
         const __amdgpu_buffer_rsrc_t rf =
             make_rsrc((const float2v*)p.fold_stats + (int64_t)m0 * p.fold_groups,
                       ((int64_t)(p.M - m0) * p.fold_groups) * 8);
-        uint8_t* fl = smem + NS * C::A_STAGE;
+        uint8_t* fl = smem_all + C::BODY - C::FOLD_BYTES;
         for (int c0 = wid * 64; c0 < total; c0 += 256) {
             const int ch = c0 + lane, r = ch >> lc;
             const uint32_t off = ch < total ? (uint32_t)(min(r, p.M - 1 - m0) << (lc + 4)) + ((ch & ((1 << lc) - 1)) << 4)
@@ -1695,15 +1754,28 @@ __global__ __launch_bounds__(256, 1) void gemm_rb_kernel(GemmParams p) {
             lds_dma16(rf, fl + c0 * 16, off, 0);
         }
     }
-    // the epilogue's column constants: {alpha * bias} and the fold's c1 of
-    // column nw + lane + 64 t (written to LDS after the main loop)
+    // the epilogue's column constants of column nw + lane + 64 t (written to
+    // LDS after the main loop): alpha * bias, then the fold's c1 (store / SiLU)
     const float alpha = EPI == EPI_SILU ? 1.f : p.alpha;
-    float colb[WTN / 2], colc[WTN / 2];
+    constexpr int CPL = (WC + 63) / 64;
+    float colv[C::NCA][CPL];
 #pragma unroll
-    for (int t = 0; t < WTN / 2; ++t) {
-        const int n = nw + lane + 64 * t;
-        colb[t] = n < p.N && p.bias ? alpha * p.bias[n] : 0.f;
-        colc[t] = fold && n < p.N ? p.fold_c1[n] : 0.f;
+    for (int t = 0; t < CPL; ++t) {
+        const int c = lane + 64 * t, n = nw + c;
+        const bool ok = c < WC && n < p.N;
+        colv[0][t] = ok && p.bias ? p.bias[n] : 0.f;   // times alpha when written to LDS
+        if constexpr (C::NCA == 2) colv[1][t] = fold && ok ? p.fold_c1[n] : 0.f;
+    }
+    // residual epilogues: the wave's 32-row block of the residual stream (row
+    // block kg of the tile) in the copy-out's layout, its rows' statistics
+    // and the copy-out's columns of gamma, res_g, res_b, in registers before
+    // the main loop
+    constexpr bool RS = EPI == EPI_RESID_LN;
+    ResidPre<C::RESID ? 32 : 64, C::RESID ? 8 * WTN : 1, RS> rpre;
+    EpiCols<WTN> ecol;
+    if constexpr (C::RESID) {
+        rpre.load(p, m0 + 32 * kg, nw, lane);
+        ecol.load(p, nw, lane, false, RS);
     }
 
     // A: 64-column slabs of rows m0.., swizzled 16-byte chunks (as DmaSrc)
@@ -1725,8 +1797,8 @@ __global__ __launch_bounds__(256, 1) void gemm_rb_kernel(GemmParams p) {
         constexpr int WB = WT == GT_Q8_0 ? 64 : 32, SB = WT == GT_Q8_0 ? 4 : 16;
         // a view into a larger weight keeps the allocation's slab stride L: its
         // last byte is in slab nk-1, row N-1
-        rq = make_rsrc(p.Wq, ((int64_t)(nk - 1) * L + p.N) * WB);
-        rs = make_rsrc(p.Ws, ((int64_t)(nk - 1) * L + p.N) * SB);
+        rq = make_rsrc(p.Wq, ((int64_t)(nkt - 1) * L + p.N) * WB);
+        rs = make_rsrc(p.Ws, ((int64_t)(nkt - 1) * L + p.N) * SB);
 #pragma unroll
         for (int j = 0; j < WTN; ++j) {
             const int n = nw + 32 * j + tail_col(r32);
@@ -1742,18 +1814,18 @@ __global__ __launch_bounds__(256, 1) void gemm_rb_kernel(GemmParams p) {
             vs[j] = 0;
         }
     }
-    // scalar offsets of slab k (out of range past the last slab)
+    // scalar offsets of the group's slab k (out of range past its last slab)
     auto soq = [&](int k) -> int {
         if (k >= nk) return (int)OOB;
-        return WT == GT_Q8_0 ? k * L * 64 : WT == GT_Q4_K ? k * L * 32 : k * 128;
+        return WT == GT_Q8_0 ? (kb + k) * L * 64 : WT == GT_Q4_K ? (kb + k) * L * 32 : (kb + k) * 128;
     };
     auto sos = [&](int k) -> int {
         if (k >= nk) return (int)OOB;
-        return WT == GT_Q8_0 ? k * L * 4 : WT == GT_Q4_K ? k * L * 16 : 0;
+        return WT == GT_Q8_0 ? (kb + k) * L * 4 : WT == GT_Q4_K ? (kb + k) * L * 16 : 0;
     };
     auto issue_a = [&](int k) {
         uint8_t* st = smem + (k % NS) * C::A_STAGE + wid * C::NA * 1024;
-        const int so = k < nk ? k * 128 : (int)OOB;
+        const int so = k < nk ? (kb + k) * 128 : (int)OOB;
 #pragma unroll
         for (int i = 0; i < C::NA; ++i) lds_dma16(ra, st + i * 1024, va[i], so);
     };
@@ -1824,29 +1896,50 @@ __global__ __launch_bounds__(256, 1) void gemm_rb_kernel(GemmParams p) {
     __syncthreads();
 
     // folded LayerNorm: {mean, rstd} of the tile's rows at the top of LDS
-    float2v* ftab = (float2v*)(smem + C::LDS) - BM;
+    float2v* ftab = (float2v*)(smem_all + C::LDS) - BM;
     if constexpr (fold) {
         FoldStats<BM> fst;
         const int lc = __builtin_ctz(p.fold_groups / 2), total = BM << lc;
 #pragma unroll
         for (int i = 0; i < FoldStats<BM>::MAXC; ++i) {
             const int ch = tid + 256 * i;
-            fst.c[i] = ch < total ? ((const float4v*)(smem + NS * C::A_STAGE))[ch] : (float4v){0.f, 0.f, 0.f, 0.f};
+            fst.c[i] = ch < total ? ((const float4v*)(smem_all + C::BODY - C::FOLD_BYTES))[ch] : (float4v){0.f, 0.f, 0.f, 0.f};
         }
         fst.finish(p, ftab, tid);
         __syncthreads();
     }
-    // this wave's column constants (the ring is free): written and read by
-    // the wave alone
-    float* ctab = (float*)smem + wid * 2 * 32 * WTN;
+    // two K groups: group g's partial of row block 1 - g goes to the other
+    // group, which adds it to its own (lane-major [wave][register][lane] f32)
+    float16v fin[WTN];
+    if constexpr (KG == 2) {
+        constexpr int R = 16 * WTN;
+        float* give = (float*)smem_all + wid_all * R * 64 + lane;
+        const float* take = (const float*)smem_all + ((1 - kg) * 4 + wid) * R * 64 + lane;
 #pragma unroll
-    for (int t = 0; t < WTN / 2; ++t) {
-        ctab[lane + 64 * t] = colb[t];
-        ctab[32 * WTN + lane + 64 * t] = colc[t];
+        for (int j = 0; j < WTN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) give[(j * 16 + r) * 64] = kg ? acc[0][j][r] : acc[1][j][r];
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < WTN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) fin[j][r] = (kg ? acc[1][j][r] : acc[0][j][r]) + take[(j * 16 + r) * 64];
     }
+    // this wave's column constants (the ring is free; past the exchange):
+    // written and read by the wave alone
+    float* ctab = (float*)(smem_all + C::XCH) + wid_all * C::NCA * WC;
+    float* wsm = (float*)(smem_all + C::XCH + C::CTAB) + wid_all * 32 * (WC + 4);
+#pragma unroll
+    for (int a = 0; a < C::NCA; ++a)
+#pragma unroll
+        for (int t = 0; t < CPL; ++t)
+            if (lane + 64 * t < WC) ctab[a * WC + lane + 64 * t] = a == 0 ? alpha * colv[a][t] : colv[a][t];
     __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0)
     __builtin_amdgcn_wave_barrier();
-    epilogue_rb<EPI, WTM, WTN>(p, acc, ctab, m0, nw, lane, alpha, fold, ftab);
+    if constexpr (C::RESID)
+        epilogue_rb_resid<EPI, WTN>(p, fin, ctab, wsm, m0 + 32 * kg, nw, lane, alpha, ecol, rpre.v,
+                                    RS && p.res_rows ? rpre.rs : nullptr);
+    else epilogue_rb<EPI, WTM, WTN>(p, acc, ctab, m0, nw, lane, alpha, fold, ftab);
 }
 
 // ===========================================================================
@@ -2164,20 +2257,21 @@ static void run_dma(const GemmParams& p, hipStream_t s) {
     }
 }
 
-template <int WTM, int WTN, int WT, int EPI, int NS>
+template <int WTM, int WTN, int WT, int EPI, int NS, int KG = 1>
 static void run_rb(const GemmParams& p, hipStream_t s) {
-    typedef RbCfg<WTM, WTN, WT, EPI, NS> C;
-    constexpr bool can_fold = EPI == EPI_STORE || EPI == EPI_SILU;
-    require(p.K % (64 * C::U) == 0, "gemm: register-B kernel needs K % 256 == 0");
+    typedef RbCfg<WTM, WTN, WT, EPI, NS, false, KG> C;
+    constexpr bool can_fold = (EPI == EPI_STORE || EPI == EPI_SILU) && KG == 1;
+    require(p.K % (64 * C::U * KG) == 0, "gemm: register-B kernel needs K % (256 x K groups) == 0");
+    if (EPI == EPI_RESID_LN) require(p.N % 32 == 0, "gemm: register-B residual + LayerNorm statistics needs N % 32 == 0");
     require(p.N % 16 == 0, "gemm: register-B kernel needs N % 16 == 0 (16-column stores)");
-    require((int64_t)p.M * p.ldy * (EPI == EPI_STORE_F32 ? 4 : 2) < ((int64_t)1 << 31),
+    require((int64_t)p.M * p.ldy * (EPI == EPI_STORE_F32 || C::RESID ? 4 : 2) < ((int64_t)1 << 31),
             "gemm: register-B kernel output must stay below 2 GB (32-bit store offsets)");
     if (p.fold_stats) require(p.fold_groups <= 32, "gemm: register-B kernel folds at most 32 statistics groups");
     const int tiles = cdiv(p.M, C::BM) * cdiv(p.N, C::BN);
     GemmParams q = p;
     q.xcd_gm = choose_xcd_gm(p, WT, C::BM, C::BN);
-    if (can_fold && p.fold_stats) launch((gemm_rb_kernel<WTM, WTN, WT, EPI, NS, can_fold>), dim3(tiles), dim3(256), 0, s, q);
-    else launch((gemm_rb_kernel<WTM, WTN, WT, EPI, NS, false>), dim3(tiles), dim3(256), 0, s, q);
+    if (can_fold && p.fold_stats) launch((gemm_rb_kernel<WTM, WTN, WT, EPI, NS, can_fold, KG>), dim3(tiles), dim3(256 * KG), 0, s, q);
+    else launch((gemm_rb_kernel<WTM, WTN, WT, EPI, NS, false, KG>), dim3(tiles), dim3(256 * KG), 0, s, q);
     PKX_LAUNCH_CHECK();
 }
 
@@ -2281,6 +2375,26 @@ static bool dma_rb(int epi, const GemmParams& p, hipStream_t s) {
     return true;
 }
 
+// Register-B kernel with two K groups (64 x 128 tiles, eight waves, two per
+// SIMD) for the quantised residual products whose grid of those tiles is about
+// one round of the chip: N = 1024 at M = 2000 (FFN linear2 at K = 4096,
+// attention output at K = 1024).  The LDS-B kernel's main loop there waits on
+// its LDS reads (both operands from LDS, no read-ahead): on MI355X at
+// M = 2000, N = 1024 (q8_0) 27.0 against 30.2 us at K = 4096 and 12.7 against
+// 13.3 us at K = 1024.  f16 weights (pointwise_conv2) stream twice the bytes
+// per slab from L2 and stay on the LDS-B kernel (16.4 against 13.6 us).
+template <int WT>
+static bool dma_rb_resid(int epi, const GemmParams& p, hipStream_t s) {
+    if (epi != EPI_RESID && epi != EPI_RESID_LN) return false;
+    if (p.K % 512 != 0 || p.N % 32 != 0 || p.ldy % 4 != 0) return false;
+    if ((int64_t)p.M * p.ldy * 4 >= ((int64_t)1 << 31)) return false;
+    const int64_t tiles = (int64_t)cdiv(p.M, 64) * cdiv(p.N, 128), cus = device_cu_count();
+    if (!((tiles <= cus && tiles * 10 >= cus * 7) || tiles >= 4 * cus)) return false;
+    if (epi == EPI_RESID) run_rb<2, 1, WT, EPI_RESID, 4, 2>(p, s);
+    else run_rb<2, 1, WT, EPI_RESID_LN, 4, 2>(p, s);
+    return true;
+}
+
 template <int TM, int TN, int WT>
 static void f32_epi(int epi, const GemmParams& p, hipStream_t s) { PKX_EPI_SWITCH(run_f32, TM, TN, WT) }
 // tiles narrower than 64 columns per wave pair: every epilogue but GLU (which
@@ -2362,6 +2476,8 @@ void launch_gemm(Precision prec, int wtype, int epi, const GemmParams& p, hipStr
         const bool glu = epi == EPI_GLU || epi == EPI_GLU_DW;
         if (wtype == GT_Q8_0 && dma_rb<GT_Q8_0>(epi, p, s)) return;
         if (wtype == GT_Q4_K && dma_rb<GT_Q4_K>(epi, p, s)) return;
+        if (wtype == GT_Q8_0 && dma_rb_resid<GT_Q8_0>(epi, p, s)) return;
+        if (wtype == GT_Q4_K && dma_rb_resid<GT_Q4_K>(epi, p, s)) return;
         if (wtype == GT_Q8_0 && dma_splitk<GT_Q8_0>(epi, p, s)) return;
         if (wtype == GT_Q4_K && dma_splitk<GT_Q4_K>(epi, p, s)) return;
         if (wtype == GT_F16 && dma_splitk<GT_F16>(epi, p, s)) return;

@@ -117,23 +117,15 @@ def test_linear_tile_shapes(gpu, stream, gtype, M, N, K):
     assert err < 2e-3, err
 
 
-@pytest.mark.parametrize("gtype", [pm.GGML_Q8_0, pm.GGML_F16])
-def test_residual_split_k_fresh_inputs(gpu, stream, gtype):
-    """The split-K residual product (M <= 512 rows, K >= 1024: S workgroups per
-    tile hand partial tiles to the last arriver, which sums them in split order)
-    on fresh random inputs at every call, the calls of different sizes (some
-    with a tile's splits on two XCDs), so a stale or missing partial cannot
-    repeat the previous result.  Every element is
-    checked against a float64 product of the exact f16 operands the kernel
-    multiplies (activations rounded to f16; q8_0 weights f16(d q), f16 weights
-    as stored), within the worst-case f32 summation bound of its K terms, and
-    the first element outside it fails the test."""
-    rng = _rng(2048)
-    K, alpha = 2048, 0.5
-    # (M, N): 128 64x64 tiles x 2 splits and 64 x 4 (32 positions per XCD, a
-    # tile's splits on one XCD), then 10 tiles x 8 splits and 21 x 4, whose
-    # per-XCD ranges (10, 10-11 positions) cut tiles' splits over two XCDs
-    for call, (M, N) in enumerate(((512, 1024), (200, 1024), (128, 320), (192, 448), (512, 1024))):
+def _residual_calls(gpu, stream, gtype, K, shapes, rng, tag):
+    """linear_residual (y += alpha (x W^T + b)) on fresh random inputs at each
+    (M, N) of shapes.  Every element is checked against a float64 product of
+    the exact f16 operands the kernel multiplies (activations rounded to f16;
+    q8_0 weights f16(d q), f16 weights as stored), within the worst-case f32
+    summation bound of its K terms, and the first element outside it fails
+    the test."""
+    alpha = 0.5
+    for call, (M, N) in enumerate(shapes):
         raw, wf = _weights(gtype, N, K, rng)
         if gtype == pm.GGML_Q8_0:
             blk = raw.reshape(-1, 34)
@@ -150,7 +142,7 @@ def test_residual_split_k_fresh_inputs(gpu, stream, gtype):
         ref = y0.astype(np.float64) + alpha * (acc + b)
         # |f32 sum - exact| <= K 2^-24 sum|x w| (+ the rounding of the last adds)
         bound = K * 2.0 ** -24 * (np.abs(x16) @ np.abs(w16).T) + 2.0 ** -22 * (np.abs(ref) + 1.0)
-        print(f"[split-k] call {call} type={gtype} M={M} N={N} K={K}", flush=True)
+        print(f"[{tag}] call {call} type={gtype} M={M} N={N} K={K}", flush=True)
         dx = gpu.DeviceArray.from_numpy(x, stream)
         db = gpu.DeviceArray.from_numpy(b, stream)
         dy = gpu.DeviceArray.from_numpy(y0, stream)
@@ -162,3 +154,32 @@ def test_residual_split_k_fresh_inputs(gpu, stream, gtype):
             raise AssertionError(f"call {call}: y[{i}][{j}] = {got[i, j]!r}, float64 {ref[i, j]!r}, "
                                  f"bound {bound[i, j]:.3g} ({int(bad.sum())} elements outside)")
         dx.free(), db.free(), dy.free()
+
+
+@pytest.mark.parametrize("gtype", [pm.GGML_Q8_0, pm.GGML_F16])
+def test_residual_split_k_fresh_inputs(gpu, stream, gtype):
+    """The split-K residual product (M <= 512 rows, K >= 1024: S workgroups per
+    tile hand partial tiles to the last arriver, which sums them in split order)
+    on fresh random inputs at every call, the calls of different sizes (some
+    with a tile's splits on two XCDs), so a stale or missing partial cannot
+    repeat the previous result."""
+    # (M, N): 128 64x64 tiles x 2 splits and 64 x 4 (32 positions per XCD, a
+    # tile's splits on one XCD), then 10 tiles x 8 splits and 21 x 4, whose
+    # per-XCD ranges (10, 10-11 positions) cut tiles' splits over two XCDs
+    _residual_calls(gpu, stream, gtype, 2048, ((512, 1024), (200, 1024), (128, 320), (192, 448), (512, 1024)),
+                    _rng(2048), "split-k")
+
+
+@pytest.mark.parametrize("gtype", [pm.GGML_Q8_0, pm.GGML_F16])
+@pytest.mark.parametrize("K", [4096, 1024, 512])
+def test_residual_two_k_groups(gpu, stream, gtype, K):
+    """The residual products at N = 1024, M = 2000 (FFN linear2 and attention
+    output shapes): q8_0 weights on the register-B kernel with two K groups
+    (64 x 128 tiles, one per CU), f16 weights on the LDS-B kernel with two K
+    groups.  In the former group g sums the other group's partial into row
+    block g; M = 2040 leaves the last tile's second row block 24 rows,
+    M = 1990 leaves it none (the first 6), and N = 960 leaves the last column
+    tile's two right waves no columns."""
+    _residual_calls(gpu, stream, gtype, K, ((2000, 1024), (2040, 1024), (1990, 1024), (2000, 960)),
+                    _rng(K + gtype), "two-k-groups")
+
