@@ -1866,6 +1866,11 @@ __global__ __launch_bounds__(256 * KG, 1) void gemm_rb_kernel(GemmParams p) {
 #pragma unroll
         for (int u = 0; u < C::U; ++u) {
             const int k = k0 + u;
+            // No instruction crosses a slab boundary: the scheduler would
+            // otherwise fill the slab's VALU slots with the next slab's
+            // dequantisation, whose weights were loaded only one slab ago
+            // (a wait on them that empties the read-ahead).
+            __builtin_amdgcn_sched_barrier(0);
             // slab k+1 (A in LDS from every wave, B in this wave's registers) has landed
             wait_vmcnt<(NS - 3) * C::PER_SLAB>();
             __builtin_amdgcn_s_barrier();
