@@ -414,7 +414,7 @@ def main():
                            tj["calibration"]["fetch_factor"], tj["calibration"]["write_factor"],
                            tj["algorithmic_bytes_per_launch"]["family_avg"]))
     roofline = {"bound": "mfma",
-                "kernel": "gemm_ffn (f16 MFMA; linear1 q8_0 weights dequantised in registers, linear2 after LDS)",
+                "kernel": "gemm_ffn (f16 MFMA; q8_0 weights dequantised in registers: linear1 on 128x256 tiles, linear2 on 64x128 tiles in two K groups)",
                 "achieved": round(ffn_tf, 2), "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(ffn_tf / PEAK_F16_TFLOPS, 4), "traffic": traffic, "traffic_source": traffic_src,
                 "avg_us": round(ffn_avg_s * 1e6, 2), "launches_sampled": int(ffn_n),
