@@ -1849,17 +1849,22 @@ __global__ __launch_bounds__(256 * KG, 1) void gemm_rb_kernel(GemmParams p) {
             }
     };
 
-    // prologue: slabs 0 .. NS-2 in flight, slab 0 in registers
+    // prologue: slabs 0 .. NS-3 issued; once slab 0 has landed it goes into
+    // registers and slab NS-2 is issued behind it (the loop starts with
+    // slabs 1 .. NS-2 in flight).  Issuing slab NS-2 first kept every wave
+    // issuing loads for ~0.9k cycles after slab 0 had arrived.
 #pragma unroll
-    for (int k = 0; k < NS - 1; ++k) {
+    for (int k = 0; k < NS - 2; ++k) {
         issue_a(k);
         braw[k % NR].load(rq, rs, vq, vs, soq(k), sos(k));
     }
-    wait_vmcnt<(NS - 2) * C::PER_SLAB>();
+    wait_vmcnt<(NS - 3) * C::PER_SLAB>();
     __builtin_amdgcn_s_barrier();
     read_a(af[0], 0);
 #pragma unroll
     for (int j = 0; j < WTN; ++j) braw[0].convert_j(bf[0][j], j, q);
+    issue_a(NS - 2);
+    braw[(NS - 2) % NR].load(rq, rs, vq, vs, soq(NS - 2), sos(NS - 2));
 
     // nk % U == 0 (checked on the host): the ring indices of slab k are u-static
     for (int k0 = 0; k0 < nk; k0 += C::U) {
