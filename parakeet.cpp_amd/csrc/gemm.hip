@@ -1690,11 +1690,17 @@ __device__ __forceinline__ void epilogue_rb_resid(const GemmParams& p, const flo
 // and finishes row block g of the 64-row tile (the other group's partial of
 // it comes through LDS): two waves per SIMD for grids of about one tile per
 // CU.  Used with the residual epilogues on 64 x 128 tiles.
-template <int WTM, int WTN, int WT, int EPI, int NS, bool FO = false, int KG = 1>
+// NWV = 8: eight waves side by side along N (one K group), two per SIMD, each
+// reading its slab's activation fragments within the slab (a two-step
+// buffer) instead of one slab ahead, which the registers of two waves per
+// SIMD cannot hold; the other wave on the SIMD covers the LDS latency.
+template <int WTM, int WTN, int WT, int EPI, int NS, bool FO = false, int KG = 1, int NWV = 4>
 struct RbCfg {
-    static constexpr int BM = 32 * WTM, BN = 128 * WTN, WC = 32 * WTN;
+    static constexpr int BM = 32 * WTM, BN = NWV * 32 * WTN, WC = 32 * WTN;
+    static constexpr int NT = 64 * NWV * KG;                  // threads
+    static constexpr bool SB = NWV == 8;                      // fragments read within their slab
     static constexpr int A_STAGE = BM * 128;                  // f16 [BM][64]
-    static constexpr int NA = A_STAGE / 4096;                 // 1 KB A DMAs per wave per slab
+    static constexpr int NA = A_STAGE / (NWV * 1024);         // 1 KB A DMAs per wave per slab
     static constexpr int NB = rb_b_ops<WT, WTN>();
     static constexpr int PER_SLAB = NA + NB;
     static constexpr int NR = 4;                              // weight register sets (>= NS - 1 in flight)
@@ -1705,12 +1711,13 @@ struct RbCfg {
     static constexpr int RING = KG * NS * A_STAGE;
     static constexpr int FOLD_BYTES = FOLD ? BM * 32 * 8 : 0; // {mean, M2} of up to 32 groups per row
     static constexpr int XCH = KG == 2 ? 8 * 16 * WTN * 64 * 4 : 0;   // K-group exchange
-    static constexpr int CTAB = 4 * KG * NCA * WC * 4;        // epilogue column constants
+    static constexpr int CTAB = NWV * KG * NCA * WC * 4;      // epilogue column constants
     static constexpr int STG = RESID ? 8 * 32 * (WC + 4) * 4 : 0;   // residual staging
     static constexpr int AFTER = XCH + CTAB + STG;            // the post-loop regions, from offset 0
     static constexpr int BODY = (RING > AFTER ? RING : AFTER) + FOLD_BYTES;
     static constexpr int LDS = BODY + BM * 8;
-    static_assert(A_STAGE % 4096 == 0, "A slab splits into 1 KB DMAs per wave");
+    static_assert(A_STAGE % (NWV * 1024) == 0, "A slab splits into 1 KB DMAs per wave");
+    static_assert(NWV == 4 || (NWV == 8 && KG == 1 && !RESID), "eight waves: one K group, store / SiLU");
     static_assert(!FOLD || AFTER <= RING, "the fold statistics sit past the ring");
     static_assert(LDS <= 160 * 1024, "LDS budget");
     static_assert(KG == 1 || KG == 2, "K groups");
@@ -1719,9 +1726,9 @@ struct RbCfg {
     static_assert(!FOLD || KG == 1, "folded LayerNorm: one K group");
 };
 
-template <int WTM, int WTN, int WT, int EPI, int NS, bool FO = false, int KG = 1>
-__global__ __launch_bounds__(256 * KG, 1) void gemm_rb_kernel(GemmParams p) {
-    typedef RbCfg<WTM, WTN, WT, EPI, NS, FO, KG> C;
+template <int WTM, int WTN, int WT, int EPI, int NS, bool FO = false, int KG = 1, int NWV = 4>
+__global__ __launch_bounds__(64 * NWV * KG, 1) void gemm_rb_kernel(GemmParams p) {
+    typedef RbCfg<WTM, WTN, WT, EPI, NS, FO, KG, NWV> C;
     static_assert(NS >= 3 && NS <= 5, "ring depth");
     static_assert(EPI == EPI_STORE || EPI == EPI_STORE_F32 || EPI == EPI_SILU || C::RESID,
                   "register-B kernel: store / SiLU / residual epilogues");
@@ -1729,7 +1736,7 @@ __global__ __launch_bounds__(256 * KG, 1) void gemm_rb_kernel(GemmParams p) {
     __shared__ __attribute__((aligned(1024))) uint8_t smem_all[C::LDS];
 
     const int tid = threadIdx.x, lane = tid & 63, wid_all = wave_id_uniform();
-    const int kg = wid_all >> 2, wid = wid_all & 3;
+    const int kg = KG == 2 ? wid_all >> 2 : 0, wid = KG == 2 ? wid_all & 3 : wid_all;
     const int q = lane >> 5, r32 = lane & 31;
     uint8_t* smem = smem_all + kg * NS * C::A_STAGE;   // this group's ring
     int bm, bn;
@@ -1747,7 +1754,7 @@ __global__ __launch_bounds__(256 * KG, 1) void gemm_rb_kernel(GemmParams p) {
             make_rsrc((const float2v*)p.fold_stats + (int64_t)m0 * p.fold_groups,
                       ((int64_t)(p.M - m0) * p.fold_groups) * 8);
         uint8_t* fl = smem_all + C::BODY - C::FOLD_BYTES;
-        for (int c0 = wid * 64; c0 < total; c0 += 256) {
+        for (int c0 = wid * 64; c0 < total; c0 += 64 * NWV) {
             const int ch = c0 + lane, r = ch >> lc;
             const uint32_t off = ch < total ? (uint32_t)(min(r, p.M - 1 - m0) << (lc + 4)) + ((ch & ((1 << lc) - 1)) << 4)
                                             : OOB;
@@ -1849,56 +1856,99 @@ __global__ __launch_bounds__(256 * KG, 1) void gemm_rb_kernel(GemmParams p) {
             }
     };
 
-    // prologue: slabs 0 .. NS-3 issued; once slab 0 has landed it goes into
-    // registers and slab NS-2 is issued behind it (the loop starts with
-    // slabs 1 .. NS-2 in flight).  Issuing slab NS-2 first kept every wave
-    // issuing loads for ~0.9k cycles after slab 0 had arrived.
+    if constexpr (C::SB) {
+        // slabs 0 .. NS-2 in flight; per slab: wait for it, one barrier, issue
+        // slab k+NS-1, dequantise slab k's weights, then its MFMAs with the A
+        // fragments of step s+1 read under those of step s
 #pragma unroll
-    for (int k = 0; k < NS - 2; ++k) {
-        issue_a(k);
-        braw[k % NR].load(rq, rs, vq, vs, soq(k), sos(k));
-    }
-    wait_vmcnt<(NS - 3) * C::PER_SLAB>();
-    __builtin_amdgcn_s_barrier();
-    read_a(af[0], 0);
+        for (int k = 0; k < NS - 1; ++k) {
+            issue_a(k);
+            braw[k % NR].load(rq, rs, vq, vs, soq(k), sos(k));
+        }
+        for (int k0 = 0; k0 < nk; k0 += C::U) {
 #pragma unroll
-    for (int j = 0; j < WTN; ++j) braw[0].convert_j(bf[0][j], j, q);
-    issue_a(NS - 2);
-    braw[(NS - 2) % NR].load(rq, rs, vq, vs, soq(NS - 2), sos(NS - 2));
+            for (int u = 0; u < C::U; ++u) {
+                const int k = k0 + u;
+                __builtin_amdgcn_sched_barrier(0);
+                wait_vmcnt<(NS - 2) * C::PER_SLAB>();   // slab k has landed
+                __builtin_amdgcn_s_barrier();
+                issue_a(k + NS - 1);
+                braw[(u + NS - 1) % NR].load(rq, rs, vq, vs, soq(k + NS - 1), sos(k + NS - 1));
+                half8v b1[WTN][4], a2[2][WTM];
+#pragma unroll
+                for (int j = 0; j < WTN; ++j) braw[u % NR].convert_j(b1[j], j, q);
+                const uint8_t* st = smem + (k % NS) * C::A_STAGE;
+                auto read_step = [&](half8v (&a)[WTM], int s2) {
+#pragma unroll
+                    for (int i = 0; i < WTM; ++i) {
+                        const int row = 32 * i + r32;
+                        a[i] = *(const half8v*)(st + row * 128 + (((4 * q + s2) ^ ((row >> 1) & 7)) << 4));
+                    }
+                };
+                read_step(a2[0], 0);
+#pragma unroll
+                for (int s2 = 0; s2 < 4; ++s2) {
+                    if (s2 < 3) read_step(a2[(s2 + 1) & 1], s2 + 1);
+#pragma unroll
+                    for (int i = 0; i < WTM; ++i)
+#pragma unroll
+                        for (int j = 0; j < WTN; ++j)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b1[j][s2], a2[s2 & 1][i], acc[i][j], 0, 0, 0);
+                }
+            }
+        }
+    } else {
+        // prologue: slabs 0 .. NS-3 issued; once slab 0 has landed it goes into
+        // registers and slab NS-2 is issued behind it (the loop starts with
+        // slabs 1 .. NS-2 in flight).  Issuing slab NS-2 first kept every wave
+        // issuing loads for ~0.9k cycles after slab 0 had arrived.
+    #pragma unroll
+        for (int k = 0; k < NS - 2; ++k) {
+            issue_a(k);
+            braw[k % NR].load(rq, rs, vq, vs, soq(k), sos(k));
+        }
+        wait_vmcnt<(NS - 3) * C::PER_SLAB>();
+        __builtin_amdgcn_s_barrier();
+        read_a(af[0], 0);
+    #pragma unroll
+        for (int j = 0; j < WTN; ++j) braw[0].convert_j(bf[0][j], j, q);
+        issue_a(NS - 2);
+        braw[(NS - 2) % NR].load(rq, rs, vq, vs, soq(NS - 2), sos(NS - 2));
 
-    // nk % U == 0 (checked on the host): the ring indices of slab k are u-static
-    for (int k0 = 0; k0 < nk; k0 += C::U) {
-#pragma unroll
-        for (int u = 0; u < C::U; ++u) {
-            const int k = k0 + u;
-            // No instruction crosses a slab boundary: the scheduler would
-            // otherwise fill the slab's VALU slots with the next slab's
-            // dequantisation, whose weights were loaded only one slab ago
-            // (a wait on them that empties the read-ahead).
-            __builtin_amdgcn_sched_barrier(0);
-            // slab k+1 (A in LDS from every wave, B in this wave's registers) has landed
-            wait_vmcnt<(NS - 3) * C::PER_SLAB>();
-            __builtin_amdgcn_s_barrier();
-            issue_a(k + NS - 1);
-            braw[(u + NS - 1) % NR].load(rq, rs, vq, vs, soq(k + NS - 1), sos(k + NS - 1));
-            const int cu = u & 1, nx = cu ^ 1;
-            // the MFMAs of slab k, with the next slab's A reads and weight
-            // dequantisation interleaved (one MFMA, then an LDS read or four VALU)
-            read_a(af[nx], k + 1);
-#pragma unroll
-            for (int j = 0; j < WTN; ++j) braw[(u + 1) % NR].convert_j(bf[nx][j], j, q);
-#pragma unroll
-            for (int s = 0; s < 4; ++s)
-#pragma unroll
-                for (int i = 0; i < WTM; ++i)
-#pragma unroll
-                    for (int j = 0; j < WTN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[cu][j][s], af[cu][s][i], acc[i][j], 0, 0, 0);
-#pragma unroll
-            for (int g = 0; g < 4 * WTM * WTN; ++g) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-                if (g < 4 * WTM) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // LDS read
-                __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // VALU
+        // nk % U == 0 (checked on the host): the ring indices of slab k are u-static
+        for (int k0 = 0; k0 < nk; k0 += C::U) {
+    #pragma unroll
+            for (int u = 0; u < C::U; ++u) {
+                const int k = k0 + u;
+                // No instruction crosses a slab boundary: the scheduler would
+                // otherwise fill the slab's VALU slots with the next slab's
+                // dequantisation, whose weights were loaded only one slab ago
+                // (a wait on them that empties the read-ahead).
+                __builtin_amdgcn_sched_barrier(0);
+                // slab k+1 (A in LDS from every wave, B in this wave's registers) has landed
+                wait_vmcnt<(NS - 3) * C::PER_SLAB>();
+                __builtin_amdgcn_s_barrier();
+                issue_a(k + NS - 1);
+                braw[(u + NS - 1) % NR].load(rq, rs, vq, vs, soq(k + NS - 1), sos(k + NS - 1));
+                const int cu = u & 1, nx = cu ^ 1;
+                // the MFMAs of slab k, with the next slab's A reads and weight
+                // dequantisation interleaved (one MFMA, then an LDS read or four VALU)
+                read_a(af[nx], k + 1);
+    #pragma unroll
+                for (int j = 0; j < WTN; ++j) braw[(u + 1) % NR].convert_j(bf[nx][j], j, q);
+    #pragma unroll
+                for (int s = 0; s < 4; ++s)
+    #pragma unroll
+                    for (int i = 0; i < WTM; ++i)
+    #pragma unroll
+                        for (int j = 0; j < WTN; ++j)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[cu][j][s], af[cu][s][i], acc[i][j], 0, 0, 0);
+    #pragma unroll
+                for (int g = 0; g < 4 * WTM * WTN; ++g) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                    if (g < 4 * WTM) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // LDS read
+                    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // VALU
+                }
             }
         }
     }
@@ -1910,12 +1960,15 @@ __global__ __launch_bounds__(256 * KG, 1) void gemm_rb_kernel(GemmParams p) {
     if constexpr (fold) {
         FoldStats<BM> fst;
         const int lc = __builtin_ctz(p.fold_groups / 2), total = BM << lc;
+        if (tid < 256) {   // the table is built by 256 threads
 #pragma unroll
-        for (int i = 0; i < FoldStats<BM>::MAXC; ++i) {
-            const int ch = tid + 256 * i;
-            fst.c[i] = ch < total ? ((const float4v*)(smem_all + C::BODY - C::FOLD_BYTES))[ch] : (float4v){0.f, 0.f, 0.f, 0.f};
+            for (int i = 0; i < FoldStats<BM>::MAXC; ++i) {
+                const int ch = tid + 256 * i;
+                fst.c[i] = ch < total ? ((const float4v*)(smem_all + C::BODY - C::FOLD_BYTES))[ch]
+                                      : (float4v){0.f, 0.f, 0.f, 0.f};
+            }
+            fst.finish(p, ftab, tid);
         }
-        fst.finish(p, ftab, tid);
         __syncthreads();
     }
     // two K groups: group g's partial of row block 1 - g goes to the other
@@ -2267,9 +2320,9 @@ static void run_dma(const GemmParams& p, hipStream_t s) {
     }
 }
 
-template <int WTM, int WTN, int WT, int EPI, int NS, int KG = 1>
+template <int WTM, int WTN, int WT, int EPI, int NS, int KG = 1, int NWV = 4>
 static void run_rb(const GemmParams& p, hipStream_t s) {
-    typedef RbCfg<WTM, WTN, WT, EPI, NS, false, KG> C;
+    typedef RbCfg<WTM, WTN, WT, EPI, NS, false, KG, NWV> C;
     constexpr bool can_fold = (EPI == EPI_STORE || EPI == EPI_SILU) && KG == 1;
     require(p.K % (64 * C::U * KG) == 0, "gemm: register-B kernel needs K % (256 x K groups) == 0");
     if (EPI == EPI_RESID_LN) require(p.N % 32 == 0, "gemm: register-B residual + LayerNorm statistics needs N % 32 == 0");
@@ -2280,8 +2333,8 @@ static void run_rb(const GemmParams& p, hipStream_t s) {
     const int tiles = cdiv(p.M, C::BM) * cdiv(p.N, C::BN);
     GemmParams q = p;
     q.xcd_gm = choose_xcd_gm(p, WT, C::BM, C::BN);
-    if (can_fold && p.fold_stats) launch((gemm_rb_kernel<WTM, WTN, WT, EPI, NS, can_fold, KG>), dim3(tiles), dim3(256 * KG), 0, s, q);
-    else launch((gemm_rb_kernel<WTM, WTN, WT, EPI, NS, false, KG>), dim3(tiles), dim3(256 * KG), 0, s, q);
+    if (can_fold && p.fold_stats) launch((gemm_rb_kernel<WTM, WTN, WT, EPI, NS, can_fold, KG, NWV>), dim3(tiles), dim3(C::NT), 0, s, q);
+    else launch((gemm_rb_kernel<WTM, WTN, WT, EPI, NS, false, KG, NWV>), dim3(tiles), dim3(C::NT), 0, s, q);
     PKX_LAUNCH_CHECK();
 }
 
@@ -2361,9 +2414,10 @@ static bool dma_kg2(int epi, const GemmParams& p, hipStream_t s) {
     default: return false;
     }
 }
-// Register-B kernel (128 x 256 tiles, one per CU) for the wide quantised
-// products: FFN linear1 (N = 4096), q/k/v (N = 3072) and the all-layer
-// positional projection.  On MI355X at M = 2000, K = 1024 (q8_0): 25.7 against
+// Register-B kernel (128 x 256 tiles, one per CU, eight waves of 32 columns:
+// two per SIMD; 4.56 -> 4.52 ms per step against four waves of 64 columns,
+// same machine) for the wide quantised products: FFN linear1 (N = 4096),
+// q/k/v (N = 3072) and the all-layer positional projection.  On MI355X at M = 2000, K = 1024 (q8_0): 25.7 against
 // 27.8 us (FFN linear1), 25.0 against 27.7 (q/k/v, folded LayerNorm), 22.2
 // against 24.9 (positional, M = 249, N = 24576) for the LDS-B 128 x 128 tiles.
 // Taken when the grid is one round of the chip at least 70% full, or four
@@ -2378,9 +2432,9 @@ static bool dma_rb(int epi, const GemmParams& p, hipStream_t s) {
     const int64_t tiles = (int64_t)cdiv(p.M, 128) * cdiv(p.N, 256), cus = device_cu_count();
     if (!((tiles <= cus && tiles * 10 >= cus * 7) || tiles >= 4 * cus)) return false;
     switch (epi) {
-    case EPI_STORE: run_rb<4, 2, WT, EPI_STORE, 4>(p, s); break;
-    case EPI_SILU: run_rb<4, 2, WT, EPI_SILU, 4>(p, s); break;
-    default: run_rb<4, 2, WT, EPI_STORE_F32, 4>(p, s); break;
+    case EPI_STORE: run_rb<4, 1, WT, EPI_STORE, 4, 1, 8>(p, s); break;
+    case EPI_SILU: run_rb<4, 1, WT, EPI_SILU, 4, 1, 8>(p, s); break;
+    default: run_rb<4, 1, WT, EPI_STORE_F32, 4, 1, 8>(p, s); break;
     }
     return true;
 }
