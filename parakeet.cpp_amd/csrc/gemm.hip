@@ -1492,13 +1492,15 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
 // Register-B kernel (gemm_rb_kernel): only the activation tile goes through
 // LDS; the weights stream from L2 straight into registers.
 //
-// Four waves side by side along N, each owning 32 WTM rows x 32 WTN columns of
-// a (32 WTM) x (128 WTN) workgroup tile, one workgroup per CU.  A wave's
-// weight columns are its own, so each weight is loaded and dequantised once
-// per workgroup and never written to or read from LDS; the A tile (BM rows x
-// 64 K per slab) arrives by global_load_lds DMA into an NS-stage ring and is
-// read by all four waves.  LDS bytes per slab: BM*128 written + 4*BM*128 read,
-// i.e. 5/BN bytes per flop (the 128 x 128 LDS-B kernel moves about 2.4x that).
+// NWV waves (4 or 8) side by side along N, each owning 32 WTM rows x 32 WTN
+// columns of a (32 WTM) x (NWV 32 WTN) workgroup tile, one workgroup per CU.  A
+// wave's weight columns are its own, so each weight is loaded and dequantised
+// once per workgroup and never written to or read from LDS; the A tile (BM
+// rows x 64 K per slab) arrives by global_load_lds DMA into an NS-stage ring
+// and is read by every wave.  LDS bytes per slab: BM*128 written + NWV*BM*128
+// read (four waves: 5/BN bytes per flop, the 128 x 128 LDS-B kernel moves
+// about 2.4x that; eight waves of 32 columns read the A tile twice as often
+// and run two waves per SIMD).
 //
 // Per slab k one barrier, then the slab k+NS-1 loads are issued (A DMA, B
 // register loads; slabs past K read out of range and return zeros, so the
