@@ -2395,8 +2395,9 @@ static bool dma_splitk(int epi, const GemmParams& p, hipStream_t s) {
     return true;
 }
 // 128 x 64 tiles with two K groups (eight waves): products of K >= 1024 whose
-// grid is about one tile per CU (FFN linear2 at K = 4096; attention out and
-// pw2 at K = 1024, where the split takes 0.3 - 0.9 us off a 14 - 15 us launch)
+// grid is about one tile per CU and that the register-B kernels do not take
+// (pw2 with f16 weights at K = 1024; the split took 0.3 - 0.9 us off a
+// 14 - 15 us launch of these shapes)
 template <int WT>
 static bool dma_kg2(int epi, const GemmParams& p, hipStream_t s) {
     if (p.K % 128 != 0 || p.K < 1024 || (int64_t)cdiv(p.M, 128) * cdiv(p.N, 64) > 256) return false;
@@ -2532,11 +2533,12 @@ void launch_gemm(Precision prec, int wtype, int epi, const GemmParams& p, hipStr
     const bool big = (int64_t)cdiv(p.M, 128) * cdiv(p.N, 128) >= 256;
     if (dma_ok) {
         // Tile shapes from sweeps over the encoder's shapes on MI355X (M = B*T' = 2000):
-        // q8_0 and q4_K weights prefer 128x128 when the grid holds >= 384 of them (N >= 3072,
-        // and the all-layer positional projection), 128x64 at N = 1024 (FFN2, attention
-        // output), 64x64 for grids too small to fill the chip; f16 weights run best at
-        // 64x128 throughout.  The GLU epilogue pairs 64-column groups, so it needs a
-        // tile at least 128 wide.
+        // the register-B kernels take the wide quantised products and the quantised
+        // N = 1024 residual products when their grids fit one round of the chip;
+        // otherwise q8_0 and q4_K weights prefer 128x128 when the grid holds >= 384 of
+        // them, 128x64 with two K groups for long K, 64x64 for grids too small to fill
+        // the chip; f16 weights run best at 64x128 (pw2: 128x64, two K groups).  The
+        // GLU epilogue pairs 64-column groups, so it needs a tile at least 128 wide.
         const int64_t t22 = (int64_t)cdiv(p.M, 128) * cdiv(p.N, 128);
         const int64_t t21 = (int64_t)cdiv(p.M, 128) * cdiv(p.N, 64);
         const bool glu = epi == EPI_GLU || epi == EPI_GLU_DW;
