@@ -1768,13 +1768,6 @@ __global__ __launch_bounds__(64 * NWV * KG, 1) void gemm_rb_kernel(GemmParams p)
     const float alpha = EPI == EPI_SILU ? 1.f : p.alpha;
     constexpr int CPL = (WC + 63) / 64;
     float colv[C::NCA][CPL];
-#pragma unroll
-    for (int t = 0; t < CPL; ++t) {
-        const int c = lane + 64 * t, n = nw + c;
-        const bool ok = c < WC && n < p.N;
-        colv[0][t] = ok && p.bias ? p.bias[n] : 0.f;   // times alpha when written to LDS
-        if constexpr (C::NCA == 2) colv[1][t] = fold && ok ? p.fold_c1[n] : 0.f;
-    }
     // residual epilogues: the wave's 32-row block of the residual stream (row
     // block kg of the tile) in the copy-out's layout, its rows' statistics
     // and the copy-out's columns of gamma, res_g, res_b, in registers before
@@ -1782,10 +1775,25 @@ __global__ __launch_bounds__(64 * NWV * KG, 1) void gemm_rb_kernel(GemmParams p)
     constexpr bool RS = EPI == EPI_RESID_LN;
     ResidPre<C::RESID ? 32 : 64, C::RESID ? 8 * WTN : 1, RS> rpre;
     EpiCols<WTN> ecol;
-    if constexpr (C::RESID) {
-        rpre.load(p, m0 + 32 * kg, nw, lane);
-        ecol.load(p, nw, lane, false, RS);
-    }
+    // issued right behind slab 0's loads, so that those go out first (ahead
+    // of them the second K group's slab 0 waited ~2k cycles behind the first
+    // group's operand loads); the first slab wait covers them (they are older
+    // than slab 1's loads)
+    auto load_epi_operands = [&]() {
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int t = 0; t < CPL; ++t) {
+            const int c = lane + 64 * t, n = nw + c;
+            const bool ok = c < WC && n < p.N;
+            colv[0][t] = ok && p.bias ? p.bias[n] : 0.f;   // times alpha when written to LDS
+            if constexpr (C::NCA == 2) colv[1][t] = fold && ok ? p.fold_c1[n] : 0.f;
+        }
+        if constexpr (C::RESID) {
+            rpre.load(p, m0 + 32 * kg, nw, lane);
+            ecol.load(p, nw, lane, false, RS);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
 
     // A: 64-column slabs of rows m0.., swizzled 16-byte chunks (as DmaSrc)
     const __amdgpu_buffer_rsrc_t ra =
@@ -1866,6 +1874,7 @@ __global__ __launch_bounds__(64 * NWV * KG, 1) void gemm_rb_kernel(GemmParams p)
         for (int k = 0; k < NS - 1; ++k) {
             issue_a(k);
             braw[k % NR].load(rq, rs, vq, vs, soq(k), sos(k));
+            if (k == 0) load_epi_operands();
         }
         for (int k0 = 0; k0 < nk; k0 += C::U) {
 #pragma unroll
@@ -1908,6 +1917,7 @@ __global__ __launch_bounds__(64 * NWV * KG, 1) void gemm_rb_kernel(GemmParams p)
         for (int k = 0; k < NS - 2; ++k) {
             issue_a(k);
             braw[k % NR].load(rq, rs, vq, vs, soq(k), sos(k));
+            if (k == 0) load_epi_operands();
         }
         wait_vmcnt<(NS - 3) * C::PER_SLAB>();
         __builtin_amdgcn_s_barrier();
