@@ -1987,18 +1987,28 @@ __global__ __launch_bounds__(64 * NWV * KG, 1) void gemm_rb_kernel(GemmParams p)
     // group, which adds it to its own (lane-major [wave][register][lane] f32)
     float16v fin[WTN];
     if constexpr (KG == 2) {
+        // [wave][register / 4][lane] float4s: 16-byte accesses, 1 KB per instruction
         constexpr int R = 16 * WTN;
-        float* give = (float*)smem_all + wid_all * R * 64 + lane;
-        const float* take = (const float*)smem_all + ((1 - kg) * 4 + wid) * R * 64 + lane;
+        float4v* give = (float4v*)smem_all + wid_all * (R / 4) * 64 + lane;
+        const float4v* take = (const float4v*)smem_all + ((1 - kg) * 4 + wid) * (R / 4) * 64 + lane;
 #pragma unroll
         for (int j = 0; j < WTN; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) give[(j * 16 + r) * 64] = kg ? acc[0][j][r] : acc[1][j][r];
+            for (int t = 0; t < 4; ++t) {
+                float4v g;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) g[e] = kg ? acc[0][j][4 * t + e] : acc[1][j][4 * t + e];
+                give[(j * 4 + t) * 64] = g;
+            }
         __syncthreads();
 #pragma unroll
         for (int j = 0; j < WTN; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) fin[j][r] = (kg ? acc[1][j][r] : acc[0][j][r]) + take[(j * 16 + r) * 64];
+            for (int t = 0; t < 4; ++t) {
+                const float4v o = take[(j * 4 + t) * 64];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) fin[j][4 * t + e] = (kg ? acc[1][j][4 * t + e] : acc[0][j][4 * t + e]) + o[e];
+            }
     }
     // this wave's column constants (the ring is free; past the exchange):
     // written and read by the wave alone
