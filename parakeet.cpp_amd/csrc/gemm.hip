@@ -1317,21 +1317,32 @@ __global__ __launch_bounds__(256 * KG, KG == 1 ? 2 : 1) void gemm_dma_kernel(Gem
     if constexpr (KHALF) {
         constexpr int R = WTN * 16;
         static_assert(8 * R * 64 * 4 <= KG * NS * C::STAGE, "partial tiles exceed LDS");
-        float* give = (float*)smem_all + wid_all * R * 64 + lane;                      // region (kg, wid)
-        const float* take = (const float*)smem_all + ((1 - kg) * 4 + wid) * R * 64 + lane;   // (1-kg, wid)
+        // [wave][register / 4][lane] float4s: 16-byte accesses, 1 KB per instruction
+        float4v* give = (float4v*)smem_all + wid_all * (R / 4) * 64 + lane;                      // region (kg, wid)
+        const float4v* take = (const float4v*)smem_all + ((1 - kg) * 4 + wid) * (R / 4) * 64 + lane;   // (1-kg, wid)
         __syncthreads();
 #pragma unroll
         for (int j = 0; j < WTN; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                give[(j * 16 + r) * 64] = kg ? acc[0][j][r] : acc[1][j][r];
-                fin[0][j][r] = kg ? acc[1][j][r] : acc[0][j][r];
+            for (int t = 0; t < 4; ++t) {
+                float4v g;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int r = 4 * t + e;
+                    g[e] = kg ? acc[0][j][r] : acc[1][j][r];
+                    fin[0][j][r] = kg ? acc[1][j][r] : acc[0][j][r];
+                }
+                give[(j * 4 + t) * 64] = g;
             }
         __syncthreads();
 #pragma unroll
         for (int j = 0; j < WTN; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) fin[0][j][r] += take[(j * 16 + r) * 64];
+            for (int t = 0; t < 4; ++t) {
+                const float4v o = take[(j * 4 + t) * 64];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) fin[0][j][4 * t + e] += o[e];
+            }
     } else if constexpr (KG == 2) {
         // lane-major [wave][register][lane] f32: conflict-free both ways
         constexpr int R = WTM * WTN * 16;
