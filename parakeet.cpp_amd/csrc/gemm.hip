@@ -1154,15 +1154,15 @@ __device__ __forceinline__ void epilogue32_glu_dw(const GemmParams& p, float16v 
 // row, so a row's chunks sit in G/2 consecutive lanes of one wave), and
 // finish() combines each row with shuffles (Chan's pairwise formula) into
 // {mean, 1/sqrt(var + eps)} in LDS.
-template <int BM>
+template <int BM, int NTH = 256>
 struct FoldStats {
-    static constexpr int MAXC = BM * 32 / 2 / 256;   // chunks per thread for G <= 32
+    static constexpr int MAXC = BM * 32 / 2 / NTH;   // chunks per thread for G <= 32
     float4v c[MAXC];
     __device__ __forceinline__ void prefetch(const GemmParams& p, int m0, int t) {
         const int lc = __builtin_ctz(p.fold_groups / 2), total = BM << lc;   // log2 chunks per row
 #pragma unroll
         for (int i = 0; i < MAXC; ++i) {
-            const int ch = t + 256 * i;
+            const int ch = t + NTH * i;
             if (ch < total) {
                 const int r = ch >> lc, m = min(max(m0 + r, 0), p.M - 1);
                 c[i] = *((const float4v*)p.fold_stats + ((int64_t)m << lc) + (ch & ((1 << lc) - 1)));
@@ -1173,11 +1173,11 @@ struct FoldStats {
     }
     template <int CPR>
     __device__ __forceinline__ void finish_t(const GemmParams& p, float2v* tab, int t) const {
-        constexpr int G = 2 * CPR, NC = BM * CPR / 256 > 0 ? BM * CPR / 256 : 1;
+        constexpr int G = 2 * CPR, NC = BM * CPR / NTH > 0 ? BM * CPR / NTH : 1;
         static_assert(NC <= MAXC, "chunks");
 #pragma unroll
         for (int i = 0; i < NC; ++i) {
-            const int ch = t + 256 * i;
+            const int ch = t + NTH * i;
             const float mean = group_sum(c[i][0] + c[i][2], CPR) * (1.0f / G);
             const float da = c[i][0] - mean, db = c[i][2] - mean;
             const float q = group_sum(c[i][1] + c[i][3] + 32.0f * (da * da + db * db), CPR);
@@ -1601,9 +1601,40 @@ template <int WTN> struct BRaw<GT_F16, WTN> {
     }
 };
 
+// f16 weights copied into the conv-module kernel's fragment order
+// (glu_frag_prepare): per 64-deep slab and 32-column block, four 1 KB pieces
+// [t][lane] of 16 bytes, lane (q, c) holding column c's halves
+// k = 32 q + 8 t .. + 7 of the slab, so that each load instruction of a wave
+// reads 1 KB contiguous (row-major f16 rows put 32 rows x 2 pieces in every
+// instruction: four times the L1 work).  Not a GGML type.
+constexpr int GT_F16F = 101;
+template <int WTN> struct BRaw<GT_F16F, WTN> {
+    int4v q[WTN][4];
+    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rq, __amdgpu_buffer_rsrc_t, const uint32_t (&vq)[WTN],
+                                         const uint32_t (&)[WTN], int soq, int) {
+#pragma unroll
+        for (int j = 0; j < WTN; ++j)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) q[j][t] = __builtin_amdgcn_raw_buffer_load_b128(rq, (int)(vq[j] + 1024 * t), soq, 0);
+    }
+    __device__ __forceinline__ void convert_j(half8v (&bf)[4], int j, int) const {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) bf[t] = __builtin_bit_cast(half8v, q[j][t]);
+    }
+};
+
+// Conv-module item tiles: the weight row (GEMM column) of wave column c
+// (0 .. 31) of wave wid in column tile bn.  The weights hold 32-row groups of
+// GLU inputs and gates alternately; the wave takes channels c0 .. c0 + 15
+// (c0 = 64 bn + 16 wid): columns 0 .. 15 their inputs, 16 .. 31 their gates.
+__device__ __forceinline__ int glu_wcol(int bn, int wid, int c) {
+    const int c0 = 64 * bn + 16 * wid;
+    return 2 * c0 - (c0 & 31) + (c & 15) + 32 * (c >> 4);
+}
+
 // Vector-memory instructions of one slab's weight loads per wave.
 template <int WT, int WTN>
-constexpr int rb_b_ops() { return WT == GT_F16 ? 4 * WTN : 3 * WTN; }
+constexpr int rb_b_ops() { return WT == GT_F16 || WT == GT_F16F ? 4 * WTN : 3 * WTN; }
 
 // Register-B epilogue: lane l holds row 32 i + l % 32 of the tile at columns
 // nw + 32 j + 16 (l / 32) + r in acc[i][j][r].  y = alpha (acc + bias), with a
@@ -1698,6 +1729,87 @@ __device__ __forceinline__ void epilogue_rb_resid(const GemmParams& p, const flo
     epilogue_lds_out<EPI, 32, WC, WTN>(p, wsm, mb, nw, lane, ec, xpre, xrs);
 }
 
+// Register-B conv-module epilogue (item tiles of 128 rows x 64 channels,
+// rows t = 0 .. T-1 of one item): K group kg holds the summed rows 64 kg +
+// 32 ii + l % 32 in fin[ii], lane half l / 32 the inputs (0) or the gates (1)
+// of the wave's 16 channels in registers 0 .. 15.  One lane-half swap per
+// register pair hands each lane the input and the gate of channel
+// 16 wid + 8 (l / 32) + e; the GLU (folded LayerNorm, bias, a * sigmoid(b))
+// with the pad mask (rows t >= valid are zero, and with them the next item's
+// rows) goes into G [128][LDG] f32 in LDS.  Then the depthwise conv over time
+// (zero rows outside the item's valid frames), its bias, the folded BatchNorm
+// and SiLU for the T rows: thread tid takes the channel pair 2 (tid % 32) and
+// rows 8 (tid / 32) .. + 7, its 16-row window in registers, and stores f16
+// pairs (conformer.cpp:55-157).
+template <int LDG>
+__device__ __forceinline__ void epilogue_rb_glu_dw(const GemmParams& p, const float16v (&fin)[2][1], const float* ctab,
+                                                   const float2v* ftab, float* G, int m0, int item, int n0, int kg,
+                                                   int wid, int lane, int tid, bool fold, float4v taps4,
+                                                   const float2v (&dwc)[3]) {
+    constexpr int K = GLU_DW_K, H = (K - 1) / 2, RPT = 8;
+    // the tile's taps [64][K] past the GLU tile (thread tid < 144 brought 16 bytes)
+    float* taps = G + 128 * LDG;
+    if (tid < 64 * K / 4) ((float4v*)taps)[tid] = taps4;
+    const int h = lane >> 5, r32 = lane & 31;
+    const int T = p.T;
+    const int vl = p.valid ? min(p.valid[item], T) : T;
+    float4v bi[2], bg[2], ci[2], cg[2];   // input / gate bias, input / gate c1 of the lane's 8 channels
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        bi[t] = *(const float4v*)(ctab + 8 * h + 4 * t);
+        bg[t] = *(const float4v*)(ctab + 16 + 8 * h + 4 * t);
+        ci[t] = *(const float4v*)(ctab + 32 + 8 * h + 4 * t);
+        cg[t] = *(const float4v*)(ctab + 48 + 8 * h + 4 * t);
+    }
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii) {
+        const int row = 64 * kg + 32 * ii + r32;
+        float a = 1.f, nb = 0.f;
+        if (fold) {
+            const float2v st = ftab[row];
+            a = st.y;
+            nb = -a * st.x;
+        }
+        float o[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(fin[ii][0][e]),
+                                                             __float_as_uint(fin[ii][0][8 + e]), false, false);
+            const float xa = __uint_as_float(sw[0]), xg = __uint_as_float(sw[1]);
+            const float ba = fold ? __builtin_fmaf(nb, ci[e >> 2][e & 3], bi[e >> 2][e & 3]) : bi[e >> 2][e & 3];
+            const float bb = fold ? __builtin_fmaf(nb, cg[e >> 2][e & 3], bg[e >> 2][e & 3]) : bg[e >> 2][e & 3];
+            const float va = __builtin_fmaf(a, xa, ba), vg = __builtin_fmaf(a, xg, bb);
+            o[e] = row < vl ? va * sigmoid_dev(vg) : 0.f;
+        }
+        float* gr = G + row * LDG + 16 * wid + 8 * h;
+        *(float4v*)gr = (float4v){o[0], o[1], o[2], o[3]};
+        *(float4v*)(gr + 4) = (float4v){o[4], o[5], o[6], o[7]};
+    }
+    __syncthreads();
+    const int cl = 2 * (tid & 31), r0 = RPT * (tid >> 5), c = n0 / 2 + cl;
+    float2v wk[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) wk[j] = (float2v){taps[cl * K + j], taps[(cl + 1) * K + j]};
+    float2v win[RPT + K - 1];
+#pragma unroll
+    for (int q = 0; q < RPT + K - 1; ++q) {
+        const int row = r0 - H + q;
+        win[q] = row >= 0 && row < 128 ? *(const float2v*)(G + row * LDG + cl) : (float2v){0.f, 0.f};
+    }
+#pragma unroll
+    for (int q = 0; q < RPT; ++q) {
+        const int t = r0 + q;
+        if (t < T) {
+            float2v acc = {0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < K; ++j) acc += wk[j] * win[q + j];
+            const float2v y = (acc + dwc[0]) * dwc[1] + dwc[2];
+            const half2v hv = {(f16)silu_dev(y[0]), (f16)silu_dev(y[1])};
+            *(half2v*)((f16*)p.Y + (int64_t)(m0 + t) * p.ldy + c) = hv;
+        }
+    }
+}
+
 // KG = 2: eight waves in two groups of four; group g streams K slabs
 // [g nk, (g+1) nk) through its own ring, and after the main loop group g sums
 // and finishes row block g of the 64-row tile (the other group's partial of
@@ -1707,11 +1819,16 @@ __device__ __forceinline__ void epilogue_rb_resid(const GemmParams& p, const flo
 // reading its slab's activation fragments within the slab (a two-step
 // buffer) instead of one slab ahead, which the registers of two waves per
 // SIMD cannot hold; the other wave on the SIMD covers the LDS latency.
+// EPI_GLU_DW (the conformer conv module after pointwise_conv1): one item of
+// T <= 128 frames per 128-row tile, 64 channels (their 64 input and 64 gate
+// columns) per tile, two K groups; the depthwise conv never crosses an item,
+// so the tile needs no halo rows.
 template <int WTM, int WTN, int WT, int EPI, int NS, bool FO = false, int KG = 1, int NWV = 4>
 struct RbCfg {
     static constexpr int BM = 32 * WTM, BN = NWV * 32 * WTN, WC = 32 * WTN;
     static constexpr int NT = 64 * NWV * KG;                  // threads
-    static constexpr bool SB = NWV == 8;                      // fragments read within their slab
+    static constexpr bool GD = EPI == EPI_GLU_DW;             // item tiles, GLU + depthwise epilogue
+    static constexpr bool SB = NWV == 8 || GD;                // fragments read within their slab
     static constexpr int A_STAGE = BM * 128;                  // f16 [BM][64]
     static constexpr int NA = A_STAGE / (NWV * 1024);         // 1 KB A DMAs per wave per slab
     static constexpr int NB = rb_b_ops<WT, WTN>();
@@ -1719,33 +1836,41 @@ struct RbCfg {
     static constexpr int NR = 4;                              // weight register sets (>= NS - 1 in flight)
     static constexpr int U = 4;                               // loop unroll: every ring index static
     static constexpr bool RESID = EPI == EPI_RESID || EPI == EPI_RESID_LN;
-    static constexpr bool FOLD = FO && (EPI == EPI_STORE || EPI == EPI_SILU);
+    static constexpr bool FOLD = FO && (EPI == EPI_STORE || EPI == EPI_SILU || GD);
     static constexpr int NCA = RESID ? 1 : 2;                 // column constant arrays
     static constexpr int RING = KG * NS * A_STAGE;
     static constexpr int FOLD_BYTES = FOLD ? BM * 32 * 8 : 0; // {mean, M2} of up to 32 groups per row
-    static constexpr int XCH = KG == 2 ? 8 * 16 * WTN * 64 * 4 : 0;   // K-group exchange
+    static constexpr int XCH = KG == 2 ? 8 * (WTM / 2) * 16 * WTN * 64 * 4 : 0;   // K-group exchange
     static constexpr int CTAB = NWV * KG * NCA * WC * 4;      // epilogue column constants
-    static constexpr int STG = RESID ? 8 * 32 * (WC + 4) * 4 : 0;   // residual staging
+    static constexpr int LDG = 64 + 4;                        // GLU staging row (floats, GD)
+    static constexpr int TAPS = GD ? 64 * GLU_DW_K * 4 : 0;   // the tile's depthwise taps (GD)
+    static constexpr int STG = RESID ? 8 * 32 * (WC + 4) * 4 : GD ? BM * LDG * 4 + TAPS : 0;   // epilogue staging
     static constexpr int AFTER = XCH + CTAB + STG;            // the post-loop regions, from offset 0
     static constexpr int BODY = (RING > AFTER ? RING : AFTER) + FOLD_BYTES;
-    static constexpr int LDS = BODY + BM * 8;
+    // the row table {mean, rstd}: past the body, or (GD) over the start of the
+    // fold statistics, once they are in registers
+    static constexpr int FTAB = GD && FOLD ? BODY - FOLD_BYTES : BODY;
+    static constexpr int LDS = GD && FOLD ? BODY : BODY + BM * 8;
     static_assert(A_STAGE % (NWV * 1024) == 0, "A slab splits into 1 KB DMAs per wave");
     static_assert(NWV == 4 || (NWV == 8 && KG == 1 && !RESID), "eight waves: one K group, store / SiLU");
     static_assert(!FOLD || AFTER <= RING, "the fold statistics sit past the ring");
     static_assert(LDS <= 160 * 1024, "LDS budget");
     static_assert(KG == 1 || KG == 2, "K groups");
     static_assert(!RESID || (KG == 2 && WTM == 2), "residual epilogues: two K groups, one row block per group");
-    static_assert(RESID || KG == 1, "store / SiLU epilogues: one K group");
-    static_assert(!FOLD || KG == 1, "folded LayerNorm: one K group");
+    static_assert(!GD || (KG == 2 && WTM == 4 && WTN == 1 && NWV == 4), "conv module: 128 x 128 item tiles, two K groups");
+    static_assert(WT != GT_F16F || GD, "fragment-ordered f16 weights: conv-module kernel only");
+    static_assert(RESID || GD || KG == 1, "store / SiLU epilogues: one K group");
+    static_assert(!FOLD || KG == 1 || GD, "folded LayerNorm: one K group (or the conv module)");
 };
 
 template <int WTM, int WTN, int WT, int EPI, int NS, bool FO = false, int KG = 1, int NWV = 4>
 __global__ __launch_bounds__(64 * NWV * KG, 1) void gemm_rb_kernel(GemmParams p) {
     typedef RbCfg<WTM, WTN, WT, EPI, NS, FO, KG, NWV> C;
     static_assert(NS >= 3 && NS <= 5, "ring depth");
-    static_assert(EPI == EPI_STORE || EPI == EPI_STORE_F32 || EPI == EPI_SILU || C::RESID,
-                  "register-B kernel: store / SiLU / residual epilogues");
+    static_assert(EPI == EPI_STORE || EPI == EPI_STORE_F32 || EPI == EPI_SILU || C::RESID || C::GD,
+                  "register-B kernel: store / SiLU / residual / conv-module epilogues");
     constexpr int BM = C::BM, NR = C::NR, WC = C::WC;
+    constexpr bool GD = C::GD;
     __shared__ __attribute__((aligned(1024))) uint8_t smem_all[C::LDS];
 
     const int tid = threadIdx.x, lane = tid & 63, wid_all = wave_id_uniform();
@@ -1753,9 +1878,17 @@ __global__ __launch_bounds__(64 * NWV * KG, 1) void gemm_rb_kernel(GemmParams p)
     const int q = lane >> 5, r32 = lane & 31;
     uint8_t* smem = smem_all + kg * NS * C::A_STAGE;   // this group's ring
     int bm, bn;
-    xcd_tile_2d(blockIdx.x, cdiv_dev(p.M, BM), cdiv_dev(p.N, C::BN), p.xcd_gm, bm, bn);
-    const int m0 = bm * BM, n0 = bn * C::BN, nw = n0 + wid * WC;
+    // conv module: row tile bm is item bm (rows bm T .. bm T + T - 1; the rest
+    // of the 128 rows belong to the next item or lie past M and are masked)
+    xcd_tile_2d(blockIdx.x, GD ? p.M / p.T : cdiv_dev(p.M, BM), cdiv_dev(p.N, C::BN), p.xcd_gm, bm, bn);
+    const int m0 = bm * (GD ? p.T : BM), n0 = bn * C::BN, nw = n0 + wid * WC;
     const int nkt = p.K / 64, nk = nkt / KG, kb = kg * nk;   // slabs: all, this group's, its first
+    // weight column of the wave's column c (0 .. WC-1); conv module: lanes l
+    // and l + 32 end with the input and the gate of the same 16 channels
+    auto wcol = [&](int c) -> int {
+        if constexpr (GD) return glu_wcol(bn, wid, c);
+        else return nw + c;
+    };
 
     // folded LayerNorm (FO: p.fold_stats is set) statistics of the tile's rows:
     // DMA into LDS first (the oldest vector-memory operations, complete by the
@@ -1767,7 +1900,7 @@ __global__ __launch_bounds__(64 * NWV * KG, 1) void gemm_rb_kernel(GemmParams p)
             make_rsrc((const float2v*)p.fold_stats + (int64_t)m0 * p.fold_groups,
                       ((int64_t)(p.M - m0) * p.fold_groups) * 8);
         uint8_t* fl = smem_all + C::BODY - C::FOLD_BYTES;
-        for (int c0 = wid * 64; c0 < total; c0 += 64 * NWV) {
+        for (int c0 = wid_all * 64; c0 < total; c0 += 64 * NWV * KG) {
             const int ch = c0 + lane, r = ch >> lc;
             const uint32_t off = ch < total ? (uint32_t)(min(r, p.M - 1 - m0) << (lc + 4)) + ((ch & ((1 << lc) - 1)) << 4)
                                             : OOB;
@@ -1776,9 +1909,12 @@ __global__ __launch_bounds__(64 * NWV * KG, 1) void gemm_rb_kernel(GemmParams p)
     }
     // the epilogue's column constants of column nw + lane + 64 t (written to
     // LDS after the main loop): alpha * bias, then the fold's c1 (store / SiLU)
-    const float alpha = EPI == EPI_SILU ? 1.f : p.alpha;
+    const float alpha = EPI == EPI_SILU || GD ? 1.f : p.alpha;
     constexpr int CPL = (WC + 63) / 64;
     float colv[C::NCA][CPL];
+    // conv module: the depthwise bias and folded BatchNorm of this thread's
+    // channel pair 64 bn + 2 (tid % 32) (the taps come through LDS later)
+    float2v dwc[3];
     // residual epilogues: the wave's 32-row block of the residual stream (row
     // block kg of the tile) in the copy-out's layout, its rows' statistics
     // and the copy-out's columns of gamma, res_g, res_b, in registers before
@@ -1794,7 +1930,7 @@ __global__ __launch_bounds__(64 * NWV * KG, 1) void gemm_rb_kernel(GemmParams p)
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int t = 0; t < CPL; ++t) {
-            const int c = lane + 64 * t, n = nw + c;
+            const int c = lane + 64 * t, n = wcol(c);
             const bool ok = c < WC && n < p.N;
             colv[0][t] = ok && p.bias ? p.bias[n] : 0.f;   // times alpha when written to LDS
             if constexpr (C::NCA == 2) colv[1][t] = fold && ok ? p.fold_c1[n] : 0.f;
@@ -1802,6 +1938,12 @@ __global__ __launch_bounds__(64 * NWV * KG, 1) void gemm_rb_kernel(GemmParams p)
         if constexpr (C::RESID) {
             rpre.load(p, m0 + 32 * kg, nw, lane);
             ecol.load(p, nw, lane, false, RS);
+        }
+        if constexpr (GD) {
+            const int c = n0 / 2 + 2 * (tid & 31);
+            dwc[0] = p.dw_b ? (float2v){p.dw_b[c], p.dw_b[c + 1]} : (float2v){0.f, 0.f};
+            dwc[1] = (float2v){p.dw_scale[c], p.dw_scale[c + 1]};
+            dwc[2] = (float2v){p.dw_shift[c], p.dw_shift[c + 1]};
         }
         __builtin_amdgcn_sched_barrier(0);
     };
@@ -1829,15 +1971,21 @@ __global__ __launch_bounds__(64 * NWV * KG, 1) void gemm_rb_kernel(GemmParams p)
         rs = make_rsrc(p.Ws, ((int64_t)(nkt - 1) * L + p.N) * SB);
 #pragma unroll
         for (int j = 0; j < WTN; ++j) {
-            const int n = nw + 32 * j + tail_col(r32);
+            const int n = wcol(32 * j + tail_col(r32));
             vq[j] = n < p.N ? (uint32_t)(n * WB + (WT == GT_Q8_0 ? 32 * q : 0)) : OOB;
             vs[j] = n < p.N ? (uint32_t)(n * SB + (WT == GT_Q8_0 ? 2 * q : 8 * q)) : OOB;
         }
+    } else if constexpr (WT == GT_F16F) {
+        // [slab][block of 32 columns][t][lane] pieces; this wave's block is
+        // 4 bn + wid (the fragment copy is in the kernel's column order)
+        rq = make_rsrc(p.Wq, (int64_t)p.N * p.K * 2);
+        vq[0] = (uint32_t)(((4 * bn + wid) * 256 + lane) * 16);
+        vs[0] = 0;
     } else {
         rq = make_rsrc(p.Wq, (int64_t)p.N * p.K * 2);
 #pragma unroll
         for (int j = 0; j < WTN; ++j) {
-            const int n = nw + 32 * j + tail_col(r32);
+            const int n = wcol(32 * j + tail_col(r32));
             vq[j] = n < p.N ? (uint32_t)(((int64_t)n * p.K + 32 * q) * 2) : OOB;
             vs[j] = 0;
         }
@@ -1845,7 +1993,8 @@ __global__ __launch_bounds__(64 * NWV * KG, 1) void gemm_rb_kernel(GemmParams p)
     // scalar offsets of the group's slab k (out of range past its last slab)
     auto soq = [&](int k) -> int {
         if (k >= nk) return (int)OOB;
-        return WT == GT_Q8_0 ? (kb + k) * L * 64 : WT == GT_Q4_K ? (kb + k) * L * 32 : (kb + k) * 128;
+        return WT == GT_Q8_0 ? (kb + k) * L * 64 : WT == GT_Q4_K ? (kb + k) * L * 32
+             : WT == GT_F16F ? (kb + k) * p.N * 128 : (kb + k) * 128;
     };
     auto sos = [&](int k) -> int {
         if (k >= nk) return (int)OOB;
@@ -1977,49 +2126,66 @@ __global__ __launch_bounds__(64 * NWV * KG, 1) void gemm_rb_kernel(GemmParams p)
     }
     wait_vmcnt<0>();
     __syncthreads();
+    // conv module: the tile's 64 x 9 depthwise taps ([channel][tap], contiguous
+    // in dw_w) by 144 lanes, into LDS in the epilogue
+    float4v taps4 = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (GD) {
+        if (tid < 64 * GLU_DW_K / 4) taps4 = *((const float4v*)(p.dw_w + (int64_t)(n0 / 2) * GLU_DW_K) + tid);
+    }
 
-    // folded LayerNorm: {mean, rstd} of the tile's rows at the top of LDS
-    float2v* ftab = (float2v*)(smem_all + C::LDS) - BM;
+    // folded LayerNorm: {mean, rstd} of the tile's rows (past the body, or
+    // over the start of the statistics once they are in registers)
+    float2v* ftab = (float2v*)(smem_all + C::FTAB);
     if constexpr (fold) {
-        FoldStats<BM> fst;
+        // the table is built by 256 threads (the conv module's by all 512)
+        constexpr int FT = GD ? C::NT : 256;
+        FoldStats<BM, FT> fst;
         const int lc = __builtin_ctz(p.fold_groups / 2), total = BM << lc;
-        if (tid < 256) {   // the table is built by 256 threads
+        if (tid < FT) {
 #pragma unroll
-            for (int i = 0; i < FoldStats<BM>::MAXC; ++i) {
-                const int ch = tid + 256 * i;
+            for (int i = 0; i < FoldStats<BM, FT>::MAXC; ++i) {
+                const int ch = tid + FT * i;
                 fst.c[i] = ch < total ? ((const float4v*)(smem_all + C::BODY - C::FOLD_BYTES))[ch]
                                       : (float4v){0.f, 0.f, 0.f, 0.f};
             }
-            fst.finish(p, ftab, tid);
         }
+        if constexpr (C::FTAB != C::BODY) __syncthreads();   // the table overwrites the statistics
+        if (tid < FT) fst.finish(p, ftab, tid);
         __syncthreads();
     }
-    // two K groups: group g's partial of row block 1 - g goes to the other
-    // group, which adds it to its own (lane-major [wave][register][lane] f32)
-    float16v fin[WTN];
+    // two K groups: group g finishes row blocks HB g .. HB g + HB - 1; its
+    // partial of the other group's blocks goes to that group, which adds it to
+    // its own (lane-major [wave][register][lane] f32)
+    constexpr int HB = KG == 2 ? WTM / 2 : 1;
+    float16v fin[HB][WTN];
     if constexpr (KG == 2) {
         // [wave][register / 4][lane] float4s: 16-byte accesses, 1 KB per instruction
-        constexpr int R = 16 * WTN;
+        constexpr int R = 16 * WTN * HB;
         float4v* give = (float4v*)smem_all + wid_all * (R / 4) * 64 + lane;
         const float4v* take = (const float4v*)smem_all + ((1 - kg) * 4 + wid) * (R / 4) * 64 + lane;
 #pragma unroll
-        for (int j = 0; j < WTN; ++j)
+        for (int ii = 0; ii < HB; ++ii)
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                float4v g;
+            for (int j = 0; j < WTN; ++j)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) g[e] = kg ? acc[0][j][4 * t + e] : acc[1][j][4 * t + e];
-                give[(j * 4 + t) * 64] = g;
-            }
+                for (int t = 0; t < 4; ++t) {
+                    float4v g;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) g[e] = kg ? acc[ii][j][4 * t + e] : acc[HB + ii][j][4 * t + e];
+                    give[((ii * WTN + j) * 4 + t) * 64] = g;
+                }
         __syncthreads();
 #pragma unroll
-        for (int j = 0; j < WTN; ++j)
+        for (int ii = 0; ii < HB; ++ii)
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const float4v o = take[(j * 4 + t) * 64];
+            for (int j = 0; j < WTN; ++j)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) fin[j][4 * t + e] = (kg ? acc[1][j][4 * t + e] : acc[0][j][4 * t + e]) + o[e];
-            }
+                for (int t = 0; t < 4; ++t) {
+                    const float4v o = take[((ii * WTN + j) * 4 + t) * 64];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        fin[ii][j][4 * t + e] = (kg ? acc[HB + ii][j][4 * t + e] : acc[ii][j][4 * t + e]) + o[e];
+                }
     }
     // this wave's column constants (the ring is free; past the exchange):
     // written and read by the wave alone
@@ -2033,8 +2199,11 @@ __global__ __launch_bounds__(64 * NWV * KG, 1) void gemm_rb_kernel(GemmParams p)
     __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0)
     __builtin_amdgcn_wave_barrier();
     if constexpr (C::RESID)
-        epilogue_rb_resid<EPI, WTN>(p, fin, ctab, wsm, m0 + 32 * kg, nw, lane, alpha, ecol, rpre.v,
+        epilogue_rb_resid<EPI, WTN>(p, fin[0], ctab, wsm, m0 + 32 * kg, nw, lane, alpha, ecol, rpre.v,
                                     RS && p.res_rows ? rpre.rs : nullptr);
+    else if constexpr (GD)
+        epilogue_rb_glu_dw<C::LDG>(p, fin, ctab, ftab, (float*)(smem_all + C::XCH + C::CTAB), m0, bm, n0, kg, wid,
+                                   lane, tid, fold, taps4, dwc);
     else epilogue_rb<EPI, WTM, WTN>(p, acc, ctab, m0, nw, lane, alpha, fold, ftab);
 }
 
@@ -2493,6 +2662,59 @@ static bool dma_rb_resid(int epi, const GemmParams& p, hipStream_t s) {
     return true;
 }
 
+// The conv module (pointwise_conv1 + GLU + depthwise conv + BatchNorm + SiLU)
+// on item tiles: items of T <= 128 frames, one 128-row tile per item and 64
+// channels, so B x N / 128 workgroups (256 at B = 16, one per CU) and no
+// halo rows; the register-B kernel in two K groups (128 x 128 tiles, eight
+// waves, two per SIMD).  The LDS-B kernel's 64-row tiles writing 56 rows
+// (576 of them at B = 16, T' = 125) run 2.25 rounds of the chip.
+// f16 weights run from their fragment-order copy (p.wfrag) when one is given.
+template <int WT>
+static bool rb_glu_dw(const GemmParams& p, hipStream_t s) {
+    if (p.T > 128 || p.M % p.T != 0 || p.N % 128 != 0 || p.K % 512 != 0) return false;
+    require((int64_t)p.M * p.ldy * 2 < ((int64_t)1 << 31), "gemm: conv-module output must stay below 2 GB");
+    const int tiles = p.M / p.T * (p.N / 128);
+    GemmParams q = p;
+    q.xcd_gm = choose_xcd_gm(p, WT, p.T, 128);
+    auto go = [&](auto WTC) {
+        constexpr int W = decltype(WTC)::value;
+        constexpr int NT = RbCfg<4, 1, W, EPI_GLU_DW, 4, true, 2, 4>::NT;
+        if (p.fold_stats) launch((gemm_rb_kernel<4, 1, W, EPI_GLU_DW, 4, true, 2, 4>), dim3(tiles), dim3(NT), 0, s, q);
+        else launch((gemm_rb_kernel<4, 1, W, EPI_GLU_DW, 4, false, 2, 4>), dim3(tiles), dim3(NT), 0, s, q);
+    };
+    if (WT == GT_F16 && p.wfrag) {
+        q.Wq = p.wfrag;
+        go(std::integral_constant<int, GT_F16F>{});
+    } else {
+        go(std::integral_constant<int, WT>{});
+    }
+    PKX_LAUNCH_CHECK();
+    return true;
+}
+
+// One 16-byte piece per thread: piece i = ((slab (N/32) + block) 4 + t) 64 +
+// lane holds weight row glu_wcol(block / 4, block % 4, tail_col(lane % 32)),
+// halves 64 slab + 32 (lane / 32) + 8 t .. + 7.
+__global__ void glu_frag_kernel(const f16* __restrict__ w, int N, int K, f16* __restrict__ frag) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)N * K / 8) return;
+    const int lane = (int)(i & 63), t = (int)((i >> 6) & 3);
+    const int64_t sb = i >> 8;
+    const int nblk = N / 32, blk = (int)(sb % nblk), slab = (int)(sb / nblk);
+    const int n = glu_wcol(blk >> 2, blk & 3, tail_col(lane & 31));
+    const int k = 64 * slab + 32 * (lane >> 5) + 8 * t;
+    ((int4v*)frag)[i] = *(const int4v*)(w + (int64_t)n * K + k);
+}
+
+bool glu_frag_supported(int wtype, int N, int K) { return wtype == GT_F16 && N % 128 == 0 && K % 512 == 0; }
+size_t glu_frag_bytes(int N, int K) { return (size_t)N * K * 2; }
+void glu_frag_prepare(const void* w, int N, int K, void* frag, hipStream_t s) {
+    require(glu_frag_supported(GT_F16, N, K), "glu_frag_prepare: f16 weights, N % 128 == 0, K % 512 == 0");
+    const int64_t pieces = (int64_t)N * K / 8;
+    launch(glu_frag_kernel, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, s, (const f16*)w, N, K, (f16*)frag);
+    PKX_LAUNCH_CHECK();
+}
+
 template <int TM, int TN, int WT>
 static void f32_epi(int epi, const GemmParams& p, hipStream_t s) { PKX_EPI_SWITCH(run_f32, TM, TN, WT) }
 // tiles narrower than 64 columns per wave pair: every epilogue but GLU (which
@@ -2552,8 +2774,12 @@ void launch_gemm(Precision prec, int wtype, int epi, const GemmParams& p, hipStr
                     (epi == EPI_STORE || epi == EPI_SILU || epi == EPI_GLU || epi == EPI_GLU_DW),
                 "gemm: a folded LayerNorm needs the f16 path, 2..32 (a power of two) statistics groups and a STORE / SILU / GLU epilogue");
     if (epi == EPI_GLU_DW) {
-        // 64 x 128 tiles (56 output rows, 64 channels) on a 2-stage ring, three
-        // workgroups per CU: the overlapping row tiles outnumber two slots per CU
+        if (wtype == GT_F16 && rb_glu_dw<GT_F16>(p, s)) return;
+        if (wtype == GT_Q8_0 && rb_glu_dw<GT_Q8_0>(p, s)) return;
+        if (wtype == GT_Q4_K && rb_glu_dw<GT_Q4_K>(p, s)) return;
+        // longer items: 64 x 128 tiles (56 output rows, 64 channels) on a
+        // 2-stage ring, three workgroups per CU: the overlapping row tiles
+        // outnumber two slots per CU
         switch (wtype) {
         case GT_F16: run_dma<1, 2, GT_F16, EPI_GLU_DW, 2>(p, s); break;
         case GT_Q8_0: run_dma<1, 2, GT_Q8_0, EPI_GLU_DW, 2>(p, s); break;

@@ -53,6 +53,9 @@ struct GemmParams {
     const float* dw_b = nullptr;
     const float* dw_scale = nullptr;
     const float* dw_shift = nullptr;
+    // EPI_GLU_DW with f16 weights: their copy in the item-tile kernel's
+    // fragment order (glu_frag_prepare), or null (the kernel then reads Wq)
+    const void* wfrag = nullptr;
     // EPI_RESID_LN outputs (N % 32 == 0)
     const float* ln_g = nullptr;   // [N] gamma of the next LayerNorm
     void* ln_h = nullptr;          // f16 [M][N]: R * gamma
@@ -94,6 +97,14 @@ void launch_ln_fold_consts(int wtype, const void* Wq, const void* Ws, int N, int
 // True when launch_gemm can run EPI_GLU_DW for this shape: the f16 MFMA path,
 // N (= 2 x channels) a multiple of 64 and K a multiple of 64.
 bool gemm_glu_dw_supported(Precision prec, int wtype, int N, int K);
+
+// EPI_GLU_DW on items of T <= 128 frames runs one 128-row tile per item; with
+// f16 weights it reads them from a copy in its fragment order (GemmParams::
+// wfrag, glu_frag_bytes(N, K) bytes), made once by glu_frag_prepare from the
+// row-major [N][K] weights.  Supported for f16, N % 128 == 0, K % 512 == 0.
+bool glu_frag_supported(int wtype, int N, int K);
+size_t glu_frag_bytes(int N, int K);
+void glu_frag_prepare(const void* w, int N, int K, void* frag, hipStream_t s);
 
 // Launch one GEMM.  prec selects the activation type (f16: MFMA 16x16x32 f16
 // with weights dequantised to f16 in registers; f32: MFMA 16x16x4 f32 with

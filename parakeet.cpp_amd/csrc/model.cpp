@@ -676,6 +676,16 @@ void Model::finalize() {
             PKX_HIP(hipDeviceSynchronize());
         }
     }
+    // f16 pointwise_conv1 weights in the conv-module kernel's fragment order:
+    // items of T <= 128 frames run one tile per item, reading this copy
+    if (f16g && cfg_.conv_kernel == GLU_DW_K && !cfg_.conv_ln && !cfg_.conv_causal) {
+        for (LayerDev& L : layers_)
+            if (glu_frag_supported(L.pw1.gtype, L.pw1.N, L.pw1.K)) {
+                L.pw1_frag = dalloc(glu_frag_bytes(L.pw1.N, L.pw1.K));
+                glu_frag_prepare(L.pw1.q, L.pw1.N, L.pw1.K, L.pw1_frag, nullptr);
+            }
+        PKX_HIP(hipDeviceSynchronize());
+    }
     host_.clear();
     // split-K workspace (residual products of few rows): created here, once, so
     // that no forward or streaming step allocates or synchronises for it
@@ -875,6 +885,7 @@ void Model::conv_front(const LayerDev& L, const void* A, int64_t M, const int* v
         p.dw_b = L.dw_b;
         p.dw_scale = L.bn_scale;
         p.dw_shift = L.bn_shift;
+        p.wfrag = L.pw1_frag;
         mark(KF_GEMM_PW1_GLU, true);
         launch_gemm(prec_, L.pw1.gtype, EPI_GLU_DW, p, s);
         mark(KF_GEMM_PW1_GLU, false);

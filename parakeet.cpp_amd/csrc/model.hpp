@@ -76,6 +76,9 @@ struct LayerDev {
     // norm_conv -> pointwise_conv1, norm_feed_forward2 -> feed_forward2.linear1
     float *qkv_c1 = nullptr, *qkv_c2 = nullptr, *pw1_c1 = nullptr, *pw1_c2 = nullptr;
     float *ff2_c1 = nullptr, *ff2_c2 = nullptr;
+    // f16 pointwise_conv1 in the conv-module item-tile kernel's fragment order
+    // (glu_frag_prepare), or null
+    void* pw1_frag = nullptr;
 };
 
 struct SubDev {

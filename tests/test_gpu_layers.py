@@ -26,6 +26,14 @@ CASES = {
     # (kernel 9 takes the fused one-pass conv-module GEMM)
     "f16_k5": (dict(d_model=128, n_heads=2, ff_dim=256, conv_kernel=5), "f16", 1),
 }
+# d_model 512 (pointwise_conv1: K = 512, N = 1024): items of T <= 128 frames
+# take the conv module's item-tile kernel (one 128-row tile per item, no
+# halo), longer items the 56-row tiles
+CONV_CASES = {
+    "q8_d512": (dict(d_model=512, n_heads=4, ff_dim=1024), "q8_0", 1),
+    "f16_d512": (dict(d_model=512, n_heads=4, ff_dim=1024), "f16", 1),
+    "q4k_d512": (dict(d_model=512, n_heads=4, ff_dim=1024, conv_bias=False), "q4_k", 1),
+}
 
 
 def _cfg(kw, n_layers=2):
@@ -40,7 +48,7 @@ _CACHE = {}
 
 def _models(gpu, name):
     if name not in _CACHE:
-        kw, wt, prec = CASES[name]
+        kw, wt, prec = CASES[name] if name in CASES else CONV_CASES[name]
         m = pm.synthesize(_cfg(kw), wt, bn_random=True)
         _CACHE[name] = (m, oracle.OracleModel(m), gpu.Model.from_tensors(m, prec), prec)
     return _CACHE[name]
@@ -95,7 +103,15 @@ def test_conv_module(gpu, stream, name, B, T, valid):
     assert rel_l2(got[mask], ref[mask]) < _tol(prec)
 
 
-@pytest.mark.parametrize("name", list(CASES))
+@pytest.mark.parametrize("name", list(CONV_CASES))
+@pytest.mark.parametrize("B,T,valid", [(16, 125, [125, 125, 100, 1, 64, 65, 124, 125, 33, 2, 125, 90, 125, 7, 125, 50]),
+                                       (3, 128, [128, 127, 1]), (4, 1, [1, 1, 1, 1]), (1, 37, [37]),
+                                       (2, 200, [200, 150])])
+def test_conv_module_item_tiles(gpu, stream, name, B, T, valid):
+    test_conv_module(gpu, stream, name, B, T, valid)
+
+
+@pytest.mark.parametrize("name", list(CASES) + ["q8_d512", "f16_d512"])
 @pytest.mark.parametrize("B,T,valid", [(1, 26, [26]), (2, 63, [63, 40])])
 def test_conformer_layer(gpu, stream, name, B, T, valid):
     m, om, gm, prec = _models(gpu, name)
