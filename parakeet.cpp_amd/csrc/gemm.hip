@@ -1741,10 +1741,10 @@ __device__ __forceinline__ void epilogue_rb_resid(const GemmParams& p, const flo
 // and SiLU for the T rows: thread tid takes the channel pair 2 (tid % 32) and
 // rows 8 (tid / 32) .. + 7, its 16-row window in registers, and stores f16
 // pairs (conformer.cpp:55-157).
-template <int LDG>
+template <int LDG, bool FOLD>
 __device__ __forceinline__ void epilogue_rb_glu_dw(const GemmParams& p, const float16v (&fin)[2][1], const float* ctab,
                                                    const float2v* ftab, float* G, int m0, int item, int n0, int kg,
-                                                   int wid, int lane, int tid, bool fold, float4v taps4,
+                                                   int wid, int lane, int tid, float4v taps4,
                                                    const float2v (&dwc)[3]) {
     constexpr int K = GLU_DW_K, H = (K - 1) / 2, RPT = 8;
     // the tile's taps [64][K] past the GLU tile (thread tid < 144 brought 16 bytes)
@@ -1764,8 +1764,10 @@ __device__ __forceinline__ void epilogue_rb_glu_dw(const GemmParams& p, const fl
 #pragma unroll
     for (int ii = 0; ii < 2; ++ii) {
         const int row = 64 * kg + 32 * ii + r32;
+        // the pad mask as a bit mask (no branch around the sigmoid)
+        const uint32_t keep = row < vl ? 0xffffffffu : 0u;
         float a = 1.f, nb = 0.f;
-        if (fold) {
+        if constexpr (FOLD) {
             const float2v st = ftab[row];
             a = st.y;
             nb = -a * st.x;
@@ -1776,10 +1778,15 @@ __device__ __forceinline__ void epilogue_rb_glu_dw(const GemmParams& p, const fl
             const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(fin[ii][0][e]),
                                                              __float_as_uint(fin[ii][0][8 + e]), false, false);
             const float xa = __uint_as_float(sw[0]), xg = __uint_as_float(sw[1]);
-            const float ba = fold ? __builtin_fmaf(nb, ci[e >> 2][e & 3], bi[e >> 2][e & 3]) : bi[e >> 2][e & 3];
-            const float bb = fold ? __builtin_fmaf(nb, cg[e >> 2][e & 3], bg[e >> 2][e & 3]) : bg[e >> 2][e & 3];
-            const float va = __builtin_fmaf(a, xa, ba), vg = __builtin_fmaf(a, xg, bb);
-            o[e] = row < vl ? va * sigmoid_dev(vg) : 0.f;
+            float va, vg;
+            if constexpr (FOLD) {
+                va = __builtin_fmaf(a, xa, __builtin_fmaf(nb, ci[e >> 2][e & 3], bi[e >> 2][e & 3]));
+                vg = __builtin_fmaf(a, xg, __builtin_fmaf(nb, cg[e >> 2][e & 3], bg[e >> 2][e & 3]));
+            } else {
+                va = xa + bi[e >> 2][e & 3];
+                vg = xg + bg[e >> 2][e & 3];
+            }
+            o[e] = __uint_as_float(__float_as_uint(va * sigmoid_dev(vg)) & keep);
         }
         float* gr = G + row * LDG + 16 * wid + 8 * h;
         *(float4v*)gr = (float4v){o[0], o[1], o[2], o[3]};
@@ -1796,17 +1803,19 @@ __device__ __forceinline__ void epilogue_rb_glu_dw(const GemmParams& p, const fl
         const int row = r0 - H + q;
         win[q] = row >= 0 && row < 128 ? *(const float2v*)(G + row * LDG + cl) : (float2v){0.f, 0.f};
     }
+    // rows t < T of the item: 4-byte stores at 32-bit offsets from the
+    // item's first row (rows past T out of range)
+    const __amdgpu_buffer_rsrc_t ry = make_rsrc((const f16*)p.Y + (int64_t)m0 * p.ldy, ((int64_t)T * p.ldy) * 2);
+    const uint32_t off0 = (uint32_t)((r0 * p.ldy + c) * 2), ldb = (uint32_t)(p.ldy * 2);
 #pragma unroll
     for (int q = 0; q < RPT; ++q) {
-        const int t = r0 + q;
-        if (t < T) {
-            float2v acc = {0.f, 0.f};
+        float2v acc = {0.f, 0.f};
 #pragma unroll
-            for (int j = 0; j < K; ++j) acc += wk[j] * win[q + j];
-            const float2v y = (acc + dwc[0]) * dwc[1] + dwc[2];
-            const half2v hv = {(f16)silu_dev(y[0]), (f16)silu_dev(y[1])};
-            *(half2v*)((f16*)p.Y + (int64_t)(m0 + t) * p.ldy + c) = hv;
-        }
+        for (int j = 0; j < K; ++j) acc += wk[j] * win[q + j];
+        const float2v y = (acc + dwc[0]) * dwc[1] + dwc[2];
+        const half2v hv = {(f16)silu_dev(y[0]), (f16)silu_dev(y[1])};
+        const uint32_t off = r0 + q < T ? off0 + q * ldb : OOB;
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, hv), ry, off, 0, 0);
     }
 }
 
@@ -2202,8 +2211,8 @@ __global__ __launch_bounds__(64 * NWV * KG, 1) void gemm_rb_kernel(GemmParams p)
         epilogue_rb_resid<EPI, WTN>(p, fin[0], ctab, wsm, m0 + 32 * kg, nw, lane, alpha, ecol, rpre.v,
                                     RS && p.res_rows ? rpre.rs : nullptr);
     else if constexpr (GD)
-        epilogue_rb_glu_dw<C::LDG>(p, fin, ctab, ftab, (float*)(smem_all + C::XCH + C::CTAB), m0, bm, n0, kg, wid,
-                                   lane, tid, fold, taps4, dwc);
+        epilogue_rb_glu_dw<C::LDG, fold>(p, fin, ctab, ftab, (float*)(smem_all + C::XCH + C::CTAB), m0, bm, n0, kg,
+                                         wid, lane, tid, taps4, dwc);
     else epilogue_rb<EPI, WTM, WTN>(p, acc, ctab, m0, nw, lane, alpha, fold, ftab);
 }
 
