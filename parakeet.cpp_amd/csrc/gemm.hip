@@ -2146,8 +2146,8 @@ __global__ __launch_bounds__(64 * NWV * KG, 1) void gemm_rb_kernel(GemmParams p)
     // over the start of the statistics once they are in registers)
     float2v* ftab = (float2v*)(smem_all + C::FTAB);
     if constexpr (fold) {
-        // the table is built by 256 threads (the conv module's by all 512)
-        constexpr int FT = GD ? C::NT : 256;
+        // the table is built by every thread of the workgroup
+        constexpr int FT = C::NT;
         FoldStats<BM, FT> fst;
         const int lc = __builtin_ctz(p.fold_groups / 2), total = BM << lc;
         if (tid < FT) {
