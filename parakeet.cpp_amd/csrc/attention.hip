@@ -178,8 +178,6 @@ __global__ __launch_bounds__(64 * NQW * NG, 1) void relpos_attn_ks_kernel(AttnPa
     auto dma_p = [&](int st) { dma_rows(rp, sm.p, a.ldp, rlo + SK * st, PPW); };    // its band
     auto dma_v = [&](int st) { dma_rows(rv, sm.vs, a.ldv, SK * st, KPW); };         // its V
     dma_k(0);
-    dma_p(0);
-    dma_v(0);
     float4v bq[NKC][4];   // bias_u, bias_u, bias_v, bias_v halves of each fragment's 8 columns
     {
         float4v* bs = (float4v*)sm.g[w];
@@ -207,6 +205,10 @@ __global__ __launch_bounds__(64 * NQW * NG, 1) void relpos_attn_ks_kernel(AttnPa
             qu[kc][e] = (f16)(xf + bq[kc][e >> 2][e & 3]);
             qv[kc][e] = (f16)(xf + bq[kc][2 + (e >> 2)][e & 3]);
         }
+    // the step's band and V behind K: the query conversion above runs while
+    // K is in flight instead of after the issue of all 112 KB
+    dma_p(0);
+    dma_v(0);
     // scores in log2 units: exp(scale * x) = exp2(scale * log2(e) * x)
     const float sl2 = a.scale * 1.4426950408889634f;
     // the keys this lane's query sees: [jlo, jhi), the valid frames and, with
