@@ -174,8 +174,9 @@ public:
                  std::vector<float>& out, int& Tout, int& d_model) const;
     void forward(const std::vector<float>& mel, int n_mels, int T,
                  std::vector<float>& out, int& Tout, int& d_model, int& valid_len) const;
-    // in_valid_frames >= 0 replaces the offline T-1 entry valid length; values
-    // above T-1 (whole-window streaming chunks) are outside this offline build.
+    // in_valid_frames >= 0 replaces the offline T-1 entry valid length;
+    // in_valid_frames == T is the whole window (the streaming chunks'
+    // convention, subsampling.hpp:53-61); a count above T is refused.
     void forward(const std::vector<float>& mel, int n_mels, int T,
                  std::vector<float>& out, int& Tout, int& d_model, int& valid_len,
                  int in_valid_frames) const;
