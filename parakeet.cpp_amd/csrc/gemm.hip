@@ -1729,22 +1729,24 @@ __device__ __forceinline__ void epilogue_rb_resid(const GemmParams& p, const flo
     epilogue_lds_out<EPI, 32, WC, WTN>(p, wsm, mb, nw, lane, ec, xpre, xrs);
 }
 
-// Register-B conv-module epilogue (item tiles of 128 rows x 64 channels,
-// rows t = 0 .. T-1 of one item): K group kg holds the summed rows 64 kg +
+// Register-B conv-module epilogue (item tiles of 128 rows x 64 channels: tile
+// row r is frame tb + r of item `item`, the tile writes frames [tlo, thi)):
+// K group kg holds the summed rows 64 kg +
 // 32 ii + l % 32 in fin[ii], lane half l / 32 the inputs (0) or the gates (1)
 // of the wave's 16 channels in registers 0 .. 15.  One lane-half swap per
 // register pair hands each lane the input and the gate of channel
 // 16 wid + 8 (l / 32) + e; the GLU (folded LayerNorm, bias, a * sigmoid(b))
-// with the pad mask (rows t >= valid are zero, and with them the next item's
-// rows) goes into G [128][LDG] f32 in LDS.  Then the depthwise conv over time
-// (zero rows outside the item's valid frames), its bias, the folded BatchNorm
-// and SiLU for the T rows: thread tid takes the channel pair 2 (tid % 32) and
-// rows 8 (tid / 32) .. + 7, its 16-row window in registers, and stores f16
-// pairs (conformer.cpp:55-157).
+// with the pad mask (frames t >= valid are zero, and with them the next
+// item's rows) goes into G [128][LDG] f32 in LDS.  Then the depthwise conv
+// over time (zero rows outside the item's valid frames: frames before tb are
+// outside the item), its bias, the folded BatchNorm and SiLU for frames
+// [tlo, thi): thread tid takes the channel pair 2 (tid % 32) and rows
+// 8 (tid / 32) .. + 7, its 16-row window in registers, and stores f16 pairs
+// (conformer.cpp:55-157).
 template <int LDG, bool FOLD>
 __device__ __forceinline__ void epilogue_rb_glu_dw(const GemmParams& p, const float16v (&fin)[2][1], const float* ctab,
-                                                   const float2v* ftab, float* G, int m0, int item, int n0, int kg,
-                                                   int wid, int lane, int tid, float4v taps4,
+                                                   const float2v* ftab, float* G, int m0, int item, int tb, int tlo,
+                                                   int thi, int n0, int kg, int wid, int lane, int tid, float4v taps4,
                                                    const float2v (&dwc)[3]) {
     constexpr int K = GLU_DW_K, H = (K - 1) / 2, RPT = 8;
     // the tile's taps [64][K] past the GLU tile (thread tid < 144 brought 16 bytes)
@@ -1765,7 +1767,7 @@ __device__ __forceinline__ void epilogue_rb_glu_dw(const GemmParams& p, const fl
     for (int ii = 0; ii < 2; ++ii) {
         const int row = 64 * kg + 32 * ii + r32;
         // the pad mask as a bit mask (no branch around the sigmoid)
-        const uint32_t keep = row < vl ? 0xffffffffu : 0u;
+        const uint32_t keep = tb + row < vl ? 0xffffffffu : 0u;
         float a = 1.f, nb = 0.f;
         if constexpr (FOLD) {
             const float2v st = ftab[row];
@@ -1803,9 +1805,9 @@ __device__ __forceinline__ void epilogue_rb_glu_dw(const GemmParams& p, const fl
         const int row = r0 - H + q;
         win[q] = row >= 0 && row < 128 ? *(const float2v*)(G + row * LDG + cl) : (float2v){0.f, 0.f};
     }
-    // rows t < T of the item: 4-byte stores at 32-bit offsets from the
-    // item's first row (rows past T out of range)
-    const __amdgpu_buffer_rsrc_t ry = make_rsrc((const f16*)p.Y + (int64_t)m0 * p.ldy, ((int64_t)T * p.ldy) * 2);
+    // frames [tlo, thi): 4-byte stores at 32-bit offsets from the tile's
+    // first row (other rows out of range)
+    const __amdgpu_buffer_rsrc_t ry = make_rsrc((const f16*)p.Y + (int64_t)m0 * p.ldy, ((int64_t)(thi - tb) * p.ldy) * 2);
     const uint32_t off0 = (uint32_t)((r0 * p.ldy + c) * 2), ldb = (uint32_t)(p.ldy * 2);
 #pragma unroll
     for (int q = 0; q < RPT; ++q) {
@@ -1814,7 +1816,8 @@ __device__ __forceinline__ void epilogue_rb_glu_dw(const GemmParams& p, const fl
         for (int j = 0; j < K; ++j) acc += wk[j] * win[q + j];
         const float2v y = (acc + dwc[0]) * dwc[1] + dwc[2];
         const half2v hv = {(f16)silu_dev(y[0]), (f16)silu_dev(y[1])};
-        const uint32_t off = r0 + q < T ? off0 + q * ldb : OOB;
+        const int t = tb + r0 + q;
+        const uint32_t off = t >= tlo && t < thi ? off0 + q * ldb : OOB;
         __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, hv), ry, off, 0, 0);
     }
 }
@@ -1887,10 +1890,27 @@ __global__ __launch_bounds__(64 * NWV * KG, 1) void gemm_rb_kernel(GemmParams p)
     const int q = lane >> 5, r32 = lane & 31;
     uint8_t* smem = smem_all + kg * NS * C::A_STAGE;   // this group's ring
     int bm, bn;
-    // conv module: row tile bm is item bm (rows bm T .. bm T + T - 1; the rest
-    // of the 128 rows belong to the next item or lie past M and are masked)
-    xcd_tile_2d(blockIdx.x, GD ? p.M / p.T : cdiv_dev(p.M, BM), cdiv_dev(p.N, C::BN), p.xcd_gm, bm, bn);
-    const int m0 = bm * (GD ? p.T : BM), n0 = bn * C::BN, nw = n0 + wid * WC;
+    // conv module: item tiles.  An item of T <= 128 frames is one row tile
+    // (tile row r = frame r; the rest of the 128 rows belong to the next item
+    // or lie past M and are masked); a longer item is cut into nti parts of at
+    // most 120 output frames [tlo, thi), a part after the first starting 4
+    // frames early (tile row r = frame tb + r) so that its 128 rows hold the
+    // depthwise conv's halo on both sides.
+    int item = 0, tb = 0, tlo = 0, thi = 0;
+    if constexpr (GD) {
+        constexpr int HALO = (GLU_DW_K - 1) / 2;
+        const int T = p.T, nti = T <= 128 ? 1 : (T + 127 - 2 * HALO) / (128 - 2 * HALO);
+        const int orows = udiv_small(T + nti - 1, nti);
+        xcd_tile_2d(blockIdx.x, p.M / T * nti, cdiv_dev(p.N, C::BN), p.xcd_gm, bm, bn);
+        item = udiv_small(bm, nti);
+        const int part = bm - item * nti;
+        tlo = part * orows;
+        thi = min(tlo + orows, T);
+        tb = part > 0 ? tlo - HALO : 0;
+    } else {
+        xcd_tile_2d(blockIdx.x, cdiv_dev(p.M, BM), cdiv_dev(p.N, C::BN), p.xcd_gm, bm, bn);
+    }
+    const int m0 = GD ? item * p.T + tb : bm * BM, n0 = bn * C::BN, nw = n0 + wid * WC;
     const int nkt = p.K / 64, nk = nkt / KG, kb = kg * nk;   // slabs: all, this group's, its first
     // weight column of the wave's column c (0 .. WC-1); conv module: lanes l
     // and l + 32 end with the input and the gate of the same 16 channels
@@ -2211,8 +2231,8 @@ __global__ __launch_bounds__(64 * NWV * KG, 1) void gemm_rb_kernel(GemmParams p)
         epilogue_rb_resid<EPI, WTN>(p, fin[0], ctab, wsm, m0 + 32 * kg, nw, lane, alpha, ecol, rpre.v,
                                     RS && p.res_rows ? rpre.rs : nullptr);
     else if constexpr (GD)
-        epilogue_rb_glu_dw<C::LDG, fold>(p, fin, ctab, ftab, (float*)(smem_all + C::XCH + C::CTAB), m0, bm, n0, kg,
-                                         wid, lane, tid, taps4, dwc);
+        epilogue_rb_glu_dw<C::LDG, fold>(p, fin, ctab, ftab, (float*)(smem_all + C::XCH + C::CTAB), m0, item, tb,
+                                         tlo, thi, n0, kg, wid, lane, tid, taps4, dwc);
     else epilogue_rb<EPI, WTM, WTN>(p, acc, ctab, m0, nw, lane, alpha, fold, ftab);
 }
 
@@ -2672,19 +2692,22 @@ static bool dma_rb_resid(int epi, const GemmParams& p, hipStream_t s) {
 }
 
 // The conv module (pointwise_conv1 + GLU + depthwise conv + BatchNorm + SiLU)
-// on item tiles: items of T <= 128 frames, one 128-row tile per item and 64
+// on item tiles: one 128-row tile per item of T <= 128 frames and 64
 // channels, so B x N / 128 workgroups (256 at B = 16, one per CU) and no
-// halo rows; the register-B kernel in two K groups (128 x 128 tiles, eight
-// waves, two per SIMD).  The LDS-B kernel's 64-row tiles writing 56 rows
-// (576 of them at B = 16, T' = 125) run 2.25 rounds of the chip.
+// halo rows; longer items in ceil(T / 120) parts with 4-row halos.  The
+// register-B kernel in two K groups (128 x 128 tiles, eight waves, two per
+// SIMD).  The LDS-B kernel's 64-row tiles writing 56 rows (576 of them at
+// B = 16, T' = 125) run 2.25 rounds of the chip.
 // f16 weights run from their fragment-order copy (p.wfrag) when one is given.
 template <int WT>
 static bool rb_glu_dw(const GemmParams& p, hipStream_t s) {
-    if (p.T > 128 || p.M % p.T != 0 || p.N % 128 != 0 || p.K % 512 != 0) return false;
+    if (p.M % p.T != 0 || p.N % 128 != 0 || p.K % 512 != 0) return false;
     require((int64_t)p.M * p.ldy * 2 < ((int64_t)1 << 31), "gemm: conv-module output must stay below 2 GB");
-    const int tiles = p.M / p.T * (p.N / 128);
+    constexpr int HALO = (GLU_DW_K - 1) / 2;
+    const int nti = p.T <= 128 ? 1 : cdiv(p.T, 128 - 2 * HALO), orows = cdiv(p.T, nti);   // as in the kernel
+    const int tiles = p.M / p.T * nti * (p.N / 128);
     GemmParams q = p;
-    q.xcd_gm = choose_xcd_gm(p, WT, p.T, 128);
+    q.xcd_gm = choose_xcd_gm(p, WT, orows, 128);
     auto go = [&](auto WTC) {
         constexpr int W = decltype(WTC)::value;
         constexpr int NT = RbCfg<4, 1, W, EPI_GLU_DW, 4, true, 2, 4>::NT;

@@ -26,9 +26,10 @@ CASES = {
     # (kernel 9 takes the fused one-pass conv-module GEMM)
     "f16_k5": (dict(d_model=128, n_heads=2, ff_dim=256, conv_kernel=5), "f16", 1),
 }
-# d_model 512 (pointwise_conv1: K = 512, N = 1024): items of T <= 128 frames
-# take the conv module's item-tile kernel (one 128-row tile per item, no
-# halo), longer items the 56-row tiles
+# d_model 512 (pointwise_conv1: K = 512, N = 1024): the conv module's
+# item-tile kernel, one 128-row tile per item of T <= 128 frames (no halo),
+# longer items in parts of at most 120 frames with 4-row halos (T = 129: two
+# parts of 65; 240: two of 120; 375: four of 94)
 CONV_CASES = {
     "q8_d512": (dict(d_model=512, n_heads=4, ff_dim=1024), "q8_0", 1),
     "f16_d512": (dict(d_model=512, n_heads=4, ff_dim=1024), "f16", 1),
@@ -106,7 +107,8 @@ def test_conv_module(gpu, stream, name, B, T, valid):
 @pytest.mark.parametrize("name", list(CONV_CASES))
 @pytest.mark.parametrize("B,T,valid", [(16, 125, [125, 125, 100, 1, 64, 65, 124, 125, 33, 2, 125, 90, 125, 7, 125, 50]),
                                        (3, 128, [128, 127, 1]), (4, 1, [1, 1, 1, 1]), (1, 37, [37]),
-                                       (2, 200, [200, 150])])
+                                       (1, 129, [129]), (2, 200, [200, 150]), (3, 240, [240, 121, 5]),
+                                       (2, 375, [375, 241])])
 def test_conv_module_item_tiles(gpu, stream, name, B, T, valid):
     test_conv_module(gpu, stream, name, B, T, valid)
 
