@@ -2705,7 +2705,13 @@ static bool rb_glu_dw(const GemmParams& p, hipStream_t s) {
     require((int64_t)p.M * p.ldy * 2 < ((int64_t)1 << 31), "gemm: conv-module output must stay below 2 GB");
     constexpr int HALO = (GLU_DW_K - 1) / 2;
     const int nti = p.T <= 128 ? 1 : cdiv(p.T, 128 - 2 * HALO), orows = cdiv(p.T, nti);   // as in the kernel
-    const int tiles = p.M / p.T * nti * (p.N / 128);
+    const int64_t tiles64 = (int64_t)(p.M / p.T) * nti * (p.N / 128);
+    // one workgroup per CU: past two rounds of the chip the LDS-B kernel's
+    // three co-resident workgroups per CU win (on MI355X, f16 weights:
+    // 256 / 512 tiles 17.0 / 33.0 us against 23.7 / 37.7; 704 tiles at
+    // d = 1408 58.5 against 46.2, 5632 tiles 437 against 401)
+    if (tiles64 > 2 * (int64_t)device_cu_count()) return false;
+    const int tiles = (int)tiles64;
     GemmParams q = p;
     q.xcd_gm = choose_xcd_gm(p, WT, orows, 128);
     auto go = [&](auto WTC) {
