@@ -136,7 +136,7 @@ def test_conformer_layer(gpu, stream, name, B, T, valid):
     assert rel_l2(delta_got, delta_ref) < 3 * _tol(prec)
 
 
-@pytest.mark.parametrize("name", list(CASES))
+@pytest.mark.parametrize("name", list(CASES) + ["q8_d512", "f16_d512"])
 @pytest.mark.parametrize("offset", [0.0, 4.0])
 def test_conformer_layer_folded_layernorm(gpu, stream, name, offset):
     """The encoder's own path through a block (no conv-module capture): on the
@@ -144,7 +144,8 @@ def test_conformer_layer_folded_layernorm(gpu, stream, name, offset):
     the neighbouring GEMMs (statistics from the residual product, the
     normalisation in the next product's epilogue).  A per-row mean of 4 sigma
     in the residual stream checks that the folded form keeps its accuracy when
-    the mean is large against the spread."""
+    the mean is large against the spread (d_model 512: the conv module's
+    item-tile kernel with norm_conv folded in)."""
     m, om, gm, prec = _models(gpu, name)
     D, B, T = m.cfg.d_model, 3, 77
     valid = [77, 50, 9]
