@@ -101,7 +101,12 @@ def test_conv_module(gpu, stream, name, B, T, valid):
     gm.conv_module(0, dc, valid, dy, stream)
     got = dy.numpy(stream)
     mask = _valid_mask(B, T, valid)
-    assert rel_l2(got[mask], ref[mask]) < _tol(prec)
+    err = rel_l2(got[mask], ref[mask])
+    print(f"  rel_l2 {err:.3e}")
+    # f16 path: 2.1-3.1e-4 measured (the f16 roundings of the activations,
+    # pointwise weights and stored GLU / depthwise values; deterministic), so
+    # the bar is kept at 3e-3 rather than the layer-level 1e-2
+    assert err < (3e-3 if prec else _tol(prec)), err
 
 
 @pytest.mark.parametrize("name", list(CONV_CASES))
